@@ -1,0 +1,171 @@
+/*
+ * representax_amd: MI355X (gfx950) kernels for representax's quantized-linear
+ * path, behind a plain C ABI.
+ *
+ * Conventions
+ *   - Every pointer is a device pointer unless the name says host.
+ *   - `stream` is a hipStream_t (NULL = the legacy default stream). All work
+ *     is enqueued on it; no entry point synchronizes or allocates device
+ *     memory. Scratch comes from the caller's `workspace`, sized by the
+ *     matching *_workspace() query.
+ *   - bf16 tensors are passed as their 16-bit patterns; fp8 tensors as uint8
+ *     codes in the OCP e4m3fn / e5m2 encodings.
+ *   - Matrices are row-major and dense unless strides are given.
+ *   - Return value: RPX_OK, or an error code with a message available from
+ *     rpx_last_error() (thread local). Invalid arguments are rejected before
+ *     anything is launched.
+ *
+ * The reference (ckgresla/representax) is pure JAX; it has no native FFI. Each
+ * entry point below names the reference function whose numerics it replaces;
+ * those functions would call it through jax.ffi custom calls.
+ */
+#ifndef REPRESENTAX_AMD_H_
+#define REPRESENTAX_AMD_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RPX_ABI_VERSION 1
+
+#define RPX_OK 0
+#define RPX_ERR_INVALID 1
+#define RPX_ERR_HIP 2
+
+#define RPX_DTYPE_F32 0
+#define RPX_DTYPE_BF16 1
+
+#define RPX_FP8_E4M3FN 0
+#define RPX_FP8_E5M2 1
+
+const char* rpx_last_error(void);
+int rpx_abi_version(void);
+
+/* ---------------------------------------------------------------------------
+ * Packed INT4 weights.
+ *   packed     uint8 [n, ceil(k/2)]  low nibble = even column, two's
+ *                                    complement int4
+ *   scale_bits uint16[n, k/group]    bf16 bit patterns
+ * group_size <= 0 or == k selects one scale per output row, the reference's
+ * scheme; other values must divide k and be even (an extension).
+ * ------------------------------------------------------------------------- */
+
+/* Quantize weight [n, k] (f32 or bf16). Replaces _pack_int4_rows,
+ * src/representax/models/adapters.py:38-65 (and _bits_from_bfloat16, :30-31). */
+int rpx_int4_pack(const void* weight, int dtype, int64_t n, int64_t k, int64_t group_size,
+                  uint8_t* packed, uint16_t* scale_bits, void* stream);
+
+/* Dequantize to bf16 bits out [n, k]: bf16(q * s), bit-exact. Replaces
+ * _unpack_int4_rows / QuantizedLoRALinear.base_weight,
+ * src/representax/models/adapters.py:68-79,141-148. */
+int rpx_int4_dequant(const uint8_t* packed, const uint16_t* scale_bits, int64_t n, int64_t k,
+                     int64_t group_size, uint16_t* out, void* stream);
+
+/* Merged float32 export weight out [n, k] = f32(W_b) + (B @ A) * scaling with
+ * float32 masters lora_a [rank, k], lora_b [n, rank]. Replaces
+ * QuantizedLoRALinear.merged_weight, src/representax/models/adapters.py:150-156. */
+int rpx_int4_merge(const uint8_t* packed, const uint16_t* scale_bits, const float* lora_a,
+                   const float* lora_b, int64_t n, int64_t k, int64_t group_size, int64_t rank,
+                   float scaling, float* out, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * INT4 base + LoRA linear. `dtype` is the compute dtype of x, the LoRA compute
+ * views lora_a [rank, k] / lora_b [n, rank], y, h, grad and dx. `scaling` is
+ * alpha / rank; it is rounded to the compute dtype like the reference's weakly
+ * typed Python scalar. bias_bits (bf16 bits [n]) may be NULL.
+ * ------------------------------------------------------------------------- */
+
+size_t rpx_int4lora_forward_workspace(int64_t m, int64_t n, int64_t k, int64_t group_size,
+                                      int64_t rank, int dtype);
+
+/* y [m, n] = x W_b^T + ((x A^T) B^T) * scaling (+ bias), h [m, rank] = x A^T,
+ * with the reference's rounding points. Replaces QuantizedLoRALinear.__call__,
+ * src/representax/models/adapters.py:158-182. */
+int rpx_int4lora_forward(const void* x, int dtype, int64_t m, int64_t k, const uint8_t* packed,
+                         const uint16_t* scale_bits, int64_t n, int64_t group_size,
+                         const uint16_t* bias_bits, const void* lora_a, const void* lora_b,
+                         int64_t rank, float scaling, void* y, void* h, void* workspace,
+                         size_t workspace_bytes, void* stream);
+
+size_t rpx_int4lora_backward_workspace(int64_t m, int64_t n, int64_t k, int64_t group_size,
+                                       int64_t rank, int dtype);
+
+/* dx [m, k], d_lora_a f32 [rank, k], d_lora_b f32 [n, rank] from grad [m, n]
+ * and the forward's h. Replaces JAX's transpose of
+ * src/representax/models/adapters.py:162-181 (the reference has no
+ * hand-written VJP for this path). */
+int rpx_int4lora_backward(const void* grad, const void* x, int dtype, int64_t m, int64_t k,
+                          const uint8_t* packed, const uint16_t* scale_bits, int64_t n,
+                          int64_t group_size, const void* lora_a, const void* lora_b,
+                          int64_t rank, float scaling, const void* h, void* dx, float* d_lora_a,
+                          float* d_lora_b, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Dynamically scaled fp8.
+ * ------------------------------------------------------------------------- */
+
+size_t rpx_fp8_scale_workspace(int64_t numel);
+
+/* scale_out[0] = max(max|t| / fmax, FLT_MIN) over numel dense elements (NaN
+ * propagates). Replaces the scale half of _scaled_quantize,
+ * src/representax/precision.py:133-139. */
+int rpx_fp8_scale(const void* t, int dtype, int64_t numel, int fmt, float* scale_out,
+                  void* workspace, size_t workspace_bytes, void* stream);
+
+/* codes = f8(f32(t) / scale) for the logical matrix t[r * row_stride +
+ * c * col_stride] (rows x cols); writes out [rows, cols] and/or out_t
+ * [cols, rows] (either may be NULL). Replaces the cast half of
+ * _scaled_quantize, src/representax/precision.py:140. */
+int rpx_fp8_cast(const void* t, int dtype, int64_t rows, int64_t cols, int64_t row_stride,
+                 int64_t col_stride, const float* scale, int fmt, uint8_t* out, uint8_t* out_t,
+                 void* stream);
+
+size_t rpx_fp8_gemm_workspace(int64_t m, int64_t n, int64_t k);
+
+/* out [m, n] = ((a [m, k] . b [n, k]^T) * scale_a) * scale_b on fp8 codes, f32
+ * accumulate. Replaces the dot_general + rescale of _scaled_fp8_dot,
+ * src/representax/precision.py:154-170. */
+int rpx_fp8_gemm(const uint8_t* a, int fmt_a, const float* scale_a, const uint8_t* b, int fmt_b,
+                 const float* scale_b, int64_t m, int64_t n, int64_t k, void* out, int out_dtype,
+                 void* workspace, size_t workspace_bytes, void* stream);
+
+size_t rpx_fp8_linear_forward_workspace(int64_t m, int64_t n, int64_t k);
+
+/* out [m, n] = _fp8_linear_dot(left [m, k], right [k, n]) with e4m3 operands;
+ * right is addressed through (row_stride, col_stride) so a transposed weight
+ * view needs no copy. scales_out[0..1] receive (s_left, s_right) for the
+ * backward. Replaces _fp8_linear_dot / _fp8_linear_dot_forward,
+ * src/representax/precision.py:173-198 (as used by linear_matmul, :224-239). */
+int rpx_fp8_linear_forward(const void* left, int left_dtype, int64_t m, int64_t k,
+                           const void* right, int right_dtype, int64_t n, int64_t right_row_stride,
+                           int64_t right_col_stride, void* out, int out_dtype, float* scales_out,
+                           void* workspace, size_t workspace_bytes, void* stream);
+
+size_t rpx_fp8_linear_backward_workspace(int64_t m, int64_t n, int64_t k);
+
+/* d_left [m, k] = scaled_dot(g[e5m2], right^T[e4m3]) and d_right =
+ * scaled_dot(left^T[e4m3], g[e5m2]) as [k, n], or as [n, k] when
+ * d_right_transposed; either output may be NULL to skip it. `scales` are the
+ * forward's (s_left, s_right). m, n, k must be positive.
+ * Replaces _fp8_linear_dot_backward, src/representax/precision.py:201-218. */
+int rpx_fp8_linear_backward(const void* left, int left_dtype, const void* right, int right_dtype,
+                            int64_t m, int64_t k, int64_t n, int64_t right_row_stride,
+                            int64_t right_col_stride, const void* grad, int grad_dtype,
+                            const float* scales, void* d_left, void* d_right,
+                            int d_right_transposed, int out_dtype, void* workspace,
+                            size_t workspace_bytes, void* stream);
+
+/* Host-side test hook: the device quantizer (divide by scale, round to fp8)
+ * run on host memory, so that it can be checked exhaustively on a CPU. No
+ * reference counterpart. */
+int rpx_host_fp8_quantize(const float* host_in, int64_t n, float scale, int fmt,
+                          uint8_t* host_out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* REPRESENTAX_AMD_H_ */

@@ -1,0 +1,38 @@
+"""CPU oracle for representax's quantized-linear path.
+
+TEST INFRASTRUCTURE ONLY. This package restates, in numpy with bit-level
+codecs, the numerics of
+
+* ``src/representax/models/adapters.py:30-79,141-182`` (bf16 bit casts, the
+  per-output-row INT4 packer and unpacker, the INT4-LoRA forward and its JAX
+  autodiff transpose), and
+* ``src/representax/precision.py:127-239`` (dynamic amax scaling, OCP fp8
+  casts, the scaled fp8 dot and its custom VJP),
+
+so that tests, the smoke check and the benchmark's CPU-baseline leg can check
+the HIP kernels of ``representax_amd``. Nothing in the product imports it; the
+product fails loudly when its HIP library is missing instead of falling back
+here.
+
+Pinning (what checks each function against something other than itself):
+
+* ``codecs``: bf16 and fp8 casts are compared with torch's own
+  ``bfloat16``/``float8_e4m3fn``/``float8_e5m2`` conversions (a library
+  routine) over every bf16 bit pattern, every fp8 code, and boundary sweeps;
+  the decoders are compared with the OCP fp8 closed form.
+* ``int4``: hand-built known answers (zero rows, ties-to-even, clipping,
+  odd K padding, nibble order), exhaustive unpack over all 256 byte values,
+  and the pack/unpack round-trip bound.
+* ``lora``: forward compared with the merged-weight closed form and an fp64
+  brute-force loop on tiny shapes; backward compared with central finite
+  differences of the fp64 forward and with closed-form identities.
+* ``fp8``: amax/scale closed forms (zero, inf, NaN tensors), cast through the
+  torch-pinned codec, dot compared with an fp64 product of the exactly decoded
+  operands, VJP compared with the transposed-product identities.
+
+Parity unpinned (no reference test or fixture fixes these bits, and the
+reference cannot run here): XLA:CPU's accumulation order of bf16 dots, whether
+its f32->f8 convert rounds directly or through f16, and whether bf16-typed
+elementwise ops keep excess precision. The oracle takes the HLO-typed reading:
+every bf16-typed op rounds once to nearest-even and f32->f8 rounds directly.
+"""

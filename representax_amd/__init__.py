@@ -1,0 +1,50 @@
+"""MI355X-native implementation of representax's quantized-linear path.
+
+Public API mirrors the reference (``representax.models.adapters``,
+``representax.precision``, ``representax.config``): ``QuantizedLoRALinear``,
+``apply_quantized_lora``, ``merge_quantized_lora``, ``lora_parameter_filter``,
+``Linear``, ``linear_matmul``, ``precision_context``, ``PrecisionConfig``,
+``QuantizedLoRAConfig``. The arithmetic runs in hand-written gfx950 HIP
+kernels (``librepresentax_amd.so``, C ABI in ``include/representax_amd.h``).
+"""
+
+from .adapters import (
+    QuantizedLoRALinear,
+    apply_quantized_lora,
+    lora_parameter_filter,
+    lora_parameters,
+    matched_linear_paths,
+    merge_quantized_lora,
+)
+from .components import Linear
+from .config import PrecisionConfig, QuantizedLoRAConfig
+from .precision import (
+    FP32_POLICY,
+    PrecisionPolicy,
+    activation_inputs,
+    active_compute_dtype,
+    compute_parameter,
+    linear_matmul,
+    precision_context,
+    resolve_precision_policy,
+)
+
+__all__ = [
+    "FP32_POLICY",
+    "Linear",
+    "PrecisionConfig",
+    "PrecisionPolicy",
+    "QuantizedLoRAConfig",
+    "QuantizedLoRALinear",
+    "activation_inputs",
+    "active_compute_dtype",
+    "apply_quantized_lora",
+    "compute_parameter",
+    "linear_matmul",
+    "lora_parameter_filter",
+    "lora_parameters",
+    "matched_linear_paths",
+    "merge_quantized_lora",
+    "precision_context",
+    "resolve_precision_policy",
+]

@@ -1,0 +1,113 @@
+"""ctypes binding of ``librepresentax_amd.so`` (the C ABI in include/).
+
+``import torch`` happens first on purpose: torch's ROCm wheel ships its own
+HIP runtime under the same soname, so the library binds to that one runtime
+and torch's streams and device pointers are valid inside it.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import torch  # noqa: F401  (load torch's HIP runtime before the library)
+
+LIB_PATH = Path(__file__).resolve().parent / "_lib" / "librepresentax_amd.so"
+
+RPX_OK = 0
+RPX_ERR_INVALID = 1
+RPX_ERR_HIP = 2
+DTYPE_F32 = 0
+DTYPE_BF16 = 1
+FP8_E4M3FN = 0
+FP8_E5M2 = 1
+
+_p = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
+_f32 = ctypes.c_float
+_size = ctypes.c_size_t
+
+# name -> (restype, argtypes); mirrors include/representax_amd.h
+SIGNATURES: dict[str, tuple[object, list[object]]] = {
+    "rpx_last_error": (ctypes.c_char_p, []),
+    "rpx_abi_version": (_int, []),
+    "rpx_int4_pack": (_int, [_p, _int, _i64, _i64, _i64, _p, _p, _p]),
+    "rpx_int4_dequant": (_int, [_p, _p, _i64, _i64, _i64, _p, _p]),
+    "rpx_int4_merge": (_int, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _f32, _p, _p]),
+    "rpx_int4lora_forward_workspace": (_size, [_i64, _i64, _i64, _i64, _i64, _int]),
+    "rpx_int4lora_forward": (
+        _int,
+        [_p, _int, _i64, _i64, _p, _p, _i64, _i64, _p, _p, _p, _i64, _f32, _p, _p, _p, _size, _p],
+    ),
+    "rpx_int4lora_backward_workspace": (_size, [_i64, _i64, _i64, _i64, _i64, _int]),
+    "rpx_int4lora_backward": (
+        _int,
+        [_p, _p, _int, _i64, _i64, _p, _p, _i64, _i64, _p, _p, _i64, _f32, _p, _p, _p, _p, _p,
+         _size, _p],
+    ),
+    "rpx_fp8_scale_workspace": (_size, [_i64]),
+    "rpx_fp8_scale": (_int, [_p, _int, _i64, _int, _p, _p, _size, _p]),
+    "rpx_fp8_cast": (_int, [_p, _int, _i64, _i64, _i64, _i64, _p, _int, _p, _p, _p]),
+    "rpx_fp8_gemm_workspace": (_size, [_i64, _i64, _i64]),
+    "rpx_fp8_gemm": (
+        _int, [_p, _int, _p, _p, _int, _p, _i64, _i64, _i64, _p, _int, _p, _size, _p]
+    ),
+    "rpx_fp8_linear_forward_workspace": (_size, [_i64, _i64, _i64]),
+    "rpx_fp8_linear_forward": (
+        _int, [_p, _int, _i64, _i64, _p, _int, _i64, _i64, _i64, _p, _int, _p, _p, _size, _p]
+    ),
+    "rpx_fp8_linear_backward_workspace": (_size, [_i64, _i64, _i64]),
+    "rpx_fp8_linear_backward": (
+        _int,
+        [_p, _int, _p, _int, _i64, _i64, _i64, _i64, _i64, _p, _int, _p, _p, _p, _int, _int, _p,
+         _size, _p],
+    ),
+    "rpx_host_fp8_quantize": (_int, [_p, _i64, _f32, _int, _p]),
+}
+
+
+class NativeError(RuntimeError):
+    """A HIP-side failure reported by the library."""
+
+
+_LIB: ctypes.CDLL | None = None
+
+
+def load() -> ctypes.CDLL:
+    """Load the library, or raise: there is no fallback implementation."""
+
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    path = Path(os.environ.get("RPX_LIBRARY", LIB_PATH))
+    if not path.exists():
+        raise ImportError(
+            f"{path} is missing; build it with `python -m representax_amd.build` "
+            "(the quantized-linear path has no non-HIP implementation)"
+        )
+    lib = ctypes.CDLL(str(path))
+    for name, (restype, argtypes) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    _LIB = lib
+    return lib
+
+
+def check(status: int) -> None:
+    if status == RPX_OK:
+        return
+    msg = (load().rpx_last_error() or b"").decode(errors="replace")
+    if status == RPX_ERR_INVALID:
+        raise ValueError(msg)
+    raise NativeError(msg)
+
+
+def call(name: str, *args) -> None:
+    check(getattr(load(), name)(*args))
+
+
+def query(name: str, *args) -> int:
+    return int(getattr(load(), name)(*args))

@@ -1,0 +1,732 @@
+// C-ABI of librepresentax_amd: validation, workspace planning and launch
+// sequencing for the quantized-linear path. No entry point allocates device
+// memory or synchronizes; every launch goes to the caller's stream.
+#include <cstring>
+#include <string>
+
+#include "../../include/representax_amd.h"
+#include "common.h"
+#include "kernels.h"
+
+namespace rpx {
+
+namespace {
+thread_local std::string g_last_error;
+
+// Bump allocator over a caller-provided workspace.
+struct Arena {
+  uint8_t* base;
+  size_t cap;
+  size_t used = 0;
+  bool overflow = false;
+  Arena(void* p, size_t c) : base(static_cast<uint8_t*>(p)), cap(c) {}
+  template <typename T>
+  T* take(int64_t count) {
+    const size_t bytes = (static_cast<size_t>(count) * sizeof(T) + 255) & ~static_cast<size_t>(255);
+    if (used + bytes > cap) {
+      overflow = true;
+      return nullptr;
+    }
+    T* p = reinterpret_cast<T*>(base + used);
+    used += bytes;
+    return p;
+  }
+};
+
+// Size-only twin of Arena.
+struct Sizer {
+  size_t used = 0;
+  template <typename T>
+  void take(int64_t count) {
+    used += (static_cast<size_t>(count) * sizeof(T) + 255) & ~static_cast<size_t>(255);
+  }
+};
+
+size_t elem_size(int dtype) { return dtype == kBF16 ? 2 : 4; }
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+bool pow2(int64_t v) { return v > 0 && (v & (v - 1)) == 0; }
+
+float round_to_dtype(float v, int dtype) {
+  if (dtype != kBF16) return v;
+  uint32_t u;
+  std::memcpy(&u, &v, 4);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return v;
+  u = (u + 0x7FFFu + ((u >> 16) & 1u)) & 0xFFFF0000u;
+  float r;
+  std::memcpy(&r, &u, 4);
+  return r;
+}
+
+int check_int4_shape(int64_t n, int64_t k, int64_t group_size, int64_t* n_groups, int64_t* group) {
+  if (n < 0 || k <= 0) return fail_invalid("INT4 weight needs n >= 0 and k > 0");
+  if (group_size <= 0 || group_size == k) {
+    *n_groups = 1;
+    *group = k;
+    return kOk;
+  }
+  if (k % group_size != 0) return fail_invalid("group_size must divide the input size");
+  if (group_size % 2 != 0) return fail_invalid("group_size must be even");
+  *n_groups = k / group_size;
+  *group = group_size;
+  return kOk;
+}
+
+int check_dtype(int dtype) {
+  if (dtype != kF32 && dtype != kBF16) return fail_invalid("dtype must be RPX_DTYPE_F32 or RPX_DTYPE_BF16");
+  return kOk;
+}
+
+int check_fmt(int fmt) {
+  if (fmt != kE4M3FN && fmt != kE5M2) return fail_invalid("fp8 format must be RPX_FP8_E4M3FN or RPX_FP8_E5M2");
+  return kOk;
+}
+
+#define RPX_TRY(expr)            \
+  do {                           \
+    const int _rc = (expr);      \
+    if (_rc != kOk) return _rc;  \
+  } while (0)
+
+#define RPX_HIP(expr, what) RPX_TRY(check_hip((expr), (what)))
+
+// --- INT4 + LoRA path selection -------------------------------------------
+bool lora_fast_shape(int dtype, int64_t k, int64_t n_groups, int64_t group, int64_t rank) {
+  if (dtype != kBF16) return false;
+  if (k % 64 != 0) return false;
+  if (rank < 1 || rank > 64) return false;
+  if (n_groups > 1 && !(pow2(group) && group >= 32)) return false;
+  return true;
+}
+
+template <typename A>
+void plan_forward(A& a, bool fast, int64_t m, int64_t n, int64_t k, int64_t rank) {
+  (void)k;
+  (void)rank;
+  if (fast) return;
+  a.template take<float>(m * n);  // base product
+  a.template take<float>(m * n);  // adapter product
+  a.template take<float>(m * rank);
+}
+
+template <typename A>
+void plan_backward(A& a, bool fast, int64_t m, int64_t n, int64_t k, int64_t rank, int dtype) {
+  if (fast) {
+    a.template take<uint16_t>(rank * n);  // B^T
+    a.template take<uint16_t>(m * rank);  // dh
+    a.template take<uint16_t>(k * n);     // W_b^T
+    int64_t part = rank_tn_workspace_floats(m, n, rank);
+    const int64_t part_a = rank_tn_workspace_floats(m, rank, k);
+    if (part_a > part) part = part_a;
+    a.template take<float>(part);
+    return;
+  }
+  a.template take<uint8_t>(m * n * static_cast<int64_t>(elem_size(dtype)));  // g_a
+  a.template take<uint8_t>(m * rank * static_cast<int64_t>(elem_size(dtype)));  // dh
+  a.template take<float>(m * rank);  // dh (f32 product)
+  a.template take<float>(m * k);     // g W
+  a.template take<float>(m * k);     // dh A
+}
+
+__global__ void __launch_bounds__(256)
+    k_lora_combine(const float* __restrict__ base, const float* __restrict__ lowrank,
+                   int64_t rows, int64_t cols, float scale, const uint16_t* __restrict__ bias,
+                   int dtype, void* __restrict__ out) {
+  const int64_t total = rows * cols;
+  for (int64_t e = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; e < total;
+       e += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    float y;
+    if (dtype == kBF16) {
+      y = round_bf16(round_bf16(base[e]) + round_bf16(round_bf16(lowrank[e]) * scale));
+      if (bias != nullptr) y = round_bf16(y + bf16_to_f32(bias[e % cols]));
+      static_cast<uint16_t*>(out)[e] = f32_to_bf16(y);
+    } else {
+      y = base[e] + lowrank[e] * scale;
+      if (bias != nullptr) y = y + bf16_to_f32(bias[e % cols]);
+      static_cast<float*>(out)[e] = y;
+    }
+  }
+}
+
+__global__ void __launch_bounds__(256)
+    k_scale_round(const void* __restrict__ in, int64_t n, float scale, int dtype,
+                  void* __restrict__ out) {
+  for (int64_t e = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; e < n;
+       e += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    if (dtype == kBF16) {
+      const float v = bf16_to_f32(static_cast<const uint16_t*>(in)[e]) * scale;
+      static_cast<uint16_t*>(out)[e] = f32_to_bf16(v);
+    } else {
+      static_cast<float*>(out)[e] = static_cast<const float*>(in)[e] * scale;
+    }
+  }
+}
+
+__global__ void __launch_bounds__(256)
+    k_round_inplace_f32(float* __restrict__ buf, int64_t n, int dtype) {
+  for (int64_t e = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; e < n;
+       e += static_cast<int64_t>(gridDim.x) * blockDim.x)
+    if (dtype == kBF16) buf[e] = round_bf16(buf[e]);
+}
+
+int grid1d(int64_t work) {
+  int64_t g = ceil_div(work, 256);
+  if (g > 8192) g = 8192;
+  if (g < 1) g = 1;
+  return static_cast<int>(g);
+}
+
+}  // namespace
+
+void set_error(const std::string& msg) { g_last_error = msg; }
+
+int fail_invalid(const std::string& msg) {
+  g_last_error = msg;
+  return kErrInvalid;
+}
+
+int check_hip(hipError_t err, const char* what) {
+  if (err == hipSuccess) return kOk;
+  g_last_error = std::string(what) + ": " + hipGetErrorString(err);
+  return kErrHip;
+}
+
+}  // namespace rpx
+
+using namespace rpx;
+
+extern "C" {
+
+const char* rpx_last_error(void) { return g_last_error.c_str(); }
+
+int rpx_abi_version(void) { return RPX_ABI_VERSION; }
+
+// ---------------------------------------------------------------------------
+// INT4 codec
+// ---------------------------------------------------------------------------
+int rpx_int4_pack(const void* weight, int dtype, int64_t n, int64_t k, int64_t group_size,
+                  uint8_t* packed, uint16_t* scale_bits, void* stream) {
+  RPX_TRY(check_dtype(dtype));
+  int64_t ng, g;
+  RPX_TRY(check_int4_shape(n, k, group_size, &ng, &g));
+  if (n > 0 && (weight == nullptr || packed == nullptr || scale_bits == nullptr))
+    return fail_invalid("rpx_int4_pack: null pointer");
+  RPX_HIP(launch_int4_pack(weight, dtype, packed, scale_bits, n, k, (k + 1) / 2, ng, g,
+                           static_cast<hipStream_t>(stream)),
+          "rpx_int4_pack");
+  return kOk;
+}
+
+int rpx_int4_dequant(const uint8_t* packed, const uint16_t* scale_bits, int64_t n, int64_t k,
+                     int64_t group_size, uint16_t* out, void* stream) {
+  int64_t ng, g;
+  RPX_TRY(check_int4_shape(n, k, group_size, &ng, &g));
+  if (n > 0 && (packed == nullptr || scale_bits == nullptr || out == nullptr))
+    return fail_invalid("rpx_int4_dequant: null pointer");
+  RPX_HIP(launch_int4_dequant(packed, scale_bits, out, n, k, (k + 1) / 2, ng, g,
+                              static_cast<hipStream_t>(stream)),
+          "rpx_int4_dequant");
+  return kOk;
+}
+
+int rpx_int4_merge(const uint8_t* packed, const uint16_t* scale_bits, const float* lora_a,
+                   const float* lora_b, int64_t n, int64_t k, int64_t group_size, int64_t rank,
+                   float scaling, float* out, void* stream) {
+  int64_t ng, g;
+  RPX_TRY(check_int4_shape(n, k, group_size, &ng, &g));
+  if (rank < 0) return fail_invalid("rank must be non-negative");
+  if (n > 0 && (packed == nullptr || scale_bits == nullptr || out == nullptr ||
+                (rank > 0 && (lora_a == nullptr || lora_b == nullptr))))
+    return fail_invalid("rpx_int4_merge: null pointer");
+  RPX_HIP(launch_int4_merge(packed, scale_bits, lora_a, lora_b, out, n, k, (k + 1) / 2, ng, g,
+                            rank, scaling, static_cast<hipStream_t>(stream)),
+          "rpx_int4_merge");
+  return kOk;
+}
+
+// ---------------------------------------------------------------------------
+// INT4 + LoRA linear
+// ---------------------------------------------------------------------------
+size_t rpx_int4lora_forward_workspace(int64_t m, int64_t n, int64_t k, int64_t group_size,
+                                      int64_t rank, int dtype) {
+  int64_t ng = 1, g = k;
+  if (group_size > 0 && group_size != k && k % group_size == 0) {
+    ng = k / group_size;
+    g = group_size;
+  }
+  Sizer s;
+  plan_forward(s, lora_fast_shape(dtype, k, ng, g, rank), m, n, k, rank);
+  return s.used;
+}
+
+int rpx_int4lora_forward(const void* x, int dtype, int64_t m, int64_t k, const uint8_t* packed,
+                         const uint16_t* scale_bits, int64_t n, int64_t group_size,
+                         const uint16_t* bias_bits, const void* lora_a, const void* lora_b,
+                         int64_t rank, float scaling, void* y, void* h, void* workspace,
+                         size_t workspace_bytes, void* stream) {
+  RPX_TRY(check_dtype(dtype));
+  int64_t ng, g;
+  RPX_TRY(check_int4_shape(n, k, group_size, &ng, &g));
+  if (m < 0) return fail_invalid("m must be non-negative");
+  if (rank < 1 || rank > n || rank > k) return fail_invalid("adapter rank must fit both linear dimensions");
+  if (m == 0 || n == 0) return kOk;
+  if (x == nullptr || packed == nullptr || scale_bits == nullptr || lora_a == nullptr ||
+      lora_b == nullptr || y == nullptr || h == nullptr)
+    return fail_invalid("rpx_int4lora_forward: null pointer");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const float c = round_to_dtype(scaling, dtype);
+  const int64_t pc = (k + 1) / 2;
+  Int4Operand w;
+  w.packed = packed;
+  w.packed_cols = pc;
+  w.scales = scale_bits;
+  w.n_groups = ng;
+  w.group = g;
+  const bool fast = lora_fast_shape(dtype, k, ng, g, rank) && aligned16(x) && aligned16(packed) &&
+                    aligned16(lora_a) && aligned16(y);
+  Arena arena(workspace, workspace_bytes);
+  if (fast) {
+    const uint16_t* xb = static_cast<const uint16_t*>(x);
+    uint16_t* hb = static_cast<uint16_t*>(h);
+    RPX_HIP(launch_rank_nt(xb, k, static_cast<const uint16_t*>(lora_a), k, m, rank, k, false, 1.0f,
+                           hb, rank, st),
+            "int4lora_forward: adapter down-projection");
+    LowRankEpilogue epi;
+    epi.rows = static_cast<const uint16_t*>(lora_b);
+    epi.rows_sn = rank;
+    epi.rows_sj = 1;
+    epi.cols = hb;
+    epi.cols_sm = rank;
+    epi.cols_sj = 1;
+    epi.rank = rank;
+    epi.scale = c;
+    epi.bias = bias_bits;
+    RPX_HIP(launch_gemm_int4(xb, k, w, m, n, k, static_cast<uint16_t*>(y), n, epi, st),
+            "int4lora_forward: fused dequant GEMM");
+    return kOk;
+  }
+  float* base = arena.take<float>(m * n);
+  float* low = arena.take<float>(m * n);
+  float* hf = arena.take<float>(m * rank);
+  if (arena.overflow) return fail_invalid("rpx_int4lora_forward: workspace too small");
+  RPX_HIP(launch_generic_gemm(x, dtype, k, 1, nullptr, dtype, 0, 0, &w, false, m, n, k, base, st),
+          "int4lora_forward: base product");
+  RPX_HIP(launch_generic_gemm(x, dtype, k, 1, lora_a, dtype, k, 1, nullptr, false, m, rank, k, hf,
+                              st),
+          "int4lora_forward: adapter down-projection");
+  RPX_HIP(launch_round_store(hf, m * rank, dtype, h, st), "int4lora_forward: round h");
+  RPX_HIP(launch_generic_gemm(h, dtype, rank, 1, lora_b, dtype, rank, 1, nullptr, false, m, n,
+                              rank, low, st),
+          "int4lora_forward: adapter up-projection");
+  hipLaunchKernelGGL(k_lora_combine, dim3(grid1d(m * n)), dim3(256), 0, st, base, low, m, n, c,
+                     bias_bits, dtype, y);
+  RPX_HIP(hipGetLastError(), "int4lora_forward: combine");
+  return kOk;
+}
+
+size_t rpx_int4lora_backward_workspace(int64_t m, int64_t n, int64_t k, int64_t group_size,
+                                       int64_t rank, int dtype) {
+  int64_t ng = 1, g = k;
+  if (group_size > 0 && group_size != k && k % group_size == 0) {
+    ng = k / group_size;
+    g = group_size;
+  }
+  Sizer s;
+  plan_backward(s, lora_fast_shape(dtype, k, ng, g, rank) && n % 64 == 0, m, n, k, rank, dtype);
+  return s.used;
+}
+
+int rpx_int4lora_backward(const void* grad, const void* x, int dtype, int64_t m, int64_t k,
+                          const uint8_t* packed, const uint16_t* scale_bits, int64_t n,
+                          int64_t group_size, const void* lora_a, const void* lora_b,
+                          int64_t rank, float scaling, const void* h, void* dx, float* d_lora_a,
+                          float* d_lora_b, void* workspace, size_t workspace_bytes,
+                          void* stream) {
+  RPX_TRY(check_dtype(dtype));
+  int64_t ng, g;
+  RPX_TRY(check_int4_shape(n, k, group_size, &ng, &g));
+  if (m < 0) return fail_invalid("m must be non-negative");
+  if (rank < 1 || rank > n || rank > k) return fail_invalid("adapter rank must fit both linear dimensions");
+  if (grad == nullptr && m > 0) return fail_invalid("rpx_int4lora_backward: null gradient");
+  if (x == nullptr || packed == nullptr || scale_bits == nullptr || lora_a == nullptr ||
+      lora_b == nullptr || dx == nullptr || d_lora_a == nullptr || d_lora_b == nullptr ||
+      (h == nullptr && m > 0))
+    return fail_invalid("rpx_int4lora_backward: null pointer");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (m == 0) {
+    RPX_HIP(launch_fill_f32(d_lora_a, rank * k, 0.0f, st), "int4lora_backward: zero dA");
+    RPX_HIP(launch_fill_f32(d_lora_b, n * rank, 0.0f, st), "int4lora_backward: zero dB");
+    return kOk;
+  }
+  const float c = round_to_dtype(scaling, dtype);
+  const int64_t pc = (k + 1) / 2;
+  Int4Operand w;
+  w.packed = packed;
+  w.packed_cols = pc;
+  w.scales = scale_bits;
+  w.n_groups = ng;
+  w.group = g;
+  const bool fast = lora_fast_shape(dtype, k, ng, g, rank) && n % 64 == 0 && aligned16(grad) &&
+                    aligned16(x) && aligned16(dx) && aligned16(lora_b);
+  Arena arena(workspace, workspace_bytes);
+  if (fast) {
+    const uint16_t* gb = static_cast<const uint16_t*>(grad);
+    const uint16_t* xb = static_cast<const uint16_t*>(x);
+    const uint16_t* ab = static_cast<const uint16_t*>(lora_a);
+    const uint16_t* bb = static_cast<const uint16_t*>(lora_b);
+    uint16_t* bt = arena.take<uint16_t>(rank * n);
+    uint16_t* dh = arena.take<uint16_t>(m * rank);
+    uint16_t* wt = arena.take<uint16_t>(k * n);
+    int64_t part_n = rank_tn_workspace_floats(m, n, rank);
+    const int64_t part_a = rank_tn_workspace_floats(m, rank, k);
+    if (part_a > part_n) part_n = part_a;
+    float* part = arena.take<float>(part_n);
+    if (arena.overflow) return fail_invalid("rpx_int4lora_backward: workspace too small");
+    // B^T [r, N] so that dh = g_a . B is an NT product
+    RPX_HIP(launch_transpose_bf16(bb, n, rank, rank, bt, n, st), "int4lora_backward: B^T");
+    // dh = bf16(bf16(g * c) . B)
+    RPX_HIP(launch_rank_nt(gb, n, bt, n, m, rank, n, true, c, dh, rank, st),
+            "int4lora_backward: dh");
+    // dB = f32(bf16(g_a^T . h))
+    RPX_HIP(launch_rank_tn(gb, n, static_cast<const uint16_t*>(h), rank, m, n, rank, true, c, part,
+                           d_lora_b, st),
+            "int4lora_backward: dB");
+    // W_b^T [K, N]
+    RPX_HIP(launch_int4_dequant_t(packed, scale_bits, wt, n, k, pc, ng, g, n, st),
+            "int4lora_backward: dequantized transpose");
+    // dx = bf16(bf16(g . W_b) + bf16(dh . A))
+    LowRankEpilogue epi;
+    epi.rows = ab;  // R(k, j) = A[j, k]
+    epi.rows_sn = 1;
+    epi.rows_sj = k;
+    epi.cols = dh;
+    epi.cols_sm = rank;
+    epi.cols_sj = 1;
+    epi.rank = rank;
+    epi.scale = 1.0f;
+    RPX_HIP(launch_gemm_bf16(gb, n, wt, n, m, k, n, static_cast<uint16_t*>(dx), k, epi, st),
+            "int4lora_backward: dx");
+    // dA = f32(bf16(dh^T . x))
+    RPX_HIP(launch_rank_tn(dh, rank, xb, k, m, rank, k, false, 1.0f, part, d_lora_a, st),
+            "int4lora_backward: dA");
+    return kOk;
+  }
+  const size_t es = elem_size(dtype);
+  void* ga = arena.take<uint8_t>(m * n * static_cast<int64_t>(es));
+  void* dh = arena.take<uint8_t>(m * rank * static_cast<int64_t>(es));
+  float* dhf = arena.take<float>(m * rank);
+  float* p1 = arena.take<float>(m * k);
+  float* p2 = arena.take<float>(m * k);
+  if (arena.overflow) return fail_invalid("rpx_int4lora_backward: workspace too small");
+  hipLaunchKernelGGL(k_scale_round, dim3(grid1d(m * n)), dim3(256), 0, st, grad, m * n, c, dtype,
+                     ga);
+  RPX_HIP(hipGetLastError(), "int4lora_backward: g_a");
+  // dh[m, j] = sum_n g_a[m, n] B[n, j]
+  RPX_HIP(launch_generic_gemm(ga, dtype, n, 1, lora_b, dtype, 1, rank, nullptr, false, m, rank, n,
+                              dhf, st),
+          "int4lora_backward: dh");
+  RPX_HIP(launch_round_store(dhf, m * rank, dtype, dh, st), "int4lora_backward: round dh");
+  // dB[n, j] = sum_m g_a[m, n] h[m, j]
+  RPX_HIP(launch_generic_gemm(ga, dtype, 1, n, h, dtype, 1, rank, nullptr, false, n, rank, m,
+                              d_lora_b, st),
+          "int4lora_backward: dB");
+  hipLaunchKernelGGL(k_round_inplace_f32, dim3(grid1d(n * rank)), dim3(256), 0, st, d_lora_b,
+                     n * rank, dtype);
+  RPX_HIP(hipGetLastError(), "int4lora_backward: round dB");
+  // g . W_b : B(k, n) = W_b[n, k]
+  RPX_HIP(launch_generic_gemm(grad, dtype, n, 1, nullptr, dtype, 0, 0, &w, true, m, k, n, p1, st),
+          "int4lora_backward: g W");
+  // dh . A : B(k, j) = A[j, k]
+  RPX_HIP(launch_generic_gemm(dh, dtype, rank, 1, lora_a, dtype, 1, k, nullptr, false, m, k, rank,
+                              p2, st),
+          "int4lora_backward: dh A");
+  hipLaunchKernelGGL(k_lora_combine, dim3(grid1d(m * k)), dim3(256), 0, st, p1, p2, m, k, 1.0f,
+                     nullptr, dtype, dx);
+  RPX_HIP(hipGetLastError(), "int4lora_backward: combine dx");
+  // dA[j, k] = sum_m dh[m, j] x[m, k]
+  RPX_HIP(launch_generic_gemm(dh, dtype, 1, rank, x, dtype, 1, k, nullptr, false, rank, k, m,
+                              d_lora_a, st),
+          "int4lora_backward: dA");
+  hipLaunchKernelGGL(k_round_inplace_f32, dim3(grid1d(rank * k)), dim3(256), 0, st, d_lora_a,
+                     rank * k, dtype);
+  RPX_HIP(hipGetLastError(), "int4lora_backward: round dA");
+  return kOk;
+}
+
+// ---------------------------------------------------------------------------
+// FP8
+// ---------------------------------------------------------------------------
+size_t rpx_fp8_scale_workspace(int64_t numel) {
+  return static_cast<size_t>(fp8_amax_partials(numel)) * sizeof(uint32_t);
+}
+
+int rpx_fp8_scale(const void* t, int dtype, int64_t numel, int fmt, float* scale_out,
+                  void* workspace, size_t workspace_bytes, void* stream) {
+  RPX_TRY(check_dtype(dtype));
+  RPX_TRY(check_fmt(fmt));
+  if (numel < 0) return fail_invalid("numel must be non-negative");
+  if (scale_out == nullptr || (numel > 0 && t == nullptr)) return fail_invalid("rpx_fp8_scale: null pointer");
+  const int64_t np = fp8_amax_partials(numel);
+  if (workspace == nullptr || workspace_bytes < static_cast<size_t>(np) * sizeof(uint32_t))
+    return fail_invalid("rpx_fp8_scale: workspace too small");
+  RPX_HIP(launch_fp8_amax(t, dtype, numel, 1, 1, 1, static_cast<uint32_t*>(workspace), np, fmt,
+                          scale_out, static_cast<hipStream_t>(stream)),
+          "rpx_fp8_scale");
+  return kOk;
+}
+
+int rpx_fp8_cast(const void* t, int dtype, int64_t rows, int64_t cols, int64_t row_stride,
+                 int64_t col_stride, const float* scale, int fmt, uint8_t* out, uint8_t* out_t,
+                 void* stream) {
+  RPX_TRY(check_dtype(dtype));
+  RPX_TRY(check_fmt(fmt));
+  if (rows < 0 || cols < 0) return fail_invalid("rows and cols must be non-negative");
+  if (scale == nullptr || (rows * cols > 0 && t == nullptr)) return fail_invalid("rpx_fp8_cast: null pointer");
+  if (out == nullptr && out_t == nullptr) return fail_invalid("rpx_fp8_cast: no output requested");
+  RPX_HIP(launch_fp8_cast(t, dtype, rows, cols, row_stride, col_stride, scale, fmt, out, out_t,
+                          static_cast<hipStream_t>(stream)),
+          "rpx_fp8_cast");
+  return kOk;
+}
+
+size_t rpx_fp8_gemm_workspace(int64_t m, int64_t n, int64_t k) {
+  if (k % 128 != 0) return static_cast<size_t>(m * n) * sizeof(float);
+  return static_cast<size_t>(fp8_gemm_workspace_floats(m, n, k)) * sizeof(float);
+}
+
+}  // extern "C"
+
+namespace rpx {
+namespace {
+__constant__ float c_fp8_table[2][256];
+bool g_table_ready = false;
+
+__global__ void __launch_bounds__(256)
+    k_fp8_gemm_generic(const uint8_t* __restrict__ a, int fmt_a, const uint8_t* __restrict__ b,
+                       int fmt_b, int64_t M, int64_t N, int64_t K, const float* __restrict__ s_a,
+                       const float* __restrict__ s_b, void* __restrict__ out, int out_dtype) {
+  const int64_t total = M * N;
+  for (int64_t e = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; e < total;
+       e += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t m = e / N;
+    const int64_t n = e % N;
+    float acc = 0.0f;
+    for (int64_t kk = 0; kk < K; ++kk)
+      acc = __builtin_fmaf(c_fp8_table[fmt_a][a[m * K + kk]], c_fp8_table[fmt_b][b[n * K + kk]], acc);
+    const float y = (acc * s_a[0]) * s_b[0];
+    if (out_dtype == kBF16)
+      static_cast<uint16_t*>(out)[e] = f32_to_bf16(y);
+    else
+      static_cast<float*>(out)[e] = y;
+  }
+}
+
+float decode_fp8_host(uint32_t code, int fmt) {
+  const int eb = fmt == kE4M3FN ? 4 : 5;
+  const int mb = fmt == kE4M3FN ? 3 : 2;
+  const int bias = fmt == kE4M3FN ? 7 : 15;
+  const float sign = (code & 0x80u) ? -1.0f : 1.0f;
+  const uint32_t e = (code >> mb) & ((1u << eb) - 1u);
+  const uint32_t mnt = code & ((1u << mb) - 1u);
+  const uint32_t all = (1u << eb) - 1u;
+  if (fmt == kE5M2 && e == all) return mnt == 0 ? sign * __builtin_inff() : __builtin_nanf("");
+  if (fmt == kE4M3FN && e == all && mnt == (1u << mb) - 1u) return __builtin_nanf("");
+  if (e == 0) return sign * static_cast<float>(mnt) * __builtin_ldexpf(1.0f, 1 - bias - mb);
+  return sign * (1.0f + static_cast<float>(mnt) / static_cast<float>(1u << mb)) *
+         __builtin_ldexpf(1.0f, static_cast<int>(e) - bias);
+}
+
+int ensure_fp8_table() {
+  if (g_table_ready) return kOk;
+  float host[2][256];
+  for (int f = 0; f < 2; ++f)
+    for (int c = 0; c < 256; ++c) host[f][c] = decode_fp8_host(static_cast<uint32_t>(c), f);
+  RPX_HIP(hipMemcpyToSymbol(HIP_SYMBOL(c_fp8_table), host, sizeof(host)), "fp8 decode table");
+  g_table_ready = true;
+  return kOk;
+}
+}  // namespace
+}  // namespace rpx
+
+extern "C" {
+
+int rpx_fp8_gemm(const uint8_t* a, int fmt_a, const float* scale_a, const uint8_t* b, int fmt_b,
+                 const float* scale_b, int64_t m, int64_t n, int64_t k, void* out, int out_dtype,
+                 void* workspace, size_t workspace_bytes, void* stream) {
+  RPX_TRY(check_fmt(fmt_a));
+  RPX_TRY(check_fmt(fmt_b));
+  RPX_TRY(check_dtype(out_dtype));
+  if (m < 0 || n < 0 || k < 0) return fail_invalid("m, n, k must be non-negative");
+  if (m == 0 || n == 0) return kOk;
+  if (a == nullptr || b == nullptr || scale_a == nullptr || scale_b == nullptr || out == nullptr)
+    return fail_invalid("rpx_fp8_gemm: null pointer");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool fast = k > 0 && k % 128 == 0 && aligned16(a) && aligned16(b);
+  if (fast) {
+    const int64_t need = fp8_gemm_workspace_floats(m, n, k);
+    if (static_cast<size_t>(need) * sizeof(float) > workspace_bytes || (need > 0 && workspace == nullptr))
+      return fail_invalid("rpx_fp8_gemm: workspace too small");
+    RPX_HIP(launch_fp8_gemm(a, fmt_a, scale_a, b, fmt_b, scale_b, m, n, k, out, out_dtype, n,
+                            static_cast<float*>(workspace), need, st),
+            "rpx_fp8_gemm");
+    return kOk;
+  }
+  RPX_TRY(ensure_fp8_table());
+  hipLaunchKernelGGL(k_fp8_gemm_generic, dim3(grid1d(m * n)), dim3(256), 0, st, a, fmt_a, b, fmt_b,
+                     m, n, k, scale_a, scale_b, out, out_dtype);
+  RPX_HIP(hipGetLastError(), "rpx_fp8_gemm (generic)");
+  return kOk;
+}
+
+}  // extern "C"
+
+namespace {
+template <typename A>
+void plan_fp8_forward(A& a, int64_t m, int64_t n, int64_t k) {
+  a.template take<uint32_t>(fp8_amax_partials(m * k));
+  a.template take<uint32_t>(fp8_amax_partials(k * n));
+  a.template take<uint8_t>(m * k);
+  a.template take<uint8_t>(n * k);
+  a.template take<uint8_t>(rpx_fp8_gemm_workspace(m, n, k));
+}
+template <typename A>
+void plan_fp8_backward(A& a, int64_t m, int64_t n, int64_t k) {
+  a.template take<uint32_t>(fp8_amax_partials(m * n));
+  a.template take<float>(1);
+  a.template take<uint8_t>(m * n);  // g codes [M, N]
+  a.template take<uint8_t>(n * m);  // g codes [N, M]
+  a.template take<uint8_t>(k * n);  // right codes [K, N]
+  a.template take<uint8_t>(k * m);  // left codes [K, M]
+  size_t g1 = rpx_fp8_gemm_workspace(m, k, n);
+  size_t g2 = rpx_fp8_gemm_workspace(k, n, m);
+  const size_t g3 = rpx_fp8_gemm_workspace(n, k, m);
+  if (g2 < g3) g2 = g3;
+  a.template take<uint8_t>(static_cast<int64_t>(g1 > g2 ? g1 : g2));
+}
+}  // namespace
+
+extern "C" {
+
+size_t rpx_fp8_linear_forward_workspace(int64_t m, int64_t n, int64_t k) {
+  Sizer s;
+  plan_fp8_forward(s, m, n, k);
+  return s.used;
+}
+
+int rpx_fp8_linear_forward(const void* left, int left_dtype, int64_t m, int64_t k,
+                           const void* right, int right_dtype, int64_t n, int64_t right_row_stride,
+                           int64_t right_col_stride, void* out, int out_dtype, float* scales_out,
+                           void* workspace, size_t workspace_bytes, void* stream) {
+  RPX_TRY(check_dtype(left_dtype));
+  RPX_TRY(check_dtype(right_dtype));
+  RPX_TRY(check_dtype(out_dtype));
+  if (m < 0 || n < 0 || k < 0) return fail_invalid("m, n, k must be non-negative");
+  if (scales_out == nullptr) return fail_invalid("rpx_fp8_linear_forward: null scales_out");
+  if (m == 0 || n == 0) return kOk;
+  if (left == nullptr || right == nullptr || out == nullptr)
+    return fail_invalid("rpx_fp8_linear_forward: null pointer");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  Arena ar(workspace, workspace_bytes);
+  uint32_t* pl = ar.take<uint32_t>(fp8_amax_partials(m * k));
+  uint32_t* pr = ar.take<uint32_t>(fp8_amax_partials(k * n));
+  uint8_t* ql = ar.take<uint8_t>(m * k);
+  uint8_t* qr = ar.take<uint8_t>(n * k);
+  const size_t gws = rpx_fp8_gemm_workspace(m, n, k);
+  uint8_t* gw = ar.take<uint8_t>(static_cast<int64_t>(gws));
+  if (ar.overflow) return fail_invalid("rpx_fp8_linear_forward: workspace too small");
+  RPX_HIP(launch_fp8_amax(left, left_dtype, m, k, k, 1, pl, fp8_amax_partials(m * k), kE4M3FN,
+                          scales_out, st),
+          "fp8_linear_forward: amax(left)");
+  RPX_HIP(launch_fp8_amax(right, right_dtype, k, n, right_row_stride, right_col_stride, pr,
+                          fp8_amax_partials(k * n), kE4M3FN, scales_out + 1, st),
+          "fp8_linear_forward: amax(right)");
+  RPX_HIP(launch_fp8_cast(left, left_dtype, m, k, k, 1, scales_out, kE4M3FN, ql, nullptr, st),
+          "fp8_linear_forward: cast(left)");
+  RPX_HIP(launch_fp8_cast(right, right_dtype, k, n, right_row_stride, right_col_stride,
+                          scales_out + 1, kE4M3FN, nullptr, qr, st),
+          "fp8_linear_forward: cast(right)");
+  return rpx_fp8_gemm(ql, kE4M3FN, scales_out, qr, kE4M3FN, scales_out + 1, m, n, k, out,
+                      out_dtype, gw, gws, stream);
+}
+
+size_t rpx_fp8_linear_backward_workspace(int64_t m, int64_t n, int64_t k) {
+  Sizer s;
+  plan_fp8_backward(s, m, n, k);
+  return s.used;
+}
+
+int rpx_fp8_linear_backward(const void* left, int left_dtype, const void* right, int right_dtype,
+                            int64_t m, int64_t k, int64_t n, int64_t right_row_stride,
+                            int64_t right_col_stride, const void* grad, int grad_dtype,
+                            const float* scales, void* d_left, void* d_right,
+                            int d_right_transposed, int out_dtype, void* workspace,
+                            size_t workspace_bytes, void* stream) {
+  RPX_TRY(check_dtype(left_dtype));
+  RPX_TRY(check_dtype(right_dtype));
+  RPX_TRY(check_dtype(grad_dtype));
+  RPX_TRY(check_dtype(out_dtype));
+  if (m < 0 || n < 0 || k < 0) return fail_invalid("m, n, k must be non-negative");
+  if (left == nullptr || right == nullptr || grad == nullptr || scales == nullptr)
+    return fail_invalid("rpx_fp8_linear_backward: null pointer");
+  if (m == 0 || n == 0 || k == 0)
+    return fail_invalid("rpx_fp8_linear_backward: empty operands are handled by the caller");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  Arena ar(workspace, workspace_bytes);
+  uint32_t* pg = ar.take<uint32_t>(fp8_amax_partials(m * n));
+  float* sg = ar.take<float>(1);
+  uint8_t* qg = ar.take<uint8_t>(m * n);
+  uint8_t* qgt = ar.take<uint8_t>(n * m);
+  uint8_t* qr = ar.take<uint8_t>(k * n);
+  uint8_t* qlt = ar.take<uint8_t>(k * m);
+  size_t g1 = rpx_fp8_gemm_workspace(m, k, n);
+  size_t g2 = rpx_fp8_gemm_workspace(k, n, m);
+  const size_t g3 = rpx_fp8_gemm_workspace(n, k, m);
+  if (g2 < g3) g2 = g3;
+  const size_t gws = g1 > g2 ? g1 : g2;
+  uint8_t* gw = ar.take<uint8_t>(static_cast<int64_t>(gws));
+  if (ar.overflow) return fail_invalid("rpx_fp8_linear_backward: workspace too small");
+  // s_g (e5m2) and both layouts of the gradient codes
+  RPX_HIP(launch_fp8_amax(grad, grad_dtype, m, n, n, 1, pg, fp8_amax_partials(m * n), kE5M2, sg,
+                          st),
+          "fp8_linear_backward: amax(grad)");
+  RPX_HIP(launch_fp8_cast(grad, grad_dtype, m, n, n, 1, sg, kE5M2, d_left ? qg : nullptr,
+                          d_right ? qgt : nullptr, st),
+          "fp8_linear_backward: cast(grad)");
+  // operands re-quantized with the forward scales (same values, same amax)
+  if (d_left != nullptr) {
+    RPX_HIP(launch_fp8_cast(right, right_dtype, k, n, right_row_stride, right_col_stride,
+                            scales + 1, kE4M3FN, qr, nullptr, st),
+            "fp8_linear_backward: cast(right)");
+    // d_left [M, K] = ((g . right^T) * s_g) * s_r
+    RPX_TRY(rpx_fp8_gemm(qg, kE5M2, sg, qr, kE4M3FN, scales + 1, m, k, n, d_left, out_dtype, gw,
+                         gws, stream));
+  }
+  if (d_right == nullptr) return kOk;
+  RPX_HIP(launch_fp8_cast(left, left_dtype, m, k, k, 1, scales, kE4M3FN, nullptr, qlt, st),
+          "fp8_linear_backward: cast(left)");
+  // d_right = ((left^T . g) * s_l) * s_g, as [K, N] or transposed [N, K]
+  if (d_right_transposed) {
+    RPX_TRY(rpx_fp8_gemm(qgt, kE5M2, scales, qlt, kE4M3FN, sg, n, k, m, d_right, out_dtype, gw, gws,
+                         stream));
+  } else {
+    RPX_TRY(rpx_fp8_gemm(qlt, kE4M3FN, scales, qgt, kE5M2, sg, k, n, m, d_right, out_dtype, gw, gws,
+                         stream));
+  }
+  return kOk;
+}
+
+// ---------------------------------------------------------------------------
+// Host-side codec hook: runs the exact device quantizer (divide + fp8
+// rounding) on the CPU so that it can be checked exhaustively without a GPU.
+// ---------------------------------------------------------------------------
+int rpx_host_fp8_quantize(const float* in, int64_t n, float scale, int fmt, uint8_t* out) {
+  RPX_TRY(check_fmt(fmt));
+  if (n > 0 && (in == nullptr || out == nullptr)) return fail_invalid("null pointer");
+  const float r = 1.0f / scale;
+  for (int64_t i = 0; i < n; ++i) {
+    const float q = div_rn(in[i], scale, r);
+    out[i] = static_cast<uint8_t>(fmt == kE4M3FN ? f32_to_e4m3fn(q) : f32_to_e5m2(q));
+  }
+  return kOk;
+}
+
+}  // extern "C"

@@ -1,0 +1,495 @@
+// Dynamically scaled OCP fp8 linear for gfx950
+// (src/representax/precision.py:127-221).
+//
+//   amax  : per-block max |t| over ordered f32 bit patterns (NaN sorts above
+//           inf, so NaN propagates like XLA's max), then a one-block finalize
+//           that writes s = max(amax / fmax, FLT_MIN).
+//   cast  : codes = f8(f32(t) / s), IEEE-rounded divide then a direct
+//           round-to-nearest-even cast; optional row-major and transposed
+//           outputs from one read of t.
+//   gemm  : v_mfma_f32_32x32x64_f8f6f4 NT GEMM on fp8 codes, f32 accumulate,
+//           epilogue ((acc * s_a) * s_b) rounded once to the output dtype;
+//           optional split-K with fp32 partials and a deterministic sum.
+#include "common.h"
+#include "kernels.h"
+
+namespace rpx {
+
+namespace {
+
+constexpr int kAmaxBlocks = 1024;
+
+__device__ __forceinline__ uint32_t abs_bits_f32(float f) {
+  return __builtin_bit_cast(uint32_t, f) & 0x7FFFFFFFu;
+}
+
+__device__ __forceinline__ uint32_t umax(uint32_t a, uint32_t b) { return a > b ? a : b; }
+
+__device__ __forceinline__ uint32_t block_reduce_max(uint32_t v, uint32_t* sh) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1)
+    v = umax(v, static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), off, 64)));
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  if (lane == 0) sh[wave] = v;
+  __syncthreads();
+  uint32_t r = 0;
+  const int nw = blockDim.x / 64;
+  for (int i = 0; i < nw; ++i) r = umax(r, sh[i]);
+  return r;
+}
+
+// Dense buffer of numel elements (any logical layout).
+__global__ void __launch_bounds__(256)
+    k_amax_partial(const void* __restrict__ t, int dtype, int64_t numel,
+                   uint32_t* __restrict__ partials) {
+  __shared__ uint32_t sh[4];
+  uint32_t m = 0;
+  const int64_t tid = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  if (dtype == kBF16) {
+    const uint16_t* p = static_cast<const uint16_t*>(t);
+    const bool al = (reinterpret_cast<uintptr_t>(p) & 15) == 0;
+    const int64_t nvec = al ? numel / 8 : 0;
+    const u32x4_t* pv = reinterpret_cast<const u32x4_t*>(p);
+    for (int64_t i = tid; i < nvec; i += stride) {
+      const u32x4_t w = pv[i];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        m = umax(m, (w[e] & 0x7FFFu) << 16);
+        m = umax(m, (w[e] >> 16 & 0x7FFFu) << 16);
+      }
+    }
+    for (int64_t i = nvec * 8 + tid; i < numel; i += stride)
+      m = umax(m, static_cast<uint32_t>(p[i] & 0x7FFFu) << 16);
+  } else {
+    const float* p = static_cast<const float*>(t);
+    const bool al = (reinterpret_cast<uintptr_t>(p) & 15) == 0;
+    const int64_t nvec = al ? numel / 4 : 0;
+    const u32x4_t* pv = reinterpret_cast<const u32x4_t*>(p);
+    for (int64_t i = tid; i < nvec; i += stride) {
+      const u32x4_t w = pv[i];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) m = umax(m, w[e] & 0x7FFFFFFFu);
+    }
+    for (int64_t i = nvec * 4 + tid; i < numel; i += stride) m = umax(m, abs_bits_f32(p[i]));
+  }
+  m = block_reduce_max(m, sh);
+  if (threadIdx.x == 0) partials[blockIdx.x] = m;
+}
+
+__global__ void __launch_bounds__(256)
+    k_amax_finalize(const uint32_t* __restrict__ partials, int64_t n, float fmax,
+                    float* __restrict__ scale_out) {
+  __shared__ uint32_t sh[4];
+  uint32_t m = 0;
+  for (int64_t i = threadIdx.x; i < n; i += blockDim.x) m = umax(m, partials[i]);
+  m = block_reduce_max(m, sh);
+  if (threadIdx.x == 0) {
+    const float amax = __builtin_bit_cast(float, m);
+    float s;
+    if (m > 0x7F800000u) {
+      s = __builtin_bit_cast(float, 0x7FC00000u);
+    } else {
+      s = amax / fmax;
+      const float tiny = 1.17549435e-38f;
+      s = s > tiny ? s : tiny;
+    }
+    scale_out[0] = s;
+  }
+}
+
+__device__ __forceinline__ uint32_t encode(float v, int fmt) {
+  return fmt == kE4M3FN ? f32_to_e4m3fn(v) : f32_to_e5m2(v);
+}
+
+__device__ __forceinline__ float load_val(const void* t, int dtype, int64_t idx) {
+  if (dtype == kBF16) return bf16_to_f32(static_cast<const uint16_t*>(t)[idx]);
+  return static_cast<const float*>(t)[idx];
+}
+
+// Tile of 64 x 64 logical elements; writes row-major codes (out) and/or
+// transposed codes (out_t), four bytes per store.
+__global__ void __launch_bounds__(256)
+    k_fp8_cast(const void* __restrict__ t, int dtype, int64_t rows, int64_t cols, int64_t s_row,
+               int64_t s_col, const float* __restrict__ scale, int fmt, uint8_t* __restrict__ out,
+               uint8_t* __restrict__ out_t) {
+  __shared__ uint8_t tile[64][64 + 4];
+  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * 64;
+  const int64_t c0 = static_cast<int64_t>(blockIdx.x) * 64;
+  const float s = scale[0];
+  const float rcp = 1.0f / s;
+  const int tid = threadIdx.x;
+  const bool col_fast = (s_col == 1) || (s_row != 1);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int a = tid % 64;
+    const int b = tid / 64 + 4 * i;
+    const int rl = col_fast ? b : a;
+    const int cl = col_fast ? a : b;
+    const int64_t r = r0 + rl;
+    const int64_t c = c0 + cl;
+    uint32_t code = 0;
+    if (r < rows && c < cols) code = encode(div_rn(load_val(t, dtype, r * s_row + c * s_col), s, rcp), fmt);
+    tile[rl][cl] = static_cast<uint8_t>(code);
+  }
+  __syncthreads();
+  if (out != nullptr) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int rl = tid / 16 + 16 * i;
+      const int cl = (tid % 16) * 4;
+      const int64_t r = r0 + rl;
+      const int64_t c = c0 + cl;
+      if (r >= rows) continue;
+      uint8_t* dst = out + r * cols + c;
+      if (c + 3 < cols && ((reinterpret_cast<uintptr_t>(dst) & 3) == 0)) {
+        *reinterpret_cast<uint32_t*>(dst) =
+            static_cast<uint32_t>(tile[rl][cl]) | (static_cast<uint32_t>(tile[rl][cl + 1]) << 8) |
+            (static_cast<uint32_t>(tile[rl][cl + 2]) << 16) |
+            (static_cast<uint32_t>(tile[rl][cl + 3]) << 24);
+      } else {
+        for (int e = 0; e < 4; ++e)
+          if (c + e < cols) dst[e] = tile[rl][cl + e];
+      }
+    }
+  }
+  if (out_t != nullptr) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int cl = tid / 16 + 16 * i;
+      const int rl = (tid % 16) * 4;
+      const int64_t c = c0 + cl;
+      const int64_t r = r0 + rl;
+      if (c >= cols) continue;
+      uint8_t* dst = out_t + c * rows + r;
+      if (r + 3 < rows && ((reinterpret_cast<uintptr_t>(dst) & 3) == 0)) {
+        *reinterpret_cast<uint32_t*>(dst) =
+            static_cast<uint32_t>(tile[rl][cl]) | (static_cast<uint32_t>(tile[rl + 1][cl]) << 8) |
+            (static_cast<uint32_t>(tile[rl + 2][cl]) << 16) |
+            (static_cast<uint32_t>(tile[rl + 3][cl]) << 24);
+      } else {
+        for (int e = 0; e < 4; ++e)
+          if (r + e < rows) dst[e] = tile[rl + e][cl];
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// fp8 NT GEMM
+// ---------------------------------------------------------------------------
+constexpr int kBKb = 128;            // bytes (= fp8 elements) per K slice
+constexpr int kLd8 = kBKb + 16;      // LDS row stride in bytes
+
+template <int FA, int FB>
+__device__ __forceinline__ f32x16_t mfma_f8(i32x8_t a, i32x8_t b, f32x16_t c) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, FA, FB, 0, 0, 0, 0);
+}
+
+template <int BM, int BN, int WM, int WN, int FA, int FB>
+__global__ void __launch_bounds__(64 * WM * WN)
+    k_fp8_gemm(const uint8_t* __restrict__ A, const uint8_t* __restrict__ B, int64_t M,
+               int64_t N, int64_t K, int64_t k_per_split, const float* __restrict__ s_a,
+               const float* __restrict__ s_b, void* __restrict__ out, int out_dtype,
+               int64_t ldc, float* __restrict__ partials, int tiles_m, int tiles_n) {
+  constexpr int NT = 64 * WM * WN;
+  constexpr int TM = BM / WM;
+  constexpr int TN = BN / WN;
+  constexpr int FM = TM / 32;
+  constexpr int FN = TN / 32;
+  extern __shared__ __align__(16) uint8_t smem8[];
+  uint8_t* sA = smem8;
+  uint8_t* sB = smem8 + 2 * BM * kLd8;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave % WM;
+  const int wn = wave / WM;
+  const int tiles = tiles_m * tiles_n;
+  const int split = blockIdx.x / tiles;
+  const int tile = blockIdx.x % tiles;
+  const int tm = tile % tiles_m;
+  const int tn = tile / tiles_m;
+  const int64_t m0 = static_cast<int64_t>(tm) * BM;
+  const int64_t n0 = static_cast<int64_t>(tn) * BN;
+  const int64_t kbeg = static_cast<int64_t>(split) * k_per_split;
+  int64_t kend = kbeg + k_per_split;
+  if (kend > K) kend = K;
+
+  constexpr int VPR = kBKb / 16;  // 16-byte vectors per row
+  constexpr int A_PER_T = BM * VPR / NT;
+  constexpr int B_PER_T = BN * VPR / NT;
+  static_assert(BM * VPR % NT == 0 && BN * VPR % NT == 0, "tiles must split evenly");
+  u32x4_t a_reg[A_PER_T];
+  u32x4_t b_reg[B_PER_T];
+
+  auto load = [&](int64_t k0) {
+#pragma unroll
+    for (int i = 0; i < A_PER_T; ++i) {
+      const int v = tid + i * NT;
+      const int64_t gm = m0 + v / VPR;
+      a_reg[i] = gm < M ? *reinterpret_cast<const u32x4_t*>(A + gm * K + k0 + (v % VPR) * 16)
+                        : u32x4_t{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int i = 0; i < B_PER_T; ++i) {
+      const int v = tid + i * NT;
+      const int64_t gn = n0 + v / VPR;
+      b_reg[i] = gn < N ? *reinterpret_cast<const u32x4_t*>(B + gn * K + k0 + (v % VPR) * 16)
+                        : u32x4_t{0u, 0u, 0u, 0u};
+    }
+  };
+  auto store = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < A_PER_T; ++i) {
+      const int v = tid + i * NT;
+      *reinterpret_cast<u32x4_t*>(sA + buf * BM * kLd8 + (v / VPR) * kLd8 + (v % VPR) * 16) =
+          a_reg[i];
+    }
+#pragma unroll
+    for (int i = 0; i < B_PER_T; ++i) {
+      const int v = tid + i * NT;
+      *reinterpret_cast<u32x4_t*>(sB + buf * BN * kLd8 + (v / VPR) * kLd8 + (v % VPR) * 16) =
+          b_reg[i];
+    }
+  };
+
+  f32x16_t acc[FN][FM];
+#pragma unroll
+  for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[fn][fm][v] = 0.0f;
+
+  auto compute = [&](int buf) {
+    const uint8_t* a_base = sA + buf * BM * kLd8 + (wm * TM + (lane & 31)) * kLd8 + (lane >> 5) * 32;
+    const uint8_t* b_base = sB + buf * BN * kLd8 + (wn * TN + (lane & 31)) * kLd8 + (lane >> 5) * 32;
+#pragma unroll
+    for (int kk = 0; kk < kBKb / 64; ++kk) {
+      i32x8_t af[FM];
+      i32x8_t bfr[FN];
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm) {
+        const u32x4_t* p = reinterpret_cast<const u32x4_t*>(a_base + fm * 32 * kLd8 + kk * 64);
+        const u32x4_t lo = p[0];
+        const u32x4_t hi = p[1];
+        af[fm] = i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3],
+                         (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+      }
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn) {
+        const u32x4_t* p = reinterpret_cast<const u32x4_t*>(b_base + fn * 32 * kLd8 + kk * 64);
+        const u32x4_t lo = p[0];
+        const u32x4_t hi = p[1];
+        bfr[fn] = i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3],
+                          (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+      }
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm) acc[fn][fm] = mfma_f8<FB, FA>(bfr[fn], af[fm], acc[fn][fm]);
+    }
+  };
+
+  const int64_t nk = (kend - kbeg) / kBKb;
+  if (nk > 0) {
+    load(kbeg);
+    store(0);
+    __syncthreads();
+    for (int64_t kt = 0; kt < nk; ++kt) {
+      const int cur = static_cast<int>(kt & 1);
+      const bool more = kt + 1 < nk;
+      if (more) load(kbeg + (kt + 1) * kBKb);
+      compute(cur);
+      if (more) store(cur ^ 1);
+      __syncthreads();
+    }
+  }
+
+  const float sa = s_a[0];
+  const float sb = s_b[0];
+  float* part = partials != nullptr ? partials + static_cast<int64_t>(split) * M * N : nullptr;
+#pragma unroll
+  for (int fn = 0; fn < FN; ++fn) {
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm) {
+      const int64_t m = m0 + wm * TM + fm * 32 + (lane & 31);
+      if (m >= M) continue;
+#pragma unroll
+      for (int vg = 0; vg < 4; ++vg) {
+        const int64_t nb = n0 + wn * TN + fn * 32 + 8 * vg + 4 * (lane >> 5);
+        float y[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[e] = acc[fn][fm][4 * vg + e];
+        if (part != nullptr) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (nb + e < N) part[m * N + nb + e] = y[e];
+          continue;
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[e] = (y[e] * sa) * sb;
+        if (out_dtype == kBF16) {
+          uint16_t* dst = static_cast<uint16_t*>(out) + m * ldc + nb;
+          if (nb + 3 < N && (ldc % 4 == 0)) {
+            *reinterpret_cast<u32x2_t*>(dst) =
+                u32x2_t{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])};
+          } else {
+            for (int e = 0; e < 4; ++e)
+              if (nb + e < N) dst[e] = f32_to_bf16(y[e]);
+          }
+        } else {
+          float* dst = static_cast<float*>(out) + m * ldc + nb;
+          for (int e = 0; e < 4; ++e)
+            if (nb + e < N) dst[e] = y[e];
+        }
+      }
+    }
+  }
+}
+
+__global__ void __launch_bounds__(256)
+    k_fp8_split_reduce(const float* __restrict__ partials, int64_t splits, int64_t M, int64_t N,
+                       const float* __restrict__ s_a, const float* __restrict__ s_b,
+                       void* __restrict__ out, int out_dtype, int64_t ldc) {
+  const float sa = s_a[0];
+  const float sb = s_b[0];
+  const int64_t count = M * N;
+  for (int64_t e = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; e < count;
+       e += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    float s = 0.0f;
+    for (int64_t i = 0; i < splits; ++i) s += partials[i * count + e];
+    s = (s * sa) * sb;
+    const int64_t m = e / N;
+    const int64_t n = e % N;
+    if (out_dtype == kBF16)
+      static_cast<uint16_t*>(out)[m * ldc + n] = f32_to_bf16(s);
+    else
+      static_cast<float*>(out)[m * ldc + n] = s;
+  }
+}
+
+struct Fp8Plan {
+  int bm, bn;
+  int64_t splits, k_per_split;
+};
+
+Fp8Plan plan_fp8(int64_t m, int64_t n, int64_t k) {
+  Fp8Plan p;
+  if (ceil_div(m, 256) * ceil_div(n, 128) >= 256) {
+    p.bm = 256;
+    p.bn = 128;
+  } else {
+    p.bm = 128;
+    p.bn = 128;
+  }
+  const int64_t tiles = ceil_div(m, p.bm) * ceil_div(n, p.bn);
+  const int64_t kslices = k / kBKb;
+  int64_t s = 1;
+  while (tiles * s < 256 && s * 2 <= kslices && s < 8) s *= 2;
+  p.splits = s;
+  p.k_per_split = ceil_div(kslices, s) * kBKb;
+  p.splits = ceil_div(k, p.k_per_split);
+  return p;
+}
+
+template <int BM, int BN, int FA, int FB>
+hipError_t run_fp8(const uint8_t* a, const uint8_t* b, int64_t m, int64_t n, int64_t k,
+                   const Fp8Plan& plan, const float* s_a, const float* s_b, void* out,
+                   int out_dtype, int64_t ldc, float* partials, hipStream_t stream) {
+  const int tiles_m = static_cast<int>(ceil_div(m, BM));
+  const int tiles_n = static_cast<int>(ceil_div(n, BN));
+  const size_t lds = static_cast<size_t>(2) * (BM + BN) * kLd8;
+  auto kern = k_fp8_gemm<BM, BN, 2, 2, FA, FB>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       static_cast<int>(lds));
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  const unsigned blocks = static_cast<unsigned>(tiles_m) * tiles_n * plan.splits;
+  hipLaunchKernelGGL(kern, dim3(blocks), dim3(256), lds, stream, a, b, m, n, k, plan.k_per_split,
+                     s_a, s_b, out, out_dtype, ldc, plan.splits > 1 ? partials : nullptr,
+                     tiles_m, tiles_n);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || plan.splits == 1) return e;
+  int64_t g = ceil_div(m * n, 256);
+  if (g > 8192) g = 8192;
+  hipLaunchKernelGGL(k_fp8_split_reduce, dim3(static_cast<unsigned>(g)), dim3(256), 0, stream,
+                     partials, plan.splits, m, n, s_a, s_b, out, out_dtype, ldc);
+  return hipGetLastError();
+}
+
+template <int FA, int FB>
+hipError_t dispatch_fp8(const uint8_t* a, const uint8_t* b, int64_t m, int64_t n, int64_t k,
+                        const float* s_a, const float* s_b, void* out, int out_dtype, int64_t ldc,
+                        float* partials, hipStream_t stream) {
+  const Fp8Plan plan = plan_fp8(m, n, k);
+  if (plan.bm == 256)
+    return run_fp8<256, 128, FA, FB>(a, b, m, n, k, plan, s_a, s_b, out, out_dtype, ldc,
+                                     partials, stream);
+  return run_fp8<128, 128, FA, FB>(a, b, m, n, k, plan, s_a, s_b, out, out_dtype, ldc, partials,
+                                   stream);
+}
+
+}  // namespace
+
+int64_t fp8_amax_partials(int64_t numel) {
+  int64_t g = ceil_div(numel, 256 * 16);
+  if (g > kAmaxBlocks) g = kAmaxBlocks;
+  if (g < 1) g = 1;
+  return g;
+}
+
+hipError_t launch_fp8_amax(const void* t, int dtype, int64_t rows, int64_t cols, int64_t s_row,
+                           int64_t s_col, uint32_t* partials, int64_t n_partials, int fmt,
+                           float* scale_out, hipStream_t stream) {
+  (void)s_row;
+  (void)s_col;
+  const int64_t numel = rows * cols;
+  hipLaunchKernelGGL(k_amax_partial, dim3(static_cast<unsigned>(n_partials)), dim3(256), 0, stream,
+                     t, dtype, numel, partials);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(k_amax_finalize, dim3(1), dim3(256), 0, stream, partials, n_partials,
+                     fp8_max(fmt), scale_out);
+  return hipGetLastError();
+}
+
+hipError_t launch_fp8_cast(const void* t, int dtype, int64_t rows, int64_t cols, int64_t s_row,
+                           int64_t s_col, const float* scale, int fmt, uint8_t* out,
+                           uint8_t* out_t, hipStream_t stream) {
+  if (rows == 0 || cols == 0) return hipSuccess;
+  const dim3 grid(static_cast<unsigned>(ceil_div(cols, 64)), static_cast<unsigned>(ceil_div(rows, 64)));
+  hipLaunchKernelGGL(k_fp8_cast, grid, dim3(256), 0, stream, t, dtype, rows, cols, s_row, s_col,
+                     scale, fmt, out, out_t);
+  return hipGetLastError();
+}
+
+int64_t fp8_gemm_workspace_floats(int64_t m, int64_t n, int64_t k) {
+  const Fp8Plan p = plan_fp8(m, n, k);
+  return p.splits > 1 ? p.splits * m * n : 0;
+}
+
+hipError_t launch_fp8_gemm(const uint8_t* a, int fmt_a, const float* s_a, const uint8_t* b,
+                           int fmt_b, const float* s_b, int64_t m, int64_t n, int64_t k,
+                           void* out, int out_dtype, int64_t ldc, float* split_ws,
+                           int64_t split_ws_floats, hipStream_t stream) {
+  if (m == 0 || n == 0) return hipSuccess;
+  if (split_ws_floats < fp8_gemm_workspace_floats(m, n, k)) return hipErrorInvalidValue;
+  // MFMA format codes: 0 = fp8 (e4m3), 1 = bf8 (e5m2)
+  if (fmt_a == kE4M3FN && fmt_b == kE4M3FN)
+    return dispatch_fp8<0, 0>(a, b, m, n, k, s_a, s_b, out, out_dtype, ldc, split_ws, stream);
+  if (fmt_a == kE5M2 && fmt_b == kE4M3FN)
+    return dispatch_fp8<1, 0>(a, b, m, n, k, s_a, s_b, out, out_dtype, ldc, split_ws, stream);
+  if (fmt_a == kE4M3FN && fmt_b == kE5M2)
+    return dispatch_fp8<0, 1>(a, b, m, n, k, s_a, s_b, out, out_dtype, ldc, split_ws, stream);
+  return dispatch_fp8<1, 1>(a, b, m, n, k, s_a, s_b, out, out_dtype, ldc, split_ws, stream);
+}
+
+}  // namespace rpx

@@ -1,0 +1,102 @@
+// Kernel launchers shared between translation units.
+#pragma once
+
+#include "common.h"
+
+namespace rpx {
+
+// INT4 -----------------------------------------------------------------------
+hipError_t launch_int4_dequant(const uint8_t* packed, const uint16_t* scales, uint16_t* out,
+                               int64_t n, int64_t k, int64_t packed_cols, int64_t n_groups,
+                               int64_t group, hipStream_t stream);
+hipError_t launch_int4_dequant_t(const uint8_t* packed, const uint16_t* scales, uint16_t* out,
+                                 int64_t n, int64_t k, int64_t packed_cols, int64_t n_groups,
+                                 int64_t group, int64_t ld_out, hipStream_t stream);
+hipError_t launch_int4_pack(const void* weight, int dtype, uint8_t* packed, uint16_t* scales,
+                            int64_t n, int64_t k, int64_t packed_cols, int64_t n_groups,
+                            int64_t group, hipStream_t stream);
+hipError_t launch_int4_merge(const uint8_t* packed, const uint16_t* scales, const float* lora_a,
+                             const float* lora_b, float* out, int64_t n, int64_t k,
+                             int64_t packed_cols, int64_t n_groups, int64_t group, int64_t rank,
+                             float scaling, hipStream_t stream);
+
+// GEMM -----------------------------------------------------------------------
+// Low-rank epilogue term added to a GEMM tile:
+//   t[m, n] = sum_j C(m, j) * R(n, j)      (fp32 accumulate)
+//   y       = bf16(bf16(acc) + bf16(bf16(t) * scale))
+//   y       = bf16(y + bias[n])             (when bias != nullptr)
+// rank == 0 disables the low-rank term.
+struct LowRankEpilogue {
+  const uint16_t* rows = nullptr;  // R, indexed by (output column n, j)
+  int64_t rows_sn = 0, rows_sj = 0;
+  const uint16_t* cols = nullptr;  // C, indexed by (output row m, j)
+  int64_t cols_sm = 0, cols_sj = 0;
+  int64_t rank = 0;
+  float scale = 1.0f;
+  const uint16_t* bias = nullptr;  // bf16 bits [N]
+};
+
+// Packed INT4 operand [N, K] (row n holds ceil(K/2) bytes).
+struct Int4Operand {
+  const uint8_t* packed = nullptr;
+  int64_t packed_cols = 0;
+  const uint16_t* scales = nullptr;
+  int64_t n_groups = 1;
+  int64_t group = 0;
+};
+
+// y[M, N] = epilogue(A[M, K] . W_b[N, K]^T); A bf16 row-major (lda).
+hipError_t launch_gemm_int4(const uint16_t* a, int64_t lda, const Int4Operand& w, int64_t m,
+                            int64_t n, int64_t k, uint16_t* out, int64_t ldc,
+                            const LowRankEpilogue& epi, hipStream_t stream);
+// y[M, N] = epilogue(A[M, K] . B[N, K]^T); A, B bf16 row-major.
+hipError_t launch_gemm_bf16(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb,
+                            int64_t m, int64_t n, int64_t k, uint16_t* out, int64_t ldc,
+                            const LowRankEpilogue& epi, hipStream_t stream);
+bool gemm_fast_path_ok(int64_t k, int64_t lda, int64_t ldb_elems, const void* a, const void* b,
+                       int64_t ldc, const void* out);
+
+// Rank-r kernels --------------------------------------------------------------
+// out[M, r] = bf16(sum_k op(A[m, k]) * R[j, k]); op(a) = bf16(a * a_scale) when
+// round_a, else a. R bf16 [r, K] row-major (ldr).
+hipError_t launch_rank_nt(const uint16_t* a, int64_t lda, const uint16_t* r_mat, int64_t ldr,
+                          int64_t m, int64_t rank, int64_t k, bool round_a, float a_scale,
+                          uint16_t* out, int64_t ldo, hipStream_t stream);
+// out[P, Q] = f32(bf16(sum_m op(X[m, p]) * Y[m, q])); X [M, P] (ldx), Y [M, Q] (ldy)
+// bf16 row-major; op as above on X. Uses `partials` (fp32) workspace of
+// rank_tn_workspace_floats(...) elements.
+int64_t rank_tn_workspace_floats(int64_t m, int64_t p, int64_t q);
+hipError_t launch_rank_tn(const uint16_t* x, int64_t ldx, const uint16_t* y, int64_t ldy,
+                          int64_t m, int64_t p, int64_t q, bool round_x, float x_scale,
+                          float* partials, float* out, hipStream_t stream);
+hipError_t launch_transpose_bf16(const uint16_t* in, int64_t rows, int64_t cols, int64_t ld_in,
+                                 uint16_t* out, int64_t ld_out, hipStream_t stream);
+hipError_t launch_fill_f32(float* out, int64_t n, float v, hipStream_t stream);
+hipError_t launch_f32_to_bf16(const float* in, uint16_t* out, int64_t n, hipStream_t stream);
+
+// Generic (any shape, any dtype) reference-shaped kernels --------------------
+// out[M, N] (fp32) = sum_k A(m, k) * B(n, k) with strided operands.
+// a_dtype/b_dtype: kF32 or kBF16; b_int4 replaces B with the packed operand
+// W_b, read as B(n, k) = W_b[n, k], or W_b[k, n] when int4_transposed.
+hipError_t launch_generic_gemm(const void* a, int a_dtype, int64_t a_sm, int64_t a_sk,
+                               const void* b, int b_dtype, int64_t b_sn, int64_t b_sk,
+                               const Int4Operand* b_int4, bool int4_transposed, int64_t m,
+                               int64_t n, int64_t k, float* out, hipStream_t stream);
+hipError_t launch_round_store(const float* in, int64_t n, int dtype, void* out,
+                              hipStream_t stream);
+
+// FP8 ------------------------------------------------------------------------
+int64_t fp8_amax_partials(int64_t numel);
+hipError_t launch_fp8_amax(const void* t, int dtype, int64_t rows, int64_t cols, int64_t s_row,
+                           int64_t s_col, uint32_t* partials, int64_t n_partials, int fmt,
+                           float* scale_out, hipStream_t stream);
+hipError_t launch_fp8_cast(const void* t, int dtype, int64_t rows, int64_t cols, int64_t s_row,
+                           int64_t s_col, const float* scale, int fmt, uint8_t* out,
+                           uint8_t* out_t, hipStream_t stream);
+hipError_t launch_fp8_gemm(const uint8_t* a, int fmt_a, const float* s_a, const uint8_t* b,
+                           int fmt_b, const float* s_b, int64_t m, int64_t n, int64_t k,
+                           void* out, int out_dtype, int64_t ldc, float* split_ws,
+                           int64_t split_ws_floats, hipStream_t stream);
+int64_t fp8_gemm_workspace_floats(int64_t m, int64_t n, int64_t k);
+
+}  // namespace rpx

@@ -1,0 +1,411 @@
+// Rank-r products of the LoRA adapter and the generic any-shape kernels.
+//
+//   rank_nt: out[M, r] = bf16(sum_k op(A[m, k]) R[j, k])   (h = x A^T, dh = g_a B)
+//   rank_tn: out[P, Q] = f32(bf16(sum_m op(X[m, p]) Y[m, q]))  (dB = g_a^T h,
+//            dA = dh^T x), split over token chunks with fp32 partials and a
+//            deterministic second-pass sum.
+// Both use v_mfma_f32_16x16x32_bf16: lane l of a 16x16 block owns column
+// l % 16 and rows 4*(l/16) + v.
+#include "common.h"
+#include "kernels.h"
+
+namespace rpx {
+
+namespace {
+
+__device__ __forceinline__ bf16x8_t as_bf16x8(u32x4_t v) {
+  return __builtin_bit_cast(bf16x8_t, v);
+}
+
+__device__ __forceinline__ u32x4_t scale_round8(u32x4_t v, float s) {
+  u32x4_t o;
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    o[e] = pack_bf16x2(bf16lo_to_f32(v[e]) * s, bf16hi_to_f32(v[e]) * s);
+  return o;
+}
+
+// Loads 8 consecutive bf16 starting at p when all are in range, else only the
+// first `valid` (the rest are zero).
+__device__ __forceinline__ u32x4_t load8(const uint16_t* p, int valid, bool aligned) {
+  if (valid >= 8 && aligned) return *reinterpret_cast<const u32x4_t*>(p);
+  uint32_t w[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const uint32_t lo = (2 * e < valid) ? p[2 * e] : 0u;
+    const uint32_t hi = (2 * e + 1 < valid) ? p[2 * e + 1] : 0u;
+    w[e] = lo | (hi << 16);
+  }
+  return u32x4_t{w[0], w[1], w[2], w[3]};
+}
+
+// One workgroup per 16 output rows; its four waves split K and reduce in LDS.
+template <int RB>
+__global__ void __launch_bounds__(256)
+    k_rank_nt(const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ R,
+              int64_t ldr, int64_t M, int64_t rank, int64_t K, int round_a, float a_scale,
+              uint16_t* __restrict__ out, int64_t ldo) {
+  __shared__ float red[4][RB][64][4];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int64_t m0 = static_cast<int64_t>(blockIdx.x) * 16;
+  const int64_t row = m0 + (lane & 15);
+  const int koff = (lane >> 4) * 8;
+  const bool a_al = (lda % 8 == 0) && ((reinterpret_cast<uintptr_t>(A) & 15) == 0);
+  const bool r_al = (ldr % 8 == 0) && ((reinterpret_cast<uintptr_t>(R) & 15) == 0);
+  f32x4_t acc[RB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) acc[rb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int64_t k0 = static_cast<int64_t>(wave) * 32; k0 < K; k0 += 128) {
+    const int64_t kc = k0 + koff;
+    int kv = static_cast<int>(K - kc);
+    kv = kv < 0 ? 0 : (kv > 8 ? 8 : kv);
+    u32x4_t av = load8(A + row * lda + kc, row < M ? kv : 0, a_al);
+    if (round_a) av = scale_round8(av, a_scale);
+    const bf16x8_t af = as_bf16x8(av);
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      const int64_t j = rb * 16 + (lane & 15);
+      const u32x4_t rv = load8(R + j * ldr + kc, j < rank ? kv : 0, r_al);
+      acc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, as_bf16x8(rv), acc[rb], 0, 0, 0);
+    }
+  }
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) red[wave][rb][lane][v] = acc[rb][v];
+  __syncthreads();
+  for (int o = tid; o < 16 * RB * 16; o += 256) {
+    const int i = o / (RB * 16);
+    const int j = o % (RB * 16);
+    const int64_t mm = m0 + i;
+    if (mm >= M || j >= rank) continue;
+    const int ln = (j & 15) + 16 * (i >> 2);
+    const int v = i & 3;
+    const int rb = j >> 4;
+    const float s = red[0][rb][ln][v] + red[1][rb][ln][v] + red[2][rb][ln][v] + red[3][rb][ln][v];
+    out[mm * ldo + j] = f32_to_bf16(s);
+  }
+}
+
+// Token-reduction product. Tile BP x BQ outputs, chunk of `chunk` tokens per
+// workgroup (blockIdx.z), 32 tokens per LDS step.
+template <int BP, int BQ>
+__global__ void __launch_bounds__(256)
+    k_rank_tn(const uint16_t* __restrict__ X, int64_t ldx, const uint16_t* __restrict__ Y,
+              int64_t ldy, int64_t M, int64_t P, int64_t Q, int round_x, float x_scale,
+              int64_t chunk, float* __restrict__ partials) {
+  constexpr int PP = 16 / 2;  // padding (elements) per LDS row
+  __shared__ uint16_t sX[32][BP + PP];
+  __shared__ uint16_t sY[32][BQ + PP];
+  constexpr int NB = (BP / 16) * (BQ / 16);
+  constexpr int PER_WAVE = (NB + 3) / 4;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int64_t p0 = static_cast<int64_t>(blockIdx.x) * BP;
+  const int64_t q0 = static_cast<int64_t>(blockIdx.y) * BQ;
+  const int64_t mbeg = static_cast<int64_t>(blockIdx.z) * chunk;
+  int64_t mend = mbeg + chunk;
+  if (mend > M) mend = M;
+  const bool x_al = (ldx % 8 == 0) && ((reinterpret_cast<uintptr_t>(X) & 15) == 0);
+  const bool y_al = (ldy % 8 == 0) && ((reinterpret_cast<uintptr_t>(Y) & 15) == 0);
+  f32x4_t acc[PER_WAVE];
+#pragma unroll
+  for (int b = 0; b < PER_WAVE; ++b) acc[b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  for (int64_t ms = mbeg; ms < mend; ms += 32) {
+    // stage X[ms:ms+32, p0:p0+BP] and Y[ms:ms+32, q0:q0+BQ]
+    for (int v = tid; v < 32 * (BP / 8); v += 256) {
+      const int r = v / (BP / 8);
+      const int c = (v % (BP / 8)) * 8;
+      const int64_t gm = ms + r;
+      int valid = static_cast<int>(P - (p0 + c));
+      valid = (gm < mend) ? (valid < 0 ? 0 : (valid > 8 ? 8 : valid)) : 0;
+      u32x4_t xv = load8(X + gm * ldx + p0 + c, valid, x_al);
+      if (round_x) xv = scale_round8(xv, x_scale);
+      *reinterpret_cast<u32x4_t*>(&sX[r][c]) = xv;
+    }
+    for (int v = tid; v < 32 * (BQ / 8); v += 256) {
+      const int r = v / (BQ / 8);
+      const int c = (v % (BQ / 8)) * 8;
+      const int64_t gm = ms + r;
+      int valid = static_cast<int>(Q - (q0 + c));
+      valid = (gm < mend) ? (valid < 0 ? 0 : (valid > 8 ? 8 : valid)) : 0;
+      *reinterpret_cast<u32x4_t*>(&sY[r][c]) = load8(Y + gm * ldy + q0 + c, valid, y_al);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int b = 0; b < PER_WAVE; ++b) {
+      const int blk = wave + 4 * b;
+      if (blk < NB) {
+        const int bp = blk / (BQ / 16);
+        const int bq = blk % (BQ / 16);
+        const int pl = bp * 16 + (lane & 15);
+        const int ql = bq * 16 + (lane & 15);
+        const int mo = (lane >> 4) * 8;
+        uint32_t xw[4], yw[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          xw[e] = static_cast<uint32_t>(sX[mo + 2 * e][pl]) |
+                  (static_cast<uint32_t>(sX[mo + 2 * e + 1][pl]) << 16);
+          yw[e] = static_cast<uint32_t>(sY[mo + 2 * e][ql]) |
+                  (static_cast<uint32_t>(sY[mo + 2 * e + 1][ql]) << 16);
+        }
+        acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            as_bf16x8(u32x4_t{xw[0], xw[1], xw[2], xw[3]}),
+            as_bf16x8(u32x4_t{yw[0], yw[1], yw[2], yw[3]}), acc[b], 0, 0, 0);
+      }
+    }
+    __syncthreads();
+  }
+  float* part = partials + static_cast<int64_t>(blockIdx.z) * P * Q;
+#pragma unroll
+  for (int b = 0; b < PER_WAVE; ++b) {
+    const int blk = wave + 4 * b;
+    if (blk >= NB) continue;
+    const int bp = blk / (BQ / 16);
+    const int bq = blk % (BQ / 16);
+    const int64_t q = q0 + bq * 16 + (lane & 15);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int64_t p = p0 + bp * 16 + 4 * (lane >> 4) + v;
+      if (p < P && q < Q) part[p * Q + q] = acc[b][v];
+    }
+  }
+}
+
+__global__ void __launch_bounds__(256)
+    k_reduce_partials(const float* __restrict__ partials, int64_t splits, int64_t count,
+                      float* __restrict__ out) {
+  for (int64_t e = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; e < count;
+       e += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    float s = 0.0f;
+    for (int64_t i = 0; i < splits; ++i) s += partials[i * count + e];
+    out[e] = round_bf16(s);
+  }
+}
+
+struct RankTnPlan {
+  int64_t gp, gq, splits, chunk;
+  bool wide_p;
+};
+
+RankTnPlan plan_rank_tn(int64_t m, int64_t p, int64_t q) {
+  RankTnPlan pl;
+  pl.wide_p = p >= q;  // <64,16> when P is the long side, else <16,64>
+  const int64_t bp = pl.wide_p ? 64 : 16;
+  const int64_t bq = pl.wide_p ? 16 : 64;
+  pl.gp = ceil_div(p, bp);
+  pl.gq = ceil_div(q, bq);
+  int64_t want = ceil_div(512, pl.gp * pl.gq);
+  const int64_t max_splits = ceil_div(m, 64);
+  if (want > max_splits) want = max_splits;
+  if (want < 1) want = 1;
+  pl.chunk = ceil_div(ceil_div(m, want), 32) * 32;
+  if (pl.chunk < 32) pl.chunk = 32;
+  pl.splits = ceil_div(m, pl.chunk);
+  if (pl.splits < 1) pl.splits = 1;
+  return pl;
+}
+
+// ---------------------------------------------------------------------------
+// Generic strided GEMM (any shape/dtype), fp32 accumulate and output.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float load_elem(const void* p, int dtype, int64_t idx) {
+  if (dtype == kBF16) return bf16_to_f32(static_cast<const uint16_t*>(p)[idx]);
+  return static_cast<const float*>(p)[idx];
+}
+
+__device__ __forceinline__ float int4_elem(const Int4Operand& w, int64_t row, int64_t col) {
+  const uint32_t byte = w.packed[row * w.packed_cols + col / 2];
+  const uint32_t nib = (col & 1) ? (byte >> 4) : (byte & 0xFu);
+  const float s = bf16_to_f32(w.scales[row * w.n_groups + col / w.group]);
+  const float q = static_cast<float>(static_cast<int>(nib ^ 8u) - 8);
+  return round_bf16(q * s);
+}
+
+// B(n, k) is B[n * b_sn + k * b_sk], or, for a packed INT4 operand,
+// W_b[n, k] (int4_mode 1) or W_b[k, n] (int4_mode 2).
+__global__ void __launch_bounds__(256)
+    k_generic_gemm(const void* __restrict__ A, int a_dtype, int64_t a_sm, int64_t a_sk,
+                   const void* __restrict__ B, int b_dtype, int64_t b_sn, int64_t b_sk,
+                   Int4Operand w, int int4_mode, int64_t M, int64_t N, int64_t K,
+                   float* __restrict__ out) {
+  __shared__ float sa[16][17];
+  __shared__ float sb[16][17];
+  const int tx = threadIdx.x % 16;
+  const int ty = threadIdx.x / 16;
+  const int64_t m = static_cast<int64_t>(blockIdx.y) * 16 + ty;
+  const int64_t n = static_cast<int64_t>(blockIdx.x) * 16 + tx;
+  float acc = 0.0f;
+  for (int64_t k0 = 0; k0 < K; k0 += 16) {
+    const int64_t ka = k0 + tx;
+    sa[ty][tx] = (m < M && ka < K) ? load_elem(A, a_dtype, m * a_sm + ka * a_sk) : 0.0f;
+    const int64_t nb = static_cast<int64_t>(blockIdx.x) * 16 + ty;
+    const int64_t kb = k0 + tx;
+    float bv = 0.0f;
+    if (nb < N && kb < K) {
+      if (int4_mode != 0) {
+        bv = (int4_mode == 1) ? int4_elem(w, nb, kb) : int4_elem(w, kb, nb);
+      } else {
+        bv = load_elem(B, b_dtype, nb * b_sn + kb * b_sk);
+      }
+    }
+    sb[ty][tx] = bv;
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < 16; ++kk) acc = __builtin_fmaf(sa[ty][kk], sb[tx][kk], acc);
+    __syncthreads();
+  }
+  if (m < M && n < N) out[m * N + n] = acc;
+}
+
+__global__ void __launch_bounds__(256)
+    k_round_store(const float* __restrict__ in, int64_t n, int dtype, void* __restrict__ out) {
+  for (int64_t e = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; e < n;
+       e += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    if (dtype == kBF16)
+      static_cast<uint16_t*>(out)[e] = f32_to_bf16(in[e]);
+    else
+      static_cast<float*>(out)[e] = in[e];
+  }
+}
+
+__global__ void __launch_bounds__(256)
+    k_transpose_bf16(const uint16_t* __restrict__ in, int64_t rows, int64_t cols, int64_t ld_in,
+                     uint16_t* __restrict__ out, int64_t ld_out) {
+  __shared__ uint16_t tile[32][33];
+  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * 32;
+  const int64_t c0 = static_cast<int64_t>(blockIdx.x) * 32;
+  const int tx = threadIdx.x % 32;
+  const int ty = threadIdx.x / 32;  // 0..7
+  for (int i = ty; i < 32; i += 8) {
+    const int64_t r = r0 + i;
+    const int64_t c = c0 + tx;
+    tile[i][tx] = (r < rows && c < cols) ? in[r * ld_in + c] : 0;
+  }
+  __syncthreads();
+  for (int i = ty; i < 32; i += 8) {
+    const int64_t c = c0 + i;
+    const int64_t r = r0 + tx;
+    if (c < cols && r < rows) out[c * ld_out + r] = tile[tx][i];
+  }
+}
+
+__global__ void __launch_bounds__(256)
+    k_f32_to_bf16(const float* __restrict__ in, uint16_t* __restrict__ out, int64_t n) {
+  for (int64_t e = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; e < n;
+       e += static_cast<int64_t>(gridDim.x) * blockDim.x)
+    out[e] = f32_to_bf16(in[e]);
+}
+
+__global__ void __launch_bounds__(256) k_fill_f32(float* __restrict__ out, int64_t n, float v) {
+  for (int64_t e = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; e < n;
+       e += static_cast<int64_t>(gridDim.x) * blockDim.x)
+    out[e] = v;
+}
+
+int grid1d(int64_t work) {
+  int64_t g = ceil_div(work, 256);
+  if (g > 8192) g = 8192;
+  if (g < 1) g = 1;
+  return static_cast<int>(g);
+}
+
+}  // namespace
+
+hipError_t launch_rank_nt(const uint16_t* a, int64_t lda, const uint16_t* r_mat, int64_t ldr,
+                          int64_t m, int64_t rank, int64_t k, bool round_a, float a_scale,
+                          uint16_t* out, int64_t ldo, hipStream_t stream) {
+  if (m == 0 || rank == 0) return hipSuccess;
+  const dim3 grid(static_cast<unsigned>(ceil_div(m, 16)));
+  const int ra = round_a ? 1 : 0;
+  if (rank <= 16)
+    hipLaunchKernelGGL(k_rank_nt<1>, grid, dim3(256), 0, stream, a, lda, r_mat, ldr, m, rank, k,
+                       ra, a_scale, out, ldo);
+  else if (rank <= 32)
+    hipLaunchKernelGGL(k_rank_nt<2>, grid, dim3(256), 0, stream, a, lda, r_mat, ldr, m, rank, k,
+                       ra, a_scale, out, ldo);
+  else if (rank <= 64)
+    hipLaunchKernelGGL(k_rank_nt<4>, grid, dim3(256), 0, stream, a, lda, r_mat, ldr, m, rank, k,
+                       ra, a_scale, out, ldo);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+int64_t rank_tn_workspace_floats(int64_t m, int64_t p, int64_t q) {
+  const RankTnPlan pl = plan_rank_tn(m, p, q);
+  return pl.splits * p * q;
+}
+
+hipError_t launch_rank_tn(const uint16_t* x, int64_t ldx, const uint16_t* y, int64_t ldy,
+                          int64_t m, int64_t p, int64_t q, bool round_x, float x_scale,
+                          float* partials, float* out, hipStream_t stream) {
+  if (p == 0 || q == 0) return hipSuccess;
+  if (m == 0) return launch_fill_f32(out, p * q, 0.0f, stream);
+  const RankTnPlan pl = plan_rank_tn(m, p, q);
+  const dim3 grid(static_cast<unsigned>(pl.gp), static_cast<unsigned>(pl.gq),
+                  static_cast<unsigned>(pl.splits));
+  const int rx = round_x ? 1 : 0;
+  if (pl.wide_p)
+    hipLaunchKernelGGL((k_rank_tn<64, 16>), grid, dim3(256), 0, stream, x, ldx, y, ldy, m, p, q,
+                       rx, x_scale, pl.chunk, partials);
+  else
+    hipLaunchKernelGGL((k_rank_tn<16, 64>), grid, dim3(256), 0, stream, x, ldx, y, ldy, m, p, q,
+                       rx, x_scale, pl.chunk, partials);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(k_reduce_partials, dim3(grid1d(p * q)), dim3(256), 0, stream, partials,
+                     pl.splits, p * q, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_fill_f32(float* out, int64_t n, float v, hipStream_t stream) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_fill_f32, dim3(grid1d(n)), dim3(256), 0, stream, out, n, v);
+  return hipGetLastError();
+}
+
+hipError_t launch_transpose_bf16(const uint16_t* in, int64_t rows, int64_t cols, int64_t ld_in,
+                                 uint16_t* out, int64_t ld_out, hipStream_t stream) {
+  if (rows == 0 || cols == 0) return hipSuccess;
+  const dim3 grid(static_cast<unsigned>(ceil_div(cols, 32)), static_cast<unsigned>(ceil_div(rows, 32)));
+  hipLaunchKernelGGL(k_transpose_bf16, grid, dim3(256), 0, stream, in, rows, cols, ld_in, out,
+                     ld_out);
+  return hipGetLastError();
+}
+
+hipError_t launch_f32_to_bf16(const float* in, uint16_t* out, int64_t n, hipStream_t stream) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_f32_to_bf16, dim3(grid1d(n)), dim3(256), 0, stream, in, out, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_generic_gemm(const void* a, int a_dtype, int64_t a_sm, int64_t a_sk,
+                               const void* b, int b_dtype, int64_t b_sn, int64_t b_sk,
+                               const Int4Operand* b_int4, bool int4_transposed, int64_t m,
+                               int64_t n, int64_t k, float* out, hipStream_t stream) {
+  if (m == 0 || n == 0) return hipSuccess;
+  Int4Operand w;
+  int mode = 0;
+  if (b_int4 != nullptr) {
+    w = *b_int4;
+    mode = int4_transposed ? 2 : 1;
+  }
+  const dim3 grid(static_cast<unsigned>(ceil_div(n, 16)), static_cast<unsigned>(ceil_div(m, 16)));
+  hipLaunchKernelGGL(k_generic_gemm, grid, dim3(256), 0, stream, a, a_dtype, a_sm, a_sk, b,
+                     b_dtype, b_sn, b_sk, w, mode, m, n, k, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_round_store(const float* in, int64_t n, int dtype, void* out,
+                              hipStream_t stream) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_round_store, dim3(grid1d(n)), dim3(256), 0, stream, in, n, dtype, out);
+  return hipGetLastError();
+}
+
+}  // namespace rpx

@@ -1,0 +1,341 @@
+"""torch-facing wrappers over the C ABI (device memory and streams only).
+
+Every function here launches HIP kernels from ``librepresentax_amd.so`` on
+torch's current stream. Tensors must live on a ROCm device; there is no CPU
+implementation, and a missing library or a CPU tensor raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+
+import torch
+
+from . import _native as nat
+
+BF16 = torch.bfloat16
+F32 = torch.float32
+
+
+def _ptr(t: torch.Tensor | None) -> ctypes.c_void_p | None:
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(device: torch.device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _dtype_code(dtype: torch.dtype) -> int:
+    if dtype == BF16:
+        return nat.DTYPE_BF16
+    if dtype == F32:
+        return nat.DTYPE_F32
+    raise TypeError(f"unsupported dtype {dtype}; expected float32 or bfloat16")
+
+
+def _on_device(*tensors: torch.Tensor | None) -> torch.device:
+    device = None
+    for t in tensors:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise RuntimeError(
+                "representax_amd kernels run on ROCm devices only; got a tensor on "
+                f"{t.device}"
+            )
+        if device is None:
+            device = t.device
+        elif t.device != device:
+            raise RuntimeError("all operands must be on the same device")
+    if device is None:
+        raise RuntimeError("no device tensor given")
+    nat.load()
+    return device
+
+
+def _workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+def _u16(t: torch.Tensor) -> torch.Tensor:
+    """View bf16/int16/uint16 storage as uint16 bit patterns."""
+
+    if t.dtype == torch.uint16:
+        return t
+    if t.dtype in (BF16, torch.int16):
+        return t.view(torch.uint16)
+    raise TypeError(f"expected 16-bit bit patterns, got {t.dtype}")
+
+
+def group_arg(group_size: int | None, k: int) -> int:
+    return 0 if group_size is None or group_size == k else int(group_size)
+
+
+# ---------------------------------------------------------------------------
+# INT4 codec
+# ---------------------------------------------------------------------------
+def int4_pack(weight: torch.Tensor, group_size: int | None = None):
+    """Quantize ``weight[*, N, K]`` -> ``(packed uint8[*, N, ceil(K/2)], scale_bits)``.
+
+    ``scale_bits`` is ``uint16[*, N]`` (one bf16 scale per row, the reference
+    scheme) or ``uint16[*, N, K/G]`` with ``group_size=G``.
+    """
+
+    device = _on_device(weight)
+    *stack, n, k = weight.shape
+    w = weight.contiguous()
+    if w.dtype not in (F32, BF16):
+        w = w.to(F32)
+    rows = int(math.prod(stack)) * n if stack else n
+    packed = torch.empty((*stack, n, (k + 1) // 2), dtype=torch.uint8, device=device)
+    g = group_arg(group_size, k)
+    scale_shape = (*stack, n) if g == 0 else (*stack, n, k // g)
+    scales = torch.empty(scale_shape, dtype=torch.uint16, device=device)
+    nat.call("rpx_int4_pack", _ptr(w), _dtype_code(w.dtype), rows, k, g, _ptr(packed),
+             _ptr(scales), _stream(device))
+    return packed, scales
+
+
+def int4_dequant(packed: torch.Tensor, scale_bits: torch.Tensor, input_size: int,
+                 group_size: int | None = None) -> torch.Tensor:
+    """``bf16[*, N, K]`` dequantized weight, bit-exact ``bf16(q * s)``."""
+
+    device = _on_device(packed, scale_bits)
+    *stack, n, pc = packed.shape
+    k = int(input_size)
+    if pc != (k + 1) // 2:
+        raise ValueError("packed width does not match input_size")
+    rows = int(math.prod(stack)) * n if stack else n
+    out = torch.empty((*stack, n, k), dtype=BF16, device=device)
+    nat.call("rpx_int4_dequant", _ptr(packed.contiguous()), _ptr(_u16(scale_bits).contiguous()),
+             rows, k, group_arg(group_size, k), _ptr(out), _stream(device))
+    return out
+
+
+def int4_merge(packed, scale_bits, lora_a, lora_b, *, alpha: float, rank: int, input_size: int,
+               group_size: int | None = None) -> torch.Tensor:
+    """float32 ``f32(W_b) + (B @ A) * (alpha / rank)`` for one ``[N, K]`` slice."""
+
+    device = _on_device(packed, scale_bits, lora_a, lora_b)
+    n = packed.shape[-2]
+    k = int(input_size)
+    out = torch.empty((n, k), dtype=F32, device=device)
+    nat.call("rpx_int4_merge", _ptr(packed.contiguous()), _ptr(_u16(scale_bits).contiguous()),
+             _ptr(lora_a.to(F32).contiguous()), _ptr(lora_b.to(F32).contiguous()), n, k,
+             group_arg(group_size, k), int(rank), float(alpha / rank), _ptr(out),
+             _stream(device))
+    return out
+
+
+# ---------------------------------------------------------------------------
+# INT4 + LoRA linear
+# ---------------------------------------------------------------------------
+def int4lora_forward(x2d, packed, scale_bits, lora_a_c, lora_b_c, *, scaling: float,
+                     group_size: int | None = None, bias_bits=None):
+    """Return ``(y [M, N], h [M, r])`` in x's compute dtype."""
+
+    device = _on_device(x2d, packed, scale_bits, lora_a_c, lora_b_c, bias_bits)
+    m, k = x2d.shape
+    n = packed.shape[-2]
+    r = lora_a_c.shape[0]
+    dt = x2d.dtype
+    code = _dtype_code(dt)
+    x2d = x2d.contiguous()
+    a = lora_a_c.to(dt).contiguous()
+    b = lora_b_c.to(dt).contiguous()
+    y = torch.empty((m, n), dtype=dt, device=device)
+    h = torch.empty((m, r), dtype=dt, device=device)
+    g = group_arg(group_size, k)
+    ws_bytes = nat.query("rpx_int4lora_forward_workspace", m, n, k, g, r, code)
+    ws = _workspace(ws_bytes, device)
+    bias = None if bias_bits is None else _u16(bias_bits).contiguous()
+    nat.call("rpx_int4lora_forward", _ptr(x2d), code, m, k, _ptr(packed.contiguous()),
+             _ptr(_u16(scale_bits).contiguous()), n, g, _ptr(bias), _ptr(a), _ptr(b), r,
+             float(scaling), _ptr(y), _ptr(h), _ptr(ws), ws.numel(), _stream(device))
+    return y, h
+
+
+def int4lora_backward(grad, x2d, packed, scale_bits, lora_a_c, lora_b_c, h, *, scaling: float,
+                      group_size: int | None = None):
+    """Return ``(dx [M, K], dA f32 [r, K], dB f32 [N, r])``."""
+
+    device = _on_device(grad, x2d, packed, scale_bits, lora_a_c, lora_b_c, h)
+    m, k = x2d.shape
+    n = packed.shape[-2]
+    r = lora_a_c.shape[0]
+    dt = x2d.dtype
+    code = _dtype_code(dt)
+    grad = grad.to(dt).contiguous()
+    a = lora_a_c.to(dt).contiguous()
+    b = lora_b_c.to(dt).contiguous()
+    dx = torch.empty((m, k), dtype=dt, device=device)
+    d_a = torch.empty((r, k), dtype=F32, device=device)
+    d_b = torch.empty((n, r), dtype=F32, device=device)
+    g = group_arg(group_size, k)
+    ws_bytes = nat.query("rpx_int4lora_backward_workspace", m, n, k, g, r, code)
+    ws = _workspace(ws_bytes, device)
+    nat.call("rpx_int4lora_backward", _ptr(grad), _ptr(x2d.contiguous()), code, m, k,
+             _ptr(packed.contiguous()), _ptr(_u16(scale_bits).contiguous()), n, g, _ptr(a),
+             _ptr(b), r, float(scaling), _ptr(h.contiguous()), _ptr(dx), _ptr(d_a), _ptr(d_b),
+             _ptr(ws), ws.numel(), _stream(device))
+    return dx, d_a, d_b
+
+
+class Int4LoRALinearFn(torch.autograd.Function):
+    """Autograd node of the fused INT4 + LoRA linear on 2-D activations.
+
+    Inputs are the activations, the LoRA compute views (differentiable; their
+    gradients are the bf16-rounded products returned in the views' dtype)
+    and the frozen integer leaves.
+    """
+
+    @staticmethod
+    def forward(ctx, x2d, lora_a_c, lora_b_c, packed, scale_bits, bias_bits, scaling, group_size):
+        y, h = int4lora_forward(x2d, packed, scale_bits, lora_a_c, lora_b_c, scaling=scaling,
+                                group_size=group_size, bias_bits=bias_bits)
+        ctx.save_for_backward(x2d, lora_a_c, lora_b_c, packed, scale_bits, h)
+        ctx.scaling = scaling
+        ctx.group_size = group_size
+        return y
+
+    @staticmethod
+    def backward(ctx, grad_y):
+        x2d, lora_a_c, lora_b_c, packed, scale_bits, h = ctx.saved_tensors
+        dx, d_a, d_b = int4lora_backward(grad_y, x2d, packed, scale_bits, lora_a_c, lora_b_c, h,
+                                         scaling=ctx.scaling, group_size=ctx.group_size)
+        return (dx, d_a.to(lora_a_c.dtype), d_b.to(lora_b_c.dtype), None, None, None, None, None)
+
+
+# ---------------------------------------------------------------------------
+# FP8
+# ---------------------------------------------------------------------------
+FORMATS = {"e4m3fn": nat.FP8_E4M3FN, "e5m2": nat.FP8_E5M2}
+
+
+def _fmt(fmt: str | int) -> int:
+    return FORMATS[fmt] if isinstance(fmt, str) else int(fmt)
+
+
+def fp8_scale(t: torch.Tensor, fmt: str = "e4m3fn") -> torch.Tensor:
+    """``float32[1]`` scale ``max(max|t| / fmax, FLT_MIN)``."""
+
+    device = _on_device(t)
+    t = t.contiguous()
+    out = torch.empty(1, dtype=F32, device=device)
+    ws = _workspace(nat.query("rpx_fp8_scale_workspace", t.numel()), device)
+    nat.call("rpx_fp8_scale", _ptr(t), _dtype_code(t.dtype), t.numel(), _fmt(fmt), _ptr(out),
+             _ptr(ws), ws.numel(), _stream(device))
+    return out
+
+
+def fp8_cast(t: torch.Tensor, scale: torch.Tensor, fmt: str = "e4m3fn", *, rowmajor=True,
+             transposed=False):
+    """Codes of a 2-D tensor: ``(out [R, C] or None, out_t [C, R] or None)``."""
+
+    device = _on_device(t, scale)
+    rows, cols = t.shape
+    out = torch.empty((rows, cols), dtype=torch.uint8, device=device) if rowmajor else None
+    out_t = torch.empty((cols, rows), dtype=torch.uint8, device=device) if transposed else None
+    nat.call("rpx_fp8_cast", _ptr(t), _dtype_code(t.dtype), rows, cols, t.stride(0), t.stride(1),
+             _ptr(scale), _fmt(fmt), _ptr(out), _ptr(out_t), _stream(device))
+    return out, out_t
+
+
+def fp8_gemm(a_codes, fmt_a, scale_a, b_codes, fmt_b, scale_b, out_dtype=BF16):
+    """``((a [M,K] . b [N,K]^T) * s_a) * s_b`` -> ``[M, N]``."""
+
+    device = _on_device(a_codes, b_codes, scale_a, scale_b)
+    m, k = a_codes.shape
+    n = b_codes.shape[0]
+    out = torch.empty((m, n), dtype=out_dtype, device=device)
+    ws = _workspace(nat.query("rpx_fp8_gemm_workspace", m, n, k), device)
+    nat.call("rpx_fp8_gemm", _ptr(a_codes.contiguous()), _fmt(fmt_a), _ptr(scale_a),
+             _ptr(b_codes.contiguous()), _fmt(fmt_b), _ptr(scale_b), m, n, k, _ptr(out),
+             _dtype_code(out_dtype), _ptr(ws), ws.numel(), _stream(device))
+    return out
+
+
+def _dense_2d(t: torch.Tensor) -> torch.Tensor:
+    """A 2-D tensor whose storage is dense (row-major or its transpose)."""
+
+    if t.is_contiguous() or t.t().is_contiguous():
+        return t
+    return t.contiguous()
+
+
+def fp8_linear_forward(left, right, out_dtype=BF16):
+    """``(out [M, N], scales f32[2])`` for ``left [M,K] . right [K,N]``."""
+
+    device = _on_device(left, right)
+    left = left.contiguous()
+    right = _dense_2d(right)
+    m, k = left.shape
+    n = right.shape[1]
+    out = torch.empty((m, n), dtype=out_dtype, device=device)
+    scales = torch.empty(2, dtype=F32, device=device)
+    if m == 0 or n == 0:
+        return out, scales
+    if k == 0:
+        raise ValueError("fp8 linear needs a non-empty contraction")
+    ws = _workspace(nat.query("rpx_fp8_linear_forward_workspace", m, n, k), device)
+    nat.call("rpx_fp8_linear_forward", _ptr(left), _dtype_code(left.dtype), m, k, _ptr(right),
+             _dtype_code(right.dtype), n, right.stride(0), right.stride(1), _ptr(out),
+             _dtype_code(out_dtype), _ptr(scales), _ptr(ws), ws.numel(), _stream(device))
+    return out, scales
+
+
+def fp8_linear_backward(left, right, grad, scales, *, need_left=True, need_right=True):
+    """``(d_left [M,K] or None, d_right [K,N] or None)`` in the operand dtypes."""
+
+    device = _on_device(left, right, grad, scales)
+    left = left.contiguous()
+    right = _dense_2d(right)
+    grad = grad.contiguous()
+    m, k = left.shape
+    n = right.shape[1]
+    if left.dtype != right.dtype:
+        raise TypeError("fp8 linear backward expects operands of one dtype")
+    d_left = torch.empty((m, k), dtype=left.dtype, device=device) if need_left else None
+    right_t = not right.is_contiguous()  # a transposed weight view gets a [N, K] gradient
+    d_right = None
+    if need_right:
+        d_right = torch.empty((n, k) if right_t else (k, n), dtype=right.dtype, device=device)
+    if m == 0 or n == 0 or k == 0:
+        if d_left is not None:
+            d_left.zero_()
+        if d_right is not None:
+            d_right.zero_()
+    elif need_left or need_right:
+        ws = _workspace(nat.query("rpx_fp8_linear_backward_workspace", m, n, k), device)
+        nat.call("rpx_fp8_linear_backward", _ptr(left), _dtype_code(left.dtype), _ptr(right),
+                 _dtype_code(right.dtype), m, k, n, right.stride(0), right.stride(1), _ptr(grad),
+                 _dtype_code(grad.dtype), _ptr(scales), _ptr(d_left), _ptr(d_right),
+                 1 if right_t else 0, _dtype_code(left.dtype), _ptr(ws), ws.numel(),
+                 _stream(device))
+    if d_right is not None and right_t:
+        d_right = d_right.t()
+    return d_left, d_right
+
+
+class Fp8LinearFn(torch.autograd.Function):
+    """``_fp8_linear_dot`` (precision.py:173-221): e4m3 forward, e5m2 backward.
+
+    The output is produced directly in ``out_dtype`` (the reference computes
+    float32 and the caller casts it to the activation dtype; rounding once
+    from the float32 epilogue value is the same result).
+    """
+
+    @staticmethod
+    def forward(ctx, left, right, out_dtype):
+        out, scales = fp8_linear_forward(left, right, out_dtype)
+        ctx.save_for_backward(left, right, scales)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad):
+        left, right, scales = ctx.saved_tensors
+        d_left, d_right = fp8_linear_backward(
+            left, right, grad, scales, need_left=ctx.needs_input_grad[0],
+            need_right=ctx.needs_input_grad[1])
+        return d_left, d_right, None

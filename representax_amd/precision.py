@@ -1,0 +1,217 @@
+"""Numerical precision boundaries (mirror of src/representax/precision.py).
+
+Same names and meaning as the reference, over torch dtypes. A policy is made
+visible with ``precision_context``; ``linear_matmul`` routes projections
+through the fp8 kernels when the policy's ``matrix_dtype`` is
+``float8_e4m3fn`` (precision.py:224-239), and otherwise through an ordinary
+matmul, as the reference does with ``jnp.matmul``.
+"""
+
+from __future__ import annotations
+
+from collections.abc import Iterator
+from contextlib import contextmanager
+from contextvars import ContextVar
+from dataclasses import dataclass
+from typing import Any
+
+import torch
+
+from . import ops
+
+
+@dataclass(frozen=True, slots=True)
+class PrecisionPolicy:
+    """Resolved dtypes for stored state, forward compute, and objectives
+    (precision.py:19-34)."""
+
+    parameter_dtype: torch.dtype
+    compute_dtype: torch.dtype
+    activation_dtype: torch.dtype
+    matrix_dtype: torch.dtype
+    accumulation_dtype: torch.dtype
+    loss_dtype: torch.dtype
+
+    @property
+    def communication_dtype(self) -> torch.dtype:
+        return self.compute_dtype
+
+
+FP32_POLICY = PrecisionPolicy(
+    parameter_dtype=torch.float32,
+    compute_dtype=torch.float32,
+    activation_dtype=torch.float32,
+    matrix_dtype=torch.float32,
+    accumulation_dtype=torch.float32,
+    loss_dtype=torch.float32,
+)
+
+_DTYPES = {
+    "float32": torch.float32,
+    "bfloat16": torch.bfloat16,
+    "float8_e4m3fn": torch.float8_e4m3fn,
+}
+_ACTIVE_PRECISION: ContextVar[PrecisionPolicy | None] = ContextVar(
+    "representax_amd_precision", default=None
+)
+
+
+def resolve_precision_policy(config: Any) -> PrecisionPolicy:
+    """Resolve a ``PrecisionConfig`` into torch dtypes (precision.py:57-67)."""
+
+    return PrecisionPolicy(
+        parameter_dtype=_DTYPES[config.parameter_dtype],
+        compute_dtype=_DTYPES[config.compute_dtype],
+        activation_dtype=_DTYPES[config.activation_dtype],
+        matrix_dtype=_DTYPES[config.resolved_matrix_dtype],
+        accumulation_dtype=_DTYPES[config.accumulation_dtype],
+        loss_dtype=_DTYPES[config.loss_dtype],
+    )
+
+
+@contextmanager
+def precision_context(policy: PrecisionPolicy) -> Iterator[None]:
+    """Make one policy visible at model/objective boundaries (precision.py:70-78)."""
+
+    token = _ACTIVE_PRECISION.set(policy)
+    try:
+        yield
+    finally:
+        _ACTIVE_PRECISION.reset(token)
+
+
+def active_policy() -> PrecisionPolicy | None:
+    return _ACTIVE_PRECISION.get()
+
+
+def _is_inexact(value: Any) -> bool:
+    return isinstance(value, torch.Tensor) and (value.is_floating_point() or value.is_complex())
+
+
+def cast_floating_tree(tree: Any, dtype: torch.dtype) -> Any:
+    """Cast floating tensors in nested dict/list/tuple containers (precision.py:81-87).
+
+    Integer tensors (packed weights, scale bits) are returned unchanged.
+    """
+
+    if isinstance(tree, torch.Tensor):
+        return tree.to(dtype) if _is_inexact(tree) else tree
+    if isinstance(tree, dict):
+        return {k: cast_floating_tree(v, dtype) for k, v in tree.items()}
+    if isinstance(tree, (list, tuple)):
+        return type(tree)(cast_floating_tree(v, dtype) for v in tree)
+    return tree
+
+
+def prepare_master_model(model: torch.nn.Module, policy: PrecisionPolicy) -> torch.nn.Module:
+    """Store floating parameters in the master dtype (precision.py:90-93)."""
+
+    for p in model.parameters():
+        if p.is_floating_point():
+            p.data = p.data.to(policy.parameter_dtype)
+    return model
+
+
+def model_for_compute(model: torch.nn.Module, policy: PrecisionPolicy) -> torch.nn.Module:
+    """Transient compute copy with floating parameters in the compute dtype
+    (precision.py:96-99). Modules of this package also cast at each use site
+    through ``compute_parameter``, which keeps the fp32 masters as the leaves
+    that receive gradients."""
+
+    import copy
+
+    view = copy.deepcopy(model)
+    for p in view.parameters():
+        if p.is_floating_point():
+            p.data = p.data.to(policy.compute_dtype)
+    return view
+
+
+def active_model_for_compute(model: torch.nn.Module) -> torch.nn.Module:
+    """``model_for_compute`` under the active policy, else ``model``
+    (precision.py:102-108)."""
+
+    policy = _ACTIVE_PRECISION.get()
+    if policy is None:
+        return model
+    return model_for_compute(model, policy)
+
+
+def compute_parameter(value: torch.Tensor) -> torch.Tensor:
+    """Compute view of a parameter at its use site (precision.py:111-117)."""
+
+    policy = _ACTIVE_PRECISION.get()
+    if policy is None:
+        return value
+    return value.to(policy.compute_dtype)
+
+
+def active_compute_dtype(fallback: torch.dtype) -> torch.dtype:
+    """Active policy's compute dtype, else ``fallback`` (precision.py:120-124)."""
+
+    policy = _ACTIVE_PRECISION.get()
+    return fallback if policy is None else policy.compute_dtype
+
+
+def linear_matmul(left: torch.Tensor, right: torch.Tensor, *, out_sharding: Any = None) -> torch.Tensor:
+    """Apply the active matrix policy to ``left [..., K] @ right [K, N]``
+    (precision.py:224-239)."""
+
+    del out_sharding  # single-device: sharding annotations are the identity
+    policy = _ACTIVE_PRECISION.get()
+    if policy is None or policy.matrix_dtype != torch.float8_e4m3fn:
+        return torch.matmul(left, right)
+    leading = left.shape[:-1]
+    flat = left.reshape(-1, left.shape[-1])
+    out = ops.Fp8LinearFn.apply(flat, right, policy.activation_dtype)
+    return out.reshape(*leading, right.shape[-1]).to(policy.activation_dtype)
+
+
+def activation_inputs(inputs: Any) -> Any:
+    """Cast model inputs to the activation dtype (precision.py:242-248)."""
+
+    policy = _ACTIVE_PRECISION.get()
+    if policy is None:
+        return inputs
+    return cast_floating_tree(inputs, policy.activation_dtype)
+
+
+def objective_output(value: torch.Tensor) -> torch.Tensor:
+    policy = _ACTIVE_PRECISION.get()
+    if policy is None:
+        return value
+    return value.to(policy.accumulation_dtype)
+
+
+def loss_value(value: torch.Tensor) -> torch.Tensor:
+    policy = _ACTIVE_PRECISION.get()
+    if policy is None:
+        return value
+    return value.to(policy.loss_dtype)
+
+
+def accumulated_values(tree: Any) -> Any:
+    policy = _ACTIVE_PRECISION.get()
+    if policy is None:
+        return tree
+    return cast_floating_tree(tree, policy.accumulation_dtype)
+
+
+__all__ = [
+    "FP32_POLICY",
+    "PrecisionPolicy",
+    "accumulated_values",
+    "active_compute_dtype",
+    "active_model_for_compute",
+    "active_policy",
+    "activation_inputs",
+    "cast_floating_tree",
+    "compute_parameter",
+    "linear_matmul",
+    "loss_value",
+    "model_for_compute",
+    "objective_output",
+    "precision_context",
+    "prepare_master_model",
+    "resolve_precision_policy",
+]

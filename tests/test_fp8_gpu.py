@@ -1,0 +1,144 @@
+"""FP8 amax / cast / GEMM / linear: HIP kernels vs the oracle (GPU)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import fp8 as ofp8
+from oracle.codecs import E4M3FN, E5M2, bf16_bits_to_f32
+from representax_amd import ops
+from tests.helpers import bf16_values, from_dev, rel_l2, rng, to_dev, to_dev_bf16
+
+pytestmark = pytest.mark.gpu
+
+FP8_TOL = 5e-2  # rel-L2 bound for fp8 GEMM outputs and gradients
+
+
+def _all_bf16_values() -> np.ndarray:
+    return bf16_bits_to_f32(np.arange(65536, dtype=np.uint32).astype(np.uint16))
+
+
+@pytest.mark.parametrize("fmt", ["e4m3fn", "e5m2"])
+def test_cast_every_bf16_value_bit_exact(fmt):
+    """All 65536 bf16 patterns x a sweep of scales: codes must match exactly."""
+
+    vals = _all_bf16_values().reshape(256, 256)
+    g = rng(3)
+    scales = [1.0, 1.17549435e-38, 2.0 ** -126, 0.1, 3.0, 1e-3, 7.5e5]
+    scales += list((10.0 ** g.uniform(-6, 6, size=12)).astype(np.float32))
+    xd = to_dev_bf16(vals)
+    for s in scales:
+        sd = torch.tensor([s], dtype=torch.float32, device="cuda")
+        out, out_t = ops.fp8_cast(xd, sd, fmt, rowmajor=True, transposed=True)
+        torch.cuda.synchronize()
+        want = ofp8.cast_with_scale(vals, np.float32(s), fmt)
+        got = out.cpu().numpy()
+        assert np.array_equal(got, want), (fmt, s)
+        assert np.array_equal(out_t.cpu().numpy(), want.T)
+
+
+@pytest.mark.parametrize("fmt", ["e4m3fn", "e5m2"])
+def test_cast_random_f32_bit_exact(fmt):
+    g = rng(4)
+    bits = g.integers(0, 2**32, size=(512, 1024), dtype=np.uint64).astype(np.uint32)
+    vals = bits.view(np.float32)
+    vals = np.where(np.isfinite(vals), vals, np.float32(1.0)).astype(np.float32)
+    for s in (np.float32(1e-30), np.float32(1.0), np.float32(3.1e30)):
+        sd = torch.tensor([s], dtype=torch.float32, device="cuda")
+        out, _ = ops.fp8_cast(to_dev(vals), sd, fmt)
+        want = ofp8.cast_with_scale(vals, s, fmt)
+        assert np.array_equal(out.cpu().numpy(), want), (fmt, s)
+
+
+@pytest.mark.parametrize("fmt", ["e4m3fn", "e5m2"])
+def test_scale_matches_oracle(fmt):
+    g = rng(5)
+    x = bf16_values(g.standard_normal((8192, 768)))
+    mask = g.random(x.shape) < 1e-3
+    x = bf16_values(np.where(mask, x * 50, x))
+    cases = {
+        "outliers": x,
+        "zeros": np.zeros((64, 96), np.float32),
+        "tiny": np.full((10, 10), 1e-39, np.float32),
+        "ragged": bf16_values(g.standard_normal((3, 7))),
+    }
+    for name, arr in cases.items():
+        s = ops.fp8_scale(to_dev_bf16(arr), fmt)
+        want = ofp8.scale_from_amax(ofp8.amax(bf16_values(arr)), fmt)
+        assert from_dev(s)[0] == want, name
+    nan_case = np.ones((4, 4), np.float32)
+    nan_case[2, 3] = np.nan
+    assert np.isnan(from_dev(ops.fp8_scale(to_dev(nan_case), fmt))[0])
+    inf_case = np.ones((4, 4), np.float32)
+    inf_case[0, 0] = -np.inf
+    assert np.isinf(from_dev(ops.fp8_scale(to_dev(inf_case), fmt))[0])
+
+
+@pytest.mark.parametrize(
+    "m,n,k,fa,fb",
+    [(256, 256, 256, E4M3FN, E4M3FN), (512, 384, 768, E5M2, E4M3FN),
+     (768, 3072, 1024, E4M3FN, E5M2), (100, 70, 200, E4M3FN, E4M3FN), (64, 96, 8192, E5M2, E5M2)],
+)
+def test_fp8_gemm_matches_oracle(m, n, k, fa, fb):
+    g = rng(m + n + k)
+    qa = g.integers(0, 256, size=(m, k), dtype=np.uint8)
+    qb = g.integers(0, 256, size=(n, k), dtype=np.uint8)
+    # keep codes finite: drop NaN / inf patterns
+    for q, f in ((qa, fa), (qb, fb)):
+        vals = ofp8.fp8_decode(q, f)
+        q[~np.isfinite(vals)] = 0x01
+    sa, sb = np.float32(0.0123), np.float32(3.7)
+    want = ofp8.scaled_dot_codes(qa, sa, fa, qb.T, sb, fb)
+    got = ops.fp8_gemm(to_dev(qa), fa, torch.tensor([sa], device="cuda"), to_dev(qb), fb,
+                       torch.tensor([sb], device="cuda"), out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    # products are exact; only the MFMA's float32 accumulation differs from the
+    # float64 sum (codes span the whole fp8 range, so cancellation is heavy)
+    assert rel_l2(from_dev(got), want) < 2e-4
+
+
+def _fp8_case(m, k, n, seed):
+    g = rng(seed)
+    x = g.standard_normal((m, k))
+    mask = g.random(x.shape) < 1e-3
+    x = bf16_values(np.where(mask, x * 50, x))
+    w = bf16_values(g.standard_normal((n, k)) * 0.02)
+    gy = bf16_values(g.standard_normal((m, n)))
+    return x, w, gy
+
+
+@pytest.mark.parametrize("m,k,n", [(1024, 768, 768), (2048, 768, 3072), (2048, 3072, 768),
+                                   (50, 40, 30)])
+def test_fp8_linear_forward_backward(m, k, n):
+    x, w, gy = _fp8_case(m, k, n, seed=m + k + n)
+    right = w.T  # linear_matmul(value, weight.T)
+    y_o = bf16_values(ofp8.fp8_linear_forward(x, right))
+    dl_o, dr_o = ofp8.fp8_linear_backward(x, right, gy)
+    xd = to_dev_bf16(x)
+    wd = to_dev_bf16(w)
+    y, scales = ops.fp8_linear_forward(xd, wd.t())
+    dl, dr = ops.fp8_linear_backward(xd, wd.t(), to_dev_bf16(gy), scales)
+    torch.cuda.synchronize()
+    s = from_dev(scales)
+    assert s[0] == ofp8.scale_from_amax(ofp8.amax(x), E4M3FN)
+    assert s[1] == ofp8.scale_from_amax(ofp8.amax(w), E4M3FN)
+    assert dr.shape == (k, n)
+    assert rel_l2(from_dev(y), y_o) < FP8_TOL
+    assert rel_l2(from_dev(dl), dl_o) < FP8_TOL
+    assert rel_l2(from_dev(dr), dr_o) < FP8_TOL
+
+
+def test_fp8_linear_bert_ffn_full_size():
+    m, k, n = 8192, 768, 3072
+    x, w, gy = _fp8_case(m, k, n, seed=77)
+    right = w.T
+    y_o = bf16_values(ofp8.fp8_linear_forward(x, right, acc=np.float32))
+    dl_o, dr_o = ofp8.fp8_linear_backward(x, right, gy, acc=np.float32)
+    xd, wd = to_dev_bf16(x), to_dev_bf16(w)
+    y, scales = ops.fp8_linear_forward(xd, wd.t())
+    dl, dr = ops.fp8_linear_backward(xd, wd.t(), to_dev_bf16(gy), scales)
+    torch.cuda.synchronize()
+    errs = [rel_l2(from_dev(y), y_o), rel_l2(from_dev(dl), dl_o), rel_l2(from_dev(dr), dr_o)]
+    assert max(errs) < FP8_TOL, errs

@@ -1,0 +1,208 @@
+"""INT4 codec and INT4+LoRA linear: HIP kernels vs the oracle (GPU)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import int4 as oint4
+from oracle import lora as olora
+from oracle.codecs import bf16_bits_to_f32, f32_to_bf16_bits
+from representax_amd import ops
+from tests.helpers import bits_from_dev, bf16_values, from_dev, rel_l2, rng, to_dev, to_dev_bf16
+
+pytestmark = pytest.mark.gpu
+
+# bf16 rel-L2 bound for GEMM outputs and gradients (accumulation order only)
+TOL = 1e-2
+
+
+def _scale_patterns(count: int, seed: int) -> np.ndarray:
+    g = rng(seed)
+    special = np.array(
+        [0x0000, 0x8000, 0x0001, 0x007F, 0x0080, 0x3F80, 0xBF80, 0x3C23, 0x7F7F, 0x4000, 0x3E00,
+         0x0100, 0x3A83, 0x3D4D],
+        dtype=np.uint16,
+    )
+    finite = g.integers(0, 0x7F80, size=count - special.size, dtype=np.uint16)
+    sign = g.integers(0, 2, size=finite.size, dtype=np.uint16) << 15
+    return np.concatenate([special, finite | sign])
+
+
+@pytest.mark.parametrize("group", [None, 64])
+def test_dequant_exhaustive_bytes(group):
+    """Every byte value (both nibbles) against many scale patterns, bit-exact."""
+
+    n = 2048
+    k = 512  # each row holds all 256 byte values
+    packed = np.tile(np.arange(256, dtype=np.uint8), (n, 1))
+    if group is None:
+        scales = _scale_patterns(n, 11)
+    else:
+        scales = _scale_patterns(n * (k // group), 12).reshape(n, k // group)
+    out = ops.int4_dequant(to_dev(packed), to_dev(scales.view(np.int16)).view(torch.uint16), k,
+                           group)
+    torch.cuda.synchronize()
+    got = bits_from_dev(out)
+    want = oint4.dequant_int4_bits(packed, scales, k, group)
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize(
+    "n,k,group",
+    [(6, 8, None), (5, 7, None), (33, 130, None), (3072, 768, None), (3072, 768, 64), (64, 256, 32),
+     (17, 96, 48)],
+)
+def test_pack_and_dequant_match_oracle(n, k, group):
+    g = rng(100 + n + k)
+    w = (g.standard_normal((n, k)) * 0.02).astype(np.float32)
+    if n > 4:
+        w[1] = 0.0  # zero row -> scale 1.0, zero nibbles
+        w[2, : min(k, 4)] = [0.5, -0.5, 0.25, 1.25][: min(k, 4)]
+    packed_d, scales_d = ops.int4_pack(to_dev(w), group)
+    torch.cuda.synchronize()
+    packed_o, scales_o = oint4.pack_int4(w, group)
+    assert np.array_equal(packed_d.cpu().numpy(), packed_o)
+    assert np.array_equal(bits_from_dev(scales_d), scales_o)
+    deq = ops.int4_dequant(packed_d, scales_d, k, group)
+    assert np.array_equal(bits_from_dev(deq), oint4.dequant_int4_bits(packed_o, scales_o, k, group))
+
+
+def test_pack_from_bf16_weights():
+    g = rng(7)
+    w = bf16_values(g.standard_normal((64, 128)) * 0.05)
+    packed_d, scales_d = ops.int4_pack(to_dev_bf16(w))
+    packed_o, scales_o = oint4.pack_int4(w)
+    assert np.array_equal(packed_d.cpu().numpy(), packed_o)
+    assert np.array_equal(bits_from_dev(scales_d), scales_o)
+
+
+def _lora_case(m, k, n, r, group, seed, bias=True):
+    g = rng(seed)
+    x = bf16_values(g.standard_normal((m, k)))
+    w = (g.standard_normal((n, k)) * 0.02).astype(np.float32)
+    a = (g.standard_normal((r, k)) * 0.02).astype(np.float32)
+    b = (g.standard_normal((n, r)) * 0.02).astype(np.float32)
+    bias_v = (g.standard_normal(n) * 0.1).astype(np.float32) if bias else None
+    gy = bf16_values(g.standard_normal((m, n)))
+    packed, scales = oint4.pack_int4(w, group)
+    bias_bits = None if bias_v is None else f32_to_bf16_bits(bias_v)
+    return x, packed, scales, a, b, bias_bits, gy
+
+
+LORA_SHAPES = [
+    # (m, k, n, r, group): fused MFMA path
+    (256, 128, 192, 16, None),
+    (300, 256, 320, 16, 64),
+    (512, 768, 3072, 16, None),
+    (96, 512, 256, 32, 128),
+    (64, 192, 128, 8, None),
+    # generic path (the reference test's 8->6, rank 2; odd sizes)
+    (4, 8, 6, 2, None),
+    (37, 100, 52, 3, None),
+    (20, 96, 100, 72, None),
+]
+
+
+@pytest.mark.parametrize("m,k,n,r,group", LORA_SHAPES)
+def test_int4lora_forward_backward(m, k, n, r, group):
+    x, packed, scales, a, b, bias_bits, gy = _lora_case(m, k, n, r, group, seed=m * 7 + k)
+    alpha = 2.0 * r
+    y_o, h_o = olora.lora_forward(x, packed, scales, a, b, alpha=alpha, rank=r,
+                                  bias_bits=bias_bits, group_size=group)
+    dx_o, da_o, db_o = olora.lora_backward(gy, x, packed, scales, a, b, h_o, alpha=alpha, rank=r,
+                                           group_size=group)
+    xd = to_dev_bf16(x)
+    pd = to_dev(packed)
+    sd = to_dev(scales.view(np.int16)).view(torch.uint16)
+    ad = to_dev_bf16(a)
+    bd = to_dev_bf16(b)
+    biasd = None if bias_bits is None else to_dev(bias_bits.view(np.int16)).view(torch.uint16)
+    y, h = ops.int4lora_forward(xd, pd, sd, ad, bd, scaling=alpha / r, group_size=group,
+                                bias_bits=biasd)
+    dx, da, db = ops.int4lora_backward(to_dev_bf16(gy), xd, pd, sd, ad, bd, h, scaling=alpha / r,
+                                       group_size=group)
+    torch.cuda.synchronize()
+    assert rel_l2(from_dev(h), h_o) < TOL
+    assert rel_l2(from_dev(y), y_o) < TOL
+    assert rel_l2(from_dev(dx), dx_o) < TOL
+    assert rel_l2(from_dev(da), da_o) < TOL
+    assert rel_l2(from_dev(db), db_o) < TOL
+    # dA / dB are float32 holding bf16-rounded values (reference: f32(bf16(.)))
+    assert np.array_equal(bf16_values(from_dev(da)), from_dev(da))
+    assert np.array_equal(bf16_values(from_dev(db)), from_dev(db))
+
+
+def test_int4lora_fp32_policy_generic():
+    """fp32 compute (no precision context): every op in float32."""
+
+    m, k, n, r = 16, 64, 48, 4
+    x, packed, scales, a, b, bias_bits, gy = _lora_case(m, k, n, r, None, seed=5)
+    x = np.random.default_rng(1).standard_normal((m, k)).astype(np.float32)
+    gy = np.random.default_rng(2).standard_normal((m, n)).astype(np.float32)
+    y_o, h_o = olora.lora_forward(x, packed, scales, a, b, alpha=8.0, rank=r, bias_bits=bias_bits,
+                                  compute="f32")
+    dx_o, da_o, db_o = olora.lora_backward(gy, x, packed, scales, a, b, h_o, alpha=8.0, rank=r,
+                                           compute="f32")
+    pd = to_dev(packed)
+    sd = to_dev(scales.view(np.int16)).view(torch.uint16)
+    biasd = to_dev(bias_bits.view(np.int16)).view(torch.uint16)
+    y, h = ops.int4lora_forward(to_dev(x), pd, sd, to_dev(a), to_dev(b), scaling=2.0,
+                                bias_bits=biasd)
+    dx, da, db = ops.int4lora_backward(to_dev(gy), to_dev(x), pd, sd, to_dev(a), to_dev(b), h,
+                                       scaling=2.0)
+    torch.cuda.synchronize()
+    for got, want in ((y, y_o), (h, h_o), (dx, dx_o), (da, da_o), (db, db_o)):
+        assert rel_l2(from_dev(got), want) < 1e-5
+
+
+def test_int4lora_full_bert_ffn_shape():
+    """BERT-base FFN up-projection at the benchmark size: x [4096, 768], W 768->3072."""
+
+    m, k, n, r = 4096, 768, 3072, 16
+    x, packed, scales, a, b, bias_bits, gy = _lora_case(m, k, n, r, None, seed=2024)
+    y_o, h_o = olora.lora_forward(x, packed, scales, a, b, alpha=32.0, rank=r, bias_bits=bias_bits)
+    dx_o, da_o, db_o = olora.lora_backward(gy, x, packed, scales, a, b, h_o, alpha=32.0, rank=r)
+    xd = to_dev_bf16(x)
+    pd = to_dev(packed)
+    sd = to_dev(scales.view(np.int16)).view(torch.uint16)
+    ad, bd = to_dev_bf16(a), to_dev_bf16(b)
+    biasd = to_dev(bias_bits.view(np.int16)).view(torch.uint16)
+    y, h = ops.int4lora_forward(xd, pd, sd, ad, bd, scaling=2.0, bias_bits=biasd)
+    dx, da, db = ops.int4lora_backward(to_dev_bf16(gy), xd, pd, sd, ad, bd, h, scaling=2.0)
+    torch.cuda.synchronize()
+    errs = {name: rel_l2(from_dev(got), want) for name, got, want in
+            (("y", y, y_o), ("h", h, h_o), ("dx", dx, dx_o), ("dA", da, da_o), ("dB", db, db_o))}
+    assert all(e < TOL for e in errs.values()), errs
+
+
+def test_merge_matches_oracle():
+    n, k, r = 96, 128, 8
+    g = rng(9)
+    w = (g.standard_normal((n, k)) * 0.02).astype(np.float32)
+    a = (g.standard_normal((r, k)) * 0.1).astype(np.float32)
+    b = (g.standard_normal((n, r)) * 0.1).astype(np.float32)
+    packed, scales = oint4.pack_int4(w)
+    got = ops.int4_merge(to_dev(packed), to_dev(scales.view(np.int16)).view(torch.uint16),
+                         to_dev(a), to_dev(b), alpha=16.0, rank=r, input_size=k)
+    want = olora.merged_weight(packed, scales, a, b, alpha=16.0, rank=r, input_size=k)
+    np.testing.assert_allclose(got.cpu().numpy(), want, rtol=1e-5, atol=1e-6)
+
+
+def test_invalid_arguments_raise_before_launch():
+    pd = torch.zeros((4, 4), dtype=torch.uint8, device="cuda")
+    sd = torch.zeros(4, dtype=torch.uint16, device="cuda")
+    with pytest.raises(ValueError):
+        ops.int4_dequant(pd, sd, 8, group_size=3)
+    x = torch.zeros((2, 8), dtype=torch.bfloat16, device="cuda")
+    a = torch.zeros((9, 8), dtype=torch.bfloat16, device="cuda")
+    b = torch.zeros((4, 9), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(ValueError):
+        ops.int4lora_forward(x, pd, sd, a, b, scaling=1.0)
+
+
+def test_cpu_tensor_is_rejected():
+    with pytest.raises(RuntimeError):
+        ops.int4_dequant(torch.zeros((4, 4), dtype=torch.uint8),
+                         torch.zeros(4, dtype=torch.uint16), 8)
