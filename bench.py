@@ -1,0 +1,439 @@
+"""Throughput of the quantized-linear hot path on one MI355X.
+
+Primary line: FP8 e4m3 linear with dynamic per-tensor amax scaling, forward +
+backward, over all four BERT-base linear shapes (768->768 x4 for Q/K/V/O,
+768->3072, 3072->768) at 8192 tokens; x ~N(0,1) bf16 with 0.1% outliers x50,
+W ~N(0,0.02). One step = fwd+bwd of the six linears. Value = algorithmic
+TFLOP/s (3 GEMMs of 2*M*N*K per linear).
+
+Secondary lines (same JSON object): the packed-INT4 + LoRA linear fwd+bwd at
+the BERT-base FFN up-projection (x [4096, 768], W 768->3072, rank 16,
+alpha 32) and the skinny-M inference sweep (M in {1,4,16,64}, Qwen3-2B-shaped
+projections, rank 32) with rotating weight copies larger than the 256 MB
+Infinity Cache.
+
+The roofline object is for the dominant kernel (the fp8 MFMA GEMM): its
+algorithmic FLOPs over its own launch durations, timed with HIP events on the
+stream the kernels run on. cpu_baseline times the numpy oracle on host cores
+on a bounded sample of the same workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+FP8_PEAK_TFLOPS = 5000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+BERT_LINEARS = [("q", 768, 768), ("k", 768, 768), ("v", 768, 768), ("o", 768, 768),
+                ("ffn_up", 768, 3072), ("ffn_down", 3072, 768)]
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__)
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--tokens", type=int, default=8192)
+    p.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a HIP graph")
+    p.add_argument("--no-secondary", action="store_true")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--only", choices=["fp8", "int4lora", "skinny"], default=None,
+                   help="run one workload and nothing else (profiling)")
+    return p.parse_args()
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def bf16_tensor(a, device):
+    import torch
+
+    from oracle.codecs import f32_to_bf16_bits
+
+    bits = f32_to_bf16_bits(np.asarray(a, np.float32)).view(np.int16)
+    return torch.from_numpy(bits.copy()).to(device).view(torch.bfloat16)
+
+
+def outlier_activations(g, m, k):
+    x = g.standard_normal((m, k)).astype(np.float32)
+    mask = g.random((m, k)) < 1e-3
+    return np.where(mask, x * 50.0, x).astype(np.float32)
+
+
+def time_region(fn, steps, warmup):
+    """Mean ms per call of fn over `steps` calls after `warmup`, bracketed by
+    device synchronization."""
+
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e3 / steps
+
+
+def maybe_graph(fn, use_graph):
+    """Capture fn into a HIP graph (torch.cuda.CUDAGraph) when requested."""
+
+    import torch
+
+    if not use_graph:
+        return fn, "eager"
+    fn()  # first launch outside capture (one-time kernel attribute setup)
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        for _ in range(2):
+            fn()
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        fn()
+    torch.cuda.synchronize()
+    return graph.replay, "hipgraph"
+
+
+def event_time_ms(fn, reps):
+    """Per-call GPU duration of fn (HIP events on the current stream)."""
+
+    import torch
+
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    fn()
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(reps):
+        fn()
+    end.record()
+    end.synchronize()
+    return start.elapsed_time(end) / reps
+
+
+# ---------------------------------------------------------------------------
+# FP8 workload (primary)
+# ---------------------------------------------------------------------------
+def fp8_setup(tokens, device, seed=0):
+    g = np.random.Generator(np.random.PCG64(seed))
+    layers = []
+    for name, k, n in BERT_LINEARS:
+        x = bf16_tensor(outlier_activations(g, tokens, k), device)
+        w = bf16_tensor(g.standard_normal((n, k)).astype(np.float32) * 0.02, device)
+        gy = bf16_tensor(g.standard_normal((tokens, n)).astype(np.float32), device)
+        layers.append((name, x, w, gy, k, n))
+    return layers
+
+
+def fp8_step_fn(layers):
+    from representax_amd import ops
+
+    def step():
+        for _, x, w, gy, _, _ in layers:
+            _, scales = ops.fp8_linear_forward(x, w.t())
+            ops.fp8_linear_backward(x, w.t(), gy, scales)
+
+    return step
+
+
+def fp8_flops(tokens):
+    return sum(6.0 * tokens * k * n for _, k, n in BERT_LINEARS)
+
+
+def fp8_gemm_roofline(layers, reps=20):
+    """Dominant kernel: the fp8 MFMA GEMMs of one step, launched on the same
+    codes the step produces; achieved = algorithmic FLOPs / event time."""
+
+    import torch
+
+    from representax_amd import ops
+
+    calls = []
+    for _, x, w, gy, k, n in layers:
+        m = x.shape[0]
+        s_x = ops.fp8_scale(x, "e4m3fn")
+        s_w = ops.fp8_scale(w, "e4m3fn")
+        s_g = ops.fp8_scale(gy, "e5m2")
+        qx, qxt = ops.fp8_cast(x, s_x, "e4m3fn", rowmajor=True, transposed=True)
+        qw, qwt = ops.fp8_cast(w, s_w, "e4m3fn", rowmajor=True, transposed=True)
+        qg, qgt = ops.fp8_cast(gy, s_g, "e5m2", rowmajor=True, transposed=True)
+        calls.append((lambda a=qx, b=qw, sa=s_x, sb=s_w: ops.fp8_gemm(a, "e4m3fn", sa, b, "e4m3fn", sb),
+                      2.0 * m * n * k))
+        calls.append((lambda a=qg, b=qwt, sa=s_g, sb=s_w: ops.fp8_gemm(a, "e5m2", sa, b, "e4m3fn", sb),
+                      2.0 * m * n * k))
+        calls.append((lambda a=qgt, b=qxt, sa=s_x, sb=s_g: ops.fp8_gemm(a, "e5m2", sa, b, "e4m3fn", sb),
+                      2.0 * m * n * k))
+    torch.cuda.synchronize()
+    total_ms = 0.0
+    total_flops = 0.0
+    per_call = []
+    for fn, flops in calls:
+        ms = event_time_ms(fn, reps)
+        per_call.append(ms)
+        total_ms += ms
+        total_flops += flops
+    achieved = total_flops / (total_ms * 1e-3) / 1e12
+    return {
+        "bound": "mfma",
+        "achieved": round(achieved, 2),
+        "peak": FP8_PEAK_TFLOPS,
+        "unit": "TFLOP/s",
+        "frac": round(achieved / FP8_PEAK_TFLOPS, 4),
+        "traffic": None,
+        "kernel": "k_fp8_gemm (fwd e4m3xe4m3, dX e5m2xe4m3, dW e5m2xe4m3; 18 launches/step)",
+        "avg_launch_us": round(1e3 * total_ms / len(calls), 2),
+        "flops_per_launch_avg": total_flops / len(calls),
+    }
+
+
+def fp8_cpu_baseline(seed=1):
+    """Oracle fp8 linear fwd+bwd (numpy, float32 BLAS accumulate) on a bounded
+    sample: the 768->3072 linear at 1024 tokens, repeated to ~10-20 s."""
+
+    from oracle import fp8 as ofp8
+    from oracle.codecs import bf16_round
+
+    g = np.random.Generator(np.random.PCG64(seed))
+    m, k, n = 1024, 768, 3072
+    x = bf16_round(outlier_activations(g, m, k))
+    w = bf16_round(g.standard_normal((n, k)).astype(np.float32) * 0.02)
+    gy = bf16_round(g.standard_normal((m, n)).astype(np.float32))
+    flops = 6.0 * m * n * k
+    reps = 0
+    t0 = time.perf_counter()
+    while True:
+        ofp8.fp8_linear_forward(x, w.T, acc=np.float32)
+        ofp8.fp8_linear_backward(x, w.T, gy, acc=np.float32)
+        reps += 1
+        if time.perf_counter() - t0 > 10.0 or reps >= 50:
+            break
+    dt = (time.perf_counter() - t0) / reps
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return {
+        "value": round(flops / dt / 1e12, 5),
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"numpy oracle fp8 linear fwd+bwd, 768->3072 at {m} tokens, {reps} reps, "
+                  f"{dt * 1e3:.0f} ms each (fp32 BLAS accumulate)",
+    }
+
+
+# ---------------------------------------------------------------------------
+# INT4 + LoRA workload (secondary)
+# ---------------------------------------------------------------------------
+def int4lora_setup(device, group_size=None, seed=2):
+    import torch
+
+    from representax_amd import ops
+
+    g = np.random.Generator(np.random.PCG64(seed))
+    m, k, n, r = 4096, 768, 3072, 16
+    x = bf16_tensor(g.standard_normal((m, k)).astype(np.float32), device)
+    w = torch.from_numpy((g.standard_normal((n, k)) * 0.02).astype(np.float32)).to(device)
+    packed, scales = ops.int4_pack(w, group_size)
+    a = bf16_tensor(g.standard_normal((r, k)).astype(np.float32) * 0.02, device)
+    b = bf16_tensor(g.standard_normal((n, r)).astype(np.float32) * 0.02, device)
+    bias = bf16_tensor(np.zeros(n, np.float32), device).view(torch.uint16)
+    gy = bf16_tensor(g.standard_normal((m, n)).astype(np.float32), device)
+    return dict(x=x, packed=packed, scales=scales, a=a, b=b, bias=bias, gy=gy, m=m, k=k, n=n, r=r,
+                group=group_size)
+
+
+def int4lora_step_fn(c):
+    from representax_amd import ops
+
+    def step():
+        _, h = ops.int4lora_forward(c["x"], c["packed"], c["scales"], c["a"], c["b"], scaling=2.0,
+                                    group_size=c["group"], bias_bits=c["bias"])
+        ops.int4lora_backward(c["gy"], c["x"], c["packed"], c["scales"], c["a"], c["b"], h,
+                              scaling=2.0, group_size=c["group"])
+
+    return step
+
+
+def int4lora_flops(c):
+    m, k, n, r = c["m"], c["k"], c["n"], c["r"]
+    fwd = 2 * m * n * k + 2 * m * k * r + 2 * m * r * n
+    bwd = 2 * m * n * k + 4 * m * n * r + 4 * m * r * k
+    return float(fwd + bwd)
+
+
+def int4lora_roofline(c, reps=20):
+    """The fused dequant + MFMA forward GEMM (the path's defining kernel)."""
+
+    from representax_amd import ops
+
+    def fwd():
+        ops.int4lora_forward(c["x"], c["packed"], c["scales"], c["a"], c["b"], scaling=2.0,
+                             group_size=c["group"], bias_bits=c["bias"])
+
+    ms = event_time_ms(fwd, reps)
+    m, k, n, r = c["m"], c["k"], c["n"], c["r"]
+    flops = 2.0 * m * n * k + 2 * m * k * r + 2 * m * r * n
+    achieved = flops / (ms * 1e-3) / 1e12
+    return {"bound": "mfma", "achieved": round(achieved, 2), "peak": BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s", "frac": round(achieved / BF16_PEAK_TFLOPS, 4),
+            "kernel": "int4lora_forward (rank-r down kernel + fused dequant GEMM)",
+            "avg_call_us": round(ms * 1e3, 2)}
+
+
+def run_int4lora(steps, warmup, use_graph, group_size=None):
+    import torch
+
+    c = int4lora_setup(torch.device("cuda:0"), group_size)
+    fn, mode = maybe_graph(int4lora_step_fn(c), use_graph)
+    ms = time_region(fn, steps, warmup)
+    tflops = int4lora_flops(c) / (ms * 1e-3) / 1e12
+    line = {
+        "workload": "int4lora linear fwd+bwd, x[4096,768] bf16, W 768->3072 INT4 "
+                    f"({'per-row scales' if group_size is None else f'group {group_size}'}), "
+                    "rank 16, alpha 32",
+        "value": round(tflops, 2), "unit": "TFLOP/s", "ms_per_step": round(ms, 4), "mode": mode,
+        "roofline": int4lora_roofline(c),
+    }
+    return line
+
+
+# ---------------------------------------------------------------------------
+# Skinny-M inference sweep (secondary)
+# ---------------------------------------------------------------------------
+SKINNY_SHAPES = [(2048, 6144), (6144, 2048), (2048, 2048)]
+
+
+def run_skinny(reps=200):
+    import torch
+
+    from representax_amd import ops
+
+    dev = torch.device("cuda:0")
+    g = np.random.Generator(np.random.PCG64(5))
+    r = 32
+    out = []
+    for k, n in SKINNY_SHAPES:
+        per_copy = n * k // 2 + n * 2 + (r * k + n * r) * 2
+        copies = max(8, int(np.ceil(300e6 / per_copy)))  # > 256 MB Infinity Cache
+        w = torch.from_numpy((g.standard_normal((n, k)) * 0.02).astype(np.float32)).to(dev)
+        packed, scales = ops.int4_pack(w)
+        del w
+        pool = [(packed.clone(), scales.clone(),
+                 bf16_tensor(g.standard_normal((r, k)).astype(np.float32) * 0.02, dev),
+                 bf16_tensor(g.standard_normal((n, r)).astype(np.float32) * 0.02, dev))
+                for _ in range(copies)]
+        for m in (1, 4, 16, 64):
+            x = bf16_tensor(g.standard_normal((m, k)).astype(np.float32), dev)
+            starts = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
+            ends = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
+            for i in range(min(copies, 16)):
+                p, s, a, b = pool[i % copies]
+                ops.int4lora_forward(x, p, s, a, b, scaling=1.0)
+            torch.cuda.synchronize()
+            for i in range(reps):
+                p, s, a, b = pool[i % copies]
+                starts[i].record()
+                ops.int4lora_forward(x, p, s, a, b, scaling=1.0)
+                ends[i].record()
+            torch.cuda.synchronize()
+            lat = sorted(st.elapsed_time(en) * 1e3 for st, en in zip(starts, ends))
+            p50 = statistics.median(lat)
+            nbytes = n * k / 2 + n * 2 + (r * k + n * r) * 2 + m * k * 2 + m * n * 2
+            out.append({"m": m, "k": k, "n": n, "p50_us": round(p50, 2),
+                        "gbs": round(nbytes / (p50 * 1e-6) / 1e9, 1),
+                        "frac_hbm": round(nbytes / (p50 * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
+        del pool
+        torch.cuda.empty_cache()
+    return {"workload": "skinny-M INT4+LoRA forward (rank 32, per-row scales), rotating "
+                        "weight copies > 256 MB", "points": out}
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
+              "(the path would shard tokens across GPUs with one dA/dB all-reduce per linear)",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        sys.exit(1)
+    from representax_amd import _native
+
+    _native.load()
+    dev = torch.device("cuda:0")
+    use_graph = not args.no_graph
+
+    if args.only == "int4lora":
+        print(json.dumps(run_int4lora(args.steps, args.warmup, use_graph)))
+        return
+    if args.only == "skinny":
+        print(json.dumps(run_skinny()))
+        return
+
+    log("fp8: setting up inputs")
+    layers = fp8_setup(args.tokens, dev)
+    fn, mode = maybe_graph(fp8_step_fn(layers), use_graph)
+    log(f"fp8: timing {args.steps} steps ({mode})")
+    ms = time_region(fn, args.steps, args.warmup)
+    value = fp8_flops(args.tokens) / (ms * 1e-3) / 1e12
+    log(f"fp8: {ms:.3f} ms/step, {value:.1f} TFLOP/s; timing GEMM launches")
+    roofline = fp8_gemm_roofline(layers)
+    result = {
+        "metric": "INT4-LoRA/FP8 linear TFLOP/s & % roofline; train-step tokens/sec, 1 GPU",
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8-e4m3/e5m2 (f32 accumulate, bf16 out)",
+        "data": "synthetic",
+        "config": {
+            "workload": "fp8 e4m3 linear fwd+bwd, dynamic per-tensor amax, BERT-base shapes "
+                        "768->768 x4, 768->3072, 3072->768",
+            "tokens": args.tokens,
+            "x": "bf16 ~N(0,1), 0.1% outliers x50",
+            "w": "bf16 ~N(0,0.02)",
+            "mode": mode,
+        },
+        "roofline": roofline,
+    }
+    if args.only is None and not args.no_secondary:
+        del layers, fn
+        torch.cuda.empty_cache()
+        log("int4lora: per-row and group-64")
+        result["secondary"] = [run_int4lora(args.steps, args.warmup, use_graph),
+                               run_int4lora(args.steps, args.warmup, use_graph, group_size=64)]
+        log("skinny-M sweep")
+        result["secondary"].append(run_skinny())
+    if args.only is None and not args.no_cpu_baseline:
+        log("cpu baseline (numpy oracle)")
+        result["cpu_baseline"] = fp8_cpu_baseline()
+    print(json.dumps(result))
+
+
+if __name__ == "__main__":
+    main()
