@@ -148,9 +148,10 @@ def fp8_step_fn(layers):
     from representax_amd import ops
 
     def step():
-        for _, x, w, gy, _, _ in layers:
-            _, scales = ops.fp8_linear_forward(x, w.t())
-            ops.fp8_linear_backward(x, w.t(), gy, scales)
+        for _, x, w, gy, k, _ in layers:
+            _, scales, codes = ops.fp8_linear_forward(x, w.t(), save_codes=True)
+            ops.fp8_linear_backward_codes(codes, scales, gy, k=k, dtype=x.dtype,
+                                          right_transposed=True)
 
     return step
 

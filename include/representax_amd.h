@@ -136,20 +136,24 @@ size_t rpx_fp8_linear_forward_workspace(int64_t m, int64_t n, int64_t k);
 
 /* out [m, n] = _fp8_linear_dot(left [m, k], right [k, n]) with e4m3 operands;
  * right is addressed through (row_stride, col_stride) so a transposed weight
- * view needs no copy. scales_out[0..1] receive (s_left, s_right) for the
- * backward. Replaces _fp8_linear_dot / _fp8_linear_dot_forward,
- * src/representax/precision.py:173-198 (as used by linear_matmul, :224-239). */
+ * view needs no copy. scales_out[0..1] receive (s_left, s_right). The same
+ * pass can also write the backward's operand codes: left_t_codes [k, m] and
+ * right_codes [k, n] (either may be NULL). Replaces _fp8_linear_dot /
+ * _fp8_linear_dot_forward, src/representax/precision.py:173-198 (as used by
+ * linear_matmul, :224-239). */
 int rpx_fp8_linear_forward(const void* left, int left_dtype, int64_t m, int64_t k,
                            const void* right, int right_dtype, int64_t n, int64_t right_row_stride,
                            int64_t right_col_stride, void* out, int out_dtype, float* scales_out,
-                           void* workspace, size_t workspace_bytes, void* stream);
+                           uint8_t* left_t_codes, uint8_t* right_codes, void* workspace,
+                           size_t workspace_bytes, void* stream);
 
 size_t rpx_fp8_linear_backward_workspace(int64_t m, int64_t n, int64_t k);
 
 /* d_left [m, k] = scaled_dot(g[e5m2], right^T[e4m3]) and d_right =
  * scaled_dot(left^T[e4m3], g[e5m2]) as [k, n], or as [n, k] when
  * d_right_transposed; either output may be NULL to skip it. `scales` are the
- * forward's (s_left, s_right). m, n, k must be positive.
+ * forward's (s_left, s_right); the operands are re-quantized with them,
+ * which reproduces the reference's recomputed amax exactly. m, n, k > 0.
  * Replaces _fp8_linear_dot_backward, src/representax/precision.py:201-218. */
 int rpx_fp8_linear_backward(const void* left, int left_dtype, const void* right, int right_dtype,
                             int64_t m, int64_t k, int64_t n, int64_t right_row_stride,
@@ -157,6 +161,24 @@ int rpx_fp8_linear_backward(const void* left, int left_dtype, const void* right,
                             const float* scales, void* d_left, void* d_right,
                             int d_right_transposed, int out_dtype, void* workspace,
                             size_t workspace_bytes, void* stream);
+
+/* The same backward from the operand codes that rpx_fp8_linear_forward
+ * saved (left_t_codes [k, m], right_codes [k, n]); the bf16 operands are not
+ * read again. Workspace: rpx_fp8_linear_backward_workspace(m, n, k).
+ * Replaces _fp8_linear_dot_backward, src/representax/precision.py:201-218. */
+int rpx_fp8_linear_backward_codes(const uint8_t* left_t_codes, const uint8_t* right_codes,
+                                  const float* scales, int64_t m, int64_t k, int64_t n,
+                                  const void* grad, int grad_dtype, void* d_left, void* d_right,
+                                  int d_right_transposed, int out_dtype, void* workspace,
+                                  size_t workspace_bytes, void* stream);
+
+/* Test hook: compares the cast kernels' fp8 encoder (hardware convert in
+ * range) with the integer encoder for the f32 bit patterns
+ * [first, first + count) and their negations; block_counts[b] /
+ * block_first[b] receive each block's mismatch count and lowest mismatching
+ * pattern (0xFFFFFFFF if none). No reference counterpart. */
+int rpx_fp8_encode_selfcheck(int fmt, uint64_t first, uint64_t count, uint32_t* block_counts,
+                             uint32_t* block_first, int64_t blocks, void* stream);
 
 /* Host-side test hook: the device quantizer (divide by scale, round to fp8)
  * run on host memory, so that it can be checked exhaustively on a CPU. No

@@ -56,13 +56,19 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
     "rpx_fp8_linear_forward_workspace": (_size, [_i64, _i64, _i64]),
     "rpx_fp8_linear_forward": (
-        _int, [_p, _int, _i64, _i64, _p, _int, _i64, _i64, _i64, _p, _int, _p, _p, _size, _p]
+        _int, [_p, _int, _i64, _i64, _p, _int, _i64, _i64, _i64, _p, _int, _p, _p, _p, _p, _size, _p]
     ),
     "rpx_fp8_linear_backward_workspace": (_size, [_i64, _i64, _i64]),
     "rpx_fp8_linear_backward": (
         _int,
         [_p, _int, _p, _int, _i64, _i64, _i64, _i64, _i64, _p, _int, _p, _p, _p, _int, _int, _p,
          _size, _p],
+    ),
+    "rpx_fp8_linear_backward_codes": (
+        _int, [_p, _p, _p, _i64, _i64, _i64, _p, _int, _p, _p, _int, _int, _p, _size, _p]
+    ),
+    "rpx_fp8_encode_selfcheck": (
+        _int, [_int, ctypes.c_uint64, ctypes.c_uint64, _p, _p, _i64, _p]
     ),
     "rpx_host_fp8_quantize": (_int, [_p, _i64, _f32, _int, _p]),
 }

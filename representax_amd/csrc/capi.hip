@@ -468,8 +468,8 @@ int rpx_fp8_scale(const void* t, int dtype, int64_t numel, int fmt, float* scale
   const int64_t np = fp8_amax_partials(numel);
   if (workspace == nullptr || workspace_bytes < static_cast<size_t>(np) * sizeof(uint32_t))
     return fail_invalid("rpx_fp8_scale: workspace too small");
-  RPX_HIP(launch_fp8_amax(t, dtype, numel, 1, 1, 1, static_cast<uint32_t*>(workspace), np, fmt,
-                          scale_out, static_cast<hipStream_t>(stream)),
+  RPX_HIP(launch_fp8_amax(t, dtype, numel, static_cast<uint32_t*>(workspace), np, fmt, scale_out,
+                          static_cast<hipStream_t>(stream)),
           "rpx_fp8_scale");
   return kOk;
 }
@@ -482,8 +482,8 @@ int rpx_fp8_cast(const void* t, int dtype, int64_t rows, int64_t cols, int64_t r
   if (rows < 0 || cols < 0) return fail_invalid("rows and cols must be non-negative");
   if (scale == nullptr || (rows * cols > 0 && t == nullptr)) return fail_invalid("rpx_fp8_cast: null pointer");
   if (out == nullptr && out_t == nullptr) return fail_invalid("rpx_fp8_cast: no output requested");
-  RPX_HIP(launch_fp8_cast(t, dtype, rows, cols, row_stride, col_stride, scale, fmt, out, out_t,
-                          static_cast<hipStream_t>(stream)),
+  RPX_HIP(launch_fp8_cast(t, dtype, rows, cols, row_stride, col_stride, scale, nullptr, 0, nullptr,
+                          fmt, out, out_t, static_cast<hipStream_t>(stream)),
           "rpx_fp8_cast");
   return kOk;
 }
@@ -615,34 +615,39 @@ size_t rpx_fp8_linear_forward_workspace(int64_t m, int64_t n, int64_t k) {
 int rpx_fp8_linear_forward(const void* left, int left_dtype, int64_t m, int64_t k,
                            const void* right, int right_dtype, int64_t n, int64_t right_row_stride,
                            int64_t right_col_stride, void* out, int out_dtype, float* scales_out,
-                           void* workspace, size_t workspace_bytes, void* stream) {
+                           uint8_t* left_t_codes, uint8_t* right_codes, void* workspace,
+                           size_t workspace_bytes, void* stream) {
   RPX_TRY(check_dtype(left_dtype));
   RPX_TRY(check_dtype(right_dtype));
   RPX_TRY(check_dtype(out_dtype));
   if (m < 0 || n < 0 || k < 0) return fail_invalid("m, n, k must be non-negative");
   if (scales_out == nullptr) return fail_invalid("rpx_fp8_linear_forward: null scales_out");
   if (m == 0 || n == 0) return kOk;
+  if (k == 0) return fail_invalid("rpx_fp8_linear_forward: empty contraction");
   if (left == nullptr || right == nullptr || out == nullptr)
     return fail_invalid("rpx_fp8_linear_forward: null pointer");
   hipStream_t st = static_cast<hipStream_t>(stream);
   Arena ar(workspace, workspace_bytes);
-  uint32_t* pl = ar.take<uint32_t>(fp8_amax_partials(m * k));
-  uint32_t* pr = ar.take<uint32_t>(fp8_amax_partials(k * n));
+  const int64_t npl = fp8_amax_partials(m * k);
+  const int64_t npr = fp8_amax_partials(k * n);
+  uint32_t* pl = ar.take<uint32_t>(npl);
+  uint32_t* pr = ar.take<uint32_t>(npr);
   uint8_t* ql = ar.take<uint8_t>(m * k);
   uint8_t* qr = ar.take<uint8_t>(n * k);
   const size_t gws = rpx_fp8_gemm_workspace(m, n, k);
   uint8_t* gw = ar.take<uint8_t>(static_cast<int64_t>(gws));
   if (ar.overflow) return fail_invalid("rpx_fp8_linear_forward: workspace too small");
-  RPX_HIP(launch_fp8_amax(left, left_dtype, m, k, k, 1, pl, fp8_amax_partials(m * k), kE4M3FN,
-                          scales_out, st),
+  RPX_HIP(launch_fp8_amax(left, left_dtype, m * k, pl, npl, kE4M3FN, nullptr, st),
           "fp8_linear_forward: amax(left)");
-  RPX_HIP(launch_fp8_amax(right, right_dtype, k, n, right_row_stride, right_col_stride, pr,
-                          fp8_amax_partials(k * n), kE4M3FN, scales_out + 1, st),
+  RPX_HIP(launch_fp8_amax(right, right_dtype, k * n, pr, npr, kE4M3FN, nullptr, st),
           "fp8_linear_forward: amax(right)");
-  RPX_HIP(launch_fp8_cast(left, left_dtype, m, k, k, 1, scales_out, kE4M3FN, ql, nullptr, st),
+  // left [M, K] -> codes [M, K] (+ [K, M] for the weight gradient)
+  RPX_HIP(launch_fp8_cast(left, left_dtype, m, k, k, 1, nullptr, pl, npl, scales_out, kE4M3FN, ql,
+                          left_t_codes, st),
           "fp8_linear_forward: cast(left)");
-  RPX_HIP(launch_fp8_cast(right, right_dtype, k, n, right_row_stride, right_col_stride,
-                          scales_out + 1, kE4M3FN, nullptr, qr, st),
+  // right [K, N] -> codes [N, K] for this product (+ [K, N] for the input gradient)
+  RPX_HIP(launch_fp8_cast(right, right_dtype, k, n, right_row_stride, right_col_stride, nullptr, pr,
+                          npr, scales_out + 1, kE4M3FN, right_codes, qr, st),
           "fp8_linear_forward: cast(right)");
   return rpx_fp8_gemm(ql, kE4M3FN, scales_out, qr, kE4M3FN, scales_out + 1, m, n, k, out,
                       out_dtype, gw, gws, stream);
@@ -654,6 +659,56 @@ size_t rpx_fp8_linear_backward_workspace(int64_t m, int64_t n, int64_t k) {
   return s.used;
 }
 
+int rpx_fp8_linear_backward_codes(const uint8_t* left_t_codes, const uint8_t* right_codes,
+                                  const float* scales, int64_t m, int64_t k, int64_t n,
+                                  const void* grad, int grad_dtype, void* d_left, void* d_right,
+                                  int d_right_transposed, int out_dtype, void* workspace,
+                                  size_t workspace_bytes, void* stream) {
+  RPX_TRY(check_dtype(grad_dtype));
+  RPX_TRY(check_dtype(out_dtype));
+  if (m <= 0 || n <= 0 || k <= 0)
+    return fail_invalid("rpx_fp8_linear_backward: m, n, k must be positive");
+  if (grad == nullptr || scales == nullptr || (d_left != nullptr && right_codes == nullptr) ||
+      (d_right != nullptr && left_t_codes == nullptr))
+    return fail_invalid("rpx_fp8_linear_backward: null pointer");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  Arena ar(workspace, workspace_bytes);
+  const int64_t npg = fp8_amax_partials(m * n);
+  uint32_t* pg = ar.take<uint32_t>(npg);
+  float* sg = ar.take<float>(1);
+  uint8_t* qg = ar.take<uint8_t>(m * n);
+  uint8_t* qgt = ar.take<uint8_t>(n * m);
+  ar.take<uint8_t>(k * n);
+  ar.take<uint8_t>(k * m);
+  size_t g1 = rpx_fp8_gemm_workspace(m, k, n);
+  size_t g2 = rpx_fp8_gemm_workspace(k, n, m);
+  const size_t g3 = rpx_fp8_gemm_workspace(n, k, m);
+  if (g2 < g3) g2 = g3;
+  const size_t gws = g1 > g2 ? g1 : g2;
+  uint8_t* gw = ar.take<uint8_t>(static_cast<int64_t>(gws));
+  if (ar.overflow) return fail_invalid("rpx_fp8_linear_backward: workspace too small");
+  // s_g (e5m2) and the gradient codes in the layouts the two products need
+  RPX_HIP(launch_fp8_amax(grad, grad_dtype, m * n, pg, npg, kE5M2, nullptr, st),
+          "fp8_linear_backward: amax(grad)");
+  RPX_HIP(launch_fp8_cast(grad, grad_dtype, m, n, n, 1, nullptr, pg, npg, sg, kE5M2,
+                          d_left ? qg : nullptr, d_right ? qgt : nullptr, st),
+          "fp8_linear_backward: cast(grad)");
+  // d_left [M, K] = ((g . right^T) * s_g) * s_r
+  if (d_left != nullptr)
+    RPX_TRY(rpx_fp8_gemm(qg, kE5M2, sg, right_codes, kE4M3FN, scales + 1, m, k, n, d_left,
+                         out_dtype, gw, gws, stream));
+  if (d_right == nullptr) return kOk;
+  // d_right = ((left^T . g) * s_l) * s_g, as [K, N] or transposed [N, K]
+  if (d_right_transposed) {
+    RPX_TRY(rpx_fp8_gemm(qgt, kE5M2, scales, left_t_codes, kE4M3FN, sg, n, k, m, d_right,
+                         out_dtype, gw, gws, stream));
+  } else {
+    RPX_TRY(rpx_fp8_gemm(left_t_codes, kE4M3FN, scales, qgt, kE5M2, sg, k, n, m, d_right,
+                         out_dtype, gw, gws, stream));
+  }
+  return kOk;
+}
+
 int rpx_fp8_linear_backward(const void* left, int left_dtype, const void* right, int right_dtype,
                             int64_t m, int64_t k, int64_t n, int64_t right_row_stride,
                             int64_t right_col_stride, const void* grad, int grad_dtype,
@@ -662,55 +717,44 @@ int rpx_fp8_linear_backward(const void* left, int left_dtype, const void* right,
                             size_t workspace_bytes, void* stream) {
   RPX_TRY(check_dtype(left_dtype));
   RPX_TRY(check_dtype(right_dtype));
-  RPX_TRY(check_dtype(grad_dtype));
-  RPX_TRY(check_dtype(out_dtype));
-  if (m < 0 || n < 0 || k < 0) return fail_invalid("m, n, k must be non-negative");
   if (left == nullptr || right == nullptr || grad == nullptr || scales == nullptr)
     return fail_invalid("rpx_fp8_linear_backward: null pointer");
-  if (m == 0 || n == 0 || k == 0)
-    return fail_invalid("rpx_fp8_linear_backward: empty operands are handled by the caller");
+  if (m <= 0 || n <= 0 || k <= 0)
+    return fail_invalid("rpx_fp8_linear_backward: m, n, k must be positive");
   hipStream_t st = static_cast<hipStream_t>(stream);
+  // re-quantize the operands with the forward scales (same values, same
+  // amax), into the tail of the workspace that the code path reserves
   Arena ar(workspace, workspace_bytes);
-  uint32_t* pg = ar.take<uint32_t>(fp8_amax_partials(m * n));
-  float* sg = ar.take<float>(1);
-  uint8_t* qg = ar.take<uint8_t>(m * n);
-  uint8_t* qgt = ar.take<uint8_t>(n * m);
+  ar.take<uint32_t>(fp8_amax_partials(m * n));
+  ar.take<float>(1);
+  ar.take<uint8_t>(m * n);
+  ar.take<uint8_t>(n * m);
   uint8_t* qr = ar.take<uint8_t>(k * n);
   uint8_t* qlt = ar.take<uint8_t>(k * m);
-  size_t g1 = rpx_fp8_gemm_workspace(m, k, n);
-  size_t g2 = rpx_fp8_gemm_workspace(k, n, m);
-  const size_t g3 = rpx_fp8_gemm_workspace(n, k, m);
-  if (g2 < g3) g2 = g3;
-  const size_t gws = g1 > g2 ? g1 : g2;
-  uint8_t* gw = ar.take<uint8_t>(static_cast<int64_t>(gws));
   if (ar.overflow) return fail_invalid("rpx_fp8_linear_backward: workspace too small");
-  // s_g (e5m2) and both layouts of the gradient codes
-  RPX_HIP(launch_fp8_amax(grad, grad_dtype, m, n, n, 1, pg, fp8_amax_partials(m * n), kE5M2, sg,
-                          st),
-          "fp8_linear_backward: amax(grad)");
-  RPX_HIP(launch_fp8_cast(grad, grad_dtype, m, n, n, 1, sg, kE5M2, d_left ? qg : nullptr,
-                          d_right ? qgt : nullptr, st),
-          "fp8_linear_backward: cast(grad)");
-  // operands re-quantized with the forward scales (same values, same amax)
-  if (d_left != nullptr) {
+  if (d_left != nullptr)
     RPX_HIP(launch_fp8_cast(right, right_dtype, k, n, right_row_stride, right_col_stride,
-                            scales + 1, kE4M3FN, qr, nullptr, st),
+                            scales + 1, nullptr, 0, nullptr, kE4M3FN, qr, nullptr, st),
             "fp8_linear_backward: cast(right)");
-    // d_left [M, K] = ((g . right^T) * s_g) * s_r
-    RPX_TRY(rpx_fp8_gemm(qg, kE5M2, sg, qr, kE4M3FN, scales + 1, m, k, n, d_left, out_dtype, gw,
-                         gws, stream));
-  }
-  if (d_right == nullptr) return kOk;
-  RPX_HIP(launch_fp8_cast(left, left_dtype, m, k, k, 1, scales, kE4M3FN, nullptr, qlt, st),
-          "fp8_linear_backward: cast(left)");
-  // d_right = ((left^T . g) * s_l) * s_g, as [K, N] or transposed [N, K]
-  if (d_right_transposed) {
-    RPX_TRY(rpx_fp8_gemm(qgt, kE5M2, scales, qlt, kE4M3FN, sg, n, k, m, d_right, out_dtype, gw, gws,
-                         stream));
-  } else {
-    RPX_TRY(rpx_fp8_gemm(qlt, kE4M3FN, scales, qgt, kE5M2, sg, k, n, m, d_right, out_dtype, gw, gws,
-                         stream));
-  }
+  if (d_right != nullptr)
+    RPX_HIP(launch_fp8_cast(left, left_dtype, m, k, k, 1, scales, nullptr, 0, nullptr, kE4M3FN,
+                            nullptr, qlt, st),
+            "fp8_linear_backward: cast(left)");
+  return rpx_fp8_linear_backward_codes(qlt, qr, scales, m, k, n, grad, grad_dtype, d_left, d_right,
+                                       d_right_transposed, out_dtype, workspace, workspace_bytes,
+                                       stream);
+}
+
+int rpx_fp8_encode_selfcheck(int fmt, uint64_t first, uint64_t count, uint32_t* block_counts,
+                             uint32_t* block_first, int64_t blocks, void* stream) {
+  RPX_TRY(check_fmt(fmt));
+  if (blocks < 1 || block_counts == nullptr || block_first == nullptr)
+    return fail_invalid("rpx_fp8_encode_selfcheck: bad output slots");
+  if (count == 0 || first + count - 1 > 0xFFFFFFFFull)
+    return fail_invalid("rpx_fp8_encode_selfcheck: range must lie within 32-bit patterns");
+  RPX_HIP(launch_fp8_encode_selfcheck(fmt, first, count, block_counts, block_first, blocks,
+                                      static_cast<hipStream_t>(stream)),
+          "rpx_fp8_encode_selfcheck");
   return kOk;
 }
 

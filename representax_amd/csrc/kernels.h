@@ -87,16 +87,21 @@ hipError_t launch_round_store(const float* in, int64_t n, int dtype, void* out,
 
 // FP8 ------------------------------------------------------------------------
 int64_t fp8_amax_partials(int64_t numel);
-hipError_t launch_fp8_amax(const void* t, int dtype, int64_t rows, int64_t cols, int64_t s_row,
-                           int64_t s_col, uint32_t* partials, int64_t n_partials, int fmt,
-                           float* scale_out, hipStream_t stream);
+// Per-block max |t| partials; with scale_out, also the finalized scale.
+hipError_t launch_fp8_amax(const void* t, int dtype, int64_t numel, uint32_t* partials,
+                           int64_t n_partials, int fmt, float* scale_out, hipStream_t stream);
+// codes = f8(t / s) where s is scale[0], or, when partials is given, the
+// scale finalized from those amax partials (also written to scale_out).
 hipError_t launch_fp8_cast(const void* t, int dtype, int64_t rows, int64_t cols, int64_t s_row,
-                           int64_t s_col, const float* scale, int fmt, uint8_t* out,
+                           int64_t s_col, const float* scale, const uint32_t* partials,
+                           int64_t n_partials, float* scale_out, int fmt, uint8_t* out,
                            uint8_t* out_t, hipStream_t stream);
 hipError_t launch_fp8_gemm(const uint8_t* a, int fmt_a, const float* s_a, const uint8_t* b,
                            int fmt_b, const float* s_b, int64_t m, int64_t n, int64_t k,
                            void* out, int out_dtype, int64_t ldc, float* split_ws,
                            int64_t split_ws_floats, hipStream_t stream);
 int64_t fp8_gemm_workspace_floats(int64_t m, int64_t n, int64_t k);
+hipError_t launch_fp8_encode_selfcheck(int fmt, uint64_t first, uint64_t count, uint32_t* counts,
+                                       uint32_t* firsts, int64_t blocks, hipStream_t stream);
 
 }  // namespace rpx

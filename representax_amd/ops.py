@@ -242,6 +242,23 @@ def fp8_cast(t: torch.Tensor, scale: torch.Tensor, fmt: str = "e4m3fn", *, rowma
     return out, out_t
 
 
+def fp8_encode_selfcheck(fmt: str, first: int = 0, count: int = 1 << 31, blocks: int = 4096,
+                         device="cuda"):
+    """Mismatches between the cast kernels' encoder and the integer encoder
+    over f32 patterns [first, first+count) and their negations:
+    ``(count, lowest mismatching pattern or None)``."""
+
+    dev = torch.device(device)
+    nat.load()
+    counts = torch.zeros(blocks, dtype=torch.int32, device=dev)
+    firsts = torch.zeros(blocks, dtype=torch.int32, device=dev)
+    nat.call("rpx_fp8_encode_selfcheck", _fmt(fmt), int(first), int(count), _ptr(counts),
+             _ptr(firsts), blocks, _stream(dev))
+    c = counts.cpu().numpy().view("uint32").astype("int64").sum()
+    f = firsts.cpu().numpy().view("uint32").min()
+    return int(c), (None if f == 0xFFFFFFFF else int(f))
+
+
 def fp8_gemm(a_codes, fmt_a, scale_a, b_codes, fmt_b, scale_b, out_dtype=BF16):
     """``((a [M,K] . b [N,K]^T) * s_a) * s_b`` -> ``[M, N]``."""
 
@@ -264,8 +281,13 @@ def _dense_2d(t: torch.Tensor) -> torch.Tensor:
     return t.contiguous()
 
 
-def fp8_linear_forward(left, right, out_dtype=BF16):
-    """``(out [M, N], scales f32[2])`` for ``left [M,K] . right [K,N]``."""
+def fp8_linear_forward(left, right, out_dtype=BF16, save_codes=False):
+    """``(out [M, N], scales f32[2], codes)`` for ``left [M,K] . right [K,N]``.
+
+    With ``save_codes`` the same cast pass also returns the backward's operand
+    codes ``(left^T codes [K, M], right codes [K, N])``; otherwise ``codes``
+    is None.
+    """
 
     device = _on_device(left, right)
     left = left.contiguous()
@@ -274,19 +296,33 @@ def fp8_linear_forward(left, right, out_dtype=BF16):
     n = right.shape[1]
     out = torch.empty((m, n), dtype=out_dtype, device=device)
     scales = torch.empty(2, dtype=F32, device=device)
+    codes = None
+    if save_codes:
+        codes = (torch.empty((k, m), dtype=torch.uint8, device=device),
+                 torch.empty((k, n), dtype=torch.uint8, device=device))
     if m == 0 or n == 0:
-        return out, scales
+        return out, scales, codes
     if k == 0:
         raise ValueError("fp8 linear needs a non-empty contraction")
     ws = _workspace(nat.query("rpx_fp8_linear_forward_workspace", m, n, k), device)
     nat.call("rpx_fp8_linear_forward", _ptr(left), _dtype_code(left.dtype), m, k, _ptr(right),
              _dtype_code(right.dtype), n, right.stride(0), right.stride(1), _ptr(out),
-             _dtype_code(out_dtype), _ptr(scales), _ptr(ws), ws.numel(), _stream(device))
-    return out, scales
+             _dtype_code(out_dtype), _ptr(scales), _ptr(codes[0] if codes else None),
+             _ptr(codes[1] if codes else None), _ptr(ws), ws.numel(), _stream(device))
+    return out, scales, codes
+
+
+def _grad_buffers(m, k, n, dtype, right_t, need_left, need_right, device):
+    d_left = torch.empty((m, k), dtype=dtype, device=device) if need_left else None
+    d_right = None
+    if need_right:
+        d_right = torch.empty((n, k) if right_t else (k, n), dtype=dtype, device=device)
+    return d_left, d_right
 
 
 def fp8_linear_backward(left, right, grad, scales, *, need_left=True, need_right=True):
-    """``(d_left [M,K] or None, d_right [K,N] or None)`` in the operand dtypes."""
+    """``(d_left [M,K] or None, d_right [K,N] or None)`` in the operand dtypes,
+    re-quantizing the bf16 operands with the forward's scales."""
 
     device = _on_device(left, right, grad, scales)
     left = left.contiguous()
@@ -296,16 +332,12 @@ def fp8_linear_backward(left, right, grad, scales, *, need_left=True, need_right
     n = right.shape[1]
     if left.dtype != right.dtype:
         raise TypeError("fp8 linear backward expects operands of one dtype")
-    d_left = torch.empty((m, k), dtype=left.dtype, device=device) if need_left else None
     right_t = not right.is_contiguous()  # a transposed weight view gets a [N, K] gradient
-    d_right = None
-    if need_right:
-        d_right = torch.empty((n, k) if right_t else (k, n), dtype=right.dtype, device=device)
+    d_left, d_right = _grad_buffers(m, k, n, left.dtype, right_t, need_left, need_right, device)
     if m == 0 or n == 0 or k == 0:
-        if d_left is not None:
-            d_left.zero_()
-        if d_right is not None:
-            d_right.zero_()
+        for t in (d_left, d_right):
+            if t is not None:
+                t.zero_()
     elif need_left or need_right:
         ws = _workspace(nat.query("rpx_fp8_linear_backward_workspace", m, n, k), device)
         nat.call("rpx_fp8_linear_backward", _ptr(left), _dtype_code(left.dtype), _ptr(right),
@@ -318,24 +350,57 @@ def fp8_linear_backward(left, right, grad, scales, *, need_left=True, need_right
     return d_left, d_right
 
 
+def fp8_linear_backward_codes(codes, scales, grad, *, k, dtype, right_transposed,
+                              need_left=True, need_right=True):
+    """Backward from the codes saved by ``fp8_linear_forward(save_codes=True)``."""
+
+    left_t, right_c = codes
+    device = _on_device(left_t, right_c, grad, scales)
+    grad = grad.contiguous()
+    m, n = grad.shape
+    d_left, d_right = _grad_buffers(m, k, n, dtype, right_transposed, need_left, need_right,
+                                    device)
+    if m == 0 or n == 0 or k == 0:
+        for t in (d_left, d_right):
+            if t is not None:
+                t.zero_()
+    elif need_left or need_right:
+        ws = _workspace(nat.query("rpx_fp8_linear_backward_workspace", m, n, k), device)
+        nat.call("rpx_fp8_linear_backward_codes", _ptr(left_t), _ptr(right_c), _ptr(scales), m, k,
+                 n, _ptr(grad), _dtype_code(grad.dtype), _ptr(d_left), _ptr(d_right),
+                 1 if right_transposed else 0, _dtype_code(dtype), _ptr(ws), ws.numel(),
+                 _stream(device))
+    if d_right is not None and right_transposed:
+        d_right = d_right.t()
+    return d_left, d_right
+
+
 class Fp8LinearFn(torch.autograd.Function):
     """``_fp8_linear_dot`` (precision.py:173-221): e4m3 forward, e5m2 backward.
 
     The output is produced directly in ``out_dtype`` (the reference computes
     float32 and the caller casts it to the activation dtype; rounding once
-    from the float32 epilogue value is the same result).
+    from the float32 epilogue value is the same result). The residuals are the
+    operands' e4m3 codes and scales, which are exactly what the reference's
+    backward recomputes from its bf16 residuals.
     """
 
     @staticmethod
     def forward(ctx, left, right, out_dtype):
-        out, scales = fp8_linear_forward(left, right, out_dtype)
-        ctx.save_for_backward(left, right, scales)
+        need = left.requires_grad or right.requires_grad
+        out, scales, codes = fp8_linear_forward(left, right, out_dtype, save_codes=need)
+        if need:
+            ctx.save_for_backward(scales, *codes)
+            ctx.k = left.shape[1]
+            ctx.dtype = left.dtype
+            ctx.right_t = not _dense_2d(right).is_contiguous()
         return out
 
     @staticmethod
     def backward(ctx, grad):
-        left, right, scales = ctx.saved_tensors
-        d_left, d_right = fp8_linear_backward(
-            left, right, grad, scales, need_left=ctx.needs_input_grad[0],
+        scales, left_t, right_c = ctx.saved_tensors
+        d_left, d_right = fp8_linear_backward_codes(
+            (left_t, right_c), scales, grad, k=ctx.k, dtype=ctx.dtype,
+            right_transposed=ctx.right_t, need_left=ctx.needs_input_grad[0],
             need_right=ctx.needs_input_grad[1])
         return d_left, d_right, None

@@ -21,6 +21,16 @@ def _all_bf16_values() -> np.ndarray:
 
 
 @pytest.mark.parametrize("fmt", ["e4m3fn", "e5m2"])
+def test_hardware_convert_matches_integer_encoder_everywhere(fmt):
+    """The cast kernels convert with the gfx950 packed fp8/bf8 instruction in
+    range; it must agree with the integer encoder (pinned to the oracle on the
+    host) on every one of the 2^32 f32 bit patterns."""
+
+    bad, first = ops.fp8_encode_selfcheck(fmt, 0, 1 << 31)
+    assert bad == 0, f"{bad} mismatches, first pattern {first:#010x}" if first is not None else bad
+
+
+@pytest.mark.parametrize("fmt", ["e4m3fn", "e5m2"])
 def test_cast_every_bf16_value_bit_exact(fmt):
     """All 65536 bf16 patterns x a sweep of scales: codes must match exactly."""
 
@@ -118,9 +128,13 @@ def test_fp8_linear_forward_backward(m, k, n):
     dl_o, dr_o = ofp8.fp8_linear_backward(x, right, gy)
     xd = to_dev_bf16(x)
     wd = to_dev_bf16(w)
-    y, scales = ops.fp8_linear_forward(xd, wd.t())
+    y, scales, codes = ops.fp8_linear_forward(xd, wd.t(), save_codes=True)
     dl, dr = ops.fp8_linear_backward(xd, wd.t(), to_dev_bf16(gy), scales)
+    dl_c, dr_c = ops.fp8_linear_backward_codes(codes, scales, to_dev_bf16(gy), k=k,
+                                               dtype=torch.bfloat16, right_transposed=True)
     torch.cuda.synchronize()
+    # the saved-codes backward is the same computation as re-quantizing
+    assert torch.equal(dl, dl_c) and torch.equal(dr, dr_c)
     s = from_dev(scales)
     assert s[0] == ofp8.scale_from_amax(ofp8.amax(x), E4M3FN)
     assert s[1] == ofp8.scale_from_amax(ofp8.amax(w), E4M3FN)
@@ -137,8 +151,41 @@ def test_fp8_linear_bert_ffn_full_size():
     y_o = bf16_values(ofp8.fp8_linear_forward(x, right, acc=np.float32))
     dl_o, dr_o = ofp8.fp8_linear_backward(x, right, gy, acc=np.float32)
     xd, wd = to_dev_bf16(x), to_dev_bf16(w)
-    y, scales = ops.fp8_linear_forward(xd, wd.t())
-    dl, dr = ops.fp8_linear_backward(xd, wd.t(), to_dev_bf16(gy), scales)
+    y, scales, codes = ops.fp8_linear_forward(xd, wd.t(), save_codes=True)
+    dl, dr = ops.fp8_linear_backward_codes(codes, scales, to_dev_bf16(gy), k=k,
+                                           dtype=torch.bfloat16, right_transposed=True)
     torch.cuda.synchronize()
     errs = [rel_l2(from_dev(y), y_o), rel_l2(from_dev(dl), dl_o), rel_l2(from_dev(dr), dr_o)]
     assert max(errs) < FP8_TOL, errs
+
+
+def test_fp8_linear_natural_right_layout():
+    """right given as a row-major [K, N] matrix (not a transposed view)."""
+
+    m, k, n = 256, 384, 512
+    x, w, gy = _fp8_case(m, k, n, seed=9)
+    right = np.ascontiguousarray(w.T)
+    y_o = bf16_values(ofp8.fp8_linear_forward(x, right))
+    dl_o, dr_o = ofp8.fp8_linear_backward(x, right, gy)
+    rd = to_dev_bf16(right)
+    y, scales, codes = ops.fp8_linear_forward(to_dev_bf16(x), rd, save_codes=True)
+    dl, dr = ops.fp8_linear_backward_codes(codes, scales, to_dev_bf16(gy), k=k,
+                                           dtype=torch.bfloat16, right_transposed=False)
+    torch.cuda.synchronize()
+    assert dr.shape == (k, n) and dr.is_contiguous()
+    for got, want in ((y, y_o), (dl, dl_o), (dr, dr_o)):
+        assert rel_l2(from_dev(got), want) < FP8_TOL
+
+
+def test_fp8_autograd_function_gradients():
+    """Fp8LinearFn through torch autograd equals the explicit backward."""
+
+    m, k, n = 512, 256, 384
+    x, w, gy = _fp8_case(m, k, n, seed=10)
+    xd = to_dev_bf16(x).requires_grad_(True)
+    wd = to_dev_bf16(w).requires_grad_(True)
+    y = ops.Fp8LinearFn.apply(xd, wd.t(), torch.bfloat16)
+    y.backward(to_dev_bf16(gy))
+    dl_o, dr_o = ofp8.fp8_linear_backward(x, w.T, gy)
+    assert rel_l2(from_dev(xd.grad), dl_o) < FP8_TOL
+    assert rel_l2(from_dev(wd.grad), dr_o.T) < FP8_TOL

@@ -50,8 +50,9 @@ def test_fp8_linear_graph_replays_match_eager():
     gy = to_dev_bf16(g.standard_normal((1024, 3072)))
 
     def fn():
-        y, s = ops.fp8_linear_forward(x, w.t())
-        dl, dr = ops.fp8_linear_backward(x, w.t(), gy, s)
+        y, s, codes = ops.fp8_linear_forward(x, w.t(), save_codes=True)
+        dl, dr = ops.fp8_linear_backward_codes(codes, s, gy, k=768, dtype=torch.bfloat16,
+                                               right_transposed=True)
         return [y, s, dl, dr]
 
     eager = [t.clone() for t in fn()]
