@@ -26,11 +26,13 @@ FLT_MIN = np.float32(np.finfo(np.float32).tiny)
 
 
 def f32_bits(x) -> np.ndarray:
-    return np.ascontiguousarray(np.asarray(x, dtype=np.float32)).view(np.uint32)
+    """float32 bit patterns (same shape, including 0-d)."""
+
+    return np.array(x, dtype=np.float32, copy=True).view(np.uint32)
 
 
 def bits_f32(u) -> np.ndarray:
-    return np.ascontiguousarray(np.asarray(u, dtype=np.uint32)).view(np.float32)
+    return np.array(u, dtype=np.uint32, copy=True).view(np.float32)
 
 
 def f32_to_bf16_bits(x) -> np.ndarray:

@@ -29,11 +29,21 @@ from .int4 import dequant_int4
 
 
 def _rounder(compute: str):
+    """Rounding applied after every op in the given compute dtype; "f64" keeps
+    float64 throughout (used to check the transpose rules against finite
+    differences)."""
+
     if compute == "bf16":
         return bf16_round
     if compute == "f32":
         return lambda v: np.asarray(v, dtype=np.float32)
+    if compute == "f64":
+        return lambda v: np.asarray(v, dtype=np.float64)
     raise ValueError(compute)
+
+
+def _master(v, compute: str):
+    return np.asarray(v, dtype=np.float64 if compute == "f64" else np.float32)
 
 
 def _dot(a, b, acc):
@@ -43,6 +53,8 @@ def _dot(a, b, acc):
 def lora_scaling(alpha: float, rank: int, compute: str = "bf16") -> np.float32:
     """``alpha / rank`` as the weakly typed scalar the reference multiplies by."""
 
+    if compute == "f64":
+        return np.float64(alpha / rank)
     return _rounder(compute)(np.float32(alpha / rank))
 
 
@@ -112,9 +124,9 @@ def lora_backward(
     c = lora_scaling(alpha, rank, compute)
     g_a = rnd(g * c)
     dh = rnd(_dot(g_a, b_c, acc))
-    d_b = rnd(_dot(g_a.T, h, acc)).astype(np.float32)
+    d_b = _master(rnd(_dot(g_a.T, h, acc)), compute)
     dx = rnd(rnd(_dot(g, w, acc)) + rnd(_dot(dh, a_c, acc)))
-    d_a = rnd(_dot(dh.T, x, acc)).astype(np.float32)
+    d_a = _master(rnd(_dot(dh.T, x, acc)), compute)
     return dx, d_a, d_b
 
 

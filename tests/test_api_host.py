@@ -1,0 +1,133 @@
+"""Host logic of the reference-API mirror (CPU only, nothing launched)."""
+
+from __future__ import annotations
+
+import pydantic
+import pytest
+import torch
+
+import representax_amd as rx
+from representax_amd.adapters import _path_name
+
+
+class _Block(torch.nn.Module):
+    def __init__(self):
+        super().__init__()
+        self.query = rx.Linear.init(8, 8, key=1, scale=0.1)
+        self.value = rx.Linear.init(8, 8, key=2, scale=0.1)
+        self.norm = torch.nn.LayerNorm(8)
+
+
+class _Model(torch.nn.Module):
+    def __init__(self):
+        super().__init__()
+        self.layers = torch.nn.ModuleList([_Block(), _Block()])
+        self.head = rx.Linear.init(8, 6, key=3, scale=0.1, bias=True)
+
+
+def test_path_names_follow_keystr_style():
+    assert _path_name("layers.0.query") == ".layers[0].query"
+    assert _path_name("head") == ".head"
+
+
+def test_target_pattern_selects_linear_leaves():
+    model = _Model()
+    assert rx.matched_linear_paths(model) == [
+        "layers.0.query", "layers.0.value", "layers.1.query", "layers.1.value", "head"]
+    assert rx.matched_linear_paths(model, r"layers\[1\]\.query") == ["layers.1.query"]
+    assert rx.matched_linear_paths(model, r"head$") == ["head"]
+
+
+def test_apply_rejects_bad_arguments_before_packing():
+    model = _Model()
+    with pytest.raises(ValueError, match="matched no native Linear"):
+        rx.apply_quantized_lora(model, rank=2, alpha=4.0, key=0, target_pattern="nothing")
+    with pytest.raises(ValueError, match="rank"):
+        rx.apply_quantized_lora(model, rank=0, alpha=4.0, key=0)
+    with pytest.raises(ValueError, match="alpha"):
+        rx.apply_quantized_lora(model, rank=2, alpha=0.0, key=0)
+
+
+def _adapter_on_cpu():
+    return rx.QuantizedLoRALinear(
+        packed_weight=torch.zeros((6, 4), dtype=torch.uint8),
+        scale_bits=torch.full((6,), 0x3F80, dtype=torch.uint16),
+        bias_bits=torch.zeros(6, dtype=torch.uint16),
+        lora_a=torch.zeros((2, 8)), lora_b=torch.zeros((6, 2)),
+        input_size=8, output_size=6, rank=2, alpha=4.0)
+
+
+def test_lora_filter_selects_exactly_the_adapter_arrays():
+    """Same selection as tests/models/test_adapters.py:97-117."""
+
+    model = torch.nn.Module()
+    model.projection = _adapter_on_cpu()
+    model.other = torch.nn.Linear(3, 3)
+    chosen = rx.lora_parameter_filter(model)
+    assert chosen == {"projection.lora_a": True, "projection.lora_b": True,
+                      "other.weight": False, "other.bias": False}
+    assert {tuple(p.shape) for p in rx.lora_parameters(model)} == {(2, 8), (6, 2)}
+    # frozen integer leaves are buffers, never parameters
+    names = {n for n, _ in model.named_buffers()}
+    assert {"projection.packed_weight", "projection.scale_bits", "projection.bias_bits"} <= names
+
+
+def test_forward_on_cpu_fails_loudly():
+    with pytest.raises(RuntimeError, match="ROCm"):
+        _adapter_on_cpu()(torch.zeros((3, 8)))
+
+
+def test_quantized_config_validation():
+    cfg = rx.QuantizedLoRAConfig(rank=8, alpha=16.0, target_pattern=r"layers.*(attention|mlp)")
+    assert cfg.bits == 4 and cfg.group_size is None
+    for bad in (dict(rank=0, alpha=1.0), dict(rank=2, alpha=0.0), dict(rank=2, alpha=1.0, bits=8),
+                dict(rank=2, alpha=1.0, target_pattern="("), dict(rank=2, alpha=1.0, target_pattern="")):
+        with pytest.raises(pydantic.ValidationError):
+            rx.QuantizedLoRAConfig(**bad)
+    assert rx.QuantizedLoRAConfig.model_validate(cfg.model_dump()) == cfg
+
+
+def test_precision_config_and_policy():
+    cfg = rx.PrecisionConfig.float8_mixed()
+    assert (cfg.compute_dtype, cfg.activation_dtype, cfg.resolved_matrix_dtype) == (
+        "bfloat16", "bfloat16", "float8_e4m3fn")
+    policy = rx.resolve_precision_policy(cfg)
+    assert policy.matrix_dtype == torch.float8_e4m3fn
+    assert policy.compute_dtype == torch.bfloat16 and policy.parameter_dtype == torch.float32
+    bf = rx.resolve_precision_policy(rx.PrecisionConfig.bfloat16_mixed())
+    assert bf.matrix_dtype == torch.bfloat16
+    with pytest.raises(pydantic.ValidationError):
+        rx.PrecisionConfig(compute_dtype="float16")
+
+
+def test_precision_context_nests_and_restores():
+    from representax_amd.precision import active_policy
+
+    bf = rx.resolve_precision_policy(rx.PrecisionConfig.bfloat16_mixed())
+    assert active_policy() is None
+    with rx.precision_context(bf):
+        assert active_policy() is bf
+        assert rx.compute_parameter(torch.zeros(2)).dtype == torch.bfloat16
+        assert rx.activation_inputs({"x": torch.zeros(2), "ids": torch.zeros(2, dtype=torch.int64)})[
+            "ids"].dtype == torch.int64
+        with rx.precision_context(rx.FP32_POLICY):
+            assert active_policy() is rx.FP32_POLICY
+        assert active_policy() is bf
+    assert active_policy() is None
+
+
+def test_linear_matmul_without_fp8_policy_is_a_plain_product():
+    a = torch.randn(3, 4, 5)
+    b = torch.randn(5, 2)
+    torch.testing.assert_close(rx.linear_matmul(a, b), a @ b)
+    bf = rx.resolve_precision_policy(rx.PrecisionConfig.bfloat16_mixed())
+    with rx.precision_context(bf):
+        torch.testing.assert_close(rx.linear_matmul(a, b), a @ b)
+
+
+def test_fp8_policy_on_cpu_fails_loudly():
+    policy = rx.resolve_precision_policy(rx.PrecisionConfig.float8_mixed())
+    with rx.precision_context(policy):
+        with pytest.raises(RuntimeError, match="ROCm"):
+            rx.linear_matmul(torch.randn(4, 8, dtype=torch.bfloat16),
+                             torch.randn(8, 2, dtype=torch.bfloat16))

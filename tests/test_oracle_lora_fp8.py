@@ -1,0 +1,181 @@
+"""Pin the oracle's INT4-LoRA and FP8 linears against closed forms, brute
+force and finite differences (CPU)."""
+
+from __future__ import annotations
+
+import numpy as np
+
+from oracle import fp8 as ofp8
+from oracle import int4 as oint4
+from oracle import lora as olora
+from oracle.codecs import E4M3FN, E5M2, FLT_MIN, bf16_bits_to_f32, bf16_round, f32_to_bf16_bits
+
+
+def _case(m=5, k=8, n=6, r=2, seed=0):
+    g = np.random.Generator(np.random.PCG64(seed))
+    x = bf16_round(g.standard_normal((m, k)))
+    w = (g.standard_normal((n, k)) * 0.3).astype(np.float32)
+    a = (g.standard_normal((r, k)) * 0.3).astype(np.float32)
+    b = (g.standard_normal((n, r)) * 0.3).astype(np.float32)
+    packed, scales = oint4.pack_int4(w)
+    bias = f32_to_bf16_bits(g.standard_normal(n).astype(np.float32))
+    return x, packed, scales, a, b, bias
+
+
+def test_forward_brute_force_loops():
+    """Element-by-element loops with the documented rounding points."""
+
+    x, packed, scales, a, b, bias = _case()
+    alpha, r = 3.0, 2
+    y, h = olora.lora_forward(x, packed, scales, a, b, alpha=alpha, rank=r, bias_bits=bias)
+    w = oint4.dequant_int4(packed, scales, x.shape[1])
+    ab, bb = bf16_round(a), bf16_round(b)
+    c = float(bf16_round(np.float32(alpha / r)))
+    m, k = x.shape
+    n = w.shape[0]
+    for i in range(m):
+        hh = [float(bf16_round(np.float32(sum(float(x[i, t]) * float(ab[j, t]) for t in range(k)))))
+              for j in range(r)]
+        assert np.allclose(hh, h[i])
+        for o in range(n):
+            base = bf16_round(np.float32(sum(float(x[i, t]) * float(w[o, t]) for t in range(k))))
+            ad = bf16_round(np.float32(sum(hh[j] * float(bb[o, j]) for j in range(r))))
+            yy = bf16_round(np.float32(base + bf16_round(np.float32(ad * c))))
+            yy = bf16_round(np.float32(yy + bf16_bits_to_f32(bias[o])))
+            assert yy == y[i, o]
+
+
+def test_zero_adapter_equals_base_projection():
+    """lora_b = 0 (the reference's init) leaves exactly the base projection."""
+
+    x, packed, scales, a, _, bias = _case(seed=1)
+    y, _ = olora.lora_forward(x, packed, scales, a, np.zeros((6, 2), np.float32), alpha=4.0,
+                              rank=2, bias_bits=bias)
+    w = oint4.dequant_int4(packed, scales, 8)
+    base = bf16_round(bf16_round(x.astype(np.float64) @ w.T.astype(np.float64)) +
+                      bf16_bits_to_f32(bias))
+    assert np.array_equal(y, base)
+
+
+def test_forward_close_to_merged_weight():
+    """Adapted output ~ x W_merged^T + bias (tests/models/test_adapters.py:77-94)."""
+
+    x, packed, scales, a, b, bias = _case(m=16, k=32, n=24, r=4, seed=2)
+    y, _ = olora.lora_forward(x, packed, scales, a, b, alpha=8.0, rank=4, bias_bits=bias,
+                              compute="f32")
+    merged = olora.merged_weight(packed, scales, a, b, alpha=8.0, rank=4, input_size=32)
+    np.testing.assert_allclose(y, x @ merged.T + bf16_bits_to_f32(bias), rtol=2e-3, atol=2e-3)
+
+
+def test_backward_matches_finite_differences():
+    """The transpose rules (float64 mode) against central differences of
+    L = sum(g * y) in x, A and B."""
+
+    m, k, n, r = 4, 8, 6, 3
+    x, packed, scales, a, b, _ = _case(m, k, n, r, seed=3)
+    x = x.astype(np.float64)
+    a = a.astype(np.float64)
+    b = b.astype(np.float64)
+    gy = np.random.Generator(np.random.PCG64(9)).standard_normal((m, n))
+    kw = dict(alpha=2.5, rank=r, compute="f64")
+
+    def loss(xx, aa, bb):
+        y, _ = olora.lora_forward(xx, packed, scales, aa, bb, **kw)
+        return float((gy * y).sum())
+
+    _, h = olora.lora_forward(x, packed, scales, a, b, **kw)
+    dx, da, db = olora.lora_backward(gy, x, packed, scales, a, b, h, **kw)
+    eps = 1e-6
+    for arr, grad, which in ((x, dx, 0), (a, da, 1), (b, db, 2)):
+        num = np.zeros_like(arr)
+        for idx in np.ndindex(arr.shape):
+            plus = [x.copy(), a.copy(), b.copy()]
+            minus = [x.copy(), a.copy(), b.copy()]
+            plus[which][idx] += eps
+            minus[which][idx] -= eps
+            num[idx] = (loss(*plus) - loss(*minus)) / (2 * eps)
+        np.testing.assert_allclose(grad, num, rtol=1e-6, atol=1e-8)
+
+
+def test_bf16_backward_gradients_are_bf16_values():
+    x, packed, scales, a, b, _ = _case(seed=4)
+    gy = bf16_round(np.random.Generator(np.random.PCG64(5)).standard_normal((5, 6)))
+    _, h = olora.lora_forward(x, packed, scales, a, b, alpha=4.0, rank=2)
+    dx, da, db = olora.lora_backward(gy, x, packed, scales, a, b, h, alpha=4.0, rank=2)
+    for t in (dx, da, db):
+        assert np.array_equal(bf16_round(t), t)
+    assert da.dtype == np.float32 and db.dtype == np.float32
+
+
+def test_scaling_is_rounded_like_a_weak_scalar():
+    assert olora.lora_scaling(32.0, 16) == 2.0
+    assert olora.lora_scaling(1.0, 3) == bf16_round(np.float32(1 / 3))
+    assert olora.lora_scaling(1.0, 3, "f32") == np.float32(1 / 3)
+
+
+# ---------------------------------------------------------------------------
+# FP8
+# ---------------------------------------------------------------------------
+def test_scale_closed_forms():
+    assert ofp8.scale_from_amax(ofp8.amax(np.zeros((3, 3))), E4M3FN) == FLT_MIN
+    assert ofp8.scale_from_amax(np.float32(448.0), E4M3FN) == 1.0
+    assert ofp8.scale_from_amax(np.float32(57344.0 * 4), E5M2) == 4.0
+    assert np.isnan(ofp8.scale_from_amax(ofp8.amax(np.array([1.0, np.nan])), E4M3FN))
+    assert np.isinf(ofp8.scale_from_amax(ofp8.amax(np.array([1.0, -np.inf])), E4M3FN))
+    # max |x| maps onto fmax
+    x = np.array([[0.5, -3.0], [2.0, 1.0]], np.float32)
+    q, s = ofp8.scaled_quantize(x, E4M3FN)
+    assert s == np.float32(3.0) / np.float32(448.0)
+    assert ofp8.fp8_decode(q, E4M3FN)[0, 1] == -448.0
+
+
+def test_nonfinite_operands():
+    """inf in an operand -> scale inf -> finite/inf = 0 and inf/inf = NaN."""
+
+    q, s = ofp8.scaled_quantize(np.array([1.0, np.inf, -2.0], np.float32), E4M3FN)
+    assert np.isinf(s)
+    v = ofp8.fp8_decode(q, E4M3FN)
+    assert v[0] == 0 and np.isnan(v[1]) and v[2] == 0
+
+
+def test_dot_is_exact_on_representable_operands():
+    """Operands whose scaled values are exact fp8 numbers: the scaled dot must
+    equal the plain float64 product (no quantization error at all)."""
+
+    g = np.random.Generator(np.random.PCG64(7))
+    grid4 = ofp8.fp8_decode(np.arange(0, 0x7F, dtype=np.uint8), E4M3FN)  # finite >= 0
+    grid5 = ofp8.fp8_decode(np.arange(0, 0x7C, dtype=np.uint8), E5M2)
+    left = g.choice(grid4, size=(12, 32)) * g.choice([-1, 1], size=(12, 32))
+    left[0, 0] = 448.0  # amax -> scale exactly 1
+    right = g.choice(grid4, size=(32, 9)) * g.choice([-1, 1], size=(32, 9))
+    right[0, 0] = -448.0
+    out = ofp8.fp8_linear_forward(left, right)
+    np.testing.assert_allclose(out, (left.astype(np.float64) @ right).astype(np.float32),
+                               rtol=1e-6)
+    gy = g.choice(grid5, size=(12, 9)) * g.choice([-1, 1], size=(12, 9))
+    gy[0, 0] = 57344.0
+    dl, dr = ofp8.fp8_linear_backward(left, right, gy, operand_round=lambda v: v)
+    np.testing.assert_allclose(dl, (gy @ right.T).astype(np.float32), rtol=1e-6)
+    np.testing.assert_allclose(dr, (left.T @ gy).astype(np.float32), rtol=1e-6)
+
+
+def test_backward_scales_are_the_forward_ones():
+    """The backward's re-quantization of left/right uses the same amax as the
+    forward, so caching the forward codes is exact."""
+
+    g = np.random.Generator(np.random.PCG64(8))
+    left = bf16_round(g.standard_normal((16, 24)))
+    right = bf16_round(g.standard_normal((24, 8)) * 0.02)
+    ql, sl = ofp8.scaled_quantize(left, E4M3FN)
+    qlt, slt = ofp8.scaled_quantize(left.T, E4M3FN)
+    assert sl == slt and np.array_equal(ql.T, qlt)
+
+
+def test_linear_matmul_flattens_leading_dims():
+    g = np.random.Generator(np.random.PCG64(10))
+    x = bf16_round(g.standard_normal((2, 3, 16)))
+    right = bf16_round(g.standard_normal((16, 5)))
+    out = ofp8.linear_matmul_fp8(x, right)
+    flat = ofp8.linear_matmul_fp8(x.reshape(6, 16), right)
+    assert out.shape == (2, 3, 5) and np.array_equal(out.reshape(6, 5), flat)
+    assert np.array_equal(bf16_round(out), out)
