@@ -98,10 +98,16 @@ bool lora_fast_shape(int dtype, int64_t k, int64_t n_groups, int64_t group, int6
   return true;
 }
 
+bool lora_skinny(int dtype, int64_t m, int64_t k, int64_t n_groups, int64_t group, int64_t rank) {
+  return dtype == kBF16 && skinny_ok(m, k, rank, n_groups, group);
+}
+
 template <typename A>
-void plan_forward(A& a, bool fast, int64_t m, int64_t n, int64_t k, int64_t rank) {
-  (void)k;
-  (void)rank;
+void plan_forward(A& a, bool fast, bool skinny, int64_t m, int64_t n, int64_t k, int64_t rank) {
+  if (skinny) {
+    a.template take<float>(skinny_workspace_floats(m, n, k, rank));
+    return;
+  }
   if (fast) return;
   a.template take<float>(m * n);  // base product
   a.template take<float>(m * n);  // adapter product
@@ -112,6 +118,7 @@ template <typename A>
 void plan_backward(A& a, bool fast, int64_t m, int64_t n, int64_t k, int64_t rank, int dtype) {
   if (fast) {
     a.template take<uint16_t>(rank * n);  // B^T
+    a.template take<uint16_t>(k * rank);  // A^T
     a.template take<uint16_t>(m * rank);  // dh
     a.template take<uint16_t>(k * n);     // W_b^T
     int64_t part = rank_tn_workspace_floats(m, n, rank);
@@ -254,7 +261,8 @@ size_t rpx_int4lora_forward_workspace(int64_t m, int64_t n, int64_t k, int64_t g
     g = group_size;
   }
   Sizer s;
-  plan_forward(s, lora_fast_shape(dtype, k, ng, g, rank), m, n, k, rank);
+  plan_forward(s, lora_fast_shape(dtype, k, ng, g, rank), lora_skinny(dtype, m, k, ng, g, rank), m,
+               n, k, rank);
   return s.used;
 }
 
@@ -284,6 +292,17 @@ int rpx_int4lora_forward(const void* x, int dtype, int64_t m, int64_t k, const u
   const bool fast = lora_fast_shape(dtype, k, ng, g, rank) && aligned16(x) && aligned16(packed) &&
                     aligned16(lora_a) && aligned16(y);
   Arena arena(workspace, workspace_bytes);
+  if (lora_skinny(dtype, m, k, ng, g, rank) && aligned16(x) && aligned16(packed) &&
+      aligned16(lora_a)) {
+    float* ws = arena.take<float>(skinny_workspace_floats(m, n, k, rank));
+    if (arena.overflow) return fail_invalid("rpx_int4lora_forward: workspace too small");
+    RPX_HIP(launch_skinny_forward(static_cast<const uint16_t*>(x), m, k, w, n,
+                                  static_cast<const uint16_t*>(lora_a),
+                                  static_cast<const uint16_t*>(lora_b), rank, c, bias_bits,
+                                  static_cast<uint16_t*>(y), static_cast<uint16_t*>(h), ws, st),
+            "int4lora_forward: skinny-M kernels");
+    return kOk;
+  }
   if (fast) {
     const uint16_t* xb = static_cast<const uint16_t*>(x);
     uint16_t* hb = static_cast<uint16_t*>(h);
@@ -374,6 +393,7 @@ int rpx_int4lora_backward(const void* grad, const void* x, int dtype, int64_t m,
     const uint16_t* ab = static_cast<const uint16_t*>(lora_a);
     const uint16_t* bb = static_cast<const uint16_t*>(lora_b);
     uint16_t* bt = arena.take<uint16_t>(rank * n);
+    uint16_t* at = arena.take<uint16_t>(k * rank);
     uint16_t* dh = arena.take<uint16_t>(m * rank);
     uint16_t* wt = arena.take<uint16_t>(k * n);
     int64_t part_n = rank_tn_workspace_floats(m, n, rank);
@@ -381,8 +401,10 @@ int rpx_int4lora_backward(const void* grad, const void* x, int dtype, int64_t m,
     if (part_a > part_n) part_n = part_a;
     float* part = arena.take<float>(part_n);
     if (arena.overflow) return fail_invalid("rpx_int4lora_backward: workspace too small");
-    // B^T [r, N] so that dh = g_a . B is an NT product
+    // B^T [r, N] so that dh = g_a . B is an NT product; A^T [K, r] for the
+    // dx epilogue's contiguous fragment loads
     RPX_HIP(launch_transpose_bf16(bb, n, rank, rank, bt, n, st), "int4lora_backward: B^T");
+    RPX_HIP(launch_transpose_bf16(ab, rank, k, k, at, rank, st), "int4lora_backward: A^T");
     // dh = bf16(bf16(g * c) . B)
     RPX_HIP(launch_rank_nt(gb, n, bt, n, m, rank, n, true, c, dh, rank, st),
             "int4lora_backward: dh");
@@ -395,9 +417,9 @@ int rpx_int4lora_backward(const void* grad, const void* x, int dtype, int64_t m,
             "int4lora_backward: dequantized transpose");
     // dx = bf16(bf16(g . W_b) + bf16(dh . A))
     LowRankEpilogue epi;
-    epi.rows = ab;  // R(k, j) = A[j, k]
-    epi.rows_sn = 1;
-    epi.rows_sj = k;
+    epi.rows = at;  // R(k, j) = A[j, k] = A^T[k, j]
+    epi.rows_sn = rank;
+    epi.rows_sj = 1;
     epi.cols = dh;
     epi.cols_sm = rank;
     epi.cols_sj = 1;

@@ -10,6 +10,9 @@
 //   gemm  : v_mfma_f32_32x32x64_f8f6f4 NT GEMM on fp8 codes, f32 accumulate,
 //           epilogue ((acc * s_a) * s_b) rounded once to the output dtype;
 //           optional split-K with fp32 partials and a deterministic sum.
+#include <cstdlib>
+#include <cstring>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -286,82 +289,106 @@ __global__ void __launch_bounds__(256)
 // fp8 NT GEMM
 // ---------------------------------------------------------------------------
 constexpr int kBKb = 128;            // bytes (= fp8 elements) per K slice
-constexpr int kLd8 = kBKb + 16;      // LDS row stride in bytes
 
 template <int FA, int FB>
 __device__ __forceinline__ f32x16_t mfma_f8(i32x8_t a, i32x8_t b, f32x16_t c) {
   return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, FA, FB, 0, 0, 0, 0);
 }
 
-template <int BM, int BN, int WM, int WN, int FA, int FB>
+// vmcnt(n) with the expcnt / lgkmcnt fields left at "no wait" (gfx9 encoding).
+#define RPX_WAIT_VMCNT(n) \
+  __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (15 << 8) | ((((n) >> 4) & 3) << 14))
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// Issues one K-slice of direct-to-LDS loads for this wave: AS A-segments and
+// BS B-segments of 8 rows x 128 bytes (kept out of lambdas: the builtin is
+// device-only).
+template <int BM, int AS, int BS>
+__device__ __forceinline__ void dma_stage(uint8_t* st, const uint8_t* const* a_src,
+                                          const uint8_t* const* b_src, int64_t koff, int wave) {
+#pragma unroll
+  for (int i = 0; i < AS; ++i)
+    __builtin_amdgcn_global_load_lds(
+        a_src[i] + koff,
+        reinterpret_cast<lds_void_t*>(reinterpret_cast<uintptr_t>(st) + (wave * AS + i) * 1024),
+        16, 0, 0);
+#pragma unroll
+  for (int i = 0; i < BS; ++i)
+    __builtin_amdgcn_global_load_lds(
+        b_src[i] + koff,
+        reinterpret_cast<lds_void_t*>(reinterpret_cast<uintptr_t>(st) + BM * kBKb +
+                                      (wave * BS + i) * 1024),
+        16, 0, 0);
+}
+
+// Pipelined fp8 NT GEMM. Each K-slice of 128 bytes of A [BM rows] and B [BN
+// rows] moves global -> LDS with 16-byte direct-to-LDS loads (no register
+// staging) into one of NS stages; NS - 1 slices are in flight while one is
+// multiplied. LDS rows are 128 bytes, unpadded, with their eight 16-byte
+// chunks XOR-swizzled by (row & 7) so that fragment reads are conflict-free:
+// a DMA wave instruction writes 64 x 16 bytes = 8 rows contiguously, lane l
+// landing at (row l/8, physical chunk l%8), so lane l fetches logical chunk
+// (l%8) ^ (row & 7). Completion is tracked with explicit vmcnt waits and a
+// plain s_barrier (a __syncthreads would wait for every load in flight).
+template <int BM, int BN, int WM, int WN, int NS, int FA, int FB>
 __global__ void __launch_bounds__(64 * WM * WN)
     k_fp8_gemm(const uint8_t* __restrict__ A, const uint8_t* __restrict__ B, int64_t M,
                int64_t N, int64_t K, int64_t k_per_split, const float* __restrict__ s_a,
                const float* __restrict__ s_b, void* __restrict__ out, int out_dtype,
                int64_t ldc, float* __restrict__ partials, int tiles_m, int tiles_n) {
-  constexpr int NT = 64 * WM * WN;
+  constexpr int NW = WM * WN;
   constexpr int TM = BM / WM;
   constexpr int TN = BN / WN;
   constexpr int FM = TM / 32;
   constexpr int FN = TN / 32;
+  constexpr int A_SEGS = BM / 8;  // 1 KB DMA segments (8 rows) per stage
+  constexpr int B_SEGS = BN / 8;
+  static_assert(A_SEGS % NW == 0 && B_SEGS % NW == 0, "segments must split over waves");
+  constexpr int LPW = (A_SEGS + B_SEGS) / NW;  // DMA instructions per wave per stage
+  static_assert(LPW * (NS - 2) < 64, "vmcnt range");
+  constexpr int STAGE = (BM + BN) * kBKb;
   extern __shared__ __align__(16) uint8_t smem8[];
-  uint8_t* sA = smem8;
-  uint8_t* sB = smem8 + 2 * BM * kLd8;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int wm = wave % WM;
   const int wn = wave / WM;
+  // Row-major (n fastest) tiles dealt to the 8 XCDs in contiguous ranges so
+  // each XCD's L2 keeps a few A row-blocks; split-K slices are outermost.
   const int tiles = tiles_m * tiles_n;
-  const int split = blockIdx.x / tiles;
-  const int tile = blockIdx.x % tiles;
-  const int tm = tile % tiles_m;
-  const int tn = tile / tiles_m;
+  const int total = static_cast<int>(gridDim.x);
+  int b = blockIdx.x;
+  if (total % 8 == 0) b = (blockIdx.x % 8) * (total / 8) + blockIdx.x / 8;
+  const int split = b / tiles;
+  const int tile = b % tiles;
+  const int tm = tile / tiles_n;
+  const int tn = tile % tiles_n;
   const int64_t m0 = static_cast<int64_t>(tm) * BM;
   const int64_t n0 = static_cast<int64_t>(tn) * BN;
   const int64_t kbeg = static_cast<int64_t>(split) * k_per_split;
   int64_t kend = kbeg + k_per_split;
   if (kend > K) kend = K;
+  const int64_t nk = (kend - kbeg) / kBKb;
 
-  constexpr int VPR = kBKb / 16;  // 16-byte vectors per row
-  constexpr int A_PER_T = BM * VPR / NT;
-  constexpr int B_PER_T = BN * VPR / NT;
-  static_assert(BM * VPR % NT == 0 && BN * VPR % NT == 0, "tiles must split evenly");
-  u32x4_t a_reg[A_PER_T];
-  u32x4_t b_reg[B_PER_T];
-
-  auto load = [&](int64_t k0) {
+  // per-lane source rows/chunks for this wave's DMA segments
+  const int seg_row = lane >> 3;                        // row within a segment
+  const int chunk = (lane & 7) ^ (seg_row & 7);         // logical 16-byte chunk
+  const uint8_t* a_src[A_SEGS / NW];
+  const uint8_t* b_src[B_SEGS / NW];
 #pragma unroll
-    for (int i = 0; i < A_PER_T; ++i) {
-      const int v = tid + i * NT;
-      const int64_t gm = m0 + v / VPR;
-      a_reg[i] = gm < M ? *reinterpret_cast<const u32x4_t*>(A + gm * K + k0 + (v % VPR) * 16)
-                        : u32x4_t{0u, 0u, 0u, 0u};
-    }
+  for (int i = 0; i < A_SEGS / NW; ++i) {
+    int64_t r = m0 + (wave * (A_SEGS / NW) + i) * 8 + seg_row;
+    r = r < M ? r : M - 1;
+    a_src[i] = A + r * K + chunk * 16;
+  }
 #pragma unroll
-    for (int i = 0; i < B_PER_T; ++i) {
-      const int v = tid + i * NT;
-      const int64_t gn = n0 + v / VPR;
-      b_reg[i] = gn < N ? *reinterpret_cast<const u32x4_t*>(B + gn * K + k0 + (v % VPR) * 16)
-                        : u32x4_t{0u, 0u, 0u, 0u};
-    }
-  };
-  auto store = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < A_PER_T; ++i) {
-      const int v = tid + i * NT;
-      *reinterpret_cast<u32x4_t*>(sA + buf * BM * kLd8 + (v / VPR) * kLd8 + (v % VPR) * 16) =
-          a_reg[i];
-    }
-#pragma unroll
-    for (int i = 0; i < B_PER_T; ++i) {
-      const int v = tid + i * NT;
-      *reinterpret_cast<u32x4_t*>(sB + buf * BN * kLd8 + (v / VPR) * kLd8 + (v % VPR) * 16) =
-          b_reg[i];
-    }
-  };
-
+  for (int i = 0; i < B_SEGS / NW; ++i) {
+    int64_t r = n0 + (wave * (B_SEGS / NW) + i) * 8 + seg_row;
+    r = r < N ? r : N - 1;
+    b_src[i] = B + r * K + chunk * 16;
+  }
   f32x16_t acc[FN][FM];
 #pragma unroll
   for (int fn = 0; fn < FN; ++fn)
@@ -370,29 +397,27 @@ __global__ void __launch_bounds__(64 * WM * WN)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[fn][fm][v] = 0.0f;
 
-  auto compute = [&](int buf) {
-    const uint8_t* a_base = sA + buf * BM * kLd8 + (wm * TM + (lane & 31)) * kLd8 + (lane >> 5) * 32;
-    const uint8_t* b_base = sB + buf * BN * kLd8 + (wn * TN + (lane & 31)) * kLd8 + (lane >> 5) * 32;
+  const int frow = lane & 31;        // fragment row within a 32-row block
+  const int fhalf = lane >> 5;       // which 32 bytes of the 64-byte k sub-step
+  auto frag = [&](const uint8_t* base, int row, int kk) -> i32x8_t {
+    const int c0 = 4 * kk + 2 * fhalf;
+    const uint8_t* r = base + row * kBKb;
+    const u32x4_t lo = *reinterpret_cast<const u32x4_t*>(r + ((c0 ^ (row & 7)) * 16));
+    const u32x4_t hi = *reinterpret_cast<const u32x4_t*>(r + (((c0 + 1) ^ (row & 7)) * 16));
+    return i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3],
+                   (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+  };
+  auto compute = [&](int64_t t) {
+    const uint8_t* sa = smem8 + (t % NS) * STAGE;
+    const uint8_t* sb = sa + BM * kBKb;
 #pragma unroll
     for (int kk = 0; kk < kBKb / 64; ++kk) {
       i32x8_t af[FM];
       i32x8_t bfr[FN];
 #pragma unroll
-      for (int fm = 0; fm < FM; ++fm) {
-        const u32x4_t* p = reinterpret_cast<const u32x4_t*>(a_base + fm * 32 * kLd8 + kk * 64);
-        const u32x4_t lo = p[0];
-        const u32x4_t hi = p[1];
-        af[fm] = i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3],
-                         (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
-      }
+      for (int fm = 0; fm < FM; ++fm) af[fm] = frag(sa, wm * TM + fm * 32 + frow, kk);
 #pragma unroll
-      for (int fn = 0; fn < FN; ++fn) {
-        const u32x4_t* p = reinterpret_cast<const u32x4_t*>(b_base + fn * 32 * kLd8 + kk * 64);
-        const u32x4_t lo = p[0];
-        const u32x4_t hi = p[1];
-        bfr[fn] = i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3],
-                          (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
-      }
+      for (int fn = 0; fn < FN; ++fn) bfr[fn] = frag(sb, wn * TN + fn * 32 + frow, kk);
 #pragma unroll
       for (int fn = 0; fn < FN; ++fn)
 #pragma unroll
@@ -400,19 +425,23 @@ __global__ void __launch_bounds__(64 * WM * WN)
     }
   };
 
-  const int64_t nk = (kend - kbeg) / kBKb;
-  if (nk > 0) {
-    load(kbeg);
-    store(0);
-    __syncthreads();
-    for (int64_t kt = 0; kt < nk; ++kt) {
-      const int cur = static_cast<int>(kt & 1);
-      const bool more = kt + 1 < nk;
-      if (more) load(kbeg + (kt + 1) * kBKb);
-      compute(cur);
-      if (more) store(cur ^ 1);
-      __syncthreads();
+#pragma unroll
+  for (int s = 0; s < NS - 1; ++s)
+    if (s < nk)
+      dma_stage<BM, A_SEGS / NW, B_SEGS / NW>(smem8 + (s % NS) * STAGE, a_src, b_src,
+                                               kbeg + s * kBKb, wave);
+  for (int64_t t = 0; t < nk; ++t) {
+    // slice t has landed once at most the later slices' loads are pending
+    if (t + NS - 2 < nk) {
+      RPX_WAIT_VMCNT(LPW * (NS - 2));
+    } else {
+      RPX_WAIT_VMCNT(0);
     }
+    __builtin_amdgcn_s_barrier();
+    if (t + NS - 1 < nk)  // refills the stage read at t - 1
+      dma_stage<BM, A_SEGS / NW, B_SEGS / NW>(smem8 + ((t + NS - 1) % NS) * STAGE, a_src, b_src,
+                                               kbeg + (t + NS - 1) * kBKb, wave);
+    compute(t);
   }
 
   const float sa = s_a[0];
@@ -479,37 +508,65 @@ __global__ void __launch_bounds__(256)
 }
 
 struct Fp8Plan {
+  int cfg;  // 1: 256x128 (2x2), 2: 128x128 (2x2), 3: 256x256 (2x2), 4: 256x96 (4x1)
   int bm, bn;
   int64_t splits, k_per_split;
 };
 
-Fp8Plan plan_fp8(int64_t m, int64_t n, int64_t k) {
-  Fp8Plan p;
-  if (ceil_div(m, 256) * ceil_div(n, 128) >= 256) {
-    p.bm = 256;
-    p.bn = 128;
-  } else {
-    p.bm = 128;
-    p.bn = 128;
+int fp8_tile_override() {
+  static int cached = -1;
+  if (cached < 0) {
+    const char* env = std::getenv("RPX_FP8_TILE");
+    cached = 0;
+    if (env != nullptr) {
+      if (std::strcmp(env, "256x128") == 0) cached = 1;
+      if (std::strcmp(env, "128x128") == 0) cached = 2;
+      if (std::strcmp(env, "256x256") == 0) cached = 3;
+      if (std::strcmp(env, "256x96") == 0) cached = 4;
+    }
   }
+  return cached;
+}
+
+Fp8Plan plan_fp8(int64_t m, int64_t n, int64_t k) {
+  static const int kBM[5] = {0, 256, 128, 256, 256};
+  static const int kBN[5] = {0, 128, 128, 256, 96};
+  Fp8Plan p;
+  p.cfg = fp8_tile_override();
+  if (p.cfg == 0) {
+    // biggest tile that still gives one tile per CU, else 128x128 + split-K
+    if (ceil_div(m, 256) * ceil_div(n, 256) >= 256)
+      p.cfg = 3;
+    else if (ceil_div(m, 256) * ceil_div(n, 128) >= 256)
+      p.cfg = 1;
+    else if (n % 96 == 0 && ceil_div(m, 256) * (n / 96) >= 256)
+      p.cfg = 4;
+    else
+      p.cfg = 2;
+  }
+  p.bm = kBM[p.cfg];
+  p.bn = kBN[p.cfg];
   const int64_t tiles = ceil_div(m, p.bm) * ceil_div(n, p.bn);
   const int64_t kslices = k / kBKb;
   int64_t s = 1;
-  while (tiles * s < 256 && s * 2 <= kslices && s < 8) s *= 2;
-  p.splits = s;
+  while (tiles * s < 256 && s * 2 <= kslices && s < 16) s *= 2;
   p.k_per_split = ceil_div(kslices, s) * kBKb;
   p.splits = ceil_div(k, p.k_per_split);
   return p;
 }
 
-template <int BM, int BN, int FA, int FB>
+template <int BM, int BN, int WM, int WN, int FA, int FB>
 hipError_t run_fp8(const uint8_t* a, const uint8_t* b, int64_t m, int64_t n, int64_t k,
                    const Fp8Plan& plan, const float* s_a, const float* s_b, void* out,
                    int out_dtype, int64_t ldc, float* partials, hipStream_t stream) {
+  // as many stages as fit in 160 KB of LDS (at most 4)
+  constexpr int kStage = (BM + BN) * kBKb;
+  constexpr int NS = (160 * 1024 / kStage) >= 4 ? 4 : (160 * 1024 / kStage);
+  static_assert(NS >= 2, "tile too large for LDS");
   const int tiles_m = static_cast<int>(ceil_div(m, BM));
   const int tiles_n = static_cast<int>(ceil_div(n, BN));
-  const size_t lds = static_cast<size_t>(2) * (BM + BN) * kLd8;
-  auto kern = k_fp8_gemm<BM, BN, 2, 2, FA, FB>;
+  const size_t lds = static_cast<size_t>(NS) * kStage;
+  auto kern = k_fp8_gemm<BM, BN, WM, WN, NS, FA, FB>;
   static bool attr_set = false;
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -519,9 +576,9 @@ hipError_t run_fp8(const uint8_t* a, const uint8_t* b, int64_t m, int64_t n, int
     attr_set = true;
   }
   const unsigned blocks = static_cast<unsigned>(tiles_m) * tiles_n * plan.splits;
-  hipLaunchKernelGGL(kern, dim3(blocks), dim3(256), lds, stream, a, b, m, n, k, plan.k_per_split,
-                     s_a, s_b, out, out_dtype, ldc, plan.splits > 1 ? partials : nullptr,
-                     tiles_m, tiles_n);
+  hipLaunchKernelGGL(kern, dim3(blocks), dim3(64 * WM * WN), lds, stream, a, b, m, n, k,
+                     plan.k_per_split, s_a, s_b, out, out_dtype, ldc,
+                     plan.splits > 1 ? partials : nullptr, tiles_m, tiles_n);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || plan.splits == 1) return e;
   int64_t g = ceil_div(m * n, 256);
@@ -536,11 +593,20 @@ hipError_t dispatch_fp8(const uint8_t* a, const uint8_t* b, int64_t m, int64_t n
                         const float* s_a, const float* s_b, void* out, int out_dtype, int64_t ldc,
                         float* partials, hipStream_t stream) {
   const Fp8Plan plan = plan_fp8(m, n, k);
-  if (plan.bm == 256)
-    return run_fp8<256, 128, FA, FB>(a, b, m, n, k, plan, s_a, s_b, out, out_dtype, ldc,
-                                     partials, stream);
-  return run_fp8<128, 128, FA, FB>(a, b, m, n, k, plan, s_a, s_b, out, out_dtype, ldc, partials,
-                                   stream);
+  switch (plan.cfg) {
+    case 1:
+      return run_fp8<256, 128, 2, 2, FA, FB>(a, b, m, n, k, plan, s_a, s_b, out, out_dtype, ldc,
+                                             partials, stream);
+    case 3:
+      return run_fp8<256, 256, 2, 2, FA, FB>(a, b, m, n, k, plan, s_a, s_b, out, out_dtype, ldc,
+                                             partials, stream);
+    case 4:
+      return run_fp8<256, 96, 4, 1, FA, FB>(a, b, m, n, k, plan, s_a, s_b, out, out_dtype, ldc,
+                                            partials, stream);
+    default:
+      return run_fp8<128, 128, 2, 2, FA, FB>(a, b, m, n, k, plan, s_a, s_b, out, out_dtype, ldc,
+                                             partials, stream);
+  }
 }
 
 }  // namespace

@@ -12,6 +12,9 @@
 // fragment, so lane l of a 32x32 block owns output row m = l % 32 and the
 // registers v = 0..15 hold output columns n = 8*(v/4) + 4*(l/32) + v%4,
 // which lets each lane store 4 consecutive bf16 outputs at once.
+#include <cstdlib>
+#include <cstring>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -27,8 +30,17 @@ __device__ __forceinline__ bf16x8_t as_bf16x8(u32x4_t v) {
   return __builtin_bit_cast(bf16x8_t, v);
 }
 
-__device__ __forceinline__ bf16x8_t load8_strided(const uint16_t* base, int64_t stride,
-                                                  int valid) {
+// Number of the 8 ranks starting at j that exist (0..8).
+__device__ __forceinline__ int valid8(int64_t rank, int64_t j) {
+  const int64_t v = rank - j;
+  return static_cast<int>(v < 0 ? 0 : (v > 8 ? 8 : v));
+}
+
+// 8 bf16 at base[e * stride], e < valid (zero beyond); one 16-byte load when
+// contiguous, complete and aligned.
+__device__ __forceinline__ bf16x8_t load8_j(const uint16_t* base, int64_t stride, int valid) {
+  if (stride == 1 && valid == 8 && (reinterpret_cast<uintptr_t>(base) & 15) == 0)
+    return *reinterpret_cast<const bf16x8_t*>(base);
   uint32_t w[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
@@ -53,8 +65,8 @@ __device__ __forceinline__ void dequant8(uint32_t word, float s, float m8s, uint
   }
 }
 
-template <int BM, int BN, int WM, int WN, bool INT4>
-__global__ void __launch_bounds__(64 * WM * WN)
+template <int BM, int BN, int WM, int WN, bool INT4, int JB>
+__global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(JB == 4 ? 1 : 2)))
     k_gemm_nt(const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ B,
               int64_t ldb, Int4Operand w, int group_shift, int64_t M, int64_t N, int64_t K,
               uint16_t* __restrict__ out, int64_t ldc, LowRankEpilogue epi, int tiles_m) {
@@ -73,8 +85,15 @@ __global__ void __launch_bounds__(64 * WM * WN)
   const int wave = tid >> 6;
   const int wm = wave % WM;
   const int wn = wave / WM;
-  const int tm = blockIdx.x % tiles_m;
-  const int tn = blockIdx.x / tiles_m;
+  // Tiles in row-major (n fastest) order, dealt to the 8 XCDs (which take
+  // workgroups round-robin) in contiguous ranges, so that each XCD's L2
+  // holds a few A row-blocks and streams the weight tiles.
+  const int tiles = gridDim.x;
+  int tile = blockIdx.x;
+  if (tiles % 8 == 0) tile = (blockIdx.x % 8) * (tiles / 8) + blockIdx.x / 8;
+  const int tiles_n = tiles / tiles_m;
+  const int tm = tile / tiles_n;
+  const int tn = tile % tiles_n;
   const int64_t m0 = static_cast<int64_t>(tm) * BM;
   const int64_t n0 = static_cast<int64_t>(tn) * BN;
 
@@ -208,30 +227,57 @@ __global__ void __launch_bounds__(64 * WM * WN)
   }
 
   // Epilogue --------------------------------------------------------------
+  // The low-rank term t = C R^T for this lane's rows m and columns n is one
+  // more 32x32x16 MFMA per 16 ranks; its fragments are loaded up front.
+  constexpr int kMaxJB = JB > 0 ? JB : 1;  // ceil(rank / 16), rank <= 16 * JB
+  const int jblocks = JB > 0 ? static_cast<int>((epi.rank + 15) / 16) : 0;
   const bool vec_store = (ldc % 4 == 0) && ((reinterpret_cast<uintptr_t>(out) & 7) == 0);
+  bf16x8_t cf[kMaxJB][FM];
+  if (jblocks > 0) {
+#pragma unroll
+    for (int jb = 0; jb < kMaxJB; ++jb) {
+      if (jb >= jblocks) break;
+      const int64_t jl = jb * 16 + (lane >> 5) * 8;
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm) {
+        const int64_t m = m0 + wm * TM + fm * 32 + (lane & 31);
+        cf[jb][fm] = load8_j(epi.cols + m * epi.cols_sm + jl * epi.cols_sj, epi.cols_sj,
+                             m < M ? valid8(epi.rank, jl) : 0);
+      }
+    }
+  }
 #pragma unroll
   for (int fn = 0; fn < FN; ++fn) {
+    const int64_t n_blk = n0 + wn * TN + fn * 32;
+    bf16x8_t rf[kMaxJB];
+    if (jblocks > 0) {
+      const int64_t n_row = n_blk + (lane & 31);
+#pragma unroll
+      for (int jb = 0; jb < kMaxJB; ++jb) {
+        if (jb >= jblocks) break;
+        const int64_t jl = jb * 16 + (lane >> 5) * 8;
+        rf[jb] = load8_j(epi.rows + n_row * epi.rows_sn + jl * epi.rows_sj, epi.rows_sj,
+                         n_row < N ? valid8(epi.rank, jl) : 0);
+      }
+    }
+    float bias4[4][4];
+#pragma unroll
+    for (int vg = 0; vg < 4; ++vg)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int64_t nn = n_blk + 8 * vg + 4 * (lane >> 5) + e;
+        bias4[vg][e] = (epi.bias != nullptr && nn < N) ? bf16_to_f32(epi.bias[nn]) : 0.0f;
+      }
 #pragma unroll
     for (int fm = 0; fm < FM; ++fm) {
       const int64_t m = m0 + wm * TM + fm * 32 + (lane & 31);
-      const int64_t n_blk = n0 + wn * TN + fn * 32;
       f32x16_t t;
 #pragma unroll
       for (int v = 0; v < 16; ++v) t[v] = 0.0f;
-      if (epi.rank > 0) {
-        const int64_t n_row = n_blk + (lane & 31);
-        for (int64_t j0 = 0; j0 < epi.rank; j0 += 16) {
-          const int64_t jl = j0 + (lane >> 5) * 8;
-          int valid = static_cast<int>(epi.rank - jl);
-          valid = valid < 0 ? 0 : (valid > 8 ? 8 : valid);
-          const int vr = (n_row < N) ? valid : 0;
-          const int vc = (m < M) ? valid : 0;
-          const bf16x8_t rf = load8_strided(epi.rows + n_row * epi.rows_sn + jl * epi.rows_sj,
-                                            epi.rows_sj, vr);
-          const bf16x8_t cf = load8_strided(epi.cols + m * epi.cols_sm + jl * epi.cols_sj,
-                                            epi.cols_sj, vc);
-          t = __builtin_amdgcn_mfma_f32_32x32x16_bf16(rf, cf, t, 0, 0, 0);
-        }
+#pragma unroll
+      for (int jb = 0; jb < kMaxJB; ++jb) {
+        if (jb >= jblocks) break;
+        t = __builtin_amdgcn_mfma_f32_32x32x16_bf16(rf[jb], cf[jb][fm], t, 0, 0, 0);
       }
       if (m >= M) continue;
 #pragma unroll
@@ -242,8 +288,8 @@ __global__ void __launch_bounds__(64 * WM * WN)
         for (int e = 0; e < 4; ++e) {
           const int v = 4 * vg + e;
           float r = round_bf16(acc[fn][fm][v]);
-          if (epi.rank > 0) r = round_bf16(r + round_bf16(round_bf16(t[v]) * epi.scale));
-          if (epi.bias != nullptr && nb + e < N) r = round_bf16(r + bf16_to_f32(epi.bias[nb + e]));
+          if (jblocks > 0) r = round_bf16(r + round_bf16(round_bf16(t[v]) * epi.scale));
+          if (epi.bias != nullptr) r = round_bf16(r + bias4[vg][e]);
           y[e] = r;
         }
         uint16_t* dst = out + m * ldc + nb;
@@ -260,14 +306,14 @@ __global__ void __launch_bounds__(64 * WM * WN)
   }
 }
 
-template <int BM, int BN, int WM, int WN, bool INT4>
-hipError_t run_gemm(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb,
-                    const Int4Operand& w, int64_t m, int64_t n, int64_t k, uint16_t* out,
-                    int64_t ldc, const LowRankEpilogue& epi, hipStream_t stream) {
+template <int BM, int BN, int WM, int WN, bool INT4, int JB>
+hipError_t run_gemm_jb(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb,
+                       const Int4Operand& w, int64_t m, int64_t n, int64_t k, uint16_t* out,
+                       int64_t ldc, const LowRankEpilogue& epi, hipStream_t stream) {
   const int tiles_m = static_cast<int>(ceil_div(m, BM));
   const int tiles_n = static_cast<int>(ceil_div(n, BN));
   const size_t lds = static_cast<size_t>(2) * (BM + BN) * kLdsLd * sizeof(uint16_t);
-  auto kern = k_gemm_nt<BM, BN, WM, WN, INT4>;
+  auto kern = k_gemm_nt<BM, BN, WM, WN, INT4, JB>;
   static bool attr_set = false;
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -286,15 +332,49 @@ hipError_t run_gemm(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t l
   return hipGetLastError();
 }
 
+template <int BM, int BN, int WM, int WN, bool INT4>
+hipError_t run_gemm(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb,
+                    const Int4Operand& w, int64_t m, int64_t n, int64_t k, uint16_t* out,
+                    int64_t ldc, const LowRankEpilogue& epi, hipStream_t stream) {
+  if (epi.rank <= 0)
+    return run_gemm_jb<BM, BN, WM, WN, INT4, 0>(a, lda, b, ldb, w, m, n, k, out, ldc, epi, stream);
+  if (epi.rank <= 16)
+    return run_gemm_jb<BM, BN, WM, WN, INT4, 1>(a, lda, b, ldb, w, m, n, k, out, ldc, epi, stream);
+  if (epi.rank <= 32)
+    return run_gemm_jb<BM, BN, WM, WN, INT4, 2>(a, lda, b, ldb, w, m, n, k, out, ldc, epi, stream);
+  return run_gemm_jb<BM, BN, WM, WN, INT4, 4>(a, lda, b, ldb, w, m, n, k, out, ldc, epi, stream);
+}
+
+// Tile configuration: RPX_GEMM_TILE=256x128|128x128|128x64 overrides the
+// size-based choice (for tuning sweeps).
+int tile_override() {
+  static int cached = -1;
+  if (cached < 0) {
+    const char* env = std::getenv("RPX_GEMM_TILE");
+    cached = 0;
+    if (env != nullptr) {
+      if (std::strcmp(env, "256x128") == 0) cached = 1;
+      if (std::strcmp(env, "128x128") == 0) cached = 2;
+      if (std::strcmp(env, "128x64") == 0) cached = 3;
+    }
+  }
+  return cached;
+}
+
 template <bool INT4>
 hipError_t dispatch(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb,
                     const Int4Operand& w, int64_t m, int64_t n, int64_t k, uint16_t* out,
                     int64_t ldc, const LowRankEpilogue& epi, hipStream_t stream) {
-  // Pick the largest tile that still yields about one tile per CU.
-  const int64_t cus = 256;
-  if (ceil_div(m, 256) * ceil_div(n, 128) >= cus)
+  int cfg = tile_override();
+  if (cfg == 0) {
+    // 128x128 tiles (two workgroups per CU by LDS) unless that leaves CUs
+    // idle; measured faster than 256x128 at one workgroup per CU
+    const int64_t cus = 256;
+    cfg = (ceil_div(m, 128) * ceil_div(n, 128) >= cus) ? 2 : 3;
+  }
+  if (cfg == 1)
     return run_gemm<256, 128, 2, 2, INT4>(a, lda, b, ldb, w, m, n, k, out, ldc, epi, stream);
-  if (ceil_div(m, 128) * ceil_div(n, 128) >= cus)
+  if (cfg == 2)
     return run_gemm<128, 128, 2, 2, INT4>(a, lda, b, ldb, w, m, n, k, out, ldc, epi, stream);
   return run_gemm<128, 64, 2, 2, INT4>(a, lda, b, ldb, w, m, n, k, out, ldc, epi, stream);
 }

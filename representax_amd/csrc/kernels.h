@@ -56,6 +56,14 @@ hipError_t launch_gemm_bf16(const uint16_t* a, int64_t lda, const uint16_t* b, i
 bool gemm_fast_path_ok(int64_t k, int64_t lda, int64_t ldb_elems, const void* a, const void* b,
                        int64_t ldc, const void* out);
 
+// Skinny-M (M <= 64) INT4 + LoRA forward -------------------------------------
+bool skinny_ok(int64_t m, int64_t k, int64_t rank, int64_t n_groups, int64_t group);
+int64_t skinny_workspace_floats(int64_t m, int64_t n, int64_t k, int64_t rank);
+hipError_t launch_skinny_forward(const uint16_t* x, int64_t m, int64_t k, const Int4Operand& w,
+                                 int64_t n, const uint16_t* lora_a, const uint16_t* lora_b,
+                                 int64_t rank, float scale, const uint16_t* bias, uint16_t* y,
+                                 uint16_t* h, float* ws, hipStream_t stream);
+
 // Rank-r kernels --------------------------------------------------------------
 // out[M, r] = bf16(sum_k op(A[m, k]) * R[j, k]); op(a) = bf16(a * a_scale) when
 // round_a, else a. R bf16 [r, K] row-major (ldr).

@@ -206,3 +206,24 @@ def test_cpu_tensor_is_rejected():
     with pytest.raises(RuntimeError):
         ops.int4_dequant(torch.zeros((4, 4), dtype=torch.uint8),
                          torch.zeros(4, dtype=torch.uint16), 8)
+
+
+@pytest.mark.parametrize(
+    "m,k,n,r,group,bias",
+    [(1, 2048, 6144, 32, None, False), (4, 6144, 2048, 32, None, True),
+     (16, 2048, 2048, 32, 64, False), (17, 1024, 640, 16, None, True),
+     (64, 2048, 1024, 32, 64, True), (33, 384, 200, 8, 128, False), (2, 128, 70, 3, None, True)],
+)
+def test_skinny_forward_matches_oracle(m, k, n, r, group, bias):
+    """M <= 64 runs the split-K skinny kernels (rotating nothing: parity only)."""
+
+    x, packed, scales, a, b, bias_bits, _ = _lora_case(m, k, n, r, group, seed=m + n, bias=bias)
+    y_o, h_o = olora.lora_forward(x, packed, scales, a, b, alpha=float(r), rank=r,
+                                  bias_bits=bias_bits, group_size=group)
+    biasd = None if bias_bits is None else to_dev(bias_bits.view(np.int16)).view(torch.uint16)
+    y, h = ops.int4lora_forward(to_dev_bf16(x), to_dev(packed),
+                                to_dev(scales.view(np.int16)).view(torch.uint16), to_dev_bf16(a),
+                                to_dev_bf16(b), scaling=1.0, group_size=group, bias_bits=biasd)
+    torch.cuda.synchronize()
+    assert rel_l2(from_dev(h), h_o) < TOL
+    assert rel_l2(from_dev(y), y_o) < TOL
