@@ -285,330 +285,6 @@ __global__ void __launch_bounds__(256)
   }
 }
 
-// ---------------------------------------------------------------------------
-// fp8 NT GEMM
-// ---------------------------------------------------------------------------
-constexpr int kBKb = 128;            // bytes (= fp8 elements) per K slice
-
-template <int FA, int FB>
-__device__ __forceinline__ f32x16_t mfma_f8(i32x8_t a, i32x8_t b, f32x16_t c) {
-  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, FA, FB, 0, 0, 0, 0);
-}
-
-// vmcnt(n) with the expcnt / lgkmcnt fields left at "no wait" (gfx9 encoding).
-#define RPX_WAIT_VMCNT(n) \
-  __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (15 << 8) | ((((n) >> 4) & 3) << 14))
-
-typedef __attribute__((address_space(3))) void lds_void_t;
-
-// Issues one K-slice of direct-to-LDS loads for this wave: AS A-segments and
-// BS B-segments of 8 rows x 128 bytes (kept out of lambdas: the builtin is
-// device-only).
-template <int BM, int AS, int BS>
-__device__ __forceinline__ void dma_stage(uint8_t* st, const uint8_t* const* a_src,
-                                          const uint8_t* const* b_src, int64_t koff, int wave) {
-#pragma unroll
-  for (int i = 0; i < AS; ++i)
-    __builtin_amdgcn_global_load_lds(
-        a_src[i] + koff,
-        reinterpret_cast<lds_void_t*>(reinterpret_cast<uintptr_t>(st) + (wave * AS + i) * 1024),
-        16, 0, 0);
-#pragma unroll
-  for (int i = 0; i < BS; ++i)
-    __builtin_amdgcn_global_load_lds(
-        b_src[i] + koff,
-        reinterpret_cast<lds_void_t*>(reinterpret_cast<uintptr_t>(st) + BM * kBKb +
-                                      (wave * BS + i) * 1024),
-        16, 0, 0);
-}
-
-// Pipelined fp8 NT GEMM. Each K-slice of 128 bytes of A [BM rows] and B [BN
-// rows] moves global -> LDS with 16-byte direct-to-LDS loads (no register
-// staging) into one of NS stages; NS - 1 slices are in flight while one is
-// multiplied. LDS rows are 128 bytes, unpadded, with their eight 16-byte
-// chunks XOR-swizzled by (row & 7) so that fragment reads are conflict-free:
-// a DMA wave instruction writes 64 x 16 bytes = 8 rows contiguously, lane l
-// landing at (row l/8, physical chunk l%8), so lane l fetches logical chunk
-// (l%8) ^ (row & 7). Completion is tracked with explicit vmcnt waits and a
-// plain s_barrier (a __syncthreads would wait for every load in flight).
-template <int BM, int BN, int WM, int WN, int NS, int FA, int FB>
-__global__ void __launch_bounds__(64 * WM * WN)
-    k_fp8_gemm(const uint8_t* __restrict__ A, const uint8_t* __restrict__ B, int64_t M,
-               int64_t N, int64_t K, int64_t k_per_split, const float* __restrict__ s_a,
-               const float* __restrict__ s_b, void* __restrict__ out, int out_dtype,
-               int64_t ldc, float* __restrict__ partials, int tiles_m, int tiles_n) {
-  constexpr int NW = WM * WN;
-  constexpr int TM = BM / WM;
-  constexpr int TN = BN / WN;
-  constexpr int FM = TM / 32;
-  constexpr int FN = TN / 32;
-  constexpr int A_SEGS = BM / 8;  // 1 KB DMA segments (8 rows) per stage
-  constexpr int B_SEGS = BN / 8;
-  static_assert(A_SEGS % NW == 0 && B_SEGS % NW == 0, "segments must split over waves");
-  constexpr int LPW = (A_SEGS + B_SEGS) / NW;  // DMA instructions per wave per stage
-  static_assert(LPW * (NS - 2) < 64, "vmcnt range");
-  constexpr int STAGE = (BM + BN) * kBKb;
-  extern __shared__ __align__(16) uint8_t smem8[];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int wm = wave % WM;
-  const int wn = wave / WM;
-  // Row-major (n fastest) tiles dealt to the 8 XCDs in contiguous ranges so
-  // each XCD's L2 keeps a few A row-blocks; split-K slices are outermost.
-  const int tiles = tiles_m * tiles_n;
-  const int total = static_cast<int>(gridDim.x);
-  int b = blockIdx.x;
-  if (total % 8 == 0) b = (blockIdx.x % 8) * (total / 8) + blockIdx.x / 8;
-  const int split = b / tiles;
-  const int tile = b % tiles;
-  const int tm = tile / tiles_n;
-  const int tn = tile % tiles_n;
-  const int64_t m0 = static_cast<int64_t>(tm) * BM;
-  const int64_t n0 = static_cast<int64_t>(tn) * BN;
-  const int64_t kbeg = static_cast<int64_t>(split) * k_per_split;
-  int64_t kend = kbeg + k_per_split;
-  if (kend > K) kend = K;
-  const int64_t nk = (kend - kbeg) / kBKb;
-
-  // per-lane source rows/chunks for this wave's DMA segments
-  const int seg_row = lane >> 3;                        // row within a segment
-  const int chunk = (lane & 7) ^ (seg_row & 7);         // logical 16-byte chunk
-  const uint8_t* a_src[A_SEGS / NW];
-  const uint8_t* b_src[B_SEGS / NW];
-#pragma unroll
-  for (int i = 0; i < A_SEGS / NW; ++i) {
-    int64_t r = m0 + (wave * (A_SEGS / NW) + i) * 8 + seg_row;
-    r = r < M ? r : M - 1;
-    a_src[i] = A + r * K + chunk * 16;
-  }
-#pragma unroll
-  for (int i = 0; i < B_SEGS / NW; ++i) {
-    int64_t r = n0 + (wave * (B_SEGS / NW) + i) * 8 + seg_row;
-    r = r < N ? r : N - 1;
-    b_src[i] = B + r * K + chunk * 16;
-  }
-  f32x16_t acc[FN][FM];
-#pragma unroll
-  for (int fn = 0; fn < FN; ++fn)
-#pragma unroll
-    for (int fm = 0; fm < FM; ++fm)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) acc[fn][fm][v] = 0.0f;
-
-  const int frow = lane & 31;        // fragment row within a 32-row block
-  const int fhalf = lane >> 5;       // which 32 bytes of the 64-byte k sub-step
-  auto frag = [&](const uint8_t* base, int row, int kk) -> i32x8_t {
-    const int c0 = 4 * kk + 2 * fhalf;
-    const uint8_t* r = base + row * kBKb;
-    const u32x4_t lo = *reinterpret_cast<const u32x4_t*>(r + ((c0 ^ (row & 7)) * 16));
-    const u32x4_t hi = *reinterpret_cast<const u32x4_t*>(r + (((c0 + 1) ^ (row & 7)) * 16));
-    return i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3],
-                   (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
-  };
-  auto compute = [&](int64_t t) {
-    const uint8_t* sa = smem8 + (t % NS) * STAGE;
-    const uint8_t* sb = sa + BM * kBKb;
-#pragma unroll
-    for (int kk = 0; kk < kBKb / 64; ++kk) {
-      i32x8_t af[FM];
-      i32x8_t bfr[FN];
-#pragma unroll
-      for (int fm = 0; fm < FM; ++fm) af[fm] = frag(sa, wm * TM + fm * 32 + frow, kk);
-#pragma unroll
-      for (int fn = 0; fn < FN; ++fn) bfr[fn] = frag(sb, wn * TN + fn * 32 + frow, kk);
-#pragma unroll
-      for (int fn = 0; fn < FN; ++fn)
-#pragma unroll
-        for (int fm = 0; fm < FM; ++fm) acc[fn][fm] = mfma_f8<FB, FA>(bfr[fn], af[fm], acc[fn][fm]);
-    }
-  };
-
-#pragma unroll
-  for (int s = 0; s < NS - 1; ++s)
-    if (s < nk)
-      dma_stage<BM, A_SEGS / NW, B_SEGS / NW>(smem8 + (s % NS) * STAGE, a_src, b_src,
-                                               kbeg + s * kBKb, wave);
-  for (int64_t t = 0; t < nk; ++t) {
-    // slice t has landed once at most the later slices' loads are pending
-    if (t + NS - 2 < nk) {
-      RPX_WAIT_VMCNT(LPW * (NS - 2));
-    } else {
-      RPX_WAIT_VMCNT(0);
-    }
-    __builtin_amdgcn_s_barrier();
-    if (t + NS - 1 < nk)  // refills the stage read at t - 1
-      dma_stage<BM, A_SEGS / NW, B_SEGS / NW>(smem8 + ((t + NS - 1) % NS) * STAGE, a_src, b_src,
-                                               kbeg + (t + NS - 1) * kBKb, wave);
-    compute(t);
-  }
-
-  const float sa = s_a[0];
-  const float sb = s_b[0];
-  float* part = partials != nullptr ? partials + static_cast<int64_t>(split) * M * N : nullptr;
-#pragma unroll
-  for (int fn = 0; fn < FN; ++fn) {
-#pragma unroll
-    for (int fm = 0; fm < FM; ++fm) {
-      const int64_t m = m0 + wm * TM + fm * 32 + (lane & 31);
-      if (m >= M) continue;
-#pragma unroll
-      for (int vg = 0; vg < 4; ++vg) {
-        const int64_t nb = n0 + wn * TN + fn * 32 + 8 * vg + 4 * (lane >> 5);
-        float y[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) y[e] = acc[fn][fm][4 * vg + e];
-        if (part != nullptr) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (nb + e < N) part[m * N + nb + e] = y[e];
-          continue;
-        }
-#pragma unroll
-        for (int e = 0; e < 4; ++e) y[e] = (y[e] * sa) * sb;
-        if (out_dtype == kBF16) {
-          uint16_t* dst = static_cast<uint16_t*>(out) + m * ldc + nb;
-          if (nb + 3 < N && (ldc % 4 == 0)) {
-            *reinterpret_cast<u32x2_t*>(dst) =
-                u32x2_t{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])};
-          } else {
-            for (int e = 0; e < 4; ++e)
-              if (nb + e < N) dst[e] = f32_to_bf16(y[e]);
-          }
-        } else {
-          float* dst = static_cast<float*>(out) + m * ldc + nb;
-          for (int e = 0; e < 4; ++e)
-            if (nb + e < N) dst[e] = y[e];
-        }
-      }
-    }
-  }
-}
-
-__global__ void __launch_bounds__(256)
-    k_fp8_split_reduce(const float* __restrict__ partials, int64_t splits, int64_t M, int64_t N,
-                       const float* __restrict__ s_a, const float* __restrict__ s_b,
-                       void* __restrict__ out, int out_dtype, int64_t ldc) {
-  const float sa = s_a[0];
-  const float sb = s_b[0];
-  const int64_t count = M * N;
-  for (int64_t e = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; e < count;
-       e += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    float s = 0.0f;
-    for (int64_t i = 0; i < splits; ++i) s += partials[i * count + e];
-    s = (s * sa) * sb;
-    const int64_t m = e / N;
-    const int64_t n = e % N;
-    if (out_dtype == kBF16)
-      static_cast<uint16_t*>(out)[m * ldc + n] = f32_to_bf16(s);
-    else
-      static_cast<float*>(out)[m * ldc + n] = s;
-  }
-}
-
-struct Fp8Plan {
-  int cfg;  // 1: 256x128 (2x2), 2: 128x128 (2x2), 3: 256x256 (2x2), 4: 256x96 (4x1)
-  int bm, bn;
-  int64_t splits, k_per_split;
-};
-
-int fp8_tile_override() {
-  static int cached = -1;
-  if (cached < 0) {
-    const char* env = std::getenv("RPX_FP8_TILE");
-    cached = 0;
-    if (env != nullptr) {
-      if (std::strcmp(env, "256x128") == 0) cached = 1;
-      if (std::strcmp(env, "128x128") == 0) cached = 2;
-      if (std::strcmp(env, "256x256") == 0) cached = 3;
-      if (std::strcmp(env, "256x96") == 0) cached = 4;
-    }
-  }
-  return cached;
-}
-
-Fp8Plan plan_fp8(int64_t m, int64_t n, int64_t k) {
-  static const int kBM[5] = {0, 256, 128, 256, 256};
-  static const int kBN[5] = {0, 128, 128, 256, 96};
-  Fp8Plan p;
-  p.cfg = fp8_tile_override();
-  if (p.cfg == 0) {
-    // biggest tile that still gives one tile per CU, else 128x128 + split-K
-    if (ceil_div(m, 256) * ceil_div(n, 256) >= 256)
-      p.cfg = 3;
-    else if (ceil_div(m, 256) * ceil_div(n, 128) >= 256)
-      p.cfg = 1;
-    else if (n % 96 == 0 && ceil_div(m, 256) * (n / 96) >= 256)
-      p.cfg = 4;
-    else
-      p.cfg = 2;
-  }
-  p.bm = kBM[p.cfg];
-  p.bn = kBN[p.cfg];
-  const int64_t tiles = ceil_div(m, p.bm) * ceil_div(n, p.bn);
-  const int64_t kslices = k / kBKb;
-  int64_t s = 1;
-  while (tiles * s < 256 && s * 2 <= kslices && s < 16) s *= 2;
-  p.k_per_split = ceil_div(kslices, s) * kBKb;
-  p.splits = ceil_div(k, p.k_per_split);
-  return p;
-}
-
-template <int BM, int BN, int WM, int WN, int FA, int FB>
-hipError_t run_fp8(const uint8_t* a, const uint8_t* b, int64_t m, int64_t n, int64_t k,
-                   const Fp8Plan& plan, const float* s_a, const float* s_b, void* out,
-                   int out_dtype, int64_t ldc, float* partials, hipStream_t stream) {
-  // as many stages as fit in 160 KB of LDS (at most 4)
-  constexpr int kStage = (BM + BN) * kBKb;
-  constexpr int NS = (160 * 1024 / kStage) >= 4 ? 4 : (160 * 1024 / kStage);
-  static_assert(NS >= 2, "tile too large for LDS");
-  const int tiles_m = static_cast<int>(ceil_div(m, BM));
-  const int tiles_n = static_cast<int>(ceil_div(n, BN));
-  const size_t lds = static_cast<size_t>(NS) * kStage;
-  auto kern = k_fp8_gemm<BM, BN, WM, WN, NS, FA, FB>;
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       static_cast<int>(lds));
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
-  const unsigned blocks = static_cast<unsigned>(tiles_m) * tiles_n * plan.splits;
-  hipLaunchKernelGGL(kern, dim3(blocks), dim3(64 * WM * WN), lds, stream, a, b, m, n, k,
-                     plan.k_per_split, s_a, s_b, out, out_dtype, ldc,
-                     plan.splits > 1 ? partials : nullptr, tiles_m, tiles_n);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess || plan.splits == 1) return e;
-  int64_t g = ceil_div(m * n, 256);
-  if (g > 8192) g = 8192;
-  hipLaunchKernelGGL(k_fp8_split_reduce, dim3(static_cast<unsigned>(g)), dim3(256), 0, stream,
-                     partials, plan.splits, m, n, s_a, s_b, out, out_dtype, ldc);
-  return hipGetLastError();
-}
-
-template <int FA, int FB>
-hipError_t dispatch_fp8(const uint8_t* a, const uint8_t* b, int64_t m, int64_t n, int64_t k,
-                        const float* s_a, const float* s_b, void* out, int out_dtype, int64_t ldc,
-                        float* partials, hipStream_t stream) {
-  const Fp8Plan plan = plan_fp8(m, n, k);
-  switch (plan.cfg) {
-    case 1:
-      return run_fp8<256, 128, 2, 2, FA, FB>(a, b, m, n, k, plan, s_a, s_b, out, out_dtype, ldc,
-                                             partials, stream);
-    case 3:
-      return run_fp8<256, 256, 2, 2, FA, FB>(a, b, m, n, k, plan, s_a, s_b, out, out_dtype, ldc,
-                                             partials, stream);
-    case 4:
-      return run_fp8<256, 96, 4, 1, FA, FB>(a, b, m, n, k, plan, s_a, s_b, out, out_dtype, ldc,
-                                            partials, stream);
-    default:
-      return run_fp8<128, 128, 2, 2, FA, FB>(a, b, m, n, k, plan, s_a, s_b, out, out_dtype, ldc,
-                                             partials, stream);
-  }
-}
-
 }  // namespace
 
 int64_t fp8_amax_partials(int64_t numel) {
@@ -711,27 +387,6 @@ hipError_t launch_fp8_encode_selfcheck(int fmt, uint64_t first, uint64_t count, 
   hipLaunchKernelGGL(k_fp8_encode_selfcheck, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
                      stream, fmt, first, count, counts, firsts);
   return hipGetLastError();
-}
-
-int64_t fp8_gemm_workspace_floats(int64_t m, int64_t n, int64_t k) {
-  const Fp8Plan p = plan_fp8(m, n, k);
-  return p.splits > 1 ? p.splits * m * n : 0;
-}
-
-hipError_t launch_fp8_gemm(const uint8_t* a, int fmt_a, const float* s_a, const uint8_t* b,
-                           int fmt_b, const float* s_b, int64_t m, int64_t n, int64_t k,
-                           void* out, int out_dtype, int64_t ldc, float* split_ws,
-                           int64_t split_ws_floats, hipStream_t stream) {
-  if (m == 0 || n == 0) return hipSuccess;
-  if (split_ws_floats < fp8_gemm_workspace_floats(m, n, k)) return hipErrorInvalidValue;
-  // MFMA format codes: 0 = fp8 (e4m3), 1 = bf8 (e5m2)
-  if (fmt_a == kE4M3FN && fmt_b == kE4M3FN)
-    return dispatch_fp8<0, 0>(a, b, m, n, k, s_a, s_b, out, out_dtype, ldc, split_ws, stream);
-  if (fmt_a == kE5M2 && fmt_b == kE4M3FN)
-    return dispatch_fp8<1, 0>(a, b, m, n, k, s_a, s_b, out, out_dtype, ldc, split_ws, stream);
-  if (fmt_a == kE4M3FN && fmt_b == kE5M2)
-    return dispatch_fp8<0, 1>(a, b, m, n, k, s_a, s_b, out, out_dtype, ldc, split_ws, stream);
-  return dispatch_fp8<1, 1>(a, b, m, n, k, s_a, s_b, out, out_dtype, ldc, split_ws, stream);
 }
 
 }  // namespace rpx

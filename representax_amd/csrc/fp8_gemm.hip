@@ -1,0 +1,549 @@
+// fp8 "NT" GEMM for gfx950: out[m, n] = ((sum_k A[m, k] * B[n, k]) * s_a) * s_b
+// with A [M, K] and B [N, K] row-major fp8 codes (e4m3fn or e5m2 each), fp32
+// accumulation on the 32x32x64 f8f6f4 MFMA, bf16 (round-to-nearest-even) or
+// fp32 output. This is the dot_general + rescale of _scaled_fp8_dot
+// (representax/precision.py:154-170): the scaling is applied after the
+// fp32 dot as (acc * s_a) * s_b, in that order.
+#include <cstdlib>
+#include <cstring>
+
+#include "common.h"
+#include "kernels.h"
+
+namespace rpx {
+namespace {
+
+constexpr int kBK = 128;  // k bytes (= fp8 elements) per pipeline slice
+
+template <int FA, int FB>
+__device__ __forceinline__ f32x16_t mfma_f8(i32x8_t a, i32x8_t b, f32x16_t c) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, FA, FB, 0, 0, 0, 0);
+}
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// LDS rows are 128 bytes (eight 16-byte chunks), unpadded. Chunk c of row r
+// lives at physical chunk c ^ swz(r). A ds_read_b128 fragment read has every
+// lane of a 16-lane group on a different row of the same logical chunk; with
+// this swizzle those 16 reads hit 16 distinct 16-byte bank groups of a
+// 256-byte LDS cycle, and any 8 consecutive rows hit 8 distinct chunks.
+__device__ __forceinline__ int swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
+
+// Waits until at most n of this wave's vector-memory operations are pending
+// and every LDS operation has returned, then joins the workgroup barrier. The
+// memory clobber keeps LDS reads of the next slice below the barrier.
+template <int N>
+__device__ __forceinline__ void wait_sync() {
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+// Direct-to-LDS loads of one K-slice: this wave's LPW segments (1 KB: 8 rows
+// x 128 bytes each; lane l writes bytes [16 l, 16 l + 16) of its segment).
+template <int LPW, int NW>
+__device__ __forceinline__ void dma_slice(uint8_t* stage, const uint8_t* const* src, int64_t koff,
+                                          int wave) {
+#pragma unroll
+  for (int i = 0; i < LPW; ++i)
+    __builtin_amdgcn_global_load_lds(
+        src[i] + koff,
+        reinterpret_cast<lds_void_t*>(reinterpret_cast<uintptr_t>(stage) + (wave + i * NW) * 1024),
+        16, 0, 0);
+}
+
+// Fragment of the 32x32x64 MFMA: lane l holds row (l & 31) of a 32-row block,
+// k bytes [32 (l >> 5), +32) of the 64-deep step kk.
+__device__ __forceinline__ i32x8_t load_frag(const uint8_t* stage, int row, int kk, int half) {
+  const int c0 = 4 * kk + 2 * half;
+  const int s = swz(row);
+  const uint8_t* r = stage + row * kBK;
+  const u32x4_t lo = *reinterpret_cast<const u32x4_t*>(r + ((c0 ^ s) << 4));
+  const u32x4_t hi = *reinterpret_cast<const u32x4_t*>(r + (((c0 + 1) ^ s) << 4));
+  return i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3],
+                 (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+}
+
+// Pipelined fp8 GEMM. A workgroup of WM x WN waves computes a BM x BN tile
+// (each wave a (BM/WM) x (BN/WN) sub-tile of 32x32 MFMA blocks) over the
+// K-range of its split. K-slices of 128 bytes of A and B move global -> LDS
+// with direct-to-LDS loads into NS rotating stages, NS - 1 slices ahead of
+// the one being multiplied. Per slice each wave issues the MFMAs of the first
+// 64-deep step, reads the fragments of the second while they run, issues
+// those, then waits for the next slice and the barrier while the MFMA pipe is
+// still busy. bf16 results go through LDS so each global store writes whole
+// 128-byte row segments; fp32 results and split-K partials are stored from
+// registers (16 bytes per lane).
+// One 16-byte-per-lane direct-to-LDS load: segment `seg` (1 KB) of a stage.
+__device__ __forceinline__ void dma_seg(uint8_t* stage, const uint8_t* src, int64_t koff, int seg) {
+  __builtin_amdgcn_global_load_lds(
+      src + koff, reinterpret_cast<lds_void_t*>(reinterpret_cast<uintptr_t>(stage) + seg * 1024), 16,
+      0, 0);
+}
+
+template <int BM, int BN, int WM, int WN, int NS, int WPE, int FA, int FB>
+__global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
+    k_fp8_gemm(const uint8_t* __restrict__ A, const uint8_t* __restrict__ B, int64_t M, int64_t N,
+               int64_t K, int64_t k_per_split, const float* __restrict__ s_a,
+               const float* __restrict__ s_b, void* __restrict__ out, int out_dtype, int64_t ldc,
+               float* __restrict__ partials, int tiles_m, int tiles_n) {
+  constexpr int NW = WM * WN;
+  constexpr int TM = BM / WM;
+  constexpr int TN = BN / WN;
+  constexpr int FM = TM / 32;
+  constexpr int FN = TN / 32;
+  static_assert(TM % 32 == 0 && TN % 32 == 0, "wave tile must be made of 32x32 blocks");
+  constexpr int A_SEGS = BM / 8;
+  constexpr int SEGS = (BM + BN) / 8;
+  static_assert(SEGS % NW == 0, "DMA segments must split evenly over the waves");
+  constexpr int LPW = SEGS / NW;
+  static_assert(NS >= 2 && NS <= 4 && LPW * (NS - 1) < 64, "vmcnt range");
+  constexpr int STAGE = (BM + BN) * kBK;
+  extern __shared__ __align__(16) uint8_t smem[];
+
+  // the scales are needed only by the epilogue; their load is issued first so
+  // its latency hides under the main loop
+  const float sa = s_a[0];
+  const float sb = s_b[0];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave % WM;
+  const int wn = wave / WM;
+
+  // Tiles (n fastest) are dealt to the 8 XCDs in contiguous ranges so each
+  // XCD's L2 holds a few A row-blocks; split-K slices are outermost.
+  const int tiles = tiles_m * tiles_n;
+  const int total = static_cast<int>(gridDim.x);
+  int b = blockIdx.x;
+  if (total % 8 == 0) b = (blockIdx.x % 8) * (total / 8) + blockIdx.x / 8;
+  const int split = b / tiles;
+  const int tile = b % tiles;
+  const int64_t m0 = static_cast<int64_t>(tile / tiles_n) * BM;
+  const int64_t n0 = static_cast<int64_t>(tile % tiles_n) * BN;
+  const int64_t kbeg = static_cast<int64_t>(split) * k_per_split;
+  int64_t kend = kbeg + k_per_split;
+  if (kend > K) kend = K;
+  const int nk = static_cast<int>((kend - kbeg) / kBK);
+
+  // Per-lane DMA sources: segment j = wave + i * NW covers tile rows 8j..8j+7
+  // of A (j < A_SEGS) or of B; rows past the edge re-read the last row.
+  const int seg_row = lane >> 3;
+  const uint8_t* src[LPW];
+#pragma unroll
+  for (int i = 0; i < LPW; ++i) {
+    const int j = wave + i * NW;
+    const bool is_a = j < A_SEGS;
+    const int trow = (is_a ? 8 * j : 8 * (j - A_SEGS)) + seg_row;
+    int64_t r = (is_a ? m0 : n0) + trow;
+    const int64_t lim = is_a ? M : N;
+    r = r < lim ? r : lim - 1;
+    src[i] = (is_a ? A : B) + r * K + kbeg + (((lane & 7) ^ swz(trow)) << 4);
+  }
+
+  f32x16_t acc[FN][FM];
+#pragma unroll
+  for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[fn][fm][v] = 0.0f;
+
+  const int frow = lane & 31;
+  const int half = lane >> 5;
+  i32x8_t a_cur[FM], b_cur[FN], a_nxt[FM], b_nxt[FN];
+  auto load_all = [&](const uint8_t* st, int kk, i32x8_t* af, i32x8_t* bf) {
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm) af[fm] = load_frag(st, wm * TM + fm * 32 + frow, kk, half);
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn)
+      bf[fn] = load_frag(st + BM * kBK, wn * TN + fn * 32 + frow, kk, half);
+  };
+  // Main loop, branch-free. Slice t lives in stage t % NS. Per slice:
+  //   A: MFMAs of 64-deep step 0, each followed by DS reads of step 1's
+  //      fragments
+  //   barrier: step-1 fragments in registers, slice t + 1 landed (its DMA was
+  //            issued NS - 1 slices ago); every wave is done with stage t
+  //   B: MFMAs of step 1, each followed by part of the DMA of slice t + NS
+  //      into stage t and of the DS reads of slice t + 1's step-0 fragments
+  // The fixed order (sched_barrier fences) keeps the DMA and LDS traffic
+  // under the MFMAs and the barrier wait under the queued step-0 MFMAs.
+  // Refills past the last slice re-read slice nk - 1 into a stage nothing
+  // reads again, which keeps the vmcnt accounting constant (LPW per slice).
+  constexpr int NMF = FM * FN;
+  constexpr int NFR = FM + FN;
+  auto mma_one = [&](int i, const i32x8_t* af, const i32x8_t* bf) {
+    acc[i / FM][i % FM] = mfma_f8<FB, FA>(bf[i / FM], af[i % FM], acc[i / FM][i % FM]);
+  };
+  auto frag_one = [&](const uint8_t* st, int kk, int j, i32x8_t* af, i32x8_t* bf) {
+    if (j < FM)
+      af[j] = load_frag(st, wm * TM + j * 32 + frow, kk, half);
+    else
+      bf[j - FM] = load_frag(st + BM * kBK, wn * TN + (j - FM) * 32 + frow, kk, half);
+  };
+#pragma unroll
+  for (int s = 0; s < NS; ++s)
+    dma_slice<LPW, NW>(smem + s * STAGE, src, static_cast<int64_t>(s < nk ? s : nk - 1) * kBK,
+                       wave);
+  wait_sync<(NS - 1) * LPW>();
+  load_all(smem, 0, a_cur, b_cur);
+  int stage = 0;
+  for (int t = 0; t < nk; ++t) {
+    const int next = stage + 1 == NS ? 0 : stage + 1;
+    const uint8_t* st = smem + stage * STAGE;
+#pragma unroll
+    for (int i = 0; i < NMF; ++i) {
+      mma_one(i, a_cur, b_cur);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int j = i * NFR / NMF; j < (i + 1) * NFR / NMF; ++j) frag_one(st, 1, j, a_nxt, b_nxt);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    wait_sync<(NS - 2) * LPW>();
+    const int64_t refill = static_cast<int64_t>(t + NS < nk ? t + NS : nk - 1) * kBK;
+    uint8_t* fill = smem + stage * STAGE;
+    const uint8_t* nst = smem + next * STAGE;
+#pragma unroll
+    for (int i = 0; i < NMF; ++i) {
+      mma_one(i, a_nxt, b_nxt);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int d = i * LPW / NMF; d < (i + 1) * LPW / NMF; ++d)
+        dma_seg(fill, src[d], refill, wave + d * NW);
+#pragma unroll
+      for (int j = i * NFR / NMF; j < (i + 1) * NFR / NMF; ++j) frag_one(nst, 0, j, a_cur, b_cur);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    stage = next;
+  }
+  // no LDS DMA may still be in flight when the waves go on to the epilogue
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  const int64_t mw = m0 + wm * TM;  // first row of this wave's sub-tile
+  const int64_t nw = n0 + wn * TN;  // first column
+  // D layout (src0 = B fragment): lane holds row m = lane & 31 of the block
+  // and columns 8 vg + 4 half + e, e = 0..3, in acc[..][4 vg + e].
+  if (partials != nullptr) {
+    // Split-K partial tile in fragment order: for each (wave, fn, fm, vg)
+    // the 64 lanes store 64 consecutive 16-byte chunks, so every store
+    // instruction writes one contiguous kilobyte.
+    f32x4_t* dst = reinterpret_cast<f32x4_t*>(
+        partials + (static_cast<int64_t>(split) * tiles + tile) * (BM * BN));
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+        for (int vg = 0; vg < 4; ++vg) {
+          const f32x16_t& a = acc[fn][fm];
+          dst[(((wave * FN + fn) * FM + fm) * 4 + vg) * 64 + lane] =
+              f32x4_t{a[4 * vg], a[4 * vg + 1], a[4 * vg + 2], a[4 * vg + 3]};
+        }
+    return;
+  }
+  if (out_dtype != kBF16) {
+    float* o = static_cast<float*>(out);
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm) {
+      const int64_t m = mw + fm * 32 + frow;
+      if (m >= M) continue;
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn) {
+#pragma unroll
+        for (int vg = 0; vg < 4; ++vg) {
+          const int64_t nb = nw + fn * 32 + 8 * vg + 4 * half;
+          float y[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) y[e] = (acc[fn][fm][4 * vg + e] * sa) * sb;
+          float* d = o + m * ldc + nb;
+          if (nb + 3 < N && (ldc & 3) == 0) {
+            *reinterpret_cast<f32x4_t*>(d) = f32x4_t{y[0], y[1], y[2], y[3]};
+          } else {
+            for (int e = 0; e < 4; ++e)
+              if (nb + e < N) d[e] = y[e];
+          }
+        }
+      }
+    }
+    return;
+  }
+
+  // bf16: stage this wave's sub-tile in LDS (row pitch TN*2 + 16 bytes), then
+  // write whole row segments.
+  constexpr int P = TN * 2 + 16;
+  wait_sync<0>();  // every wave is done reading the pipeline stages
+  uint8_t* reg = smem + wave * (TM * P);
+#pragma unroll
+  for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+      for (int vg = 0; vg < 4; ++vg) {
+        const int ml = fm * 32 + frow;
+        const int nl = fn * 32 + 8 * vg + 4 * half;
+        const f32x16_t& a = acc[fn][fm];
+        *reinterpret_cast<u32x2_t*>(reg + ml * P + nl * 2) =
+            u32x2_t{pack_bf16x2((a[4 * vg] * sa) * sb, (a[4 * vg + 1] * sa) * sb),
+                    pack_bf16x2((a[4 * vg + 2] * sa) * sb, (a[4 * vg + 3] * sa) * sb)};
+      }
+  constexpr int CPR = TN / 8;  // 16-byte chunks per row
+  constexpr int ITS = TM * CPR / 64;
+  uint16_t* o = static_cast<uint16_t*>(out);
+  const bool vec_ok = (ldc & 7) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0;
+  if (vec_ok && mw + TM <= M && nw + TN <= N) {
+    // interior sub-tile: all LDS reads, then all 16-byte stores
+    u32x4_t v[ITS];
+#pragma unroll
+    for (int it = 0; it < ITS; ++it) {
+      const int idx = it * 64 + lane;
+      v[it] = *reinterpret_cast<const u32x4_t*>(reg + (idx / CPR) * P + (idx % CPR) * 16);
+    }
+#pragma unroll
+    for (int it = 0; it < ITS; ++it) {
+      const int idx = it * 64 + lane;
+      *reinterpret_cast<u32x4_t*>(o + (mw + idx / CPR) * ldc + nw + 8 * (idx % CPR)) = v[it];
+    }
+    return;
+  }
+  for (int it = 0; it < ITS; ++it) {
+    const int idx = it * 64 + lane;
+    const int r = idx / CPR;
+    const int c = idx % CPR;
+    const u32x4_t v = *reinterpret_cast<const u32x4_t*>(reg + r * P + c * 16);
+    const int64_t m = mw + r;
+    const int64_t n = nw + 8 * c;
+    if (m >= M) continue;
+    uint16_t* d = o + m * ldc + n;
+    if (vec_ok && n + 7 < N) {
+      *reinterpret_cast<u32x4_t*>(d) = v;
+    } else {
+      for (int e = 0; e < 8; ++e)
+        if (n + e < N) d[e] = static_cast<uint16_t>((v[e >> 1] >> (16 * (e & 1))) & 0xFFFFu);
+    }
+  }
+}
+
+// Sums the split-K partial tiles written by k_fp8_gemm<BM, BN, WM, WN, ...>
+// in split order, scales as (acc * s_a) * s_b and writes bf16 or fp32. One
+// thread per 16-byte chunk of the fragment-ordered tile: consecutive threads
+// read consecutive chunks of every split.
+template <int BM, int BN, int WM, int WN>
+__global__ void __launch_bounds__(256)
+    k_fp8_split_reduce(const float* __restrict__ partials, int splits, int64_t M, int64_t N,
+                       int tiles_n, int64_t tiles, const float* __restrict__ s_a,
+                       const float* __restrict__ s_b, void* __restrict__ out, int out_dtype,
+                       int64_t ldc) {
+  constexpr int TM = BM / WM;
+  constexpr int TN = BN / WN;
+  constexpr int FM = TM / 32;
+  constexpr int FN = TN / 32;
+  constexpr int CHUNKS = BM * BN / 4;  // per tile
+  const float sa = s_a[0];
+  const float sb = s_b[0];
+  const int64_t total = tiles * CHUNKS;
+  const int64_t split_stride = tiles * (BM * BN / 4);
+  const f32x4_t* p = reinterpret_cast<const f32x4_t*>(partials);
+  for (int64_t q = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; q < total;
+       q += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    f32x4_t s = p[q];
+    for (int i = 1; i < splits; ++i) s += p[i * split_stride + q];
+    const int64_t tile = q / CHUNKS;
+    int r = static_cast<int>(q % CHUNKS);
+    const int lane = r & 63;
+    r >>= 6;
+    const int vg = r & 3;
+    r >>= 2;
+    const int fm = r % FM;
+    r /= FM;
+    const int fn = r % FN;
+    const int wave = r / FN;
+    const int64_t m = (tile / tiles_n) * BM + (wave % WM) * TM + fm * 32 + (lane & 31);
+    const int64_t n = (tile % tiles_n) * BN + (wave / WM) * TN + fn * 32 + 8 * vg + 4 * (lane >> 5);
+    if (m >= M) continue;
+    float y[4];
+    for (int e = 0; e < 4; ++e) y[e] = (s[e] * sa) * sb;
+    if (out_dtype == kBF16) {
+      uint16_t* d = static_cast<uint16_t*>(out) + m * ldc + n;
+      if (n + 3 < N && (ldc & 3) == 0) {
+        *reinterpret_cast<u32x2_t*>(d) = u32x2_t{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])};
+      } else {
+        for (int e = 0; e < 4; ++e)
+          if (n + e < N) d[e] = f32_to_bf16(y[e]);
+      }
+    } else {
+      float* d = static_cast<float*>(out) + m * ldc + n;
+      for (int e = 0; e < 4; ++e)
+        if (n + e < N) d[e] = y[e];
+    }
+  }
+}
+
+// Tile configurations: id, BM, BN, waves along M, waves along N, pipeline
+// stages, waves per SIMD the registers are budgeted for.
+#define RPX_FP8_CONFIGS(X)     \
+  X(1, 128, 128, 2, 2, 2, 2)   \
+  X(2, 256, 128, 4, 2, 2, 2)   \
+  X(3, 256, 192, 4, 2, 2, 2)   \
+  X(4, 128, 192, 2, 2, 2, 2)   \
+  X(5, 256, 256, 4, 2, 2, 2)   \
+  X(6, 128, 128, 2, 2, 4, 1)   \
+  X(7, 128, 192, 2, 2, 3, 1)   \
+  X(8, 256, 96, 4, 1, 3, 1)    \
+  X(9, 128, 128, 2, 2, 3, 2)   \
+  X(10, 256, 128, 2, 2, 3, 1)
+
+constexpr int fp8_lds_bytes(int bm, int bn, int wm, int wn, int ns) {
+  return ns * (bm + bn) * kBK > wm * wn * (bm / wm) * ((bn / wn) * 2 + 16)
+             ? ns * (bm + bn) * kBK
+             : wm * wn * (bm / wm) * ((bn / wn) * 2 + 16);
+}
+constexpr int fp8_blocks_per_cu(int bm, int bn, int wm, int wn, int ns, int wpe) {
+  return (160 * 1024 / fp8_lds_bytes(bm, bn, wm, wn, ns)) < (4 * wpe) / (wm * wn)
+             ? 160 * 1024 / fp8_lds_bytes(bm, bn, wm, wn, ns)
+             : (4 * wpe) / (wm * wn);
+}
+constexpr int kNumCfg = 11;
+#define RPX_CFG_BM(id, bm, bn, wm, wn, ns, wpe) bm,
+#define RPX_CFG_BN(id, bm, bn, wm, wn, ns, wpe) bn,
+#define RPX_CFG_SLOTS(id, bm, bn, wm, wn, ns, wpe) 256 * fp8_blocks_per_cu(bm, bn, wm, wn, ns, wpe),
+constexpr int kCfgBM[kNumCfg] = {0, RPX_FP8_CONFIGS(RPX_CFG_BM)};
+constexpr int kCfgBN[kNumCfg] = {0, RPX_FP8_CONFIGS(RPX_CFG_BN)};
+constexpr int kCfgSlots[kNumCfg] = {0, RPX_FP8_CONFIGS(RPX_CFG_SLOTS)};
+
+struct Fp8Plan {
+  int cfg;
+  int64_t splits, k_per_split;
+};
+
+int fp8_tile_override() {
+  static int cached = -1;
+  if (cached < 0) {
+    const char* env = std::getenv("RPX_FP8_TILE");
+    cached = 0;
+    if (env != nullptr) cached = std::atoi(env);
+    if (cached < 0 || cached >= kNumCfg) cached = 0;
+  }
+  return cached;
+}
+
+// Estimated cycles of a plan on 256 CUs. Per round of resident blocks a CU
+// runs `per_cu` blocks whose MFMA work (8192 fp8 flops per clock per CU) and
+// global->LDS fill (about 64 bytes per clock per CU when every CU of an XCD
+// streams from its L2) overlap, plus a fixed pipeline fill/drain. Split-K adds
+// the partial tiles' write and read-back at about 2 KB per clock chip-wide and
+// one more launch.
+double plan_cycles(int cfg, int64_t m, int64_t n, int64_t kslices, int64_t kps, int64_t splits) {
+  const double bm = kCfgBM[cfg], bn = kCfgBN[cfg];
+  const int64_t tiles = ceil_div(m, kCfgBM[cfg]) * ceil_div(n, kCfgBN[cfg]);
+  const int64_t blocks = tiles * splits;
+  const int64_t slots = kCfgSlots[cfg];
+  const double per_cu = static_cast<double>(slots) / 256.0;
+  const double rounds = static_cast<double>(ceil_div(blocks, slots));
+  // a last partial round only occupies the CUs it has blocks for
+  const double k = static_cast<double>(kps) * kBK;
+  const double mfma = per_cu * bm * bn * k * 2.0 / 8192.0;
+  const double fill = per_cu * (bm + bn) * k / 64.0;
+  const double round = (mfma > fill ? mfma : fill) + 2500.0;
+  double cyc = rounds * round;
+  if (splits > 1) cyc += static_cast<double>(splits + 1) * tiles * bm * bn * 4.0 / 2048.0 + 4000.0;
+  (void)kslices;
+  return cyc;
+}
+
+Fp8Plan plan_fp8(int64_t m, int64_t n, int64_t k) {
+  const int64_t kslices = k / kBK;
+  Fp8Plan best{1, 1, k};
+  double best_cost = -1.0;
+  const int forced = fp8_tile_override();
+  for (int cfg = 1; cfg < kNumCfg; ++cfg) {
+    if (forced != 0 && cfg != forced) continue;
+    if (forced == 0 && cfg > 5) continue;
+    const int64_t tiles = ceil_div(m, kCfgBM[cfg]) * ceil_div(n, kCfgBN[cfg]);
+    for (int64_t s = 1; s <= 32 && s <= kslices; ++s) {
+      if (s > 1 && tiles * s > 2 * kCfgSlots[cfg]) break;
+      const int64_t kps = ceil_div(kslices, s);
+      const int64_t splits = ceil_div(kslices, kps);
+      if (splits != s) continue;
+      const double cost = plan_cycles(cfg, m, n, kslices, kps, splits);
+      if (best_cost < 0.0 || cost < best_cost) {
+        best_cost = cost;
+        best = Fp8Plan{cfg, splits, kps * kBK};
+      }
+    }
+  }
+  return best;
+}
+
+template <int BM, int BN, int WM, int WN, int NS, int WPE, int FA, int FB>
+hipError_t run_fp8(const uint8_t* a, const uint8_t* b, int64_t m, int64_t n, int64_t k,
+                   const Fp8Plan& plan, const float* s_a, const float* s_b, void* out,
+                   int out_dtype, int64_t ldc, float* partials, hipStream_t stream) {
+  constexpr int kLds = fp8_lds_bytes(BM, BN, WM, WN, NS);
+  static_assert(kLds <= 160 * 1024, "LDS budget");
+  const int tiles_m = static_cast<int>(ceil_div(m, BM));
+  const int tiles_n = static_cast<int>(ceil_div(n, BN));
+  auto kern = k_fp8_gemm<BM, BN, WM, WN, NS, WPE, FA, FB>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  const unsigned blocks = static_cast<unsigned>(tiles_m) * tiles_n * plan.splits;
+  hipLaunchKernelGGL(kern, dim3(blocks), dim3(64 * WM * WN), kLds, stream, a, b, m, n, k,
+                     plan.k_per_split, s_a, s_b, out, out_dtype, ldc,
+                     plan.splits > 1 ? partials : nullptr, tiles_m, tiles_n);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || plan.splits == 1) return e;
+  const int64_t tiles = static_cast<int64_t>(tiles_m) * tiles_n;
+  int64_t g = ceil_div(tiles * (BM * BN / 4), 256);
+  if (g > 8192) g = 8192;
+  hipLaunchKernelGGL((k_fp8_split_reduce<BM, BN, WM, WN>), dim3(static_cast<unsigned>(g)), dim3(256),
+                     0, stream, partials, static_cast<int>(plan.splits), m, n, tiles_n, tiles, s_a,
+                     s_b, out, out_dtype, ldc);
+  return hipGetLastError();
+}
+
+template <int FA, int FB>
+hipError_t dispatch_fp8(const uint8_t* a, const uint8_t* b, int64_t m, int64_t n, int64_t k,
+                        const float* s_a, const float* s_b, void* out, int out_dtype, int64_t ldc,
+                        float* partials, hipStream_t stream) {
+  const Fp8Plan p = plan_fp8(m, n, k);
+  switch (p.cfg) {
+#define RPX_CFG_CASE(id, bm, bn, wm, wn, ns, wpe)                                                 \
+  case id:                                                                                        \
+    return run_fp8<bm, bn, wm, wn, ns, wpe, FA, FB>(a, b, m, n, k, p, s_a, s_b, out, out_dtype, \
+                                                    ldc, partials, stream);
+    RPX_FP8_CONFIGS(RPX_CFG_CASE)
+#undef RPX_CFG_CASE
+    default:
+      return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace
+
+int64_t fp8_gemm_workspace_floats(int64_t m, int64_t n, int64_t k) {
+  const Fp8Plan p = plan_fp8(m, n, k);
+  if (p.splits <= 1) return 0;
+  return p.splits * ceil_div(m, kCfgBM[p.cfg]) * ceil_div(n, kCfgBN[p.cfg]) * kCfgBM[p.cfg] *
+         kCfgBN[p.cfg];
+}
+
+hipError_t launch_fp8_gemm(const uint8_t* a, int fmt_a, const float* s_a, const uint8_t* b,
+                           int fmt_b, const float* s_b, int64_t m, int64_t n, int64_t k,
+                           void* out, int out_dtype, int64_t ldc, float* split_ws,
+                           int64_t split_ws_floats, hipStream_t stream) {
+  if (m == 0 || n == 0) return hipSuccess;
+  if (k % kBK != 0 || split_ws_floats < fp8_gemm_workspace_floats(m, n, k))
+    return hipErrorInvalidValue;
+  // MFMA format codes: 0 = fp8 (e4m3), 1 = bf8 (e5m2)
+  if (fmt_a == kE4M3FN && fmt_b == kE4M3FN)
+    return dispatch_fp8<0, 0>(a, b, m, n, k, s_a, s_b, out, out_dtype, ldc, split_ws, stream);
+  if (fmt_a == kE5M2 && fmt_b == kE4M3FN)
+    return dispatch_fp8<1, 0>(a, b, m, n, k, s_a, s_b, out, out_dtype, ldc, split_ws, stream);
+  if (fmt_a == kE4M3FN && fmt_b == kE5M2)
+    return dispatch_fp8<0, 1>(a, b, m, n, k, s_a, s_b, out, out_dtype, ldc, split_ws, stream);
+  return dispatch_fp8<1, 1>(a, b, m, n, k, s_a, s_b, out, out_dtype, ldc, split_ws, stream);
+}
+
+}  // namespace rpx

@@ -89,7 +89,8 @@ def test_scale_matches_oracle(fmt):
 @pytest.mark.parametrize(
     "m,n,k,fa,fb",
     [(256, 256, 256, E4M3FN, E4M3FN), (512, 384, 768, E5M2, E4M3FN),
-     (768, 3072, 1024, E4M3FN, E5M2), (100, 70, 200, E4M3FN, E4M3FN), (64, 96, 8192, E5M2, E5M2)],
+     (768, 3072, 1024, E4M3FN, E5M2), (100, 70, 200, E4M3FN, E4M3FN), (64, 96, 8192, E5M2, E5M2),
+     (1000, 770, 384, E4M3FN, E4M3FN), (300, 1000, 640, E5M2, E4M3FN)],
 )
 def test_fp8_gemm_matches_oracle(m, n, k, fa, fb):
     g = rng(m + n + k)
@@ -107,6 +108,28 @@ def test_fp8_gemm_matches_oracle(m, n, k, fa, fb):
     # products are exact; only the MFMA's float32 accumulation differs from the
     # float64 sum (codes span the whole fp8 range, so cancellation is heavy)
     assert rel_l2(from_dev(got), want) < 2e-4
+
+
+@pytest.mark.parametrize(
+    "m,n,k,fa",
+    [(8192, 768, 768, E4M3FN), (768, 768, 8192, E5M2), (1000, 770, 384, E4M3FN),
+     (130, 4100, 128, E5M2), (300, 1000, 640, E4M3FN), (8192, 3072, 768, E4M3FN)],
+)
+def test_fp8_gemm_bf16_output_is_rounded_f32_output(m, n, k, fa):
+    # the bf16 epilogue (staged through LDS, whole-row stores, edge tiles) must
+    # write exactly the round-to-nearest-even of what the fp32 epilogue writes
+    g = torch.Generator(device="cuda").manual_seed(m * 7 + n)
+    qa = torch.randint(0, 256, (m, k), dtype=torch.uint8, device="cuda", generator=g)
+    qb = torch.randint(0, 256, (n, k), dtype=torch.uint8, device="cuda", generator=g)
+    qa[(qa & 0x7F) >= 0x78] = 0x11  # finite codes in both formats
+    qb[(qb & 0x7F) >= 0x78] = 0x22
+    sa = torch.tensor([0.03], device="cuda")
+    sb = torch.tensor([0.5], device="cuda")
+    f32 = ops.fp8_gemm(qa, fa, sa, qb, E4M3FN, sb, out_dtype=torch.float32)
+    b16 = ops.fp8_gemm(qa, fa, sa, qb, E4M3FN, sb, out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    assert torch.isfinite(f32).all()
+    assert torch.equal(b16.view(torch.int16), f32.to(torch.bfloat16).view(torch.int16))
 
 
 def _fp8_case(m, k, n, seed):
