@@ -49,7 +49,7 @@ def parse_args():
     p.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a HIP graph")
     p.add_argument("--no-secondary", action="store_true")
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--only", choices=["fp8", "int4lora", "skinny"], default=None,
+    p.add_argument("--only", choices=["fp8", "int4lora", "skinny", "bert"], default=None,
                    help="run one workload and nothing else (profiling)")
     return p.parse_args()
 
@@ -353,6 +353,42 @@ def run_int4lora(steps, warmup, use_graph, group_size=None):
 SKINNY_SHAPES = [(2048, 6144), (6144, 2048), (2048, 2048)]
 
 
+def run_bert(steps=10, warmup=3):
+    """BERT-base encoder train step with every Q/K/V/O/FFN linear packed INT4
+    (group 64) + rank-16 LoRA (alpha 32): in-batch MNR loss over 64
+    query/document pairs x 256 tokens, bf16 compute, AdamW on the fp32 LoRA
+    masters, the whole step replayed as one HIP graph."""
+
+    import torch
+
+    from representax_amd.trainstep import BertConfig, MNRTrainStep, build_int4lora_encoder
+
+    cfg = BertConfig()
+    pairs, seq = 64, 256
+    model = build_int4lora_encoder(cfg, rank=16, alpha=32.0, group_size=64, seed=0,
+                                   device=torch.device("cuda:0"))
+    step = MNRTrainStep(model, batch=pairs, sequence=seq)
+    step.capture(warmup=2)
+    ms = time_region(step, steps, warmup)
+    loss = float(step.loss)
+    tokens = 2 * pairs * seq
+    flops = cfg.step_flops(2 * pairs, seq)
+    line = {
+        "workload": "BERT-base (12L, H768, 12 heads, FFN 3072, vocab 30522) train step, every "
+                    "Q/K/V/O/FFN linear INT4 group-64 + LoRA r16 a32, in-batch MNR loss (scale 20), "
+                    "64 query/document pairs x 256 tokens, bf16 compute, AdamW on fp32 LoRA "
+                    "masters, no recompute, HIP graph",
+        "value": round(tokens / (ms * 1e-3), 1), "unit": "tokens/s",
+        "ms_per_step": round(ms, 3), "tokens_per_step": tokens,
+        "matrix_tflops": round(flops / (ms * 1e-3) / 1e12, 1),
+        "matrix_tflop_per_step": round(flops / 1e12, 3),
+        "loss_after_timed_steps": round(loss, 4),
+    }
+    del step, model
+    torch.cuda.empty_cache()
+    return line
+
+
 def run_skinny(batch=96):
     """Per-call GPU latency of the skinny-M forward: a HIP graph of `batch`
     calls cycling through a pool of weight copies larger than the 256 MB
@@ -418,6 +454,9 @@ def main():
     if args.only == "skinny":
         print(json.dumps(run_skinny()))
         return
+    if args.only == "bert":
+        print(json.dumps(run_bert()))
+        return
 
     log("fp8: setting up inputs")
     layers = fp8_setup(args.tokens, dev)
@@ -458,6 +497,8 @@ def main():
                                run_int4lora(args.steps, args.warmup, use_graph, group_size=64)]
         log("skinny-M sweep")
         result["secondary"].append(run_skinny())
+        log("bert-base int4-lora train step")
+        result["secondary"].append(run_bert())
     if args.only is None and not args.no_cpu_baseline:
         log("cpu baseline (numpy oracle)")
         result["cpu_baseline"] = fp8_cpu_baseline()

@@ -1,0 +1,308 @@
+"""INT4-LoRA encoder train step: the harness around the quantized linear path.
+
+A BERT-base-shaped encoder whose every Q/K/V/O/FFN projection is a
+``QuantizedLoRALinear`` (the fused INT4-LoRA HIP kernels), trained with the
+in-batch multiple-negatives ranking (MNR) loss and AdamW on the fp32 LoRA
+masters only. It restates the reference's model and step:
+
+* embeddings (word + position + token type, LayerNorm) and post-LN layers
+  with a GELU MLP: src/representax/models/bert/model.py:74-330;
+* mean pooling over the attention mask and L2 normalisation:
+  src/representax/models/bert/model.py:566-574,
+  src/representax/models/components.py:238-270;
+* LayerNorm with float32 statistics: src/representax/models/components.py:110-132;
+* MNR loss (cosine logits times ``scale``, logsumexp over the in-batch
+  documents, forward direction): src/representax/tasks/retrieval/mnr.py:48-158;
+* adapters on every layer projection with only ``lora_a``/``lora_b``
+  trainable: src/representax/models/adapters.py:201-267.
+
+bf16 compute with fp32 masters follows the ``bfloat16_mixed`` policy
+(src/representax/precision.py:19-124). Dropout is off (probability 0, as in
+the reference's benchmark configuration). Attention runs as explicit batched
+products with contiguous right-hand operands (softmax in float32).
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+
+from .adapters import apply_quantized_lora, lora_parameters
+from .components import Linear
+from .config import PrecisionConfig
+from .precision import precision_context, resolve_precision_policy
+
+
+@dataclass(frozen=True)
+class BertConfig:
+    """Shape of the encoder (BERT-base defaults)."""
+
+    vocab_size: int = 30522
+    hidden_size: int = 768
+    num_hidden_layers: int = 12
+    num_attention_heads: int = 12
+    intermediate_size: int = 3072
+    max_position_embeddings: int = 512
+    type_vocab_size: int = 2
+    norm_epsilon: float = 1e-12
+    initializer_range: float = 0.02
+    pad_token_id: int = 0
+
+    @property
+    def head_dimension(self) -> int:
+        return self.hidden_size // self.num_attention_heads
+
+    def step_flops(self, batch: int, sequence: int, *, remat: bool = False) -> float:
+        """Matrix FLOPs of one train step over ``batch`` sequences (linears,
+        attention products; forward, optional recompute, backward)."""
+
+        h, f, s = self.hidden_size, self.intermediate_size, sequence
+        tokens = batch * sequence
+        linear = 2.0 * tokens * (4 * h * h + 2 * h * f)
+        attention = 4.0 * batch * s * s * h
+        forward = self.num_hidden_layers * (linear + attention)
+        # backward: dX through every linear and both attention products twice
+        backward = self.num_hidden_layers * (linear + 2 * attention)
+        return forward * (2 if remat else 1) + backward
+
+
+class LayerNorm(torch.nn.Module):
+    """Last-axis LayerNorm with float32 statistics, output in the input dtype."""
+
+    def __init__(self, size: int, eps: float, device=None) -> None:
+        super().__init__()
+        self.weight = torch.nn.Parameter(torch.ones(size, device=device))
+        self.bias = torch.nn.Parameter(torch.zeros(size, device=device))
+        self.eps = eps
+
+    def forward(self, value: torch.Tensor) -> torch.Tensor:
+        out = F.layer_norm(value.float(), value.shape[-1:], self.weight.float(),
+                           self.bias.float(), self.eps)
+        return out.to(value.dtype)
+
+
+class _Attention(torch.autograd.Function):
+    """softmax(Q K^T * scale + bias) V over ``[B, H, S, D]`` with every
+    batched product taking a contiguous right operand."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, bias, scale):
+        s = torch.matmul(q, k.transpose(-1, -2).contiguous()).float() * scale
+        if bias is not None:
+            s = s + bias
+        p = torch.softmax(s, dim=-1).to(q.dtype)
+        ctx.save_for_backward(q, k, v, p)
+        ctx.scale = scale
+        return torch.matmul(p, v)
+
+    @staticmethod
+    def backward(ctx, do):
+        q, k, v, p = ctx.saved_tensors
+        do = do.contiguous()
+        dv = torch.matmul(p.transpose(-1, -2).contiguous(), do)
+        dp = torch.matmul(do, v.transpose(-1, -2).contiguous()).float()
+        pf = p.float()
+        ds = (pf * (dp - (dp * pf).sum(-1, keepdim=True)) * ctx.scale).to(q.dtype)
+        dq = torch.matmul(ds, k)
+        dk = torch.matmul(ds.transpose(-1, -2).contiguous(), q)
+        return dq, dk, dv, None, None
+
+
+def attention(q, k, v, bias, scale):
+    return _Attention.apply(q, k, v, bias, scale)
+
+
+class BertSelfAttention(torch.nn.Module):
+    def __init__(self, config: BertConfig, key: int, device=None) -> None:
+        super().__init__()
+        arg = dict(scale=config.initializer_range, bias=True, device=device)
+        h = config.hidden_size
+        self.query = Linear.init(h, h, key=key + 0, **arg)
+        self.key = Linear.init(h, h, key=key + 1, **arg)
+        self.value = Linear.init(h, h, key=key + 2, **arg)
+        self.output = Linear.init(h, h, key=key + 3, **arg)
+        self.heads = config.num_attention_heads
+        self.head_dim = config.head_dimension
+
+    def forward(self, hidden: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor:
+        b, s, h = hidden.shape
+
+        def project(layer):
+            return layer(hidden).reshape(b, s, self.heads, self.head_dim).permute(0, 2, 1, 3).contiguous()
+
+        out = attention(project(self.query), project(self.key), project(self.value), bias,
+                        1.0 / math.sqrt(self.head_dim))
+        return self.output(out.permute(0, 2, 1, 3).reshape(b, s, h))
+
+
+class BertMLP(torch.nn.Module):
+    def __init__(self, config: BertConfig, key: int, device=None) -> None:
+        super().__init__()
+        arg = dict(scale=config.initializer_range, bias=True, device=device)
+        self.input = Linear.init(config.hidden_size, config.intermediate_size, key=key, **arg)
+        self.output = Linear.init(config.intermediate_size, config.hidden_size, key=key + 1, **arg)
+
+    def forward(self, hidden: torch.Tensor) -> torch.Tensor:
+        return self.output(F.gelu(self.input(hidden)))
+
+
+class BertLayer(torch.nn.Module):
+    def __init__(self, config: BertConfig, key: int, device=None) -> None:
+        super().__init__()
+        self.attention = BertSelfAttention(config, key, device)
+        self.attention_norm = LayerNorm(config.hidden_size, config.norm_epsilon, device)
+        self.mlp = BertMLP(config, key + 4, device)
+        self.output_norm = LayerNorm(config.hidden_size, config.norm_epsilon, device)
+
+    def forward(self, hidden: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor:
+        hidden = self.attention_norm(hidden + self.attention(hidden, bias))
+        return self.output_norm(hidden + self.mlp(hidden))
+
+
+class BertEncoder(torch.nn.Module):
+    """Embeddings, post-LN layers, masked mean pooling, L2 normalisation."""
+
+    def __init__(self, config: BertConfig, seed: int = 0, device=None) -> None:
+        super().__init__()
+        self.config = config
+        g = torch.Generator().manual_seed(seed)
+
+        def table(rows):
+            t = config.initializer_range * torch.randn(rows, config.hidden_size, generator=g)
+            return torch.nn.Parameter(t.to(device))
+
+        self.word = table(config.vocab_size)
+        with torch.no_grad():
+            self.word[config.pad_token_id].zero_()
+        self.position = table(config.max_position_embeddings)
+        self.token_type = table(config.type_vocab_size)
+        self.embedding_norm = LayerNorm(config.hidden_size, config.norm_epsilon, device)
+        self.layers = torch.nn.ModuleList(
+            BertLayer(config, seed * 1000 + 10 * (i + 1), device)
+            for i in range(config.num_hidden_layers))
+
+    def hidden_states(self, input_ids: torch.Tensor, attention_mask: torch.Tensor | None = None,
+                      compute_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+        """``attention_mask`` None means every position is a real token."""
+
+        s = input_ids.shape[1]
+        hidden = (self.word[input_ids] + self.position[:s][None]
+                  + self.token_type[torch.zeros_like(input_ids)])
+        hidden = self.embedding_norm(hidden).to(compute_dtype)
+        bias = None
+        if attention_mask is not None:
+            bias = torch.zeros(attention_mask.shape, dtype=torch.float32, device=hidden.device)
+            bias = bias.masked_fill(~attention_mask.bool(), float("-inf"))[:, None, None, :]
+        for layer in self.layers:
+            hidden = layer(hidden, bias)
+        return hidden
+
+    def encode(self, input_ids: torch.Tensor, attention_mask: torch.Tensor | None = None,
+               compute_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+        hidden = self.hidden_states(input_ids, attention_mask, compute_dtype).float()
+        if attention_mask is None:
+            pooled = hidden.mean(1)
+        else:
+            mask = attention_mask.to(hidden.dtype)[..., None]
+            pooled = (hidden * mask).sum(1) / mask.sum(1).clamp_min(1.0)
+        return pooled / pooled.norm(dim=-1, keepdim=True).clamp_min(1e-12)
+
+
+def mnr_loss(queries: torch.Tensor, documents: torch.Tensor, scale: float = 20.0) -> torch.Tensor:
+    """Mean over queries of ``logsumexp_j(scale cos(q, d_j)) - scale cos(q, d_q)``
+    with each query's own document as its positive."""
+
+    q = queries.float() / queries.float().norm(dim=-1, keepdim=True).clamp_min(1e-12)
+    d = documents.float() / documents.float().norm(dim=-1, keepdim=True).clamp_min(1e-12)
+    logits = (q @ d.t()) * scale
+    return (torch.logsumexp(logits, dim=1) - logits.diagonal()).mean()
+
+
+LAYER_LINEARS = r"\.layers\[\d+\]\.(attention\.(query|key|value|output)|mlp\.(input|output))$"
+
+
+def build_int4lora_encoder(config: BertConfig, *, rank: int = 16, alpha: float = 32.0,
+                           group_size: int | None = 64, seed: int = 0,
+                           device: torch.device | str = "cuda") -> BertEncoder:
+    """Random-init encoder with every layer projection packed INT4 plus a
+    rank-``rank`` adapter; every other parameter is frozen."""
+
+    model = BertEncoder(config, seed=seed, device=device)
+    model = apply_quantized_lora(model, rank=rank, alpha=alpha, key=seed,
+                                 target_pattern=LAYER_LINEARS, group_size=group_size,
+                                 inplace=True)
+    trainable = {id(p) for p in lora_parameters(model)}
+    for p in model.parameters():
+        p.requires_grad_(id(p) in trainable)
+    return model
+
+
+class MNRTrainStep:
+    """One AdamW step of the MNR loss on (query, document) token batches.
+
+    ``capture()`` records forward, backward and the optimizer update into one
+    HIP graph over static input buffers; ``__call__`` replays it (or runs
+    eagerly before capture).
+    """
+
+    def __init__(self, model: BertEncoder, *, batch: int, sequence: int, lr: float = 1e-4,
+                 scale: float = 20.0, seed: int = 6) -> None:
+        self.model = model
+        self.policy = resolve_precision_policy(PrecisionConfig.bfloat16_mixed())
+        device = next(model.parameters()).device
+        self.params = lora_parameters(model)
+        self.optimizer = torch.optim.AdamW(self.params, lr=lr, weight_decay=0.01,
+                                           capturable=True, foreach=True)
+        g = torch.Generator(device="cpu").manual_seed(seed)
+        vocab = model.config.vocab_size
+        self.query_ids = torch.randint(0, vocab, (batch, sequence), generator=g).to(device)
+        self.document_ids = torch.randint(0, vocab, (batch, sequence), generator=g).to(device)
+        self.scale = scale
+        self.loss = torch.zeros((), dtype=torch.float32, device=device)
+        self.graph = None
+
+    def _step(self) -> None:
+        self.optimizer.zero_grad(set_to_none=False)
+        with precision_context(self.policy):
+            ids = torch.cat([self.query_ids, self.document_ids], 0)
+            emb = self.model.encode(ids)
+            b = self.query_ids.shape[0]
+            loss = mnr_loss(emb[:b], emb[b:], self.scale)
+        loss.backward()
+        self.optimizer.step()
+        self.loss.copy_(loss.detach())
+
+    def capture(self, warmup: int = 2) -> None:
+        for p in self.params:
+            if p.grad is None:
+                p.grad = torch.zeros_like(p)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(warmup):
+                self._step()
+        torch.cuda.current_stream().wait_stream(side)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self._step()
+
+    def __call__(self) -> torch.Tensor:
+        if self.graph is None:
+            self._step()
+        else:
+            self.graph.replay()
+        return self.loss
+
+
+__all__ = [
+    "BertConfig",
+    "BertEncoder",
+    "LAYER_LINEARS",
+    "MNRTrainStep",
+    "attention",
+    "build_int4lora_encoder",
+    "mnr_loss",
+]

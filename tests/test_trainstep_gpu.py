@@ -1,0 +1,110 @@
+"""The INT4-LoRA encoder train step on the GPU: only the LoRA masters move,
+and the bf16 fused path agrees with a float32 torch restatement of the same
+model (tests/models/test_adapters.py:97-153 for the training invariants)."""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+from representax_amd import QuantizedLoRALinear, lora_parameters
+from representax_amd.trainstep import BertConfig, MNRTrainStep, build_int4lora_encoder, mnr_loss
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+TINY = BertConfig(vocab_size=512, hidden_size=128, num_hidden_layers=2, num_attention_heads=4,
+                  intermediate_size=256, max_position_embeddings=64)
+
+
+def _frozen_state(model):
+    state = {n: t.detach().clone() for n, t in model.named_buffers() if t is not None}
+    state.update({n: p.detach().clone() for n, p in model.named_parameters() if not p.requires_grad})
+    return state
+
+
+def test_train_step_moves_only_lora_masters():
+    model = build_int4lora_encoder(TINY, rank=4, alpha=8.0, group_size=64, seed=3, device=DEV)
+    frozen = _frozen_state(model)
+    lora = {id(p) for p in lora_parameters(model)}
+    assert len(lora) == 2 * 6 * TINY.num_hidden_layers
+    assert all(p.requires_grad == (id(p) in lora) for p in model.parameters())
+    before = [p.detach().clone() for p in lora_parameters(model)]
+    step = MNRTrainStep(model, batch=8, sequence=32, lr=1e-2)
+    losses = [float(step()) for _ in range(3)]
+    torch.cuda.synchronize()
+    assert all(math.isfinite(v) for v in losses)
+    after = lora_parameters(model)
+    assert all(not torch.equal(b, a.detach()) for b, a in zip(before, after))
+    for name, value in _frozen_state(model).items():
+        assert torch.equal(value, frozen[name]), name
+    # optimizer state exists only for the adapter masters
+    assert {id(p) for p in step.optimizer.state} == lora
+    assert all(p.dtype == torch.float32 for p in after)
+
+
+def test_graph_replay_matches_eager_steps():
+    # capture() runs two eager warm-up steps, then each replay is one step
+    def run(capture):
+        model = build_int4lora_encoder(TINY, rank=4, alpha=8.0, group_size=None, seed=5,
+                                       device=DEV)
+        step = MNRTrainStep(model, batch=8, sequence=32, lr=1e-2)
+        if capture:
+            step.capture(warmup=2)
+            out = [float(step()) for _ in range(3)]
+        else:
+            out = [float(step()) for _ in range(5)][2:]
+        torch.cuda.synchronize()
+        return out, [p.detach().clone() for p in lora_parameters(model)]
+
+    eager_losses, eager_params = run(False)
+    graph_losses, graph_params = run(True)
+    assert graph_losses == eager_losses
+    assert all(torch.equal(a, b) for a, b in zip(eager_params, graph_params))
+
+
+def _fp32_adapter_forward(self, value):
+    """float32 restatement of the adapter: x W_b^T + (x A^T) B^T * alpha/r + b."""
+
+    w = self.base_weight().float()
+    x = value.float()
+    y = x @ w.t() + (x @ self.lora_a.t()) @ self.lora_b.t() * (self.alpha / self.rank)
+    if self.bias_bits is not None:
+        y = y + self.bias_bits.view(torch.bfloat16).float()
+    return y
+
+
+def test_bf16_step_matches_float32_restatement(monkeypatch):
+    model = build_int4lora_encoder(TINY, rank=8, alpha=16.0, group_size=64, seed=7, device=DEV)
+    g = torch.Generator(device="cpu").manual_seed(11)
+    with torch.no_grad():
+        for mod in model.modules():
+            if isinstance(mod, QuantizedLoRALinear):
+                mod.lora_b.copy_(0.05 * torch.randn(mod.lora_b.shape, generator=g))
+    ids = torch.randint(0, TINY.vocab_size, (16, 32), generator=g).to(DEV)
+    params = lora_parameters(model)
+
+    step = MNRTrainStep(model, batch=8, sequence=32)
+    with torch.no_grad():
+        step.query_ids.copy_(ids[:8])
+        step.document_ids.copy_(ids[8:])
+    with torch.autograd.set_grad_enabled(True):
+        from representax_amd.precision import precision_context
+
+        with precision_context(step.policy):
+            emb = model.encode(ids)
+            loss = mnr_loss(emb[:8], emb[8:])
+        grads = torch.autograd.grad(loss, params)
+
+    monkeypatch.setattr(QuantizedLoRALinear, "forward", _fp32_adapter_forward)
+    emb32 = model.encode(ids, compute_dtype=torch.float32)
+    loss32 = mnr_loss(emb32[:8], emb32[8:])
+    grads32 = torch.autograd.grad(loss32, params)
+    torch.cuda.synchronize()
+
+    assert abs(float(loss) - float(loss32)) < 2e-2 * max(1.0, abs(float(loss32)))
+    num = sum(float((a.float() - b).square().sum()) for a, b in zip(grads, grads32))
+    den = sum(float(b.square().sum()) for b in grads32)
+    # bf16 activations through two layers versus float32 throughout
+    assert math.sqrt(num / den) < 5e-2
