@@ -9,6 +9,7 @@
 
 #include "common.h"
 #include "kernels.h"
+#include "lds_pipeline.h"
 
 namespace rpx {
 namespace {
@@ -18,23 +19,6 @@ constexpr int kBK = 128;  // k bytes (= fp8 elements) per pipeline slice
 template <int FA, int FB>
 __device__ __forceinline__ f32x16_t mfma_f8(i32x8_t a, i32x8_t b, f32x16_t c) {
   return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, FA, FB, 0, 0, 0, 0);
-}
-
-typedef __attribute__((address_space(3))) void lds_void_t;
-
-// LDS rows are 128 bytes (eight 16-byte chunks), unpadded. Chunk c of row r
-// lives at physical chunk c ^ swz(r). A ds_read_b128 fragment read has every
-// lane of a 16-lane group on a different row of the same logical chunk; with
-// this swizzle those 16 reads hit 16 distinct 16-byte bank groups of a
-// 256-byte LDS cycle, and any 8 consecutive rows hit 8 distinct chunks.
-__device__ __forceinline__ int swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
-
-// Waits until at most n of this wave's vector-memory operations are pending
-// and every LDS operation has returned, then joins the workgroup barrier. The
-// memory clobber keeps LDS reads of the next slice below the barrier.
-template <int N>
-__device__ __forceinline__ void wait_sync() {
-  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
 // Direct-to-LDS loads of one K-slice: this wave's LPW segments (1 KB: 8 rows
@@ -72,13 +56,6 @@ __device__ __forceinline__ i32x8_t load_frag(const uint8_t* stage, int row, int 
 // still busy. bf16 results go through LDS so each global store writes whole
 // 128-byte row segments; fp32 results and split-K partials are stored from
 // registers (16 bytes per lane).
-// One 16-byte-per-lane direct-to-LDS load: segment `seg` (1 KB) of a stage.
-__device__ __forceinline__ void dma_seg(uint8_t* stage, const uint8_t* src, int64_t koff, int seg) {
-  __builtin_amdgcn_global_load_lds(
-      src + koff, reinterpret_cast<lds_void_t*>(reinterpret_cast<uintptr_t>(stage) + seg * 1024), 16,
-      0, 0);
-}
-
 template <int BM, int BN, int WM, int WN, int NS, int WPE, int FA, int FB>
 __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
     k_fp8_gemm(const uint8_t* __restrict__ A, const uint8_t* __restrict__ B, int64_t M, int64_t N,
@@ -112,9 +89,7 @@ __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_
   // Tiles (n fastest) are dealt to the 8 XCDs in contiguous ranges so each
   // XCD's L2 holds a few A row-blocks; split-K slices are outermost.
   const int tiles = tiles_m * tiles_n;
-  const int total = static_cast<int>(gridDim.x);
-  int b = blockIdx.x;
-  if (total % 8 == 0) b = (blockIdx.x % 8) * (total / 8) + blockIdx.x / 8;
+  const int b = xcd_block(blockIdx.x, static_cast<int>(gridDim.x));
   const int split = b / tiles;
   const int tile = b % tiles;
   const int64_t m0 = static_cast<int64_t>(tile / tiles_n) * BM;
@@ -388,7 +363,8 @@ __global__ void __launch_bounds__(256)
   X(7, 128, 192, 2, 2, 3, 1)   \
   X(8, 256, 96, 4, 1, 3, 1)    \
   X(9, 128, 128, 2, 2, 3, 2)   \
-  X(10, 256, 128, 2, 2, 3, 1)
+  X(10, 256, 128, 2, 2, 3, 1)  \
+  X(11, 256, 256, 2, 2, 2, 1)
 
 constexpr int fp8_lds_bytes(int bm, int bn, int wm, int wn, int ns) {
   return ns * (bm + bn) * kBK > wm * wn * (bm / wm) * ((bn / wn) * 2 + 16)
@@ -400,7 +376,7 @@ constexpr int fp8_blocks_per_cu(int bm, int bn, int wm, int wn, int ns, int wpe)
              ? 160 * 1024 / fp8_lds_bytes(bm, bn, wm, wn, ns)
              : (4 * wpe) / (wm * wn);
 }
-constexpr int kNumCfg = 11;
+constexpr int kNumCfg = 12;
 #define RPX_CFG_BM(id, bm, bn, wm, wn, ns, wpe) bm,
 #define RPX_CFG_BN(id, bm, bn, wm, wn, ns, wpe) bn,
 #define RPX_CFG_SLOTS(id, bm, bn, wm, wn, ns, wpe) 256 * fp8_blocks_per_cu(bm, bn, wm, wn, ns, wpe),

@@ -1,12 +1,14 @@
 // bf16 MFMA "NT" GEMM for gfx950: C[M, N] = A[M, K] . B[N, K]^T with both
-// operands K-contiguous. B is either bf16 rows or packed INT4 rows that are
-// dequantized (exactly: bf16(q * s)) while being staged into LDS.
+// operands K-contiguous. B is either bf16 rows or packed INT4 rows (two
+// nibbles per byte, per-row or per-group bf16 scales) that are dequantized
+// exactly, bf16(q * s), from LDS into the MFMA fragments.
 //
-// Tiling: BM x BN x 64 block tile, WM x WN waves, each wave a
-// (BM/WM) x (BN/WN) sub-tile of v_mfma_f32_32x32x16_bf16 blocks. LDS is
-// double buffered; the next K-slice's global loads are in flight while the
-// current slice is multiplied, and the INT4 nibble unpack runs on the VALU
-// between MFMA issues.
+// Pipeline: K-slices of 64 elements. A (and bf16 B) rows move global -> LDS
+// as 128-byte swizzled rows, packed B rows as 32 bytes, all with direct-to-LDS
+// loads into NS rotating stages. Within a slice a lane covers 32 consecutive
+// k of each row: MFMA step j takes k = 32 h + 8 j + [0, 8) from lane half h
+// (the same permutation for both operands), so one 16-byte LDS read per
+// packed B fragment serves the whole slice.
 //
 // Accumulator orientation: the MFMA's first operand is the B (weight) row
 // fragment, so lane l of a 32x32 block owns output row m = l % 32 and the
@@ -17,14 +19,13 @@
 
 #include "common.h"
 #include "kernels.h"
+#include "lds_pipeline.h"
 
 namespace rpx {
 
 namespace {
 
-constexpr int kBK = 64;
-constexpr int kPad = 8;              // bf16 elements of padding per LDS row
-constexpr int kLdsLd = kBK + kPad;   // 144-byte rows: conflict-free b128 reads
+constexpr int kBK = 64;  // k elements per slice
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(u32x4_t v) {
   return __builtin_bit_cast(bf16x8_t, v);
@@ -65,112 +66,93 @@ __device__ __forceinline__ void dequant8(uint32_t word, float s, float m8s, uint
   }
 }
 
-template <int BM, int BN, int WM, int WN, bool INT4, int JB>
-__global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(JB == 4 ? 1 : 2)))
+// Packed-B rows are 32 bytes per slice; the two 16-byte halves of rows 8..15
+// of every 16 swap places so a fragment read (16 lanes on 16 rows, one half)
+// is conflict-free.
+__device__ __forceinline__ int pswz(int row) { return (row >> 3) & 1; }
+
+template <int BM, int BN, int WM, int WN, int NS, int WPE, bool INT4, int JB>
+__global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
     k_gemm_nt(const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ B,
               int64_t ldb, Int4Operand w, int group_shift, int64_t M, int64_t N, int64_t K,
-              uint16_t* __restrict__ out, int64_t ldc, LowRankEpilogue epi, int tiles_m) {
-  constexpr int NT = 64 * WM * WN;
+              uint16_t* __restrict__ out, int64_t ldc, LowRankEpilogue epi, int tiles_m,
+              int tiles_n) {
+  constexpr int NW = WM * WN;
+  constexpr int NT = 64 * NW;
   constexpr int TM = BM / WM;
   constexpr int TN = BN / WN;
   constexpr int FM = TM / 32;
   constexpr int FN = TN / 32;
-  static_assert(TM % 32 == 0 && TN % 32 == 0, "wave tile must be a multiple of 32");
-  extern __shared__ __align__(16) uint16_t smem[];
-  uint16_t* sA = smem;
-  uint16_t* sB = smem + 2 * BM * kLdsLd;
+  static_assert(TM % 32 == 0 && TN % 32 == 0, "wave tile must be made of 32x32 blocks");
+  constexpr int A_BYTES = BM * 128;
+  constexpr int B_ROW = INT4 ? 32 : 128;
+  constexpr int STAGE = A_BYTES + BN * B_ROW;
+  constexpr int A_SEGS = BM / 8;
+  constexpr int SEGS = A_SEGS + BN * B_ROW / 1024;
+  static_assert((BN * B_ROW) % 1024 == 0 && SEGS % NW == 0, "DMA segments must split evenly");
+  constexpr int LPW = SEGS / NW;
+  static_assert(NS >= 2 && NS <= 4 && LPW * (NS - 1) < 64, "vmcnt range");
+  extern __shared__ __align__(16) uint8_t smem[];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave % WM;
   const int wn = wave / WM;
-  // Tiles in row-major (n fastest) order, dealt to the 8 XCDs (which take
-  // workgroups round-robin) in contiguous ranges, so that each XCD's L2
-  // holds a few A row-blocks and streams the weight tiles.
-  const int tiles = gridDim.x;
-  int tile = blockIdx.x;
-  if (tiles % 8 == 0) tile = (blockIdx.x % 8) * (tiles / 8) + blockIdx.x / 8;
-  const int tiles_n = tiles / tiles_m;
-  const int tm = tile / tiles_n;
-  const int tn = tile % tiles_n;
-  const int64_t m0 = static_cast<int64_t>(tm) * BM;
-  const int64_t n0 = static_cast<int64_t>(tn) * BN;
+  const int tile = xcd_block(blockIdx.x, static_cast<int>(gridDim.x));
+  const int64_t m0 = static_cast<int64_t>(tile / tiles_n) * BM;
+  const int64_t n0 = static_cast<int64_t>(tile % tiles_n) * BN;
+  const int nk = static_cast<int>(K / kBK);
+  const int half = lane >> 5;
+  const int frow = lane & 31;
 
-  constexpr int A_VECS = BM * kBK / 8;
-  static_assert(A_VECS % NT == 0, "A tile must split evenly");
-  constexpr int A_PER_T = A_VECS / NT;
-  constexpr int B_VECS = INT4 ? BN * kBK / 32 : BN * kBK / 8;
-  constexpr int B_PER_T = (B_VECS + NT - 1) / NT;
-  constexpr int B_VPR = INT4 ? kBK / 32 : kBK / 8;  // vectors per row
+  // INT4 scales of this block's B rows for every group, copied to LDS after
+  // the stages ([row][group], 16-byte vectors); the first chunk's loads go
+  // out before the prologue DMA and its LDS stores after it.
+  constexpr int SC_CAP = INT4 ? 8 : 1;
+  uint16_t* sc = reinterpret_cast<uint16_t*>(smem + NS * STAGE);
+  const int ng = INT4 ? static_cast<int>(w.n_groups) : 0;
+  const int sc_total = INT4 ? static_cast<int>(((N - n0) < BN ? (N - n0) : BN) * ng) : 0;
+  const int sc_vecs = sc_total / 8;
+  const u32x4_t* sc_src = reinterpret_cast<const u32x4_t*>(INT4 ? w.scales + n0 * ng : nullptr);
+  u32x4_t sc_reg[SC_CAP];
+  if constexpr (INT4) {
+#pragma unroll
+    for (int c = 0; c < SC_CAP; ++c) {
+      const int v = tid + c * NT;
+      if (v < sc_vecs) sc_reg[c] = sc_src[v];
+    }
+  }
 
-  u32x4_t a_reg[A_PER_T];
-  u32x4_t b_reg[B_PER_T];
-  float b_scale[B_PER_T];
-
-  auto load_a = [&](int64_t k0) {
+  // DMA sources. Segment j = wave + i * NW: A rows 8j..8j+7 (128 B each), or
+  // B rows (8 per segment of bf16 rows, 32 per segment of packed rows). Rows
+  // past the edge re-read the last row.
+  const uint8_t* src[LPW];
 #pragma unroll
-    for (int i = 0; i < A_PER_T; ++i) {
-      const int v = tid + i * NT;
-      const int row = v / (kBK / 8);
-      const int c = (v % (kBK / 8)) * 8;
-      const int64_t gm = m0 + row;
-      a_reg[i] = (gm < M) ? *reinterpret_cast<const u32x4_t*>(A + gm * lda + k0 + c)
-                          : u32x4_t{0u, 0u, 0u, 0u};
+  for (int i = 0; i < LPW; ++i) {
+    const int j = wave + i * NW;
+    if (j < A_SEGS) {
+      const int trow = 8 * j + (lane >> 3);
+      int64_t r = m0 + trow;
+      r = r < M ? r : M - 1;
+      src[i] = reinterpret_cast<const uint8_t*>(A + r * lda) + (((lane & 7) ^ swz(trow)) << 4);
+    } else if constexpr (INT4) {
+      const int trow = 32 * (j - A_SEGS) + (lane >> 1);
+      int64_t r = n0 + trow;
+      r = r < N ? r : N - 1;
+      src[i] = w.packed + r * w.packed_cols + (((lane & 1) ^ pswz(trow)) << 4);
+    } else {
+      const int trow = 8 * (j - A_SEGS) + (lane >> 3);
+      int64_t r = n0 + trow;
+      r = r < N ? r : N - 1;
+      src[i] = reinterpret_cast<const uint8_t*>(B + r * ldb) + (((lane & 7) ^ swz(trow)) << 4);
     }
-  };
-  auto load_b = [&](int64_t k0) {
-#pragma unroll
-    for (int i = 0; i < B_PER_T; ++i) {
-      const int v = tid + i * NT;
-      const int row = v / B_VPR;
-      const int c = v % B_VPR;
-      const int64_t gn = n0 + row;
-      const bool ok = (v < B_VECS) && (gn < N);
-      if constexpr (INT4) {
-        const int64_t kc = k0 + c * 32;
-        b_reg[i] = ok ? *reinterpret_cast<const u32x4_t*>(w.packed + gn * w.packed_cols + kc / 2)
-                      : u32x4_t{0u, 0u, 0u, 0u};
-        const int64_t gi = (w.n_groups == 1) ? 0 : (kc >> group_shift);
-        b_scale[i] = ok ? bf16_to_f32(w.scales[gn * w.n_groups + gi]) : 0.0f;
-      } else {
-        b_reg[i] = ok ? *reinterpret_cast<const u32x4_t*>(B + gn * ldb + k0 + c * 8)
-                      : u32x4_t{0u, 0u, 0u, 0u};
-      }
-    }
-  };
-  auto store_a = [&](int buf) {
-    uint16_t* base = sA + buf * BM * kLdsLd;
-#pragma unroll
-    for (int i = 0; i < A_PER_T; ++i) {
-      const int v = tid + i * NT;
-      const int row = v / (kBK / 8);
-      const int c = (v % (kBK / 8)) * 8;
-      *reinterpret_cast<u32x4_t*>(base + row * kLdsLd + c) = a_reg[i];
-    }
-  };
-  auto store_b = [&](int buf) {
-    uint16_t* base = sB + buf * BN * kLdsLd;
-#pragma unroll
-    for (int i = 0; i < B_PER_T; ++i) {
-      const int v = tid + i * NT;
-      if (v >= B_VECS) continue;
-      const int row = v / B_VPR;
-      const int c = v % B_VPR;
-      if constexpr (INT4) {
-        const float s = b_scale[i];
-        const float m8s = -8.0f * s;
-        uint32_t o[16];
-#pragma unroll
-        for (int d = 0; d < 4; ++d) dequant8(b_reg[i][d], s, m8s, o + 4 * d);
-        u32x4_t* dst = reinterpret_cast<u32x4_t*>(base + row * kLdsLd + c * 32);
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          dst[q] = u32x4_t{o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]};
-      } else {
-        *reinterpret_cast<u32x4_t*>(base + row * kLdsLd + c * 8) = b_reg[i];
-      }
-    }
+  }
+  // byte offset of slice s in the source rows
+  auto koff = [&](int s, int i) -> int64_t {
+    const int j = wave + i * NW;
+    return (INT4 && j >= A_SEGS) ? static_cast<int64_t>(s) * (kBK / 2)
+                                 : static_cast<int64_t>(s) * (kBK * 2);
   };
 
   f32x16_t acc[FN][FM];
@@ -181,50 +163,155 @@ __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[fn][fm][v] = 0.0f;
 
-  auto compute = [&](int buf) {
-    const uint16_t* a_base =
-        sA + buf * BM * kLdsLd + (wm * TM + (lane & 31)) * kLdsLd + (lane >> 5) * 8;
-    const uint16_t* b_base =
-        sB + buf * BN * kLdsLd + (wn * TN + (lane & 31)) * kLdsLd + (lane >> 5) * 8;
+  // Fragments, double-buffered by 16-deep step: a[kk & 1][fm], b[kk & 1][fn]
+  // for bf16 B; for INT4 B the packed bytes of the whole slice (bp, one
+  // 16-byte read per fragment) are dequantized unit by unit into bq[kk].
+  bf16x8_t af[2][FM];
+  bf16x8_t bfr[2][FN];
+  u32x4_t bp[FN];
+  float bs[FN];
+  uint32_t bq[4][FN][4];
+  auto read_a = [&](const uint8_t* st, int kk, int buf) {
 #pragma unroll
-    for (int kk = 0; kk < kBK / 16; ++kk) {
-      bf16x8_t af[FM];
-      bf16x8_t bfr[FN];
+    for (int fm = 0; fm < FM; ++fm)
+      af[buf][fm] = as_bf16x8(lds_chunk(st, wm * TM + fm * 32 + frow, 4 * half + kk));
+  };
+  auto read_b = [&](const uint8_t* st, int kk, int buf) {
 #pragma unroll
-      for (int fm = 0; fm < FM; ++fm)
-        af[fm] = *reinterpret_cast<const bf16x8_t*>(a_base + fm * 32 * kLdsLd + kk * 16);
+    for (int fn = 0; fn < FN; ++fn)
+      bfr[buf][fn] = as_bf16x8(lds_chunk(st + A_BYTES, wn * TN + fn * 32 + frow, 4 * half + kk));
+  };
+  auto read_bp = [&](const uint8_t* st) {
 #pragma unroll
-      for (int fn = 0; fn < FN; ++fn)
-        bfr[fn] = *reinterpret_cast<const bf16x8_t*>(b_base + fn * 32 * kLdsLd + kk * 16);
-#pragma unroll
-      for (int fn = 0; fn < FN; ++fn)
-#pragma unroll
-        for (int fm = 0; fm < FM; ++fm)
-          acc[fn][fm] =
-              __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[fn], af[fm], acc[fn][fm], 0, 0, 0);
+    for (int fn = 0; fn < FN; ++fn) {
+      const int r = wn * TN + fn * 32 + frow;
+      bp[fn] = *reinterpret_cast<const u32x4_t*>(st + A_BYTES + r * 32 + ((half ^ pswz(r)) << 4));
     }
   };
+  auto read_bs = [&](int s) {
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn) {
+      const int r = wn * TN + fn * 32 + frow;
+      const int g = ng == 1 ? 0 : ((s * kBK + 32 * half) >> group_shift);
+      bs[fn] = bf16_to_f32(sc[r * ng + g]);
+    }
+  };
+  // unit u (0 .. 4 FN - 1) of step kk: fragment u / 4, dword u % 4; the same
+  // arithmetic as dequant8
+  auto dq_unit = [&](int kk, int u) {
+    const int fn = u / 4;
+    const int b = u % 4;
+    const uint32_t x = bp[fn][kk] ^ 0x88888888u;
+    const float fl = static_cast<float>(((x & 0x0F0F0F0Fu) >> (8 * b)) & 0xFFu);
+    const float fh = static_cast<float>((((x >> 4) & 0x0F0F0F0Fu) >> (8 * b)) & 0xFFu);
+    const float m8s = -8.0f * bs[fn];
+    bq[kk][fn][b] = pack_bf16x2(__builtin_fmaf(fl, bs[fn], m8s), __builtin_fmaf(fh, bs[fn], m8s));
+  };
+  auto mma = [&](int i, int kk) {
+    const int fn = i / FM;
+    const int fm = i % FM;
+    bf16x8_t bv;
+    if constexpr (INT4)
+      bv = as_bf16x8(u32x4_t{bq[kk][fn][0], bq[kk][fn][1], bq[kk][fn][2], bq[kk][fn][3]});
+    else
+      bv = bfr[kk & 1][fn];
+    acc[fn][fm] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bv, af[kk & 1][fm], acc[fn][fm], 0, 0, 0);
+  };
 
-  const int64_t nk = K / kBK;
-  load_a(0);
-  load_b(0);
-  store_a(0);
-  store_b(0);
-  __syncthreads();
-  for (int64_t kt = 0; kt < nk; ++kt) {
-    const int cur = static_cast<int>(kt & 1);
-    const bool more = kt + 1 < nk;
-    if (more) {
-      load_a((kt + 1) * kBK);
-      load_b((kt + 1) * kBK);
+  // prologue: NS slices in flight (refills past the end re-read the last
+  // slice into a stage nothing reads again: LPW loads per slice always)
+#pragma unroll
+  for (int s = 0; s < NS; ++s)
+#pragma unroll
+    for (int i = 0; i < LPW; ++i)
+      dma_seg(smem + s * STAGE, src[i], koff(s < nk ? s : nk - 1, i), wave + i * NW);
+  if constexpr (INT4) {
+#pragma unroll
+    for (int c = 0; c < SC_CAP; ++c) {
+      const int v = tid + c * NT;
+      if (v < sc_vecs) reinterpret_cast<u32x4_t*>(sc)[v] = sc_reg[c];
     }
-    compute(cur);
-    if (more) {
-      store_a(cur ^ 1);
-      store_b(cur ^ 1);
-    }
-    __syncthreads();
+    for (int v = tid + SC_CAP * NT; v < sc_vecs; v += NT)
+      reinterpret_cast<u32x4_t*>(sc)[v] = sc_src[v];
+    for (int i = 8 * sc_vecs + tid; i < sc_total; i += NT) sc[i] = w.scales[n0 * ng + i];
   }
+  wait_sync<(NS - 1) * LPW>();
+  read_a(smem, 0, 0);
+  if constexpr (INT4) {
+    read_bp(smem);
+    read_bs(0);
+#pragma unroll
+    for (int u = 0; u < 4 * FN; ++u) dq_unit(0, u);
+  } else {
+    read_b(smem, 0, 0);
+  }
+
+  // Main loop, one 16-deep step at a time. Slice t lives in stage t % NS.
+  // Each step issues its FM x FN MFMAs, each followed by its share of the
+  // step-ahead work: the DS reads of the next step's fragments and, for
+  // INT4, the dequantization of the next step's B (one unit per slot). The
+  // barrier sits before step 3 (steps 0-3 of the slice have been read by
+  // then, slice t + 1 has landed and stage t is free); step 3 then also
+  // carries the DMA of slice t + NS into stage t and the reads of slice
+  // t + 1's packed rows, scales and step-0 fragments. sched_barrier fences
+  // keep the order.
+  constexpr int NS1 = FM * FN;  // MFMA slots per step
+  constexpr int NU = 4 * FN;    // dequantization units per step
+  int stage = 0;
+  for (int t = 0; t < nk; ++t) {
+    const int next = stage + 1 == NS ? 0 : stage + 1;
+    const uint8_t* st = smem + stage * STAGE;
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int kk = 0; kk < 3; ++kk) {
+#pragma unroll
+      for (int i = 0; i < NS1; ++i) {
+        mma(i, kk);
+        __builtin_amdgcn_sched_barrier(0);
+        if (i == 0) read_a(st, kk + 1, (kk + 1) & 1);
+        if constexpr (INT4) {
+#pragma unroll
+          for (int u = i * NU / NS1; u < (i + 1) * NU / NS1; ++u) dq_unit(kk + 1, u);
+        } else {
+          if (i == NS1 / 2) read_b(st, kk + 1, (kk + 1) & 1);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    wait_sync<(NS - 2) * LPW>();
+    const int refill = t + NS < nk ? t + NS : nk - 1;
+    uint8_t* fill = smem + stage * STAGE;
+    const uint8_t* nst = smem + next * STAGE;
+    // INT4: packed rows and scales first, their units in the last half
+    constexpr int U0 = NS1 / 2;
+#pragma unroll
+    for (int i = 0; i < NS1; ++i) {
+      mma(i, 3);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int d = i * LPW / NS1; d < (i + 1) * LPW / NS1; ++d)
+        dma_seg(fill, src[d], koff(refill, d), wave + d * NW);
+      if constexpr (INT4) {
+        if (i == 0) {
+          read_bp(nst);
+          read_bs(t + 1 < nk ? t + 1 : t);
+        }
+        if (i == 1) read_a(nst, 0, 0);
+        if (i >= U0) {
+#pragma unroll
+          for (int u = (i - U0) * NU / (NS1 - U0); u < (i - U0 + 1) * NU / (NS1 - U0); ++u)
+            dq_unit(0, u);
+        }
+      } else {
+        if (i == 0) read_a(nst, 0, 0);
+        if (i == NS1 / 2) read_b(nst, 0, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    stage = next;
+  }
+  // no LDS DMA may still be in flight when the waves leave the loop
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   // Epilogue --------------------------------------------------------------
   // The low-rank term t = C R^T for this lane's rows m and columns n is one
@@ -306,19 +393,24 @@ __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_
   }
 }
 
-template <int BM, int BN, int WM, int WN, bool INT4, int JB>
+constexpr int gemm_lds_bytes(int bm, int bn, int ns, bool int4) {
+  return ns * (bm * 128 + bn * (int4 ? 32 : 128));
+}
+
+template <int BM, int BN, int WM, int WN, int NS, int WPE, bool INT4, int JB>
 hipError_t run_gemm_jb(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb,
                        const Int4Operand& w, int64_t m, int64_t n, int64_t k, uint16_t* out,
                        int64_t ldc, const LowRankEpilogue& epi, hipStream_t stream) {
   const int tiles_m = static_cast<int>(ceil_div(m, BM));
   const int tiles_n = static_cast<int>(ceil_div(n, BN));
-  const size_t lds = static_cast<size_t>(2) * (BM + BN) * kLdsLd * sizeof(uint16_t);
-  auto kern = k_gemm_nt<BM, BN, WM, WN, INT4, JB>;
+  const size_t scale_bytes = INT4 ? static_cast<size_t>(BN) * w.n_groups * 2 : 0;
+  const size_t lds = gemm_lds_bytes(BM, BN, NS, INT4) + ((scale_bytes + 15) & ~size_t{15});
+  if (lds > 160 * 1024) return hipErrorInvalidValue;
+  auto kern = k_gemm_nt<BM, BN, WM, WN, NS, WPE, INT4, JB>;
   static bool attr_set = false;
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       static_cast<int>(lds));
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     if (e != hipSuccess) return e;
     attr_set = true;
   }
@@ -327,56 +419,88 @@ hipError_t run_gemm_jb(const uint16_t* a, int64_t lda, const uint16_t* b, int64_
     while ((int64_t{1} << group_shift) < w.group) ++group_shift;
   }
   hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(tiles_m) * tiles_n), dim3(64 * WM * WN),
-                     lds, stream, a, lda, b, ldb, w, group_shift, m, n, k, out, ldc, epi,
-                     tiles_m);
+                     lds, stream, a, lda, b, ldb, w, group_shift, m, n, k, out, ldc, epi, tiles_m,
+                     tiles_n);
   return hipGetLastError();
 }
 
-template <int BM, int BN, int WM, int WN, bool INT4>
+template <int BM, int BN, int WM, int WN, int NS, int WPE, bool INT4>
 hipError_t run_gemm(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb,
                     const Int4Operand& w, int64_t m, int64_t n, int64_t k, uint16_t* out,
                     int64_t ldc, const LowRankEpilogue& epi, hipStream_t stream) {
   if (epi.rank <= 0)
-    return run_gemm_jb<BM, BN, WM, WN, INT4, 0>(a, lda, b, ldb, w, m, n, k, out, ldc, epi, stream);
+    return run_gemm_jb<BM, BN, WM, WN, NS, WPE, INT4, 0>(a, lda, b, ldb, w, m, n, k, out, ldc,
+                                                         epi, stream);
   if (epi.rank <= 16)
-    return run_gemm_jb<BM, BN, WM, WN, INT4, 1>(a, lda, b, ldb, w, m, n, k, out, ldc, epi, stream);
+    return run_gemm_jb<BM, BN, WM, WN, NS, WPE, INT4, 1>(a, lda, b, ldb, w, m, n, k, out, ldc,
+                                                         epi, stream);
   if (epi.rank <= 32)
-    return run_gemm_jb<BM, BN, WM, WN, INT4, 2>(a, lda, b, ldb, w, m, n, k, out, ldc, epi, stream);
-  return run_gemm_jb<BM, BN, WM, WN, INT4, 4>(a, lda, b, ldb, w, m, n, k, out, ldc, epi, stream);
+    return run_gemm_jb<BM, BN, WM, WN, NS, WPE, INT4, 2>(a, lda, b, ldb, w, m, n, k, out, ldc,
+                                                         epi, stream);
+  return run_gemm_jb<BM, BN, WM, WN, NS, WPE, INT4, 4>(a, lda, b, ldb, w, m, n, k, out, ldc, epi,
+                                                       stream);
 }
 
-// Tile configuration: RPX_GEMM_TILE=256x128|128x128|128x64 overrides the
-// size-based choice (for tuning sweeps).
+// Tile configuration override for tuning sweeps: RPX_GEMM_TILE=<id>.
 int tile_override() {
   static int cached = -1;
   if (cached < 0) {
     const char* env = std::getenv("RPX_GEMM_TILE");
-    cached = 0;
-    if (env != nullptr) {
-      if (std::strcmp(env, "256x128") == 0) cached = 1;
-      if (std::strcmp(env, "128x128") == 0) cached = 2;
-      if (std::strcmp(env, "128x64") == 0) cached = 3;
-    }
+    cached = env != nullptr ? std::atoi(env) : 0;
   }
   return cached;
 }
 
-template <bool INT4>
-hipError_t dispatch(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb,
-                    const Int4Operand& w, int64_t m, int64_t n, int64_t k, uint16_t* out,
-                    int64_t ldc, const LowRankEpilogue& epi, hipStream_t stream) {
+// INT4 B: one wave row (WM = 1) so every packed row is dequantized by a
+// single wave. bf16 B: 2 x 2 or 4 x 2 waves.
+hipError_t dispatch_int4(const uint16_t* a, int64_t lda, const Int4Operand& w, int64_t m,
+                         int64_t n, int64_t k, uint16_t* out, int64_t ldc,
+                         const LowRankEpilogue& epi, hipStream_t stream) {
+  // scales are copied in 16-byte vectors from a 16-byte aligned base, and the
+  // packed rows are read in 16-byte chunks
+  if ((reinterpret_cast<uintptr_t>(w.scales) & 15) != 0 || (w.packed_cols & 15) != 0 ||
+      (reinterpret_cast<uintptr_t>(w.packed) & 15) != 0)
+    return hipErrorInvalidValue;
   int cfg = tile_override();
-  if (cfg == 0) {
-    // 128x128 tiles (two workgroups per CU by LDS) unless that leaves CUs
-    // idle; measured faster than 256x128 at one workgroup per CU
-    const int64_t cus = 256;
-    cfg = (ceil_div(m, 128) * ceil_div(n, 128) >= cus) ? 2 : 3;
+  if (cfg == 7)
+    return run_gemm<256, 256, 2, 2, 3, 1, true>(a, lda, nullptr, 0, w, m, n, k, out, ldc, epi,
+                                                stream);
+  if (cfg < 1 || cfg > 3) {
+    // 128 x 32 wave tiles at two workgroups (8 waves) per CU: each
+    // dequantized B fragment feeds four MFMAs, and a CU's 8 waves keep the
+    // LDS fragment reads and the dequantization VALU work under the MFMAs
+    cfg = ceil_div(m, 128) * ceil_div(n, 128) >= 128 ? 2 : 3;
   }
   if (cfg == 1)
-    return run_gemm<256, 128, 2, 2, INT4>(a, lda, b, ldb, w, m, n, k, out, ldc, epi, stream);
+    return run_gemm<256, 128, 1, 4, 3, 1, true>(a, lda, nullptr, 0, w, m, n, k, out, ldc, epi,
+                                                stream);
   if (cfg == 2)
-    return run_gemm<128, 128, 2, 2, INT4>(a, lda, b, ldb, w, m, n, k, out, ldc, epi, stream);
-  return run_gemm<128, 64, 2, 2, INT4>(a, lda, b, ldb, w, m, n, k, out, ldc, epi, stream);
+    return run_gemm<128, 128, 1, 4, 3, 2, true>(a, lda, nullptr, 0, w, m, n, k, out, ldc, epi,
+                                                stream);
+  return run_gemm<64, 128, 1, 4, 3, 2, true>(a, lda, nullptr, 0, w, m, n, k, out, ldc, epi,
+                                             stream);
+}
+
+hipError_t dispatch_bf16(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb,
+                         int64_t m, int64_t n, int64_t k, uint16_t* out, int64_t ldc,
+                         const LowRankEpilogue& epi, hipStream_t stream) {
+  Int4Operand none;
+  int cfg = tile_override();
+  if (cfg == 8)
+    return run_gemm<256, 256, 2, 2, 2, 1, false>(a, lda, b, ldb, none, m, n, k, out, ldc, epi,
+                                                 stream);
+  if (cfg < 4 || cfg > 6) {
+    cfg = ceil_div(m, 256) * ceil_div(n, 128) >= 256 ? 4
+          : (ceil_div(m, 128) * ceil_div(n, 128) >= 256 ? 5 : 6);
+  }
+  if (cfg == 4)
+    return run_gemm<256, 128, 4, 2, 2, 2, false>(a, lda, b, ldb, none, m, n, k, out, ldc, epi,
+                                                 stream);
+  if (cfg == 5)
+    return run_gemm<128, 128, 2, 2, 2, 2, false>(a, lda, b, ldb, none, m, n, k, out, ldc, epi,
+                                                 stream);
+  return run_gemm<64, 128, 2, 2, 3, 2, false>(a, lda, b, ldb, none, m, n, k, out, ldc, epi,
+                                              stream);
 }
 
 }  // namespace
@@ -393,15 +517,14 @@ hipError_t launch_gemm_int4(const uint16_t* a, int64_t lda, const Int4Operand& w
                             int64_t n, int64_t k, uint16_t* out, int64_t ldc,
                             const LowRankEpilogue& epi, hipStream_t stream) {
   if (m == 0 || n == 0) return hipSuccess;
-  return dispatch<true>(a, lda, nullptr, 0, w, m, n, k, out, ldc, epi, stream);
+  return dispatch_int4(a, lda, w, m, n, k, out, ldc, epi, stream);
 }
 
 hipError_t launch_gemm_bf16(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb,
                             int64_t m, int64_t n, int64_t k, uint16_t* out, int64_t ldc,
                             const LowRankEpilogue& epi, hipStream_t stream) {
   if (m == 0 || n == 0) return hipSuccess;
-  Int4Operand none;
-  return dispatch<false>(a, lda, b, ldb, none, m, n, k, out, ldc, epi, stream);
+  return dispatch_bf16(a, lda, b, ldb, m, n, k, out, ldc, epi, stream);
 }
 
 }  // namespace rpx

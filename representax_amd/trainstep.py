@@ -19,7 +19,8 @@ masters only. It restates the reference's model and step:
 bf16 compute with fp32 masters follows the ``bfloat16_mixed`` policy
 (src/representax/precision.py:19-124). Dropout is off (probability 0, as in
 the reference's benchmark configuration). Attention runs as explicit batched
-products with contiguous right-hand operands (softmax in float32).
+products with contiguous right-hand operands in float32, and through torch's
+fused flash / memory-efficient kernels in bf16.
 """
 
 from __future__ import annotations
@@ -79,9 +80,10 @@ class LayerNorm(torch.nn.Module):
         self.eps = eps
 
     def forward(self, value: torch.Tensor) -> torch.Tensor:
-        out = F.layer_norm(value.float(), value.shape[-1:], self.weight.float(),
-                           self.bias.float(), self.eps)
-        return out.to(value.dtype)
+        # torch's reduced-precision layer_norm keeps float32 statistics and
+        # rounds the normalized, affine-transformed value once
+        return F.layer_norm(value, value.shape[-1:], self.weight.to(value.dtype),
+                            self.bias.to(value.dtype), self.eps)
 
 
 class _Attention(torch.autograd.Function):
@@ -90,6 +92,7 @@ class _Attention(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, v, bias, scale):
+        q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
         s = torch.matmul(q, k.transpose(-1, -2).contiguous()).float() * scale
         if bias is not None:
             s = s + bias
@@ -112,6 +115,19 @@ class _Attention(torch.autograd.Function):
 
 
 def attention(q, k, v, bias, scale):
+    """``[B, H, S, D]`` attention. bf16/fp16 inputs use torch's fused flash
+    or memory-efficient kernels only (never the unfused math fallback);
+    float32 inputs use the explicit products above."""
+
+    if q.dtype in (torch.bfloat16, torch.float16):
+        from torch.nn.attention import SDPBackend, sdpa_kernel
+
+        backends = [SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]
+        if bias is not None:
+            backends = [SDPBackend.EFFICIENT_ATTENTION]
+        with sdpa_kernel(backends):
+            return F.scaled_dot_product_attention(
+                q, k, v, attn_mask=None if bias is None else bias.to(q.dtype), scale=scale)
     return _Attention.apply(q, k, v, bias, scale)
 
 
@@ -131,11 +147,11 @@ class BertSelfAttention(torch.nn.Module):
         b, s, h = hidden.shape
 
         def project(layer):
-            return layer(hidden).reshape(b, s, self.heads, self.head_dim).permute(0, 2, 1, 3).contiguous()
+            return layer(hidden).reshape(b, s, self.heads, self.head_dim).transpose(1, 2)
 
         out = attention(project(self.query), project(self.key), project(self.value), bias,
                         1.0 / math.sqrt(self.head_dim))
-        return self.output(out.permute(0, 2, 1, 3).reshape(b, s, h))
+        return self.output(out.transpose(1, 2).reshape(b, s, h))
 
 
 class BertMLP(torch.nn.Module):
