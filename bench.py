@@ -49,7 +49,7 @@ def parse_args():
     p.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a HIP graph")
     p.add_argument("--no-secondary", action="store_true")
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--only", choices=["fp8", "int4lora", "skinny", "bert"], default=None,
+    p.add_argument("--only", choices=["fp8", "int4lora", "skinny", "bert", "qwen3"], default=None,
                    help="run one workload and nothing else (profiling)")
     return p.parse_args()
 
@@ -389,6 +389,42 @@ def run_bert(steps=10, warmup=3):
     return line
 
 
+def run_qwen3(steps=6, warmup=2):
+    """Qwen3-VL-2B-shaped text tower train step (28 layers, hidden 2048, 16 Q /
+    8 KV heads of 128, SwiGLU 6144, vocab 151936) with all seven projections
+    INT4 group 64 + LoRA r32 (alpha 64): last-token-pooled MNR loss over 16
+    query/document pairs x 512 tokens, bf16 compute, AdamW on the fp32 LoRA
+    masters, one HIP graph per step."""
+
+    import torch
+
+    from representax_amd.trainstep import MNRTrainStep, Qwen3TextConfig, build_int4lora_qwen3
+
+    cfg = Qwen3TextConfig()
+    pairs, seq = 16, 512
+    model = build_int4lora_qwen3(cfg, rank=32, alpha=64.0, group_size=64, seed=0,
+                                 device=torch.device("cuda:0"))
+    step = MNRTrainStep(model, batch=pairs, sequence=seq)
+    step.capture(warmup=2)
+    ms = time_region(step, steps, warmup)
+    tokens = 2 * pairs * seq
+    flops = cfg.step_flops(2 * pairs, seq)
+    line = {
+        "workload": "Qwen3-VL-2B-shaped text tower train step (28L, H2048, 16 Q / 8 KV heads x 128, "
+                    "SwiGLU 6144, vocab 151936), all 7 projections INT4 group-64 + LoRA r32 a64, "
+                    "last-token MNR loss, 16 query/document pairs x 512 tokens, bf16 compute, AdamW "
+                    "on fp32 LoRA masters, no recompute, HIP graph",
+        "value": round(tokens / (ms * 1e-3), 1), "unit": "tokens/s",
+        "ms_per_step": round(ms, 3), "tokens_per_step": tokens,
+        "matrix_tflops": round(flops / (ms * 1e-3) / 1e12, 1),
+        "matrix_tflop_per_step": round(flops / 1e12, 3),
+        "loss_after_timed_steps": round(float(step.loss), 4),
+    }
+    del step, model
+    torch.cuda.empty_cache()
+    return line
+
+
 def run_skinny(batch=96):
     """Per-call GPU latency of the skinny-M forward: a HIP graph of `batch`
     calls cycling through a pool of weight copies larger than the 256 MB
@@ -457,6 +493,9 @@ def main():
     if args.only == "bert":
         print(json.dumps(run_bert()))
         return
+    if args.only == "qwen3":
+        print(json.dumps(run_qwen3()))
+        return
 
     log("fp8: setting up inputs")
     layers = fp8_setup(args.tokens, dev)
@@ -499,6 +538,8 @@ def main():
         result["secondary"].append(run_skinny())
         log("bert-base int4-lora train step")
         result["secondary"].append(run_bert())
+        log("qwen3-shaped int4-lora train step")
+        result["secondary"].append(run_qwen3())
     if args.only is None and not args.no_cpu_baseline:
         log("cpu baseline (numpy oracle)")
         result["cpu_baseline"] = fp8_cpu_baseline()

@@ -237,7 +237,7 @@ def mnr_loss(queries: torch.Tensor, documents: torch.Tensor, scale: float = 20.0
     return (torch.logsumexp(logits, dim=1) - logits.diagonal()).mean()
 
 
-LAYER_LINEARS = r"\.layers\[\d+\]\.(attention\.(query|key|value|output)|mlp\.(input|output))$"
+LAYER_LINEARS = r"\.layers\[\d+\]\.(attention\.(query|key|value|output)|mlp\.(input|output|gate|up|down))$"
 
 
 def build_int4lora_encoder(config: BertConfig, *, rank: int = 16, alpha: float = 32.0,
@@ -256,6 +256,185 @@ def build_int4lora_encoder(config: BertConfig, *, rank: int = 16, alpha: float =
     return model
 
 
+# ---------------------------------------------------------------------------
+# Qwen3-VL-shaped text tower (src/representax/models/qwen3_vl/text.py:23-359,
+# model.py:212-223): pre-norm causal GQA / SwiGLU decoder layers with per-head
+# query/key RMSNorm and rotary positions, final RMSNorm, last-token pooling.
+# For text-only inputs the three MRoPE position streams are equal, so the
+# interleaved rotary embedding is the ordinary one (text.py:30-61).
+# ---------------------------------------------------------------------------
+@dataclass(frozen=True)
+class Qwen3TextConfig:
+    """Shape of the text tower (Qwen3-VL-2B defaults)."""
+
+    vocab_size: int = 151936
+    hidden_size: int = 2048
+    num_hidden_layers: int = 28
+    num_attention_heads: int = 16
+    num_key_value_heads: int = 8
+    head_dimension: int = 128
+    intermediate_size: int = 6144
+    rope_theta: float = 5_000_000.0
+    norm_epsilon: float = 1e-6
+    initializer_range: float = 0.02
+
+    def step_flops(self, batch: int, sequence: int, *, remat: bool = False) -> float:
+        h, f, d = self.hidden_size, self.intermediate_size, self.head_dimension
+        q = self.num_attention_heads * d
+        kv = self.num_key_value_heads * d
+        tokens = batch * sequence
+        linear = 2.0 * tokens * (h * q + 2 * h * kv + q * h + 3 * h * f)
+        # causal attention: half of the score and value products
+        attention = 2.0 * batch * sequence * sequence * q
+        forward = self.num_hidden_layers * (linear + attention)
+        backward = self.num_hidden_layers * (linear + 2 * attention)
+        return forward * (2 if remat else 1) + backward
+
+
+class RMSNorm(torch.nn.Module):
+    """Last-axis RMS normalisation with float32 statistics
+    (src/representax/models/components.py:134-150)."""
+
+    def __init__(self, size: int, eps: float, device=None) -> None:
+        super().__init__()
+        self.weight = torch.nn.Parameter(torch.ones(size, device=device))
+        self.eps = eps
+
+    def forward(self, value: torch.Tensor) -> torch.Tensor:
+        v = value.float()
+        v = v * torch.rsqrt(v.square().mean(-1, keepdim=True) + self.eps)
+        return (v * self.weight.float()).to(value.dtype)
+
+
+def _rotate_half(value: torch.Tensor) -> torch.Tensor:
+    first, second = value.chunk(2, dim=-1)
+    return torch.cat((-second, first), dim=-1)
+
+
+class Qwen3Attention(torch.nn.Module):
+    def __init__(self, config: Qwen3TextConfig, key: int, device=None) -> None:
+        super().__init__()
+        arg = dict(scale=config.initializer_range, bias=False, device=device)
+        h, d = config.hidden_size, config.head_dimension
+        self.heads, self.kv_heads, self.head_dim = (config.num_attention_heads,
+                                                    config.num_key_value_heads, d)
+        self.query = Linear.init(h, self.heads * d, key=key + 0, **arg)
+        self.key = Linear.init(h, self.kv_heads * d, key=key + 1, **arg)
+        self.value = Linear.init(h, self.kv_heads * d, key=key + 2, **arg)
+        self.output = Linear.init(self.heads * d, h, key=key + 3, **arg)
+        self.query_norm = RMSNorm(d, config.norm_epsilon, device)
+        self.key_norm = RMSNorm(d, config.norm_epsilon, device)
+
+    def forward(self, hidden, cos, sin):
+        b, s, _ = hidden.shape
+        q = self.query_norm(self.query(hidden).reshape(b, s, self.heads, self.head_dim))
+        k = self.key_norm(self.key(hidden).reshape(b, s, self.kv_heads, self.head_dim))
+        v = self.value(hidden).reshape(b, s, self.kv_heads, self.head_dim)
+        cos, sin = cos[:, :, None], sin[:, :, None]
+        q = (q.float() * cos + _rotate_half(q.float()) * sin).to(hidden.dtype)
+        k = (k.float() * cos + _rotate_half(k.float()) * sin).to(hidden.dtype)
+        rep = self.heads // self.kv_heads
+        q, k, v = q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)
+        if rep > 1:
+            k = k.repeat_interleave(rep, dim=1)
+            v = v.repeat_interleave(rep, dim=1)
+        out = causal_attention(q, k, v, 1.0 / math.sqrt(self.head_dim))
+        return self.output(out.transpose(1, 2).reshape(b, s, self.heads * self.head_dim))
+
+
+def causal_attention(q, k, v, scale):
+    """Causal ``[B, H, S, D]`` attention; bf16 through torch's fused kernels,
+    float32 through explicit products with a -inf upper triangle."""
+
+    if q.dtype in (torch.bfloat16, torch.float16):
+        from torch.nn.attention import SDPBackend, sdpa_kernel
+
+        with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+            return F.scaled_dot_product_attention(q, k, v, is_causal=True, scale=scale)
+    s = q.shape[-2]
+    bias = torch.full((s, s), float("-inf"), device=q.device).triu(1)
+    return _Attention.apply(q, k, v, bias, scale)
+
+
+class Qwen3MLP(torch.nn.Module):
+    def __init__(self, config: Qwen3TextConfig, key: int, device=None) -> None:
+        super().__init__()
+        arg = dict(scale=config.initializer_range, bias=False, device=device)
+        h, f = config.hidden_size, config.intermediate_size
+        self.gate = Linear.init(h, f, key=key, **arg)
+        self.up = Linear.init(h, f, key=key + 1, **arg)
+        self.down = Linear.init(f, h, key=key + 2, **arg)
+
+    def forward(self, hidden):
+        return self.down(F.silu(self.gate(hidden)) * self.up(hidden))
+
+
+class Qwen3Layer(torch.nn.Module):
+    def __init__(self, config: Qwen3TextConfig, key: int, device=None) -> None:
+        super().__init__()
+        self.input_norm = RMSNorm(config.hidden_size, config.norm_epsilon, device)
+        self.attention = Qwen3Attention(config, key, device)
+        self.post_attention_norm = RMSNorm(config.hidden_size, config.norm_epsilon, device)
+        self.mlp = Qwen3MLP(config, key + 4, device)
+
+    def forward(self, hidden, cos, sin):
+        hidden = hidden + self.attention(self.input_norm(hidden), cos, sin)
+        return hidden + self.mlp(self.post_attention_norm(hidden))
+
+
+class Qwen3TextEncoder(torch.nn.Module):
+    """Token embedding, decoder layers, final norm, last-token pooling and L2
+    normalisation (every sequence is full length)."""
+
+    def __init__(self, config: Qwen3TextConfig, seed: int = 0, device=None) -> None:
+        super().__init__()
+        self.config = config
+        g = torch.Generator().manual_seed(seed)
+        table = config.initializer_range * torch.randn(config.vocab_size, config.hidden_size,
+                                                       generator=g)
+        self.embedding = torch.nn.Parameter(table.to(device))
+        self.layers = torch.nn.ModuleList(
+            Qwen3Layer(config, seed * 1000 + 10 * (i + 1), device)
+            for i in range(config.num_hidden_layers))
+        self.final_norm = RMSNorm(config.hidden_size, config.norm_epsilon, device)
+        inv = 1.0 / (config.rope_theta ** (torch.arange(0, config.head_dimension, 2,
+                                                        dtype=torch.float32)
+                                           / config.head_dimension))
+        self.register_buffer("inverse_frequency", inv.to(device), persistent=False)
+
+    def rotary(self, sequence: int):
+        pos = torch.arange(sequence, device=self.inverse_frequency.device, dtype=torch.float32)
+        freq = pos[:, None] * self.inverse_frequency[None]
+        emb = torch.cat((freq, freq), dim=-1)
+        return emb.cos()[None], emb.sin()[None]
+
+    def encode(self, input_ids: torch.Tensor, attention_mask=None,
+               compute_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+        del attention_mask  # full-length sequences: the last token is position S - 1
+        hidden = self.embedding[input_ids].to(compute_dtype)
+        cos, sin = self.rotary(input_ids.shape[1])
+        for layer in self.layers:
+            hidden = layer(hidden, cos, sin)
+        pooled = self.final_norm(hidden)[:, -1].float()
+        return pooled / pooled.norm(dim=-1, keepdim=True).clamp_min(1e-12)
+
+
+def build_int4lora_qwen3(config: Qwen3TextConfig, *, rank: int = 32, alpha: float = 64.0,
+                         group_size: int | None = 64, seed: int = 0,
+                         device: torch.device | str = "cuda") -> Qwen3TextEncoder:
+    """Random-init text tower with all seven projections of every layer packed
+    INT4 plus a rank-``rank`` adapter; every other parameter is frozen."""
+
+    model = Qwen3TextEncoder(config, seed=seed, device=device)
+    model = apply_quantized_lora(model, rank=rank, alpha=alpha, key=seed,
+                                 target_pattern=LAYER_LINEARS, group_size=group_size,
+                                 inplace=True)
+    trainable = {id(p) for p in lora_parameters(model)}
+    for p in model.parameters():
+        p.requires_grad_(id(p) in trainable)
+    return model
+
+
 class MNRTrainStep:
     """One AdamW step of the MNR loss on (query, document) token batches.
 
@@ -264,7 +443,7 @@ class MNRTrainStep:
     eagerly before capture).
     """
 
-    def __init__(self, model: BertEncoder, *, batch: int, sequence: int, lr: float = 1e-4,
+    def __init__(self, model: torch.nn.Module, *, batch: int, sequence: int, lr: float = 1e-4,
                  scale: float = 20.0, seed: int = 6) -> None:
         self.model = model
         self.policy = resolve_precision_policy(PrecisionConfig.bfloat16_mixed())
@@ -316,6 +495,10 @@ class MNRTrainStep:
 __all__ = [
     "BertConfig",
     "BertEncoder",
+    "Qwen3TextConfig",
+    "Qwen3TextEncoder",
+    "build_int4lora_qwen3",
+    "causal_attention",
     "LAYER_LINEARS",
     "MNRTrainStep",
     "attention",

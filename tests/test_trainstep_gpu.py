@@ -10,7 +10,8 @@ import pytest
 import torch
 
 from representax_amd import QuantizedLoRALinear, lora_parameters
-from representax_amd.trainstep import BertConfig, MNRTrainStep, build_int4lora_encoder, mnr_loss
+from representax_amd.trainstep import (BertConfig, MNRTrainStep, Qwen3TextConfig,
+                                       build_int4lora_encoder, build_int4lora_qwen3, mnr_loss)
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
@@ -103,8 +104,55 @@ def test_bf16_step_matches_float32_restatement(monkeypatch):
     grads32 = torch.autograd.grad(loss32, params)
     torch.cuda.synchronize()
 
-    assert abs(float(loss) - float(loss32)) < 2e-2 * max(1.0, abs(float(loss32)))
+    assert abs(float(loss.detach()) - float(loss32.detach())) < 2e-2 * max(1.0, abs(float(loss32.detach())))
     num = sum(float((a.float() - b).square().sum()) for a, b in zip(grads, grads32))
     den = sum(float(b.square().sum()) for b in grads32)
     # bf16 activations through two layers versus float32 throughout
+    assert math.sqrt(num / den) < 5e-2
+
+
+QWEN_TINY = Qwen3TextConfig(vocab_size=640, hidden_size=256, num_hidden_layers=2,
+                            num_attention_heads=4, num_key_value_heads=2, head_dimension=64,
+                            intermediate_size=512)
+
+
+def test_qwen3_tower_step_moves_only_lora_masters():
+    model = build_int4lora_qwen3(QWEN_TINY, rank=8, alpha=16.0, group_size=64, seed=2, device=DEV)
+    frozen = _frozen_state(model)
+    lora = lora_parameters(model)
+    assert len(lora) == 2 * 7 * QWEN_TINY.num_hidden_layers
+    before = [p.detach().clone() for p in lora]
+    step = MNRTrainStep(model, batch=4, sequence=64, lr=1e-2)
+    losses = [float(step()) for _ in range(3)]
+    torch.cuda.synchronize()
+    assert all(math.isfinite(v) for v in losses)
+    assert all(not torch.equal(b, a.detach()) for b, a in zip(before, lora))
+    for name, value in _frozen_state(model).items():
+        assert torch.equal(value, frozen[name]), name
+
+
+def test_qwen3_bf16_forward_backward_matches_float32(monkeypatch):
+    model = build_int4lora_qwen3(QWEN_TINY, rank=8, alpha=16.0, group_size=64, seed=4, device=DEV)
+    g = torch.Generator(device="cpu").manual_seed(12)
+    with torch.no_grad():
+        for mod in model.modules():
+            if isinstance(mod, QuantizedLoRALinear):
+                mod.lora_b.copy_(0.05 * torch.randn(mod.lora_b.shape, generator=g))
+    ids = torch.randint(0, QWEN_TINY.vocab_size, (8, 64), generator=g).to(DEV)
+    params = lora_parameters(model)
+    from representax_amd.config import PrecisionConfig
+    from representax_amd.precision import precision_context, resolve_precision_policy
+
+    with precision_context(resolve_precision_policy(PrecisionConfig.bfloat16_mixed())):
+        emb = model.encode(ids)
+        loss = mnr_loss(emb[:4], emb[4:])
+    grads = torch.autograd.grad(loss, params)
+    monkeypatch.setattr(QuantizedLoRALinear, "forward", _fp32_adapter_forward)
+    emb32 = model.encode(ids, compute_dtype=torch.float32)
+    loss32 = mnr_loss(emb32[:4], emb32[4:])
+    grads32 = torch.autograd.grad(loss32, params)
+    torch.cuda.synchronize()
+    assert abs(float(loss.detach()) - float(loss32.detach())) < 2e-2 * max(1.0, abs(float(loss32.detach())))
+    num = sum(float((a.float() - b).square().sum()) for a, b in zip(grads, grads32))
+    den = sum(float(b.square().sum()) for b in grads32)
     assert math.sqrt(num / den) < 5e-2
