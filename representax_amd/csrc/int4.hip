@@ -68,6 +68,84 @@ __global__ void __launch_bounds__(256) k_int4_dequant_any(
   }
 }
 
+// Transposed dequant for groups that are multiples of 32 (and per-row
+// scales): out[k, n] = W_b[n, k]. A block takes 64 rows (n) x 128 columns (k):
+// the packed bytes arrive in LDS with one 16-byte load per thread; each
+// thread then turns one byte column of 8 consecutive rows into two output
+// rows (k even / odd) of 8 consecutive n, stored as 16 bytes each.
+__global__ void __launch_bounds__(256) k_int4_dequant_t32(
+    const uint8_t* __restrict__ packed, const uint16_t* __restrict__ scales,
+    uint16_t* __restrict__ out, int64_t n_rows, int64_t k, int64_t packed_cols,
+    int64_t n_groups, int64_t group, int64_t ld_out) {
+  // 16-byte chunk c of row r sits at chunk c ^ ((r >> 4) & 3), and scale
+  // rows are padded to 5 floats: the byte and scale reads of a wave's eight
+  // row-octets then fall in eight different banks.
+  __shared__ __align__(16) uint8_t pk[64][80];
+  __shared__ float sc[64][5];
+  const int64_t n0 = static_cast<int64_t>(blockIdx.y) * 64;
+  const int64_t k0 = static_cast<int64_t>(blockIdx.x) * 128;
+  const int t = threadIdx.x;
+  {
+    const int r = t >> 2;
+    const int c = t & 3;  // 16-byte chunk: columns k0 + 32 c .. + 31
+    const int64_t n = n0 + r;
+    const int64_t b0 = k0 / 2 + 16 * c;
+    u32x4_t v = {0u, 0u, 0u, 0u};
+    if (n < n_rows) {
+      const uint8_t* src = packed + n * packed_cols + b0;
+      if (b0 + 16 <= packed_cols && (reinterpret_cast<uintptr_t>(src) & 15) == 0) {
+        v = *reinterpret_cast<const u32x4_t*>(src);
+      } else {
+        uint32_t w[4] = {0u, 0u, 0u, 0u};
+        for (int i = 0; i < 16; ++i)
+          if (b0 + i < packed_cols) w[i >> 2] |= static_cast<uint32_t>(src[i]) << (8 * (i & 3));
+        v = u32x4_t{w[0], w[1], w[2], w[3]};
+      }
+    }
+    *reinterpret_cast<u32x4_t*>(&pk[r][16 * (c ^ ((r >> 4) & 3))]) = v;
+    const int64_t kc = k0 + 32 * c;
+    sc[r][c] = (n < n_rows && kc < k) ? bf16_to_f32(scales[n * n_groups + kc / group]) : 0.0f;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int unit = 0; unit < 2; ++unit) {
+    const int o = t & 7;                 // n-octet
+    const int pb = (t >> 3) + 32 * unit;  // byte column = k pair
+    const int64_t ke = k0 + 2 * pb;
+    uint32_t lo4[4], hi4[4];
+#pragma unroll
+    for (int i = 0; i < 8; i += 2) {
+      float ve[2], vo[2];
+#pragma unroll
+      for (int d = 0; d < 2; ++d) {
+        const int r = 8 * o + i + d;
+        const uint32_t byte = pk[r][(((pb >> 4) ^ ((r >> 4) & 3)) << 4) | (pb & 15)] ^ 0x88u;
+        const float s = sc[r][pb >> 4];
+        ve[d] = __builtin_fmaf(static_cast<float>(byte & 0xFu), s, -8.0f * s);
+        vo[d] = __builtin_fmaf(static_cast<float>(byte >> 4), s, -8.0f * s);
+      }
+      lo4[i >> 1] = pack_bf16x2(ve[0], ve[1]);
+      hi4[i >> 1] = pack_bf16x2(vo[0], vo[1]);
+    }
+    const int64_t n = n0 + 8 * o;
+    const bool full = n + 8 <= n_rows && (ld_out & 7) == 0 &&
+                      (reinterpret_cast<uintptr_t>(out) & 15) == 0;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int64_t kk = ke + h;
+      if (kk >= k) continue;
+      const uint32_t* w = h ? hi4 : lo4;
+      uint16_t* dst = out + kk * ld_out + n;
+      if (full) {
+        *reinterpret_cast<u32x4_t*>(dst) = u32x4_t{w[0], w[1], w[2], w[3]};
+      } else {
+        for (int e = 0; e < 8; ++e)
+          if (n + e < n_rows) dst[e] = static_cast<uint16_t>((w[e >> 1] >> (16 * (e & 1))) & 0xFFFFu);
+      }
+    }
+  }
+}
+
 // Transposed dequant: out[k, n] = W_b[n, k], row stride ld_out (>= N).
 // Tile of 64 rows (n) x 64 columns (k) through LDS.
 __global__ void __launch_bounds__(256) k_int4_dequant_t(
@@ -231,6 +309,12 @@ hipError_t launch_int4_dequant_t(const uint8_t* packed, const uint16_t* scales, 
                                  int64_t n, int64_t k, int64_t packed_cols, int64_t n_groups,
                                  int64_t group, int64_t ld_out, hipStream_t stream) {
   if (n == 0 || k == 0) return hipSuccess;
+  if (group % 32 == 0) {
+    dim3 grid(static_cast<unsigned>(ceil_div(k, 128)), static_cast<unsigned>(ceil_div(n, 64)));
+    hipLaunchKernelGGL(k_int4_dequant_t32, grid, dim3(256), 0, stream, packed, scales, out, n, k,
+                       packed_cols, n_groups, group, ld_out);
+    return hipGetLastError();
+  }
   dim3 grid(static_cast<unsigned>(ceil_div(k, 64)), static_cast<unsigned>(ceil_div(n, 64)));
   hipLaunchKernelGGL(k_int4_dequant_t, grid, dim3(256), 0, stream, packed, scales, out, n, k,
                      packed_cols, n_groups, group, ld_out);
