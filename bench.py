@@ -425,10 +425,14 @@ def run_qwen3(steps=6, warmup=2):
     return line
 
 
-def run_skinny(batch=96):
-    """Per-call GPU latency of the skinny-M forward: a HIP graph of `batch`
-    calls cycling through a pool of weight copies larger than the 256 MB
-    Infinity Cache, so every call streams its packed weight from HBM."""
+def run_skinny(batch=96, latency_calls=64):
+    """Skinny-M INT4 (group 64) + LoRA r32 forward on the Qwen3-2B projection
+    shapes. `us_per_call`: GPU time per call inside a HIP graph of `batch`
+    calls that cycle through a pool of weight copies larger than the 256 MB
+    Infinity Cache, so every call streams its packed weight from HBM.
+    `p50_us`: median over `latency_calls` single eager calls (HIP events
+    around each, weights cycling the same way). HBM bytes: packed weight,
+    group scales, A, B, x and y."""
 
     import torch
 
@@ -436,13 +440,13 @@ def run_skinny(batch=96):
 
     dev = torch.device("cuda:0")
     g = np.random.Generator(np.random.PCG64(5))
-    r = 32
+    r, group = 32, 64
     out = []
     for k, n in SKINNY_SHAPES:
-        per_copy = n * k // 2 + n * 2 + (r * k + n * r) * 2
+        per_copy = n * k // 2 + n * (k // group) * 2 + (r * k + n * r) * 2
         copies = max(8, int(np.ceil(300e6 / per_copy)))
         w = torch.from_numpy((g.standard_normal((n, k)) * 0.02).astype(np.float32)).to(dev)
-        packed, scales = ops.int4_pack(w)
+        packed, scales = ops.int4_pack(w, group_size=group)
         del w
         a0 = bf16_tensor(g.standard_normal((r, k)).astype(np.float32) * 0.02, dev)
         b0 = bf16_tensor(g.standard_normal((n, r)).astype(np.float32) * 0.02, dev)
@@ -452,18 +456,29 @@ def run_skinny(batch=96):
             calls = []
             for i in range(batch):
                 p, s, a, b = pool[i % copies]
-                calls.append(lambda p=p, s=s, a=a, b=b: ops.int4lora_forward(x, p, s, a, b,
-                                                                             scaling=1.0))
+                calls.append(lambda p=p, s=s, a=a, b=b: ops.int4lora_forward(
+                    x, p, s, a, b, scaling=2.0, group_size=group))
             us = graph_time_per_call_ms(calls, replays=3) * 1e3
-            nbytes = n * k / 2 + n * 2 + (r * k + n * r) * 2 + m * k * 2 + m * n * 2
+            lat = []
+            for i in range(latency_calls):
+                fn = calls[(i * 7) % batch]
+                e0 = torch.cuda.Event(enable_timing=True)
+                e1 = torch.cuda.Event(enable_timing=True)
+                e0.record()
+                fn()
+                e1.record()
+                e1.synchronize()
+                lat.append(e0.elapsed_time(e1) * 1e3)
+            nbytes = n * k / 2 + n * (k // group) * 2 + (r * k + n * r) * 2 + m * k * 2 + m * n * 2
             out.append({"m": m, "k": k, "n": n, "us_per_call": round(us, 2),
+                        "p50_us": round(float(np.median(lat)), 2),
                         "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
                         "frac_hbm": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
         del pool
         torch.cuda.empty_cache()
-    return {"workload": "skinny-M INT4+LoRA forward (rank 32, per-row scales); mean GPU time "
-                        "per call over a HIP graph of 96 calls cycling through weight copies "
-                        "> 256 MB", "points": out}
+    return {"workload": "skinny-M INT4 (group 64) + LoRA r32 forward, Qwen3-2B projection shapes; "
+                        "us_per_call inside a HIP graph of 96 calls cycling weight copies > 256 MB, "
+                        "p50_us over single eager calls", "points": out}
 
 
 def main():

@@ -98,8 +98,9 @@ bool lora_fast_shape(int dtype, int64_t k, int64_t n_groups, int64_t group, int6
   return true;
 }
 
-bool lora_skinny(int dtype, int64_t m, int64_t k, int64_t n_groups, int64_t group, int64_t rank) {
-  return dtype == kBF16 && skinny_ok(m, k, rank, n_groups, group);
+bool lora_skinny(int dtype, int64_t m, int64_t n, int64_t k, int64_t n_groups, int64_t group,
+                 int64_t rank) {
+  return dtype == kBF16 && skinny_ok(m, n, k, rank, n_groups, group);
 }
 
 template <typename A>
@@ -261,7 +262,7 @@ size_t rpx_int4lora_forward_workspace(int64_t m, int64_t n, int64_t k, int64_t g
     g = group_size;
   }
   Sizer s;
-  plan_forward(s, lora_fast_shape(dtype, k, ng, g, rank), lora_skinny(dtype, m, k, ng, g, rank), m,
+  plan_forward(s, lora_fast_shape(dtype, k, ng, g, rank), lora_skinny(dtype, m, n, k, ng, g, rank), m,
                n, k, rank);
   return s.used;
 }
@@ -292,7 +293,7 @@ int rpx_int4lora_forward(const void* x, int dtype, int64_t m, int64_t k, const u
   const bool fast = lora_fast_shape(dtype, k, ng, g, rank) && aligned16(x) && aligned16(packed) &&
                     aligned16(lora_a) && aligned16(y);
   Arena arena(workspace, workspace_bytes);
-  if (lora_skinny(dtype, m, k, ng, g, rank) && aligned16(x) && aligned16(packed) &&
+  if (lora_skinny(dtype, m, n, k, ng, g, rank) && aligned16(x) && aligned16(packed) &&
       aligned16(lora_a)) {
     float* ws = arena.take<float>(skinny_workspace_floats(m, n, k, rank));
     if (arena.overflow) return fail_invalid("rpx_int4lora_forward: workspace too small");

@@ -57,7 +57,7 @@ bool gemm_fast_path_ok(int64_t k, int64_t lda, int64_t ldb_elems, const void* a,
                        int64_t ldc, const void* out);
 
 // Skinny-M (M <= 64) INT4 + LoRA forward -------------------------------------
-bool skinny_ok(int64_t m, int64_t k, int64_t rank, int64_t n_groups, int64_t group);
+bool skinny_ok(int64_t m, int64_t n, int64_t k, int64_t rank, int64_t n_groups, int64_t group);
 int64_t skinny_workspace_floats(int64_t m, int64_t n, int64_t k, int64_t rank);
 hipError_t launch_skinny_forward(const uint16_t* x, int64_t m, int64_t k, const Int4Operand& w,
                                  int64_t n, const uint16_t* lora_a, const uint16_t* lora_b,

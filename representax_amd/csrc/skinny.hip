@@ -1,16 +1,27 @@
 // Skinny-M INT4 + LoRA forward (M <= 64 tokens): the memory-bound inference
 // regime where every call streams the whole packed weight for a few rows.
 //
-// Launch 1 (k_skinny_partials), two kinds of blocks:
-//   weight blocks  (64 rows of W x one K chunk): x[:, chunk] staged in LDS,
-//                  each wave streams 16 rows with 16-byte loads, dequantizes
-//                  exactly (bf16(q*s)) and runs v_mfma_f32_16x16x32_bf16 with
-//                  the weights as the row operand; fp32 partial sums go to
-//                  part_w[chunk][m][n].
-//   adapter blocks (one K chunk of h = x A^T): fp32 partials part_h[chunk][m][j].
-// Launch 2 (k_skinny_finish): fixed-order sums of the partials, then the
-// reference's rounding points: h = bf16(.), base = bf16(.),
-// a = bf16(h B^T), y = bf16(base + bf16(a * c)) (+ bias).
+// One launch. Blocks of 4 waves:
+//   adapter blocks (one per K split, first in the grid): fp32 partials of
+//     h = x A^T over the split's columns;
+//   weight blocks (row tile x K split): every wave issues all of its 16-byte
+//     packed-weight loads (and their scales) before any arithmetic, so the
+//     whole weight is in flight at once; then dequantizes exactly
+//     (bf16(q * s)) and runs v_mfma_f32_16x16x32_bf16 with the weight rows as
+//     the row operand and x as the column operand. Waves that split the
+//     block's K range are reduced through LDS in a fixed order.
+// Partials go to the workspace through device-coherent stores. Arrival
+// counters (a small per-device array, one slot per call in flight) pick the
+// finisher of each row tile: the last of the tile's K-split blocks, which
+// waits (bounded) until every adapter block has arrived, sums the partials in
+// split order and applies the reference's rounding points: h = bf16(.),
+// base = bf16(.), t = bf16(h B^T), y = bf16(base + bf16(t * c)) (+ bias,
+// rounded again). Results do not depend on arrival order. Calls take the
+// counter slots in turn, so at most kSlots calls may run at once on a device
+// (kernels of one stream never overlap).
+#include <atomic>
+#include <cstdlib>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -18,14 +29,41 @@ namespace rpx {
 
 namespace {
 
-constexpr int kRowsPerBlock = 64;  // 4 waves x 16 rows
-constexpr int kMaxVec = 4;         // 16-byte weight vectors per lane per chunk (kc <= 512)
+constexpr int kMaxTiles = 1024;
+constexpr int kSlots = 8;
+constexpr int kAdapterSpan = 256;  // columns of x A^T per adapter block
+constexpr int kSpinLimit = 1 << 22;
 
-__device__ __forceinline__ bf16x8_t as_bf16x8(u32x4_t v) {
-  return __builtin_bit_cast(bf16x8_t, v);
-}
+struct SkinnyParams {
+  const uint16_t* x;  // [M, K] bf16
+  int m;
+  int rank;
+  int64_t k, n;
+  const uint8_t* packed;   // [N, K/2]
+  int64_t pcols;
+  const uint16_t* scales;  // [N, n_groups] bf16
+  int64_t n_groups;
+  int group_shift;         // log2(group) when n_groups > 1
+  int b_vec;               // lora_b rows load as 16-byte vectors
+  const uint16_t* lora_a;  // [r, K] bf16
+  const uint16_t* lora_b;  // [N, r] bf16
+  float scale;
+  const uint16_t* bias;    // [N] bf16 bits or null
+  uint16_t* y;             // [M, N]
+  uint16_t* h;             // [M, r]
+  int64_t tiles;           // row tiles
+  int64_t splits;          // K splits of the weight
+  int64_t kspan;           // columns per weight split
+  int64_t a_splits;        // adapter blocks (kAdapterSpan columns each)
+  float* part_w;           // [splits][tiles][frags][64][4]
+  float* part_h;           // [a_splits][4][MB][64][4]
+  int slot;               // counter slot of this call
+};
 
-// Exact dequant of one packed dword (8 nibbles) into 4 bf16 pairs.
+__device__ __forceinline__ bf16x8_t as_bf16x8(u32x4_t v) { return __builtin_bit_cast(bf16x8_t, v); }
+
+// Exact dequant of one packed dword (8 nibbles, k ascending) into 4 bf16
+// pairs: bf16((nibble ^ 8) * s - 8 s), the product being exact in fp32.
 __device__ __forceinline__ void dequant8_exact(uint32_t word, float s, float m8s, uint32_t* o) {
   const uint32_t x = word ^ 0x88888888u;
   const uint32_t lo = x & 0x0F0F0F0Fu;
@@ -38,217 +76,517 @@ __device__ __forceinline__ void dequant8_exact(uint32_t word, float s, float m8s
   }
 }
 
-struct SkinnyArgs {
-  const uint16_t* x;   // [M, K] bf16
-  int64_t m, k, n;
-  const uint8_t* packed;  // [N, K/2]
-  const uint16_t* scales; // [N, n_groups]
-  int64_t n_groups;
-  int group_shift;        // log2(group) when n_groups > 1
-  const uint16_t* lora_a; // [r, K] bf16
-  int64_t rank;
-  int64_t kc;             // K chunk (multiple of 128)
-  int64_t splits;         // number of K chunks
-  int64_t w_blocks_n;     // ceil(N / 64)
-  float* part_w;          // [splits][M][N]
-  float* part_h;          // [splits][M][r]
-};
+// Arrival counters, one slot per call in flight (calls take the slots in
+// turn): [0] adapter blocks, [1] finished tiles, [2 + t] K splits of tile t.
+// They are zero when the module loads and every call leaves its slot at zero.
+__device__ unsigned int g_skinny_counters[kSlots][kMaxTiles + 2];
 
-template <int MB>
-__global__ void __launch_bounds__(256) k_skinny_partials(SkinnyArgs a) {
-  extern __shared__ __align__(16) uint16_t xs[];  // [MB*16][kc + 8]
+// One arrival; true for the last of `target`, which puts the word back to 0.
+__device__ __forceinline__ bool arrive(unsigned int* word, unsigned int target) {
+  const unsigned int old = __hip_atomic_fetch_add(word, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (old + 1u != target) return false;
+  __hip_atomic_store(word, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return true;
+}
+
+__device__ __forceinline__ u32x4_t load16(const void* p) {
+  return *reinterpret_cast<const u32x4_t*>(p);
+}
+
+// Partial sums cross blocks through agent-scope (device-coherent) 64-bit
+// stores and loads instead of plain accesses plus a release/acquire fence
+// pair: on this target an agent-scope release fence writes back the whole
+// L2 of the XCD, which at one fence per block costs more than the weight
+// stream itself. A coherent store has reached the coherence point once the
+// wave's vmcnt drains (drain_stores), before the block's arrival is counted.
+__device__ __forceinline__ void store_coherent(f32x4_t* dst, f32x4_t v) {
+  unsigned long long* d = reinterpret_cast<unsigned long long*>(dst);
+  const u32x4_t u = __builtin_bit_cast(u32x4_t, v);
+  __hip_atomic_store(d, static_cast<unsigned long long>(u[0]) | (static_cast<unsigned long long>(u[1]) << 32),
+                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(d + 1, static_cast<unsigned long long>(u[2]) | (static_cast<unsigned long long>(u[3]) << 32),
+                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ f32x4_t load_coherent(const f32x4_t* src) {
+  unsigned long long* s = reinterpret_cast<unsigned long long*>(const_cast<f32x4_t*>(src));
+  const unsigned long long a = __hip_atomic_load(s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const unsigned long long b = __hip_atomic_load(s + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return __builtin_bit_cast(f32x4_t, u32x4_t{static_cast<uint32_t>(a), static_cast<uint32_t>(a >> 32),
+                                             static_cast<uint32_t>(b), static_cast<uint32_t>(b >> 32)});
+}
+__device__ __forceinline__ void drain_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// x fragment for MFMA column m, columns [k, k + 8); zero past the last row.
+__device__ __forceinline__ u32x4_t x_frag(const SkinnyParams& p, int m, int64_t k) {
+  const int mc = m < p.m ? m : p.m - 1;
+  const u32x4_t v = load16(p.x + static_cast<int64_t>(mc) * p.k + k);
+  return m < p.m ? v : u32x4_t{0u, 0u, 0u, 0u};
+}
+
+// Weight block: rows [tile * 16 T WR, +16 T WR) x columns of `split`.
+// Wave (wr, wk) takes rows wr * 16 T + [0, 16 T) and columns
+// split * kspan + wk * 128 U + [0, 128 U). Within a 128-column unit, lane
+// (rl, g) loads row rl's bytes for columns 32 g + [0, 32), and MFMA step st
+// consumes its columns 32 g + 8 st + [0, 8), matched by the x fragment.
+// Branch-free: units past K read a clamped address and are zeroed, so every
+// load of the wave is issued before the first wait.
+template <int MB, int T, int U, int WK>
+__device__ __forceinline__ void weight_part(const SkinnyParams& p, int64_t tile, int64_t split,
+                                            f32x4_t* red, uint16_t* b_lds) {
+  constexpr int WR = 4 / WK;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int64_t ld = a.kc + 8;
-  const int64_t weight_blocks = a.w_blocks_n * a.splits;
-  const bool is_weight = blockIdx.x < weight_blocks;
-  const int64_t bid = is_weight ? blockIdx.x : blockIdx.x - weight_blocks;
-  const int64_t split = is_weight ? bid / a.w_blocks_n : bid;
-  const int64_t k0 = split * a.kc;
-  int64_t k1 = k0 + a.kc;
-  if (k1 > a.k) k1 = a.k;
-  const int64_t klen = k1 - k0;
-
-  // stage x[:, k0:k1] (rows >= M are zero)
-  const int64_t vecs = static_cast<int64_t>(MB) * 16 * (klen / 8);
-  for (int64_t v = tid; v < vecs; v += 256) {
-    const int64_t row = v / (klen / 8);
-    const int64_t c = (v % (klen / 8)) * 8;
-    const u32x4_t val = row < a.m ? *reinterpret_cast<const u32x4_t*>(a.x + row * a.k + k0 + c)
-                                  : u32x4_t{0u, 0u, 0u, 0u};
-    *reinterpret_cast<u32x4_t*>(xs + row * ld + c) = val;
-  }
-  __syncthreads();
-
+  const int wr = wave / WK;
+  const int wk = wave % WK;
   const int rl = lane & 15;
   const int g = lane >> 4;
-  if (is_weight) {
-    const int64_t n_blk = bid % a.w_blocks_n;
-    const int64_t row = n_blk * kRowsPerBlock + wave * 16 + rl;
-    const bool row_ok = row < a.n;
-    const uint8_t* wrow = a.packed + (row_ok ? row : 0) * (a.k / 2);
-    float s_row = 0.0f;
-    if (a.n_groups == 1 && row_ok) s_row = bf16_to_f32(a.scales[row]);
-    f32x4_t acc[MB];
+  const int64_t row0 = tile * (16 * T * WR) + wr * (16 * T);
+  const int64_t kw = split * p.kspan + wk * (128 * U);
+
+  u32x4_t wv[T][U];
+  float sv[T][U];
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    const int64_t nblk128 = klen / 128;  // <= kMaxVec
-    u32x4_t wv[kMaxVec];
-    float sv[kMaxVec];
+  for (int t = 0; t < T; ++t) {
+    const int64_t row = row0 + 16 * t + rl;
+    const bool row_ok = row < p.n;
+    const int64_t rc = row_ok ? row : p.n - 1;
+    const uint8_t* wrow = p.packed + rc * p.pcols;
+    const uint16_t* srow = p.scales + rc * p.n_groups;
 #pragma unroll
-    for (int b = 0; b < kMaxVec; ++b) {
-      const int64_t kb = k0 + b * 128;
-      const bool ok = row_ok && b < nblk128;
-      wv[b] = ok ? *reinterpret_cast<const u32x4_t*>(wrow + (kb + 32 * g) / 2)
-                 : u32x4_t{0u, 0u, 0u, 0u};
-      sv[b] = s_row;
-      if (a.n_groups > 1)
-        sv[b] = ok ? bf16_to_f32(a.scales[row * a.n_groups + ((kb + 32 * g) >> a.group_shift)])
-                   : 0.0f;
+    for (int u = 0; u < U; ++u) {
+      const bool ok = row_ok && kw + 128 * u < p.k;
+      const int64_t kk = ok ? kw + 128 * u + 32 * g : 0;
+      const u32x4_t v = load16(wrow + kk / 2);
+      wv[t][u] = ok ? v : u32x4_t{0u, 0u, 0u, 0u};
+      const float s = bf16_to_f32(srow[p.n_groups == 1 ? 0 : (kk >> p.group_shift)]);
+      sv[t][u] = ok ? s : 0.0f;
     }
+  }
+  u32x4_t xf[U][4][MB];
 #pragma unroll
-    for (int b = 0; b < kMaxVec; ++b) {
-      if (b >= nblk128) break;
-      const int64_t kb = k0 + b * 128;
-      const float s = sv[b];
-      const float m8s = -8.0f * s;
+  for (int u = 0; u < U; ++u) {
+    const bool uok = kw + 128 * u < p.k;
+    const int64_t kb = uok ? kw + 128 * u : 0;
+#pragma unroll
+    for (int st = 0; st < 4; ++st)
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        const u32x4_t v = x_frag(p, 16 * mb + rl, kb + 32 * g + 8 * st);
+        xf[u][st][mb] = uok ? v : u32x4_t{0u, 0u, 0u, 0u};
+      }
+  }
+
+  // the tile's rows of B, for the block that ends up finishing the tile
+  constexpr int ROWS = 16 * T * WR;
+  constexpr int BV = (ROWS * 8 + 255) / 256;
+  const int r = p.rank;
+  const int per_row = r / 8;
+  u32x4_t bv[BV];
+#pragma unroll
+  for (int i = 0; i < BV; ++i) {
+    const int v = tid + 256 * i;
+    const int brow = per_row > 0 ? v / per_row : 0;
+    const int64_t n = tile * ROWS + brow;
+    const bool ok = p.b_vec && v < ROWS * per_row && n < p.n;
+    const u32x4_t w = load16(p.lora_b + (ok ? n * r + 8 * (v - brow * per_row) : 0));
+    bv[i] = ok ? w : u32x4_t{0u, 0u, 0u, 0u};
+  }
+
+  f32x4_t acc[T][MB];
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) acc[t][mb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const float s = sv[t][u];
       uint32_t dq[16];
 #pragma unroll
-      for (int d = 0; d < 4; ++d) dequant8_exact(wv[b][d], s, m8s, dq + 4 * d);
-      const uint16_t* xb = xs + (kb - k0) + 32 * g;
+      for (int d = 0; d < 4; ++d) dequant8_exact(wv[t][u][d], s, -8.0f * s, dq + 4 * d);
 #pragma unroll
       for (int st = 0; st < 4; ++st) {
-        const bf16x8_t af = as_bf16x8(u32x4_t{dq[4 * st], dq[4 * st + 1], dq[4 * st + 2],
-                                              dq[4 * st + 3]});
+        const bf16x8_t af =
+            as_bf16x8(u32x4_t{dq[4 * st], dq[4 * st + 1], dq[4 * st + 2], dq[4 * st + 3]});
 #pragma unroll
-        for (int mb = 0; mb < MB; ++mb) {
-          const bf16x8_t xf =
-              *reinterpret_cast<const bf16x8_t*>(xb + (mb * 16 + rl) * ld + 8 * st);
-          acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, xf, acc[mb], 0, 0, 0);
-        }
+        for (int mb = 0; mb < MB; ++mb)
+          acc[t][mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, as_bf16x8(xf[u][st][mb]),
+                                                              acc[t][mb], 0, 0, 0);
       }
     }
-    // D[n][m]: lane -> m = 16*mb + (lane & 15), n = 4*(lane >> 4) + v
-    float* out = a.part_w + split * a.m * a.n;
-    const int64_t nb = n_blk * kRowsPerBlock + wave * 16 + 4 * g;
+  }
+
+  if (p.b_vec) {
+#pragma unroll
+    for (int i = 0; i < BV; ++i) {
+      const int v = tid + 256 * i;
+      if (v < ROWS * per_row) {
+        const int brow = v / per_row;
+        *reinterpret_cast<u32x4_t*>(b_lds + brow * (r + 8) + 8 * (v - brow * per_row)) = bv[i];
+      }
+    }
+  }
+
+  if constexpr (WK > 1) {
+    if (wk > 0) {
+#pragma unroll
+      for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+          red[((((wk - 1) * WR + wr) * T + t) * MB + mb) * 64 + lane] = acc[t][mb];
+    }
+    __syncthreads();
+    if (wk == 0) {
+#pragma unroll
+      for (int j = 1; j < WK; ++j)
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+#pragma unroll
+          for (int mb = 0; mb < MB; ++mb)
+            acc[t][mb] += red[((((j - 1) * WR + wr) * T + t) * MB + mb) * 64 + lane];
+    }
+  }
+  if (wk == 0) {
+    constexpr int F = WR * T * MB;
+    f32x4_t* dst = reinterpret_cast<f32x4_t*>(p.part_w) + (split * p.tiles + tile) * F * 64;
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+        if (16 * mb + rl < p.m) store_coherent(dst + ((wr * T + t) * MB + mb) * 64 + lane, acc[t][mb]);
+  }
+}
+
+// Adapter block: fp32 partial of h[m, j] = sum_k x[m, k] A[j, k] over
+// columns [a_split * 256, +256); wave w takes j in [16 w, 16 w + 16). The
+// lane holds D[j = 16 w + 4 g + v][m = 16 mb + rl].
+template <int MB>
+__device__ __forceinline__ void adapter_part(const SkinnyParams& p, int64_t a_split) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int rl = lane & 15;
+  const int g = lane >> 4;
+  if (16 * wave >= p.rank) return;
+  const int j = 16 * wave + rl;
+  const bool jok = j < p.rank;
+  const uint16_t* arow = p.lora_a + static_cast<int64_t>(jok ? j : p.rank - 1) * p.k;
+  const int64_t k0 = a_split * kAdapterSpan;
+  u32x4_t av[kAdapterSpan / 32];
+  u32x4_t xv[kAdapterSpan / 32][MB];
+#pragma unroll
+  for (int s = 0; s < kAdapterSpan / 32; ++s) {
+    const bool ok = k0 + 32 * s < p.k;
+    const int64_t kk = ok ? k0 + 32 * s + 8 * g : 0;
+    const u32x4_t v = load16(arow + kk);
+    av[s] = ok && jok ? v : u32x4_t{0u, 0u, 0u, 0u};
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
-      const int64_t mm = mb * 16 + rl;
-      if (mm >= a.m) continue;
-      float* dst = out + mm * a.n + nb;
-      if (nb + 3 < a.n && (a.n % 4 == 0)) {
-        *reinterpret_cast<f32x4_t*>(dst) = acc[mb];
-      } else {
-        for (int v = 0; v < 4; ++v)
-          if (nb + v < a.n) dst[v] = acc[mb][v];
-      }
+      const u32x4_t w = x_frag(p, 16 * mb + rl, kk);
+      xv[s][mb] = ok ? w : u32x4_t{0u, 0u, 0u, 0u};
     }
-    return;
   }
-  // adapter block: partial h[m, j] over this chunk; A[:, chunk] is staged in
-  // LDS behind x (all loads issued together), wave w handles j in
-  // [16 w, 16 w + 16) (rank <= 64)
-  uint16_t* as = xs + static_cast<int64_t>(MB) * 16 * ld;
-  const int64_t avecs = a.rank * (klen / 8);
-  for (int64_t v = tid; v < avecs; v += 256) {
-    const int64_t jr = v / (klen / 8);
-    const int64_t c = (v % (klen / 8)) * 8;
-    *reinterpret_cast<u32x4_t*>(as + jr * ld + c) =
-        *reinterpret_cast<const u32x4_t*>(a.lora_a + jr * a.k + k0 + c);
-  }
-  __syncthreads();
-  const int64_t j = wave * 16 + rl;
   f32x4_t acc[MB];
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  if (wave * 16 < a.rank) {
-    for (int64_t kk = 0; kk < klen; kk += 32) {
-      u32x4_t av = u32x4_t{0u, 0u, 0u, 0u};
-      if (j < a.rank) av = *reinterpret_cast<const u32x4_t*>(as + j * ld + kk + 8 * g);
 #pragma unroll
-      for (int mb = 0; mb < MB; ++mb) {
-        const bf16x8_t xf = *reinterpret_cast<const bf16x8_t*>(xs + (mb * 16 + rl) * ld + kk + 8 * g);
-        acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(av), xf, acc[mb], 0, 0, 0);
-      }
+  for (int s = 0; s < kAdapterSpan / 32; ++s)
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+      acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(av[s]), as_bf16x8(xv[s][mb]),
+                                                       acc[mb], 0, 0, 0);
+  f32x4_t* dst = reinterpret_cast<f32x4_t*>(p.part_h) + a_split * (4 * MB * 64);
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+    if (16 * mb + rl < p.m) store_coherent(dst + (wave * MB + mb) * 64 + lane, acc[mb]);
+}
+
+// Outputs of one row tile. Each lane sums (in split order) the weight
+// fragments it would have written and, in waves below rank / 16, the h
+// fragments; both sets of loads issue from one loop. h = bf16(.) goes to LDS
+// (row stride rank + 1); the tile's rows of B are in LDS (row stride rank + 8)
+// when they load as vectors.
+template <int MB, int T, int WK>
+__device__ __forceinline__ void finish_tile(const SkinnyParams& p, int64_t tile, float* h_lds,
+                                            const uint16_t* b_lds, bool poison) {
+  constexpr int WR = 4 / WK;
+  constexpr int F = WR * T * MB;
+  constexpr int FI = (F + 3) / 4;
+  constexpr int ROWS = 16 * T * WR;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int rl = lane & 15;
+  const int g = lane >> 4;
+  const int r = p.rank;
+  const bool h_wave = 16 * wave < r;
+  const f32x4_t* part = reinterpret_cast<const f32x4_t*>(p.part_w);
+  const f32x4_t* part_h = reinterpret_cast<const f32x4_t*>(p.part_h);
+  f32x4_t wacc[FI];
+  f32x4_t hacc[MB];
+#pragma unroll
+  for (int i = 0; i < FI; ++i) wacc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) hacc[mb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  const int64_t rounds = p.splits > p.a_splits ? p.splits : p.a_splits;
+  const int hw = h_wave ? wave : 0;
+#pragma unroll 8
+  for (int64_t sp = 0; sp < rounds; ++sp) {
+    const int64_t sw = sp < p.splits ? sp : p.splits - 1;
+    const int64_t sh = sp < p.a_splits ? sp : p.a_splits - 1;
+    f32x4_t vw[FI];
+    f32x4_t vh[MB];
+#pragma unroll
+    for (int i = 0; i < FI; ++i) {
+      const int f = wave + 4 * i < F ? wave + 4 * i : 0;
+      vw[i] = load_coherent(part + ((sw * p.tiles + tile) * F + f) * 64 + lane);
     }
-    float* out = a.part_h + split * a.m * a.rank;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) vh[mb] = load_coherent(part_h + (sh * 4 * MB + hw * MB + mb) * 64 + lane);
+    if (sp < p.splits) {
+#pragma unroll
+      for (int i = 0; i < FI; ++i) wacc[i] += vw[i];
+    }
+    if (sp < p.a_splits) {
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) hacc[mb] += vh[mb];
+    }
+  }
+  if (h_wave) {
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
-      const int64_t mm = mb * 16 + rl;
-      if (mm >= a.m) continue;
+      const int m = 16 * mb + rl;
+      if (m >= p.m) continue;
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const int64_t jj = wave * 16 + 4 * g + v;
-        if (jj < a.rank) out[mm * a.rank + jj] = acc[mb][v];
+        const int j = 16 * wave + 4 * g + v;
+        if (j < r) h_lds[m * (r + 1) + j] = poison ? __builtin_nanf("") : round_bf16(hacc[mb][v]);
       }
+    }
+  }
+  __syncthreads();
+  if (tile == 0) {
+    for (int idx = tid; idx < p.m * r; idx += 256) {
+      const int m = idx / r;
+      p.h[idx] = f32_to_bf16(h_lds[m * (r + 1) + (idx - m * r)]);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < FI; ++i) {
+    const int f = wave + 4 * i;
+    if (f >= F) break;
+    const int mb = f % MB;
+    const int t = (f / MB) % T;
+    const int wr = f / (MB * T);
+    const int m = 16 * mb + rl;
+    if (m >= p.m) continue;
+    const int lrow0 = wr * (16 * T) + 16 * t + 4 * g;
+    const int64_t n0 = tile * ROWS + lrow0;
+    const float* hrow = h_lds + m * (r + 1);
+    uint16_t o[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int64_t n = n0 + v;
+      if (n >= p.n) break;
+      float tt = 0.0f;
+      if (p.b_vec) {
+        const uint16_t* brow = b_lds + (lrow0 + v) * (r + 8);
+        for (int j = 0; j < r; j += 8) {
+          const u32x4_t b8 = *reinterpret_cast<const u32x4_t*>(brow + j);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            tt = __builtin_fmaf(hrow[j + 2 * e], bf16lo_to_f32(b8[e]), tt);
+            tt = __builtin_fmaf(hrow[j + 2 * e + 1], bf16hi_to_f32(b8[e]), tt);
+          }
+        }
+      } else {
+        const uint16_t* brow = p.lora_b + n * r;
+        for (int j = 0; j < r; ++j) tt = __builtin_fmaf(hrow[j], bf16_to_f32(brow[j]), tt);
+      }
+      float out = round_bf16(round_bf16(wacc[i][v]) + round_bf16(round_bf16(tt) * p.scale));
+      if (p.bias != nullptr) out = round_bf16(out + bf16_to_f32(p.bias[n]));
+      o[v] = f32_to_bf16(out);
+    }
+    uint16_t* dst = p.y + static_cast<int64_t>(m) * p.n + n0;
+    if (n0 + 3 < p.n && (p.n & 3) == 0 && (reinterpret_cast<uintptr_t>(p.y) & 7) == 0) {
+      *reinterpret_cast<u32x2_t*>(dst) =
+          u32x2_t{static_cast<uint32_t>(o[0]) | (static_cast<uint32_t>(o[1]) << 16),
+                  static_cast<uint32_t>(o[2]) | (static_cast<uint32_t>(o[3]) << 16)};
+    } else {
+      for (int v = 0; v < 4 && n0 + v < p.n; ++v) dst[v] = o[v];
     }
   }
 }
 
-// One block per (m, 256-column slab): h row from its partials (fixed order),
-// then each thread finishes one output element.
-__global__ void __launch_bounds__(256)
-    k_skinny_finish(const float* __restrict__ part_w, const float* __restrict__ part_h,
-                    int64_t splits, int64_t m_rows, int64_t n, int64_t rank,
-                    const uint16_t* __restrict__ lora_b, float scale,
-                    const uint16_t* __restrict__ bias, uint16_t* __restrict__ y,
-                    uint16_t* __restrict__ h) {
-  __shared__ float hrow[64];
-  const int64_t mm = blockIdx.y;
-  const int tid = threadIdx.x;
-  if (tid < rank) {
-    float s = 0.0f;
-    for (int64_t i = 0; i < splits; ++i) s += part_h[(i * m_rows + mm) * rank + tid];
-    const float hb = round_bf16(s);
-    hrow[tid] = hb;
-    if (blockIdx.x == 0) h[mm * rank + tid] = f32_to_bf16(hb);
+// Bounded wait (lane 0 of the block) until all adapter blocks of this call
+// have arrived. Adapter blocks come first in the grid and are dispatched
+// before any weight block, and none of them waits on anything, so the wait
+// ends as soon as they finish; the spin limit only guarantees that every
+// wave exits. Returns false if the limit was hit.
+__device__ __forceinline__ bool wait_adapters(const unsigned int* word, unsigned int target) {
+  for (int it = 0; it < kSpinLimit; ++it) {
+    if (__hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == target) return true;
+    __builtin_amdgcn_s_sleep(2);
   }
-  __syncthreads();
-  const int64_t col = static_cast<int64_t>(blockIdx.x) * 256 + tid;
-  if (col >= n) return;
-  float s = 0.0f;
-#pragma unroll 8
-  for (int64_t i = 0; i < splits; ++i) s += part_w[(i * m_rows + mm) * n + col];
-  const float base = round_bf16(s);
-  float t = 0.0f;
-  for (int64_t jj = 0; jj < rank; ++jj)
-    t = __builtin_fmaf(hrow[jj], bf16_to_f32(lora_b[col * rank + jj]), t);
-  float out = round_bf16(base + round_bf16(round_bf16(t) * scale));
-  if (bias != nullptr) out = round_bf16(out + bf16_to_f32(bias[col]));
-  y[mm * n + col] = f32_to_bf16(out);
+  return false;
 }
 
-struct SkinnyPlan {
-  int64_t kc, splits, w_blocks_n, mb;
+template <int MB, int T, int U, int WK>
+__global__ void __launch_bounds__(256) k_skinny(SkinnyParams p) {
+  constexpr int WR = 4 / WK;
+  constexpr int kRed = WK > 1 ? (WK - 1) * WR * T * MB * 64 : 1;
+  __shared__ f32x4_t red[kRed];
+  __shared__ float h_lds[64 * 65];
+  __shared__ __align__(16) uint16_t b_lds[16 * T * WR * 72];
+  __shared__ int flag;
+  const int tid = threadIdx.x;
+  unsigned int* ctr = g_skinny_counters[p.slot];
+  const unsigned int a_target = static_cast<unsigned int>(p.a_splits);
+  if (static_cast<int64_t>(blockIdx.x) < p.a_splits) {
+    adapter_part<MB>(p, blockIdx.x);
+    drain_stores();
+    __syncthreads();
+    if (tid == 0) __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
+  const int64_t b = static_cast<int64_t>(blockIdx.x) - p.a_splits;
+  const int64_t split = b / p.tiles;
+  const int64_t tile = b - split * p.tiles;
+  weight_part<MB, T, U, WK>(p, tile, split, red, b_lds);
+  drain_stores();
+  __syncthreads();
+  if (tid == 0) {
+    // the adapter word is read together with the arrival (one round trip);
+    // it only grows until every finisher is past its wait
+    const unsigned int adapters = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    int last = arrive(ctr + 2 + tile, static_cast<unsigned int>(p.splits)) ? 1 : 0;
+    if (last && adapters != a_target && !wait_adapters(ctr, a_target)) last = 2;
+    flag = last;
+  }
+  __syncthreads();
+  const int state = flag;
+  if (state == 0) return;
+  // one lane of another wave counts the finished tile while the block works;
+  // the last one returns the adapter word to zero
+  unsigned int done_old = 0;
+  if (tid == 64)
+    done_old = __hip_atomic_fetch_add(ctr + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // state 2: the adapters never arrived within the spin limit; h is poisoned
+  finish_tile<MB, T, WK>(p, tile, h_lds, b_lds, state == 2);
+  if (tid == 64 && done_old + 1u == static_cast<unsigned int>(p.tiles)) {
+    __hip_atomic_store(ctr + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// (id, T, U, WK): wave = 16 T rows x 128 U columns; block = 4 / WK waves of
+// rows x WK waves of columns.
+#define RPX_SKINNY_CONFIGS(X) \
+  X(1, 1, 1, 4)               \
+  X(2, 1, 2, 4)               \
+  X(3, 1, 4, 4)               \
+  X(4, 1, 2, 1)               \
+  X(5, 1, 4, 1)               \
+  X(6, 2, 2, 1)               \
+  X(7, 2, 2, 2)               \
+  X(8, 4, 2, 1)               \
+  X(9, 2, 4, 1)               \
+  X(10, 1, 8, 1)              \
+  X(11, 1, 2, 2)              \
+  X(12, 1, 4, 2)              \
+  X(13, 1, 1, 2)              \
+  X(14, 2, 1, 4)
+
+struct SkinnyCfg {
+  int id, t, u, wk;
 };
 
-SkinnyPlan plan_skinny(int64_t m, int64_t n, int64_t k) {
+constexpr SkinnyCfg kSkinnyCfgs[] = {
+#define RPX_SKINNY_ENTRY(id, T, U, WK) {id, T, U, WK},
+    RPX_SKINNY_CONFIGS(RPX_SKINNY_ENTRY)
+#undef RPX_SKINNY_ENTRY
+};
+
+struct SkinnyPlan {
+  SkinnyCfg cfg;
+  int64_t mb, tiles, splits, kspan, a_splits;
+};
+
+SkinnyPlan make_plan(const SkinnyCfg& c, int64_t m, int64_t n, int64_t k) {
   SkinnyPlan p;
+  p.cfg = c;
   p.mb = (m + 15) / 16;
-  p.w_blocks_n = ceil_div(n, kRowsPerBlock);
-  const int64_t k128 = k / 128;
-  int64_t want = ceil_div(1024, p.w_blocks_n);  // ~4 blocks per CU
-  if (want > k128) want = k128;
-  if (want < 1) want = 1;
-  // chunk <= kMaxVec * 128 columns (weight vectors held in registers)
-  while (ceil_div(k128, want) > kMaxVec) ++want;
-  p.kc = ceil_div(k128, want) * 128;
-  p.splits = ceil_div(k, p.kc);
+  const int64_t rows = 16 * c.t * (4 / c.wk);
+  p.kspan = 128 * c.u * c.wk;
+  p.tiles = ceil_div(n, rows);
+  p.splits = ceil_div(k, p.kspan);
+  p.a_splits = ceil_div(k, kAdapterSpan);
   return p;
+}
+
+// Tile shape. A call is latency-bound: block dispatch, the weight stream's
+// round trip, the partials' coherent stores, one arrival and the finisher's
+// loads each cost a device round trip, so the shapes differ mainly in how
+// many blocks they dispatch and how long the finisher's reductions are.
+// Measured on the three Qwen3-2B projection shapes for M in {1, 4, 16, 64}:
+// 64-row tiles with 512-column splits (two row waves x two column waves) are
+// best or within 5% except for single-block M with K >= N, where 32-row
+// tiles with 1024-column splits win. RPX_SKINNY_TILE=<id> forces a shape.
+SkinnyPlan plan_skinny(int64_t m, int64_t n, int64_t k) {
+  const char* env = std::getenv("RPX_SKINNY_TILE");
+  int want = env != nullptr ? std::atoi(env) : 0;
+  if (want <= 0) want = ((m + 15) / 16 == 1 && k >= n) ? 12 : 7;
+  for (const SkinnyCfg& c : kSkinnyCfgs) {
+    const SkinnyPlan p = make_plan(c, m, n, k);
+    if (c.id == want && p.tiles <= kMaxTiles) return p;
+  }
+  // unknown id or too many tiles: the first shape that fits
+  for (const SkinnyCfg& c : kSkinnyCfgs) {
+    const SkinnyPlan p = make_plan(c, m, n, k);
+    if (p.tiles <= kMaxTiles) return p;
+  }
+  return make_plan(kSkinnyCfgs[0], m, n, k);
+}
+
+int64_t frags_per_tile(const SkinnyPlan& p) { return (4 / p.cfg.wk) * p.cfg.t * p.mb; }
+
+
+std::atomic<unsigned int> g_calls{0};
+
+template <int MB, int T, int U, int WK>
+void launch_cfg(const SkinnyParams& a, hipStream_t stream) {
+  const unsigned blocks = static_cast<unsigned>(a.tiles * a.splits + a.a_splits);
+  hipLaunchKernelGGL((k_skinny<MB, T, U, WK>), dim3(blocks), dim3(256), 0, stream, a);
+}
+
+template <int MB>
+bool launch_mb(int id, const SkinnyParams& a, hipStream_t stream) {
+  switch (id) {
+#define RPX_SKINNY_CASE(cid, T, U, WK) \
+  case cid:                            \
+    launch_cfg<MB, T, U, WK>(a, stream); \
+    return true;
+    RPX_SKINNY_CONFIGS(RPX_SKINNY_CASE)
+#undef RPX_SKINNY_CASE
+    default:
+      return false;
+  }
 }
 
 }  // namespace
 
-bool skinny_ok(int64_t m, int64_t k, int64_t rank, int64_t n_groups, int64_t group) {
+bool skinny_ok(int64_t m, int64_t n, int64_t k, int64_t rank, int64_t n_groups, int64_t group) {
   if (m < 1 || m > 64 || k % 128 != 0 || rank < 1 || rank > 64) return false;
   if (n_groups > 1 && (group < 32 || (group & (group - 1)) != 0)) return false;
-  return true;
+  return plan_skinny(m, n, k).tiles <= kMaxTiles;
 }
 
 int64_t skinny_workspace_floats(int64_t m, int64_t n, int64_t k, int64_t rank) {
+  (void)rank;
   const SkinnyPlan p = plan_skinny(m, n, k);
-  return p.splits * m * n + p.splits * m * rank + 64;
+  return p.splits * p.tiles * frags_per_tile(p) * 256 + p.a_splits * 4 * p.mb * 256;
 }
 
 hipError_t launch_skinny_forward(const uint16_t* x, int64_t m, int64_t k, const Int4Operand& w,
@@ -256,59 +594,42 @@ hipError_t launch_skinny_forward(const uint16_t* x, int64_t m, int64_t k, const 
                                  int64_t rank, float scale, const uint16_t* bias, uint16_t* y,
                                  uint16_t* h, float* ws, hipStream_t stream) {
   const SkinnyPlan p = plan_skinny(m, n, k);
-  SkinnyArgs a;
+  if (p.tiles > kMaxTiles) return hipErrorInvalidValue;
+  SkinnyParams a;
   a.x = x;
-  a.m = m;
+  a.m = static_cast<int>(m);
+  a.rank = static_cast<int>(rank);
   a.k = k;
   a.n = n;
   a.packed = w.packed;
+  a.pcols = w.packed_cols;
   a.scales = w.scales;
   a.n_groups = w.n_groups;
   a.group_shift = 0;
   if (w.n_groups > 1)
     while ((int64_t{1} << a.group_shift) < w.group) ++a.group_shift;
+  a.b_vec = (rank % 8 == 0 && (reinterpret_cast<uintptr_t>(lora_b) & 15) == 0) ? 1 : 0;
   a.lora_a = lora_a;
-  a.rank = rank;
-  a.kc = p.kc;
+  a.lora_b = lora_b;
+  a.scale = scale;
+  a.bias = bias;
+  a.y = y;
+  a.h = h;
+  a.tiles = p.tiles;
   a.splits = p.splits;
-  a.w_blocks_n = p.w_blocks_n;
+  a.kspan = p.kspan;
+  a.a_splits = p.a_splits;
   a.part_w = ws;
-  a.part_h = ws + p.splits * m * n;
-  const unsigned blocks = static_cast<unsigned>(p.w_blocks_n * p.splits + p.splits);
-  // x rows (16 * mb) and, for the adapter blocks, up to 64 rows of A
-  const size_t lds = static_cast<size_t>(p.mb * 16 + rank) * (p.kc + 8) * sizeof(uint16_t);
-  static bool attr_set[4] = {false, false, false, false};
-  const void* kerns[4] = {reinterpret_cast<const void*>(k_skinny_partials<1>),
-                          reinterpret_cast<const void*>(k_skinny_partials<2>),
-                          reinterpret_cast<const void*>(k_skinny_partials<3>),
-                          reinterpret_cast<const void*>(k_skinny_partials<4>)};
-  const int ki = static_cast<int>(p.mb) - 1;
-  if (!attr_set[ki]) {
-    // up to (64 + 64) rows x (512 + 8) bf16 = 133 KB
-    hipError_t e = hipFuncSetAttribute(kerns[ki], hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       160 * 1024);
-    if (e != hipSuccess) return e;
-    attr_set[ki] = true;
-  }
+  a.part_h = a.part_w + p.splits * p.tiles * frags_per_tile(p) * 256;
+  a.slot = static_cast<int>(g_calls.fetch_add(1, std::memory_order_relaxed) % kSlots);
+  bool ok = false;
   switch (p.mb) {
-    case 1:
-      hipLaunchKernelGGL(k_skinny_partials<1>, dim3(blocks), dim3(256), lds, stream, a);
-      break;
-    case 2:
-      hipLaunchKernelGGL(k_skinny_partials<2>, dim3(blocks), dim3(256), lds, stream, a);
-      break;
-    case 3:
-      hipLaunchKernelGGL(k_skinny_partials<3>, dim3(blocks), dim3(256), lds, stream, a);
-      break;
-    default:
-      hipLaunchKernelGGL(k_skinny_partials<4>, dim3(blocks), dim3(256), lds, stream, a);
-      break;
+    case 1: ok = launch_mb<1>(p.cfg.id, a, stream); break;
+    case 2: ok = launch_mb<2>(p.cfg.id, a, stream); break;
+    case 3: ok = launch_mb<3>(p.cfg.id, a, stream); break;
+    default: ok = launch_mb<4>(p.cfg.id, a, stream); break;
   }
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  const dim3 grid(static_cast<unsigned>(ceil_div(n, 256)), static_cast<unsigned>(m));
-  hipLaunchKernelGGL(k_skinny_finish, grid, dim3(256), 0, stream, a.part_w, a.part_h, p.splits, m,
-                     n, rank, lora_b, scale, bias, y, h);
+  if (!ok) return hipErrorInvalidValue;
   return hipGetLastError();
 }
 

@@ -227,3 +227,61 @@ def test_skinny_forward_matches_oracle(m, k, n, r, group, bias):
     torch.cuda.synchronize()
     assert rel_l2(from_dev(h), h_o) < TOL
     assert rel_l2(from_dev(y), y_o) < TOL
+
+
+SKINNY_TILE_IDS = list(range(1, 15))
+
+
+@pytest.mark.parametrize("tile", SKINNY_TILE_IDS)
+@pytest.mark.parametrize("m,k,n,r,group", [(3, 1024, 200, 32, 64), (40, 640, 136, 16, None)])
+def test_skinny_every_tile_shape_matches_oracle(monkeypatch, tile, m, k, n, r, group):
+    """Each row-tile x K-split shape of the one-launch skinny kernel, including
+    ragged last tiles and last splits."""
+
+    monkeypatch.setenv("RPX_SKINNY_TILE", str(tile))
+    x, packed, scales, a, b, bias_bits, _ = _lora_case(m, k, n, r, group, seed=tile + m, bias=True)
+    y_o, h_o = olora.lora_forward(x, packed, scales, a, b, alpha=2.0 * r, rank=r,
+                                  bias_bits=bias_bits, group_size=group)
+    biasd = to_dev(bias_bits.view(np.int16)).view(torch.uint16)
+    y, h = ops.int4lora_forward(to_dev_bf16(x), to_dev(packed),
+                                to_dev(scales.view(np.int16)).view(torch.uint16), to_dev_bf16(a),
+                                to_dev_bf16(b), scaling=2.0, group_size=group, bias_bits=biasd)
+    torch.cuda.synchronize()
+    assert rel_l2(from_dev(h), h_o) < TOL
+    assert rel_l2(from_dev(y), y_o) < TOL
+
+
+def test_skinny_graph_replays_and_repeats_are_bit_identical():
+    """The per-tile arrival counters return to their resting value after each
+    call: eager repeats and graph replays give the same bits."""
+
+    m, k, n, r = 8, 2048, 1536, 32
+    x, packed, scales, a, b, bias_bits, _ = _lora_case(m, k, n, r, 64, seed=91, bias=False)
+    xd, pd = to_dev_bf16(x), to_dev(packed)
+    sd = to_dev(scales.view(np.int16)).view(torch.uint16)
+    ad, bd = to_dev_bf16(a), to_dev_bf16(b)
+
+    def call():
+        return ops.int4lora_forward(xd, pd, sd, ad, bd, scaling=1.0, group_size=64)
+
+    y0, h0 = call()
+    y1, h1 = call()
+    torch.cuda.synchronize()
+    assert torch.equal(y0, y1) and torch.equal(h0, h1)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        call()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        yg, hg = call()
+    for _ in range(4):
+        yg.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(yg, y0) and torch.equal(hg, h0)
+        # eager work between replays reuses the allocator's blocks
+        ye, _ = call()
+        torch.cuda.synchronize()
+        assert torch.equal(ye, y0)
