@@ -49,8 +49,11 @@ def parse_args():
     p.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a HIP graph")
     p.add_argument("--no-secondary", action="store_true")
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--only", choices=["fp8", "int4lora", "skinny", "bert", "qwen3"], default=None,
-                   help="run one workload and nothing else (profiling)")
+    p.add_argument("--only", choices=["fp8", "int4lora", "skinny", "bert", "qwen3", "fp8gemm",
+                                      "copyref"], default=None,
+                   help="run one workload and nothing else (profiling); fp8gemm: three eager "
+                        "launches of each fp8 GEMM call of one step; copyref: a plain 256 MiB "
+                        "device copy, the reference for scaling FETCH_SIZE / WRITE_SIZE")
     return p.parse_args()
 
 
@@ -145,23 +148,6 @@ def graph_time_per_call_ms(calls, replays=5):
     return start.elapsed_time(end) / (replays * len(calls))
 
 
-def event_time_ms(fn, reps):
-    """Per-call GPU duration of fn (HIP events on the current stream)."""
-
-    import torch
-
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    fn()
-    torch.cuda.synchronize()
-    start.record()
-    for _ in range(reps):
-        fn()
-    end.record()
-    end.synchronize()
-    return start.elapsed_time(end) / reps
-
-
 # ---------------------------------------------------------------------------
 # FP8 workload (primary)
 # ---------------------------------------------------------------------------
@@ -192,9 +178,9 @@ def fp8_flops(tokens):
     return sum(6.0 * tokens * k * n for _, k, n in BERT_LINEARS)
 
 
-def fp8_gemm_roofline(layers, reps=20):
-    """Dominant kernel: the fp8 MFMA GEMMs of one step, launched on the same
-    codes the step produces; achieved = algorithmic FLOPs / event time."""
+def fp8_gemm_calls(layers):
+    """The 18 fp8 GEMM calls of one step (forward, dX, dW per linear) on the
+    codes and scales the step produces, with their algorithmic FLOPs."""
 
     import torch
 
@@ -216,13 +202,39 @@ def fp8_gemm_roofline(layers, reps=20):
         calls.append((lambda a=qgt, b=qxt, sa=s_x, sb=s_g: ops.fp8_gemm(a, "e5m2", sa, b, "e4m3fn", sb),
                       2.0 * m * n * k))
     torch.cuda.synchronize()
+    return calls
+
+
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "fp8_gemm_bert_shapes_hbm_traffic.md")
+
+
+def profiled_traffic():
+    """HBM bytes per fp8 GEMM call from the committed --pmc summary (FETCH_SIZE
+    and WRITE_SIZE of the 18 calls, scaled by a plain copy's reading), or
+    None when the summary is absent."""
+
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            for line in f:
+                if line.startswith("hbm_bytes_per_call:"):
+                    return float(line.split(":", 1)[1])
+    except OSError:
+        return None
+    return None
+
+
+def fp8_gemm_roofline(layers, reps=16):
+    """Dominant kernel: the fp8 MFMA GEMM calls of one step (k_fp8_gemm, plus
+    the split-K reduce for the calls that use one). Each call is timed as GPU
+    time per call inside a HIP graph of `reps` launches (HIP events on the
+    capturing stream); achieved = algorithmic FLOPs of the 18 calls / their
+    summed time."""
+
+    calls = fp8_gemm_calls(layers)
     total_ms = 0.0
     total_flops = 0.0
-    per_call = []
     for fn, flops in calls:
-        ms = event_time_ms(fn, reps)
-        per_call.append(ms)
-        total_ms += ms
+        total_ms += graph_time_per_call_ms([fn] * reps, replays=3)
         total_flops += flops
     achieved = total_flops / (total_ms * 1e-3) / 1e12
     return {
@@ -231,11 +243,46 @@ def fp8_gemm_roofline(layers, reps=20):
         "peak": FP8_PEAK_TFLOPS,
         "unit": "TFLOP/s",
         "frac": round(achieved / FP8_PEAK_TFLOPS, 4),
-        "traffic": None,
-        "kernel": "k_fp8_gemm (fwd e4m3xe4m3, dX e5m2xe4m3, dW e5m2xe4m3; 18 launches/step)",
+        "traffic": profiled_traffic(),
+        "kernel": "k_fp8_gemm (+ k_fp8_split_reduce where split-K): fwd e4m3xe4m3, dX e5m2xe4m3, "
+                  "dW e5m2xe4m3; 18 calls per step",
         "avg_launch_us": round(1e3 * total_ms / len(calls), 2),
         "flops_per_launch_avg": total_flops / len(calls),
+        "algorithmic_bytes_per_launch_avg": fp8_gemm_bytes(layers) / len(calls),
     }
+
+
+def fp8_gemm_bytes(layers):
+    """Compulsory HBM bytes of the 18 GEMM calls: fp8 operands read once, bf16
+    outputs (dX) and f32 outputs (dW) written once."""
+
+    total = 0.0
+    for _, x, _, _, k, n in layers:
+        m = x.shape[0]
+        total += m * k + n * k + m * n * 2          # forward: x, W codes; y bf16
+        total += m * n + n * k + m * k * 2          # dX: g, W^T codes; dX bf16
+        total += m * n + m * k + n * k * 4          # dW: g^T, x^T codes; dW f32
+    return total
+
+
+def run_fp8gemm_only(layers):
+    import torch
+
+    for fn, _ in fp8_gemm_calls(layers):
+        for _ in range(3):
+            fn()
+    torch.cuda.synchronize()
+
+
+def run_copyref(nbytes=256 << 20):
+    import torch
+
+    src = torch.ones(nbytes // 4, dtype=torch.float32, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copyref_bytes_each_way": nbytes, "launches": 3}))
 
 
 def fp8_cpu_baseline(seed=1):
@@ -510,6 +557,12 @@ def main():
         return
     if args.only == "qwen3":
         print(json.dumps(run_qwen3()))
+        return
+    if args.only == "copyref":
+        run_copyref()
+        return
+    if args.only == "fp8gemm":
+        run_fp8gemm_only(fp8_setup(args.tokens, dev))
         return
 
     log("fp8: setting up inputs")
