@@ -605,15 +605,15 @@ int rpx_fp8_gemm(const uint8_t* a, int fmt_a, const float* scale_a, const uint8_
 namespace {
 template <typename A>
 void plan_fp8_forward(A& a, int64_t m, int64_t n, int64_t k) {
-  a.template take<uint32_t>(fp8_amax_partials(m * k));
-  a.template take<uint32_t>(fp8_amax_partials(k * n));
+  a.template take<uint32_t>(fp8_quant_partials(m, k));
+  a.template take<uint32_t>(fp8_quant_partials(k, n));
   a.template take<uint8_t>(m * k);
   a.template take<uint8_t>(n * k);
   a.template take<uint8_t>(rpx_fp8_gemm_workspace(m, n, k));
 }
 template <typename A>
 void plan_fp8_backward(A& a, int64_t m, int64_t n, int64_t k) {
-  a.template take<uint32_t>(fp8_amax_partials(m * n));
+  a.template take<uint32_t>(fp8_quant_partials(m, n));
   a.template take<float>(1);
   a.template take<uint8_t>(m * n);  // g codes [M, N]
   a.template take<uint8_t>(n * m);  // g codes [N, M]
@@ -651,27 +651,20 @@ int rpx_fp8_linear_forward(const void* left, int left_dtype, int64_t m, int64_t 
     return fail_invalid("rpx_fp8_linear_forward: null pointer");
   hipStream_t st = static_cast<hipStream_t>(stream);
   Arena ar(workspace, workspace_bytes);
-  const int64_t npl = fp8_amax_partials(m * k);
-  const int64_t npr = fp8_amax_partials(k * n);
-  uint32_t* pl = ar.take<uint32_t>(npl);
-  uint32_t* pr = ar.take<uint32_t>(npr);
+  uint32_t* pl = ar.take<uint32_t>(fp8_quant_partials(m, k));
+  uint32_t* pr = ar.take<uint32_t>(fp8_quant_partials(k, n));
   uint8_t* ql = ar.take<uint8_t>(m * k);
   uint8_t* qr = ar.take<uint8_t>(n * k);
   const size_t gws = rpx_fp8_gemm_workspace(m, n, k);
   uint8_t* gw = ar.take<uint8_t>(static_cast<int64_t>(gws));
   if (ar.overflow) return fail_invalid("rpx_fp8_linear_forward: workspace too small");
-  RPX_HIP(launch_fp8_amax(left, left_dtype, m * k, pl, npl, kE4M3FN, nullptr, st),
-          "fp8_linear_forward: amax(left)");
-  RPX_HIP(launch_fp8_amax(right, right_dtype, k * n, pr, npr, kE4M3FN, nullptr, st),
-          "fp8_linear_forward: amax(right)");
-  // left [M, K] -> codes [M, K] (+ [K, M] for the weight gradient)
-  RPX_HIP(launch_fp8_cast(left, left_dtype, m, k, k, 1, nullptr, pl, npl, scales_out, kE4M3FN, ql,
-                          left_t_codes, st),
-          "fp8_linear_forward: cast(left)");
+  // both tensors' amaxes in one launch, then both casts in one launch:
+  // left [M, K] -> codes [M, K] (+ [K, M] for the weight gradient);
   // right [K, N] -> codes [N, K] for this product (+ [K, N] for the input gradient)
-  RPX_HIP(launch_fp8_cast(right, right_dtype, k, n, right_row_stride, right_col_stride, nullptr, pr,
-                          npr, scales_out + 1, kE4M3FN, right_codes, qr, st),
-          "fp8_linear_forward: cast(right)");
+  RPX_HIP(launch_fp8_quantize2(left, left_dtype, m, k, k, 1, pl, scales_out, ql, left_t_codes,
+                               right, right_dtype, k, n, right_row_stride, right_col_stride, pr,
+                               scales_out + 1, right_codes, qr, kE4M3FN, st),
+          "fp8_linear_forward: quantize");
   return rpx_fp8_gemm(ql, kE4M3FN, scales_out, qr, kE4M3FN, scales_out + 1, m, n, k, out,
                       out_dtype, gw, gws, stream);
 }
@@ -696,8 +689,7 @@ int rpx_fp8_linear_backward_codes(const uint8_t* left_t_codes, const uint8_t* ri
     return fail_invalid("rpx_fp8_linear_backward: null pointer");
   hipStream_t st = static_cast<hipStream_t>(stream);
   Arena ar(workspace, workspace_bytes);
-  const int64_t npg = fp8_amax_partials(m * n);
-  uint32_t* pg = ar.take<uint32_t>(npg);
+  uint32_t* pg = ar.take<uint32_t>(fp8_quant_partials(m, n));
   float* sg = ar.take<float>(1);
   uint8_t* qg = ar.take<uint8_t>(m * n);
   uint8_t* qgt = ar.take<uint8_t>(n * m);
@@ -711,11 +703,10 @@ int rpx_fp8_linear_backward_codes(const uint8_t* left_t_codes, const uint8_t* ri
   uint8_t* gw = ar.take<uint8_t>(static_cast<int64_t>(gws));
   if (ar.overflow) return fail_invalid("rpx_fp8_linear_backward: workspace too small");
   // s_g (e5m2) and the gradient codes in the layouts the two products need
-  RPX_HIP(launch_fp8_amax(grad, grad_dtype, m * n, pg, npg, kE5M2, nullptr, st),
-          "fp8_linear_backward: amax(grad)");
-  RPX_HIP(launch_fp8_cast(grad, grad_dtype, m, n, n, 1, nullptr, pg, npg, sg, kE5M2,
-                          d_left ? qg : nullptr, d_right ? qgt : nullptr, st),
-          "fp8_linear_backward: cast(grad)");
+  RPX_HIP(launch_fp8_quantize2(grad, grad_dtype, m, n, n, 1, pg, sg, d_left ? qg : nullptr,
+                               d_right ? qgt : nullptr, nullptr, grad_dtype, 0, 0, 0, 1, nullptr,
+                               nullptr, nullptr, nullptr, kE5M2, st),
+          "fp8_linear_backward: quantize(grad)");
   // d_left [M, K] = ((g . right^T) * s_g) * s_r
   if (d_left != nullptr)
     RPX_TRY(rpx_fp8_gemm(qg, kE5M2, sg, right_codes, kE4M3FN, scales + 1, m, k, n, d_left,
@@ -748,7 +739,7 @@ int rpx_fp8_linear_backward(const void* left, int left_dtype, const void* right,
   // re-quantize the operands with the forward scales (same values, same
   // amax), into the tail of the workspace that the code path reserves
   Arena ar(workspace, workspace_bytes);
-  ar.take<uint32_t>(fp8_amax_partials(m * n));
+  ar.take<uint32_t>(fp8_quant_partials(m, n));
   ar.take<float>(1);
   ar.take<uint8_t>(m * n);
   ar.take<uint8_t>(n * m);

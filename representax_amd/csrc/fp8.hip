@@ -20,7 +20,7 @@ namespace rpx {
 
 namespace {
 
-constexpr int kAmaxBlocks = 512;
+constexpr int kAmaxBlocks = 1024;
 
 __device__ __forceinline__ uint32_t abs_bits_f32(float f) {
   return __builtin_bit_cast(uint32_t, f) & 0x7FFFFFFFu;
@@ -42,26 +42,34 @@ __device__ __forceinline__ uint32_t block_reduce_max(uint32_t v, uint32_t* sh) {
   return r;
 }
 
-// Dense buffer of numel elements (any logical layout).
-__global__ void __launch_bounds__(256)
-    k_amax_partial(const void* __restrict__ t, int dtype, int64_t numel,
-                   uint32_t* __restrict__ partials) {
-  __shared__ uint32_t sh[4];
+// One amax problem: a dense buffer of numel elements (any logical layout)
+// reduced by `blocks` workgroups into per-block partials.
+struct AmaxPart {
+  const void* t;
+  int dtype;
+  int64_t numel;
+  uint32_t* partials;
+  int64_t blocks;
+};
+
+__device__ __forceinline__ void amax_body(const AmaxPart& a, int64_t block, uint32_t* sh) {
   uint32_t m = 0;
-  const int64_t tid = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
-  if (dtype == kBF16) {
-    const uint16_t* p = static_cast<const uint16_t*>(t);
+  const int64_t tid = block * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+  const int64_t stride = a.blocks * blockDim.x;
+  const int64_t numel = a.numel;
+  if (a.dtype == kBF16) {
+    const uint16_t* p = static_cast<const uint16_t*>(a.t);
     const bool al = (reinterpret_cast<uintptr_t>(p) & 15) == 0;
     const int64_t nvec = al ? numel / 8 : 0;
     const u32x4_t* pv = reinterpret_cast<const u32x4_t*>(p);
     int64_t i = tid;
-    for (; i + 3 * stride < nvec; i += 4 * stride) {
-      u32x4_t w[4];
+    // eight 16-byte loads in flight per thread
+    for (; i + 7 * stride < nvec; i += 8 * stride) {
+      u32x4_t w[8];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) w[u] = pv[i + u * stride];
+      for (int u = 0; u < 8; ++u) w[u] = pv[i + u * stride];
 #pragma unroll
-      for (int u = 0; u < 4; ++u)
+      for (int u = 0; u < 8; ++u)
 #pragma unroll
         for (int e = 0; e < 4; ++e) m = umax(m, umax(w[u][e] & 0x7FFFu, (w[u][e] >> 16) & 0x7FFFu));
     }
@@ -74,19 +82,41 @@ __global__ void __launch_bounds__(256)
       m = umax(m, static_cast<uint32_t>(p[j] & 0x7FFFu));
     m <<= 16;
   } else {
-    const float* p = static_cast<const float*>(t);
+    const float* p = static_cast<const float*>(a.t);
     const bool al = (reinterpret_cast<uintptr_t>(p) & 15) == 0;
     const int64_t nvec = al ? numel / 4 : 0;
     const u32x4_t* pv = reinterpret_cast<const u32x4_t*>(p);
-    for (int64_t i = tid; i < nvec; i += stride) {
+    int64_t i = tid;
+    for (; i + 3 * stride < nvec; i += 4 * stride) {
+      u32x4_t w[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) w[u] = pv[i + u * stride];
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) m = umax(m, w[u][e] & 0x7FFFFFFFu);
+    }
+    for (; i < nvec; i += stride) {
       const u32x4_t w = pv[i];
 #pragma unroll
       for (int e = 0; e < 4; ++e) m = umax(m, w[e] & 0x7FFFFFFFu);
     }
-    for (int64_t i = nvec * 4 + tid; i < numel; i += stride) m = umax(m, abs_bits_f32(p[i]));
+    for (int64_t j = nvec * 4 + tid; j < numel; j += stride) m = umax(m, abs_bits_f32(p[j]));
   }
   m = block_reduce_max(m, sh);
-  if (threadIdx.x == 0) partials[blockIdx.x] = m;
+  if (threadIdx.x == 0) a.partials[block] = m;
+}
+
+// Up to two amax problems in one launch: blocks [0, a0.blocks) take the
+// first, the rest the second.
+__global__ void __launch_bounds__(256) k_amax_partial(AmaxPart a0, AmaxPart a1) {
+  __shared__ uint32_t sh[4];
+  const int64_t b = blockIdx.x;
+  if (b < a0.blocks) {
+    amax_body(a0, b, sh);
+  } else {
+    amax_body(a1, b - a0.blocks, sh);
+  }
 }
 
 __global__ void __launch_bounds__(256)
@@ -119,6 +149,39 @@ __device__ __forceinline__ uint32_t encode(float v, int fmt) {
 // infinities and |v| > fmax take the integer encoder, which has the
 // non-saturating overflow behaviour. Agreement with the integer encoder over
 // every f32 bit pattern is checked by rpx_fp8_encode_selfcheck.
+// Code of a value outside [-fmax, fmax] (or NaN), equal to the integer
+// encoder there: NaN keeps its sign with mantissa 0x7F; e4m3fn rounds
+// (448, 464] down to 448 (the tie goes to the even code 0x7E) and overflows
+// to NaN above; e5m2 rounds (57344, 61440) down to 57344 and overflows to
+// inf from 61440 (the tie goes to the even, infinite code).
+__device__ __forceinline__ uint32_t encode_outside(float v, int fmt) {
+  const uint32_t sign = (__builtin_bit_cast(uint32_t, v) >> 24) & 0x80u;
+  const float a = __builtin_fabsf(v);
+  if (!(a == a)) return sign | 0x7Fu;
+  if (fmt == kE4M3FN) return sign | (a <= 464.0f ? 0x7Eu : 0x7Fu);
+  return sign | (a < 61440.0f ? 0x7Bu : 0x7Cu);
+}
+
+template <int FMT>
+__device__ __forceinline__ uint32_t encode_outside_t(float v) {
+  const uint32_t sign = (__builtin_bit_cast(uint32_t, v) >> 24) & 0x80u;
+  const float a = __builtin_fabsf(v);
+  const uint32_t big = FMT == kE4M3FN ? (a <= 464.0f ? 0x7Eu : 0x7Fu) : (a < 61440.0f ? 0x7Bu : 0x7Cu);
+  return sign | (a == a ? big : 0x7Fu);
+}
+
+// encode2 for a compile-time format, branch-free.
+template <int FMT>
+__device__ __forceinline__ uint32_t encode2_t(float a, float b) {
+  constexpr float fmax = FMT == kE4M3FN ? 448.0f : 57344.0f;
+  const uint32_t hw = FMT == kE4M3FN
+                          ? static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false))
+                          : static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_bf8_f32(a, b, 0, false));
+  const uint32_t lo = __builtin_fabsf(a) <= fmax ? (hw & 0xFFu) : encode_outside_t<FMT>(a);
+  const uint32_t hi = __builtin_fabsf(b) <= fmax ? ((hw >> 8) & 0xFFu) : encode_outside_t<FMT>(b);
+  return lo | (hi << 8);
+}
+
 __device__ __forceinline__ uint32_t encode2(float a, float b, int fmt) {
   uint32_t r;
   float fmax;
@@ -129,9 +192,28 @@ __device__ __forceinline__ uint32_t encode2(float a, float b, int fmt) {
     r = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_bf8_f32(a, b, 0, false)) & 0xFFFFu;
     fmax = 57344.0f;
   }
-  if (!(__builtin_fabsf(a) <= fmax)) r = (r & 0xFF00u) | encode(a, fmt);
-  if (!(__builtin_fabsf(b) <= fmax)) r = (r & 0x00FFu) | (encode(b, fmt) << 8);
+  if (!(__builtin_fabsf(a) <= fmax)) r = (r & 0xFF00u) | encode_outside(a, fmt);
+  if (!(__builtin_fabsf(b) <= fmax)) r = (r & 0x00FFu) | (encode_outside(b, fmt) << 8);
   return r;
+}
+
+// x / s for the cast, branch-free, for 1e-30 <= s <= 1e30: the Markstein
+// sequence of div_rn (q = x r, one fma correction). |x| < 2^-60 is scaled by
+// 2^64 first so the residual stays normal, which keeps the quotient
+// correctly rounded wherever it is a normal number; below that it is an fp8
+// zero of the right sign either way. An overflowing product (inf - inf in
+// the correction) becomes the infinity the exact quotient rounds to. A NaN
+// input is returned as is (the correction's negation would flip its sign),
+// and so is a signed zero (the correction's +0 + -0 would lose the sign).
+__device__ __forceinline__ float div_cast(float x, float s, float r) {
+  const bool tiny = __builtin_fabsf(x) < 0x1p-60f;
+  const float xs = tiny ? x * 0x1p64f : x;
+  float q = xs * r;
+  const float e = __builtin_fmaf(-q, s, xs);
+  q = __builtin_fmaf(e, r, q);
+  q = tiny ? q * 0x1p-64f : q;
+  q = q != q ? __builtin_copysignf(__builtin_inff(), x) : q;
+  return (x != x || x == 0.0f) ? x : q;
 }
 
 __device__ __forceinline__ float load_val(const void* t, int dtype, int64_t idx) {
@@ -143,7 +225,7 @@ __device__ __forceinline__ float load_val(const void* t, int dtype, int64_t idx)
 // the amax partials (every block reduces them; block 0 also publishes it).
 __device__ __forceinline__ float resolve_scale(const float* scale, const uint32_t* partials,
                                                int64_t n_partials, float fmax, float* scale_out,
-                                               float* sh) {
+                                               float* sh, bool publish) {
   if (partials == nullptr) return scale[0];
   uint32_t m = 0;
   for (int64_t i = threadIdx.x; i < n_partials; i += blockDim.x) m = umax(m, partials[i]);
@@ -159,91 +241,294 @@ __device__ __forceinline__ float resolve_scale(const float* scale, const uint32_
       s = s > tiny ? s : tiny;
     }
     *sh = s;
-    if (scale_out != nullptr && blockIdx.x == 0 && blockIdx.y == 0) scale_out[0] = s;
+    if (scale_out != nullptr && publish) scale_out[0] = s;
   }
   __syncthreads();
   return *sh;
 }
 
-// Row-major input [rows, cols] (unit column stride, ld % 8 == 0, 16-byte
-// aligned): a 64 x 64 tile per block, 2 x 8 contiguous elements per thread.
-// All loads are issued before the scale reduction and the conversion.
-template <int DT>
-__global__ void __launch_bounds__(256)
-    k_fp8_cast_rows(const void* __restrict__ t, int64_t rows, int64_t cols, int64_t ld,
-                    const float* __restrict__ scale, const uint32_t* __restrict__ partials,
-                    int64_t n_partials, float fmax, float* __restrict__ scale_out, int fmt,
-                    uint8_t* __restrict__ out, uint8_t* __restrict__ out_t) {
-  __shared__ __align__(16) uint8_t tile[64][64 + 16];
-  __shared__ float s_sh;
-  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * 64;
-  const int64_t c0 = static_cast<int64_t>(blockIdx.x) * 64;
-  const int tid = threadIdx.x;
-  const int cl = (tid % 8) * 8;
-  float v[2][8];
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int rl = tid / 8 + 32 * i;
-    const int64_t r = r0 + rl;
-    const int64_t c = c0 + cl;
-    const bool ok = (r < rows) && (c < cols);  // cols % 8 == 0: the 8-vector is all in or out
-    if constexpr (DT == kBF16) {
-      u32x4_t w = ok ? *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(t) + r * ld + c)
-                     : u32x4_t{0u, 0u, 0u, 0u};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        v[i][2 * e] = bf16lo_to_f32(w[e]);
-        v[i][2 * e + 1] = bf16hi_to_f32(w[e]);
-      }
+// Block-wide max of per-thread amax values -> s = max(amax / fmax, FLT_MIN)
+// (NaN amax -> NaN), broadcast through LDS; `publish` also stores it.
+__device__ __forceinline__ float finalize_scale(uint32_t m, float fmax, float* scale_out, float* sh,
+                                                bool publish) {
+  __shared__ uint32_t red[4];
+  m = block_reduce_max(m, red);
+  if (threadIdx.x == 0) {
+    float s;
+    if (m > 0x7F800000u) {
+      s = __builtin_bit_cast(float, 0x7FC00000u);
     } else {
-      const float* p = static_cast<const float*>(t) + r * ld + c;
-      f32x4_t a = ok ? *reinterpret_cast<const f32x4_t*>(p) : f32x4_t{0.f, 0.f, 0.f, 0.f};
-      f32x4_t b = ok ? *reinterpret_cast<const f32x4_t*>(p + 4) : f32x4_t{0.f, 0.f, 0.f, 0.f};
+      s = __builtin_bit_cast(float, m) / fmax;
+      const float tiny = 1.17549435e-38f;
+      s = s > tiny ? s : tiny;
+    }
+    *sh = s;
+    if (scale_out != nullptr && publish) scale_out[0] = s;
+  }
+  __syncthreads();
+  return *sh;
+}
+
+// 4 x 4 byte transpose: rows a, b, c, d (byte j = column j) -> o[j] =
+// column j (byte i = row i).
+__device__ __forceinline__ void transpose4(uint32_t a, uint32_t b, uint32_t c, uint32_t d,
+                                           uint32_t* o) {
+  const uint32_t t0 = __builtin_amdgcn_perm(b, a, 0x06020400u);  // a0 b0 a2 b2
+  const uint32_t t1 = __builtin_amdgcn_perm(b, a, 0x07030501u);  // a1 b1 a3 b3
+  const uint32_t t2 = __builtin_amdgcn_perm(d, c, 0x06020400u);  // c0 d0 c2 d2
+  const uint32_t t3 = __builtin_amdgcn_perm(d, c, 0x07030501u);  // c1 d1 c3 d3
+  o[0] = __builtin_amdgcn_perm(t2, t0, 0x05040100u);
+  o[1] = __builtin_amdgcn_perm(t3, t1, 0x05040100u);
+  o[2] = __builtin_amdgcn_perm(t2, t0, 0x07060302u);
+  o[3] = __builtin_amdgcn_perm(t3, t1, 0x07060302u);
+}
+
+// Row-major input [rows, cols] (unit column stride, ld % 8 == 0, 16-byte
+// aligned): a 128 x 128 tile per block; thread (rq, cq) owns rows
+// 8 rq + [0, 8) x columns 8 cq + [0, 8). All 16-byte loads are issued before
+// the scale reduction; the row-major codes go out as 128-byte row segments
+// per 16 lanes, the transposed codes as 8-byte column pieces after an
+// in-register 8 x 8 byte transpose.
+struct CastTile {
+  const void* t;
+  int64_t rows, cols, ld;
+  const float* scale;
+  const uint32_t* partials;
+  int64_t n_partials;
+  float* scale_out;
+  uint8_t* out;
+  uint8_t* out_t;
+  int64_t tiles_x;  // 128-column tiles
+  int64_t tiles;    // all 128 x 128 tiles
+};
+
+// Thread (rq, cq) of a tile: rows 8 rq + [0, 8), columns 8 cq + [0, 8);
+// elements outside the matrix load as zero.
+template <int DT>
+__device__ __forceinline__ void tile_load(const CastTile& a, int64_t bx, int64_t by,
+                                          uint32_t (&raw)[8][DT == kBF16 ? 4 : 8]) {
+  const void* __restrict__ t = a.t;
+  const int64_t rows = a.rows;
+  const int64_t ld = a.ld;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int cq = lane & 15;
+  const int rq = (lane >> 4) + 4 * (tid >> 6);
+  const int64_t r0 = by * 128 + 8 * rq;
+  const int64_t c0 = bx * 128 + 8 * cq;
+  const bool col_ok = c0 < a.cols;  // cols % 8 == 0: the 8 columns are all in or out
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int64_t r = r0 + i;
+    const bool ok = col_ok && r < rows;
+    const int64_t off = ok ? r * ld + c0 : 0;
+    if constexpr (DT == kBF16) {
+      const u32x4_t w0 = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(t) + off);
+      const u32x4_t w = ok ? w0 : u32x4_t{0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) raw[i][e] = w[e];
+    } else {
+      const uint32_t* p = static_cast<const uint32_t*>(t) + off;
+      const u32x4_t a0 = *reinterpret_cast<const u32x4_t*>(p);
+      const u32x4_t b0 = *reinterpret_cast<const u32x4_t*>(p + 4);
+      const u32x4_t a = ok ? a0 : u32x4_t{0u, 0u, 0u, 0u};
+      const u32x4_t b = ok ? b0 : u32x4_t{0u, 0u, 0u, 0u};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        v[i][e] = a[e];
-        v[i][4 + e] = b[e];
+        raw[i][e] = a[e];
+        raw[i][4 + e] = b[e];
       }
     }
   }
-  const float s = resolve_scale(scale, partials, n_partials, fmax, scale_out, &s_sh);
-  const float rcp = 1.0f / s;
+}
+
+// max |t| of the thread's loaded elements as ordered f32 bits.
+template <int DT>
+__device__ __forceinline__ uint32_t tile_amax(const uint32_t (&raw)[8][DT == kBF16 ? 4 : 8]) {
+  uint32_t m = 0;
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int rl = tid / 8 + 32 * i;
-    const int64_t r = r0 + rl;
-    const int64_t c = c0 + cl;
-    float q[8];
+  for (int i = 0; i < 8; ++i) {
+    if constexpr (DT == kBF16) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) q[e] = div_rn(v[i][e], s, rcp);
-    const uint32_t lo = encode2(q[0], q[1], fmt) | (encode2(q[2], q[3], fmt) << 16);
-    const uint32_t hi = encode2(q[4], q[5], fmt) | (encode2(q[6], q[7], fmt) << 16);
-    if (out != nullptr && r < rows && c < cols)
-      *reinterpret_cast<u32x2_t*>(out + r * cols + c) = u32x2_t{lo, hi};
-    if (out_t != nullptr) *reinterpret_cast<u32x2_t*>(&tile[rl][cl]) = u32x2_t{lo, hi};
+      for (int e = 0; e < 4; ++e) m = umax(m, umax(raw[i][e] & 0x7FFFu, (raw[i][e] >> 16) & 0x7FFFu));
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) m = umax(m, raw[i][e] & 0x7FFFFFFFu);
+    }
   }
-  if (out_t == nullptr) return;
-  __syncthreads();
-  // out_t [cols, rows]: thread -> column c, 16 consecutive rows
-  const int cc = tid % 64;
-  const int rb = (tid / 64) * 16;
-  const int64_t c = c0 + cc;
-  const int64_t r = r0 + rb;
-  if (c >= cols || r >= rows) return;
-  uint32_t w[4];
+  return DT == kBF16 ? m << 16 : m;
+}
+
+template <int DT, int FMT>
+__device__ __forceinline__ void cast_tile_body(const CastTile& a, int64_t bx, int64_t by,
+                                               float* s_sh) {
+  const int64_t rows = a.rows;
+  const int64_t cols = a.cols;
+  uint8_t* __restrict__ out = a.out;
+  uint8_t* __restrict__ out_t = a.out_t;
+  constexpr float fmax = FMT == kE4M3FN ? 448.0f : 57344.0f;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int cq = lane & 15;
+  const int rq = (lane >> 4) + 4 * (tid >> 6);
+  const int64_t r0 = by * 128 + 8 * rq;
+  const int64_t c0 = bx * 128 + 8 * cq;
+  const bool col_ok = c0 < cols;
+  constexpr float kFmax = fmax;
+  // the amax partials are loaded first, so their block reduction waits only
+  // for them and overlaps the tile's loads
+  uint32_t pv[8];
+  const bool have_partials = a.partials != nullptr;
+  const int64_t np = have_partials ? a.n_partials : 0;
 #pragma unroll
-  for (int q = 0; q < 4; ++q)
-    w[q] = static_cast<uint32_t>(tile[rb + 4 * q][cc]) |
-           (static_cast<uint32_t>(tile[rb + 4 * q + 1][cc]) << 8) |
-           (static_cast<uint32_t>(tile[rb + 4 * q + 2][cc]) << 16) |
-           (static_cast<uint32_t>(tile[rb + 4 * q + 3][cc]) << 24);
-  uint8_t* dst = out_t + c * rows + r;
-  if (r + 15 < rows && (reinterpret_cast<uintptr_t>(dst) & 15) == 0) {
-    *reinterpret_cast<u32x4_t*>(dst) = u32x4_t{w[0], w[1], w[2], w[3]};
+  for (int u = 0; u < 8; ++u) {
+    const int64_t i = tid + 256 * u;
+    pv[u] = have_partials ? a.partials[i < np ? i : 0] : 0u;
+  }
+  uint32_t raw[8][DT == kBF16 ? 4 : 8];
+  tile_load<DT>(a, bx, by, raw);
+  float s;
+  if (have_partials) {
+    uint32_t m = 0;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) m = umax(m, tid + 256 * u < np ? pv[u] : 0u);
+    for (int64_t i = tid + 2048; i < np; i += 256) m = umax(m, a.partials[i]);
+    s = finalize_scale(m, fmax, a.scale_out, s_sh, bx == 0 && by == 0);
   } else {
-    for (int e = 0; e < 16; ++e)
-      if (r + e < rows) dst[e] = static_cast<uint8_t>(w[e / 4] >> (8 * (e % 4)));
+    s = a.scale[0];
   }
+  const float rcp = 1.0f / s;
+  // 2^-40 <= s <= 2^40 (uniform): the Markstein quotient is correctly rounded
+  // wherever it can give a nonzero code, since the residual of any x that
+  // matters stays normal
+  const bool fast = s >= 0x1p-40f && s <= 0x1p40f;
+  uint32_t lo[8], hi[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    float x[8];
+    uint32_t sign_lo, sign_hi;  // byte j: bit 7 = sign of element j (4 j)
+    if constexpr (DT == kBF16) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        x[2 * e] = bf16lo_to_f32(raw[i][e]);
+        x[2 * e + 1] = bf16hi_to_f32(raw[i][e]);
+      }
+      sign_lo = __builtin_amdgcn_perm(raw[i][1], raw[i][0], 0x07050301u);
+      sign_hi = __builtin_amdgcn_perm(raw[i][3], raw[i][2], 0x07050301u);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = __builtin_bit_cast(float, raw[i][e]);
+      const uint32_t s01 = __builtin_amdgcn_perm(raw[i][1], raw[i][0], 0x0c0c0703u);
+      const uint32_t s23 = __builtin_amdgcn_perm(raw[i][3], raw[i][2], 0x07030c0cu);
+      const uint32_t s45 = __builtin_amdgcn_perm(raw[i][5], raw[i][4], 0x0c0c0703u);
+      const uint32_t s67 = __builtin_amdgcn_perm(raw[i][7], raw[i][6], 0x07030c0cu);
+      sign_lo = s01 | s23;
+      sign_hi = s45 | s67;
+    }
+    uint32_t c[2];
+    if (fast) {
+      float q[8];
+      bool outside = false;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float q0 = x[e] * rcp;
+        const float res = __builtin_fmaf(-q0, s, x[e]);
+        q[e] = __builtin_fmaf(res, rcp, q0);
+        outside |= !(__builtin_fabsf(q[e]) <= kFmax);
+      }
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const float* qq = q + 4 * h;
+        uint32_t w;
+        if constexpr (FMT == kE4M3FN) {
+          w = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(qq[0], qq[1], 0, false));
+          w = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(qq[2], qq[3], static_cast<int>(w), true));
+        } else {
+          w = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_bf8_f32(qq[0], qq[1], 0, false));
+          w = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_bf8_f32(qq[2], qq[3], static_cast<int>(w), true));
+        }
+        c[h] = w;
+      }
+      if (outside) {
+        // NaN, infinities and |q| > fmax (rare): exact quotient, special codes
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          if (!(__builtin_fabsf(q[e]) <= kFmax)) {
+            const uint32_t code = encode_outside_t<FMT>(x[e] / s);
+            const int sh = 8 * (e & 3);
+            c[e >> 2] = (c[e >> 2] & ~(0xFFu << sh)) | (code << sh);
+          }
+        }
+      }
+    } else {
+      // scales this extreme (or NaN) are uniform per launch: IEEE divide
+      float q[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) q[e] = x[e] / s;
+      c[0] = encode2_t<FMT>(q[0], q[1]) | (encode2_t<FMT>(q[2], q[3]) << 16);
+      c[1] = encode2_t<FMT>(q[4], q[5]) | (encode2_t<FMT>(q[6], q[7]) << 16);
+    }
+    // s > 0, so every code carries the sign of its input (signed zeros and
+    // NaNs included)
+    lo[i] = (c[0] & 0x7F7F7F7Fu) | (sign_lo & 0x80808080u);
+    hi[i] = (c[1] & 0x7F7F7F7Fu) | (sign_hi & 0x80808080u);
+  }
+  if (!col_ok) return;
+  if (out != nullptr) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (r0 + i < rows) *reinterpret_cast<u32x2_t*>(out + (r0 + i) * cols + c0) = u32x2_t{lo[i], hi[i]};
+  }
+  if (out_t == nullptr || r0 >= rows) return;
+  // column j of the 8 x 8 block: rows 0-3 in cl[j], rows 4-7 in ch[j]
+  uint32_t cl[8], ch[8];
+  transpose4(lo[0], lo[1], lo[2], lo[3], cl);
+  transpose4(lo[4], lo[5], lo[6], lo[7], ch);
+  transpose4(hi[0], hi[1], hi[2], hi[3], cl + 4);
+  transpose4(hi[4], hi[5], hi[6], hi[7], ch + 4);
+  const bool vec = r0 + 8 <= rows && (rows & 7) == 0 && (reinterpret_cast<uintptr_t>(out_t) & 7) == 0;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    uint8_t* dst = out_t + (c0 + j) * rows + r0;
+    if (vec) {
+      *reinterpret_cast<u32x2_t*>(dst) = u32x2_t{cl[j], ch[j]};
+    } else {
+      for (int e = 0; e < 8 && r0 + e < rows; ++e)
+        dst[e] = static_cast<uint8_t>((e < 4 ? cl[j] : ch[j]) >> (8 * (e & 3)));
+    }
+  }
+}
+
+// Up to two row-major cast problems of one input type and format in one
+// launch: blocks [0, a0.tiles) take the first, the rest the second.
+template <int DT, int FMT>
+__global__ void __launch_bounds__(256) k_fp8_cast_tile(CastTile a0, CastTile a1) {
+  __shared__ float s_sh;
+  int64_t b = blockIdx.x;
+  if (b < a0.tiles) {
+    cast_tile_body<DT, FMT>(a0, b % a0.tiles_x, b / a0.tiles_x, &s_sh);
+  } else {
+    b -= a0.tiles;
+    cast_tile_body<DT, FMT>(a1, b % a1.tiles_x, b / a1.tiles_x, &s_sh);
+  }
+}
+
+// Amax partials, one per 128 x 128 tile, over the same block -> tile
+// mapping as k_fp8_cast_tile: a tile's amax block and cast block have the
+// same index, so they run on the same XCD and the cast finds the tile in
+// that XCD's L2. Partials of part 0 go to a0.partials, of part 1 to
+// a1.partials (written through the const pointers' storage).
+template <int DT>
+__global__ void __launch_bounds__(256) k_amax_tiles(CastTile a0, CastTile a1) {
+  __shared__ uint32_t sh[4];
+  int64_t b = blockIdx.x;
+  const bool first = b < a0.tiles;
+  const CastTile& a = first ? a0 : a1;
+  if (!first) b -= a0.tiles;
+  uint32_t raw[8][DT == kBF16 ? 4 : 8];
+  tile_load<DT>(a, b % a.tiles_x, b / a.tiles_x, raw);
+  const uint32_t m = block_reduce_max(tile_amax<DT>(raw), sh);
+  if (threadIdx.x == 0) const_cast<uint32_t*>(a.partials)[b] = m;
 }
 
 // Any strides: 64 x 64 tile, loads first, then conversion; byte outputs.
@@ -267,7 +552,8 @@ __global__ void __launch_bounds__(256)
     const int64_t c = c0 + cl;
     v[i] = (r < rows && c < cols) ? load_val(t, dtype, r * s_row + c * s_col) : 0.0f;
   }
-  const float s = resolve_scale(scale, partials, n_partials, fmax, scale_out, &s_sh);
+  const float s = resolve_scale(scale, partials, n_partials, fmax, scale_out, &s_sh,
+                                blockIdx.x == 0 && blockIdx.y == 0);
   const float rcp = 1.0f / s;
 #pragma unroll
   for (int i = 0; i < 16; i += 2) {
@@ -288,7 +574,7 @@ __global__ void __launch_bounds__(256)
 }  // namespace
 
 int64_t fp8_amax_partials(int64_t numel) {
-  int64_t g = ceil_div(numel, 256 * 16);
+  int64_t g = ceil_div(numel, 256 * 64);
   if (g > kAmaxBlocks) g = kAmaxBlocks;
   if (g < 1) g = 1;
   return g;
@@ -296,8 +582,10 @@ int64_t fp8_amax_partials(int64_t numel) {
 
 hipError_t launch_fp8_amax(const void* t, int dtype, int64_t numel, uint32_t* partials,
                            int64_t n_partials, int fmt, float* scale_out, hipStream_t stream) {
+  AmaxPart a{t, dtype, numel, partials, n_partials};
+  AmaxPart none{nullptr, dtype, 0, nullptr, 0};
   hipLaunchKernelGGL(k_amax_partial, dim3(static_cast<unsigned>(n_partials)), dim3(256), 0, stream,
-                     t, dtype, numel, partials);
+                     a, none);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || scale_out == nullptr) return e;
   hipLaunchKernelGGL(k_amax_finalize, dim3(1), dim3(256), 0, stream, partials, n_partials,
@@ -305,40 +593,181 @@ hipError_t launch_fp8_amax(const void* t, int dtype, int64_t numel, uint32_t* pa
   return hipGetLastError();
 }
 
+hipError_t launch_fp8_amax2(const void* t0, int dtype0, int64_t numel0, uint32_t* partials0,
+                            int64_t n_partials0, const void* t1, int dtype1, int64_t numel1,
+                            uint32_t* partials1, int64_t n_partials1, hipStream_t stream) {
+  AmaxPart a0{t0, dtype0, numel0, partials0, n_partials0};
+  AmaxPart a1{t1, dtype1, numel1, partials1, n_partials1};
+  hipLaunchKernelGGL(k_amax_partial, dim3(static_cast<unsigned>(n_partials0 + n_partials1)),
+                     dim3(256), 0, stream, a0, a1);
+  return hipGetLastError();
+}
+
+namespace {
+
+struct CastRequest {
+  const void* t;
+  int dtype;
+  int64_t rows, cols, s_row, s_col;
+  const float* scale;
+  const uint32_t* partials;
+  int64_t n_partials;
+  float* scale_out;
+  uint8_t* out;
+  uint8_t* out_t;
+};
+
+// A transposed view of a row-major buffer is cast as that buffer with the two
+// outputs exchanged.
+void normalize(CastRequest& r) {
+  if (r.s_row == 1 && r.s_col != 1) {
+    const int64_t tmp = r.rows;
+    r.rows = r.cols;
+    r.cols = tmp;
+    r.s_row = r.s_col;
+    r.s_col = 1;
+    uint8_t* o = r.out;
+    r.out = r.out_t;
+    r.out_t = o;
+  }
+}
+
+bool tile_path(const CastRequest& r) {
+  return r.s_col == 1 && r.cols % 8 == 0 && r.s_row % 8 == 0 &&
+         (reinterpret_cast<uintptr_t>(r.t) % 16 == 0) &&
+         (r.out == nullptr || reinterpret_cast<uintptr_t>(r.out) % 8 == 0);
+}
+
+CastTile to_tile(const CastRequest& r) {
+  CastTile c;
+  c.t = r.t;
+  c.rows = r.rows;
+  c.cols = r.cols;
+  c.ld = r.s_row;
+  c.scale = r.scale;
+  c.partials = r.partials;
+  c.n_partials = r.n_partials;
+  c.scale_out = r.scale_out;
+  c.out = r.out;
+  c.out_t = r.out_t;
+  c.tiles_x = ceil_div(r.cols, 128);
+  c.tiles = c.tiles_x * ceil_div(r.rows, 128);
+  return c;
+}
+
+void launch_tiles(int dtype, int fmt, const CastTile& a0, const CastTile& a1, hipStream_t stream) {
+  auto kern = dtype == kBF16 ? (fmt == kE4M3FN ? k_fp8_cast_tile<kBF16, kE4M3FN>
+                                               : k_fp8_cast_tile<kBF16, kE5M2>)
+                             : (fmt == kE4M3FN ? k_fp8_cast_tile<kF32, kE4M3FN>
+                                               : k_fp8_cast_tile<kF32, kE5M2>);
+  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(a0.tiles + a1.tiles)), dim3(256), 0, stream,
+                     a0, a1);
+}
+
+hipError_t launch_one(CastRequest r, int fmt, hipStream_t stream) {
+  if (r.rows == 0 || r.cols == 0) return hipSuccess;
+  normalize(r);
+  if (tile_path(r)) {
+    CastTile none{};
+    launch_tiles(r.dtype, fmt, to_tile(r), none, stream);
+  } else {
+    const dim3 grid(static_cast<unsigned>(ceil_div(r.cols, 64)),
+                    static_cast<unsigned>(ceil_div(r.rows, 64)));
+    hipLaunchKernelGGL(k_fp8_cast_any, grid, dim3(256), 0, stream, r.t, r.dtype, r.rows, r.cols,
+                       r.s_row, r.s_col, r.scale, r.partials, r.n_partials, fp8_max(fmt),
+                       r.scale_out, fmt, r.out, r.out_t);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace
+
 hipError_t launch_fp8_cast(const void* t, int dtype, int64_t rows, int64_t cols, int64_t s_row,
                            int64_t s_col, const float* scale, const uint32_t* partials,
                            int64_t n_partials, float* scale_out, int fmt, uint8_t* out,
                            uint8_t* out_t, hipStream_t stream) {
-  if (rows == 0 || cols == 0) return hipSuccess;
-  // A transposed view of a row-major buffer is cast as that buffer with the
-  // two outputs exchanged.
-  if (s_row == 1 && s_col != 1) {
-    const int64_t tmp = rows;
-    rows = cols;
-    cols = tmp;
-    s_row = s_col;
-    s_col = 1;
-    uint8_t* o = out;
-    out = out_t;
-    out_t = o;
+  return launch_one(CastRequest{t, dtype, rows, cols, s_row, s_col, scale, partials, n_partials,
+                                scale_out, out, out_t},
+                    fmt, stream);
+}
+
+hipError_t launch_fp8_cast2(const void* t0, int dtype0, int64_t rows0, int64_t cols0,
+                            int64_t s_row0, int64_t s_col0, const uint32_t* partials0,
+                            int64_t n_partials0, float* scale_out0, uint8_t* out0,
+                            uint8_t* out_t0, const void* t1, int dtype1, int64_t rows1,
+                            int64_t cols1, int64_t s_row1, int64_t s_col1,
+                            const uint32_t* partials1, int64_t n_partials1, float* scale_out1,
+                            uint8_t* out1, uint8_t* out_t1, int fmt, hipStream_t stream) {
+  CastRequest r0{t0, dtype0, rows0, cols0, s_row0, s_col0, nullptr, partials0, n_partials0,
+                 scale_out0, out0, out_t0};
+  CastRequest r1{t1, dtype1, rows1, cols1, s_row1, s_col1, nullptr, partials1, n_partials1,
+                 scale_out1, out1, out_t1};
+  normalize(r0);
+  normalize(r1);
+  const bool empty = r0.rows == 0 || r0.cols == 0 || r1.rows == 0 || r1.cols == 0;
+  if (!empty && dtype0 == dtype1 && tile_path(r0) && tile_path(r1)) {
+    launch_tiles(dtype0, fmt, to_tile(r0), to_tile(r1), stream);
+    return hipGetLastError();
   }
-  const float fmax = fp8_max(fmt);
-  const dim3 grid(static_cast<unsigned>(ceil_div(cols, 64)), static_cast<unsigned>(ceil_div(rows, 64)));
-  const size_t esz = dtype == kBF16 ? 2 : 4;
-  const bool rows_fast = s_col == 1 && cols % 8 == 0 && s_row % 8 == 0 &&
-                         (reinterpret_cast<uintptr_t>(t) % 16 == 0) &&
-                         (out == nullptr || reinterpret_cast<uintptr_t>(out) % 8 == 0) && esz > 0;
-  if (rows_fast && dtype == kBF16) {
-    hipLaunchKernelGGL(k_fp8_cast_rows<kBF16>, grid, dim3(256), 0, stream, t, rows, cols, s_row,
-                       scale, partials, n_partials, fmax, scale_out, fmt, out, out_t);
-  } else if (rows_fast) {
-    hipLaunchKernelGGL(k_fp8_cast_rows<kF32>, grid, dim3(256), 0, stream, t, rows, cols, s_row,
-                       scale, partials, n_partials, fmax, scale_out, fmt, out, out_t);
-  } else {
-    hipLaunchKernelGGL(k_fp8_cast_any, grid, dim3(256), 0, stream, t, dtype, rows, cols, s_row,
-                       s_col, scale, partials, n_partials, fmax, scale_out, fmt, out, out_t);
+  hipError_t e = launch_one(r0, fmt, stream);
+  if (e != hipSuccess) return e;
+  return launch_one(r1, fmt, stream);
+}
+
+int64_t fp8_quant_partials(int64_t rows, int64_t cols) {
+  const int64_t tiles = ceil_div(rows, 128) * ceil_div(cols, 128);
+  const int64_t p = fp8_amax_partials(rows * cols);
+  return tiles > p ? tiles : p;
+}
+
+hipError_t launch_fp8_quantize2(const void* t0, int dtype0, int64_t rows0, int64_t cols0,
+                                int64_t s_row0, int64_t s_col0, uint32_t* partials0,
+                                float* scale_out0, uint8_t* out0, uint8_t* out_t0, const void* t1,
+                                int dtype1, int64_t rows1, int64_t cols1, int64_t s_row1,
+                                int64_t s_col1, uint32_t* partials1, float* scale_out1,
+                                uint8_t* out1, uint8_t* out_t1, int fmt, hipStream_t stream) {
+  const bool two = t1 != nullptr;
+  CastRequest r0{t0, dtype0, rows0, cols0, s_row0, s_col0, nullptr, partials0, 0, scale_out0, out0,
+                 out_t0};
+  CastRequest r1{t1, dtype1, rows1, cols1, s_row1, s_col1, nullptr, partials1, 0, scale_out1, out1,
+                 out_t1};
+  normalize(r0);
+  normalize(r1);
+  const bool tiles_ok = r0.rows > 0 && r0.cols > 0 && tile_path(r0) &&
+                        (!two || (r1.rows > 0 && r1.cols > 0 && tile_path(r1) && dtype1 == dtype0));
+  if (tiles_ok) {
+    CastTile a0 = to_tile(r0);
+    a0.n_partials = a0.tiles;
+    CastTile a1{};
+    if (two) {
+      a1 = to_tile(r1);
+      a1.n_partials = a1.tiles;
+    }
+    const unsigned blocks = static_cast<unsigned>(a0.tiles + a1.tiles);
+    if (dtype0 == kBF16) {
+      hipLaunchKernelGGL(k_amax_tiles<kBF16>, dim3(blocks), dim3(256), 0, stream, a0, a1);
+    } else {
+      hipLaunchKernelGGL(k_amax_tiles<kF32>, dim3(blocks), dim3(256), 0, stream, a0, a1);
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    launch_tiles(dtype0, fmt, a0, a1, stream);
+    return hipGetLastError();
   }
-  return hipGetLastError();
+  // other layouts: grid-stride amax partials, then the casts
+  const int64_t np0 = fp8_amax_partials(rows0 * cols0);
+  const int64_t np1 = two ? fp8_amax_partials(rows1 * cols1) : 0;
+  hipError_t e = two ? launch_fp8_amax2(t0, dtype0, rows0 * cols0, partials0, np0, t1, dtype1,
+                                        rows1 * cols1, partials1, np1, stream)
+                     : launch_fp8_amax(t0, dtype0, rows0 * cols0, partials0, np0, fmt, nullptr,
+                                       stream);
+  if (e != hipSuccess) return e;
+  if (!two)
+    return launch_fp8_cast(t0, dtype0, rows0, cols0, s_row0, s_col0, nullptr, partials0, np0,
+                           scale_out0, fmt, out0, out_t0, stream);
+  return launch_fp8_cast2(t0, dtype0, rows0, cols0, s_row0, s_col0, partials0, np0, scale_out0,
+                          out0, out_t0, t1, dtype1, rows1, cols1, s_row1, s_col1, partials1, np1,
+                          scale_out1, out1, out_t1, fmt, stream);
 }
 
 namespace {

@@ -104,6 +104,31 @@ hipError_t launch_fp8_cast(const void* t, int dtype, int64_t rows, int64_t cols,
                            int64_t s_col, const float* scale, const uint32_t* partials,
                            int64_t n_partials, float* scale_out, int fmt, uint8_t* out,
                            uint8_t* out_t, hipStream_t stream);
+// Two amax problems (partials only) in one launch.
+hipError_t launch_fp8_amax2(const void* t0, int dtype0, int64_t numel0, uint32_t* partials0,
+                            int64_t n_partials0, const void* t1, int dtype1, int64_t numel1,
+                            uint32_t* partials1, int64_t n_partials1, hipStream_t stream);
+// Two casts with scales finalized from their amax partials, one format; one
+// launch when both take the row-major tile path with the same input type.
+hipError_t launch_fp8_cast2(const void* t0, int dtype0, int64_t rows0, int64_t cols0,
+                            int64_t s_row0, int64_t s_col0, const uint32_t* partials0,
+                            int64_t n_partials0, float* scale_out0, uint8_t* out0,
+                            uint8_t* out_t0, const void* t1, int dtype1, int64_t rows1,
+                            int64_t cols1, int64_t s_row1, int64_t s_col1,
+                            const uint32_t* partials1, int64_t n_partials1, float* scale_out1,
+                            uint8_t* out1, uint8_t* out_t1, int fmt, hipStream_t stream);
+// Partials a quantize call needs for a [rows, cols] tensor.
+int64_t fp8_quant_partials(int64_t rows, int64_t cols);
+// One or two tensors (t1 == nullptr for one), each with its own dynamic
+// scale (written to scale_out*): amax, then codes in the requested layouts.
+// Row-major inputs of one type take a tile-mapped amax whose blocks touch the
+// same tiles, on the same XCDs, as the cast's.
+hipError_t launch_fp8_quantize2(const void* t0, int dtype0, int64_t rows0, int64_t cols0,
+                                int64_t s_row0, int64_t s_col0, uint32_t* partials0,
+                                float* scale_out0, uint8_t* out0, uint8_t* out_t0, const void* t1,
+                                int dtype1, int64_t rows1, int64_t cols1, int64_t s_row1,
+                                int64_t s_col1, uint32_t* partials1, float* scale_out1,
+                                uint8_t* out1, uint8_t* out_t1, int fmt, hipStream_t stream);
 hipError_t launch_fp8_gemm(const uint8_t* a, int fmt_a, const float* s_a, const uint8_t* b,
                            int fmt_b, const float* s_b, int64_t m, int64_t n, int64_t k,
                            void* out, int out_dtype, int64_t ldc, float* split_ws,

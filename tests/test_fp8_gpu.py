@@ -62,6 +62,28 @@ def test_cast_random_f32_bit_exact(fmt):
         assert np.array_equal(out.cpu().numpy(), want), (fmt, s)
 
 
+@pytest.mark.parametrize("rows,cols", [(300, 200), (37, 96), (129, 136), (8, 8), (1000, 8)])
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_cast_ragged_tiles_both_outputs_bit_exact(rows, cols, dtype):
+    """Tiles cut by the matrix edge: rows not a multiple of 8 or 128, columns
+    not a multiple of 128; row-major and transposed codes."""
+
+    g = rng(rows * 7 + cols)
+    vals = (g.standard_normal((rows, cols)) * 3.0).astype(np.float32)
+    if dtype == "bf16":
+        vals = bf16_values(vals)
+        xd = to_dev_bf16(vals)
+    else:
+        xd = to_dev(vals)
+    for fmt in ("e4m3fn", "e5m2"):
+        s = np.float32(0.037)
+        sd = torch.tensor([s], dtype=torch.float32, device="cuda")
+        out, out_t = ops.fp8_cast(xd, sd, fmt, rowmajor=True, transposed=True)
+        want = ofp8.cast_with_scale(vals, s, fmt)
+        assert np.array_equal(out.cpu().numpy(), want), (fmt, rows, cols)
+        assert np.array_equal(out_t.cpu().numpy(), want.T), (fmt, rows, cols)
+
+
 @pytest.mark.parametrize("fmt", ["e4m3fn", "e5m2"])
 def test_scale_matches_oracle(fmt):
     g = rng(5)
