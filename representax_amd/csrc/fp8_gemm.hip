@@ -424,25 +424,61 @@ double plan_cycles(int cfg, int64_t m, int64_t n, int64_t kslices, int64_t kps, 
   return cyc;
 }
 
+// Cheapest split count for one tile configuration under plan_cycles.
+Fp8Plan plan_for(int cfg, int64_t m, int64_t n, int64_t kslices, double* cost_out) {
+  Fp8Plan best{cfg, 1, kslices * kBK};
+  double best_cost = -1.0;
+  const int64_t tiles = ceil_div(m, kCfgBM[cfg]) * ceil_div(n, kCfgBN[cfg]);
+  for (int64_t s = 1; s <= 32 && s <= kslices; ++s) {
+    if (s > 1 && tiles * s > 2 * kCfgSlots[cfg]) break;
+    const int64_t kps = ceil_div(kslices, s);
+    const int64_t splits = ceil_div(kslices, kps);
+    if (splits != s) continue;
+    const double cost = plan_cycles(cfg, m, n, kslices, kps, splits);
+    if (best_cost < 0.0 || cost < best_cost) {
+      best_cost = cost;
+      best = Fp8Plan{cfg, splits, kps * kBK};
+    }
+  }
+  if (cost_out != nullptr) *cost_out = best_cost;
+  return best;
+}
+
 Fp8Plan plan_fp8(int64_t m, int64_t n, int64_t k) {
   const int64_t kslices = k / kBK;
+  const int forced = fp8_tile_override();
+  if (forced != 0) return plan_for(forced, m, n, kslices, nullptr);
   Fp8Plan best{1, 1, k};
   double best_cost = -1.0;
-  const int forced = fp8_tile_override();
-  for (int cfg = 1; cfg < kNumCfg; ++cfg) {
-    if (forced != 0 && cfg != forced) continue;
-    if (forced == 0 && cfg > 5) continue;
-    const int64_t tiles = ceil_div(m, kCfgBM[cfg]) * ceil_div(n, kCfgBN[cfg]);
-    for (int64_t s = 1; s <= 32 && s <= kslices; ++s) {
-      if (s > 1 && tiles * s > 2 * kCfgSlots[cfg]) break;
-      const int64_t kps = ceil_div(kslices, s);
-      const int64_t splits = ceil_div(kslices, kps);
-      if (splits != s) continue;
-      const double cost = plan_cycles(cfg, m, n, kslices, kps, splits);
-      if (best_cost < 0.0 || cost < best_cost) {
-        best_cost = cost;
-        best = Fp8Plan{cfg, splits, kps * kBK};
-      }
+  for (int cfg = 1; cfg <= 5; ++cfg) {
+    double cost;
+    const Fp8Plan p = plan_for(cfg, m, n, kslices, &cost);
+    if (best_cost < 0.0 || cost < best_cost) {
+      best_cost = cost;
+      best = p;
+    }
+  }
+  static const bool model_only = [] {
+    const char* env = std::getenv("RPX_FP8_PLAN");
+    return env != nullptr && std::strcmp(env, "model") == 0;
+  }();
+  if (best.cfg == 1 && !model_only) {
+    // RPX_FP8_PLAN=model keeps the model's choice (for comparisons).
+    // Measured on the BERT-base shapes (tokens 8192, widths 768 / 3072),
+    // where the model above does not see pipeline depth: split-K tiles run
+    // long K ranges and gain from a third stage (768 x 768 x 8192: 17.6 us
+    // against 22.6); unsplit products with >= 16 K slices (K >= 2048) prefer 128 x 192
+    // tiles with three stages (8192 x 768 x 3072: 21.9 us against 23.3), and
+    // short ones 128 x 192 tiles with two (8192 x 768 x 768: 10.4-11.1 us
+    // against 11.1-11.7) when those fill one or two rounds of CUs. Each keeps
+    // its own split count.
+    const int64_t tiles192 = ceil_div(m, kCfgBM[4]) * ceil_div(n, kCfgBN[4]);
+    if (best.splits > 1) {
+      best = plan_for(9, m, n, kslices, nullptr);
+    } else if (kslices >= 16 && tiles192 >= 200 && tiles192 <= 512) {
+      best = plan_for(7, m, n, kslices, nullptr);
+    } else if (tiles192 >= 256 && tiles192 <= 512) {
+      best = plan_for(4, m, n, kslices, nullptr);
     }
   }
   return best;
