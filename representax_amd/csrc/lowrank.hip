@@ -104,15 +104,21 @@ __global__ void __launch_bounds__(256)
 }
 
 // Token-reduction product. Tile BP x BQ outputs, chunk of `chunk` tokens per
-// workgroup (blockIdx.z), 32 tokens per LDS step.
+// workgroup (blockIdx.z), 256 tokens per LDS step.
 template <int BP, int BQ>
 __global__ void __launch_bounds__(256)
     k_rank_tn(const uint16_t* __restrict__ X, int64_t ldx, const uint16_t* __restrict__ Y,
               int64_t ldy, int64_t M, int64_t P, int64_t Q, int round_x, float x_scale,
               int64_t chunk, float* __restrict__ partials) {
+  // 256 tokens per step: every thread's loads of a step are issued together,
+  // and the next step's loads are in flight while this step's MFMAs run from
+  // LDS
+  constexpr int TS = 256;
   constexpr int PP = 16 / 2;  // padding (elements) per LDS row
-  __shared__ uint16_t sX[32][BP + PP];
-  __shared__ uint16_t sY[32][BQ + PP];
+  __shared__ uint16_t sX[TS][BP + PP];
+  __shared__ uint16_t sY[TS][BQ + PP];
+  constexpr int XV = TS * (BP / 8) / 256;  // 16-byte vectors per thread per step
+  constexpr int YV = TS * (BQ / 8) / 256;
   constexpr int NB = (BP / 16) * (BQ / 16);
   constexpr int PER_WAVE = (NB + 3) / 4;
   const int tid = threadIdx.x;
@@ -129,50 +135,72 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
   for (int b = 0; b < PER_WAVE; ++b) acc[b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  for (int64_t ms = mbeg; ms < mend; ms += 32) {
-    // stage X[ms:ms+32, p0:p0+BP] and Y[ms:ms+32, q0:q0+BQ]
-    for (int v = tid; v < 32 * (BP / 8); v += 256) {
+  u32x4_t xr[XV], yr[YV];
+  auto load_step = [&](int64_t ms) {
+#pragma unroll
+    for (int u = 0; u < XV; ++u) {
+      const int v = tid + 256 * u;
       const int r = v / (BP / 8);
       const int c = (v % (BP / 8)) * 8;
       const int64_t gm = ms + r;
       int valid = static_cast<int>(P - (p0 + c));
       valid = (gm < mend) ? (valid < 0 ? 0 : (valid > 8 ? 8 : valid)) : 0;
-      u32x4_t xv = load8(X + gm * ldx + p0 + c, valid, x_al);
-      if (round_x) xv = scale_round8(xv, x_scale);
-      *reinterpret_cast<u32x4_t*>(&sX[r][c]) = xv;
+      xr[u] = load8(X + (gm < mend ? gm : mbeg) * ldx + p0 + c, valid, x_al);
     }
-    for (int v = tid; v < 32 * (BQ / 8); v += 256) {
+#pragma unroll
+    for (int u = 0; u < YV; ++u) {
+      const int v = tid + 256 * u;
       const int r = v / (BQ / 8);
       const int c = (v % (BQ / 8)) * 8;
       const int64_t gm = ms + r;
       int valid = static_cast<int>(Q - (q0 + c));
       valid = (gm < mend) ? (valid < 0 ? 0 : (valid > 8 ? 8 : valid)) : 0;
-      *reinterpret_cast<u32x4_t*>(&sY[r][c]) = load8(Y + gm * ldy + q0 + c, valid, y_al);
+      yr[u] = load8(Y + (gm < mend ? gm : mbeg) * ldy + q0 + c, valid, y_al);
+    }
+  };
+
+  load_step(mbeg);
+  for (int64_t ms = mbeg; ms < mend; ms += TS) {
+    __syncthreads();  // every wave is done reading the previous step
+#pragma unroll
+    for (int u = 0; u < XV; ++u) {
+      const int v = tid + 256 * u;
+      u32x4_t xv = xr[u];
+      if (round_x) xv = scale_round8(xv, x_scale);
+      *reinterpret_cast<u32x4_t*>(&sX[v / (BP / 8)][(v % (BP / 8)) * 8]) = xv;
+    }
+#pragma unroll
+    for (int u = 0; u < YV; ++u) {
+      const int v = tid + 256 * u;
+      *reinterpret_cast<u32x4_t*>(&sY[v / (BQ / 8)][(v % (BQ / 8)) * 8]) = yr[u];
     }
     __syncthreads();
+    if (ms + TS < mend) load_step(ms + TS);
+    const int steps = static_cast<int>((mend - ms + 31) / 32 < TS / 32 ? (mend - ms + 31) / 32 : TS / 32);
+    for (int st = 0; st < steps; ++st) {
 #pragma unroll
-    for (int b = 0; b < PER_WAVE; ++b) {
-      const int blk = wave + 4 * b;
-      if (blk < NB) {
-        const int bp = blk / (BQ / 16);
-        const int bq = blk % (BQ / 16);
-        const int pl = bp * 16 + (lane & 15);
-        const int ql = bq * 16 + (lane & 15);
-        const int mo = (lane >> 4) * 8;
-        uint32_t xw[4], yw[4];
+      for (int b = 0; b < PER_WAVE; ++b) {
+        const int blk = wave + 4 * b;
+        if (blk < NB) {
+          const int bp = blk / (BQ / 16);
+          const int bq = blk % (BQ / 16);
+          const int pl = bp * 16 + (lane & 15);
+          const int ql = bq * 16 + (lane & 15);
+          const int mo = st * 32 + (lane >> 4) * 8;
+          uint32_t xw[4], yw[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          xw[e] = static_cast<uint32_t>(sX[mo + 2 * e][pl]) |
-                  (static_cast<uint32_t>(sX[mo + 2 * e + 1][pl]) << 16);
-          yw[e] = static_cast<uint32_t>(sY[mo + 2 * e][ql]) |
-                  (static_cast<uint32_t>(sY[mo + 2 * e + 1][ql]) << 16);
+          for (int e = 0; e < 4; ++e) {
+            xw[e] = static_cast<uint32_t>(sX[mo + 2 * e][pl]) |
+                    (static_cast<uint32_t>(sX[mo + 2 * e + 1][pl]) << 16);
+            yw[e] = static_cast<uint32_t>(sY[mo + 2 * e][ql]) |
+                    (static_cast<uint32_t>(sY[mo + 2 * e + 1][ql]) << 16);
+          }
+          acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              as_bf16x8(u32x4_t{xw[0], xw[1], xw[2], xw[3]}),
+              as_bf16x8(u32x4_t{yw[0], yw[1], yw[2], yw[3]}), acc[b], 0, 0, 0);
         }
-        acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-            as_bf16x8(u32x4_t{xw[0], xw[1], xw[2], xw[3]}),
-            as_bf16x8(u32x4_t{yw[0], yw[1], yw[2], yw[3]}), acc[b], 0, 0, 0);
       }
     }
-    __syncthreads();
   }
   float* part = partials + static_cast<int64_t>(blockIdx.z) * P * Q;
 #pragma unroll
