@@ -403,9 +403,16 @@ int rpx_int4lora_backward(const void* grad, const void* x, int dtype, int64_t m,
     float* part = arena.take<float>(part_n);
     if (arena.overflow) return fail_invalid("rpx_int4lora_backward: workspace too small");
     // B^T [r, N] so that dh = g_a . B is an NT product; A^T [K, r] for the
-    // dx epilogue's contiguous fragment loads
-    RPX_HIP(launch_transpose_bf16(bb, n, rank, rank, bt, n, st), "int4lora_backward: B^T");
-    RPX_HIP(launch_transpose_bf16(ab, rank, k, k, at, rank, st), "int4lora_backward: A^T");
+    // dx epilogue's contiguous fragment loads; W_b^T [K, N] for dx
+    const bool prep_fused = g % 32 == 0;
+    if (prep_fused) {
+      RPX_HIP(launch_int4lora_bwd_prep(bb, bt, ab, at, packed, scale_bits, wt, n, k, rank, pc, ng, g,
+                                       st),
+              "int4lora_backward: B^T, A^T, W_b^T");
+    } else {
+      RPX_HIP(launch_transpose_bf16(bb, n, rank, rank, bt, n, st), "int4lora_backward: B^T");
+      RPX_HIP(launch_transpose_bf16(ab, rank, k, k, at, rank, st), "int4lora_backward: A^T");
+    }
     // dh = bf16(bf16(g * c) . B)
     RPX_HIP(launch_rank_nt(gb, n, bt, n, m, rank, n, true, c, dh, rank, st),
             "int4lora_backward: dh");
@@ -413,9 +420,9 @@ int rpx_int4lora_backward(const void* grad, const void* x, int dtype, int64_t m,
     RPX_HIP(launch_rank_tn(gb, n, static_cast<const uint16_t*>(h), rank, m, n, rank, true, c, part,
                            d_lora_b, st),
             "int4lora_backward: dB");
-    // W_b^T [K, N]
-    RPX_HIP(launch_int4_dequant_t(packed, scale_bits, wt, n, k, pc, ng, g, n, st),
-            "int4lora_backward: dequantized transpose");
+    if (!prep_fused)
+      RPX_HIP(launch_int4_dequant_t(packed, scale_bits, wt, n, k, pc, ng, g, n, st),
+              "int4lora_backward: dequantized transpose");
     // dx = bf16(bf16(g . W_b) + bf16(dh . A))
     LowRankEpilogue epi;
     epi.rows = at;  // R(k, j) = A[j, k] = A^T[k, j]

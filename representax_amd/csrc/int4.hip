@@ -73,17 +73,13 @@ __global__ void __launch_bounds__(256) k_int4_dequant_any(
 // the packed bytes arrive in LDS with one 16-byte load per thread; each
 // thread then turns one byte column of 8 consecutive rows into two output
 // rows (k even / odd) of 8 consecutive n, stored as 16 bytes each.
-__global__ void __launch_bounds__(256) k_int4_dequant_t32(
+__device__ __forceinline__ void dequant_t32_tile(
     const uint8_t* __restrict__ packed, const uint16_t* __restrict__ scales,
     uint16_t* __restrict__ out, int64_t n_rows, int64_t k, int64_t packed_cols,
-    int64_t n_groups, int64_t group, int64_t ld_out) {
-  // 16-byte chunk c of row r sits at chunk c ^ ((r >> 4) & 3), and scale
-  // rows are padded to 5 floats: the byte and scale reads of a wave's eight
-  // row-octets then fall in eight different banks.
-  __shared__ __align__(16) uint8_t pk[64][80];
-  __shared__ float sc[64][5];
-  const int64_t n0 = static_cast<int64_t>(blockIdx.y) * 64;
-  const int64_t k0 = static_cast<int64_t>(blockIdx.x) * 128;
+    int64_t n_groups, int64_t group, int64_t ld_out, int64_t bx, int64_t by,
+    uint8_t (&pk)[64][80], float (&sc)[64][5]) {
+  const int64_t n0 = by * 64;
+  const int64_t k0 = bx * 128;
   const int t = threadIdx.x;
   {
     const int r = t >> 2;
@@ -144,6 +140,75 @@ __global__ void __launch_bounds__(256) k_int4_dequant_t32(
       }
     }
   }
+}
+
+__global__ void __launch_bounds__(256) k_int4_dequant_t32(
+    const uint8_t* __restrict__ packed, const uint16_t* __restrict__ scales,
+    uint16_t* __restrict__ out, int64_t n_rows, int64_t k, int64_t packed_cols,
+    int64_t n_groups, int64_t group, int64_t ld_out) {
+  // 16-byte chunk c of row r sits at chunk c ^ ((r >> 4) & 3), and scale
+  // rows are padded to 5 floats: the byte and scale reads of a wave's eight
+  // row-octets then fall in eight different banks.
+  __shared__ __align__(16) uint8_t pk[64][80];
+  __shared__ float sc[64][5];
+  dequant_t32_tile(packed, scales, out, n_rows, k, packed_cols, n_groups, group, ld_out,
+                   blockIdx.x, blockIdx.y, pk, sc);
+}
+
+// 32 x 32 tile of a bf16 transpose through LDS.
+__device__ __forceinline__ void transpose_tile(const uint16_t* __restrict__ in, int64_t rows,
+                                               int64_t cols, int64_t ld_in,
+                                               uint16_t* __restrict__ out, int64_t ld_out,
+                                               int64_t bx, int64_t by, uint16_t (&tile)[32][33]) {
+  const int64_t r0 = by * 32;
+  const int64_t c0 = bx * 32;
+  const int tx = threadIdx.x % 32;
+  const int ty = threadIdx.x / 32;  // 0..7
+  for (int i = ty; i < 32; i += 8) {
+    const int64_t r = r0 + i;
+    const int64_t c = c0 + tx;
+    tile[i][tx] = (r < rows && c < cols) ? in[r * ld_in + c] : 0;
+  }
+  __syncthreads();
+  for (int i = ty; i < 32; i += 8) {
+    const int64_t c = c0 + i;
+    const int64_t r = r0 + tx;
+    if (c < cols && r < rows) out[c * ld_out + r] = tile[tx][i];
+  }
+}
+
+// The INT4-LoRA backward's operand preparation in one launch: B^T [r, N]
+// (blocks [0, tb)), A^T [K, r] (blocks [tb, tb + ta)) and the dequantized
+// W_b^T [K, N] (the rest; groups that are multiples of 32).
+struct BwdPrep {
+  const uint16_t* b;  // [N, r]
+  uint16_t* bt;       // [r, N]
+  const uint16_t* a;  // [r, K]
+  uint16_t* at;       // [K, r]
+  const uint8_t* packed;
+  const uint16_t* scales;
+  uint16_t* wt;       // [K, N]
+  int64_t n, k, rank, packed_cols, n_groups, group;
+  int64_t tb_x, tb, ta_x, ta, tw_x;
+};
+
+__global__ void __launch_bounds__(256) k_int4lora_bwd_prep(BwdPrep p) {
+  __shared__ __align__(16) uint8_t pk[64][80];
+  __shared__ float sc[64][5];
+  __shared__ uint16_t tile[32][33];
+  int64_t b = blockIdx.x;
+  if (b < p.tb) {
+    transpose_tile(p.b, p.n, p.rank, p.rank, p.bt, p.n, b % p.tb_x, b / p.tb_x, tile);
+    return;
+  }
+  b -= p.tb;
+  if (b < p.ta) {
+    transpose_tile(p.a, p.rank, p.k, p.k, p.at, p.rank, b % p.ta_x, b / p.ta_x, tile);
+    return;
+  }
+  b -= p.ta;
+  dequant_t32_tile(p.packed, p.scales, p.wt, p.n, p.k, p.packed_cols, p.n_groups, p.group, p.n,
+                   b % p.tw_x, b / p.tw_x, pk, sc);
 }
 
 // Transposed dequant: out[k, n] = W_b[n, k], row stride ld_out (>= N).
@@ -318,6 +383,37 @@ hipError_t launch_int4_dequant_t(const uint8_t* packed, const uint16_t* scales, 
   dim3 grid(static_cast<unsigned>(ceil_div(k, 64)), static_cast<unsigned>(ceil_div(n, 64)));
   hipLaunchKernelGGL(k_int4_dequant_t, grid, dim3(256), 0, stream, packed, scales, out, n, k,
                      packed_cols, n_groups, group, ld_out);
+  return hipGetLastError();
+}
+
+hipError_t launch_int4lora_bwd_prep(const uint16_t* b, uint16_t* bt, const uint16_t* a,
+                                   uint16_t* at, const uint8_t* packed, const uint16_t* scales,
+                                   uint16_t* wt, int64_t n, int64_t k, int64_t rank,
+                                   int64_t packed_cols, int64_t n_groups, int64_t group,
+                                   hipStream_t stream) {
+  if (group % 32 != 0) return hipErrorInvalidValue;
+  BwdPrep p;
+  p.b = b;
+  p.bt = bt;
+  p.a = a;
+  p.at = at;
+  p.packed = packed;
+  p.scales = scales;
+  p.wt = wt;
+  p.n = n;
+  p.k = k;
+  p.rank = rank;
+  p.packed_cols = packed_cols;
+  p.n_groups = n_groups;
+  p.group = group;
+  p.tb_x = ceil_div(rank, 32);
+  p.tb = p.tb_x * ceil_div(n, 32);
+  p.ta_x = ceil_div(k, 32);
+  p.ta = p.ta_x * ceil_div(rank, 32);
+  p.tw_x = ceil_div(k, 128);
+  const int64_t tw = p.tw_x * ceil_div(n, 64);
+  hipLaunchKernelGGL(k_int4lora_bwd_prep, dim3(static_cast<unsigned>(p.tb + p.ta + tw)), dim3(256),
+                     0, stream, p);
   return hipGetLastError();
 }
 

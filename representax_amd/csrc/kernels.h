@@ -77,6 +77,13 @@ int64_t rank_tn_workspace_floats(int64_t m, int64_t p, int64_t q);
 hipError_t launch_rank_tn(const uint16_t* x, int64_t ldx, const uint16_t* y, int64_t ldy,
                           int64_t m, int64_t p, int64_t q, bool round_x, float x_scale,
                           float* partials, float* out, hipStream_t stream);
+// B^T [r, N], A^T [K, r] and W_b^T [K, N] (groups that are multiples of 32)
+// in one launch.
+hipError_t launch_int4lora_bwd_prep(const uint16_t* b, uint16_t* bt, const uint16_t* a,
+                                   uint16_t* at, const uint8_t* packed, const uint16_t* scales,
+                                   uint16_t* wt, int64_t n, int64_t k, int64_t rank,
+                                   int64_t packed_cols, int64_t n_groups, int64_t group,
+                                   hipStream_t stream);
 hipError_t launch_transpose_bf16(const uint16_t* in, int64_t rows, int64_t cols, int64_t ld_in,
                                  uint16_t* out, int64_t ld_out, hipStream_t stream);
 hipError_t launch_fill_f32(float* out, int64_t n, float v, hipStream_t stream);
