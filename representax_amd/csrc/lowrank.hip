@@ -218,89 +218,6 @@ __global__ void __launch_bounds__(256)
   }
 }
 
-// Token-reduction product with one thin operand:
-//   D[j, p] = sum_m T[m, j] * Wd[m, p]    (T: J <= 64 columns, Wd: P columns)
-// over the token chunk blockIdx.y, fp32 partials. Both MFMA operands need 8
-// consecutive tokens per lane; they come straight from global memory as
-// 2-byte loads (16 lanes read 16 consecutive columns of one token row), U
-// 32-token steps in flight. A block is 4 waves x 16 wide columns. `op`
-// scales and rounds an operand to bf16 first (g_a = bf16(g * c)).
-template <int JB>
-__global__ void __launch_bounds__(256)
-    k_rank_thin(const uint16_t* __restrict__ Wd, int64_t ldw, int64_t P, int round_w,
-                float w_scale, const uint16_t* __restrict__ T, int64_t ldt, int64_t J, int round_t,
-                float t_scale, int64_t M, int64_t chunk, float* __restrict__ partials) {
-  constexpr int U = 4;
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int64_t p = static_cast<int64_t>(blockIdx.x) * 64 + wave * 16 + (lane & 15);
-  const int kq = (lane >> 4) * 8;
-  const int64_t mb = static_cast<int64_t>(blockIdx.y) * chunk;
-  int64_t me = mb + chunk;
-  if (me > M) me = M;
-  f32x4_t acc[JB];
-#pragma unroll
-  for (int jb = 0; jb < JB; ++jb) acc[jb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  // column bases clamped in range (a column past the edge loads its last
-  // valid neighbour and is zeroed), rows clamped to the chunk: no branches
-  const bool p_ok = p < P;
-  const uint16_t* wcol = Wd + (p_ok ? p : P - 1);
-  const uint16_t* tcol[JB];
-  bool t_ok[JB];
-#pragma unroll
-  for (int jb = 0; jb < JB; ++jb) {
-    const int64_t j = jb * 16 + (lane & 15);
-    t_ok[jb] = j < J;
-    tcol[jb] = T + (t_ok[jb] ? j : J - 1);
-  }
-  auto fetch = [&](const uint16_t* col, int64_t ld, bool ok, int64_t m0) -> u32x4_t {
-    uint32_t w[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int64_t m = m0 + kq + 2 * e;
-      const int64_t ma = m < me ? m : me - 1;
-      const int64_t mb1 = m + 1 < me ? m + 1 : me - 1;
-      uint32_t lo = col[ma * ld];
-      uint32_t hi = col[mb1 * ld];
-      lo = (ok && m < me) ? lo : 0u;
-      hi = (ok && m + 1 < me) ? hi : 0u;
-      w[e] = lo | (hi << 16);
-    }
-    return u32x4_t{w[0], w[1], w[2], w[3]};
-  };
-  for (int64_t m0 = mb; m0 < me; m0 += 32 * U) {
-    u32x4_t wv[U];
-    u32x4_t tv[U][JB];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      wv[u] = fetch(wcol, ldw, p_ok, m0 + 32 * u);
-#pragma unroll
-      for (int jb = 0; jb < JB; ++jb) tv[u][jb] = fetch(tcol[jb], ldt, t_ok[jb], m0 + 32 * u);
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      u32x4_t w = wv[u];
-      if (round_w) w = scale_round8(w, w_scale);
-#pragma unroll
-      for (int jb = 0; jb < JB; ++jb) {
-        u32x4_t t = tv[u][jb];
-        if (round_t) t = scale_round8(t, t_scale);
-        acc[jb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(t), as_bf16x8(w), acc[jb], 0, 0, 0);
-      }
-    }
-  }
-  // lane holds column p and rows j = 16 jb + 4 (lane >> 4) + v
-  float* part = partials + static_cast<int64_t>(blockIdx.y) * J * P;
-  if (p >= P) return;
-#pragma unroll
-  for (int jb = 0; jb < JB; ++jb)
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int64_t j = jb * 16 + 4 * (lane >> 4) + v;
-      if (j < J) part[j * P + p] = acc[jb][v];
-    }
-}
-
 // out = f32(bf16(sum over splits, in split order)) of [J, P] partials,
 // stored as out[j * P + p] or, transposed, out[p * J + j].
 __global__ void __launch_bounds__(256)
@@ -341,25 +258,6 @@ TiledPlan plan_tiled(int64_t m, int64_t p, int64_t q) {
   if (want < 1) want = 1;
   pl.chunk = ceil_div(ceil_div(m, want), 32) * 32;
   if (pl.chunk < 32) pl.chunk = 32;
-  pl.splits = ceil_div(m, pl.chunk);
-  if (pl.splits < 1) pl.splits = 1;
-  return pl;
-}
-
-struct RankTnPlan {
-  int64_t gp, splits, chunk;
-};
-
-// wide side P columns in blocks of 64; token splits for about 512 workgroups,
-// chunks of whole 128-token rounds
-RankTnPlan plan_rank_tn(int64_t m, int64_t wide) {
-  RankTnPlan pl;
-  pl.gp = ceil_div(wide, 64);
-  int64_t want = ceil_div(512, pl.gp);
-  const int64_t max_splits = ceil_div(m, 128);
-  if (want > max_splits) want = max_splits;
-  if (want < 1) want = 1;
-  pl.chunk = ceil_div(ceil_div(m, want), 128) * 128;
   pl.splits = ceil_div(m, pl.chunk);
   if (pl.splits < 1) pl.splits = 1;
   return pl;
@@ -491,18 +389,8 @@ hipError_t launch_rank_nt(const uint16_t* a, int64_t lda, const uint16_t* r_mat,
   return hipGetLastError();
 }
 
-// The direct-load kernel wins for short token reductions (no LDS staging,
-// fewer splits); the LDS-tiled one for long ones.
-bool use_thin(int64_t m, int64_t p, int64_t q) {
-  return p < q && q <= 4096 && m * q <= (int64_t{8} << 20);
-}
-
 int64_t rank_tn_workspace_floats(int64_t m, int64_t p, int64_t q) {
-  if (!use_thin(m, p, q)) {
-    const TiledPlan pl = plan_tiled(m, p, q);
-    return pl.splits * p * q;
-  }
-  const RankTnPlan pl = plan_rank_tn(m, q);
+  const TiledPlan pl = plan_tiled(m, p, q);
   return pl.splits * p * q;
 }
 
@@ -511,51 +399,21 @@ hipError_t launch_rank_tn(const uint16_t* x, int64_t ldx, const uint16_t* y, int
                           float* partials, float* out, hipStream_t stream) {
   if (p == 0 || q == 0) return hipSuccess;
   if (m == 0) return launch_fill_f32(out, p * q, 0.0f, stream);
-  if (!use_thin(m, p, q)) {
-    // LDS-tiled kernel over 64 x 16 (or 16 x 64) output tiles
-    const TiledPlan pl = plan_tiled(m, p, q);
-    const dim3 grid(static_cast<unsigned>(pl.gp), static_cast<unsigned>(pl.gq),
-                    static_cast<unsigned>(pl.splits));
-    const int rx = round_x ? 1 : 0;
-    if (pl.wide_p)
-      hipLaunchKernelGGL((k_rank_tn<64, 16>), grid, dim3(256), 0, stream, x, ldx, y, ldy, m, p, q,
-                         rx, x_scale, pl.chunk, partials);
-    else
-      hipLaunchKernelGGL((k_rank_tn<16, 64>), grid, dim3(256), 0, stream, x, ldx, y, ldy, m, p, q,
-                         rx, x_scale, pl.chunk, partials);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k_reduce_partials, dim3(grid1d(p * q)), dim3(256), 0, stream, partials,
-                       pl.splits, p, q, 0, out);
-    return hipGetLastError();
-  }
-  // X thin (dh^T x), short reduction: direct-load kernel; out [P, Q] = D
-  const bool x_wide = false;
-  const int64_t wide = x_wide ? p : q;
-  const int64_t thin = x_wide ? q : p;
-  if (thin > 64) return hipErrorInvalidValue;
-  const RankTnPlan pl = plan_rank_tn(m, wide);
-  const dim3 grid(static_cast<unsigned>(pl.gp), static_cast<unsigned>(pl.splits));
-  const uint16_t* wd = x_wide ? x : y;
-  const int64_t ldw = x_wide ? ldx : ldy;
-  const uint16_t* t = x_wide ? y : x;
-  const int64_t ldt = x_wide ? ldy : ldx;
-  const int rw = (x_wide && round_x) ? 1 : 0;
-  const int rt = (!x_wide && round_x) ? 1 : 0;
-#define RPX_THIN(JB)                                                                              \
-  hipLaunchKernelGGL(k_rank_thin<JB>, grid, dim3(256), 0, stream, wd, ldw, wide, rw, x_scale, t, \
-                     ldt, thin, rt, x_scale, m, pl.chunk, partials)
-  if (thin <= 16)
-    RPX_THIN(1);
-  else if (thin <= 32)
-    RPX_THIN(2);
+  // LDS-tiled kernel over 64 x 16 (or 16 x 64) output tiles
+  const TiledPlan pl = plan_tiled(m, p, q);
+  const dim3 grid(static_cast<unsigned>(pl.gp), static_cast<unsigned>(pl.gq),
+                  static_cast<unsigned>(pl.splits));
+  const int rx = round_x ? 1 : 0;
+  if (pl.wide_p)
+    hipLaunchKernelGGL((k_rank_tn<64, 16>), grid, dim3(256), 0, stream, x, ldx, y, ldy, m, p, q,
+                       rx, x_scale, pl.chunk, partials);
   else
-    RPX_THIN(4);
-#undef RPX_THIN
+    hipLaunchKernelGGL((k_rank_tn<16, 64>), grid, dim3(256), 0, stream, x, ldx, y, ldy, m, p, q,
+                       rx, x_scale, pl.chunk, partials);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(k_reduce_partials, dim3(grid1d(thin * wide)), dim3(256), 0, stream, partials,
-                     pl.splits, thin, wide, x_wide ? 1 : 0, out);
+  hipLaunchKernelGGL(k_reduce_partials, dim3(grid1d(p * q)), dim3(256), 0, stream, partials,
+                     pl.splits, p, q, 0, out);
   return hipGetLastError();
 }
 
