@@ -122,10 +122,8 @@ void plan_backward(A& a, bool fast, int64_t m, int64_t n, int64_t k, int64_t ran
     a.template take<uint16_t>(k * rank);  // A^T
     a.template take<uint16_t>(m * rank);  // dh
     a.template take<uint16_t>(k * n);     // W_b^T
-    int64_t part = rank_tn_workspace_floats(m, n, rank);
-    const int64_t part_a = rank_tn_workspace_floats(m, rank, k);
-    if (part_a > part) part = part_a;
-    a.template take<float>(part);
+    a.template take<float>(rank_tn_workspace_floats(m, n, rank));  // dB partials
+    a.template take<float>(rank_tn_workspace_floats(m, rank, k));  // dA partials
     return;
   }
   a.template take<uint8_t>(m * n * static_cast<int64_t>(elem_size(dtype)));  // g_a
@@ -397,10 +395,8 @@ int rpx_int4lora_backward(const void* grad, const void* x, int dtype, int64_t m,
     uint16_t* at = arena.take<uint16_t>(k * rank);
     uint16_t* dh = arena.take<uint16_t>(m * rank);
     uint16_t* wt = arena.take<uint16_t>(k * n);
-    int64_t part_n = rank_tn_workspace_floats(m, n, rank);
-    const int64_t part_a = rank_tn_workspace_floats(m, rank, k);
-    if (part_a > part_n) part_n = part_a;
-    float* part = arena.take<float>(part_n);
+    float* part_b = arena.take<float>(rank_tn_workspace_floats(m, n, rank));
+    float* part_a = arena.take<float>(rank_tn_workspace_floats(m, rank, k));
     if (arena.overflow) return fail_invalid("rpx_int4lora_backward: workspace too small");
     // B^T [r, N] so that dh = g_a . B is an NT product; A^T [K, r] for the
     // dx epilogue's contiguous fragment loads; W_b^T [K, N] for dx
@@ -416,10 +412,11 @@ int rpx_int4lora_backward(const void* grad, const void* x, int dtype, int64_t m,
     // dh = bf16(bf16(g * c) . B)
     RPX_HIP(launch_rank_nt(gb, n, bt, n, m, rank, n, true, c, dh, rank, st),
             "int4lora_backward: dh");
-    // dB = f32(bf16(g_a^T . h))
-    RPX_HIP(launch_rank_tn(gb, n, static_cast<const uint16_t*>(h), rank, m, n, rank, true, c, part,
-                           d_lora_b, st),
-            "int4lora_backward: dB");
+    // dB = f32(bf16(g_a^T . h)) and dA = f32(bf16(dh^T . x)), one launch
+    RPX_HIP(launch_rank_tn2(gb, n, static_cast<const uint16_t*>(h), rank, m, n, rank, true, c,
+                            part_b, d_lora_b, dh, rank, xb, k, m, rank, k, false, 1.0f, part_a,
+                            d_lora_a, st),
+            "int4lora_backward: dB, dA");
     if (!prep_fused)
       RPX_HIP(launch_int4_dequant_t(packed, scale_bits, wt, n, k, pc, ng, g, n, st),
               "int4lora_backward: dequantized transpose");
@@ -435,9 +432,6 @@ int rpx_int4lora_backward(const void* grad, const void* x, int dtype, int64_t m,
     epi.scale = 1.0f;
     RPX_HIP(launch_gemm_bf16(gb, n, wt, n, m, k, n, static_cast<uint16_t*>(dx), k, epi, st),
             "int4lora_backward: dx");
-    // dA = f32(bf16(dh^T . x))
-    RPX_HIP(launch_rank_tn(dh, rank, xb, k, m, rank, k, false, 1.0f, part, d_lora_a, st),
-            "int4lora_backward: dA");
     return kOk;
   }
   const size_t es = elem_size(dtype);

@@ -77,6 +77,14 @@ int64_t rank_tn_workspace_floats(int64_t m, int64_t p, int64_t q);
 hipError_t launch_rank_tn(const uint16_t* x, int64_t ldx, const uint16_t* y, int64_t ldy,
                           int64_t m, int64_t p, int64_t q, bool round_x, float x_scale,
                           float* partials, float* out, hipStream_t stream);
+// Two independent products of the form above in one launch (plus one reduce
+// launch); each takes its own partials region. x1 == nullptr: first only.
+hipError_t launch_rank_tn2(const uint16_t* x0, int64_t ldx0, const uint16_t* y0, int64_t ldy0,
+                           int64_t m0, int64_t p0, int64_t q0, bool round_x0, float x_scale0,
+                           float* partials0, float* out0, const uint16_t* x1, int64_t ldx1,
+                           const uint16_t* y1, int64_t ldy1, int64_t m1, int64_t p1, int64_t q1,
+                           bool round_x1, float x_scale1, float* partials1, float* out1,
+                           hipStream_t stream);
 // B^T [r, N], A^T [K, r] and W_b^T [K, N] (groups that are multiples of 32)
 // in one launch.
 hipError_t launch_int4lora_bwd_prep(const uint16_t* b, uint16_t* bt, const uint16_t* a,

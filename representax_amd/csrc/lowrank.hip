@@ -103,32 +103,53 @@ __global__ void __launch_bounds__(256)
   }
 }
 
-// Token-reduction product. Tile BP x BQ outputs, chunk of `chunk` tokens per
-// workgroup (blockIdx.z), 256 tokens per LDS step.
+// Token-reduction product: partials[z][p][q] = sum over the token chunk z of
+// op(X[m, p]) * Y[m, q]. Tile BP x BQ outputs, `chunk` tokens per workgroup,
+// 256 tokens per LDS step.
+struct RankTnArgs {
+  const uint16_t* X;
+  int64_t ldx;
+  const uint16_t* Y;
+  int64_t ldy;
+  int64_t M, P, Q;
+  int round_x;
+  float x_scale;
+  int64_t chunk;
+  float* partials;
+  int64_t gp, gq, blocks;  // tile grid and gp * gq * splits
+  int wide_p;              // 64 x 16 tiles when P is the long side, else 16 x 64
+};
+
+constexpr int kTokStep = 256;
+constexpr int kRankLds = kTokStep * ((64 + 8) + (16 + 8));  // elements
+
 template <int BP, int BQ>
-__global__ void __launch_bounds__(256)
-    k_rank_tn(const uint16_t* __restrict__ X, int64_t ldx, const uint16_t* __restrict__ Y,
-              int64_t ldy, int64_t M, int64_t P, int64_t Q, int round_x, float x_scale,
-              int64_t chunk, float* __restrict__ partials) {
+__device__ __forceinline__ void rank_tn_body(const RankTnArgs& a, int64_t bx, int64_t by,
+                                             int64_t bz, uint16_t* lds) {
   // 256 tokens per step: every thread's loads of a step are issued together,
   // and the next step's loads are in flight while this step's MFMAs run from
   // LDS
-  constexpr int TS = 256;
+  constexpr int TS = kTokStep;
   constexpr int PP = 16 / 2;  // padding (elements) per LDS row
-  __shared__ uint16_t sX[TS][BP + PP];
-  __shared__ uint16_t sY[TS][BQ + PP];
+  typedef uint16_t RowX[BP + PP];
+  typedef uint16_t RowY[BQ + PP];
+  RowX* sX = reinterpret_cast<RowX*>(lds);
+  RowY* sY = reinterpret_cast<RowY*>(lds + TS * (BP + PP));
   constexpr int XV = TS * (BP / 8) / 256;  // 16-byte vectors per thread per step
   constexpr int YV = TS * (BQ / 8) / 256;
   constexpr int NB = (BP / 16) * (BQ / 16);
   constexpr int PER_WAVE = (NB + 3) / 4;
+  const uint16_t* __restrict__ X = a.X;
+  const uint16_t* __restrict__ Y = a.Y;
+  const int64_t ldx = a.ldx, ldy = a.ldy, P = a.P, Q = a.Q;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int64_t p0 = static_cast<int64_t>(blockIdx.x) * BP;
-  const int64_t q0 = static_cast<int64_t>(blockIdx.y) * BQ;
-  const int64_t mbeg = static_cast<int64_t>(blockIdx.z) * chunk;
-  int64_t mend = mbeg + chunk;
-  if (mend > M) mend = M;
+  const int64_t p0 = bx * BP;
+  const int64_t q0 = by * BQ;
+  const int64_t mbeg = bz * a.chunk;
+  int64_t mend = mbeg + a.chunk;
+  if (mend > a.M) mend = a.M;
   const bool x_al = (ldx % 8 == 0) && ((reinterpret_cast<uintptr_t>(X) & 15) == 0);
   const bool y_al = (ldy % 8 == 0) && ((reinterpret_cast<uintptr_t>(Y) & 15) == 0);
   f32x4_t acc[PER_WAVE];
@@ -166,7 +187,7 @@ __global__ void __launch_bounds__(256)
     for (int u = 0; u < XV; ++u) {
       const int v = tid + 256 * u;
       u32x4_t xv = xr[u];
-      if (round_x) xv = scale_round8(xv, x_scale);
+      if (a.round_x) xv = scale_round8(xv, a.x_scale);
       *reinterpret_cast<u32x4_t*>(&sX[v / (BP / 8)][(v % (BP / 8)) * 8]) = xv;
     }
 #pragma unroll
@@ -202,7 +223,7 @@ __global__ void __launch_bounds__(256)
       }
     }
   }
-  float* part = partials + static_cast<int64_t>(blockIdx.z) * P * Q;
+  float* part = a.partials + bz * P * Q;
 #pragma unroll
   for (int b = 0; b < PER_WAVE; ++b) {
     const int blk = wave + 4 * b;
@@ -218,25 +239,56 @@ __global__ void __launch_bounds__(256)
   }
 }
 
+__device__ __forceinline__ void rank_tn_dispatch(const RankTnArgs& a, int64_t b, uint16_t* lds) {
+  const int64_t per = a.gp * a.gq;
+  const int64_t bz = b / per;
+  const int64_t r = b - bz * per;
+  if (a.wide_p)
+    rank_tn_body<64, 16>(a, r % a.gp, r / a.gp, bz, lds);
+  else
+    rank_tn_body<16, 64>(a, r % a.gp, r / a.gp, bz, lds);
+}
+
+// Up to two token-reduction products in one launch: blocks [0, a0.blocks)
+// take the first, the rest the second.
+__global__ void __launch_bounds__(256) k_rank_tn(RankTnArgs a0, RankTnArgs a1) {
+  __shared__ __align__(16) uint16_t lds[kRankLds];
+  const int64_t b = blockIdx.x;
+  if (b < a0.blocks)
+    rank_tn_dispatch(a0, b, lds);
+  else
+    rank_tn_dispatch(a1, b - a0.blocks, lds);
+}
+
 // out = f32(bf16(sum over splits, in split order)) of [J, P] partials,
-// stored as out[j * P + p] or, transposed, out[p * J + j].
-__global__ void __launch_bounds__(256)
-    k_reduce_partials(const float* __restrict__ partials, int64_t splits, int64_t J, int64_t P,
-                      int transposed, float* __restrict__ out) {
-  const int64_t count = J * P;
-  for (int64_t e = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; e < count;
+// stored as out[j * P + p]; two problems in one launch (the second's
+// elements follow the first's in the grid-stride range).
+struct ReduceArgs {
+  const float* partials;
+  int64_t splits, count;
+  float* out;
+};
+
+__device__ __forceinline__ void reduce_one(const ReduceArgs& a, int64_t e) {
+  float s = 0.0f;
+  int64_t i = 0;
+  for (; i + 4 <= a.splits; i += 4) {
+    const float x0 = a.partials[i * a.count + e], x1 = a.partials[(i + 1) * a.count + e];
+    const float x2 = a.partials[(i + 2) * a.count + e], x3 = a.partials[(i + 3) * a.count + e];
+    s = (((s + x0) + x1) + x2) + x3;
+  }
+  for (; i < a.splits; ++i) s += a.partials[i * a.count + e];
+  a.out[e] = round_bf16(s);
+}
+
+__global__ void __launch_bounds__(256) k_reduce_partials(ReduceArgs a0, ReduceArgs a1) {
+  const int64_t total = a0.count + a1.count;
+  for (int64_t e = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; e < total;
        e += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    float s = 0.0f;
-    int64_t i = 0;
-    for (; i + 4 <= splits; i += 4) {
-      const float a = partials[i * count + e], b = partials[(i + 1) * count + e];
-      const float c = partials[(i + 2) * count + e], d = partials[(i + 3) * count + e];
-      s = (((s + a) + b) + c) + d;
-    }
-    for (; i < splits; ++i) s += partials[i * count + e];
-    const int64_t j = e / P;
-    const int64_t p = e % P;
-    out[transposed ? p * J + j : e] = round_bf16(s);
+    if (e < a0.count)
+      reduce_one(a0, e);
+    else
+      reduce_one(a1, e - a0.count);
   }
 }
 
@@ -394,27 +446,72 @@ int64_t rank_tn_workspace_floats(int64_t m, int64_t p, int64_t q) {
   return pl.splits * p * q;
 }
 
+namespace {
+RankTnArgs rank_tn_args(const uint16_t* x, int64_t ldx, const uint16_t* y, int64_t ldy, int64_t m,
+                        int64_t p, int64_t q, bool round_x, float x_scale, float* partials) {
+  const TiledPlan pl = plan_tiled(m, p, q);
+  RankTnArgs a;
+  a.X = x;
+  a.ldx = ldx;
+  a.Y = y;
+  a.ldy = ldy;
+  a.M = m;
+  a.P = p;
+  a.Q = q;
+  a.round_x = round_x ? 1 : 0;
+  a.x_scale = x_scale;
+  a.chunk = pl.chunk;
+  a.partials = partials;
+  a.gp = pl.gp;
+  a.gq = pl.gq;
+  a.blocks = pl.gp * pl.gq * pl.splits;
+  a.wide_p = pl.wide_p ? 1 : 0;
+  return a;
+}
+}  // namespace
+
+hipError_t launch_rank_tn2(const uint16_t* x0, int64_t ldx0, const uint16_t* y0, int64_t ldy0,
+                           int64_t m0, int64_t p0, int64_t q0, bool round_x0, float x_scale0,
+                           float* partials0, float* out0, const uint16_t* x1, int64_t ldx1,
+                           const uint16_t* y1, int64_t ldy1, int64_t m1, int64_t p1, int64_t q1,
+                           bool round_x1, float x_scale1, float* partials1, float* out1,
+                           hipStream_t stream) {
+  // empty problems: nothing, or a zero fill for an empty token range
+  RankTnArgs a0{}, a1{};
+  ReduceArgs r0{nullptr, 0, 0, out0}, r1{nullptr, 0, 0, out1};
+  if (p0 > 0 && q0 > 0) {
+    if (m0 == 0) {
+      hipError_t e = launch_fill_f32(out0, p0 * q0, 0.0f, stream);
+      if (e != hipSuccess) return e;
+    } else {
+      a0 = rank_tn_args(x0, ldx0, y0, ldy0, m0, p0, q0, round_x0, x_scale0, partials0);
+      r0 = ReduceArgs{partials0, plan_tiled(m0, p0, q0).splits, p0 * q0, out0};
+    }
+  }
+  if (x1 != nullptr && p1 > 0 && q1 > 0) {
+    if (m1 == 0) {
+      hipError_t e = launch_fill_f32(out1, p1 * q1, 0.0f, stream);
+      if (e != hipSuccess) return e;
+    } else {
+      a1 = rank_tn_args(x1, ldx1, y1, ldy1, m1, p1, q1, round_x1, x_scale1, partials1);
+      r1 = ReduceArgs{partials1, plan_tiled(m1, p1, q1).splits, p1 * q1, out1};
+    }
+  }
+  if (a0.blocks + a1.blocks == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_rank_tn, dim3(static_cast<unsigned>(a0.blocks + a1.blocks)), dim3(256), 0,
+                     stream, a0, a1);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(k_reduce_partials, dim3(grid1d(r0.count + r1.count)), dim3(256), 0, stream,
+                     r0, r1);
+  return hipGetLastError();
+}
+
 hipError_t launch_rank_tn(const uint16_t* x, int64_t ldx, const uint16_t* y, int64_t ldy,
                           int64_t m, int64_t p, int64_t q, bool round_x, float x_scale,
                           float* partials, float* out, hipStream_t stream) {
-  if (p == 0 || q == 0) return hipSuccess;
-  if (m == 0) return launch_fill_f32(out, p * q, 0.0f, stream);
-  // LDS-tiled kernel over 64 x 16 (or 16 x 64) output tiles
-  const TiledPlan pl = plan_tiled(m, p, q);
-  const dim3 grid(static_cast<unsigned>(pl.gp), static_cast<unsigned>(pl.gq),
-                  static_cast<unsigned>(pl.splits));
-  const int rx = round_x ? 1 : 0;
-  if (pl.wide_p)
-    hipLaunchKernelGGL((k_rank_tn<64, 16>), grid, dim3(256), 0, stream, x, ldx, y, ldy, m, p, q,
-                       rx, x_scale, pl.chunk, partials);
-  else
-    hipLaunchKernelGGL((k_rank_tn<16, 64>), grid, dim3(256), 0, stream, x, ldx, y, ldy, m, p, q,
-                       rx, x_scale, pl.chunk, partials);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(k_reduce_partials, dim3(grid1d(p * q)), dim3(256), 0, stream, partials,
-                     pl.splits, p, q, 0, out);
-  return hipGetLastError();
+  return launch_rank_tn2(x, ldx, y, ldy, m, p, q, round_x, x_scale, partials, out, nullptr, 0,
+                         nullptr, 0, 0, 0, 0, false, 1.0f, nullptr, nullptr, stream);
 }
 
 hipError_t launch_fill_f32(float* out, int64_t n, float v, hipStream_t stream) {
