@@ -52,18 +52,29 @@ __device__ __forceinline__ bf16x8_t load8_j(const uint16_t* base, int64_t stride
   return as_bf16x8(u32x4_t{w[0], w[1], w[2], w[3]});
 }
 
-// Exact nibble dequant of one packed dword (8 values) into 4 bf16 pairs.
-// q*s = fma(float(u ^ 8), s, -8 s) is exact in f32 (q has 4 bits, s 8).
-__device__ __forceinline__ void dequant8(uint32_t word, float s, float m8s, uint32_t* o) {
-  const uint32_t x = word ^ 0x88888888u;
-  const uint32_t lo = x & 0x0F0F0F0Fu;
-  const uint32_t hi = (x >> 4) & 0x0F0F0F0Fu;
-#pragma unroll
-  for (int b = 0; b < 4; ++b) {
-    const float fl = static_cast<float>((lo >> (8 * b)) & 0xFFu);
-    const float fh = static_cast<float>((hi >> (8 * b)) & 0xFFu);
-    o[b] = pack_bf16x2(__builtin_fmaf(fl, s, m8s), __builtin_fmaf(fh, s, m8s));
-  }
+// Byte B of v as a float. Written as uint -> float of (v >> 8B) & 0xFF, which
+// the backend selects as one v_cvt_f32_ubyte<B>.
+template <int B>
+__device__ __forceinline__ float ubyte_f32(uint32_t v) {
+  return static_cast<float>((v >> (8 * B)) & 0xFFu);
+}
+
+// Nibble pair b (columns 2b, 2b + 1) of a packed dword as one bf16 pair,
+// exact: with u = nibble ^ 8 (the two's complement value plus 8),
+// q * s = fma(float(u), s, -8 s) is exact in f32 (q has 4 bits, s 8), and
+// v_cvt_pk_bf16_f32 rounds it once. lo / hi are the dword's low / high
+// nibbles after the xor, one per byte.
+template <int B>
+__device__ __forceinline__ uint32_t dequant_pair(uint32_t lo, uint32_t hi, float s, float m8s) {
+  return pack_bf16x2(__builtin_fmaf(ubyte_f32<B>(lo), s, m8s),
+                     __builtin_fmaf(ubyte_f32<B>(hi), s, m8s));
+}
+
+// Rounds a and b to the nearest bf16 values (one v_cvt_pk_bf16_f32).
+__device__ __forceinline__ void round2(float& a, float& b) {
+  const uint32_t p = pack_bf16x2(a, b);
+  a = __builtin_bit_cast(float, p << 16);
+  b = __builtin_bit_cast(float, p & 0xFFFF0000u);
 }
 
 // Packed-B rows are 32 bytes per slice; the two 16-byte halves of rows 8..15
@@ -196,16 +207,24 @@ __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_
       bs[fn] = bf16_to_f32(sc[r * ng + g]);
     }
   };
-  // unit u (0 .. 4 FN - 1) of step kk: fragment u / 4, dword u % 4; the same
-  // arithmetic as dequant8
+  // unit u (0 .. 4 FN - 1) of step kk: fragment u / 4, bf16 pair u % 4
   auto dq_unit = [&](int kk, int u) {
     const int fn = u / 4;
-    const int b = u % 4;
     const uint32_t x = bp[fn][kk] ^ 0x88888888u;
-    const float fl = static_cast<float>(((x & 0x0F0F0F0Fu) >> (8 * b)) & 0xFFu);
-    const float fh = static_cast<float>((((x >> 4) & 0x0F0F0F0Fu) >> (8 * b)) & 0xFFu);
+    uint32_t lo = x & 0x0F0F0F0Fu;
+    uint32_t hi = (x >> 4) & 0x0F0F0F0Fu;
+    // opaque to the optimizer: keeps the per-byte conversions from being
+    // narrowed to bit-field extracts (one instruction instead of two)
+    asm("" : "+v"(lo), "+v"(hi));
     const float m8s = -8.0f * bs[fn];
-    bq[kk][fn][b] = pack_bf16x2(__builtin_fmaf(fl, bs[fn], m8s), __builtin_fmaf(fh, bs[fn], m8s));
+    uint32_t r;
+    switch (u % 4) {
+      case 0: r = dequant_pair<0>(lo, hi, bs[fn], m8s); break;
+      case 1: r = dequant_pair<1>(lo, hi, bs[fn], m8s); break;
+      case 2: r = dequant_pair<2>(lo, hi, bs[fn], m8s); break;
+      default: r = dequant_pair<3>(lo, hi, bs[fn], m8s); break;
+    }
+    bq[kk][fn][u % 4] = r;
   };
   auto mma = [&](int i, int kk) {
     const int fn = i / FM;
@@ -314,82 +333,180 @@ __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   // Epilogue --------------------------------------------------------------
-  // The low-rank term t = C R^T for this lane's rows m and columns n is one
-  // more 32x32x16 MFMA per 16 ranks; its fragments are loaded up front.
+  // y = bf16(bf16(acc) + bf16(bf16(t) * scale)) (+ bias, rounded again), the
+  // reference's rounding points, where t = C R^T is one more 32x32x16 MFMA
+  // per 16 ranks. Values are rounded in pairs (one v_cvt_pk_bf16_f32 per
+  // two), staged as bf16 in LDS and written as whole row segments of the
+  // workgroup tile.
   constexpr int kMaxJB = JB > 0 ? JB : 1;  // ceil(rank / 16), rank <= 16 * JB
   const int jblocks = JB > 0 ? static_cast<int>((epi.rank + 15) / 16) : 0;
-  const bool vec_store = (ldc % 4 == 0) && ((reinterpret_cast<uintptr_t>(out) & 7) == 0);
+  const int64_t mw = m0 + wm * TM;  // first row of this wave's sub-tile
+  const int64_t nw = n0 + wn * TN;  // first column
+  const bool inside = mw + TM <= M && nw + TN <= N;
+  // low-rank operands with unit rank stride, whole 16-rank blocks and
+  // 16-byte aligned rows: every fragment is one plain 16-byte load
+  const bool lr_vec =
+      inside && epi.rows_sj == 1 && epi.cols_sj == 1 && (epi.rank & 15) == 0 &&
+      (epi.rows_sn & 7) == 0 && (epi.cols_sm & 7) == 0 &&
+      ((reinterpret_cast<uintptr_t>(epi.rows) | reinterpret_cast<uintptr_t>(epi.cols)) & 15) == 0;
   bf16x8_t cf[kMaxJB][FM];
+  bf16x8_t rf[kMaxJB][FN];
   if (jblocks > 0) {
 #pragma unroll
     for (int jb = 0; jb < kMaxJB; ++jb) {
       if (jb >= jblocks) break;
-      const int64_t jl = jb * 16 + (lane >> 5) * 8;
+      const int64_t jl = jb * 16 + half * 8;
 #pragma unroll
       for (int fm = 0; fm < FM; ++fm) {
-        const int64_t m = m0 + wm * TM + fm * 32 + (lane & 31);
-        cf[jb][fm] = load8_j(epi.cols + m * epi.cols_sm + jl * epi.cols_sj, epi.cols_sj,
-                             m < M ? valid8(epi.rank, jl) : 0);
+        const int64_t m = mw + fm * 32 + frow;
+        cf[jb][fm] = lr_vec ? *reinterpret_cast<const bf16x8_t*>(epi.cols + m * epi.cols_sm + jl)
+                            : load8_j(epi.cols + m * epi.cols_sm + jl * epi.cols_sj, epi.cols_sj,
+                                      m < M ? valid8(epi.rank, jl) : 0);
+      }
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn) {
+        const int64_t n = nw + fn * 32 + frow;
+        rf[jb][fn] = lr_vec ? *reinterpret_cast<const bf16x8_t*>(epi.rows + n * epi.rows_sn + jl)
+                            : load8_j(epi.rows + n * epi.rows_sn + jl * epi.rows_sj, epi.rows_sj,
+                                      n < N ? valid8(epi.rank, jl) : 0);
       }
     }
   }
+  // bias of this lane's columns nw + 32 fn + 8 vg + 4 half + e
+  const bool has_bias = epi.bias != nullptr;
+  float bias4[FN][4][4];
+  if (has_bias) {
+    const bool bvec = inside && (reinterpret_cast<uintptr_t>(epi.bias) & 7) == 0;
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+      for (int vg = 0; vg < 4; ++vg) {
+        const int64_t nb = nw + fn * 32 + 8 * vg + 4 * half;
+        if (bvec) {
+          const u32x2_t w2 = *reinterpret_cast<const u32x2_t*>(epi.bias + nb);
+          bias4[fn][vg][0] = bf16lo_to_f32(w2[0]);
+          bias4[fn][vg][1] = bf16hi_to_f32(w2[0]);
+          bias4[fn][vg][2] = bf16lo_to_f32(w2[1]);
+          bias4[fn][vg][3] = bf16hi_to_f32(w2[1]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            bias4[fn][vg][e] = nb + e < N ? bf16_to_f32(epi.bias[nb + e]) : 0.0f;
+        }
+      }
+  }
+  // bf16(t) * scale is already a bf16 value when scale = 2^k, k >= 0 (the
+  // product only shifts the exponent; overflow gives inf either way)
+  const uint32_t sbits = __builtin_bit_cast(uint32_t, epi.scale);
+  const bool scale_exact = (sbits & 0x807FFFFFu) == 0 && sbits >= 0x3F800000u && sbits < 0x7F800000u;
+
+  uint32_t ypk[FN][FM][8];  // bf16 pairs (columns 8 (v / 4) + 4 half + v % 4, v even)
 #pragma unroll
   for (int fn = 0; fn < FN; ++fn) {
-    const int64_t n_blk = n0 + wn * TN + fn * 32;
-    bf16x8_t rf[kMaxJB];
-    if (jblocks > 0) {
-      const int64_t n_row = n_blk + (lane & 31);
-#pragma unroll
-      for (int jb = 0; jb < kMaxJB; ++jb) {
-        if (jb >= jblocks) break;
-        const int64_t jl = jb * 16 + (lane >> 5) * 8;
-        rf[jb] = load8_j(epi.rows + n_row * epi.rows_sn + jl * epi.rows_sj, epi.rows_sj,
-                         n_row < N ? valid8(epi.rank, jl) : 0);
-      }
-    }
-    float bias4[4][4];
-#pragma unroll
-    for (int vg = 0; vg < 4; ++vg)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int64_t nn = n_blk + 8 * vg + 4 * (lane >> 5) + e;
-        bias4[vg][e] = (epi.bias != nullptr && nn < N) ? bf16_to_f32(epi.bias[nn]) : 0.0f;
-      }
 #pragma unroll
     for (int fm = 0; fm < FM; ++fm) {
-      const int64_t m = m0 + wm * TM + fm * 32 + (lane & 31);
       f32x16_t t;
 #pragma unroll
       for (int v = 0; v < 16; ++v) t[v] = 0.0f;
 #pragma unroll
       for (int jb = 0; jb < kMaxJB; ++jb) {
         if (jb >= jblocks) break;
-        t = __builtin_amdgcn_mfma_f32_32x32x16_bf16(rf[jb], cf[jb][fm], t, 0, 0, 0);
+        t = __builtin_amdgcn_mfma_f32_32x32x16_bf16(rf[jb][fn], cf[jb][fm], t, 0, 0, 0);
       }
-      if (m >= M) continue;
 #pragma unroll
-      for (int vg = 0; vg < 4; ++vg) {
-        const int64_t nb = n_blk + 8 * vg + 4 * (lane >> 5);
-        float y[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int v = 4 * vg + e;
-          float r = round_bf16(acc[fn][fm][v]);
-          if (jblocks > 0) r = round_bf16(r + round_bf16(round_bf16(t[v]) * epi.scale));
-          if (epi.bias != nullptr) r = round_bf16(r + bias4[vg][e]);
-          y[e] = r;
+      for (int v = 0; v < 16; v += 2) {
+        float a0 = acc[fn][fm][v];
+        float a1 = acc[fn][fm][v + 1];
+        if (jblocks > 0) {
+          round2(a0, a1);
+          float t0 = t[v];
+          float t1 = t[v + 1];
+          round2(t0, t1);
+          t0 *= epi.scale;
+          t1 *= epi.scale;
+          if (!scale_exact) round2(t0, t1);
+          a0 += t0;
+          a1 += t1;
         }
-        uint16_t* dst = out + m * ldc + nb;
-        if (vec_store && nb + 3 < N) {
-          *reinterpret_cast<u32x2_t*>(dst) =
-              u32x2_t{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])};
-        } else {
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (nb + e < N) dst[e] = f32_to_bf16(y[e]);
+        if (has_bias) {
+          round2(a0, a1);
+          a0 += bias4[fn][v / 4][v % 4];
+          a1 += bias4[fn][v / 4][v % 4 + 1];
         }
+        ypk[fn][fm][v / 2] = pack_bf16x2(a0, a1);
       }
     }
+  }
+
+  const bool vec_out = (ldc & 7) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0;
+  constexpr int P = BN * 2 + 16;  // LDS row pitch of the staged tile
+  if constexpr (BM * P <= NS * STAGE) {
+    wait_sync<0>();  // every wave is done reading the pipeline stages
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+        for (int vg = 0; vg < 4; ++vg) {
+          const int ml = wm * TM + fm * 32 + frow;
+          const int nl = wn * TN + fn * 32 + 8 * vg + 4 * half;
+          *reinterpret_cast<u32x2_t*>(smem + ml * P + nl * 2) =
+              u32x2_t{ypk[fn][fm][2 * vg], ypk[fn][fm][2 * vg + 1]};
+        }
+    __syncthreads();
+    constexpr int CPR = BN / 8;  // 16-byte chunks per tile row
+    constexpr int ITS = BM * CPR / NT;
+    static_assert((BM * CPR) % NT == 0, "tile chunks must split evenly over the threads");
+    if (vec_out && m0 + BM <= M && n0 + BN <= N) {
+      u32x4_t v[ITS];
+#pragma unroll
+      for (int it = 0; it < ITS; ++it) {
+        const int idx = it * NT + tid;
+        v[it] = *reinterpret_cast<const u32x4_t*>(smem + (idx / CPR) * P + (idx % CPR) * 16);
+      }
+#pragma unroll
+      for (int it = 0; it < ITS; ++it) {
+        const int idx = it * NT + tid;
+        *reinterpret_cast<u32x4_t*>(out + (m0 + idx / CPR) * ldc + n0 + 8 * (idx % CPR)) = v[it];
+      }
+      return;
+    }
+    for (int it = 0; it < ITS; ++it) {
+      const int idx = it * NT + tid;
+      const int64_t m = m0 + idx / CPR;
+      const int64_t n = n0 + 8 * (idx % CPR);
+      if (m >= M || n >= N) continue;
+      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(smem + (idx / CPR) * P + (idx % CPR) * 16);
+      uint16_t* d = out + m * ldc + n;
+      if (vec_out && n + 7 < N) {
+        *reinterpret_cast<u32x4_t*>(d) = v;
+      } else {
+        for (int e = 0; e < 8; ++e)
+          if (n + e < N) d[e] = static_cast<uint16_t>((v[e >> 1] >> (16 * (e & 1))) & 0xFFFFu);
+      }
+    }
+  } else {
+    // tile too large to stage in the pipeline's LDS: 8-byte stores per lane
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm) {
+        const int64_t m = mw + fm * 32 + frow;
+        if (m >= M) continue;
+#pragma unroll
+        for (int vg = 0; vg < 4; ++vg) {
+          const int64_t nb = nw + fn * 32 + 8 * vg + 4 * half;
+          uint16_t* dst = out + m * ldc + nb;
+          if (vec_out && nb + 3 < N) {
+            *reinterpret_cast<u32x2_t*>(dst) = u32x2_t{ypk[fn][fm][2 * vg], ypk[fn][fm][2 * vg + 1]};
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (nb + e < N)
+                dst[e] = static_cast<uint16_t>((ypk[fn][fm][2 * vg + e / 2] >> (16 * (e & 1))) & 0xFFFFu);
+          }
+        }
+      }
   }
 }
 
