@@ -583,16 +583,29 @@ hipError_t dispatch_int4(const uint16_t* a, int64_t lda, const Int4Operand& w, i
     return run_gemm<256, 256, 2, 2, 3, 1, true>(a, lda, nullptr, 0, w, m, n, k, out, ldc, epi,
                                                 stream);
   if (cfg < 1 || cfg > 3) {
-    // 128 x 32 wave tiles at two workgroups (8 waves) per CU: each
-    // dequantized B fragment feeds four MFMAs, and a CU's 8 waves keep the
-    // LDS fragment reads and the dequantization VALU work under the MFMAs
+    // 128 x 32 wave tiles, two or three workgroups (8 or 12 waves) per CU:
+    // each dequantized B fragment feeds four MFMAs, and a CU's waves keep
+    // the LDS fragment reads and the dequantization VALU work under the MFMAs
     cfg = ceil_div(m, 128) * ceil_div(n, 128) >= 128 ? 2 : 3;
+  }
+  if (cfg == 2) {
+    // three workgroups per CU (12 waves) with a two-stage pipeline while the
+    // block's scales leave room for them in LDS, else two with three stages;
+    // when the scales (many groups) leave room for only one, the 256-row
+    // tile of the same LDS budget does twice the work per block
+    const int64_t scale_bytes = 128 * w.n_groups * 2;
+    if (gemm_lds_bytes(128, 128, 2, true) + scale_bytes <= (160 * 1024) / 3)
+      return run_gemm<128, 128, 1, 4, 2, 3, true>(a, lda, nullptr, 0, w, m, n, k, out, ldc, epi,
+                                                  stream);
+    if (gemm_lds_bytes(128, 128, 3, true) + scale_bytes > (160 * 1024) / 2 && m >= 256 &&
+        gemm_lds_bytes(256, 128, 3, true) + scale_bytes <= 160 * 1024)
+      cfg = 1;
+    else
+      return run_gemm<128, 128, 1, 4, 3, 2, true>(a, lda, nullptr, 0, w, m, n, k, out, ldc, epi,
+                                                  stream);
   }
   if (cfg == 1)
     return run_gemm<256, 128, 1, 4, 3, 1, true>(a, lda, nullptr, 0, w, m, n, k, out, ldc, epi,
-                                                stream);
-  if (cfg == 2)
-    return run_gemm<128, 128, 1, 4, 3, 2, true>(a, lda, nullptr, 0, w, m, n, k, out, ldc, epi,
                                                 stream);
   return run_gemm<64, 128, 1, 4, 3, 2, true>(a, lda, nullptr, 0, w, m, n, k, out, ldc, epi,
                                              stream);
