@@ -49,8 +49,8 @@ def parse_args():
     p.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a HIP graph")
     p.add_argument("--no-secondary", action="store_true")
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--only", choices=["fp8", "int4lora", "skinny", "bert", "qwen3", "fp8gemm",
-                                      "copyref"], default=None,
+    p.add_argument("--only", choices=["fp8", "fp8delayed", "int4lora", "skinny", "bert", "qwen3",
+                                      "fp8gemm", "copyref"], default=None,
                    help="run one workload and nothing else (profiling); fp8gemm: three eager "
                         "launches of each fp8 GEMM call of one step; copyref: a plain 256 MiB "
                         "device copy, the reference for scaling FETCH_SIZE / WRITE_SIZE")
@@ -172,6 +172,51 @@ def fp8_step_fn(layers):
                                           right_transposed=True)
 
     return step
+
+
+def fp8_delayed_step_fn(layers, history_len=16):
+    """The same step with delayed scaling: every operand is cast once with the
+    scale its slot holds (saturating) while its amax is recorded (a linear's
+    input and weight in one launch), and one launch updates all 18 slots'
+    scales at the end of the step."""
+
+    import torch
+
+    from representax_amd import ops
+    from representax_amd.precision import DelayedScaling
+
+    dev = layers[0][1].device
+    state = DelayedScaling(3 * len(layers), history_len, device=dev)
+    slots = [state.allocate(("e4m3fn", "e4m3fn", "e5m2")) for _ in layers]
+    sc = state.scales
+
+    def step():
+        for (_, x, w, gy, k, n), (sx, sw, sg) in zip(layers, slots):
+            m = x.shape[0]
+            (qx, qxt), (qw, qwt) = ops.fp8_cast_delayed2(x, sx, w, sw, state, "e4m3fn",
+                                                         rowmajor=True, transposed=True)
+            ops._gemm_into(qx, "e4m3fn", sc[sx:sx + 1], qw, "e4m3fn", sc[sw:sw + 1],
+                           torch.empty((m, n), dtype=x.dtype, device=dev))
+            qg, qgt = ops.fp8_cast_delayed(gy, state, sg, "e5m2", rowmajor=True, transposed=True)
+            ops._gemm_into(qg, "e5m2", sc[sg:sg + 1], qwt, "e4m3fn", sc[sw:sw + 1],
+                           torch.empty((m, k), dtype=x.dtype, device=dev))
+            ops._gemm_into(qgt, "e5m2", sc[sx:sx + 1], qxt, "e4m3fn", sc[sg:sg + 1],
+                           torch.empty((n, k), dtype=x.dtype, device=dev))
+        state.update()
+
+    return step
+
+
+def run_fp8_delayed(layers, tokens, steps, warmup, use_graph):
+    fn, mode = maybe_graph(fp8_delayed_step_fn(layers), use_graph)
+    ms = time_region(fn, steps, warmup)
+    return {
+        "workload": "fp8 linear fwd+bwd, BERT-base shapes, 8192 tokens, delayed scaling (amax "
+                    "history 16, saturating casts, one scale update per step; an extension, "
+                    "not the reference's dynamic semantics)",
+        "value": round(fp8_flops(tokens) / (ms * 1e-3) / 1e12, 2), "unit": "TFLOP/s",
+        "ms_per_step": round(ms, 4), "mode": mode,
+    }
 
 
 def fp8_flops(tokens):
@@ -564,6 +609,10 @@ def main():
     if args.only == "fp8gemm":
         run_fp8gemm_only(fp8_setup(args.tokens, dev))
         return
+    if args.only == "fp8delayed":
+        print(json.dumps(run_fp8_delayed(fp8_setup(args.tokens, dev), args.tokens, args.steps,
+                                         args.warmup, use_graph)))
+        return
 
     log("fp8: setting up inputs")
     layers = fp8_setup(args.tokens, dev)
@@ -597,10 +646,12 @@ def main():
         "roofline": roofline,
     }
     if args.only is None and not args.no_secondary:
+        log("fp8 with delayed scaling")
+        delayed = run_fp8_delayed(layers, args.tokens, args.steps, args.warmup, use_graph)
         del layers, fn
         torch.cuda.empty_cache()
         log("int4lora: per-row and group-64")
-        result["secondary"] = [run_int4lora(args.steps, args.warmup, use_graph),
+        result["secondary"] = [delayed, run_int4lora(args.steps, args.warmup, use_graph),
                                run_int4lora(args.steps, args.warmup, use_graph, group_size=64)]
         log("skinny-M sweep")
         result["secondary"].append(run_skinny())

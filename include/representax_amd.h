@@ -172,6 +172,55 @@ int rpx_fp8_linear_backward_codes(const uint8_t* left_t_codes, const uint8_t* ri
                                   int d_right_transposed, int out_dtype, void* workspace,
                                   size_t workspace_bytes, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * Delayed-scale fp8 state, one entry ("slot") per scaled tensor of a model:
+ *   scales       float [n_slots]                 scale used by the casts
+ *   fmax         float [n_slots]                 448 (e4m3fn) or 57344 (e5m2)
+ *   amax_pending uint32 [n_slots, pending_words] maxima recorded since the
+ *                                                last update (zero-initialized)
+ *   amax_history uint32 [history_len, n_slots]   per-step maxima, ordered f32
+ *                                                bits (zero-initialized)
+ *   cursor       int32 [1]                       history row the next update
+ *                                                writes
+ * The reference's dynamic path (rpx_fp8_linear_*) is unchanged; this is its
+ * roadmap item "persistent delayed scales and one coalesced update"
+ * (todo.org:1149-1154, docs/precision.md:67-71), which it has not built.
+ * ------------------------------------------------------------------------- */
+
+/* Words per slot of amax_pending (a slot's maxima are spread over several
+ * cache lines so that a cast's blocks do not queue on one word). */
+size_t rpx_fp8_delayed_pending_words(void);
+
+/* codes = f8_sat(f32(t) / scales[slot]) for the logical matrix t (as in
+ * rpx_fp8_cast; values beyond the format take its largest finite code, NaN
+ * stays NaN), in one pass that also records max|t| into the slot's pending
+ * maxima (atomic max, so any number of casts may record into one slot). No
+ * reference counterpart: the reference computes every scale from the tensor
+ * being cast (_scaled_quantize, src/representax/precision.py:127-140). */
+int rpx_fp8_cast_delayed(const void* t, int dtype, int64_t rows, int64_t cols, int64_t row_stride,
+                         int64_t col_stride, int fmt, const float* scales,
+                         uint32_t* amax_pending, int64_t n_slots, int64_t slot, uint8_t* out,
+                         uint8_t* out_t, void* stream);
+
+/* Two such casts of one dtype and format in one launch (an fp8 linear's
+ * input and weight). No reference counterpart (see above). */
+int rpx_fp8_cast_delayed2(const void* t0, int64_t rows0, int64_t cols0, int64_t row_stride0,
+                          int64_t col_stride0, int64_t slot0, uint8_t* out0, uint8_t* out_t0,
+                          const void* t1, int64_t rows1, int64_t cols1, int64_t row_stride1,
+                          int64_t col_stride1, int64_t slot1, uint8_t* out1, uint8_t* out_t1,
+                          int dtype, int fmt, const float* scales, uint32_t* amax_pending,
+                          int64_t n_slots, void* stream);
+
+/* The once-per-step update of every slot in one launch: the pending maxima
+ * go to history row cursor[0] (and are cleared); scales[s] =
+ * max(max_h amax_history[h, s] / fmax[s], FLT_MIN) (NaN if a NaN was
+ * recorded) for slots whose history holds a nonzero amax (others keep their
+ * scale); cursor[0] advances by one, modulo history_len. No reference
+ * counterpart (see above). */
+int rpx_fp8_scale_update(float* scales, const float* fmax, uint32_t* amax_pending,
+                         uint32_t* amax_history, int32_t* cursor, int64_t n_slots,
+                         int64_t history_len, void* stream);
+
 /* Test hook: compares the cast kernels' fp8 encoder (hardware convert in
  * range) with the integer encoder for the f32 bit patterns
  * [first, first + count) and their negations; block_counts[b] /

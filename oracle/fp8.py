@@ -105,8 +105,48 @@ def linear_matmul_fp8(left, right, acc=np.float64):
     return bf16_round(out).reshape(*lead, np.asarray(right).shape[-1])
 
 
+# ---------------------------------------------------------------------------
+# Delayed scaling (an extension: the reference's roadmap item, todo.org:
+# 1149-1154 and docs/precision.md:67-71, which the reference has not built).
+# A cast takes the scale its slot holds instead of computing one from the
+# tensor, saturates at the format's largest finite value, and records the
+# tensor's amax; once per step every slot's scale becomes
+# scale_from_amax(max of its recorded amaxes), unless nothing nonzero was
+# recorded. Pins: with a history holding exactly the tensor's own amax the
+# saturating cast equals the reference's dynamic cast (no quotient then
+# exceeds fmax: |t / s| <= amax / (amax / fmax) = fmax up to one rounding,
+# which the encoder rounds back to fmax); saturation and the update rule
+# follow from their closed forms.
+# ---------------------------------------------------------------------------
+def cast_saturating(t, s, fmt: str) -> np.ndarray:
+    """``f8(clamp(f32(t) / s, -fmax, fmax))`` (NaN stays NaN)."""
+
+    fmax = np.float32(FP8_MAX[fmt])
+    with np.errstate(invalid="ignore", divide="ignore", over="ignore"):
+        q = (np.asarray(t, dtype=np.float32) / np.float32(s)).astype(np.float32)
+        q = np.where(np.abs(q) > fmax, np.copysign(fmax, q), q).astype(np.float32)
+    return fp8_encode(q, fmt)
+
+
+def delayed_update(history, scales, formats) -> np.ndarray:
+    """New scales from recorded amaxes ``history [H, S]`` (float32; 0 =
+    nothing recorded): ``scale_from_amax(max_h history[:, s])`` where that
+    maximum is nonzero (NaN if any NaN), else the old scale."""
+
+    h = np.asarray(history, dtype=np.float32)
+    out = np.asarray(scales, dtype=np.float32).copy()
+    for sl, fmt in enumerate(formats):
+        col = h[:, sl]
+        m = np.float32(np.nan) if np.isnan(col).any() else np.float32(col.max())
+        if np.isnan(m) or m != 0:
+            out[sl] = scale_from_amax(m, fmt)
+    return out
+
+
 __all__ = [
     "amax",
+    "cast_saturating",
+    "delayed_update",
     "cast_with_scale",
     "fp8_linear_backward",
     "fp8_linear_forward",

@@ -20,6 +20,7 @@ from .components import Linear
 from .config import PrecisionConfig, QuantizedLoRAConfig
 from .precision import (
     FP32_POLICY,
+    DelayedScaling,
     PrecisionPolicy,
     activation_inputs,
     active_compute_dtype,
@@ -30,6 +31,7 @@ from .precision import (
 )
 
 __all__ = [
+    "DelayedScaling",
     "FP32_POLICY",
     "Linear",
     "PrecisionConfig",

@@ -67,6 +67,16 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "rpx_fp8_linear_backward_codes": (
         _int, [_p, _p, _p, _i64, _i64, _i64, _p, _int, _p, _p, _int, _int, _p, _size, _p]
     ),
+    "rpx_fp8_delayed_pending_words": (_size, []),
+    "rpx_fp8_cast_delayed": (
+        _int, [_p, _int, _i64, _i64, _i64, _i64, _int, _p, _p, _i64, _i64, _p, _p, _p]
+    ),
+    "rpx_fp8_cast_delayed2": (
+        _int,
+        [_p, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p, _p, _int,
+         _int, _p, _p, _i64, _p],
+    ),
+    "rpx_fp8_scale_update": (_int, [_p, _p, _p, _p, _p, _i64, _i64, _p]),
     "rpx_fp8_encode_selfcheck": (
         _int, [_int, ctypes.c_uint64, ctypes.c_uint64, _p, _p, _i64, _p]
     ),

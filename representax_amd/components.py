@@ -54,7 +54,7 @@ class Linear(torch.nn.Module):
     def forward(self, value: torch.Tensor) -> torch.Tensor:
         value = activation_inputs(value)
         weight = compute_parameter(self.weight)
-        output = linear_matmul(value, weight.transpose(-1, -2))
+        output = linear_matmul(value, weight.transpose(-1, -2), fp8_owner=self)
         if self.bias is not None:
             output = output + compute_parameter(self.bias)
         return output

@@ -25,6 +25,10 @@ class PrecisionConfig(FrozenConfig):
     matrix_dtype: MatrixDType | None = Field(default=None)
     accumulation_dtype: Literal["float32"] = Field(default="float32")
     loss_dtype: Literal["float32"] = Field(default="float32")
+    # extension (the reference's roadmap, todo.org:1149-1154): "delayed" casts
+    # fp8 operands with scales from an amax history, updated once per step
+    fp8_scaling: Literal["dynamic", "delayed"] = Field(default="dynamic")
+    amax_history_len: PositiveInt = Field(default=16)
 
     @classmethod
     def bfloat16_mixed(cls) -> "PrecisionConfig":
@@ -33,11 +37,14 @@ class PrecisionConfig(FrozenConfig):
         return cls(compute_dtype="bfloat16", activation_dtype="bfloat16")
 
     @classmethod
-    def float8_mixed(cls) -> "PrecisionConfig":
-        """Experimental fp8 matrices with bf16 everything else (config.py:426-435)."""
+    def float8_mixed(cls, fp8_scaling: Literal["dynamic", "delayed"] = "dynamic",
+                     amax_history_len: int = 16) -> "PrecisionConfig":
+        """Experimental fp8 matrices with bf16 everything else (config.py:426-435);
+        ``fp8_scaling="delayed"`` is the extension above."""
 
         return cls(compute_dtype="bfloat16", activation_dtype="bfloat16",
-                   matrix_dtype="float8_e4m3fn")
+                   matrix_dtype="float8_e4m3fn", fp8_scaling=fp8_scaling,
+                   amax_history_len=amax_history_len)
 
     @property
     def resolved_matrix_dtype(self) -> MatrixDType:

@@ -760,6 +760,71 @@ int rpx_fp8_linear_backward(const void* left, int left_dtype, const void* right,
                                        stream);
 }
 
+size_t rpx_fp8_delayed_pending_words(void) { return static_cast<size_t>(fp8_rec_words()); }
+
+namespace {
+int delayed_args(const char* who, int64_t rows, int64_t cols, int64_t n_slots, int64_t slot,
+                 const void* t, const uint8_t* out, const uint8_t* out_t) {
+  if (rows < 0 || cols < 0) return fail_invalid(std::string(who) + ": negative shape");
+  if (n_slots < 1 || slot < 0 || slot >= n_slots)
+    return fail_invalid(std::string(who) + ": slot outside the scale state");
+  if (rows > 0 && cols > 0 && (t == nullptr || (out == nullptr && out_t == nullptr)))
+    return fail_invalid(std::string(who) + ": null pointer");
+  return kOk;
+}
+}  // namespace
+
+int rpx_fp8_cast_delayed(const void* t, int dtype, int64_t rows, int64_t cols, int64_t row_stride,
+                         int64_t col_stride, int fmt, const float* scales,
+                         uint32_t* amax_pending, int64_t n_slots, int64_t slot, uint8_t* out,
+                         uint8_t* out_t, void* stream) {
+  RPX_TRY(check_dtype(dtype));
+  RPX_TRY(check_fmt(fmt));
+  if (scales == nullptr || amax_pending == nullptr)
+    return fail_invalid("rpx_fp8_cast_delayed: null scale state");
+  RPX_TRY(delayed_args("rpx_fp8_cast_delayed", rows, cols, n_slots, slot, t, out, out_t));
+  const DelayedCast c{t, dtype, rows, cols, row_stride, col_stride, scales + slot,
+                      amax_pending + slot * fp8_rec_words(), out, out_t};
+  RPX_HIP(launch_fp8_cast_delayed(c, nullptr, fmt, static_cast<hipStream_t>(stream)),
+          "rpx_fp8_cast_delayed");
+  return kOk;
+}
+
+int rpx_fp8_cast_delayed2(const void* t0, int64_t rows0, int64_t cols0, int64_t row_stride0,
+                          int64_t col_stride0, int64_t slot0, uint8_t* out0, uint8_t* out_t0,
+                          const void* t1, int64_t rows1, int64_t cols1, int64_t row_stride1,
+                          int64_t col_stride1, int64_t slot1, uint8_t* out1, uint8_t* out_t1,
+                          int dtype, int fmt, const float* scales, uint32_t* amax_pending,
+                          int64_t n_slots, void* stream) {
+  RPX_TRY(check_dtype(dtype));
+  RPX_TRY(check_fmt(fmt));
+  if (scales == nullptr || amax_pending == nullptr)
+    return fail_invalid("rpx_fp8_cast_delayed2: null scale state");
+  RPX_TRY(delayed_args("rpx_fp8_cast_delayed2", rows0, cols0, n_slots, slot0, t0, out0, out_t0));
+  RPX_TRY(delayed_args("rpx_fp8_cast_delayed2", rows1, cols1, n_slots, slot1, t1, out1, out_t1));
+  const DelayedCast c0{t0, dtype, rows0, cols0, row_stride0, col_stride0, scales + slot0,
+                       amax_pending + slot0 * fp8_rec_words(), out0, out_t0};
+  const DelayedCast c1{t1, dtype, rows1, cols1, row_stride1, col_stride1, scales + slot1,
+                       amax_pending + slot1 * fp8_rec_words(), out1, out_t1};
+  RPX_HIP(launch_fp8_cast_delayed(c0, &c1, fmt, static_cast<hipStream_t>(stream)),
+          "rpx_fp8_cast_delayed2");
+  return kOk;
+}
+
+int rpx_fp8_scale_update(float* scales, const float* fmax, uint32_t* amax_pending,
+                         uint32_t* amax_history, int32_t* cursor, int64_t n_slots,
+                         int64_t history_len, void* stream) {
+  if (n_slots < 1 || history_len < 1)
+    return fail_invalid("rpx_fp8_scale_update: need at least one slot and one history row");
+  if (scales == nullptr || fmax == nullptr || amax_pending == nullptr || amax_history == nullptr ||
+      cursor == nullptr)
+    return fail_invalid("rpx_fp8_scale_update: null scale state");
+  RPX_HIP(launch_fp8_scale_update(scales, fmax, amax_pending, amax_history, cursor, n_slots,
+                                  history_len, static_cast<hipStream_t>(stream)),
+          "rpx_fp8_scale_update");
+  return kOk;
+}
+
 int rpx_fp8_encode_selfcheck(int fmt, uint64_t first, uint64_t count, uint32_t* block_counts,
                              uint32_t* block_first, int64_t blocks, void* stream) {
   RPX_TRY(check_fmt(fmt));

@@ -170,6 +170,22 @@ __device__ __forceinline__ uint32_t encode_outside_t(float v) {
   return sign | (a == a ? big : 0x7Fu);
 }
 
+// Saturating code of a value outside [-fmax, fmax]: the largest finite code
+// with the value's sign, NaN for NaN.
+template <int FMT>
+__device__ __forceinline__ uint32_t encode_sat_outside(float v) {
+  const uint32_t sign = (__builtin_bit_cast(uint32_t, v) >> 24) & 0x80u;
+  const uint32_t big = FMT == kE4M3FN ? 0x7Eu : 0x7Bu;
+  return sign | (v == v ? big : 0x7Fu);
+}
+
+// Quotient clamped to [-fmax, fmax] (NaN stays NaN).
+template <int FMT>
+__device__ __forceinline__ float clamp_fmax(float q) {
+  constexpr float fmax = FMT == kE4M3FN ? 448.0f : 57344.0f;
+  return __builtin_fabsf(q) > fmax ? __builtin_copysignf(fmax, q) : q;
+}
+
 // encode2 for a compile-time format, branch-free.
 template <int FMT>
 __device__ __forceinline__ uint32_t encode2_t(float a, float b) {
@@ -289,10 +305,19 @@ __device__ __forceinline__ void transpose4(uint32_t a, uint32_t b, uint32_t c, u
 // or 4). All loads are issued before the scale reduction; the row-major codes
 // go out as 16 CW-byte row segments per 16 lanes, the transposed codes as
 // 8-byte column pieces after an in-register byte transpose.
+// Delayed-scale amax records: each slot has kRecLanes words, one per
+// 128-byte line, so the atomic maxima of a cast's blocks spread over that
+// many lines instead of queueing on one.
+constexpr int kRecLanes = 64;
+constexpr int kRecStride = 32;  // words between lanes
+
 struct CastTile {
   const void* t;
   int64_t rows, cols, ld;
   const float* scale;
+  // amax record (delayed scaling): atomic max of the tile's |t| (ordered f32
+  // bits) into lane (block % kRecLanes) of rec; rec == nullptr: none
+  uint32_t* rec;
   const uint32_t* partials;
   int64_t n_partials;
   float* scale_out;
@@ -361,7 +386,10 @@ __device__ __forceinline__ uint32_t tile_amax(const uint32_t (&raw)[8][TileWords
 
 // Codes of 4 consecutive elements (byte j = element j) with their sign bits
 // taken from the inputs; x4 are the values, w the input dwords they came from.
-template <int DT, int FMT>
+// SAT: values beyond the format's range take the largest finite code of
+// their sign (delayed scaling, whose scale may trail the data) instead of
+// the non-saturating NaN / inf of the reference's dynamic cast.
+template <int DT, int FMT, bool SAT = false>
 __device__ __forceinline__ uint32_t quantize4(const float* x4, const uint32_t* w, float s, float rcp,
                                               bool fast) {
   constexpr float kFmax = FMT == kE4M3FN ? 448.0f : 57344.0f;
@@ -394,21 +422,28 @@ __device__ __forceinline__ uint32_t quantize4(const float* x4, const uint32_t* w
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         if (!(__builtin_fabsf(q[e]) <= kFmax)) {
-          const uint32_t code = encode_outside_t<FMT>(x4[e] / s);
+          // the exact quotient: the Markstein correction turns an infinite
+          // input into NaN (inf - inf)
+          const float qe = x4[e] / s;
+          const uint32_t code = SAT ? encode_sat_outside<FMT>(qe) : encode_outside_t<FMT>(qe);
           c = (c & ~(0xFFu << (8 * e))) | (code << (8 * e));
         }
       }
     }
   } else {
     // scales this extreme (or NaN) are uniform per launch: IEEE divide
-    c = encode2_t<FMT>(x4[0] / s, x4[1] / s) | (encode2_t<FMT>(x4[2] / s, x4[3] / s) << 16);
+    if constexpr (SAT)
+      c = encode2_t<FMT>(clamp_fmax<FMT>(x4[0] / s), clamp_fmax<FMT>(x4[1] / s)) |
+          (encode2_t<FMT>(clamp_fmax<FMT>(x4[2] / s), clamp_fmax<FMT>(x4[3] / s)) << 16);
+    else
+      c = encode2_t<FMT>(x4[0] / s, x4[1] / s) | (encode2_t<FMT>(x4[2] / s, x4[3] / s) << 16);
   }
   // s > 0, so every code carries the sign of its input (signed zeros and
   // NaNs included)
   return (c & 0x7F7F7F7Fu) | (sign & 0x80808080u);
 }
 
-template <int DT, int FMT, int CW>
+template <int DT, int FMT, int CW, bool SAT>
 __device__ __forceinline__ void cast_tile_body(const CastTile& a, int64_t bx, int64_t by,
                                                float* s_sh) {
   constexpr int kW = TileWords<DT, CW>::kWords;
@@ -437,6 +472,13 @@ __device__ __forceinline__ void cast_tile_body(const CastTile& a, int64_t bx, in
   }
   uint32_t raw[8][kW];
   tile_load<DT, CW>(a, bx, by, raw);
+  if (a.rec != nullptr) {
+    __shared__ uint32_t rec_red[4];
+    const uint32_t m = block_reduce_max(tile_amax<DT, CW>(raw), rec_red);
+    if (tid == 0)
+      __hip_atomic_fetch_max(a.rec + (blockIdx.x % kRecLanes) * kRecStride, m, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+  }
   float s;
   if (have_partials) {
     uint32_t m = 0;
@@ -468,7 +510,7 @@ __device__ __forceinline__ void cast_tile_body(const CastTile& a, int64_t bx, in
 #pragma unroll
         for (int e = 0; e < 4; ++e) x4[e] = __builtin_bit_cast(float, w[e]);
       }
-      code[i][h] = quantize4<DT, FMT>(x4, w, s, rcp, fast);
+      code[i][h] = quantize4<DT, FMT, SAT>(x4, w, s, rcp, fast);
     }
   }
   if (!col_ok) return;
@@ -506,15 +548,15 @@ __device__ __forceinline__ void cast_tile_body(const CastTile& a, int64_t bx, in
 
 // Up to two row-major cast problems of one input type and format in one
 // launch: blocks [0, a0.tiles) take the first, the rest the second.
-template <int DT, int FMT, int CW>
+template <int DT, int FMT, int CW, bool SAT = false>
 __global__ void __launch_bounds__(256) k_fp8_cast_tile(CastTile a0, CastTile a1) {
   __shared__ float s_sh;
   int64_t b = blockIdx.x;
   if (b < a0.tiles) {
-    cast_tile_body<DT, FMT, CW>(a0, b % a0.tiles_x, b / a0.tiles_x, &s_sh);
+    cast_tile_body<DT, FMT, CW, SAT>(a0, b % a0.tiles_x, b / a0.tiles_x, &s_sh);
   } else {
     b -= a0.tiles;
-    cast_tile_body<DT, FMT, CW>(a1, b % a1.tiles_x, b / a1.tiles_x, &s_sh);
+    cast_tile_body<DT, FMT, CW, SAT>(a1, b % a1.tiles_x, b / a1.tiles_x, &s_sh);
   }
 }
 
@@ -542,9 +584,10 @@ __global__ void __launch_bounds__(256)
                    int64_t s_row, int64_t s_col, const float* __restrict__ scale,
                    const uint32_t* __restrict__ partials, int64_t n_partials, float fmax,
                    float* __restrict__ scale_out, int fmt, uint8_t* __restrict__ out,
-                   uint8_t* __restrict__ out_t) {
+                   uint8_t* __restrict__ out_t, int sat, uint32_t* __restrict__ rec) {
   __shared__ uint8_t tile[64][64 + 4];
   __shared__ float s_sh;
+  __shared__ uint32_t rec_red[4];
   const int64_t r0 = static_cast<int64_t>(blockIdx.y) * 64;
   const int64_t c0 = static_cast<int64_t>(blockIdx.x) * 64;
   const int tid = threadIdx.x;
@@ -557,12 +600,26 @@ __global__ void __launch_bounds__(256)
     const int64_t c = c0 + cl;
     v[i] = (r < rows && c < cols) ? load_val(t, dtype, r * s_row + c * s_col) : 0.0f;
   }
+  if (rec != nullptr) {
+    uint32_t m = 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) m = umax(m, __builtin_bit_cast(uint32_t, v[i]) & 0x7FFFFFFFu);
+    m = block_reduce_max(m, rec_red);
+    const int lane = static_cast<int>((blockIdx.y * gridDim.x + blockIdx.x) % kRecLanes);
+    if (tid == 0)
+      __hip_atomic_fetch_max(rec + lane * kRecStride, m, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+  }
   const float s = resolve_scale(scale, partials, n_partials, fmax, scale_out, &s_sh,
                                 blockIdx.x == 0 && blockIdx.y == 0);
   const float rcp = 1.0f / s;
+  auto clampq = [&](float q) {
+    return (sat && __builtin_fabsf(q) > fmax) ? __builtin_copysignf(fmax, q) : q;
+  };
 #pragma unroll
   for (int i = 0; i < 16; i += 2) {
-    const uint32_t two = encode2(div_rn(v[i], s, rcp), div_rn(v[i + 1], s, rcp), fmt);
+    const uint32_t two =
+        encode2(clampq(div_rn(v[i], s, rcp)), clampq(div_rn(v[i + 1], s, rcp)), fmt);
     tile[tid / 64 + 4 * i][tid % 64] = static_cast<uint8_t>(two & 0xFFu);
     tile[tid / 64 + 4 * (i + 1)][tid % 64] = static_cast<uint8_t>(two >> 8);
   }
@@ -667,6 +724,7 @@ CastTile to_tile(const CastRequest& r) {
   c.scale_out = r.scale_out;
   c.out = r.out;
   c.out_t = r.out_t;
+  c.rec = nullptr;
   c.tiles_x = ceil_div(r.cols, 16 * cast_cw());
   c.tiles = c.tiles_x * ceil_div(r.rows, 128);
   return c;
@@ -701,12 +759,141 @@ hipError_t launch_one(CastRequest r, int fmt, hipStream_t stream) {
                     static_cast<unsigned>(ceil_div(r.rows, 64)));
     hipLaunchKernelGGL(k_fp8_cast_any, grid, dim3(256), 0, stream, r.t, r.dtype, r.rows, r.cols,
                        r.s_row, r.s_col, r.scale, r.partials, r.n_partials, fp8_max(fmt),
-                       r.scale_out, fmt, r.out, r.out_t);
+                       r.scale_out, fmt, r.out, r.out_t, 0, nullptr);
   }
   return hipGetLastError();
 }
 
+template <int DT, int FMT>
+void launch_tile_delayed(const CastTile& a0, const CastTile& a1, hipStream_t stream) {
+  const unsigned blocks = static_cast<unsigned>(a0.tiles + a1.tiles);
+  if (cast_cw() == 8)
+    hipLaunchKernelGGL((k_fp8_cast_tile<DT, FMT, 8, true>), dim3(blocks), dim3(256), 0, stream, a0,
+                       a1);
+  else
+    hipLaunchKernelGGL((k_fp8_cast_tile<DT, FMT, 4, true>), dim3(blocks), dim3(256), 0, stream, a0,
+                       a1);
+}
+
+// One block for every slot: the slot's pending lanes (maxima recorded since
+// the last update) go to history row cursor[0] and are cleared; scale =
+// max(amax / fmax, FLT_MIN) over the history (NaN amax -> NaN) when it holds
+// a nonzero amax, else unchanged; then the cursor advances (after every slot
+// used it).
+__global__ void __launch_bounds__(256)
+    k_fp8_scale_update(float* __restrict__ scales, const float* __restrict__ fmax,
+                       uint32_t* __restrict__ pending, uint32_t* __restrict__ hist,
+                       int32_t* __restrict__ cursor, int64_t n_slots, int64_t hist_len) {
+  const int32_t row = cursor[0];
+  for (int64_t sl = threadIdx.x; sl < n_slots; sl += blockDim.x) {
+    uint32_t* lanes = pending + sl * (kRecLanes * kRecStride);
+    uint32_t cur = 0;
+    for (int l = 0; l < kRecLanes; ++l) {
+      cur = umax(cur, lanes[l * kRecStride]);
+      lanes[l * kRecStride] = 0u;
+    }
+    hist[static_cast<int64_t>(row) * n_slots + sl] = cur;
+    uint32_t m = 0;
+    for (int64_t h = 0; h < hist_len; ++h) m = umax(m, hist[h * n_slots + sl]);
+    if (m != 0u) {
+      float sc;
+      if (m > 0x7F800000u) {
+        sc = __builtin_bit_cast(float, 0x7FC00000u);
+      } else {
+        sc = __builtin_bit_cast(float, m) / fmax[sl];
+        const float tiny = 1.17549435e-38f;
+        sc = sc > tiny ? sc : tiny;
+      }
+      scales[sl] = sc;
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) cursor[0] = static_cast<int32_t>((row + 1) % hist_len);
+}
+
 }  // namespace
+
+int64_t fp8_rec_words() { return int64_t{kRecLanes} * kRecStride; }
+
+hipError_t launch_fp8_cast_delayed(const DelayedCast& c0, const DelayedCast* c1, int fmt,
+                                   hipStream_t stream) {
+  CastRequest r0{c0.t, c0.dtype, c0.rows, c0.cols, c0.s_row, c0.s_col, c0.scale, nullptr, 0,
+                 nullptr, c0.out, c0.out_t};
+  normalize(r0);
+  const bool e0 = r0.rows == 0 || r0.cols == 0;
+  CastRequest r1{};
+  bool e1 = true;
+  if (c1 != nullptr) {
+    r1 = CastRequest{c1->t, c1->dtype, c1->rows, c1->cols, c1->s_row, c1->s_col, c1->scale,
+                     nullptr, 0, nullptr, c1->out, c1->out_t};
+    normalize(r1);
+    e1 = r1.rows == 0 || r1.cols == 0;
+  }
+  const bool pair = !e0 && !e1 && r0.dtype == r1.dtype && tile_path(r0) && tile_path(r1);
+  const bool single = !e0 && e1 && tile_path(r0);
+  if (pair || single) {
+    CastTile a0 = to_tile(r0);
+    a0.rec = c0.rec;
+    CastTile a1{};
+    if (pair) {
+      a1 = to_tile(r1);
+      a1.rec = c1->rec;
+    }
+    if (r0.dtype == kBF16) {
+      if (fmt == kE4M3FN)
+        launch_tile_delayed<kBF16, kE4M3FN>(a0, a1, stream);
+      else
+        launch_tile_delayed<kBF16, kE5M2>(a0, a1, stream);
+    } else {
+      if (fmt == kE4M3FN)
+        launch_tile_delayed<kF32, kE4M3FN>(a0, a1, stream);
+      else
+        launch_tile_delayed<kF32, kE5M2>(a0, a1, stream);
+    }
+    return hipGetLastError();
+  }
+  // one at a time (other layouts take the generic kernel)
+  const DelayedCast* cs[2] = {&c0, c1};
+  const CastRequest* rs[2] = {&r0, &r1};
+  const bool empty[2] = {e0, e1};
+  for (int i = 0; i < 2; ++i) {
+    if (cs[i] == nullptr || empty[i]) continue;
+    const CastRequest& r = *rs[i];
+    if (tile_path(r)) {
+      CastTile a = to_tile(r);
+      a.rec = cs[i]->rec;
+      CastTile none{};
+      if (r.dtype == kBF16) {
+        if (fmt == kE4M3FN)
+          launch_tile_delayed<kBF16, kE4M3FN>(a, none, stream);
+        else
+          launch_tile_delayed<kBF16, kE5M2>(a, none, stream);
+      } else {
+        if (fmt == kE4M3FN)
+          launch_tile_delayed<kF32, kE4M3FN>(a, none, stream);
+        else
+          launch_tile_delayed<kF32, kE5M2>(a, none, stream);
+      }
+    } else {
+      const dim3 grid(static_cast<unsigned>(ceil_div(r.cols, 64)),
+                      static_cast<unsigned>(ceil_div(r.rows, 64)));
+      hipLaunchKernelGGL(k_fp8_cast_any, grid, dim3(256), 0, stream, r.t, r.dtype, r.rows, r.cols,
+                         r.s_row, r.s_col, r.scale, r.partials, r.n_partials, fp8_max(fmt),
+                         r.scale_out, fmt, r.out, r.out_t, 1, cs[i]->rec);
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+hipError_t launch_fp8_scale_update(float* scales, const float* fmax, uint32_t* pending,
+                                   uint32_t* hist, int32_t* cursor, int64_t n_slots,
+                                   int64_t hist_len, hipStream_t stream) {
+  hipLaunchKernelGGL(k_fp8_scale_update, dim3(1), dim3(256), 0, stream, scales, fmax, pending,
+                     hist, cursor, n_slots, hist_len);
+  return hipGetLastError();
+}
 
 hipError_t launch_fp8_cast(const void* t, int dtype, int64_t rows, int64_t cols, int64_t s_row,
                            int64_t s_col, const float* scale, const uint32_t* partials,

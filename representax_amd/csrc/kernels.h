@@ -149,6 +149,26 @@ hipError_t launch_fp8_gemm(const uint8_t* a, int fmt_a, const float* s_a, const 
                            void* out, int out_dtype, int64_t ldc, float* split_ws,
                            int64_t split_ws_floats, hipStream_t stream);
 int64_t fp8_gemm_workspace_floats(int64_t m, int64_t n, int64_t k);
+// Delayed scaling: saturating casts with given scales that also record each
+// tensor's amax (atomic max of ordered f32 bits) into its slot's pending
+// lanes (fp8_rec_words() words per slot); up to two tensors of one dtype in
+// one launch. The per-step update folds the pending maxima into the history
+// and recomputes every slot's scale.
+struct DelayedCast {
+  const void* t;
+  int dtype;
+  int64_t rows, cols, s_row, s_col;
+  const float* scale;
+  uint32_t* rec;  // the slot's pending lanes
+  uint8_t* out;
+  uint8_t* out_t;
+};
+int64_t fp8_rec_words();
+hipError_t launch_fp8_cast_delayed(const DelayedCast& c0, const DelayedCast* c1, int fmt,
+                                   hipStream_t stream);
+hipError_t launch_fp8_scale_update(float* scales, const float* fmax, uint32_t* pending,
+                                   uint32_t* hist, int32_t* cursor, int64_t n_slots,
+                                   int64_t hist_len, hipStream_t stream);
 hipError_t launch_fp8_encode_selfcheck(int fmt, uint64_t first, uint64_t count, uint32_t* counts,
                                        uint32_t* firsts, int64_t blocks, hipStream_t stream);
 

@@ -375,6 +375,132 @@ def fp8_linear_backward_codes(codes, scales, grad, *, k, dtype, right_transposed
     return d_left, d_right
 
 
+# ---------------------------------------------------------------------------
+# Delayed-scale fp8 (state: precision.DelayedScaling)
+# ---------------------------------------------------------------------------
+def _delayed_outputs(t, rowmajor, transposed):
+    rows, cols = t.shape
+    out = torch.empty((rows, cols), dtype=torch.uint8, device=t.device) if rowmajor else None
+    out_t = torch.empty((cols, rows), dtype=torch.uint8, device=t.device) if transposed else None
+    return out, out_t
+
+
+def fp8_cast_delayed(t: torch.Tensor, state, slot: int, fmt: str = "e4m3fn", *, rowmajor=True,
+                     transposed=False):
+    """Saturating codes of a 2-D tensor under ``state.scales[slot]``, recording
+    ``max|t|`` into the slot's pending maxima: ``(out [R, C] or None, out_t
+    [C, R] or None)``."""
+
+    device = _on_device(t, state.scales)
+    out, out_t = _delayed_outputs(t, rowmajor, transposed)
+    nat.call("rpx_fp8_cast_delayed", _ptr(t), _dtype_code(t.dtype), t.shape[0], t.shape[1],
+             t.stride(0), t.stride(1), _fmt(fmt), _ptr(state.scales), _ptr(state.amax_pending),
+             state.n_slots, int(slot), _ptr(out), _ptr(out_t), _stream(device))
+    return out, out_t
+
+
+def fp8_cast_delayed2(t0: torch.Tensor, slot0: int, t1: torch.Tensor, slot1: int, state,
+                      fmt: str = "e4m3fn", *, rowmajor=True, transposed=False):
+    """Two ``fp8_cast_delayed`` casts of one dtype in one launch:
+    ``((out0, out0_t), (out1, out1_t))``."""
+
+    device = _on_device(t0, t1, state.scales)
+    if t0.dtype != t1.dtype:
+        raise TypeError("fp8_cast_delayed2 casts two tensors of one dtype")
+    o0, o0t = _delayed_outputs(t0, rowmajor, transposed)
+    o1, o1t = _delayed_outputs(t1, rowmajor, transposed)
+    nat.call("rpx_fp8_cast_delayed2", _ptr(t0), t0.shape[0], t0.shape[1], t0.stride(0),
+             t0.stride(1), int(slot0), _ptr(o0), _ptr(o0t), _ptr(t1), t1.shape[0], t1.shape[1],
+             t1.stride(0), t1.stride(1), int(slot1), _ptr(o1), _ptr(o1t), _dtype_code(t0.dtype),
+             _fmt(fmt), _ptr(state.scales), _ptr(state.amax_pending), state.n_slots,
+             _stream(device))
+    return (o0, o0t), (o1, o1t)
+
+
+def fp8_scale_update(state) -> None:
+    """The once-per-step update of every slot's scale: pending maxima go to
+    the history row at the cursor, scales are recomputed from the history and
+    the cursor advances (one launch)."""
+
+    device = _on_device(state.scales)
+    nat.call("rpx_fp8_scale_update", _ptr(state.scales), _ptr(state.fmax),
+             _ptr(state.amax_pending), _ptr(state.amax_history), _ptr(state.cursor),
+             state.n_slots, state.history_len, _stream(device))
+
+
+def fp8_delayed_pending_words() -> int:
+    nat.load()
+    return int(nat.query("rpx_fp8_delayed_pending_words"))
+
+
+def _gemm_into(a, fmt_a, scale_a, b, fmt_b, scale_b, out):
+    """``out = ((a . b^T) * scale_a) * scale_b`` on fp8 codes (the two scales
+    are applied in this order whatever operand they belong to)."""
+
+    m, k = a.shape
+    n = b.shape[0]
+    ws = _workspace(nat.query("rpx_fp8_gemm_workspace", m, n, k), out.device)
+    nat.call("rpx_fp8_gemm", _ptr(a), _fmt(fmt_a), _ptr(scale_a), _ptr(b), _fmt(fmt_b),
+             _ptr(scale_b), m, n, k, _ptr(out), _dtype_code(out.dtype), _ptr(ws), ws.numel(),
+             _stream(out.device))
+    return out
+
+
+class Fp8DelayedLinearFn(torch.autograd.Function):
+    """``left [M, K] @ right [K, N]`` with delayed fp8 scales: e4m3 operands in
+    the forward and an e5m2 gradient in the backward, as in the dynamic
+    ``Fp8LinearFn``, but each operand is cast once with the scale its slot
+    holds (saturating) while its amax is recorded for the next update. The
+    slots are (left, right, grad)."""
+
+    @staticmethod
+    def forward(ctx, left, right, out_dtype, state, slots):
+        _on_device(left, right)
+        left = left.contiguous()
+        right = _dense_2d(right)
+        m, k = left.shape
+        n = right.shape[1]
+        s_l, s_r, s_g = (state.scales[i:i + 1] for i in slots)
+        out = torch.empty((m, n), dtype=out_dtype, device=left.device)
+        if m == 0 or n == 0:
+            return out
+        if k == 0:
+            raise ValueError("fp8 linear needs a non-empty contraction")
+        need = left.requires_grad or right.requires_grad
+        # left -> codes [M, K] (+ [K, M] for d_right); right [K, N] -> codes
+        # [N, K] for this product (+ [K, N] for d_left); one launch
+        (ql, qlt), (qrt, qr) = fp8_cast_delayed2(left, slots[0], right.t(), slots[1], state,
+                                                 "e4m3fn", rowmajor=True, transposed=need)
+        _gemm_into(ql, "e4m3fn", s_l, qrt, "e4m3fn", s_r, out)
+        if need:
+            ctx.save_for_backward(qlt, qr, s_l, s_r, s_g)
+            ctx.state = state
+            ctx.g_slot = slots[2]
+            ctx.dtype = left.dtype
+            ctx.right_t = not right.is_contiguous()
+        return out
+
+    @staticmethod
+    def backward(ctx, grad):
+        qlt, qr, s_l, s_r, s_g = ctx.saved_tensors
+        grad = grad.contiguous()
+        m, n = grad.shape
+        k = qlt.shape[0]
+        need_l, need_r = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        qg, qgt = fp8_cast_delayed(grad, ctx.state, ctx.g_slot, "e5m2", rowmajor=need_l,
+                                   transposed=need_r)
+        d_left = d_right = None
+        if need_l:
+            d_left = _gemm_into(qg, "e5m2", s_g, qr, "e4m3fn", s_r,
+                                torch.empty((m, k), dtype=ctx.dtype, device=grad.device))
+        if need_r:
+            # ((acc * s_left) * s_grad): the reference's order for this product
+            d_rt = _gemm_into(qgt, "e5m2", s_l, qlt, "e4m3fn", s_g,
+                              torch.empty((n, k), dtype=ctx.dtype, device=grad.device))
+            d_right = d_rt.t() if ctx.right_t else d_rt.t().contiguous()
+        return d_left, d_right, None, None, None
+
+
 class Fp8LinearFn(torch.autograd.Function):
     """``_fp8_linear_dot`` (precision.py:173-221): e4m3 forward, e5m2 backward.
 

@@ -20,10 +20,90 @@ import torch
 from . import ops
 
 
+class DelayedScaling:
+    """Persistent fp8 scale state with one coalesced update per step.
+
+    The reference's roadmap item (todo.org:1149-1154, docs/precision.md:67-71;
+    not built there): instead of a max|t| pass over every operand before its
+    cast, each scaled tensor ("slot") is cast with the scale its slot holds
+    and records its amax in the same pass; ``update()`` then recomputes every
+    slot's scale from the last ``history_len`` recorded amaxes in one launch,
+    ``max(amax / fmax, FLT_MIN)`` as in the dynamic rule. Casts saturate at
+    the format's largest finite value, since the data may outgrow a scale
+    set from past steps. Scales start at 1.0 and a slot whose history holds
+    no nonzero amax keeps its scale. Call ``update()`` once per step, after
+    the backward pass (the backward reuses the forward's scales).
+
+    Device buffers (one set per model): ``scales`` / ``fmax`` float32
+    [n_slots]; ``amax_pending`` uint32 [n_slots, pending words] (maxima
+    recorded since the last update, spread over several cache lines per
+    slot); ``amax_history`` uint32 [history_len, n_slots] (per-step maxima as
+    ordered f32 bits); ``cursor`` int32 [1] (the history row the next update
+    writes; it lives on the device so captured graphs advance it).
+    """
+
+    FMAX = {"e4m3fn": 448.0, "e5m2": 57344.0}
+
+    def __init__(self, n_slots: int, history_len: int = 16,
+                 device: torch.device | str = "cuda") -> None:
+        if n_slots < 1 or history_len < 1:
+            raise ValueError("delayed scaling needs at least one slot and one history row")
+        self.n_slots = int(n_slots)
+        self.history_len = int(history_len)
+        self.scales = torch.ones(self.n_slots, dtype=torch.float32, device=device)
+        self.fmax = torch.full((self.n_slots,), self.FMAX["e4m3fn"], dtype=torch.float32,
+                               device=device)
+        self.amax_history = torch.zeros((self.history_len, self.n_slots), dtype=torch.uint32,
+                                        device=device)
+        words = ops.fp8_delayed_pending_words() if torch.device(device).type == "cuda" else 2048
+        self.amax_pending = torch.zeros((self.n_slots, words), dtype=torch.uint32, device=device)
+        self.cursor = torch.zeros(1, dtype=torch.int32, device=device)
+        self._next = 0
+        self._owners: dict[int, tuple[int, ...]] = {}
+
+    def allocate(self, formats: tuple[str, ...]) -> tuple[int, ...]:
+        """Fresh slots, one per entry of ``formats`` ("e4m3fn" / "e5m2")."""
+
+        if self._next + len(formats) > self.n_slots:
+            raise ValueError(f"delayed scaling state has {self.n_slots} slots; "
+                             f"{self._next + len(formats)} needed")
+        slots = tuple(range(self._next, self._next + len(formats)))
+        for sl, fmt in zip(slots, formats):
+            self.fmax[sl] = self.FMAX[fmt]
+        self._next += len(formats)
+        return slots
+
+    def slots_for(self, owner: object, formats: tuple[str, ...]) -> tuple[int, ...]:
+        """The slots of ``owner`` (allocated on its first use)."""
+
+        key = id(owner)
+        if key not in self._owners:
+            self._owners[key] = self.allocate(formats)
+        return self._owners[key]
+
+    def update(self) -> None:
+        ops.fp8_scale_update(self)
+
+    @classmethod
+    def for_model(cls, model: torch.nn.Module, history_len: int = 16,
+                  device: torch.device | str = "cuda") -> "DelayedScaling":
+        """State sized for every ``Linear`` of ``model`` (left, right and
+        gradient slots each)."""
+
+        from .components import Linear
+
+        n = sum(1 for m in model.modules() if isinstance(m, Linear))
+        return cls(max(3 * n, 1), history_len, device)
+
+
+LINEAR_FORMATS = ("e4m3fn", "e4m3fn", "e5m2")  # left, right, gradient
+
+
 @dataclass(frozen=True, slots=True)
 class PrecisionPolicy:
     """Resolved dtypes for stored state, forward compute, and objectives
-    (precision.py:19-34)."""
+    (precision.py:19-34). ``fp8_state`` (an extension) selects delayed fp8
+    scaling when set; None keeps the reference's dynamic scaling."""
 
     parameter_dtype: torch.dtype
     compute_dtype: torch.dtype
@@ -31,6 +111,7 @@ class PrecisionPolicy:
     matrix_dtype: torch.dtype
     accumulation_dtype: torch.dtype
     loss_dtype: torch.dtype
+    fp8_state: DelayedScaling | None = None
 
     @property
     def communication_dtype(self) -> torch.dtype:
@@ -56,9 +137,15 @@ _ACTIVE_PRECISION: ContextVar[PrecisionPolicy | None] = ContextVar(
 )
 
 
-def resolve_precision_policy(config: Any) -> PrecisionPolicy:
-    """Resolve a ``PrecisionConfig`` into torch dtypes (precision.py:57-67)."""
+def resolve_precision_policy(config: Any, *, fp8_state: DelayedScaling | None = None
+                             ) -> PrecisionPolicy:
+    """Resolve a ``PrecisionConfig`` into torch dtypes (precision.py:57-67).
+    A config with ``fp8_scaling="delayed"`` needs the model's
+    ``DelayedScaling`` state."""
 
+    delayed = getattr(config, "fp8_scaling", "dynamic") == "delayed"
+    if delayed and config.resolved_matrix_dtype == "float8_e4m3fn" and fp8_state is None:
+        raise ValueError("fp8_scaling='delayed' needs a DelayedScaling state (fp8_state=...)")
     return PrecisionPolicy(
         parameter_dtype=_DTYPES[config.parameter_dtype],
         compute_dtype=_DTYPES[config.compute_dtype],
@@ -66,6 +153,7 @@ def resolve_precision_policy(config: Any) -> PrecisionPolicy:
         matrix_dtype=_DTYPES[config.resolved_matrix_dtype],
         accumulation_dtype=_DTYPES[config.accumulation_dtype],
         loss_dtype=_DTYPES[config.loss_dtype],
+        fp8_state=fp8_state if delayed else None,
     )
 
 
@@ -153,9 +241,12 @@ def active_compute_dtype(fallback: torch.dtype) -> torch.dtype:
     return fallback if policy is None else policy.compute_dtype
 
 
-def linear_matmul(left: torch.Tensor, right: torch.Tensor, *, out_sharding: Any = None) -> torch.Tensor:
+def linear_matmul(left: torch.Tensor, right: torch.Tensor, *, out_sharding: Any = None,
+                  fp8_owner: object = None) -> torch.Tensor:
     """Apply the active matrix policy to ``left [..., K] @ right [K, N]``
-    (precision.py:224-239)."""
+    (precision.py:224-239). Under delayed fp8 scaling ``fp8_owner`` (the
+    calling module) names the product's scale slots; without it the product
+    is scaled dynamically, as in the reference."""
 
     del out_sharding  # single-device: sharding annotations are the identity
     policy = _ACTIVE_PRECISION.get()
@@ -163,7 +254,12 @@ def linear_matmul(left: torch.Tensor, right: torch.Tensor, *, out_sharding: Any 
         return torch.matmul(left, right)
     leading = left.shape[:-1]
     flat = left.reshape(-1, left.shape[-1])
-    out = ops.Fp8LinearFn.apply(flat, right, policy.activation_dtype)
+    if policy.fp8_state is not None and fp8_owner is not None:
+        slots = policy.fp8_state.slots_for(fp8_owner, LINEAR_FORMATS)
+        out = ops.Fp8DelayedLinearFn.apply(flat, right, policy.activation_dtype,
+                                           policy.fp8_state, slots)
+    else:
+        out = ops.Fp8LinearFn.apply(flat, right, policy.activation_dtype)
     return out.reshape(*leading, right.shape[-1]).to(policy.activation_dtype)
 
 
@@ -198,6 +294,7 @@ def accumulated_values(tree: Any) -> Any:
 
 
 __all__ = [
+    "DelayedScaling",
     "FP32_POLICY",
     "PrecisionPolicy",
     "accumulated_values",

@@ -131,3 +131,33 @@ def test_fp8_policy_on_cpu_fails_loudly():
         with pytest.raises(RuntimeError, match="ROCm"):
             rx.linear_matmul(torch.randn(4, 8, dtype=torch.bfloat16),
                              torch.randn(8, 2, dtype=torch.bfloat16))
+
+
+def test_delayed_scaling_state_and_policy_on_cpu():
+    """Slot bookkeeping of the delayed-scale state and the policy's checks
+    (the buffers are plain tensors; no kernel runs here)."""
+
+    import torch
+
+    from representax_amd import DelayedScaling, Linear, PrecisionConfig
+    from representax_amd.precision import LINEAR_FORMATS, resolve_precision_policy
+
+    st = DelayedScaling(6, history_len=3, device="cpu")
+    assert st.scales.tolist() == [1.0] * 6 and st.amax_history.shape == (3, 6)
+    a = st.slots_for("layer0", LINEAR_FORMATS)
+    b = st.slots_for("layer1", LINEAR_FORMATS)
+    assert a == (0, 1, 2) and b == (3, 4, 5) and st.slots_for("layer0", LINEAR_FORMATS) == a
+    assert st.fmax.tolist() == [448.0, 448.0, 57344.0] * 2
+    with pytest.raises(ValueError, match="slots"):
+        st.allocate(("e4m3fn",))
+    with pytest.raises(ValueError):
+        DelayedScaling(0, device="cpu")
+    model = torch.nn.Sequential(Linear(torch.zeros(4, 8)), Linear(torch.zeros(8, 4)))
+    assert DelayedScaling.for_model(model, device="cpu").n_slots == 6
+    cfg = PrecisionConfig.float8_mixed(fp8_scaling="delayed", amax_history_len=8)
+    assert cfg.fp8_scaling == "delayed" and cfg.amax_history_len == 8
+    with pytest.raises(ValueError, match="DelayedScaling"):
+        resolve_precision_policy(cfg)
+    assert resolve_precision_policy(cfg, fp8_state=st).fp8_state is st
+    # the dynamic (reference) policy ignores a state
+    assert resolve_precision_policy(PrecisionConfig.float8_mixed(), fp8_state=st).fp8_state is None

@@ -56,6 +56,18 @@ def test_invalid_arguments_are_rejected_before_any_launch():
         nat.call("rpx_int4_pack", p, 7, 4, 8, 0, p, p, None)
     with pytest.raises(ValueError, match="format"):
         nat.call("rpx_fp8_cast", p, nat.DTYPE_BF16, 4, 4, 4, 1, p, 9, p, None, None)
+    with pytest.raises(ValueError, match="slot"):
+        nat.call("rpx_fp8_cast_delayed", p, nat.DTYPE_BF16, 4, 4, 4, 1, nat.FP8_E4M3FN, p, p, 3, 3,
+                 p, None, None)
+    with pytest.raises(ValueError, match="null scale state"):
+        nat.call("rpx_fp8_cast_delayed", p, nat.DTYPE_BF16, 4, 4, 4, 1, nat.FP8_E4M3FN, None, p,
+                 3, 0, p, None, None)
+    with pytest.raises(ValueError, match="slot"):
+        nat.call("rpx_fp8_cast_delayed2", p, 4, 4, 4, 1, 0, p, None, p, 4, 4, 4, 1, 5, p, None,
+                 nat.DTYPE_BF16, nat.FP8_E4M3FN, p, p, 3, None)
+    with pytest.raises(ValueError, match="history row"):
+        nat.call("rpx_fp8_scale_update", p, p, p, p, p, 3, 0, None)
+    assert nat.query("rpx_fp8_delayed_pending_words") >= 64
 
 
 def _host_quantize(x: np.ndarray, scale: float, fmt: int) -> np.ndarray:

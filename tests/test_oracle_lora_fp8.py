@@ -179,3 +179,47 @@ def test_linear_matmul_flattens_leading_dims():
     flat = ofp8.linear_matmul_fp8(x.reshape(6, 16), right)
     assert out.shape == (2, 3, 5) and np.array_equal(out.reshape(6, 5), flat)
     assert np.array_equal(bf16_round(out), out)
+
+
+# ---------------------------------------------------------------------------
+# Delayed scaling (extension; the reference's roadmap, todo.org:1149-1154)
+# ---------------------------------------------------------------------------
+def _outliers(rng, shape):
+    x = rng.standard_normal(shape).astype(np.float32)
+    return np.where(rng.random(shape) < 1e-2, x * 50.0, x).astype(np.float32)
+
+
+def test_saturating_cast_with_own_scale_is_the_dynamic_cast():
+    rng = np.random.default_rng(11)
+    for fmt in (E4M3FN, E5M2):
+        for trial in range(4):
+            t = bf16_round(_outliers(rng, (64, 96)) * (10.0 ** (trial - 2)))
+            codes, s = ofp8.scaled_quantize(t, fmt)
+            assert np.array_equal(ofp8.cast_saturating(t, s, fmt), codes)
+
+
+def test_saturating_cast_closed_forms():
+    for fmt, big in ((E4M3FN, 0x7E), (E5M2, 0x7B)):
+        t = np.array([1e9, -1e9, np.inf, -np.inf, np.nan, 0.0, -0.0, 1.0], np.float32)
+        c = ofp8.cast_saturating(t, np.float32(1.0), fmt)
+        assert c[0] == big and c[1] == (0x80 | big)
+        assert c[2] == big and c[3] == (0x80 | big)
+        assert (c[4] & 0x7F) == 0x7F if fmt == E4M3FN else (c[4] & 0x7C) == 0x7C and (c[4] & 3) != 0
+        assert c[5] == 0x00 and c[6] == 0x80
+        # 1.0: exponent bias 7 (e4m3fn) / 15 (e5m2), zero mantissa
+        assert c[7] == (0x38 if fmt == E4M3FN else 0x3C)
+
+
+def test_delayed_update_closed_forms():
+    hist = np.array([[0.0, 3.0, 0.0, 448.0],
+                     [0.0, 5.0, np.nan, 1.0],
+                     [0.0, 1.0, 2.0, 0.0]], np.float32)
+    old = np.array([0.5, 0.25, 0.125, 2.0], np.float32)
+    fmts = [E4M3FN, E4M3FN, E5M2, E4M3FN]
+    new = ofp8.delayed_update(hist, old, fmts)
+    assert new[0] == np.float32(0.5)                       # nothing recorded: kept
+    assert new[1] == np.float32(np.float32(5.0) / np.float32(448.0))
+    assert np.isnan(new[2])                                # a NaN was recorded
+    assert new[3] == np.float32(1.0)                       # 448 / 448
+    tiny = ofp8.delayed_update(np.array([[1e-45]], np.float32), np.ones(1, np.float32), [E4M3FN])
+    assert tiny[0] == np.float32(FLT_MIN)
