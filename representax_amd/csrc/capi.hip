@@ -295,6 +295,14 @@ int rpx_int4lora_forward(const void* x, int dtype, int64_t m, int64_t k, const u
       aligned16(lora_a)) {
     float* ws = arena.take<float>(skinny_workspace_floats(m, n, k, rank));
     if (arena.overflow) return fail_invalid("rpx_int4lora_forward: workspace too small");
+    if (skinny2_selected(m, n, k, rank, ng, g)) {
+      RPX_HIP(launch_skinny2_forward(static_cast<const uint16_t*>(x), m, k, w, n,
+                                     static_cast<const uint16_t*>(lora_a),
+                                     static_cast<const uint16_t*>(lora_b), rank, c, bias_bits,
+                                     static_cast<uint16_t*>(y), static_cast<uint16_t*>(h), ws, st),
+              "int4lora_forward: skinny-M row-block kernels");
+      return kOk;
+    }
     RPX_HIP(launch_skinny_forward(static_cast<const uint16_t*>(x), m, k, w, n,
                                   static_cast<const uint16_t*>(lora_a),
                                   static_cast<const uint16_t*>(lora_b), rank, c, bias_bits,

@@ -63,6 +63,17 @@ hipError_t launch_skinny_forward(const uint16_t* x, int64_t m, int64_t k, const 
                                  int64_t n, const uint16_t* lora_a, const uint16_t* lora_b,
                                  int64_t rank, float scale, const uint16_t* bias, uint16_t* y,
                                  uint16_t* h, float* ws, hipStream_t stream);
+// M <= 16 (selected for M <= 4): two launches (weight rows over the whole K
+// per block with the adapter's fp32 K-slice partials in the same grid, then
+// the LoRA finish), no cross-block exchange.
+bool skinny2_ok(int64_t m, int64_t n, int64_t k, int64_t rank, int64_t n_groups, int64_t group);
+bool skinny2_selected(int64_t m, int64_t n, int64_t k, int64_t rank, int64_t n_groups,
+                      int64_t group);
+hipError_t launch_skinny2_forward(const uint16_t* x, int64_t m, int64_t k, const Int4Operand& w,
+                                  int64_t n, const uint16_t* lora_a, const uint16_t* lora_b,
+                                  int64_t rank, float scale, const uint16_t* bias, uint16_t* y,
+                                  uint16_t* h, float* ws, hipStream_t stream);
+int64_t skinny2_workspace_floats(int64_t m, int64_t n, int64_t k, int64_t rank);
 
 // Rank-r kernels --------------------------------------------------------------
 // out[M, r] = bf16(sum_k op(A[m, k]) * R[j, k]); op(a) = bf16(a * a_scale) when

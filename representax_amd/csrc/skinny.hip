@@ -584,9 +584,10 @@ bool skinny_ok(int64_t m, int64_t n, int64_t k, int64_t rank, int64_t n_groups, 
 }
 
 int64_t skinny_workspace_floats(int64_t m, int64_t n, int64_t k, int64_t rank) {
-  (void)rank;
   const SkinnyPlan p = plan_skinny(m, n, k);
-  return p.splits * p.tiles * frags_per_tile(p) * 256 + p.a_splits * 4 * p.mb * 256;
+  const int64_t one = p.splits * p.tiles * frags_per_tile(p) * 256 + p.a_splits * 4 * p.mb * 256;
+  const int64_t two = skinny2_ok(m, n, k, rank, 1, 0) ? skinny2_workspace_floats(m, n, k, rank) : 0;
+  return one > two ? one : two;
 }
 
 hipError_t launch_skinny_forward(const uint16_t* x, int64_t m, int64_t k, const Int4Operand& w,

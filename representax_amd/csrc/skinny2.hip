@@ -1,0 +1,395 @@
+// Skinny-M INT4 + LoRA forward for M <= 16 tokens (selected for M <= 4) in
+// two launches with no cross-block exchange inside either (the memory-bound
+// embedding-inference regime, where a call is a few dependent device round
+// trips).
+//
+//   k_skinny_main, one grid with two block roles:
+//     adapter blocks (first in the grid, so they dispatch first): block
+//       (s, q) writes the fp32 partial P[s][m][16 q + i] = sum over its
+//       128 NW columns of x[m, k] A[16 q + i, k]; its waves take one 128-column
+//       chunk each and reduce through LDS in wave order;
+//     weight blocks: block b owns output rows [16 b, 16 b + 16) over the
+//       whole K. Every wave issues all of its 16-byte packed-weight, scale
+//       and x loads first, dequantizes exactly (bf16(q * s)) and runs
+//       v_mfma_f32_16x16x32_bf16 with the weight rows as the row operand and
+//       x as the column operand; the waves reduce through LDS in wave order
+//       and wave 0 stores base = bf16(acc) into y. Wave 0 also touches the
+//       block's rows of B and bias so that they are cache-resident for the
+//       second launch.
+//   k_skinny_finish: every block sums the partials in slice order into
+//     h = bf16(sum_s P[s]) (block 0 also stores h), then for its rows
+//     t = bf16(sum_j h[m, j] B[n, j]) (sequential fma over j) and
+//     y = bf16(base + bf16(t * c)) (+ bias, rounded again).
+// The adapter's cold loads overlap the weight stream instead of preceding
+// it, and the second launch reads only cache-resident data.
+//
+// Within a 128-column chunk lane l takes k = 32 (l >> 4) + [0, 32): one
+// 16-byte load of 32 nibbles, and MFMA step s uses k = 32 (l >> 4) + 8 s +
+// [0, 8), the same permutation on both operands. The lane then holds
+// D[row 4 (l >> 4) + v][column m = l & 15].
+#include <cstdlib>
+
+#include "common.h"
+#include "kernels.h"
+
+namespace rpx {
+
+namespace {
+
+typedef __bf16 bf16x8_v __attribute__((ext_vector_type(8)));
+typedef float f32x4_v __attribute__((ext_vector_type(4)));
+
+constexpr int kFinRows = 64;       // output rows per finishing block
+constexpr int kFinThreads = 256;
+
+struct Skinny2Params {
+  const uint16_t* x;  // [M, K] bf16
+  int m;
+  int64_t k;
+  int64_t n;
+  const uint8_t* packed;
+  int64_t pcols;
+  const uint16_t* scales;
+  int64_t n_groups;
+  int group_shift;
+  const uint16_t* lora_a;  // [rank, K]
+  const uint16_t* lora_b;  // [N, rank]
+  int rank;
+  float scale;
+  const uint16_t* bias;  // [N] or null
+  uint16_t* y;           // [M, N]
+  uint16_t* h;           // [M, rank]
+  float* part;           // [slices][M][rank]
+  int slices;            // adapter K slices of 128 * NW columns
+  int a_blocks;          // slices * ceil(rank / 16)
+  int b_vec;             // B rows may be touched with 16-byte loads
+};
+
+__device__ __forceinline__ u32x4_t ld16(const void* p) {
+  return *reinterpret_cast<const u32x4_t*>(p);
+}
+
+__device__ __forceinline__ bf16x8_v as_frag(u32x4_t v) { return __builtin_bit_cast(bf16x8_v, v); }
+
+__device__ __forceinline__ f32x4_v mfma16(u32x4_t a, u32x4_t b, f32x4_v c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_frag(a), as_frag(b), c, 0, 0, 0);
+}
+
+// 8 bf16 of x row m from column k (zeros for rows past M or chunks past K)
+__device__ __forceinline__ u32x4_t x_frag(const Skinny2Params& p, int m, int64_t k, bool ok) {
+  const u32x4_t z{0u, 0u, 0u, 0u};
+  if (!ok || m >= p.m) return z;
+  return ld16(p.x + static_cast<int64_t>(m) * p.k + k);
+}
+
+// 8 nibbles (k ascending, low nibble first) -> 8 bf16: bf16(q * s), exact
+// in f32 as fma(u, s, -8 s) with u = nibble ^ 8.
+__device__ __forceinline__ u32x4_t dequant8(uint32_t word, float s) {
+  const float m8s = -8.0f * s;
+  const uint32_t xw = word ^ 0x88888888u;
+  const uint32_t lo = xw & 0x0F0F0F0Fu;
+  const uint32_t hi = (xw >> 4) & 0x0F0F0F0Fu;
+  uint32_t o[4];
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    const float fl = static_cast<float>((lo >> (8 * b)) & 0xFFu);
+    const float fh = static_cast<float>((hi >> (8 * b)) & 0xFFu);
+    o[b] = pack_bf16x2(__builtin_fmaf(fl, s, m8s), __builtin_fmaf(fh, s, m8s));
+  }
+  return u32x4_t{o[0], o[1], o[2], o[3]};
+}
+
+// Sum of the NW waves' accumulators in wave order; the total is valid in
+// wave 0.
+template <int NW>
+__device__ __forceinline__ f32x4_v reduce_waves(f32x4_v acc, f32x4_v* red) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  if (wave > 0) red[(wave - 1) * 64 + lane] = acc;
+  __syncthreads();
+  if (wave == 0) {
+#pragma unroll
+    for (int w = 1; w < NW; ++w) acc += red[(w - 1) * 64 + lane];
+  }
+  return acc;
+}
+
+template <int NW>
+__device__ __forceinline__ void adapter_block(const Skinny2Params& p, int a, f32x4_v* red) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int rl = lane & 15;
+  const int g = lane >> 4;
+  const int groups = (p.rank + 15) / 16;
+  const int q = a % groups;
+  const int s = a / groups;
+  const int j = 16 * q + rl;
+  const bool jok = j < p.rank;
+  const uint16_t* arow = p.lora_a + static_cast<int64_t>(jok ? j : p.rank - 1) * p.k;
+  const int64_t c = static_cast<int64_t>(s) * NW + wave;
+  const bool ok = c < p.k / 128;
+  const int64_t k0 = ok ? c * 128 + 32 * g : 0;
+  u32x4_t av[4], xv[4];
+#pragma unroll
+  for (int st = 0; st < 4; ++st) {
+    av[st] = ok && jok ? ld16(arow + k0 + 8 * st) : u32x4_t{0u, 0u, 0u, 0u};
+    xv[st] = x_frag(p, rl, k0 + 8 * st, ok);
+  }
+  f32x4_v acc{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int st = 0; st < 4; ++st) acc = mfma16(av[st], xv[st], acc);
+  acc = reduce_waves<NW>(acc, red);
+  if (wave != 0 || rl >= p.m) return;
+  // lane: P[s][m = rl][j = 16 q + 4 g + v]
+  float* dst = p.part + (static_cast<int64_t>(s) * p.m + rl) * p.rank;
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int jj = 16 * q + 4 * g + v;
+    if (jj < p.rank) dst[jj] = acc[v];
+  }
+}
+
+template <int NW, int CPW>
+__device__ __forceinline__ void weight_block(const Skinny2Params& p, int64_t b, f32x4_v* red) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int rl = lane & 15;
+  const int g = lane >> 4;
+  const int64_t n0 = 16 * b;
+  const int64_t row = n0 + rl;
+  const int64_t rc = row < p.n ? row : p.n - 1;
+  const uint8_t* wrow = p.packed + rc * p.pcols;
+  const uint16_t* srow = p.scales + rc * p.n_groups;
+  const int64_t nchunks = p.k / 128;
+  // every load of the wave first
+  u32x4_t wv[CPW], xv[CPW][4];
+  uint16_t sv[CPW];
+#pragma unroll
+  for (int i = 0; i < CPW; ++i) {
+    const int64_t c = wave + static_cast<int64_t>(i) * NW;
+    const bool ok = c < nchunks;
+    const int64_t k0 = ok ? c * 128 + 32 * g : 0;
+    wv[i] = ok ? ld16(wrow + k0 / 2) : u32x4_t{0u, 0u, 0u, 0u};
+    sv[i] = srow[p.n_groups == 1 ? 0 : (k0 >> p.group_shift)];
+#pragma unroll
+    for (int st = 0; st < 4; ++st) xv[i][st] = x_frag(p, rl, k0 + 8 * st, ok);
+  }
+  // the block's B rows (16 rank contiguous bf16) and bias, touched for the
+  // finishing launch
+  uint32_t touch = 0;
+  if (wave == 0) {
+    const int64_t rows = (p.n - n0 < 16 ? p.n - n0 : 16);
+    if (p.b_vec && 8 * lane < rows * p.rank) touch = ld16(p.lora_b + n0 * p.rank + 8 * lane).x;
+    if (p.bias != nullptr && lane < rows) touch ^= p.bias[n0 + lane];
+  }
+  f32x4_v acc{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < CPW; ++i) {
+    const float s = bf16_to_f32(sv[i]);
+#pragma unroll
+    for (int st = 0; st < 4; ++st) acc = mfma16(dequant8(wv[i][st], s), xv[i][st], acc);
+  }
+  acc = reduce_waves<NW>(acc, red);
+  if (wave != 0) return;
+  asm volatile("" ::"v"(touch));
+  if (rl >= p.m) return;
+  // lane: base[m = rl][n = n0 + 4 g + v]
+  const int64_t nb = n0 + 4 * g;
+  uint16_t* dst = p.y + static_cast<int64_t>(rl) * p.n + nb;
+  if (nb + 3 < p.n && (reinterpret_cast<uintptr_t>(dst) & 7) == 0) {
+    *reinterpret_cast<u32x2_t*>(dst) =
+        u32x2_t{pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3])};
+  } else {
+    for (int v = 0; v < 4 && nb + v < p.n; ++v) dst[v] = f32_to_bf16(acc[v]);
+  }
+}
+
+template <int NW, int CPW>
+__global__ void __launch_bounds__(64 * NW) k_skinny_main(Skinny2Params p) {
+  __shared__ f32x4_v red[(NW > 1 ? NW - 1 : 1) * 64];
+  const int b = static_cast<int>(blockIdx.x);
+  if (b < p.a_blocks) {
+    adapter_block<NW>(p, b, red);
+  } else {
+    weight_block<NW, CPW>(p, b - p.a_blocks, red);
+  }
+}
+
+// Thread (row n = n0 + (tid & 63), token group tid >> 6) keeps B[n, :] in
+// registers (RV 16-byte vectors) and produces y[m, n] for m = tid >> 6,
+// (tid >> 6) + 4, ...; h comes from the partials through LDS.
+template <int RV>
+__global__ void __launch_bounds__(kFinThreads) k_skinny_finish(Skinny2Params p) {
+  __shared__ float hs[16 * 64];
+  const int tid = threadIdx.x;
+  const int mr = p.m * p.rank;
+  const int64_t n = static_cast<int64_t>(blockIdx.x) * kFinRows + (tid & 63);
+  const bool nok = n < p.n;
+  const int64_t nc = nok ? n : p.n - 1;
+  uint32_t bw[4 * RV];
+  const uint16_t* brow = p.lora_b + nc * p.rank;
+  if (p.b_vec) {
+#pragma unroll
+    for (int v = 0; v < RV; ++v) {
+      const u32x4_t q = ld16(brow + 8 * v);
+      bw[4 * v] = q.x;
+      bw[4 * v + 1] = q.y;
+      bw[4 * v + 2] = q.z;
+      bw[4 * v + 3] = q.w;
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4 * RV; ++e) {
+      const uint32_t lo = 2 * e < p.rank ? brow[2 * e] : 0u;
+      const uint32_t hi = 2 * e + 1 < p.rank ? brow[2 * e + 1] : 0u;
+      bw[e] = lo | (hi << 16);
+    }
+  }
+  const float bias = p.bias != nullptr && nok ? bf16_to_f32(p.bias[n]) : 0.0f;
+  // the thread's base values, loaded with B before the partials are summed
+  constexpr int kPerThread = 16 / (kFinThreads / 64);
+  uint16_t base[kPerThread];
+#pragma unroll
+  for (int i = 0; i < kPerThread; ++i) {
+    const int m = (tid >> 6) + (kFinThreads / 64) * i;
+    base[i] = m < p.m ? p.y[static_cast<int64_t>(m) * p.n + nc] : uint16_t{0};
+  }
+  for (int e = tid; e < mr; e += kFinThreads) {
+    float sum = 0.0f;
+#pragma unroll 8
+    for (int s = 0; s < p.slices; ++s) sum += p.part[static_cast<int64_t>(s) * mr + e];
+    const float hv = round_bf16(sum);
+    hs[e] = hv;
+    if (blockIdx.x == 0) p.h[e] = f32_to_bf16(hv);
+  }
+  __syncthreads();
+  if (!nok) return;
+#pragma unroll
+  for (int i = 0; i < kPerThread; ++i) {
+    const int m = (tid >> 6) + (kFinThreads / 64) * i;
+    if (m >= p.m) break;
+    const float* hrow = hs + m * p.rank;
+    float t = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 4 * RV; ++e) {
+      if (2 * e < p.rank) t = __builtin_fmaf(hrow[2 * e], bf16lo_to_f32(bw[e]), t);
+      if (2 * e + 1 < p.rank) t = __builtin_fmaf(hrow[2 * e + 1], bf16hi_to_f32(bw[e]), t);
+    }
+    float r = round_bf16(bf16_to_f32(base[i]) + round_bf16(round_bf16(t) * p.scale));
+    if (p.bias != nullptr) r = round_bf16(r + bias);
+    p.y[static_cast<int64_t>(m) * p.n + n] = f32_to_bf16(r);
+  }
+}
+
+template <int NW, int CPW>
+void launch_main(const Skinny2Params& p, hipStream_t stream) {
+  const int64_t blocks = p.a_blocks + ceil_div(p.n, 16);
+  hipLaunchKernelGGL((k_skinny_main<NW, CPW>), dim3(static_cast<unsigned>(blocks)), dim3(64 * NW),
+                     0, stream, p);
+}
+
+struct Skinny2Plan {
+  int nw;      // waves per block
+  int cpw;     // 128-column chunks per weight wave (1, 2 or 4)
+  int slices;  // adapter K slices
+};
+
+// Waves per block: enough weight blocks x waves to put ~8 waves on each of
+// 256 CUs, 4 to 16 per block.
+Skinny2Plan plan2(int64_t n, int64_t k) {
+  Skinny2Plan p;
+  const int64_t blocks = ceil_div(n, 16);
+  p.nw = 4;
+  while (p.nw < 16 && blocks * p.nw < 2048) p.nw *= 2;
+  const int64_t c = ceil_div(k / 128, p.nw);
+  p.cpw = c <= 1 ? 1 : (c <= 2 ? 2 : 4);
+  p.slices = static_cast<int>(c);
+  return p;
+}
+
+}  // namespace
+
+bool skinny2_ok(int64_t m, int64_t n, int64_t k, int64_t rank, int64_t n_groups, int64_t group) {
+  if (m < 1 || m > 16 || n < 1 || k % 128 != 0 || rank < 1 || rank > 64) return false;
+  if (n_groups > 1 && (group < 32 || (group & (group - 1)) != 0)) return false;
+  // every weight wave covers its K range in at most 4 chunks of 128 columns
+  return k / 128 <= 4 * plan2(n, k).nw;
+}
+
+// Measured on the three Qwen3-2B projection shapes (group 64, rank 32,
+// weights cycled beyond the 256 MB MALL): 30-40% faster than the one-launch
+// kernel for M <= 4, slower at M = 16, where every weight block re-reads all
+// of x and the finish handles 16 rows of y. RPX_SKINNY2=1 selects it for
+// every M <= 16, RPX_SKINNY2=0 never; RPX_SKINNY_TILE (a one-launch shape)
+// also turns it off.
+bool skinny2_selected(int64_t m, int64_t n, int64_t k, int64_t rank, int64_t n_groups,
+                      int64_t group) {
+  const char* tile = std::getenv("RPX_SKINNY_TILE");
+  if (tile != nullptr && std::atoi(tile) > 0) return false;
+  const char* env = std::getenv("RPX_SKINNY2");
+  const int force = env != nullptr ? std::atoi(env) : -1;
+  if (force == 0) return false;
+  if (force != 1 && m > 4) return false;
+  return skinny2_ok(m, n, k, rank, n_groups, group);
+}
+
+int64_t skinny2_workspace_floats(int64_t m, int64_t n, int64_t k, int64_t rank) {
+  return static_cast<int64_t>(plan2(n, k).slices) * m * rank;
+}
+
+hipError_t launch_skinny2_forward(const uint16_t* x, int64_t m, int64_t k, const Int4Operand& w,
+                                  int64_t n, const uint16_t* lora_a, const uint16_t* lora_b,
+                                  int64_t rank, float scale, const uint16_t* bias, uint16_t* y,
+                                  uint16_t* h, float* ws, hipStream_t stream) {
+  Skinny2Params p;
+  p.x = x;
+  p.m = static_cast<int>(m);
+  p.k = k;
+  p.n = n;
+  p.packed = w.packed;
+  p.pcols = w.packed_cols;
+  p.scales = w.scales;
+  p.n_groups = w.n_groups;
+  p.group_shift = 0;
+  if (w.n_groups > 1)
+    while ((int64_t{1} << p.group_shift) < w.group) ++p.group_shift;
+  p.lora_a = lora_a;
+  p.lora_b = lora_b;
+  p.rank = static_cast<int>(rank);
+  p.scale = scale;
+  p.bias = bias;
+  p.y = y;
+  p.h = h;
+  p.part = ws;
+  const Skinny2Plan pl = plan2(n, k);
+  p.slices = pl.slices;
+  p.a_blocks = p.slices * static_cast<int>(ceil_div(rank, 16));
+  p.b_vec = (reinterpret_cast<uintptr_t>(lora_b) & 15) == 0 && rank % 8 == 0 && rank * 16 <= 512;
+  bool launched = false;
+#define RPX_MAIN(NW, CPW)                             \
+  if (!launched && pl.nw == NW && pl.cpw == CPW) {    \
+    launch_main<NW, CPW>(p, stream);                  \
+    launched = true;                                  \
+  }
+  RPX_MAIN(4, 1) RPX_MAIN(4, 2) RPX_MAIN(4, 4)
+  RPX_MAIN(8, 1) RPX_MAIN(8, 2) RPX_MAIN(8, 4)
+  RPX_MAIN(16, 1) RPX_MAIN(16, 2) RPX_MAIN(16, 4)
+#undef RPX_MAIN
+  if (!launched) return hipErrorInvalidValue;
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const dim3 fin_grid(static_cast<unsigned>(ceil_div(n, kFinRows)));
+  switch ((rank + 7) / 8) {
+    case 1: hipLaunchKernelGGL(k_skinny_finish<1>, fin_grid, dim3(kFinThreads), 0, stream, p); break;
+    case 2: hipLaunchKernelGGL(k_skinny_finish<2>, fin_grid, dim3(kFinThreads), 0, stream, p); break;
+    case 3: hipLaunchKernelGGL(k_skinny_finish<3>, fin_grid, dim3(kFinThreads), 0, stream, p); break;
+    case 4: hipLaunchKernelGGL(k_skinny_finish<4>, fin_grid, dim3(kFinThreads), 0, stream, p); break;
+    case 5: hipLaunchKernelGGL(k_skinny_finish<5>, fin_grid, dim3(kFinThreads), 0, stream, p); break;
+    case 6: hipLaunchKernelGGL(k_skinny_finish<6>, fin_grid, dim3(kFinThreads), 0, stream, p); break;
+    case 7: hipLaunchKernelGGL(k_skinny_finish<7>, fin_grid, dim3(kFinThreads), 0, stream, p); break;
+    default: hipLaunchKernelGGL(k_skinny_finish<8>, fin_grid, dim3(kFinThreads), 0, stream, p); break;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace rpx

@@ -251,11 +251,34 @@ def test_skinny_every_tile_shape_matches_oracle(monkeypatch, tile, m, k, n, r, g
     assert rel_l2(from_dev(y), y_o) < TOL
 
 
-def test_skinny_graph_replays_and_repeats_are_bit_identical():
-    """The per-tile arrival counters return to their resting value after each
-    call: eager repeats and graph replays give the same bits."""
+@pytest.mark.parametrize("m,k,n,r,group", [(3, 1024, 200, 32, 64), (16, 640, 136, 48, None),
+                                           (9, 256, 70, 5, 128), (1, 4096, 80, 64, 64),
+                                           (2, 6144, 2048, 32, 64), (4, 384, 33, 8, None)])
+def test_skinny_two_launch_matches_oracle(monkeypatch, m, k, n, r, group):
+    """The two-launch path (forced for M up to 16): ragged last row blocks,
+    ranks that are not multiples of 8 and ranks above 32, several K slices."""
 
-    m, k, n, r = 8, 2048, 1536, 32
+    monkeypatch.setenv("RPX_SKINNY2", "1")
+    x, packed, scales, a, b, bias_bits, _ = _lora_case(m, k, n, r, group, seed=m + r, bias=True)
+    b = b * 50.0  # the adapter term comparable to the base product
+    y_o, h_o = olora.lora_forward(x, packed, scales, a, b, alpha=2.0 * r, rank=r,
+                                  bias_bits=bias_bits, group_size=group)
+    biasd = to_dev(bias_bits.view(np.int16)).view(torch.uint16)
+    y, h = ops.int4lora_forward(to_dev_bf16(x), to_dev(packed),
+                                to_dev(scales.view(np.int16)).view(torch.uint16), to_dev_bf16(a),
+                                to_dev_bf16(b), scaling=2.0, group_size=group, bias_bits=biasd)
+    torch.cuda.synchronize()
+    assert rel_l2(from_dev(h), h_o) < TOL
+    assert rel_l2(from_dev(y), y_o) < TOL
+
+
+@pytest.mark.parametrize("m", [8, 2])
+def test_skinny_graph_replays_and_repeats_are_bit_identical(m):
+    """The one-launch kernel's per-tile arrival counters (M = 8) return to
+    their resting value after each call, and the two-launch path (M = 2)
+    keeps no state: eager repeats and graph replays give the same bits."""
+
+    k, n, r = 2048, 1536, 32
     x, packed, scales, a, b, bias_bits, _ = _lora_case(m, k, n, r, 64, seed=91, bias=False)
     xd, pd = to_dev_bf16(x), to_dev(packed)
     sd = to_dev(scales.view(np.int16)).view(torch.uint16)
