@@ -104,6 +104,49 @@ int rpx_int4lora_backward(const void* grad, const void* x, int dtype, int64_t m,
                           float* d_lora_b, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------
+ * Activation epilogues: the FFN steps on either side of an INT4 + LoRA linear,
+ * fused into its GEMMs. Activations run in f32 on the bf16 operands and are
+ * rounded once; bf16 compute only. All [m, n] operands are dense row-major.
+ * ------------------------------------------------------------------------- */
+
+#define RPX_ACT_GELU 1     /* gelu(z) = z (1 + erf(z / sqrt 2)) / 2: activate("gelu"),
+                              src/representax/models/components.py:159-160, as in
+                              BertMLP, src/representax/models/bert/model.py:249 */
+#define RPX_ACT_SILU_MUL 2 /* silu(gate) * z: the Qwen3 MLP's gated product,
+                              src/representax/models/qwen3_vl/text.py:202 */
+
+/* The FFN's up projection with its activation: z [m, n] = the linear's output
+ * (as rpx_int4lora_forward's y), y [m, n] = gelu(z) (RPX_ACT_GELU) or
+ * silu(gate) * z (RPX_ACT_SILU_MUL, gate [m, n] the gate projection's
+ * output), h as in rpx_int4lora_forward. Workspace: rpx_int4lora_forward_workspace.
+ * Replaces activate(self.input(hidden)) (bert/model.py:249) and
+ * jax.nn.silu(self.gate(x)) * self.up(x) (qwen3_vl/text.py:202). */
+int rpx_int4lora_forward_act(const void* x, int dtype, int64_t m, int64_t k, const uint8_t* packed,
+                             const uint16_t* scale_bits, int64_t n, int64_t group_size,
+                             const uint16_t* bias_bits, const void* lora_a, const void* lora_b,
+                             int64_t rank, float scaling, int act, const void* gate, void* y,
+                             void* z, void* h, void* workspace, size_t workspace_bytes,
+                             void* stream);
+
+/* The FFN's down projection backward followed by the activation's backward:
+ * x [m, k] is the down projection's input (the activation output), z [m, k]
+ * and gate [m, k] the forward's operands of the activation. With d = the
+ * down projection's input gradient (rpx_int4lora_backward's dx, rounded):
+ *   RPX_ACT_GELU:     dz = d * gelu'(z);
+ *   RPX_ACT_SILU_MUL: dz = d * silu(gate) (the up projection's gradient),
+ *                     dgate = d * z * silu'(gate) (the gate projection's).
+ * d_lora_a / d_lora_b as in rpx_int4lora_backward; workspace:
+ * rpx_int4lora_backward_workspace. Replaces JAX's transpose of the same
+ * expressions. */
+int rpx_int4lora_backward_act(const void* grad, const void* x, int dtype, int64_t m, int64_t k,
+                              const uint8_t* packed, const uint16_t* scale_bits, int64_t n,
+                              int64_t group_size, const void* lora_a, const void* lora_b,
+                              int64_t rank, float scaling, const void* h, int act, const void* z,
+                              const void* gate, void* dz, void* dgate, float* d_lora_a,
+                              float* d_lora_b, void* workspace, size_t workspace_bytes,
+                              void* stream);
+
+/* ---------------------------------------------------------------------------
  * Dynamically scaled fp8.
  * ------------------------------------------------------------------------- */
 

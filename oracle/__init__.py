@@ -8,6 +8,9 @@ codecs, the numerics of
   autodiff transpose), and
 * ``src/representax/precision.py:127-239`` (dynamic amax scaling, OCP fp8
   casts, the scaled fp8 dot and its custom VJP),
+* ``src/representax/models/components.py:153-167``,
+  ``bert/model.py:243-249`` and ``qwen3_vl/text.py:200-203`` (the GELU and
+  SiLU-gated FFN steps next to the linears, ``act``),
 
 so that tests, the smoke check and the benchmark's CPU-baseline leg can check
 the HIP kernels of ``representax_amd``. Nothing in the product imports it; the
@@ -29,10 +32,16 @@ Pinning (what checks each function against something other than itself):
 * ``fp8``: amax/scale closed forms (zero, inf, NaN tensors), cast through the
   torch-pinned codec, dot compared with an fp64 product of the exactly decoded
   operands, VJP compared with the transposed-product identities.
+* ``act``: GELU and SiLU against torch's float64 routines and closed forms
+  (gelu(0) = 0, gelu(-z) = gelu(z) - z, silu(-g) = silu(g) - g), their
+  derivatives against central finite differences, the fused blocks' backward
+  against finite differences of their float64 forward.
 
 Parity unpinned (no reference test or fixture fixes these bits, and the
 reference cannot run here): XLA:CPU's accumulation order of bf16 dots, whether
 its f32->f8 convert rounds directly or through f16, and whether bf16-typed
 elementwise ops keep excess precision. The oracle takes the HLO-typed reading:
 every bf16-typed op rounds once to nearest-even and f32->f8 rounds directly.
+The FFN activations (``act``) are the exception: evaluated exactly from the
+bf16 linear outputs and rounded once, the fused-elementwise reading.
 """

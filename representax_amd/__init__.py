@@ -18,6 +18,7 @@ from .adapters import (
 )
 from .components import Linear
 from .config import PrecisionConfig, QuantizedLoRAConfig
+from .mlp import gelu_mlp, swiglu_mlp
 from .precision import (
     FP32_POLICY,
     DelayedScaling,
@@ -42,6 +43,7 @@ __all__ = [
     "active_compute_dtype",
     "apply_quantized_lora",
     "compute_parameter",
+    "gelu_mlp",
     "linear_matmul",
     "lora_parameter_filter",
     "lora_parameters",
@@ -49,4 +51,5 @@ __all__ = [
     "merge_quantized_lora",
     "precision_context",
     "resolve_precision_policy",
+    "swiglu_mlp",
 ]

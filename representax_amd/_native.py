@@ -22,6 +22,8 @@ DTYPE_F32 = 0
 DTYPE_BF16 = 1
 FP8_E4M3FN = 0
 FP8_E5M2 = 1
+ACT_GELU = 1
+ACT_SILU_MUL = 2
 
 _p = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -46,6 +48,16 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _int,
         [_p, _p, _int, _i64, _i64, _p, _p, _i64, _i64, _p, _p, _i64, _f32, _p, _p, _p, _p, _p,
          _size, _p],
+    ),
+    "rpx_int4lora_forward_act": (
+        _int,
+        [_p, _int, _i64, _i64, _p, _p, _i64, _i64, _p, _p, _p, _i64, _f32, _int, _p, _p, _p, _p,
+         _p, _size, _p],
+    ),
+    "rpx_int4lora_backward_act": (
+        _int,
+        [_p, _p, _int, _i64, _i64, _p, _p, _i64, _i64, _p, _p, _i64, _f32, _p, _int, _p, _p, _p,
+         _p, _p, _p, _p, _size, _p],
     ),
     "rpx_fp8_scale_workspace": (_size, [_i64]),
     "rpx_fp8_scale": (_int, [_p, _int, _i64, _int, _p, _p, _size, _p]),

@@ -6,6 +6,7 @@
 
 #include "../../include/representax_amd.h"
 #include "common.h"
+#include "act.h"
 #include "kernels.h"
 
 namespace rpx {
@@ -265,11 +266,22 @@ size_t rpx_int4lora_forward_workspace(int64_t m, int64_t n, int64_t k, int64_t g
   return s.used;
 }
 
-int rpx_int4lora_forward(const void* x, int dtype, int64_t m, int64_t k, const uint8_t* packed,
-                         const uint16_t* scale_bits, int64_t n, int64_t group_size,
-                         const uint16_t* bias_bits, const void* lora_a, const void* lora_b,
-                         int64_t rank, float scaling, void* y, void* h, void* workspace,
-                         size_t workspace_bytes, void* stream) {
+namespace {
+
+// Activation applied to a linear's output (ActMode) and its [M, N] operands.
+struct ActIO {
+  int mode = kActNone;
+  const uint16_t* aux = nullptr;
+  const uint16_t* aux2 = nullptr;
+  uint16_t* pre_out = nullptr;  // forward modes: the linear's own output
+  uint16_t* out2 = nullptr;     // SiLU-mul backward: d gate
+};
+
+int int4lora_forward_impl(const void* x, int dtype, int64_t m, int64_t k, const uint8_t* packed,
+                          const uint16_t* scale_bits, int64_t n, int64_t group_size,
+                          const uint16_t* bias_bits, const void* lora_a, const void* lora_b,
+                          int64_t rank, float scaling, void* y, void* h, void* workspace,
+                          size_t workspace_bytes, void* stream, const ActIO& act) {
   RPX_TRY(check_dtype(dtype));
   int64_t ng, g;
   RPX_TRY(check_int4_shape(n, k, group_size, &ng, &g));
@@ -291,6 +303,16 @@ int rpx_int4lora_forward(const void* x, int dtype, int64_t m, int64_t k, const u
   const bool fast = lora_fast_shape(dtype, k, ng, g, rank) && aligned16(x) && aligned16(packed) &&
                     aligned16(lora_a) && aligned16(y);
   Arena arena(workspace, workspace_bytes);
+  // where the paths without the activation epilogue put the linear's output;
+  // the activation then runs elementwise from there into y
+  void* lin = act.mode != kActNone ? static_cast<void*>(act.pre_out) : y;
+  auto finish_act = [&]() -> int {
+    if (act.mode != kActNone)
+      RPX_HIP(launch_act(act.mode, act.pre_out, act.aux, nullptr, m * n, static_cast<uint16_t*>(y),
+                         nullptr, st),
+              "int4lora_forward: activation");
+    return kOk;
+  };
   if (lora_skinny(dtype, m, n, k, ng, g, rank) && aligned16(x) && aligned16(packed) &&
       aligned16(lora_a)) {
     float* ws = arena.take<float>(skinny_workspace_floats(m, n, k, rank));
@@ -299,16 +321,17 @@ int rpx_int4lora_forward(const void* x, int dtype, int64_t m, int64_t k, const u
       RPX_HIP(launch_skinny2_forward(static_cast<const uint16_t*>(x), m, k, w, n,
                                      static_cast<const uint16_t*>(lora_a),
                                      static_cast<const uint16_t*>(lora_b), rank, c, bias_bits,
-                                     static_cast<uint16_t*>(y), static_cast<uint16_t*>(h), ws, st),
+                                     static_cast<uint16_t*>(lin), static_cast<uint16_t*>(h), ws,
+                                     st),
               "int4lora_forward: skinny-M row-block kernels");
-      return kOk;
+      return finish_act();
     }
     RPX_HIP(launch_skinny_forward(static_cast<const uint16_t*>(x), m, k, w, n,
                                   static_cast<const uint16_t*>(lora_a),
                                   static_cast<const uint16_t*>(lora_b), rank, c, bias_bits,
-                                  static_cast<uint16_t*>(y), static_cast<uint16_t*>(h), ws, st),
+                                  static_cast<uint16_t*>(lin), static_cast<uint16_t*>(h), ws, st),
             "int4lora_forward: skinny-M kernels");
-    return kOk;
+    return finish_act();
   }
   if (fast) {
     const uint16_t* xb = static_cast<const uint16_t*>(x);
@@ -326,6 +349,9 @@ int rpx_int4lora_forward(const void* x, int dtype, int64_t m, int64_t k, const u
     epi.rank = rank;
     epi.scale = c;
     epi.bias = bias_bits;
+    epi.act = act.mode;
+    epi.aux = act.aux;
+    epi.pre_out = act.pre_out;
     RPX_HIP(launch_gemm_int4(xb, k, w, m, n, k, static_cast<uint16_t*>(y), n, epi, st),
             "int4lora_forward: fused dequant GEMM");
     return kOk;
@@ -344,9 +370,40 @@ int rpx_int4lora_forward(const void* x, int dtype, int64_t m, int64_t k, const u
                               rank, low, st),
           "int4lora_forward: adapter up-projection");
   hipLaunchKernelGGL(k_lora_combine, dim3(grid1d(m * n)), dim3(256), 0, st, base, low, m, n, c,
-                     bias_bits, dtype, y);
+                     bias_bits, dtype, lin);
   RPX_HIP(hipGetLastError(), "int4lora_forward: combine");
-  return kOk;
+  return finish_act();
+}
+
+}  // namespace
+
+int rpx_int4lora_forward(const void* x, int dtype, int64_t m, int64_t k, const uint8_t* packed,
+                         const uint16_t* scale_bits, int64_t n, int64_t group_size,
+                         const uint16_t* bias_bits, const void* lora_a, const void* lora_b,
+                         int64_t rank, float scaling, void* y, void* h, void* workspace,
+                         size_t workspace_bytes, void* stream) {
+  return int4lora_forward_impl(x, dtype, m, k, packed, scale_bits, n, group_size, bias_bits, lora_a,
+                               lora_b, rank, scaling, y, h, workspace, workspace_bytes, stream,
+                               ActIO{});
+}
+
+int rpx_int4lora_forward_act(const void* x, int dtype, int64_t m, int64_t k, const uint8_t* packed,
+                             const uint16_t* scale_bits, int64_t n, int64_t group_size,
+                             const uint16_t* bias_bits, const void* lora_a, const void* lora_b,
+                             int64_t rank, float scaling, int act, const void* gate, void* y,
+                             void* z, void* h, void* workspace, size_t workspace_bytes,
+                             void* stream) {
+  if (act != RPX_ACT_GELU && act != RPX_ACT_SILU_MUL)
+    return fail_invalid("rpx_int4lora_forward_act: unknown activation");
+  if (dtype != kBF16) return fail_invalid("rpx_int4lora_forward_act: activations need bf16 compute");
+  if (m > 0 && n > 0 && (z == nullptr || (act == RPX_ACT_SILU_MUL && gate == nullptr)))
+    return fail_invalid("rpx_int4lora_forward_act: null pointer");
+  ActIO io;
+  io.mode = act == RPX_ACT_GELU ? kActGeluFwd : kActSiluMulFwd;
+  io.aux = static_cast<const uint16_t*>(gate);
+  io.pre_out = static_cast<uint16_t*>(z);
+  return int4lora_forward_impl(x, dtype, m, k, packed, scale_bits, n, group_size, bias_bits, lora_a,
+                               lora_b, rank, scaling, y, h, workspace, workspace_bytes, stream, io);
 }
 
 size_t rpx_int4lora_backward_workspace(int64_t m, int64_t n, int64_t k, int64_t group_size,
@@ -361,12 +418,14 @@ size_t rpx_int4lora_backward_workspace(int64_t m, int64_t n, int64_t k, int64_t 
   return s.used;
 }
 
-int rpx_int4lora_backward(const void* grad, const void* x, int dtype, int64_t m, int64_t k,
-                          const uint8_t* packed, const uint16_t* scale_bits, int64_t n,
-                          int64_t group_size, const void* lora_a, const void* lora_b,
-                          int64_t rank, float scaling, const void* h, void* dx, float* d_lora_a,
-                          float* d_lora_b, void* workspace, size_t workspace_bytes,
-                          void* stream) {
+namespace {
+
+int int4lora_backward_impl(const void* grad, const void* x, int dtype, int64_t m, int64_t k,
+                           const uint8_t* packed, const uint16_t* scale_bits, int64_t n,
+                           int64_t group_size, const void* lora_a, const void* lora_b,
+                           int64_t rank, float scaling, const void* h, void* dx, float* d_lora_a,
+                           float* d_lora_b, void* workspace, size_t workspace_bytes, void* stream,
+                           const ActIO& act) {
   RPX_TRY(check_dtype(dtype));
   int64_t ng, g;
   RPX_TRY(check_int4_shape(n, k, group_size, &ng, &g));
@@ -438,6 +497,10 @@ int rpx_int4lora_backward(const void* grad, const void* x, int dtype, int64_t m,
     epi.cols_sj = 1;
     epi.rank = rank;
     epi.scale = 1.0f;
+    epi.act = act.mode;
+    epi.aux = act.aux;
+    epi.aux2 = act.aux2;
+    epi.out2 = act.out2;
     RPX_HIP(launch_gemm_bf16(gb, n, wt, n, m, k, n, static_cast<uint16_t*>(dx), k, epi, st),
             "int4lora_backward: dx");
     return kOk;
@@ -481,7 +544,51 @@ int rpx_int4lora_backward(const void* grad, const void* x, int dtype, int64_t m,
   hipLaunchKernelGGL(k_round_inplace_f32, dim3(grid1d(rank * k)), dim3(256), 0, st, d_lora_a,
                      rank * k, dtype);
   RPX_HIP(hipGetLastError(), "int4lora_backward: round dA");
+  if (act.mode != kActNone)
+    RPX_HIP(launch_act(act.mode, static_cast<const uint16_t*>(dx), act.aux, act.aux2, m * k,
+                       static_cast<uint16_t*>(dx), act.out2, st),
+            "int4lora_backward: activation");
   return kOk;
+}
+
+}  // namespace
+
+int rpx_int4lora_backward(const void* grad, const void* x, int dtype, int64_t m, int64_t k,
+                          const uint8_t* packed, const uint16_t* scale_bits, int64_t n,
+                          int64_t group_size, const void* lora_a, const void* lora_b,
+                          int64_t rank, float scaling, const void* h, void* dx, float* d_lora_a,
+                          float* d_lora_b, void* workspace, size_t workspace_bytes,
+                          void* stream) {
+  return int4lora_backward_impl(grad, x, dtype, m, k, packed, scale_bits, n, group_size, lora_a,
+                                lora_b, rank, scaling, h, dx, d_lora_a, d_lora_b, workspace,
+                                workspace_bytes, stream, ActIO{});
+}
+
+int rpx_int4lora_backward_act(const void* grad, const void* x, int dtype, int64_t m, int64_t k,
+                              const uint8_t* packed, const uint16_t* scale_bits, int64_t n,
+                              int64_t group_size, const void* lora_a, const void* lora_b,
+                              int64_t rank, float scaling, const void* h, int act, const void* z,
+                              const void* gate, void* dz, void* dgate, float* d_lora_a,
+                              float* d_lora_b, void* workspace, size_t workspace_bytes,
+                              void* stream) {
+  if (act != RPX_ACT_GELU && act != RPX_ACT_SILU_MUL)
+    return fail_invalid("rpx_int4lora_backward_act: unknown activation");
+  if (dtype != kBF16) return fail_invalid("rpx_int4lora_backward_act: activations need bf16 compute");
+  if (m > 0 && (z == nullptr || (act == RPX_ACT_SILU_MUL && (gate == nullptr || dgate == nullptr))))
+    return fail_invalid("rpx_int4lora_backward_act: null pointer");
+  ActIO io;
+  if (act == RPX_ACT_GELU) {
+    io.mode = kActGeluBwd;
+    io.aux = static_cast<const uint16_t*>(z);
+  } else {
+    io.mode = kActSiluMulBwd;
+    io.aux = static_cast<const uint16_t*>(gate);
+    io.aux2 = static_cast<const uint16_t*>(z);
+    io.out2 = static_cast<uint16_t*>(dgate);
+  }
+  return int4lora_backward_impl(grad, x, dtype, m, k, packed, scale_bits, n, group_size, lora_a,
+                                lora_b, rank, scaling, h, dz, d_lora_a, d_lora_b, workspace,
+                                workspace_bytes, stream, io);
 }
 
 // ---------------------------------------------------------------------------

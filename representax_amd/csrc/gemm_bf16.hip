@@ -19,6 +19,7 @@
 
 #include "common.h"
 #include "kernels.h"
+#include "act.h"
 #include "lds_pipeline.h"
 
 namespace rpx {
@@ -82,7 +83,7 @@ __device__ __forceinline__ void round2(float& a, float& b) {
 // is conflict-free.
 __device__ __forceinline__ int pswz(int row) { return (row >> 3) & 1; }
 
-template <int BM, int BN, int WM, int WN, int NS, int WPE, bool INT4, int JB>
+template <int BM, int BN, int WM, int WN, int NS, int WPE, bool INT4, int JB, int ACT>
 __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
     k_gemm_nt(const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ B,
               int64_t ldb, Int4Operand w, int group_shift, int64_t M, int64_t N, int64_t K,
@@ -438,9 +439,115 @@ __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_
     }
   }
 
-  const bool vec_out = (ldc & 7) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0;
+  // Stores one [BM, BN] tile of bf16 pairs (this lane's share in vals) at
+  // dst with row stride ldc: staged in LDS and written as whole row segments
+  // when the tile fits the pipeline's LDS, else 8-byte stores per lane.
   constexpr int P = BN * 2 + 16;  // LDS row pitch of the staged tile
-  if constexpr (BM * P <= NS * STAGE) {
+  auto store_tile = [&](uint16_t* dst_base, const uint32_t (&vals)[FN][FM][8]) {
+    const bool vec_out = (ldc & 7) == 0 && (reinterpret_cast<uintptr_t>(dst_base) & 15) == 0;
+    if constexpr (BM * P <= NS * STAGE) {
+      wait_sync<0>();  // every wave is done reading the stages (or the last tile)
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+          for (int vg = 0; vg < 4; ++vg) {
+            const int ml = wm * TM + fm * 32 + frow;
+            const int nl = wn * TN + fn * 32 + 8 * vg + 4 * half;
+            *reinterpret_cast<u32x2_t*>(smem + ml * P + nl * 2) =
+                u32x2_t{vals[fn][fm][2 * vg], vals[fn][fm][2 * vg + 1]};
+          }
+      __syncthreads();
+      constexpr int CPR = BN / 8;  // 16-byte chunks per tile row
+      constexpr int ITS = BM * CPR / NT;
+      static_assert((BM * CPR) % NT == 0, "tile chunks must split evenly over the threads");
+      if (vec_out && m0 + BM <= M && n0 + BN <= N) {
+        u32x4_t v[ITS];
+#pragma unroll
+        for (int it = 0; it < ITS; ++it) {
+          const int idx = it * NT + tid;
+          v[it] = *reinterpret_cast<const u32x4_t*>(smem + (idx / CPR) * P + (idx % CPR) * 16);
+        }
+#pragma unroll
+        for (int it = 0; it < ITS; ++it) {
+          const int idx = it * NT + tid;
+          *reinterpret_cast<u32x4_t*>(dst_base + (m0 + idx / CPR) * ldc + n0 + 8 * (idx % CPR)) =
+              v[it];
+        }
+        return;
+      }
+      for (int it = 0; it < ITS; ++it) {
+        const int idx = it * NT + tid;
+        const int64_t m = m0 + idx / CPR;
+        const int64_t n = n0 + 8 * (idx % CPR);
+        if (m >= M || n >= N) continue;
+        const u32x4_t v =
+            *reinterpret_cast<const u32x4_t*>(smem + (idx / CPR) * P + (idx % CPR) * 16);
+        uint16_t* d = dst_base + m * ldc + n;
+        if (vec_out && n + 7 < N) {
+          *reinterpret_cast<u32x4_t*>(d) = v;
+        } else {
+          for (int e = 0; e < 8; ++e)
+            if (n + e < N) d[e] = static_cast<uint16_t>((v[e >> 1] >> (16 * (e & 1))) & 0xFFFFu);
+        }
+      }
+    } else {
+      // tile too large to stage in the pipeline's LDS: 8-byte stores per lane
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm) {
+          const int64_t m = mw + fm * 32 + frow;
+          if (m >= M) continue;
+#pragma unroll
+          for (int vg = 0; vg < 4; ++vg) {
+            const int64_t nb = nw + fn * 32 + 8 * vg + 4 * half;
+            uint16_t* dst = dst_base + m * ldc + nb;
+            if (vec_out && nb + 3 < N) {
+              *reinterpret_cast<u32x2_t*>(dst) = u32x2_t{vals[fn][fm][2 * vg], vals[fn][fm][2 * vg + 1]};
+            } else {
+#pragma unroll
+              for (int e = 0; e < 4; ++e)
+                if (nb + e < N)
+                  dst[e] = static_cast<uint16_t>((vals[fn][fm][2 * vg + e / 2] >> (16 * (e & 1))) &
+                                                 0xFFFFu);
+            }
+          }
+        }
+    }
+  };
+
+  if constexpr (ACT == kActNone) {
+    store_tile(out, ypk);
+  } else {
+    // Activation epilogue on the rounded outputs v: f32 from bf16 operands,
+    // rounded once (act.h). The tile of v is staged in LDS and every thread
+    // then transforms whole 8-column row segments, with the auxiliary
+    // operands' 16-byte loads issued before the staging. Forward modes also
+    // store v itself.
+    static_assert(BM * P <= NS * STAGE, "activation epilogues stage the tile in LDS");
+    constexpr bool FWD = ACT == kActGeluFwd || ACT == kActSiluMulFwd;
+    constexpr bool AUX = ACT != kActGeluFwd;
+    constexpr bool TWO = ACT == kActSiluMulBwd;
+    constexpr int CPR = BN / 8;  // 8-column segments per tile row
+    constexpr int ITS = BM * CPR / NT;
+    static_assert((BM * CPR) % NT == 0, "tile segments must split evenly over the threads");
+    const uintptr_t ptrs = reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(epi.aux) |
+                           reinterpret_cast<uintptr_t>(epi.aux2) |
+                           reinterpret_cast<uintptr_t>(epi.pre_out) |
+                           reinterpret_cast<uintptr_t>(epi.out2);
+    const bool vec = m0 + BM <= M && n0 + BN <= N && (ldc & 7) == 0 && (ptrs & 15) == 0;
+    u32x4_t av[AUX ? ITS : 1], a2v[TWO ? ITS : 1];
+    if (vec) {
+#pragma unroll
+      for (int it = 0; it < ITS; ++it) {
+        const int idx = it * NT + tid;
+        const int64_t off = (m0 + idx / CPR) * ldc + n0 + 8 * (idx % CPR);
+        if constexpr (AUX) av[it] = *reinterpret_cast<const u32x4_t*>(epi.aux + off);
+        if constexpr (TWO) a2v[it] = *reinterpret_cast<const u32x4_t*>(epi.aux2 + off);
+      }
+    }
     wait_sync<0>();  // every wave is done reading the pipeline stages
 #pragma unroll
     for (int fn = 0; fn < FN; ++fn)
@@ -454,59 +561,49 @@ __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_
               u32x2_t{ypk[fn][fm][2 * vg], ypk[fn][fm][2 * vg + 1]};
         }
     __syncthreads();
-    constexpr int CPR = BN / 8;  // 16-byte chunks per tile row
-    constexpr int ITS = BM * CPR / NT;
-    static_assert((BM * CPR) % NT == 0, "tile chunks must split evenly over the threads");
-    if (vec_out && m0 + BM <= M && n0 + BN <= N) {
-      u32x4_t v[ITS];
+    auto bf16_at = [](const u32x4_t& q, int e) {
+      return (e & 1) ? bf16hi_to_f32(q[e >> 1]) : bf16lo_to_f32(q[e >> 1]);
+    };
 #pragma unroll
-      for (int it = 0; it < ITS; ++it) {
-        const int idx = it * NT + tid;
-        v[it] = *reinterpret_cast<const u32x4_t*>(smem + (idx / CPR) * P + (idx % CPR) * 16);
-      }
-#pragma unroll
-      for (int it = 0; it < ITS; ++it) {
-        const int idx = it * NT + tid;
-        *reinterpret_cast<u32x4_t*>(out + (m0 + idx / CPR) * ldc + n0 + 8 * (idx % CPR)) = v[it];
-      }
-      return;
-    }
     for (int it = 0; it < ITS; ++it) {
       const int idx = it * NT + tid;
       const int64_t m = m0 + idx / CPR;
       const int64_t n = n0 + 8 * (idx % CPR);
       if (m >= M || n >= N) continue;
       const u32x4_t v = *reinterpret_cast<const u32x4_t*>(smem + (idx / CPR) * P + (idx % CPR) * 16);
-      uint16_t* d = out + m * ldc + n;
-      if (vec_out && n + 7 < N) {
-        *reinterpret_cast<u32x4_t*>(d) = v;
-      } else {
-        for (int e = 0; e < 8; ++e)
-          if (n + e < N) d[e] = static_cast<uint16_t>((v[e >> 1] >> (16 * (e & 1))) & 0xFFFFu);
+      const int64_t off = m * ldc + n;
+      float r[8], r2[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float a0 = 0.0f, a1 = 0.0f;
+        if (vec) {
+          if constexpr (AUX) a0 = bf16_at(av[it], e);
+          if constexpr (TWO) a1 = bf16_at(a2v[it], e);
+        } else if (n + e < N) {
+          if constexpr (AUX) a0 = bf16_to_f32(epi.aux[off + e]);
+          if constexpr (TWO) a1 = bf16_to_f32(epi.aux2[off + e]);
+        }
+        r[e] = act_apply<ACT>(bf16_at(v, e), a0, a1, &r2[e]);
       }
-    }
-  } else {
-    // tile too large to stage in the pipeline's LDS: 8-byte stores per lane
-#pragma unroll
-    for (int fn = 0; fn < FN; ++fn)
-#pragma unroll
-      for (int fm = 0; fm < FM; ++fm) {
-        const int64_t m = mw + fm * 32 + frow;
-        if (m >= M) continue;
-#pragma unroll
-        for (int vg = 0; vg < 4; ++vg) {
-          const int64_t nb = nw + fn * 32 + 8 * vg + 4 * half;
-          uint16_t* dst = out + m * ldc + nb;
-          if (vec_out && nb + 3 < N) {
-            *reinterpret_cast<u32x2_t*>(dst) = u32x2_t{ypk[fn][fm][2 * vg], ypk[fn][fm][2 * vg + 1]};
-          } else {
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-              if (nb + e < N)
-                dst[e] = static_cast<uint16_t>((ypk[fn][fm][2 * vg + e / 2] >> (16 * (e & 1))) & 0xFFFFu);
-          }
+      const u32x4_t o{pack_bf16x2(r[0], r[1]), pack_bf16x2(r[2], r[3]), pack_bf16x2(r[4], r[5]),
+                      pack_bf16x2(r[6], r[7])};
+      u32x4_t o2{0u, 0u, 0u, 0u};
+      if constexpr (TWO)
+        o2 = u32x4_t{pack_bf16x2(r2[0], r2[1]), pack_bf16x2(r2[2], r2[3]),
+                     pack_bf16x2(r2[4], r2[5]), pack_bf16x2(r2[6], r2[7])};
+      if (vec) {
+        *reinterpret_cast<u32x4_t*>(out + off) = o;
+        if constexpr (FWD) *reinterpret_cast<u32x4_t*>(epi.pre_out + off) = v;
+        if constexpr (TWO) *reinterpret_cast<u32x4_t*>(epi.out2 + off) = o2;
+      } else {
+        for (int e = 0; e < 8 && n + e < N; ++e) {
+          const int sh = 16 * (e & 1);
+          out[off + e] = static_cast<uint16_t>((o[e >> 1] >> sh) & 0xFFFFu);
+          if constexpr (FWD) epi.pre_out[off + e] = static_cast<uint16_t>((v[e >> 1] >> sh) & 0xFFFFu);
+          if constexpr (TWO) epi.out2[off + e] = static_cast<uint16_t>((o2[e >> 1] >> sh) & 0xFFFFu);
         }
       }
+    }
   }
 }
 
@@ -514,16 +611,16 @@ constexpr int gemm_lds_bytes(int bm, int bn, int ns, bool int4) {
   return ns * (bm * 128 + bn * (int4 ? 32 : 128));
 }
 
-template <int BM, int BN, int WM, int WN, int NS, int WPE, bool INT4, int JB>
-hipError_t run_gemm_jb(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb,
-                       const Int4Operand& w, int64_t m, int64_t n, int64_t k, uint16_t* out,
-                       int64_t ldc, const LowRankEpilogue& epi, hipStream_t stream) {
+template <int BM, int BN, int WM, int WN, int NS, int WPE, bool INT4, int JB, int ACT>
+hipError_t run_gemm_act(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb,
+                        const Int4Operand& w, int64_t m, int64_t n, int64_t k, uint16_t* out,
+                        int64_t ldc, const LowRankEpilogue& epi, hipStream_t stream) {
   const int tiles_m = static_cast<int>(ceil_div(m, BM));
   const int tiles_n = static_cast<int>(ceil_div(n, BN));
   const size_t scale_bytes = INT4 ? static_cast<size_t>(BN) * w.n_groups * 2 : 0;
   const size_t lds = gemm_lds_bytes(BM, BN, NS, INT4) + ((scale_bytes + 15) & ~size_t{15});
   if (lds > 160 * 1024) return hipErrorInvalidValue;
-  auto kern = k_gemm_nt<BM, BN, WM, WN, NS, WPE, INT4, JB>;
+  auto kern = k_gemm_nt<BM, BN, WM, WN, NS, WPE, INT4, JB, ACT>;
   static bool attr_set = false;
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -539,6 +636,29 @@ hipError_t run_gemm_jb(const uint16_t* a, int64_t lda, const uint16_t* b, int64_
                      lds, stream, a, lda, b, ldb, w, group_shift, m, n, k, out, ldc, epi, tiles_m,
                      tiles_n);
   return hipGetLastError();
+}
+
+// Activation epilogues: the forward modes on the INT4 GEMM (the FFN's up
+// projection), the backward modes on the bf16 dx GEMM (the down projection's
+// input gradient), for the default tile shapes.
+template <int BM, int BN, int WM, int WN, int NS, int WPE, bool INT4, int JB>
+hipError_t run_gemm_jb(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb,
+                       const Int4Operand& w, int64_t m, int64_t n, int64_t k, uint16_t* out,
+                       int64_t ldc, const LowRankEpilogue& epi, hipStream_t stream) {
+#define RPX_RUN_ACT(ACT) \
+  run_gemm_act<BM, BN, WM, WN, NS, WPE, INT4, JB, ACT>(a, lda, b, ldb, w, m, n, k, out, ldc, epi, stream)
+  if (epi.act == kActNone) return RPX_RUN_ACT(kActNone);
+  if constexpr (JB > 0 && !(BM == 256 && BN == 256)) {
+    if constexpr (INT4) {
+      if (epi.act == kActGeluFwd) return RPX_RUN_ACT(kActGeluFwd);
+      if (epi.act == kActSiluMulFwd) return RPX_RUN_ACT(kActSiluMulFwd);
+    } else {
+      if (epi.act == kActGeluBwd) return RPX_RUN_ACT(kActGeluBwd);
+      if (epi.act == kActSiluMulBwd) return RPX_RUN_ACT(kActSiluMulBwd);
+    }
+  }
+#undef RPX_RUN_ACT
+  return hipErrorInvalidValue;
 }
 
 template <int BM, int BN, int WM, int WN, int NS, int WPE, bool INT4>

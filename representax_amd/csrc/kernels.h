@@ -34,6 +34,13 @@ struct LowRankEpilogue {
   int64_t rank = 0;
   float scale = 1.0f;
   const uint16_t* bias = nullptr;  // bf16 bits [N]
+  // Activation epilogue (ActMode in act.h) on the rounded output v; the
+  // [M, N] operands below share the output's row stride.
+  int act = 0;
+  const uint16_t* aux = nullptr;   // z (GELU backward) or gate (SiLU-mul)
+  const uint16_t* aux2 = nullptr;  // up (SiLU-mul backward)
+  uint16_t* pre_out = nullptr;     // v itself (forward modes)
+  uint16_t* out2 = nullptr;        // d gate (SiLU-mul backward)
 };
 
 // Packed INT4 operand [N, K] (row n holds ceil(K/2) bytes).
@@ -74,6 +81,12 @@ hipError_t launch_skinny2_forward(const uint16_t* x, int64_t m, int64_t k, const
                                   int64_t rank, float scale, const uint16_t* bias, uint16_t* y,
                                   uint16_t* h, float* ws, hipStream_t stream);
 int64_t skinny2_workspace_floats(int64_t m, int64_t n, int64_t k, int64_t rank);
+
+// Elementwise activation transform (ActMode in act.h) over count dense
+// elements: out = f(v, aux, aux2), out2 the second output of the SiLU-mul
+// backward. out may alias v.
+hipError_t launch_act(int mode, const uint16_t* v, const uint16_t* aux, const uint16_t* aux2,
+                      int64_t count, uint16_t* out, uint16_t* out2, hipStream_t stream);
 
 // Rank-r kernels --------------------------------------------------------------
 // out[M, r] = bf16(sum_k op(A[m, k]) * R[j, k]); op(a) = bf16(a * a_scale) when

@@ -182,6 +182,72 @@ def int4lora_backward(grad, x2d, packed, scale_bits, lora_a_c, lora_b_c, h, *, s
     return dx, d_a, d_b
 
 
+ACTIVATIONS = {"gelu": nat.ACT_GELU, "silu_mul": nat.ACT_SILU_MUL}
+
+
+def int4lora_forward_act(x2d, packed, scale_bits, lora_a_c, lora_b_c, *, activation: str,
+                         scaling: float, group_size: int | None = None, bias_bits=None,
+                         gate=None):
+    """The FFN's up projection with its activation fused into the GEMM's
+    epilogue: ``(y, z, h)`` with z the linear's output, y = gelu(z)
+    (``"gelu"``) or silu(gate) * z (``"silu_mul"``, gate [M, N])."""
+
+    act = ACTIVATIONS[activation]
+    device = _on_device(x2d, packed, scale_bits, lora_a_c, lora_b_c, bias_bits, gate)
+    m, k = x2d.shape
+    n = packed.shape[-2]
+    r = lora_a_c.shape[0]
+    dt = x2d.dtype
+    code = _dtype_code(dt)
+    x2d = x2d.contiguous()
+    a = lora_a_c.to(dt).contiguous()
+    b = lora_b_c.to(dt).contiguous()
+    gate = None if gate is None else gate.to(dt).contiguous()
+    y = torch.empty((m, n), dtype=dt, device=device)
+    z = torch.empty((m, n), dtype=dt, device=device)
+    h = torch.empty((m, r), dtype=dt, device=device)
+    g = group_arg(group_size, k)
+    ws = _workspace(nat.query("rpx_int4lora_forward_workspace", m, n, k, g, r, code), device)
+    bias = None if bias_bits is None else _u16(bias_bits).contiguous()
+    nat.call("rpx_int4lora_forward_act", _ptr(x2d), code, m, k, _ptr(packed.contiguous()),
+             _ptr(_u16(scale_bits).contiguous()), n, g, _ptr(bias), _ptr(a), _ptr(b), r,
+             float(scaling), act, _ptr(gate), _ptr(y), _ptr(z), _ptr(h), _ptr(ws), ws.numel(),
+             _stream(device))
+    return y, z, h
+
+
+def int4lora_backward_act(grad, x2d, packed, scale_bits, lora_a_c, lora_b_c, h, *,
+                          activation: str, z, gate=None, scaling: float,
+                          group_size: int | None = None):
+    """The FFN's down projection backward followed by the activation's:
+    ``(dz, dgate or None, dA f32, dB f32)``; x2d is the down projection's
+    input, z (and gate) the activation's forward operands."""
+
+    act = ACTIVATIONS[activation]
+    device = _on_device(grad, x2d, packed, scale_bits, lora_a_c, lora_b_c, h, z, gate)
+    m, k = x2d.shape
+    n = packed.shape[-2]
+    r = lora_a_c.shape[0]
+    dt = x2d.dtype
+    code = _dtype_code(dt)
+    grad = grad.to(dt).contiguous()
+    a = lora_a_c.to(dt).contiguous()
+    b = lora_b_c.to(dt).contiguous()
+    z = z.to(dt).contiguous()
+    gate = None if gate is None else gate.to(dt).contiguous()
+    dz = torch.empty((m, k), dtype=dt, device=device)
+    dgate = torch.empty((m, k), dtype=dt, device=device) if act == nat.ACT_SILU_MUL else None
+    d_a = torch.empty((r, k), dtype=F32, device=device)
+    d_b = torch.empty((n, r), dtype=F32, device=device)
+    g = group_arg(group_size, k)
+    ws = _workspace(nat.query("rpx_int4lora_backward_workspace", m, n, k, g, r, code), device)
+    nat.call("rpx_int4lora_backward_act", _ptr(grad), _ptr(x2d.contiguous()), code, m, k,
+             _ptr(packed.contiguous()), _ptr(_u16(scale_bits).contiguous()), n, g, _ptr(a),
+             _ptr(b), r, float(scaling), _ptr(h.contiguous()), act, _ptr(z), _ptr(gate),
+             _ptr(dz), _ptr(dgate), _ptr(d_a), _ptr(d_b), _ptr(ws), ws.numel(), _stream(device))
+    return dz, dgate, d_a, d_b
+
+
 class Int4LoRALinearFn(torch.autograd.Function):
     """Autograd node of the fused INT4 + LoRA linear on 2-D activations.
 
@@ -205,6 +271,86 @@ class Int4LoRALinearFn(torch.autograd.Function):
         dx, d_a, d_b = int4lora_backward(grad_y, x2d, packed, scale_bits, lora_a_c, lora_b_c, h,
                                          scaling=ctx.scaling, group_size=ctx.group_size)
         return (dx, d_a.to(lora_a_c.dtype), d_b.to(lora_b_c.dtype), None, None, None, None, None)
+
+
+class Int4LoRAGeluMLPFn(torch.autograd.Function):
+    """``down(gelu(up(x)))`` over two INT4 + LoRA linears with the GELU in
+    the up projection's GEMM epilogue and its backward in the down
+    projection's dx epilogue (bert/model.py:249).
+
+    Per linear: LoRA compute views (a, b), then packed, scale_bits,
+    bias_bits, scaling, group_size.
+    """
+
+    @staticmethod
+    def forward(ctx, x2d, up_a, up_b, down_a, down_b, up_packed, up_scales, up_bias, up_scaling,
+                up_group, down_packed, down_scales, down_bias, down_scaling, down_group):
+        act, z, h_up = int4lora_forward_act(x2d, up_packed, up_scales, up_a, up_b,
+                                            activation="gelu", scaling=up_scaling,
+                                            group_size=up_group, bias_bits=up_bias)
+        y, h_down = int4lora_forward(act, down_packed, down_scales, down_a, down_b,
+                                     scaling=down_scaling, group_size=down_group,
+                                     bias_bits=down_bias)
+        ctx.save_for_backward(x2d, up_a, up_b, down_a, down_b, up_packed, up_scales, down_packed,
+                              down_scales, z, act, h_up, h_down)
+        ctx.cfg = (up_scaling, up_group, down_scaling, down_group)
+        return y
+
+    @staticmethod
+    def backward(ctx, grad_y):
+        (x2d, up_a, up_b, down_a, down_b, up_packed, up_scales, down_packed, down_scales, z, act,
+         h_up, h_down) = ctx.saved_tensors
+        up_scaling, up_group, down_scaling, down_group = ctx.cfg
+        dz, _, d_down_a, d_down_b = int4lora_backward_act(
+            grad_y, act, down_packed, down_scales, down_a, down_b, h_down, activation="gelu",
+            z=z, scaling=down_scaling, group_size=down_group)
+        dx, d_up_a, d_up_b = int4lora_backward(dz, x2d, up_packed, up_scales, up_a, up_b, h_up,
+                                               scaling=up_scaling, group_size=up_group)
+        return (dx, d_up_a.to(up_a.dtype), d_up_b.to(up_b.dtype), d_down_a.to(down_a.dtype),
+                d_down_b.to(down_b.dtype)) + (None,) * 10
+
+
+class Int4LoRASwiGLUMLPFn(torch.autograd.Function):
+    """``down(silu(gate(x)) * up(x))`` over three INT4 + LoRA linears with
+    the gated product in the up projection's GEMM epilogue and its backward
+    (both the up and the gate gradients) in the down projection's dx
+    epilogue (qwen3_vl/text.py:202-203)."""
+
+    @staticmethod
+    def forward(ctx, x2d, gate_a, gate_b, up_a, up_b, down_a, down_b, gate_packed, gate_scales,
+                gate_bias, gate_scaling, gate_group, up_packed, up_scales, up_bias, up_scaling,
+                up_group, down_packed, down_scales, down_bias, down_scaling, down_group):
+        g, h_gate = int4lora_forward(x2d, gate_packed, gate_scales, gate_a, gate_b,
+                                     scaling=gate_scaling, group_size=gate_group,
+                                     bias_bits=gate_bias)
+        act, u, h_up = int4lora_forward_act(x2d, up_packed, up_scales, up_a, up_b,
+                                            activation="silu_mul", scaling=up_scaling,
+                                            group_size=up_group, bias_bits=up_bias, gate=g)
+        y, h_down = int4lora_forward(act, down_packed, down_scales, down_a, down_b,
+                                     scaling=down_scaling, group_size=down_group,
+                                     bias_bits=down_bias)
+        ctx.save_for_backward(x2d, gate_a, gate_b, up_a, up_b, down_a, down_b, gate_packed,
+                              gate_scales, up_packed, up_scales, down_packed, down_scales, g, u,
+                              act, h_gate, h_up, h_down)
+        ctx.cfg = (gate_scaling, gate_group, up_scaling, up_group, down_scaling, down_group)
+        return y
+
+    @staticmethod
+    def backward(ctx, grad_y):
+        (x2d, gate_a, gate_b, up_a, up_b, down_a, down_b, gate_packed, gate_scales, up_packed,
+         up_scales, down_packed, down_scales, g, u, act, h_gate, h_up, h_down) = ctx.saved_tensors
+        gate_scaling, gate_group, up_scaling, up_group, down_scaling, down_group = ctx.cfg
+        du, dg, d_down_a, d_down_b = int4lora_backward_act(
+            grad_y, act, down_packed, down_scales, down_a, down_b, h_down, activation="silu_mul",
+            z=u, gate=g, scaling=down_scaling, group_size=down_group)
+        dx_up, d_up_a, d_up_b = int4lora_backward(du, x2d, up_packed, up_scales, up_a, up_b, h_up,
+                                                  scaling=up_scaling, group_size=up_group)
+        dx_gate, d_gate_a, d_gate_b = int4lora_backward(dg, x2d, gate_packed, gate_scales, gate_a,
+                                                        gate_b, h_gate, scaling=gate_scaling,
+                                                        group_size=gate_group)
+        return (dx_up + dx_gate, d_gate_a.to(gate_a.dtype), d_gate_b.to(gate_b.dtype),
+                d_up_a.to(up_a.dtype), d_up_b.to(up_b.dtype), d_down_a.to(down_a.dtype),
+                d_down_b.to(down_b.dtype)) + (None,) * 15
 
 
 # ---------------------------------------------------------------------------

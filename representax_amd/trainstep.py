@@ -34,6 +34,7 @@ import torch.nn.functional as F
 from .adapters import apply_quantized_lora, lora_parameters
 from .components import Linear
 from .config import PrecisionConfig
+from .mlp import gelu_mlp, swiglu_mlp
 from .precision import precision_context, resolve_precision_policy
 
 
@@ -162,7 +163,8 @@ class BertMLP(torch.nn.Module):
         self.output = Linear.init(config.intermediate_size, config.hidden_size, key=key + 1, **arg)
 
     def forward(self, hidden: torch.Tensor) -> torch.Tensor:
-        return self.output(F.gelu(self.input(hidden)))
+        # output(gelu(input(hidden))), fused when both are INT4 + LoRA
+        return gelu_mlp(hidden, self.input, self.output)
 
 
 class BertLayer(torch.nn.Module):
@@ -366,7 +368,8 @@ class Qwen3MLP(torch.nn.Module):
         self.down = Linear.init(f, h, key=key + 2, **arg)
 
     def forward(self, hidden):
-        return self.down(F.silu(self.gate(hidden)) * self.up(hidden))
+        # down(silu(gate(hidden)) * up(hidden)), fused when all are INT4 + LoRA
+        return swiglu_mlp(hidden, self.gate, self.up, self.down)
 
 
 class Qwen3Layer(torch.nn.Module):

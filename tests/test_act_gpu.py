@@ -1,0 +1,201 @@
+"""Activation epilogues (GELU, SiLU-gated product) fused into the INT4 + LoRA
+GEMMs, and the fused FFN blocks, against the oracle (GPU)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import DEVICE, bf16_values, bits_from_dev, from_dev, rel_l2, rng, to_dev, to_dev_bf16
+from oracle import act as oact
+from oracle import int4 as oint4
+from oracle import lora as olora
+from oracle.codecs import f32_to_bf16_bits
+from representax_amd import ops
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-2
+
+
+def _ulp_diff(a_bits: np.ndarray, b_bits: np.ndarray) -> np.ndarray:
+    """Distance in bf16 units in the last place (same-sign finite values)."""
+
+    def ordered(u):
+        u = u.astype(np.int32)
+        return np.where(u & 0x8000, 0x8000 - (u & 0x7FFF), 0x8000 + u)
+
+    return np.abs(ordered(a_bits) - ordered(b_bits))
+
+
+TINY = 1e-30  # below it f32 intermediates are subnormal; results only need to stay tiny
+
+
+def _assert_act_bits(got_bits: np.ndarray, want_f32: np.ndarray):
+    """The activation is evaluated in f32 on the GPU (an erfc fit with
+    fractional error < 1.2e-7, the hardware exp2 and reciprocal) and exactly
+    in the oracle: identical bits except where the exact value sits within a
+    few f32 ulps of a bf16 rounding boundary, and then one bf16 ulp. Results
+    below 1e-30 in magnitude (f32 subnormal intermediates) must stay below it."""
+
+    got_bits = got_bits.reshape(-1)
+    want = np.asarray(want_f32, np.float32).reshape(-1)
+    want_bits = f32_to_bf16_bits(want)
+    got = (got_bits.astype(np.uint32) << 16).view(np.float32)
+    tiny = np.abs(want) < TINY
+    assert np.all(np.abs(got[tiny]) < TINY)
+    d = _ulp_diff(got_bits[~tiny], want_bits[~tiny])
+    if d.size:
+        i = int(np.argmax(d))
+        assert d[i] <= 1, (d[i], float(got[~tiny][i]), float(want[~tiny][i]))
+        assert np.mean(d > 0) < 1e-2
+
+
+def _linear(g, n, k, r, group, bias, b_scale=1.0):
+    w = (g.standard_normal((n, k)) * 0.02).astype(np.float32)
+    packed, scales = oint4.pack_int4(w, group)
+    a = (g.standard_normal((r, k)) * 0.05).astype(np.float32)
+    b = (g.standard_normal((n, r)) * 0.05 * b_scale).astype(np.float32)
+    bias_bits = f32_to_bf16_bits((g.standard_normal(n) * 0.5).astype(np.float32)) if bias else None
+    return dict(packed=packed, scale_bits=scales, lora_a=a, lora_b=b, alpha=2.0 * r, rank=r,
+                bias_bits=bias_bits, group_size=group)
+
+
+def _dev(p):
+    return dict(packed=to_dev(p["packed"]),
+                scale_bits=to_dev(p["scale_bits"].view(np.int16)).view(torch.uint16),
+                a=to_dev_bf16(p["lora_a"]), b=to_dev_bf16(p["lora_b"]),
+                bias=None if p["bias_bits"] is None
+                else to_dev(p["bias_bits"].view(np.int16)).view(torch.uint16),
+                scaling=float(p["alpha"] / p["rank"]), group=p["group_size"])
+
+
+# (m, k, n, r, group): the fused GEMM path, a ragged tile, the skinny path
+# (elementwise activation after the skinny kernels) and the generic path
+SHAPES = [(512, 256, 384, 16, 64), (300, 128, 200, 8, None), (8, 256, 192, 16, 64),
+          (37, 100, 52, 3, None)]
+
+
+@pytest.mark.parametrize("activation", ["gelu", "silu_mul"])
+@pytest.mark.parametrize("m,k,n,r,group", SHAPES)
+def test_forward_act_matches_oracle(activation, m, k, n, r, group):
+    g = rng(m + n + (7 if activation == "gelu" else 9))
+    p = _linear(g, n, k, r, group, bias=True, b_scale=20.0)
+    x = bf16_values(g.standard_normal((m, k)))
+    gate = bf16_values(g.standard_normal((m, n)) * 2.0)
+    d = _dev(p)
+    y, z, h = ops.int4lora_forward_act(
+        to_dev_bf16(x), d["packed"], d["scale_bits"], d["a"], d["b"], activation=activation,
+        scaling=d["scaling"], group_size=group, bias_bits=d["bias"],
+        gate=to_dev_bf16(gate) if activation == "silu_mul" else None)
+    torch.cuda.synchronize()
+    z_o, h_o = olora.lora_forward(x, p["packed"], p["scale_bits"], p["lora_a"], p["lora_b"],
+                                  alpha=p["alpha"], rank=r, bias_bits=p["bias_bits"],
+                                  group_size=group)
+    assert rel_l2(from_dev(z), z_o) < TOL
+    assert rel_l2(from_dev(h), h_o) < TOL
+    # the activation of the GPU's own z, rounded once
+    zg = from_dev(z)
+    want = oact.act_forward(activation, zg, gate if activation == "silu_mul" else None)
+    _assert_act_bits(bits_from_dev(y), want)
+    # z equals the plain forward's y bit for bit
+    y_plain, _ = ops.int4lora_forward(to_dev_bf16(x), d["packed"], d["scale_bits"], d["a"], d["b"],
+                                      scaling=d["scaling"], group_size=group, bias_bits=d["bias"])
+    torch.cuda.synchronize()
+    assert torch.equal(y_plain, z)
+
+
+# (m, k, n, r, group) of the down projection: k is the activation width
+BWD_SHAPES = [(512, 384, 256, 16, 64), (300, 192, 128, 8, None), (8, 256, 192, 16, 64),
+              (37, 100, 52, 3, None)]
+
+
+@pytest.mark.parametrize("activation", ["gelu", "silu_mul"])
+@pytest.mark.parametrize("m,k,n,r,group", BWD_SHAPES)
+def test_backward_act_matches_oracle(activation, m, k, n, r, group):
+    g = rng(m + k + (11 if activation == "gelu" else 13))
+    p = _linear(g, n, k, r, group, bias=False)
+    x = bf16_values(g.standard_normal((m, k)))  # the activation output
+    z = bf16_values(g.standard_normal((m, k)) * 2.0)
+    gate = bf16_values(g.standard_normal((m, k)) * 2.0)
+    gy = bf16_values(g.standard_normal((m, n)))
+    d = _dev(p)
+    xd, gyd = to_dev_bf16(x), to_dev_bf16(gy)
+    _, h = ops.int4lora_forward(xd, d["packed"], d["scale_bits"], d["a"], d["b"],
+                                scaling=d["scaling"], group_size=group)
+    dz, dgate, d_a, d_b = ops.int4lora_backward_act(
+        gyd, xd, d["packed"], d["scale_bits"], d["a"], d["b"], h, activation=activation,
+        z=to_dev_bf16(z), gate=to_dev_bf16(gate) if activation == "silu_mul" else None,
+        scaling=d["scaling"], group_size=group)
+    dx, d_a2, d_b2 = ops.int4lora_backward(gyd, xd, d["packed"], d["scale_bits"], d["a"], d["b"],
+                                           h, scaling=d["scaling"], group_size=group)
+    torch.cuda.synchronize()
+    # the LoRA gradients are the plain backward's
+    assert torch.equal(d_a, d_a2) and torch.equal(d_b, d_b2)
+    # the activation's backward of the GPU's own (rounded) input gradient
+    dxg = from_dev(dx)
+    want_dz, want_dg = oact.act_backward(activation, dxg, z,
+                                         gate if activation == "silu_mul" else None)
+    _assert_act_bits(bits_from_dev(dz), want_dz)
+    if activation == "silu_mul":
+        _assert_act_bits(bits_from_dev(dgate), want_dg)
+    else:
+        assert dgate is None
+    # and the input gradient itself against the oracle
+    dx_o, _, _ = olora.lora_backward(gy, x, p["packed"], p["scale_bits"], p["lora_a"],
+                                     p["lora_b"], from_dev(h), alpha=p["alpha"], rank=r,
+                                     group_size=group)
+    assert rel_l2(dxg, dx_o) < TOL
+
+
+def _mlp_params(g, k, f, r, group, names):
+    return {nm: _linear(g, f if nm != "down" else k, k if nm != "down" else f, r, group,
+                        bias=nm != "gate", b_scale=10.0) for nm in names}
+
+
+@pytest.mark.parametrize("m,k,f,r,group", [(256, 128, 512, 8, 64), (40, 128, 256, 4, None)])
+def test_gelu_mlp_forward_backward_matches_oracle(m, k, f, r, group):
+    g = rng(m + f)
+    ps = _mlp_params(g, k, f, r, group, ["up", "down"])
+    x = bf16_values(g.standard_normal((m, k)))
+    gy = bf16_values(g.standard_normal((m, k)))
+    up, down = _dev(ps["up"]), _dev(ps["down"])
+    xd = to_dev_bf16(x).requires_grad_(True)
+    views = [up["a"].clone().requires_grad_(True), up["b"].clone().requires_grad_(True),
+             down["a"].clone().requires_grad_(True), down["b"].clone().requires_grad_(True)]
+    y = ops.Int4LoRAGeluMLPFn.apply(
+        xd, *views, up["packed"], up["scale_bits"], up["bias"], up["scaling"], up["group"],
+        down["packed"], down["scale_bits"], down["bias"], down["scaling"], down["group"])
+    grads = torch.autograd.grad(y, [xd] + views, to_dev_bf16(gy))
+    torch.cuda.synchronize()
+    y_o, z_o, act_o, h_up, h_down = oact.gelu_mlp_forward(x, ps["up"], ps["down"])
+    want = oact.gelu_mlp_backward(gy, x, ps["up"], ps["down"], z_o, act_o, h_up, h_down)
+    assert rel_l2(from_dev(y), y_o) < TOL
+    for got, exp in zip(grads, want):
+        assert rel_l2(from_dev(got.float()), exp) < 2 * TOL
+
+
+@pytest.mark.parametrize("m,k,f,r,group", [(256, 128, 512, 8, 64), (40, 128, 256, 4, None)])
+def test_swiglu_mlp_forward_backward_matches_oracle(m, k, f, r, group):
+    g = rng(m + f + 1)
+    ps = _mlp_params(g, k, f, r, group, ["gate", "up", "down"])
+    x = bf16_values(g.standard_normal((m, k)))
+    gy = bf16_values(g.standard_normal((m, k)))
+    dv = {nm: _dev(ps[nm]) for nm in ("gate", "up", "down")}
+    xd = to_dev_bf16(x).requires_grad_(True)
+    views = []
+    for nm in ("gate", "up", "down"):
+        views += [dv[nm]["a"].clone().requires_grad_(True), dv[nm]["b"].clone().requires_grad_(True)]
+    leaves = []
+    for nm in ("gate", "up", "down"):
+        leaves += [dv[nm]["packed"], dv[nm]["scale_bits"], dv[nm]["bias"], dv[nm]["scaling"],
+                   dv[nm]["group"]]
+    y = ops.Int4LoRASwiGLUMLPFn.apply(xd, *views, *leaves)
+    grads = torch.autograd.grad(y, [xd] + views, to_dev_bf16(gy))
+    torch.cuda.synchronize()
+    out = oact.swiglu_mlp_forward(x, ps["gate"], ps["up"], ps["down"])
+    want = oact.swiglu_mlp_backward(gy, x, ps["gate"], ps["up"], ps["down"], *out[1:])
+    assert rel_l2(from_dev(y), out[0]) < TOL
+    for got, exp in zip(grads, want):
+        assert rel_l2(from_dev(got.float()), exp) < 2 * TOL

@@ -68,6 +68,21 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     with pytest.raises(ValueError, match="history row"):
         nat.call("rpx_fp8_scale_update", p, p, p, p, p, 3, 0, None)
     assert nat.query("rpx_fp8_delayed_pending_words") >= 64
+    with pytest.raises(ValueError, match="unknown activation"):
+        nat.call("rpx_int4lora_forward_act", p, nat.DTYPE_BF16, 2, 8, p, p, 6, 0, None, p, p, 2,
+                 ctypes.c_float(1.0), 9, None, p, p, p, None, 0, None)
+    with pytest.raises(ValueError, match="bf16"):
+        nat.call("rpx_int4lora_forward_act", p, nat.DTYPE_F32, 2, 8, p, p, 6, 0, None, p, p, 2,
+                 ctypes.c_float(1.0), nat.ACT_GELU, None, p, p, p, None, 0, None)
+    with pytest.raises(ValueError, match="null pointer"):
+        nat.call("rpx_int4lora_forward_act", p, nat.DTYPE_BF16, 2, 8, p, p, 6, 0, None, p, p, 2,
+                 ctypes.c_float(1.0), nat.ACT_SILU_MUL, None, p, p, p, None, 0, None)
+    with pytest.raises(ValueError, match="null pointer"):
+        nat.call("rpx_int4lora_backward_act", p, p, nat.DTYPE_BF16, 2, 8, p, p, 6, 0, p, p, 2,
+                 ctypes.c_float(1.0), p, nat.ACT_SILU_MUL, p, p, p, None, p, p, None, 0, None)
+    with pytest.raises(ValueError, match="rank"):
+        nat.call("rpx_int4lora_backward_act", p, p, nat.DTYPE_BF16, 2, 8, p, p, 6, 0, p, p, 7,
+                 ctypes.c_float(1.0), p, nat.ACT_GELU, p, None, p, None, p, p, None, 0, None)
 
 
 def _host_quantize(x: np.ndarray, scale: float, fmt: int) -> np.ndarray:
