@@ -739,10 +739,18 @@ hipError_t dispatch_bf16(const uint16_t* a, int64_t lda, const uint16_t* b, int6
   if (cfg == 8)
     return run_gemm<256, 256, 2, 2, 2, 1, false>(a, lda, b, ldb, none, m, n, k, out, ldc, epi,
                                                  stream);
-  if (cfg < 4 || cfg > 6) {
+  if (cfg < 4 || (cfg > 6 && cfg != 9)) {
+    // 128 x 96 tiles when they make one balanced round of 192-256 workgroups
+    // where 128 x 128 would leave CUs idle (measured on 4096 x 768 outputs:
+    // 31 us against 33 us for two uneven rounds of 64 x 128)
+    const int64_t t128 = ceil_div(m, 128) * ceil_div(n, 128);
+    const int64_t t96 = ceil_div(m, 128) * ceil_div(n, 96);
     cfg = ceil_div(m, 256) * ceil_div(n, 128) >= 256 ? 4
-          : (ceil_div(m, 128) * ceil_div(n, 128) >= 256 ? 5 : 6);
+          : (t128 >= 256 ? 5 : (t96 >= 192 && t96 <= 256 ? 9 : 6));
   }
+  if (cfg == 9)
+    return run_gemm<128, 96, 4, 1, 3, 1, false>(a, lda, b, ldb, none, m, n, k, out, ldc, epi,
+                                                stream);
   if (cfg == 4)
     return run_gemm<256, 128, 4, 2, 2, 2, false>(a, lda, b, ldb, none, m, n, k, out, ldc, epi,
                                                  stream);
