@@ -439,14 +439,11 @@ __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_
     }
   }
 
-  // Stores one [BM, BN] tile of bf16 pairs (this lane's share in vals) at
-  // dst with row stride ldc: staged in LDS and written as whole row segments
-  // when the tile fits the pipeline's LDS, else 8-byte stores per lane.
   constexpr int P = BN * 2 + 16;  // LDS row pitch of the staged tile
-  auto store_tile = [&](uint16_t* dst_base, const uint32_t (&vals)[FN][FM][8]) {
-    const bool vec_out = (ldc & 7) == 0 && (reinterpret_cast<uintptr_t>(dst_base) & 15) == 0;
+  if constexpr (ACT == kActNone) {
+    const bool vec_out = (ldc & 7) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0;
     if constexpr (BM * P <= NS * STAGE) {
-      wait_sync<0>();  // every wave is done reading the stages (or the last tile)
+      wait_sync<0>();  // every wave is done reading the pipeline stages
 #pragma unroll
       for (int fn = 0; fn < FN; ++fn)
 #pragma unroll
@@ -456,7 +453,7 @@ __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_
             const int ml = wm * TM + fm * 32 + frow;
             const int nl = wn * TN + fn * 32 + 8 * vg + 4 * half;
             *reinterpret_cast<u32x2_t*>(smem + ml * P + nl * 2) =
-                u32x2_t{vals[fn][fm][2 * vg], vals[fn][fm][2 * vg + 1]};
+                u32x2_t{ypk[fn][fm][2 * vg], ypk[fn][fm][2 * vg + 1]};
           }
       __syncthreads();
       constexpr int CPR = BN / 8;  // 16-byte chunks per tile row
@@ -472,8 +469,7 @@ __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_
 #pragma unroll
         for (int it = 0; it < ITS; ++it) {
           const int idx = it * NT + tid;
-          *reinterpret_cast<u32x4_t*>(dst_base + (m0 + idx / CPR) * ldc + n0 + 8 * (idx % CPR)) =
-              v[it];
+          *reinterpret_cast<u32x4_t*>(out + (m0 + idx / CPR) * ldc + n0 + 8 * (idx % CPR)) = v[it];
         }
         return;
       }
@@ -482,9 +478,8 @@ __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_
         const int64_t m = m0 + idx / CPR;
         const int64_t n = n0 + 8 * (idx % CPR);
         if (m >= M || n >= N) continue;
-        const u32x4_t v =
-            *reinterpret_cast<const u32x4_t*>(smem + (idx / CPR) * P + (idx % CPR) * 16);
-        uint16_t* d = dst_base + m * ldc + n;
+        const u32x4_t v = *reinterpret_cast<const u32x4_t*>(smem + (idx / CPR) * P + (idx % CPR) * 16);
+        uint16_t* d = out + m * ldc + n;
         if (vec_out && n + 7 < N) {
           *reinterpret_cast<u32x4_t*>(d) = v;
         } else {
@@ -503,23 +498,18 @@ __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_
 #pragma unroll
           for (int vg = 0; vg < 4; ++vg) {
             const int64_t nb = nw + fn * 32 + 8 * vg + 4 * half;
-            uint16_t* dst = dst_base + m * ldc + nb;
+            uint16_t* dst = out + m * ldc + nb;
             if (vec_out && nb + 3 < N) {
-              *reinterpret_cast<u32x2_t*>(dst) = u32x2_t{vals[fn][fm][2 * vg], vals[fn][fm][2 * vg + 1]};
+              *reinterpret_cast<u32x2_t*>(dst) = u32x2_t{ypk[fn][fm][2 * vg], ypk[fn][fm][2 * vg + 1]};
             } else {
 #pragma unroll
               for (int e = 0; e < 4; ++e)
                 if (nb + e < N)
-                  dst[e] = static_cast<uint16_t>((vals[fn][fm][2 * vg + e / 2] >> (16 * (e & 1))) &
-                                                 0xFFFFu);
+                  dst[e] = static_cast<uint16_t>((ypk[fn][fm][2 * vg + e / 2] >> (16 * (e & 1))) & 0xFFFFu);
             }
           }
         }
     }
-  };
-
-  if constexpr (ACT == kActNone) {
-    store_tile(out, ypk);
   } else {
     // Activation epilogue on the rounded outputs v: f32 from bf16 operands,
     // rounded once (act.h). The tile of v is staged in LDS and every thread

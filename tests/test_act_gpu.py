@@ -74,7 +74,7 @@ def _dev(p):
 # (m, k, n, r, group): the fused GEMM path, a ragged tile, the skinny path
 # (elementwise activation after the skinny kernels) and the generic path
 SHAPES = [(512, 256, 384, 16, 64), (300, 128, 200, 8, None), (8, 256, 192, 16, 64),
-          (37, 100, 52, 3, None)]
+          (37, 100, 52, 3, None), (256, 128, 256, 48, 64)]
 
 
 @pytest.mark.parametrize("activation", ["gelu", "silu_mul"])
@@ -108,7 +108,7 @@ def test_forward_act_matches_oracle(activation, m, k, n, r, group):
 
 # (m, k, n, r, group) of the down projection: k is the activation width
 BWD_SHAPES = [(512, 384, 256, 16, 64), (300, 192, 128, 8, None), (8, 256, 192, 16, 64),
-              (37, 100, 52, 3, None)]
+              (37, 100, 52, 3, None), (256, 256, 128, 48, 64)]
 
 
 @pytest.mark.parametrize("activation", ["gelu", "silu_mul"])
