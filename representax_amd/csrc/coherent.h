@@ -1,0 +1,50 @@
+// Block-to-block hand-off inside one launch: arrival counters and
+// device-coherent stores and loads of partial results.
+#pragma once
+
+#include "common.h"
+
+namespace rpx {
+
+// One arrival; true for the last of `target`, which puts the word back to 0.
+__device__ __forceinline__ bool arrive(unsigned int* word, unsigned int target) {
+  const unsigned int old = __hip_atomic_fetch_add(word, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (old + 1u != target) return false;
+  __hip_atomic_store(word, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return true;
+}
+
+// Partial sums cross blocks through agent-scope (device-coherent) 64-bit
+// stores and loads instead of plain accesses plus a release/acquire fence
+// pair: on this target an agent-scope release fence writes back the whole
+// L2 of the XCD, which at one fence per block costs more than the weight
+// stream itself. A coherent store has reached the coherence point once the
+// wave's vmcnt drains (drain_stores), before the block's arrival is counted.
+__device__ __forceinline__ void store_coherent(f32x4_t* dst, f32x4_t v) {
+  unsigned long long* d = reinterpret_cast<unsigned long long*>(dst);
+  const u32x4_t u = __builtin_bit_cast(u32x4_t, v);
+  __hip_atomic_store(d, static_cast<unsigned long long>(u[0]) | (static_cast<unsigned long long>(u[1]) << 32),
+                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(d + 1, static_cast<unsigned long long>(u[2]) | (static_cast<unsigned long long>(u[3]) << 32),
+                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ f32x4_t load_coherent(const f32x4_t* src) {
+  unsigned long long* s = reinterpret_cast<unsigned long long*>(const_cast<f32x4_t*>(src));
+  const unsigned long long a = __hip_atomic_load(s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const unsigned long long b = __hip_atomic_load(s + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return __builtin_bit_cast(f32x4_t, u32x4_t{static_cast<uint32_t>(a), static_cast<uint32_t>(a >> 32),
+                                             static_cast<uint32_t>(b), static_cast<uint32_t>(b >> 32)});
+}
+__device__ __forceinline__ void drain_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// 32-bit coherent store and load (single values, flags).
+__device__ __forceinline__ void store_coherent_f32(float* dst, float v) {
+  __hip_atomic_store(reinterpret_cast<unsigned int*>(dst), __builtin_bit_cast(unsigned int, v),
+                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_coherent_f32(const float* src) {
+  return __builtin_bit_cast(float, __hip_atomic_load(reinterpret_cast<unsigned int*>(const_cast<float*>(src)),
+                                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+}
+
+}  // namespace rpx

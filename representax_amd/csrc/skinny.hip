@@ -22,6 +22,7 @@
 #include <atomic>
 #include <cstdlib>
 
+#include "coherent.h"
 #include "common.h"
 #include "kernels.h"
 
@@ -81,40 +82,9 @@ __device__ __forceinline__ void dequant8_exact(uint32_t word, float s, float m8s
 // They are zero when the module loads and every call leaves its slot at zero.
 __device__ unsigned int g_skinny_counters[kSlots][kMaxTiles + 2];
 
-// One arrival; true for the last of `target`, which puts the word back to 0.
-__device__ __forceinline__ bool arrive(unsigned int* word, unsigned int target) {
-  const unsigned int old = __hip_atomic_fetch_add(word, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  if (old + 1u != target) return false;
-  __hip_atomic_store(word, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  return true;
-}
-
 __device__ __forceinline__ u32x4_t load16(const void* p) {
   return *reinterpret_cast<const u32x4_t*>(p);
 }
-
-// Partial sums cross blocks through agent-scope (device-coherent) 64-bit
-// stores and loads instead of plain accesses plus a release/acquire fence
-// pair: on this target an agent-scope release fence writes back the whole
-// L2 of the XCD, which at one fence per block costs more than the weight
-// stream itself. A coherent store has reached the coherence point once the
-// wave's vmcnt drains (drain_stores), before the block's arrival is counted.
-__device__ __forceinline__ void store_coherent(f32x4_t* dst, f32x4_t v) {
-  unsigned long long* d = reinterpret_cast<unsigned long long*>(dst);
-  const u32x4_t u = __builtin_bit_cast(u32x4_t, v);
-  __hip_atomic_store(d, static_cast<unsigned long long>(u[0]) | (static_cast<unsigned long long>(u[1]) << 32),
-                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  __hip_atomic_store(d + 1, static_cast<unsigned long long>(u[2]) | (static_cast<unsigned long long>(u[3]) << 32),
-                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ f32x4_t load_coherent(const f32x4_t* src) {
-  unsigned long long* s = reinterpret_cast<unsigned long long*>(const_cast<f32x4_t*>(src));
-  const unsigned long long a = __hip_atomic_load(s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  const unsigned long long b = __hip_atomic_load(s + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  return __builtin_bit_cast(f32x4_t, u32x4_t{static_cast<uint32_t>(a), static_cast<uint32_t>(a >> 32),
-                                             static_cast<uint32_t>(b), static_cast<uint32_t>(b >> 32)});
-}
-__device__ __forceinline__ void drain_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // x fragment for MFMA column m, columns [k, k + 8); zero past the last row.
 __device__ __forceinline__ u32x4_t x_frag(const SkinnyParams& p, int m, int64_t k) {

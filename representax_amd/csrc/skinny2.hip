@@ -1,7 +1,8 @@
-// Skinny-M INT4 + LoRA forward for M <= 16 tokens (selected for M <= 4) in
-// two launches with no cross-block exchange inside either (the memory-bound
-// embedding-inference regime, where a call is a few dependent device round
-// trips).
+// Skinny-M INT4 + LoRA forward for M <= 16 tokens (selected for M <= 4), the
+// memory-bound embedding-inference regime, where a call is a few dependent
+// device round trips. Two forms: two launches with no cross-block exchange
+// inside either (below), and one launch in which the adapter's h is
+// published to the weight blocks (k_skinny_one, further down), chosen by K.
 //
 //   k_skinny_main, one grid with two block roles:
 //     adapter blocks (first in the grid, so they dispatch first): block
@@ -27,8 +28,10 @@
 // 16-byte load of 32 nibbles, and MFMA step s uses k = 32 (l >> 4) + 8 s +
 // [0, 8), the same permutation on both operands. The lane then holds
 // D[row 4 (l >> 4) + v][column m = l & 15].
+#include <atomic>
 #include <cstdlib>
 
+#include "coherent.h"
 #include "common.h"
 #include "kernels.h"
 
@@ -63,6 +66,12 @@ struct Skinny2Params {
   int slices;            // adapter K slices of 128 * NW columns
   int a_blocks;          // slices * ceil(rank / 16)
   int b_vec;             // B rows may be touched with 16-byte loads
+  // one-launch form: the call's slot of arrival words ([0] adapter blocks,
+  // [1] h published, [2] weight blocks; zero between calls) and the
+  // published h as f32 [M, rank]
+  int slot;
+  float* hf;
+  int w_blocks;
 };
 
 __device__ __forceinline__ u32x4_t ld16(const void* p) {
@@ -281,6 +290,234 @@ __global__ void __launch_bounds__(kFinThreads) k_skinny_finish(Skinny2Params p) 
   }
 }
 
+// ---------------------------------------------------------------------------
+// One-launch form (k_skinny_one): the same two block roles, but the last
+// adapter block to arrive sums the partials into h and publishes it
+// (device-coherent stores, then a flag), and every weight block applies the
+// LoRA term to its own rows after a bounded wait for the flag, so the
+// finishing launch and its dispatch disappear. Adapter blocks come first in
+// the grid and wait on nothing, so the wait ends once they have run; the
+// spin limit only guarantees that every wave exits (h then reads as NaN).
+// Slots are taken in turn and left at zero by every call: at most kSlots
+// calls may run at once on a device.
+
+constexpr int kSlots2 = 8;
+constexpr int kSpin2 = 1 << 22;
+__device__ unsigned int g_skinny2_state[kSlots2][4];
+
+template <int NW>
+__device__ __forceinline__ void adapter_block_one(const Skinny2Params& p, int a, f32x4_v* red,
+                                                  int* last_sh) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int rl = lane & 15;
+  const int g = lane >> 4;
+  const int groups = (p.rank + 15) / 16;
+  const int q = a % groups;
+  const int s = a / groups;
+  const int j = 16 * q + rl;
+  const bool jok = j < p.rank;
+  const uint16_t* arow = p.lora_a + static_cast<int64_t>(jok ? j : p.rank - 1) * p.k;
+  const int64_t c = static_cast<int64_t>(s) * NW + wave;
+  const bool ok = c < p.k / 128;
+  const int64_t k0 = ok ? c * 128 + 32 * g : 0;
+  u32x4_t av[4], xv[4];
+#pragma unroll
+  for (int st = 0; st < 4; ++st) {
+    av[st] = ok && jok ? ld16(arow + k0 + 8 * st) : u32x4_t{0u, 0u, 0u, 0u};
+    xv[st] = x_frag(p, rl, k0 + 8 * st, ok);
+  }
+  f32x4_v acc{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int st = 0; st < 4; ++st) acc = mfma16(av[st], xv[st], acc);
+  acc = reduce_waves<NW>(acc, red);
+  if (wave == 0 && rl < p.m) {
+    // lane: P[s][m = rl][j = 16 q + 4 g + v]
+    float* dst = p.part + (static_cast<int64_t>(s) * p.m + rl) * p.rank;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int jj = 16 * q + 4 * g + v;
+      if (jj < p.rank) store_coherent_f32(dst + jj, acc[v]);
+    }
+  }
+  drain_stores();
+  __syncthreads();
+  unsigned int* state = g_skinny2_state[p.slot];
+  if (threadIdx.x == 0) *last_sh = arrive(state, static_cast<unsigned int>(p.a_blocks)) ? 1 : 0;
+  __syncthreads();
+  if (*last_sh == 0) return;
+  // the last adapter block: h = bf16(sum over slices in slice order)
+  const int mr = p.m * p.rank;
+  for (int e = threadIdx.x; e < mr; e += 64 * NW) {
+    float sum = 0.0f;
+    for (int sl = 0; sl < p.slices; ++sl) sum += load_coherent_f32(p.part + static_cast<int64_t>(sl) * mr + e);
+    const float hv = round_bf16(sum);
+    store_coherent_f32(p.hf + e, hv);
+    p.h[e] = f32_to_bf16(hv);
+  }
+  drain_stores();
+  __syncthreads();
+  if (threadIdx.x == 0) __hip_atomic_store(state + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int NW, int CPW>
+__device__ __forceinline__ void weight_block_one(const Skinny2Params& p, int64_t b, f32x4_v* red) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int rl = lane & 15;
+  const int g = lane >> 4;
+  const int64_t n0 = 16 * b;
+  const int64_t row = n0 + rl;
+  const int64_t rc = row < p.n ? row : p.n - 1;
+  const uint8_t* wrow = p.packed + rc * p.pcols;
+  const uint16_t* srow = p.scales + rc * p.n_groups;
+  const int64_t nchunks = p.k / 128;
+  u32x4_t wv[CPW], xv[CPW][4];
+  uint16_t sv[CPW];
+#pragma unroll
+  for (int i = 0; i < CPW; ++i) {
+    const int64_t c = wave + static_cast<int64_t>(i) * NW;
+    const bool ok = c < nchunks;
+    const int64_t k0 = ok ? c * 128 + 32 * g : 0;
+    wv[i] = ok ? ld16(wrow + k0 / 2) : u32x4_t{0u, 0u, 0u, 0u};
+    sv[i] = srow[p.n_groups == 1 ? 0 : (k0 >> p.group_shift)];
+#pragma unroll
+    for (int st = 0; st < 4; ++st) xv[i][st] = x_frag(p, rl, k0 + 8 * st, ok);
+  }
+  // wave 0 also loads its rows of B as MFMA row fragments (rank <= 64: two
+  // 32-rank steps, j = 32 q + 8 g + [0, 8)) and its 4 bias values
+  u32x4_t bfr[2] = {u32x4_t{0u, 0u, 0u, 0u}, u32x4_t{0u, 0u, 0u, 0u}};
+  float bias4[4] = {0.f, 0.f, 0.f, 0.f};
+  if (wave == 0) {
+    const uint16_t* brow = p.lora_b + rc * p.rank;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int j0 = 32 * q + 8 * g;
+      if (j0 >= p.rank) continue;
+      if (p.b_vec && j0 + 8 <= p.rank) {
+        bfr[q] = ld16(brow + j0);
+      } else {
+        uint32_t w4[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t lo = j0 + 2 * e < p.rank ? brow[j0 + 2 * e] : 0u;
+          const uint32_t hi = j0 + 2 * e + 1 < p.rank ? brow[j0 + 2 * e + 1] : 0u;
+          w4[e] = lo | (hi << 16);
+        }
+        bfr[q] = u32x4_t{w4[0], w4[1], w4[2], w4[3]};
+      }
+    }
+    if (p.bias != nullptr) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int64_t nn = n0 + 4 * g + v;
+        bias4[v] = nn < p.n ? bf16_to_f32(p.bias[nn]) : 0.0f;
+      }
+    }
+  }
+  f32x4_v acc{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < CPW; ++i) {
+    const float s = bf16_to_f32(sv[i]);
+#pragma unroll
+    for (int st = 0; st < 4; ++st) acc = mfma16(dequant8(wv[i][st], s), xv[i][st], acc);
+  }
+  acc = reduce_waves<NW>(acc, red);
+  if (wave != 0) return;
+
+  // wait (lane 0, bounded) for the published h, then read it as MFMA
+  // column fragments: lane (m = rl, g) takes h[m][32 q + 8 g + e]
+  unsigned int* state = g_skinny2_state[p.slot];
+  int ready = 1;
+  if (lane == 0) {
+    ready = 0;
+    for (int it = 0; it < kSpin2; ++it) {
+      if (__hip_atomic_load(state + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u) {
+        ready = 1;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+  }
+  ready = __shfl(ready, 0, 64);
+  // the h loads below must not be issued before the flag was seen
+  asm volatile("" ::: "memory");
+  f32x4_v t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    if (32 * q >= p.rank) break;
+    float hv[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int jj = 32 * q + 8 * g + e;
+      hv[e] = (rl < p.m && jj < p.rank) ? load_coherent_f32(p.hf + rl * p.rank + jj) : 0.0f;
+      if (!ready) hv[e] = __builtin_nanf("");
+    }
+    const u32x4_t hfr{pack_bf16x2(hv[0], hv[1]), pack_bf16x2(hv[2], hv[3]), pack_bf16x2(hv[4], hv[5]),
+                      pack_bf16x2(hv[6], hv[7])};
+    t = mfma16(bfr[q], hfr, t);
+  }
+  // the last weight block to get here returns the h flag to zero
+  if (lane == 0 && arrive(state + 2, static_cast<unsigned int>(p.w_blocks)))
+    __hip_atomic_store(state + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (rl >= p.m) return;
+  // lane: y[m = rl][n = n0 + 4 g + v]
+  uint16_t o[4];
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    float r = round_bf16(acc[v]);
+    r = round_bf16(r + round_bf16(round_bf16(t[v]) * p.scale));
+    if (p.bias != nullptr) r = round_bf16(r + bias4[v]);
+    o[v] = f32_to_bf16(r);
+  }
+  const int64_t nb = n0 + 4 * g;
+  uint16_t* dst = p.y + static_cast<int64_t>(rl) * p.n + nb;
+  if (nb + 3 < p.n && (reinterpret_cast<uintptr_t>(dst) & 7) == 0) {
+    *reinterpret_cast<u32x2_t*>(dst) =
+        u32x2_t{static_cast<uint32_t>(o[0]) | (static_cast<uint32_t>(o[1]) << 16),
+                static_cast<uint32_t>(o[2]) | (static_cast<uint32_t>(o[3]) << 16)};
+  } else {
+    for (int v = 0; v < 4 && nb + v < p.n; ++v) dst[v] = o[v];
+  }
+}
+
+template <int NW, int CPW>
+__global__ void __launch_bounds__(64 * NW) k_skinny_one(Skinny2Params p) {
+  __shared__ f32x4_v red[(NW > 1 ? NW - 1 : 1) * 64];
+  __shared__ int last_sh;
+  const int b = static_cast<int>(blockIdx.x);
+  if (b < p.a_blocks) {
+    adapter_block_one<NW>(p, b, red, &last_sh);
+  } else {
+    weight_block_one<NW, CPW>(p, b - p.a_blocks, red);
+  }
+}
+
+template <int NW, int CPW>
+void launch_one(const Skinny2Params& p, hipStream_t stream) {
+  hipLaunchKernelGGL((k_skinny_one<NW, CPW>), dim3(static_cast<unsigned>(p.a_blocks + p.w_blocks)),
+                     dim3(64 * NW), 0, stream, p);
+}
+
+std::atomic<unsigned int> g_calls2{0};
+
+// The one-launch form pays for its published h with a chain of dependent
+// round trips (the adapter blocks' partials, the last one's sums, the
+// flag, the weight blocks' reads) that the weight stream hides only when it
+// is long: measured on the Qwen3-2B shapes at M = 1, 6144 -> 2048 takes
+// 11.3 us against 13.5 us for two launches, but 2048 -> 6144 12.8 against
+// 10.5 and 2048 -> 2048 9.7 against 8.2. Chosen for K >= 4096;
+// RPX_SKINNY2_ONE=1 / 0 forces either form.
+bool one_launch_selected(int64_t k) {
+  static const int force = [] {
+    const char* env = std::getenv("RPX_SKINNY2_ONE");
+    return env == nullptr ? -1 : std::atoi(env);
+  }();
+  if (force == 0) return false;
+  if (force > 0) return true;
+  return k >= 4096;
+}
+
 template <int NW, int CPW>
 void launch_main(const Skinny2Params& p, hipStream_t stream) {
   const int64_t blocks = p.a_blocks + ceil_div(p.n, 16);
@@ -334,7 +571,8 @@ bool skinny2_selected(int64_t m, int64_t n, int64_t k, int64_t rank, int64_t n_g
 }
 
 int64_t skinny2_workspace_floats(int64_t m, int64_t n, int64_t k, int64_t rank) {
-  return static_cast<int64_t>(plan2(n, k).slices) * m * rank;
+  // K-slice partials of h, then the published h
+  return static_cast<int64_t>(plan2(n, k).slices) * m * rank + m * rank;
 }
 
 hipError_t launch_skinny2_forward(const uint16_t* x, int64_t m, int64_t k, const Int4Operand& w,
@@ -365,6 +603,23 @@ hipError_t launch_skinny2_forward(const uint16_t* x, int64_t m, int64_t k, const
   p.slices = pl.slices;
   p.a_blocks = p.slices * static_cast<int>(ceil_div(rank, 16));
   p.b_vec = (reinterpret_cast<uintptr_t>(lora_b) & 15) == 0 && rank % 8 == 0 && rank * 16 <= 512;
+  p.hf = ws + static_cast<int64_t>(p.slices) * m * rank;
+  p.w_blocks = static_cast<int>(ceil_div(n, 16));
+  p.slot = 0;
+  if (one_launch_selected(k)) {
+    p.slot = static_cast<int>(g_calls2.fetch_add(1, std::memory_order_relaxed) % kSlots2);
+    bool one = false;
+#define RPX_ONE(NW, CPW)                              \
+  if (!one && pl.nw == NW && pl.cpw == CPW) {         \
+    launch_one<NW, CPW>(p, stream);                   \
+    one = true;                                       \
+  }
+    RPX_ONE(4, 1) RPX_ONE(4, 2) RPX_ONE(4, 4)
+    RPX_ONE(8, 1) RPX_ONE(8, 2) RPX_ONE(8, 4)
+    RPX_ONE(16, 1) RPX_ONE(16, 2) RPX_ONE(16, 4)
+#undef RPX_ONE
+    return one ? hipGetLastError() : hipErrorInvalidValue;
+  }
   bool launched = false;
 #define RPX_MAIN(NW, CPW)                             \
   if (!launched && pl.nw == NW && pl.cpw == CPW) {    \

@@ -272,13 +272,42 @@ def test_skinny_two_launch_matches_oracle(monkeypatch, m, k, n, r, group):
     assert rel_l2(from_dev(y), y_o) < TOL
 
 
-@pytest.mark.parametrize("m", [8, 2])
-def test_skinny_graph_replays_and_repeats_are_bit_identical(m):
-    """The one-launch kernel's per-tile arrival counters (M = 8) return to
-    their resting value after each call, and the two-launch path (M = 2)
-    keeps no state: eager repeats and graph replays give the same bits."""
+def test_skinny_one_launch_consecutive_calls_match_oracle():
+    """Twelve back-to-back calls with different inputs (more calls than
+    slots of arrival words, so slots are reused): each result matches the
+    oracle, so no call reads an h published by an earlier one."""
 
-    k, n, r = 2048, 1536, 32
+    k, n, r = 4096, 320, 32
+    base = _lora_case(4, k, n, r, 64, seed=5, bias=True)
+    _, packed, scales, a, b, bias_bits, _ = base
+    b = b * 50.0  # the adapter term comparable to the base product
+    pd = to_dev(packed)
+    sd = to_dev(scales.view(np.int16)).view(torch.uint16)
+    ad, bd = to_dev_bf16(a), to_dev_bf16(b)
+    biasd = to_dev(bias_bits.view(np.int16)).view(torch.uint16)
+    xs, outs = [], []
+    for i in range(12):
+        m = 1 + i % 4
+        x = bf16_values(rng(100 + i).standard_normal((m, k)))
+        xs.append(x)
+        outs.append(ops.int4lora_forward(to_dev_bf16(x), pd, sd, ad, bd, scaling=1.0,
+                                         group_size=64, bias_bits=biasd))
+    torch.cuda.synchronize()
+    for x, (y, h) in zip(xs, outs):
+        y_o, h_o = olora.lora_forward(x, packed, scales, a, b, alpha=float(r), rank=r,
+                                      bias_bits=bias_bits, group_size=64)
+        assert rel_l2(from_dev(h), h_o) < TOL
+        assert rel_l2(from_dev(y), y_o) < TOL
+
+
+@pytest.mark.parametrize("m,k", [(8, 2048), (2, 2048), (1, 4096)])
+def test_skinny_graph_replays_and_repeats_are_bit_identical(m, k):
+    """The arrival words of the one-launch kernels (M = 8: per-tile split
+    counters; M = 1, K = 4096: the published h) return to their resting
+    value after each call, and the two-launch path (M = 2, K = 2048) keeps
+    no state: eager repeats and graph replays give the same bits."""
+
+    n, r = 1536, 32
     x, packed, scales, a, b, bias_bits, _ = _lora_case(m, k, n, r, 64, seed=91, bias=False)
     xd, pd = to_dev_bf16(x), to_dev(packed)
     sd = to_dev(scales.view(np.int16)).view(torch.uint16)
