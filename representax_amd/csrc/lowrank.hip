@@ -6,6 +6,8 @@
 //            deterministic second-pass sum.
 // Both use v_mfma_f32_16x16x32_bf16: lane l of a 16x16 block owns column
 // l % 16 and rows 4*(l/16) + v.
+#include <cstdlib>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -39,36 +41,42 @@ __device__ __forceinline__ u32x4_t load8(const uint16_t* p, int valid, bool alig
   return u32x4_t{w[0], w[1], w[2], w[3]};
 }
 
-// One workgroup per 16 output rows; its four waves split K and reduce in LDS.
-template <int RB>
+// One workgroup per 16 G output rows (G row groups of 16); its four waves
+// split K in interleaved 32-deep steps and reduce in LDS. Every fragment of R
+// a wave loads serves the G row groups, so R's L2 traffic per row falls by G.
+template <int RB, int G>
 __global__ void __launch_bounds__(256)
     k_rank_nt(const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ R,
               int64_t ldr, int64_t M, int64_t rank, int64_t K, int round_a, float a_scale,
               uint16_t* __restrict__ out, int64_t ldo) {
-  __shared__ float red[4][RB][64][4];
+  __shared__ float red[3][G][RB][64][4];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int64_t m0 = static_cast<int64_t>(blockIdx.x) * 16;
-  const int64_t row = m0 + (lane & 15);
+  const int64_t m0 = static_cast<int64_t>(blockIdx.x) * 16 * G;
   const int koff = (lane >> 4) * 8;
   const bool a_al = (lda % 8 == 0) && ((reinterpret_cast<uintptr_t>(A) & 15) == 0);
   const bool r_al = (ldr % 8 == 0) && ((reinterpret_cast<uintptr_t>(R) & 15) == 0);
-  f32x4_t acc[RB];
+  f32x4_t acc[G][RB];
 #pragma unroll
-  for (int rb = 0; rb < RB; ++rb) acc[rb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  // the four waves take interleaved 32-deep k-steps; each wave keeps the
-  // loads of U steps in flight before their MFMAs
-  constexpr int U = 4;
+  for (int gi = 0; gi < G; ++gi)
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) acc[gi][rb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  // each wave keeps the loads of U steps in flight before their MFMAs
+  constexpr int U = G >= 4 ? 2 : 4;
   for (int64_t kb = static_cast<int64_t>(wave) * 32; kb < K; kb += 128 * U) {
-    u32x4_t av[U];
+    u32x4_t av[U][G];
     u32x4_t rv[U][RB];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int64_t kc = kb + 128 * u + koff;
       int kv = static_cast<int>(K - kc);
       kv = kv < 0 ? 0 : (kv > 8 ? 8 : kv);
-      av[u] = load8(A + row * lda + kc, row < M ? kv : 0, a_al);
+#pragma unroll
+      for (int gi = 0; gi < G; ++gi) {
+        const int64_t row = m0 + 16 * gi + (lane & 15);
+        av[u][gi] = load8(A + row * lda + kc, row < M ? kv : 0, a_al);
+      }
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) {
         const int64_t j = rb * 16 + (lane & 15);
@@ -76,31 +84,43 @@ __global__ void __launch_bounds__(256)
       }
     }
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      u32x4_t a = av[u];
-      if (round_a) a = scale_round8(a, a_scale);
-      const bf16x8_t af = as_bf16x8(a);
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int gi = 0; gi < G; ++gi) {
+        u32x4_t a = av[u][gi];
+        if (round_a) a = scale_round8(a, a_scale);
+        const bf16x8_t af = as_bf16x8(a);
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+          acc[gi][rb] =
+              __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, as_bf16x8(rv[u][rb]), acc[gi][rb], 0, 0, 0);
+      }
+  }
+  // waves 1-3 hand their sums to wave 0 through LDS, which adds them in
+  // wave order and stores (lane: rows 4 (lane >> 4) + v, column j = lane & 15)
+  if (wave > 0) {
+#pragma unroll
+    for (int gi = 0; gi < G; ++gi)
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb)
-        acc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, as_bf16x8(rv[u][rb]), acc[rb], 0, 0, 0);
-    }
+#pragma unroll
+        for (int v = 0; v < 4; ++v) red[wave - 1][gi][rb][lane][v] = acc[gi][rb][v];
   }
-#pragma unroll
-  for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-    for (int v = 0; v < 4; ++v) red[wave][rb][lane][v] = acc[rb][v];
   __syncthreads();
-  for (int o = tid; o < 16 * RB * 16; o += 256) {
-    const int i = o / (RB * 16);
-    const int j = o % (RB * 16);
-    const int64_t mm = m0 + i;
-    if (mm >= M || j >= rank) continue;
-    const int ln = (j & 15) + 16 * (i >> 2);
-    const int v = i & 3;
-    const int rb = j >> 4;
-    const float s = red[0][rb][ln][v] + red[1][rb][ln][v] + red[2][rb][ln][v] + red[3][rb][ln][v];
-    out[mm * ldo + j] = f32_to_bf16(s);
-  }
+  if (wave != 0) return;
+#pragma unroll
+  for (int gi = 0; gi < G; ++gi)
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      const int j = rb * 16 + (lane & 15);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int64_t mm = m0 + 16 * gi + 4 * (lane >> 4) + v;
+        const float s = acc[gi][rb][v] + red[0][gi][rb][lane][v] + red[1][gi][rb][lane][v] +
+                        red[2][gi][rb][lane][v];
+        if (mm < M && j < rank) out[mm * ldo + j] = f32_to_bf16(s);
+      }
+    }
 }
 
 // Token-reduction product: partials[z][p][q] = sum over the token chunk z of
@@ -421,24 +441,51 @@ int grid1d(int64_t work) {
 
 }  // namespace
 
+// Row groups per workgroup: 4 (64 rows) unless RPX_RANK_NT_G=1 asks for the
+// 16-row form; fewer when that leaves under 512 workgroups.
+int rank_nt_groups(int64_t m) {
+  static const int forced = [] {
+    const char* env = std::getenv("RPX_RANK_NT_G");
+    return env == nullptr ? 0 : std::atoi(env);
+  }();
+  if (forced == 1 || forced == 2 || forced == 4) return forced;
+  if (ceil_div(m, 64) >= 512) return 4;
+  if (ceil_div(m, 32) >= 512) return 2;
+  return 1;
+}
+
+template <int G>
+hipError_t launch_rank_nt_g(const uint16_t* a, int64_t lda, const uint16_t* r_mat, int64_t ldr,
+                            int64_t m, int64_t rank, int64_t k, int ra, float a_scale,
+                            uint16_t* out, int64_t ldo, hipStream_t stream) {
+  const dim3 grid(static_cast<unsigned>(ceil_div(m, 16 * G)));
+  if (rank <= 16)
+    hipLaunchKernelGGL((k_rank_nt<1, G>), grid, dim3(256), 0, stream, a, lda, r_mat, ldr, m, rank,
+                       k, ra, a_scale, out, ldo);
+  else if (rank <= 32)
+    hipLaunchKernelGGL((k_rank_nt<2, G>), grid, dim3(256), 0, stream, a, lda, r_mat, ldr, m, rank,
+                       k, ra, a_scale, out, ldo);
+  else if (rank <= 64)
+    hipLaunchKernelGGL((k_rank_nt<4, G>), grid, dim3(256), 0, stream, a, lda, r_mat, ldr, m, rank,
+                       k, ra, a_scale, out, ldo);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
 hipError_t launch_rank_nt(const uint16_t* a, int64_t lda, const uint16_t* r_mat, int64_t ldr,
                           int64_t m, int64_t rank, int64_t k, bool round_a, float a_scale,
                           uint16_t* out, int64_t ldo, hipStream_t stream) {
   if (m == 0 || rank == 0) return hipSuccess;
-  const dim3 grid(static_cast<unsigned>(ceil_div(m, 16)));
   const int ra = round_a ? 1 : 0;
-  if (rank <= 16)
-    hipLaunchKernelGGL(k_rank_nt<1>, grid, dim3(256), 0, stream, a, lda, r_mat, ldr, m, rank, k,
-                       ra, a_scale, out, ldo);
-  else if (rank <= 32)
-    hipLaunchKernelGGL(k_rank_nt<2>, grid, dim3(256), 0, stream, a, lda, r_mat, ldr, m, rank, k,
-                       ra, a_scale, out, ldo);
-  else if (rank <= 64)
-    hipLaunchKernelGGL(k_rank_nt<4>, grid, dim3(256), 0, stream, a, lda, r_mat, ldr, m, rank, k,
-                       ra, a_scale, out, ldo);
-  else
-    return hipErrorInvalidValue;
-  return hipGetLastError();
+  switch (rank_nt_groups(m)) {
+    case 4:
+      return launch_rank_nt_g<4>(a, lda, r_mat, ldr, m, rank, k, ra, a_scale, out, ldo, stream);
+    case 2:
+      return launch_rank_nt_g<2>(a, lda, r_mat, ldr, m, rank, k, ra, a_scale, out, ldo, stream);
+    default:
+      return launch_rank_nt_g<1>(a, lda, r_mat, ldr, m, rank, k, ra, a_scale, out, ldo, stream);
+  }
 }
 
 int64_t rank_tn_workspace_floats(int64_t m, int64_t p, int64_t q) {
