@@ -277,58 +277,146 @@ __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_
   // keep the order.
   constexpr int NS1 = FM * FN;  // MFMA slots per step
   constexpr int NU = 4 * FN;    // dequantization units per step
+  // Activation operands ([M, N], the output's row stride) for the backward
+  // epilogues of the bf16 (dx) tiles, loaded as 16-byte row segments (segment
+  // idx = it * NT + tid of the tile) before the last K slice so that their
+  // latency overlaps it; that slice runs outside the loop so the loop itself
+  // does not carry their registers.
+  constexpr bool AUX_OPS = ACT != kActNone && ACT != kActGeluFwd;
+  constexpr bool TWO_OPS = ACT == kActSiluMulBwd;
+  constexpr bool PREFETCH = AUX_OPS && !INT4;
+  constexpr int SEG_ROW = BN / 8;  // 8-column segments per tile row
+  constexpr int SEG_ITS = BM * SEG_ROW / NT;
+  static_assert(ACT == kActNone || (BM * SEG_ROW) % NT == 0,
+                "tile segments must split evenly over the threads");
+  const uintptr_t act_ptrs = reinterpret_cast<uintptr_t>(out) |
+                             reinterpret_cast<uintptr_t>(epi.aux) |
+                             reinterpret_cast<uintptr_t>(epi.aux2) |
+                             reinterpret_cast<uintptr_t>(epi.pre_out) |
+                             reinterpret_cast<uintptr_t>(epi.out2);
+  const bool act_vec = ACT != kActNone && m0 + BM <= M && n0 + BN <= N && (ldc & 7) == 0 &&
+                       (act_ptrs & 15) == 0;
+  u32x4_t av[AUX_OPS ? SEG_ITS : 1], a2v[TWO_OPS ? SEG_ITS : 1];
+  auto load_aux = [&]() {
+#pragma unroll
+    for (int it = 0; it < SEG_ITS; ++it) {
+      const int idx = it * NT + tid;
+      const int64_t off = (m0 + idx / SEG_ROW) * ldc + n0 + 8 * (idx % SEG_ROW);
+      if constexpr (AUX_OPS) av[it] = *reinterpret_cast<const u32x4_t*>(epi.aux + off);
+      if constexpr (TWO_OPS) a2v[it] = *reinterpret_cast<const u32x4_t*>(epi.aux2 + off);
+    }
+  };
+
   int stage = 0;
-  for (int t = 0; t < nk; ++t) {
-    const int next = stage + 1 == NS ? 0 : stage + 1;
-    const uint8_t* st = smem + stage * STAGE;
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int kk = 0; kk < 3; ++kk) {
-#pragma unroll
+  if constexpr (PREFETCH) {
+    auto slice = [&](int t) {
+      const int next = stage + 1 == NS ? 0 : stage + 1;
+      const uint8_t* st = smem + stage * STAGE;
+      __builtin_amdgcn_sched_barrier(0);
+  #pragma unroll
+      for (int kk = 0; kk < 3; ++kk) {
+  #pragma unroll
+        for (int i = 0; i < NS1; ++i) {
+          mma(i, kk);
+          __builtin_amdgcn_sched_barrier(0);
+          if (i == 0) read_a(st, kk + 1, (kk + 1) & 1);
+          if constexpr (INT4) {
+  #pragma unroll
+            for (int u = i * NU / NS1; u < (i + 1) * NU / NS1; ++u) dq_unit(kk + 1, u);
+          } else {
+            if (i == NS1 / 2) read_b(st, kk + 1, (kk + 1) & 1);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+      wait_sync<(NS - 2) * LPW>();
+      const int refill = t + NS < nk ? t + NS : nk - 1;
+      uint8_t* fill = smem + stage * STAGE;
+      const uint8_t* nst = smem + next * STAGE;
+      // INT4: packed rows and scales first, their units in the last half
+      constexpr int U0 = NS1 / 2;
+  #pragma unroll
       for (int i = 0; i < NS1; ++i) {
-        mma(i, kk);
+        mma(i, 3);
         __builtin_amdgcn_sched_barrier(0);
-        if (i == 0) read_a(st, kk + 1, (kk + 1) & 1);
+  #pragma unroll
+        for (int d = i * LPW / NS1; d < (i + 1) * LPW / NS1; ++d)
+          dma_seg(fill, src[d], koff(refill, d), wave + d * NW);
         if constexpr (INT4) {
-#pragma unroll
-          for (int u = i * NU / NS1; u < (i + 1) * NU / NS1; ++u) dq_unit(kk + 1, u);
+          if (i == 0) {
+            read_bp(nst);
+            read_bs(t + 1 < nk ? t + 1 : t);
+          }
+          if (i == 1) read_a(nst, 0, 0);
+          if (i >= U0) {
+  #pragma unroll
+            for (int u = (i - U0) * NU / (NS1 - U0); u < (i - U0 + 1) * NU / (NS1 - U0); ++u)
+              dq_unit(0, u);
+          }
         } else {
-          if (i == NS1 / 2) read_b(st, kk + 1, (kk + 1) & 1);
+          if (i == 0) read_a(nst, 0, 0);
+          if (i == NS1 / 2) read_b(nst, 0, 0);
         }
         __builtin_amdgcn_sched_barrier(0);
       }
-    }
-    wait_sync<(NS - 2) * LPW>();
-    const int refill = t + NS < nk ? t + NS : nk - 1;
-    uint8_t* fill = smem + stage * STAGE;
-    const uint8_t* nst = smem + next * STAGE;
-    // INT4: packed rows and scales first, their units in the last half
-    constexpr int U0 = NS1 / 2;
-#pragma unroll
-    for (int i = 0; i < NS1; ++i) {
-      mma(i, 3);
+      stage = next;
+    };
+    for (int t = 0; t + 1 < nk; ++t) slice(t);
+    if (act_vec) load_aux();
+    slice(nk - 1);
+  } else {
+    for (int t = 0; t < nk; ++t) {
+      const int next = stage + 1 == NS ? 0 : stage + 1;
+      const uint8_t* st = smem + stage * STAGE;
       __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int d = i * LPW / NS1; d < (i + 1) * LPW / NS1; ++d)
-        dma_seg(fill, src[d], koff(refill, d), wave + d * NW);
-      if constexpr (INT4) {
-        if (i == 0) {
-          read_bp(nst);
-          read_bs(t + 1 < nk ? t + 1 : t);
+  #pragma unroll
+      for (int kk = 0; kk < 3; ++kk) {
+  #pragma unroll
+        for (int i = 0; i < NS1; ++i) {
+          mma(i, kk);
+          __builtin_amdgcn_sched_barrier(0);
+          if (i == 0) read_a(st, kk + 1, (kk + 1) & 1);
+          if constexpr (INT4) {
+  #pragma unroll
+            for (int u = i * NU / NS1; u < (i + 1) * NU / NS1; ++u) dq_unit(kk + 1, u);
+          } else {
+            if (i == NS1 / 2) read_b(st, kk + 1, (kk + 1) & 1);
+          }
+          __builtin_amdgcn_sched_barrier(0);
         }
-        if (i == 1) read_a(nst, 0, 0);
-        if (i >= U0) {
-#pragma unroll
-          for (int u = (i - U0) * NU / (NS1 - U0); u < (i - U0 + 1) * NU / (NS1 - U0); ++u)
-            dq_unit(0, u);
-        }
-      } else {
-        if (i == 0) read_a(nst, 0, 0);
-        if (i == NS1 / 2) read_b(nst, 0, 0);
       }
-      __builtin_amdgcn_sched_barrier(0);
+      wait_sync<(NS - 2) * LPW>();
+      const int refill = t + NS < nk ? t + NS : nk - 1;
+      uint8_t* fill = smem + stage * STAGE;
+      const uint8_t* nst = smem + next * STAGE;
+      // INT4: packed rows and scales first, their units in the last half
+      constexpr int U0 = NS1 / 2;
+  #pragma unroll
+      for (int i = 0; i < NS1; ++i) {
+        mma(i, 3);
+        __builtin_amdgcn_sched_barrier(0);
+  #pragma unroll
+        for (int d = i * LPW / NS1; d < (i + 1) * LPW / NS1; ++d)
+          dma_seg(fill, src[d], koff(refill, d), wave + d * NW);
+        if constexpr (INT4) {
+          if (i == 0) {
+            read_bp(nst);
+            read_bs(t + 1 < nk ? t + 1 : t);
+          }
+          if (i == 1) read_a(nst, 0, 0);
+          if (i >= U0) {
+  #pragma unroll
+            for (int u = (i - U0) * NU / (NS1 - U0); u < (i - U0 + 1) * NU / (NS1 - U0); ++u)
+              dq_unit(0, u);
+          }
+        } else {
+          if (i == 0) read_a(nst, 0, 0);
+          if (i == NS1 / 2) read_b(nst, 0, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      stage = next;
     }
-    stage = next;
   }
   // no LDS DMA may still be in flight when the waves leave the loop
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -518,25 +606,13 @@ __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_
     // store v itself.
     static_assert(BM * P <= NS * STAGE, "activation epilogues stage the tile in LDS");
     constexpr bool FWD = ACT == kActGeluFwd || ACT == kActSiluMulFwd;
-    constexpr bool AUX = ACT != kActGeluFwd;
-    constexpr bool TWO = ACT == kActSiluMulBwd;
-    constexpr int CPR = BN / 8;  // 8-column segments per tile row
-    constexpr int ITS = BM * CPR / NT;
-    static_assert((BM * CPR) % NT == 0, "tile segments must split evenly over the threads");
-    const uintptr_t ptrs = reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(epi.aux) |
-                           reinterpret_cast<uintptr_t>(epi.aux2) |
-                           reinterpret_cast<uintptr_t>(epi.pre_out) |
-                           reinterpret_cast<uintptr_t>(epi.out2);
-    const bool vec = m0 + BM <= M && n0 + BN <= N && (ldc & 7) == 0 && (ptrs & 15) == 0;
-    u32x4_t av[AUX ? ITS : 1], a2v[TWO ? ITS : 1];
-    if (vec) {
-#pragma unroll
-      for (int it = 0; it < ITS; ++it) {
-        const int idx = it * NT + tid;
-        const int64_t off = (m0 + idx / CPR) * ldc + n0 + 8 * (idx % CPR);
-        if constexpr (AUX) av[it] = *reinterpret_cast<const u32x4_t*>(epi.aux + off);
-        if constexpr (TWO) a2v[it] = *reinterpret_cast<const u32x4_t*>(epi.aux2 + off);
-      }
+    constexpr bool AUX = AUX_OPS;
+    constexpr bool TWO = TWO_OPS;
+    constexpr int CPR = SEG_ROW;
+    constexpr int ITS = SEG_ITS;
+    const bool vec = act_vec;
+    if constexpr (AUX && !PREFETCH) {
+      if (vec) load_aux();
     }
     wait_sync<0>();  // every wave is done reading the pipeline stages
 #pragma unroll
