@@ -123,8 +123,13 @@ __device__ __forceinline__ f32x4_v reduce_waves(f32x4_v acc, f32x4_v* red) {
   return acc;
 }
 
+// Adapter block a = (K slice s, 16-rank group q): the fp32 partial of
+// x A^T over the slice's 128 NW columns, one 128-column chunk per wave,
+// summed over the waves in wave order; valid in wave 0, where lane l holds
+// P[s][m = l & 15][j = 16 q + 4 (l >> 4) + v].
 template <int NW>
-__device__ __forceinline__ void adapter_block(const Skinny2Params& p, int a, f32x4_v* red) {
+__device__ __forceinline__ f32x4_v adapter_partial(const Skinny2Params& p, int a, f32x4_v* red,
+                                                   int* s_out, int* q_out) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int rl = lane & 15;
@@ -147,14 +152,83 @@ __device__ __forceinline__ void adapter_block(const Skinny2Params& p, int a, f32
   f32x4_v acc{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int st = 0; st < 4; ++st) acc = mfma16(av[st], xv[st], acc);
-  acc = reduce_waves<NW>(acc, red);
-  if (wave != 0 || rl >= p.m) return;
-  // lane: P[s][m = rl][j = 16 q + 4 g + v]
+  *s_out = s;
+  *q_out = q;
+  return reduce_waves<NW>(acc, red);
+}
+
+template <int NW>
+__device__ __forceinline__ void adapter_block(const Skinny2Params& p, int a, f32x4_v* red) {
+  int s, q;
+  const f32x4_v acc = adapter_partial<NW>(p, a, red, &s, &q);
+  const int lane = threadIdx.x & 63;
+  const int rl = lane & 15;
+  if ((threadIdx.x >> 6) != 0 || rl >= p.m) return;
   float* dst = p.part + (static_cast<int64_t>(s) * p.m + rl) * p.rank;
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
-    const int jj = 16 * q + 4 * g + v;
+    const int jj = 16 * q + 4 * (lane >> 4) + v;
     if (jj < p.rank) dst[jj] = acc[v];
+  }
+}
+
+// A weight block's loads: rows n0 + (l & 15) over the wave's chunks
+// c = wave + i NW of 128 columns (16-byte packed word, scale, 4 x fragments).
+template <int CPW>
+struct WeightFrags {
+  u32x4_t wv[CPW];
+  u32x4_t xv[CPW][4];
+  uint16_t sv[CPW];
+};
+
+template <int NW, int CPW>
+__device__ __forceinline__ void weight_loads(const Skinny2Params& p, int64_t n0,
+                                             WeightFrags<CPW>& f) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int rl = lane & 15;
+  const int g = lane >> 4;
+  const int64_t row = n0 + rl;
+  const int64_t rc = row < p.n ? row : p.n - 1;
+  const uint8_t* wrow = p.packed + rc * p.pcols;
+  const uint16_t* srow = p.scales + rc * p.n_groups;
+  const int64_t nchunks = p.k / 128;
+#pragma unroll
+  for (int i = 0; i < CPW; ++i) {
+    const int64_t c = wave + static_cast<int64_t>(i) * NW;
+    const bool ok = c < nchunks;
+    const int64_t k0 = ok ? c * 128 + 32 * g : 0;
+    f.wv[i] = ok ? ld16(wrow + k0 / 2) : u32x4_t{0u, 0u, 0u, 0u};
+    f.sv[i] = srow[p.n_groups == 1 ? 0 : (k0 >> p.group_shift)];
+#pragma unroll
+    for (int st = 0; st < 4; ++st) f.xv[i][st] = x_frag(p, rl, k0 + 8 * st, ok);
+  }
+}
+
+// Dequantized MFMAs over the loaded chunks, summed over the waves in wave
+// order: valid in wave 0, lane l holding D[n0 + 4 (l >> 4) + v][m = l & 15].
+template <int NW, int CPW>
+__device__ __forceinline__ f32x4_v weight_mfma(const WeightFrags<CPW>& f, f32x4_v* red) {
+  f32x4_v acc{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < CPW; ++i) {
+    const float s = bf16_to_f32(f.sv[i]);
+#pragma unroll
+    for (int st = 0; st < 4; ++st) acc = mfma16(dequant8(f.wv[i][st], s), f.xv[i][st], acc);
+  }
+  return reduce_waves<NW>(acc, red);
+}
+
+// y[m][nb .. nb + 3] = o (bf16 bits), one 8-byte store when whole and aligned
+__device__ __forceinline__ void store_row4(const Skinny2Params& p, int m, int64_t nb,
+                                           const uint16_t (&o)[4]) {
+  uint16_t* dst = p.y + static_cast<int64_t>(m) * p.n + nb;
+  if (nb + 3 < p.n && (reinterpret_cast<uintptr_t>(dst) & 7) == 0) {
+    *reinterpret_cast<u32x2_t*>(dst) =
+        u32x2_t{static_cast<uint32_t>(o[0]) | (static_cast<uint32_t>(o[1]) << 16),
+                static_cast<uint32_t>(o[2]) | (static_cast<uint32_t>(o[3]) << 16)};
+  } else {
+    for (int v = 0; v < 4 && nb + v < p.n; ++v) dst[v] = o[v];
   }
 }
 
@@ -163,26 +237,9 @@ __device__ __forceinline__ void weight_block(const Skinny2Params& p, int64_t b, 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int rl = lane & 15;
-  const int g = lane >> 4;
   const int64_t n0 = 16 * b;
-  const int64_t row = n0 + rl;
-  const int64_t rc = row < p.n ? row : p.n - 1;
-  const uint8_t* wrow = p.packed + rc * p.pcols;
-  const uint16_t* srow = p.scales + rc * p.n_groups;
-  const int64_t nchunks = p.k / 128;
-  // every load of the wave first
-  u32x4_t wv[CPW], xv[CPW][4];
-  uint16_t sv[CPW];
-#pragma unroll
-  for (int i = 0; i < CPW; ++i) {
-    const int64_t c = wave + static_cast<int64_t>(i) * NW;
-    const bool ok = c < nchunks;
-    const int64_t k0 = ok ? c * 128 + 32 * g : 0;
-    wv[i] = ok ? ld16(wrow + k0 / 2) : u32x4_t{0u, 0u, 0u, 0u};
-    sv[i] = srow[p.n_groups == 1 ? 0 : (k0 >> p.group_shift)];
-#pragma unroll
-    for (int st = 0; st < 4; ++st) xv[i][st] = x_frag(p, rl, k0 + 8 * st, ok);
-  }
+  WeightFrags<CPW> f;
+  weight_loads<NW, CPW>(p, n0, f);
   // the block's B rows (16 rank contiguous bf16) and bias, touched for the
   // finishing launch
   uint32_t touch = 0;
@@ -191,26 +248,14 @@ __device__ __forceinline__ void weight_block(const Skinny2Params& p, int64_t b, 
     if (p.b_vec && 8 * lane < rows * p.rank) touch = ld16(p.lora_b + n0 * p.rank + 8 * lane).x;
     if (p.bias != nullptr && lane < rows) touch ^= p.bias[n0 + lane];
   }
-  f32x4_v acc{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int i = 0; i < CPW; ++i) {
-    const float s = bf16_to_f32(sv[i]);
-#pragma unroll
-    for (int st = 0; st < 4; ++st) acc = mfma16(dequant8(wv[i][st], s), xv[i][st], acc);
-  }
-  acc = reduce_waves<NW>(acc, red);
+  const f32x4_v acc = weight_mfma<NW, CPW>(f, red);
   if (wave != 0) return;
   asm volatile("" ::"v"(touch));
   if (rl >= p.m) return;
   // lane: base[m = rl][n = n0 + 4 g + v]
-  const int64_t nb = n0 + 4 * g;
-  uint16_t* dst = p.y + static_cast<int64_t>(rl) * p.n + nb;
-  if (nb + 3 < p.n && (reinterpret_cast<uintptr_t>(dst) & 7) == 0) {
-    *reinterpret_cast<u32x2_t*>(dst) =
-        u32x2_t{pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3])};
-  } else {
-    for (int v = 0; v < 4 && nb + v < p.n; ++v) dst[v] = f32_to_bf16(acc[v]);
-  }
+  const uint16_t o[4] = {f32_to_bf16(acc[0]), f32_to_bf16(acc[1]), f32_to_bf16(acc[2]),
+                         f32_to_bf16(acc[3])};
+  store_row4(p, rl, n0 + 4 * (lane >> 4), o);
 }
 
 template <int NW, int CPW>
@@ -308,35 +353,15 @@ __device__ unsigned int g_skinny2_state[kSlots2][4];
 template <int NW>
 __device__ __forceinline__ void adapter_block_one(const Skinny2Params& p, int a, f32x4_v* red,
                                                   int* last_sh) {
+  int s, q;
+  const f32x4_v acc = adapter_partial<NW>(p, a, red, &s, &q);
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
   const int rl = lane & 15;
-  const int g = lane >> 4;
-  const int groups = (p.rank + 15) / 16;
-  const int q = a % groups;
-  const int s = a / groups;
-  const int j = 16 * q + rl;
-  const bool jok = j < p.rank;
-  const uint16_t* arow = p.lora_a + static_cast<int64_t>(jok ? j : p.rank - 1) * p.k;
-  const int64_t c = static_cast<int64_t>(s) * NW + wave;
-  const bool ok = c < p.k / 128;
-  const int64_t k0 = ok ? c * 128 + 32 * g : 0;
-  u32x4_t av[4], xv[4];
-#pragma unroll
-  for (int st = 0; st < 4; ++st) {
-    av[st] = ok && jok ? ld16(arow + k0 + 8 * st) : u32x4_t{0u, 0u, 0u, 0u};
-    xv[st] = x_frag(p, rl, k0 + 8 * st, ok);
-  }
-  f32x4_v acc{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int st = 0; st < 4; ++st) acc = mfma16(av[st], xv[st], acc);
-  acc = reduce_waves<NW>(acc, red);
-  if (wave == 0 && rl < p.m) {
-    // lane: P[s][m = rl][j = 16 q + 4 g + v]
+  if ((threadIdx.x >> 6) == 0 && rl < p.m) {
     float* dst = p.part + (static_cast<int64_t>(s) * p.m + rl) * p.rank;
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
-      const int jj = 16 * q + 4 * g + v;
+      const int jj = 16 * q + 4 * (lane >> 4) + v;
       if (jj < p.rank) store_coherent_f32(dst + jj, acc[v]);
     }
   }
@@ -367,23 +392,9 @@ __device__ __forceinline__ void weight_block_one(const Skinny2Params& p, int64_t
   const int rl = lane & 15;
   const int g = lane >> 4;
   const int64_t n0 = 16 * b;
-  const int64_t row = n0 + rl;
-  const int64_t rc = row < p.n ? row : p.n - 1;
-  const uint8_t* wrow = p.packed + rc * p.pcols;
-  const uint16_t* srow = p.scales + rc * p.n_groups;
-  const int64_t nchunks = p.k / 128;
-  u32x4_t wv[CPW], xv[CPW][4];
-  uint16_t sv[CPW];
-#pragma unroll
-  for (int i = 0; i < CPW; ++i) {
-    const int64_t c = wave + static_cast<int64_t>(i) * NW;
-    const bool ok = c < nchunks;
-    const int64_t k0 = ok ? c * 128 + 32 * g : 0;
-    wv[i] = ok ? ld16(wrow + k0 / 2) : u32x4_t{0u, 0u, 0u, 0u};
-    sv[i] = srow[p.n_groups == 1 ? 0 : (k0 >> p.group_shift)];
-#pragma unroll
-    for (int st = 0; st < 4; ++st) xv[i][st] = x_frag(p, rl, k0 + 8 * st, ok);
-  }
+  const int64_t rc = n0 + rl < p.n ? n0 + rl : p.n - 1;
+  WeightFrags<CPW> f;
+  weight_loads<NW, CPW>(p, n0, f);
   // wave 0 also loads its rows of B as MFMA row fragments (rank <= 64: two
   // 32-rank steps, j = 32 q + 8 g + [0, 8)) and its 4 bias values
   u32x4_t bfr[2] = {u32x4_t{0u, 0u, 0u, 0u}, u32x4_t{0u, 0u, 0u, 0u}};
@@ -415,14 +426,7 @@ __device__ __forceinline__ void weight_block_one(const Skinny2Params& p, int64_t
       }
     }
   }
-  f32x4_v acc{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int i = 0; i < CPW; ++i) {
-    const float s = bf16_to_f32(sv[i]);
-#pragma unroll
-    for (int st = 0; st < 4; ++st) acc = mfma16(dequant8(wv[i][st], s), xv[i][st], acc);
-  }
-  acc = reduce_waves<NW>(acc, red);
+  const f32x4_v acc = weight_mfma<NW, CPW>(f, red);
   if (wave != 0) return;
 
   // wait (lane 0, bounded) for the published h, then read it as MFMA
@@ -470,15 +474,7 @@ __device__ __forceinline__ void weight_block_one(const Skinny2Params& p, int64_t
     if (p.bias != nullptr) r = round_bf16(r + bias4[v]);
     o[v] = f32_to_bf16(r);
   }
-  const int64_t nb = n0 + 4 * g;
-  uint16_t* dst = p.y + static_cast<int64_t>(rl) * p.n + nb;
-  if (nb + 3 < p.n && (reinterpret_cast<uintptr_t>(dst) & 7) == 0) {
-    *reinterpret_cast<u32x2_t*>(dst) =
-        u32x2_t{static_cast<uint32_t>(o[0]) | (static_cast<uint32_t>(o[1]) << 16),
-                static_cast<uint32_t>(o[2]) | (static_cast<uint32_t>(o[3]) << 16)};
-  } else {
-    for (int v = 0; v < 4 && nb + v < p.n; ++v) dst[v] = o[v];
-  }
+  store_row4(p, rl, n0 + 4 * g, o);
 }
 
 template <int NW, int CPW>
