@@ -8,9 +8,9 @@ TFLOP/s (3 GEMMs of 2*M*N*K per linear).
 
 Secondary lines (same JSON object): the packed-INT4 + LoRA linear fwd+bwd at
 the BERT-base FFN up-projection (x [4096, 768], W 768->3072, rank 16,
-alpha 32) and the skinny-M inference sweep (M in {1,4,16,64}, Qwen3-2B-shaped
-projections, rank 32) with rotating weight copies larger than the 256 MB
-Infinity Cache.
+alpha 32) and the skinny-M inference sweep (M in {1,4,16,64} with group-64
+scales and M in {1,16} with per-row scales, Qwen3-2B-shaped projections,
+rank 32) with rotating weight copies larger than the 256 MB Infinity Cache.
 
 The roofline object is for the dominant kernel (the fp8 MFMA GEMM): its
 algorithmic FLOPs over its own launch durations, timed with HIP events on the
@@ -518,13 +518,14 @@ def run_qwen3(steps=6, warmup=2):
 
 
 def run_skinny(batch=96, latency_calls=64):
-    """Skinny-M INT4 (group 64) + LoRA r32 forward on the Qwen3-2B projection
-    shapes. `us_per_call`: GPU time per call inside a HIP graph of `batch`
-    calls that cycle through a pool of weight copies larger than the 256 MB
-    Infinity Cache, so every call streams its packed weight from HBM.
-    `p50_us`: median over `latency_calls` single eager calls (HIP events
-    around each, weights cycling the same way). HBM bytes: packed weight,
-    group scales, A, B, x and y."""
+    """Skinny-M INT4 + LoRA r32 forward on the Qwen3-2B projection shapes:
+    group-64 scales at M in {1, 4, 16, 64}, and the reference's per-row
+    scales at M in {1, 16}. `us_per_call`: GPU time per call inside a HIP
+    graph of `batch` calls that cycle through a pool of weight copies larger
+    than the 256 MB Infinity Cache, so every call streams its packed weight
+    from HBM. `p50_us`: median over `latency_calls` single eager calls (HIP
+    events around each, weights cycling the same way). HBM bytes: packed
+    weight, scales, A, B, x and y."""
 
     import torch
 
@@ -532,45 +533,47 @@ def run_skinny(batch=96, latency_calls=64):
 
     dev = torch.device("cuda:0")
     g = np.random.Generator(np.random.PCG64(5))
-    r, group = 32, 64
+    r = 32
     out = []
-    for k, n in SKINNY_SHAPES:
-        per_copy = n * k // 2 + n * (k // group) * 2 + (r * k + n * r) * 2
-        copies = max(8, int(np.ceil(300e6 / per_copy)))
-        w = torch.from_numpy((g.standard_normal((n, k)) * 0.02).astype(np.float32)).to(dev)
-        packed, scales = ops.int4_pack(w, group_size=group)
-        del w
-        a0 = bf16_tensor(g.standard_normal((r, k)).astype(np.float32) * 0.02, dev)
-        b0 = bf16_tensor(g.standard_normal((n, r)).astype(np.float32) * 0.02, dev)
-        pool = [(packed.clone(), scales.clone(), a0.clone(), b0.clone()) for _ in range(copies)]
-        for m in (1, 4, 16, 64):
-            x = bf16_tensor(g.standard_normal((m, k)).astype(np.float32), dev)
-            calls = []
-            for i in range(batch):
-                p, s, a, b = pool[i % copies]
-                calls.append(lambda p=p, s=s, a=a, b=b: ops.int4lora_forward(
-                    x, p, s, a, b, scaling=2.0, group_size=group))
-            us = graph_time_per_call_ms(calls, replays=3) * 1e3
-            lat = []
-            for i in range(latency_calls):
-                fn = calls[(i * 7) % batch]
-                e0 = torch.cuda.Event(enable_timing=True)
-                e1 = torch.cuda.Event(enable_timing=True)
-                e0.record()
-                fn()
-                e1.record()
-                e1.synchronize()
-                lat.append(e0.elapsed_time(e1) * 1e3)
-            nbytes = n * k / 2 + n * (k // group) * 2 + (r * k + n * r) * 2 + m * k * 2 + m * n * 2
-            out.append({"m": m, "k": k, "n": n, "us_per_call": round(us, 2),
-                        "p50_us": round(float(np.median(lat)), 2),
-                        "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
-                        "frac_hbm": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
-        del pool
-        torch.cuda.empty_cache()
-    return {"workload": "skinny-M INT4 (group 64) + LoRA r32 forward, Qwen3-2B projection shapes; "
-                        "us_per_call inside a HIP graph of 96 calls cycling weight copies > 256 MB, "
-                        "p50_us over single eager calls", "points": out}
+    for group, ms in ((64, (1, 4, 16, 64)), (None, (1, 16))):
+        for k, n in SKINNY_SHAPES:
+            n_groups = 1 if group is None else k // group
+            per_copy = n * k // 2 + n * n_groups * 2 + (r * k + n * r) * 2
+            copies = max(8, int(np.ceil(300e6 / per_copy)))
+            w = torch.from_numpy((g.standard_normal((n, k)) * 0.02).astype(np.float32)).to(dev)
+            packed, scales = ops.int4_pack(w, group_size=group)
+            del w
+            a0 = bf16_tensor(g.standard_normal((r, k)).astype(np.float32) * 0.02, dev)
+            b0 = bf16_tensor(g.standard_normal((n, r)).astype(np.float32) * 0.02, dev)
+            pool = [(packed.clone(), scales.clone(), a0.clone(), b0.clone()) for _ in range(copies)]
+            for m in ms:
+                x = bf16_tensor(g.standard_normal((m, k)).astype(np.float32), dev)
+                calls = []
+                for i in range(batch):
+                    p, s, a, b = pool[i % copies]
+                    calls.append(lambda p=p, s=s, a=a, b=b: ops.int4lora_forward(
+                        x, p, s, a, b, scaling=2.0, group_size=group))
+                us = graph_time_per_call_ms(calls, replays=3) * 1e3
+                lat = []
+                for i in range(latency_calls):
+                    fn = calls[(i * 7) % batch]
+                    e0 = torch.cuda.Event(enable_timing=True)
+                    e1 = torch.cuda.Event(enable_timing=True)
+                    e0.record()
+                    fn()
+                    e1.record()
+                    e1.synchronize()
+                    lat.append(e0.elapsed_time(e1) * 1e3)
+                nbytes = n * k / 2 + n * n_groups * 2 + (r * k + n * r) * 2 + m * k * 2 + m * n * 2
+                out.append({"m": m, "k": k, "n": n, "group": group, "us_per_call": round(us, 2),
+                            "p50_us": round(float(np.median(lat)), 2),
+                            "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
+                            "frac_hbm": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
+            del pool
+            torch.cuda.empty_cache()
+    return {"workload": "skinny-M INT4 + LoRA r32 forward, Qwen3-2B projection shapes, group-64 "
+                        "and per-row scales; us_per_call inside a HIP graph of 96 calls cycling "
+                        "weight copies > 256 MB, p50_us over single eager calls", "points": out}
 
 
 def main():
