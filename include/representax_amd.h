@@ -114,6 +114,11 @@ int rpx_int4lora_backward(const void* grad, const void* x, int dtype, int64_t m,
                               BertMLP, src/representax/models/bert/model.py:249 */
 #define RPX_ACT_SILU_MUL 2 /* silu(gate) * z: the Qwen3 MLP's gated product,
                               src/representax/models/qwen3_vl/text.py:202 */
+#define RPX_ACT_ADD 3      /* backward only: dz = d + z, the input gradient added to
+                              the one accumulated so far for an input several
+                              linears share (JAX's cotangent sum of, e.g., the
+                              q/k/v projections' input, qwen3_vl/text.py and
+                              bert/model.py attention) */
 
 /* The FFN's up projection with its activation: z [m, n] = the linear's output
  * (as rpx_int4lora_forward's y), y [m, n] = gelu(z) (RPX_ACT_GELU) or
@@ -134,7 +139,9 @@ int rpx_int4lora_forward_act(const void* x, int dtype, int64_t m, int64_t k, con
  * down projection's input gradient (rpx_int4lora_backward's dx, rounded):
  *   RPX_ACT_GELU:     dz = d * gelu'(z);
  *   RPX_ACT_SILU_MUL: dz = d * silu(gate) (the up projection's gradient),
- *                     dgate = d * z * silu'(gate) (the gate projection's).
+ *                     dgate = d * z * silu'(gate) (the gate projection's);
+ *   RPX_ACT_ADD:      dz = d + z (z the gradient accumulated so far; dz must
+ *                     not alias z).
  * d_lora_a / d_lora_b as in rpx_int4lora_backward; workspace:
  * rpx_int4lora_backward_workspace. Replaces JAX's transpose of the same
  * expressions. */

@@ -89,6 +89,9 @@ def act_backward(activation: str, d, z, gate=None, compute: str = "bf16"):
     d = np.asarray(d, np.float64)
     if activation == "gelu":
         return rnd(d * gelu_grad(z)), None
+    if activation == "add":
+        # an input gradient added to the one accumulated so far (a shared input)
+        return rnd(d + np.asarray(z, np.float64)), None
     if activation == "silu_mul":
         z = np.asarray(z, np.float64)
         return rnd(d * silu(gate)), rnd(d * z * silu_grad(gate))

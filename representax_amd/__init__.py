@@ -18,7 +18,7 @@ from .adapters import (
 )
 from .components import Linear
 from .config import PrecisionConfig, QuantizedLoRAConfig
-from .mlp import gelu_mlp, swiglu_mlp
+from .mlp import gelu_mlp, shared_input_projections, swiglu_mlp
 from .precision import (
     FP32_POLICY,
     DelayedScaling,
@@ -51,5 +51,6 @@ __all__ = [
     "merge_quantized_lora",
     "precision_context",
     "resolve_precision_policy",
+    "shared_input_projections",
     "swiglu_mlp",
 ]

@@ -24,6 +24,7 @@ FP8_E4M3FN = 0
 FP8_E5M2 = 1
 ACT_GELU = 1
 ACT_SILU_MUL = 2
+ACT_ADD = 3
 
 _p = ctypes.c_void_p
 _i64 = ctypes.c_int64

@@ -1,5 +1,6 @@
 // Activations of the FFN steps on either side of a linear, evaluated in f32
-// from bf16 operands and rounded once by the caller:
+// from bf16 operands and rounded once by the caller (and the bf16 sum of two
+// input gradients of one shared input):
 //   GELU (exact, erf form): components.py:159-160, bert/model.py:249;
 //   SiLU-gated product silu(gate) * up: qwen3_vl/text.py:202.
 // The same functions serve the GEMM epilogues and the elementwise kernels,
@@ -17,6 +18,7 @@ enum ActMode : int {
   kActSiluMulFwd = 2,  // out = silu(gate) * v; v (the up projection) is stored too
   kActGeluBwd = 3,     // out = v * gelu'(z)
   kActSiluMulBwd = 4,  // out = v * silu(gate) (d up), out2 = v * up * silu'(gate) (d gate)
+  kActAddBwd = 5,      // out = v + z: an input gradient added to the one accumulated so far
 };
 
 constexpr float kInvSqrt2 = 0.70710678118654752440f;
@@ -87,6 +89,8 @@ __device__ __forceinline__ float act_apply(float v, float a0, float a1, float* s
     const float s = act_sigmoid(a0);
     *second = v * a1 * act_silu_grad(a0, s);
     return v * (a0 * s);
+  } else if constexpr (ACT == kActAddBwd) {
+    return v + a0;
   } else {
     return v;
   }

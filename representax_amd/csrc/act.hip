@@ -44,6 +44,10 @@ hipError_t launch_act(int mode, const uint16_t* v, const uint16_t* aux, const ui
       hipLaunchKernelGGL(k_act<kActGeluBwd>, dim3(grid), dim3(256), 0, stream, v, aux, aux2, count,
                          out, out2);
       break;
+    case kActAddBwd:
+      hipLaunchKernelGGL(k_act<kActAddBwd>, dim3(grid), dim3(256), 0, stream, v, aux, aux2, count,
+                         out, out2);
+      break;
     case kActSiluMulBwd:
       hipLaunchKernelGGL(k_act<kActSiluMulBwd>, dim3(grid), dim3(256), 0, stream, v, aux, aux2,
                          count, out, out2);

@@ -571,14 +571,16 @@ int rpx_int4lora_backward_act(const void* grad, const void* x, int dtype, int64_
                               const void* gate, void* dz, void* dgate, float* d_lora_a,
                               float* d_lora_b, void* workspace, size_t workspace_bytes,
                               void* stream) {
-  if (act != RPX_ACT_GELU && act != RPX_ACT_SILU_MUL)
+  if (act != RPX_ACT_GELU && act != RPX_ACT_SILU_MUL && act != RPX_ACT_ADD)
     return fail_invalid("rpx_int4lora_backward_act: unknown activation");
+  if (act == RPX_ACT_ADD && z == dz && z != nullptr)
+    return fail_invalid("rpx_int4lora_backward_act: dz must not alias z");
   if (dtype != kBF16) return fail_invalid("rpx_int4lora_backward_act: activations need bf16 compute");
   if (m > 0 && (z == nullptr || (act == RPX_ACT_SILU_MUL && (gate == nullptr || dgate == nullptr))))
     return fail_invalid("rpx_int4lora_backward_act: null pointer");
   ActIO io;
-  if (act == RPX_ACT_GELU) {
-    io.mode = kActGeluBwd;
+  if (act == RPX_ACT_GELU || act == RPX_ACT_ADD) {
+    io.mode = act == RPX_ACT_GELU ? kActGeluBwd : kActAddBwd;
     io.aux = static_cast<const uint16_t*>(z);
   } else {
     io.mode = kActSiluMulBwd;

@@ -721,6 +721,7 @@ hipError_t run_gemm_jb(const uint16_t* a, int64_t lda, const uint16_t* b, int64_
     } else {
       if (epi.act == kActGeluBwd) return RPX_RUN_ACT(kActGeluBwd);
       if (epi.act == kActSiluMulBwd) return RPX_RUN_ACT(kActSiluMulBwd);
+      if (epi.act == kActAddBwd) return RPX_RUN_ACT(kActAddBwd);
     }
   }
 #undef RPX_RUN_ACT

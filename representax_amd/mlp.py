@@ -1,5 +1,6 @@
 """Feed-forward blocks over INT4 + LoRA projections with the activation fused
-into the projections' GEMM epilogues.
+into the projections' GEMM epilogues, and projections of one shared input
+whose input gradients are summed in the dx GEMMs' epilogues.
 
 ``gelu_mlp`` is BertMLP's ``output(activate(input(hidden), "gelu"))``
 (src/representax/models/bert/model.py:243-249, activate at
@@ -65,4 +66,24 @@ def swiglu_mlp(value: torch.Tensor, gate: torch.nn.Module, up: torch.nn.Module,
     return y.reshape(*lead, down.output_size)
 
 
-__all__ = ["gelu_mlp", "swiglu_mlp"]
+def shared_input_projections(value: torch.Tensor, linears) -> list[torch.Tensor]:
+    """``[linear(value) for linear in linears]`` (e.g. the q / k / v
+    projections of attention, bert/model.py and qwen3_vl/text.py). When all
+    are INT4 + LoRA, the backward adds each input gradient to the running
+    sum inside its dx GEMM instead of in separate passes."""
+
+    linears = list(linears)
+    if not _fusable(value, *linears):
+        return [layer(value) for layer in linears]
+    x = activation_inputs(value).to(torch.bfloat16)
+    lead = x.shape[:-1]
+    views, leaves = [], []
+    for layer in linears:
+        views += list(_views(layer))
+        leaves += list(_leaves(layer))
+    outs = ops.Int4LoRASharedInputFn.apply(x.reshape(-1, linears[0].input_size), len(linears),
+                                           *views, *leaves)
+    return [y.reshape(*lead, layer.output_size) for y, layer in zip(outs, linears)]
+
+
+__all__ = ["gelu_mlp", "shared_input_projections", "swiglu_mlp"]

@@ -182,7 +182,7 @@ def int4lora_backward(grad, x2d, packed, scale_bits, lora_a_c, lora_b_c, h, *, s
     return dx, d_a, d_b
 
 
-ACTIVATIONS = {"gelu": nat.ACT_GELU, "silu_mul": nat.ACT_SILU_MUL}
+ACTIVATIONS = {"gelu": nat.ACT_GELU, "silu_mul": nat.ACT_SILU_MUL, "add": nat.ACT_ADD}
 
 
 def int4lora_forward_act(x2d, packed, scale_bits, lora_a_c, lora_b_c, *, activation: str,
@@ -221,7 +221,9 @@ def int4lora_backward_act(grad, x2d, packed, scale_bits, lora_a_c, lora_b_c, h, 
                           group_size: int | None = None):
     """The FFN's down projection backward followed by the activation's:
     ``(dz, dgate or None, dA f32, dB f32)``; x2d is the down projection's
-    input, z (and gate) the activation's forward operands."""
+    input, z (and gate) the activation's forward operands. With
+    ``activation="add"`` it is any linear's backward whose input gradient is
+    added to ``z``, the gradient accumulated so far for a shared input."""
 
     act = ACTIVATIONS[activation]
     device = _on_device(grad, x2d, packed, scale_bits, lora_a_c, lora_b_c, h, z, gate)
@@ -345,12 +347,68 @@ class Int4LoRASwiGLUMLPFn(torch.autograd.Function):
             z=u, gate=g, scaling=down_scaling, group_size=down_group)
         dx_up, d_up_a, d_up_b = int4lora_backward(du, x2d, up_packed, up_scales, up_a, up_b, h_up,
                                                   scaling=up_scaling, group_size=up_group)
-        dx_gate, d_gate_a, d_gate_b = int4lora_backward(dg, x2d, gate_packed, gate_scales, gate_a,
-                                                        gate_b, h_gate, scaling=gate_scaling,
-                                                        group_size=gate_group)
-        return (dx_up + dx_gate, d_gate_a.to(gate_a.dtype), d_gate_b.to(gate_b.dtype),
+        # the gate projection's input gradient is added to the up projection's
+        # in the dx GEMM's epilogue
+        dx, _, d_gate_a, d_gate_b = int4lora_backward_act(
+            dg, x2d, gate_packed, gate_scales, gate_a, gate_b, h_gate, activation="add", z=dx_up,
+            scaling=gate_scaling, group_size=gate_group)
+        return (dx, d_gate_a.to(gate_a.dtype), d_gate_b.to(gate_b.dtype),
                 d_up_a.to(up_a.dtype), d_up_b.to(up_b.dtype), d_down_a.to(down_a.dtype),
                 d_down_b.to(down_b.dtype)) + (None,) * 15
+
+
+class Int4LoRASharedInputFn(torch.autograd.Function):
+    """Several INT4 + LoRA linears of one input (the q / k / v projections):
+    the forward runs them one after another; in the backward every input
+    gradient after the first is added to the running sum in its dx GEMM's
+    epilogue (bf16, in projection order) instead of by a separate pass.
+
+    Arguments: x2d, the count n, the n pairs of LoRA compute views, then per
+    linear packed, scale_bits, bias_bits, scaling, group_size.
+    """
+
+    @staticmethod
+    def forward(ctx, x2d, n, *args):
+        views = args[:2 * n]
+        leaves = args[2 * n:]
+        outs, hs = [], []
+        for i in range(n):
+            packed, scales, bias, scaling, group = leaves[5 * i:5 * i + 5]
+            y, h = int4lora_forward(x2d, packed, scales, views[2 * i], views[2 * i + 1],
+                                    scaling=scaling, group_size=group, bias_bits=bias)
+            outs.append(y)
+            hs.append(h)
+        ctx.n = n
+        ctx.cfg = [(leaves[5 * i + 3], leaves[5 * i + 4]) for i in range(n)]
+        ctx.save_for_backward(x2d, *views, *[leaves[5 * i] for i in range(n)],
+                              *[leaves[5 * i + 1] for i in range(n)], *hs)
+        return tuple(outs)
+
+    @staticmethod
+    def backward(ctx, *grads):
+        n = ctx.n
+        saved = ctx.saved_tensors
+        x2d = saved[0]
+        views = saved[1:1 + 2 * n]
+        packed = saved[1 + 2 * n:1 + 3 * n]
+        scales = saved[1 + 3 * n:1 + 4 * n]
+        hs = saved[1 + 4 * n:1 + 5 * n]
+        dx = None
+        dviews = []
+        for i in range(n):
+            a, b = views[2 * i], views[2 * i + 1]
+            scaling, group = ctx.cfg[i]
+            g = grads[i] if grads[i] is not None else torch.zeros(
+                (x2d.shape[0], packed[i].shape[-2]), dtype=x2d.dtype, device=x2d.device)
+            if dx is None:
+                dx, d_a, d_b = int4lora_backward(g, x2d, packed[i], scales[i], a, b, hs[i],
+                                                 scaling=scaling, group_size=group)
+            else:
+                dx, _, d_a, d_b = int4lora_backward_act(
+                    g, x2d, packed[i], scales[i], a, b, hs[i], activation="add", z=dx,
+                    scaling=scaling, group_size=group)
+            dviews += [d_a.to(a.dtype), d_b.to(b.dtype)]
+        return (dx, None, *dviews) + (None,) * (5 * n)
 
 
 # ---------------------------------------------------------------------------

@@ -34,7 +34,7 @@ import torch.nn.functional as F
 from .adapters import apply_quantized_lora, lora_parameters
 from .components import Linear
 from .config import PrecisionConfig
-from .mlp import gelu_mlp, swiglu_mlp
+from .mlp import gelu_mlp, shared_input_projections, swiglu_mlp
 from .precision import precision_context, resolve_precision_policy
 
 
@@ -147,11 +147,9 @@ class BertSelfAttention(torch.nn.Module):
     def forward(self, hidden: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor:
         b, s, h = hidden.shape
 
-        def project(layer):
-            return layer(hidden).reshape(b, s, self.heads, self.head_dim).transpose(1, 2)
-
-        out = attention(project(self.query), project(self.key), project(self.value), bias,
-                        1.0 / math.sqrt(self.head_dim))
+        q, k, v = (t.reshape(b, s, self.heads, self.head_dim).transpose(1, 2)
+                   for t in shared_input_projections(hidden, (self.query, self.key, self.value)))
+        out = attention(q, k, v, bias, 1.0 / math.sqrt(self.head_dim))
         return self.output(out.transpose(1, 2).reshape(b, s, h))
 
 
@@ -329,9 +327,10 @@ class Qwen3Attention(torch.nn.Module):
 
     def forward(self, hidden, cos, sin):
         b, s, _ = hidden.shape
-        q = self.query_norm(self.query(hidden).reshape(b, s, self.heads, self.head_dim))
-        k = self.key_norm(self.key(hidden).reshape(b, s, self.kv_heads, self.head_dim))
-        v = self.value(hidden).reshape(b, s, self.kv_heads, self.head_dim)
+        q, k, v = shared_input_projections(hidden, (self.query, self.key, self.value))
+        q = self.query_norm(q.reshape(b, s, self.heads, self.head_dim))
+        k = self.key_norm(k.reshape(b, s, self.kv_heads, self.head_dim))
+        v = v.reshape(b, s, self.kv_heads, self.head_dim)
         cos, sin = cos[:, :, None], sin[:, :, None]
         q = (q.float() * cos + _rotate_half(q.float()) * sin).to(hidden.dtype)
         k = (k.float() * cos + _rotate_half(k.float()) * sin).to(hidden.dtype)

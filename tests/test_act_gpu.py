@@ -111,7 +111,7 @@ BWD_SHAPES = [(512, 384, 256, 16, 64), (300, 192, 128, 8, None), (8, 256, 192, 1
               (37, 100, 52, 3, None), (256, 256, 128, 48, 64)]
 
 
-@pytest.mark.parametrize("activation", ["gelu", "silu_mul"])
+@pytest.mark.parametrize("activation", ["gelu", "silu_mul", "add"])
 @pytest.mark.parametrize("m,k,n,r,group", BWD_SHAPES)
 def test_backward_act_matches_oracle(activation, m, k, n, r, group):
     g = rng(m + k + (11 if activation == "gelu" else 13))
@@ -147,6 +147,38 @@ def test_backward_act_matches_oracle(activation, m, k, n, r, group):
                                      p["lora_b"], from_dev(h), alpha=p["alpha"], rank=r,
                                      group_size=group)
     assert rel_l2(dxg, dx_o) < TOL
+
+
+@pytest.mark.parametrize("m,k,n,r,group", [(256, 128, 192, 8, 64), (37, 100, 52, 3, None)])
+def test_shared_input_projections_match_separate_linears(m, k, n, r, group):
+    """q / k / v of one input: outputs and LoRA gradients equal the separate
+    linears' bit for bit; the input gradient equals the bf16 sum of theirs in
+    projection order, bit for bit (fused GEMM and generic paths)."""
+
+    g = rng(m + 3 * n)
+    ps = [_linear(g, n, k, r, group, bias=True, b_scale=10.0) for _ in range(3)]
+    dv = [_dev(p) for p in ps]
+    x = to_dev_bf16(bf16_values(g.standard_normal((m, k))))
+    gys = [to_dev_bf16(bf16_values(g.standard_normal((m, n)))) for _ in range(3)]
+    views, leaves = [], []
+    for d in dv:
+        views += [d["a"].clone().requires_grad_(True), d["b"].clone().requires_grad_(True)]
+        leaves += [d["packed"], d["scale_bits"], d["bias"], d["scaling"], d["group"]]
+    xd = x.clone().requires_grad_(True)
+    outs = ops.Int4LoRASharedInputFn.apply(xd, 3, *views, *leaves)
+    grads = torch.autograd.grad(outs, [xd] + views, gys)
+    dx_sum = None
+    for i, d in enumerate(dv):
+        y, h = ops.int4lora_forward(x, d["packed"], d["scale_bits"], d["a"], d["b"],
+                                    scaling=d["scaling"], group_size=d["group"], bias_bits=d["bias"])
+        assert torch.equal(outs[i], y)
+        dx, d_a, d_b = ops.int4lora_backward(gys[i], x, d["packed"], d["scale_bits"], d["a"],
+                                             d["b"], h, scaling=d["scaling"], group_size=d["group"])
+        assert torch.equal(grads[1 + 2 * i], d_a.to(torch.bfloat16))
+        assert torch.equal(grads[2 + 2 * i], d_b.to(torch.bfloat16))
+        dx_sum = dx if dx_sum is None else (dx_sum.float() + dx.float()).to(torch.bfloat16)
+    torch.cuda.synchronize()
+    assert torch.equal(grads[0], dx_sum)
 
 
 def _mlp_params(g, k, f, r, group, names):

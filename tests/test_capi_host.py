@@ -83,6 +83,9 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     with pytest.raises(ValueError, match="rank"):
         nat.call("rpx_int4lora_backward_act", p, p, nat.DTYPE_BF16, 2, 8, p, p, 6, 0, p, p, 7,
                  ctypes.c_float(1.0), p, nat.ACT_GELU, p, None, p, None, p, p, None, 0, None)
+    with pytest.raises(ValueError, match="alias"):
+        nat.call("rpx_int4lora_backward_act", p, p, nat.DTYPE_BF16, 2, 8, p, p, 6, 0, p, p, 2,
+                 ctypes.c_float(1.0), p, nat.ACT_ADD, p, None, p, None, p, p, None, 0, None)
 
 
 def _host_quantize(x: np.ndarray, scale: float, fmt: int) -> np.ndarray:

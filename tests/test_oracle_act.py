@@ -58,6 +58,9 @@ def test_act_rounds_once_to_bf16():
     np.testing.assert_array_equal(oact.act_forward("silu_mul", z, gate),
                                   bf16_round(oact.silu(gate) * z))
     d = bf16_round(g.standard_normal(1000))
+    dsum, none = oact.act_backward("add", d, z)
+    assert none is None
+    np.testing.assert_array_equal(dsum, bf16_round(d.astype(np.float64) + z))
     du, dg = oact.act_backward("silu_mul", d, z, gate)
     np.testing.assert_array_equal(du, bf16_round(d * oact.silu(gate)))
     np.testing.assert_array_equal(dg, bf16_round(d * z * oact.silu_grad(gate)))
