@@ -432,9 +432,10 @@ int int4lora_backward_impl(const void* grad, const void* x, int dtype, int64_t m
   if (m < 0) return fail_invalid("m must be non-negative");
   if (rank < 1 || rank > n || rank > k) return fail_invalid("adapter rank must fit both linear dimensions");
   if (grad == nullptr && m > 0) return fail_invalid("rpx_int4lora_backward: null gradient");
-  if (x == nullptr || packed == nullptr || scale_bits == nullptr || lora_a == nullptr ||
-      lora_b == nullptr || dx == nullptr || d_lora_a == nullptr || d_lora_b == nullptr ||
-      (h == nullptr && m > 0))
+  // an empty batch has no rows to point at: x, dx and h may be null then
+  if (packed == nullptr || scale_bits == nullptr || lora_a == nullptr || lora_b == nullptr ||
+      d_lora_a == nullptr || d_lora_b == nullptr ||
+      (m > 0 && (x == nullptr || dx == nullptr || h == nullptr)))
     return fail_invalid("rpx_int4lora_backward: null pointer");
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (m == 0) {

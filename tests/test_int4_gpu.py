@@ -337,3 +337,49 @@ def test_skinny_graph_replays_and_repeats_are_bit_identical(m, k):
         ye, _ = call()
         torch.cuda.synchronize()
         assert torch.equal(ye, y0)
+
+
+@pytest.mark.parametrize("group", [None, 64])
+def test_int4lora_empty_batch(group):
+    """Zero tokens: empty outputs and all-zero adapter gradients, as the
+    reference's dense product over an empty batch gives; the empty tensors'
+    null data pointers are accepted."""
+
+    k, n, r = 256, 192, 16
+    _, packed, scales, a, b, bias_bits, _ = _lora_case(1, k, n, r, group, seed=44)
+    pd = to_dev(packed)
+    sd = to_dev(scales.view(np.int16)).view(torch.uint16)
+    ad = to_dev_bf16(a)
+    bd = to_dev_bf16(b)
+    biasd = to_dev(bias_bits.view(np.int16)).view(torch.uint16)
+    x = torch.empty((0, k), dtype=torch.bfloat16, device="cuda")
+    gy = torch.empty((0, n), dtype=torch.bfloat16, device="cuda")
+    y, h = ops.int4lora_forward(x, pd, sd, ad, bd, scaling=2.0, group_size=group, bias_bits=biasd)
+    dx, da, db = ops.int4lora_backward(gy, x, pd, sd, ad, bd, h, scaling=2.0, group_size=group)
+    dz, dgate, da2, db2 = ops.int4lora_backward_act(gy, x, pd, sd, ad, bd, h, activation="gelu",
+                                                    z=torch.empty((0, k), dtype=torch.bfloat16,
+                                                                  device="cuda"),
+                                                    scaling=2.0, group_size=group)
+    torch.cuda.synchronize()
+    assert y.shape == (0, n) and h.shape == (0, r) and dx.shape == (0, k) and dz.shape == (0, k)
+    assert dgate is None
+    for t, shape in ((da, (r, k)), (db, (n, r)), (da2, (r, k)), (db2, (n, r))):
+        assert t.shape == shape and t.dtype == torch.float32
+        assert torch.count_nonzero(t).item() == 0
+
+
+def test_module_empty_batch_gradients_are_zero():
+    import representax_amd as rx
+
+    lin = rx.Linear.init(256, 192, key=1, scale=0.02, bias=True, device="cuda")
+    layer = rx.QuantizedLoRALinear.from_linear(lin, rank=16, alpha=32.0, key=3)
+    x = torch.empty((0, 256), dtype=torch.bfloat16, device="cuda", requires_grad=True)
+    bf = rx.resolve_precision_policy(rx.PrecisionConfig.bfloat16_mixed())
+    with rx.precision_context(bf):
+        y = layer(x)
+    y.sum().backward()
+    torch.cuda.synchronize()
+    assert y.shape == (0, 192)
+    assert x.grad.shape == (0, 256)
+    assert torch.count_nonzero(layer.lora_a.grad).item() == 0
+    assert torch.count_nonzero(layer.lora_b.grad).item() == 0
