@@ -188,7 +188,8 @@ size_t rpx_fp8_linear_forward_workspace(int64_t m, int64_t n, int64_t k);
  * right is addressed through (row_stride, col_stride) so a transposed weight
  * view needs no copy. scales_out[0..1] receive (s_left, s_right). The same
  * pass can also write the backward's operand codes: left_t_codes [k, m] and
- * right_codes [k, n] (either may be NULL). Replaces _fp8_linear_dot /
+ * right_codes [k, n] (either may be NULL). m, n, k > 0: an empty operand has
+ * no amax, and the reference's max reduction raises on it. Replaces _fp8_linear_dot /
  * _fp8_linear_dot_forward, src/representax/precision.py:173-198 (as used by
  * linear_matmul, :224-239). */
 int rpx_fp8_linear_forward(const void* left, int left_dtype, int64_t m, int64_t k,

@@ -764,8 +764,10 @@ int rpx_fp8_linear_forward(const void* left, int left_dtype, int64_t m, int64_t 
   RPX_TRY(check_dtype(out_dtype));
   if (m < 0 || n < 0 || k < 0) return fail_invalid("m, n, k must be non-negative");
   if (scales_out == nullptr) return fail_invalid("rpx_fp8_linear_forward: null scales_out");
-  if (m == 0 || n == 0) return kOk;
-  if (k == 0) return fail_invalid("rpx_fp8_linear_forward: empty contraction");
+  // the dynamic scale of an empty operand is undefined: the reference's
+  // amax (a max reduction with no identity) raises on it too
+  if (m == 0 || n == 0 || k == 0)
+    return fail_invalid("rpx_fp8_linear_forward: empty operand (no amax to scale by)");
   if (left == nullptr || right == nullptr || out == nullptr)
     return fail_invalid("rpx_fp8_linear_forward: null pointer");
   hipStream_t st = static_cast<hipStream_t>(stream);

@@ -117,3 +117,15 @@ def test_device_quantizer_on_host_random_f32():
     for s in (np.float32(1e-3), np.float32(2.5), np.float32(7e4)):
         for fmt, name in ((nat.FP8_E4M3FN, "e4m3fn"), (nat.FP8_E5M2, "e5m2")):
             assert np.array_equal(_host_quantize(x, s, fmt), ofp8.cast_with_scale(x, s, name))
+
+
+def test_fp8_linear_forward_rejects_empty_operands():
+    """The reference's dynamic scale takes jnp.max over the operand, which
+    raises on an empty array (precision.py:133-137); the C-ABI refuses an
+    empty operand before any launch."""
+
+    p = ctypes.c_void_p(16)
+    for m, k, n in ((0, 8, 8), (8, 0, 8), (8, 8, 0)):
+        with pytest.raises(ValueError, match="empty operand"):
+            nat.call("rpx_fp8_linear_forward", p, nat.DTYPE_BF16, m, k, p, nat.DTYPE_BF16, n, n, 1,
+                     p, nat.DTYPE_BF16, p, None, None, p, 1 << 20, None)
