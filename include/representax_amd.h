@@ -5,9 +5,10 @@
  * Conventions
  *   - Every pointer is a device pointer unless the name says host.
  *   - `stream` is a hipStream_t (NULL = the legacy default stream). All work
- *     is enqueued on it; no entry point synchronizes or allocates device
- *     memory. Scratch comes from the caller's `workspace`, sized by the
- *     matching *_workspace() query.
+ *     is enqueued on it; no entry point allocates device memory, and none
+ *     synchronizes except the diagnostic rpx_check_device_errors. Scratch
+ *     comes from the caller's `workspace`, sized by the matching
+ *     *_workspace() query.
  *   - bf16 tensors are passed as their 16-bit patterns; fp8 tensors as uint8
  *     codes in the OCP e4m3fn / e5m2 encodings.
  *   - Matrices are row-major and dense unless strides are given.
@@ -34,6 +35,7 @@ extern "C" {
 #define RPX_OK 0
 #define RPX_ERR_INVALID 1
 #define RPX_ERR_HIP 2
+#define RPX_ERR_DEVICE 3 /* a kernel reported a problem (rpx_check_device_errors) */
 
 #define RPX_DTYPE_F32 0
 #define RPX_DTYPE_BF16 1
@@ -43,6 +45,53 @@ extern "C" {
 
 const char* rpx_last_error(void);
 int rpx_abi_version(void);
+
+/* ---------------------------------------------------------------------------
+ * Kernel-variant overrides ("knobs"), process-wide, for tests that cover every
+ * tile shape and for tuning sweeps. No reference counterpart (XLA picks its
+ * own kernels). Each knob starts from its environment variable, read once;
+ * rpx_set_tuning applies to calls that start after it. Workspace queries
+ * follow the knobs too, so a knob must not change between a *_workspace()
+ * query and the call it sizes.
+ *   RPX_TUNE_INT4_TILE   INT4 fused GEMM tile: 0 planner, 1 256x128, 2 128x128
+ *                        (stages by scale footprint), 3 64x128, 7 256x256,
+ *                        10 128x128 two stages, 11 128x128 three stages
+ *                        (env RPX_GEMM_TILE)
+ *   RPX_TUNE_BF16_TILE   bf16 GEMM tile: 0 planner, 4 256x128, 5 128x128,
+ *                        6 64x128, 8 256x256, 9 128x96 (env RPX_GEMM_TILE)
+ *   RPX_TUNE_FP8_TILE    fp8 GEMM tile: 0 planner, 1..11 (env RPX_FP8_TILE)
+ *   RPX_TUNE_SKINNY_TILE one-launch skinny tile: 0 planner, 1..14; a nonzero
+ *                        value also turns the two-launch form off
+ *                        (env RPX_SKINNY_TILE)
+ *   RPX_TUNE_SKINNY2     two-launch skinny form: -1 planner (M <= 4), 0 never,
+ *                        1 for every M <= 16 (env RPX_SKINNY2)
+ *   RPX_TUNE_SKINNY2_ONE M <= 4 form: -1 planner (one launch for K >= 4096),
+ *                        0 two launches, 1 one launch (env RPX_SKINNY2_ONE)
+ *   RPX_TUNE_SPIN_LIMIT  polls of the skinny kernels' bounded cross-block
+ *                        waits (0: the default limit)
+ * ------------------------------------------------------------------------- */
+#define RPX_TUNE_INT4_TILE 0
+#define RPX_TUNE_BF16_TILE 1
+#define RPX_TUNE_FP8_TILE 2
+#define RPX_TUNE_SKINNY_TILE 3
+#define RPX_TUNE_SKINNY2 4
+#define RPX_TUNE_SKINNY2_ONE 5
+#define RPX_TUNE_SPIN_LIMIT 6
+
+/* RPX_ERR_INVALID for an unknown knob or value. */
+int rpx_set_tuning(int knob, int value);
+/* Current value (0 for an unknown knob). */
+int rpx_get_tuning(int knob);
+
+/* Kernels with bounded cross-block waits (the one-launch skinny-M forward)
+ * raise a bit in a per-device error word when a wait expires; that call's
+ * outputs then hold NaN instead of hanging. This synchronizes `stream`, reads
+ * and clears the current device's word, and returns RPX_ERR_DEVICE (with a
+ * message naming the kernel) if any bit was set; flags_out (host, may be
+ * NULL) receives the bits: 1 = skinny M <= 64 adapter arrivals, 2 = skinny
+ * M <= 4 published h. Synchronizes, so it must not be called during graph
+ * capture. No reference counterpart (XLA's kernels have no cross-block waits). */
+int rpx_check_device_errors(void* stream, uint32_t* flags_out);
 
 /* ---------------------------------------------------------------------------
  * Packed INT4 weights.
@@ -76,6 +125,13 @@ int rpx_int4_merge(const uint8_t* packed, const uint16_t* scale_bits, const floa
  * views lora_a [rank, k] / lora_b [n, rank], y, h, grad and dx. `scaling` is
  * alpha / rank; it is rounded to the compute dtype like the reference's weakly
  * typed Python scalar. bias_bits (bf16 bits [n]) may be NULL.
+ * Shapes that take the vectorized kernels (bf16, k a multiple of 64, rank <= 64,
+ * per-row scales or power-of-two groups >= 32; the backward also needs n a
+ * multiple of 64) need x, packed, scale_bits, lora_a and y (backward: grad, x,
+ * packed, scale_bits, lora_a, lora_b and dx) 16-byte aligned, as every
+ * hipMalloc'd buffer is; the *_workspace() queries size those kernels'
+ * scratch from the shape alone, and a misaligned call is rejected with
+ * RPX_ERR_INVALID.
  * ------------------------------------------------------------------------- */
 
 size_t rpx_int4lora_forward_workspace(int64_t m, int64_t n, int64_t k, int64_t group_size,
@@ -102,6 +158,44 @@ int rpx_int4lora_backward(const void* grad, const void* x, int dtype, int64_t m,
                           int64_t group_size, const void* lora_a, const void* lora_b,
                           int64_t rank, float scaling, const void* h, void* dx, float* d_lora_a,
                           float* d_lora_b, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * INT4 base + LoRA linear without a precision policy, on bf16 activations
+ * with the float32 adapter masters: the reference then multiplies bf16 x
+ * (bf16 base) -> bf16, but jnp.matmul promotes bf16 x float32 to float32, so
+ * h = f32(x A^T), the adapter term and the module output are float32:
+ *   y [m, n] f32 = f32(bf16(x W_b^T)) + f32(f32(h B^T) * scaling) (+ f32(bias))
+ * with scaling = float32(alpha / rank) (not rounded to bf16). Replaces
+ * QuantizedLoRALinear.__call__, src/representax/models/adapters.py:158-182,
+ * with compute_parameter returning the masters unchanged
+ * (src/representax/precision.py:111-117), as in inference without a
+ * precision context (src/representax/inference.py:17-23).
+ * ------------------------------------------------------------------------- */
+
+size_t rpx_int4lora_forward_promoted_workspace(int64_t m, int64_t n, int64_t k,
+                                               int64_t group_size, int64_t rank);
+
+int rpx_int4lora_forward_promoted(const uint16_t* x, int64_t m, int64_t k, const uint8_t* packed,
+                                  const uint16_t* scale_bits, int64_t n, int64_t group_size,
+                                  const uint16_t* bias_bits, const float* lora_a,
+                                  const float* lora_b, int64_t rank, float scaling, float* y,
+                                  float* h, void* workspace, size_t workspace_bytes,
+                                  void* stream);
+
+size_t rpx_int4lora_backward_promoted_workspace(int64_t m, int64_t n, int64_t k,
+                                                int64_t group_size, int64_t rank);
+
+/* JAX's transpose of the promoted forward, grad [m, n] f32 (the float32
+ * output's cotangent): dx [m, k] bf16 = bf16(bf16(bf16(g) W_b) +
+ * bf16(f32(dh A))) with dh = f32(f32(g * scaling) B); d_lora_a = f32(dh^T x),
+ * d_lora_b = f32(f32(g * scaling)^T h), both float32 (no bf16 rounding).
+ * Replaces JAX's transpose of src/representax/models/adapters.py:162-181. */
+int rpx_int4lora_backward_promoted(const float* grad, const uint16_t* x, int64_t m, int64_t k,
+                                   const uint8_t* packed, const uint16_t* scale_bits, int64_t n,
+                                   int64_t group_size, const float* lora_a, const float* lora_b,
+                                   int64_t rank, float scaling, const float* h, uint16_t* dx,
+                                   float* d_lora_a, float* d_lora_b, void* workspace,
+                                   size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------
  * Activation epilogues: the FFN steps on either side of an INT4 + LoRA linear,

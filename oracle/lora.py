@@ -18,6 +18,25 @@ hand-written VJP for this path): with ``c = dtype(alpha / rank)``
 
 where ``rnd`` rounds to the compute dtype. The packed base and the bias are
 integer leaves and receive no gradient.
+
+``compute="promoted"`` is the reference without a precision policy on bf16
+activations (``compute_parameter`` then returns the fp32 masters unchanged,
+precision.py:111-117): the base product is bf16 x bf16 -> bf16, but
+``jnp.matmul`` promotes bf16 x f32 to f32, so the adapter runs in float32 on
+the unrounded masters and the sum (and the module output) is float32:
+
+* ``base = bf16(x @ W^T)``, ``h = f32(x @ A^T)``, ``a = f32(h @ B^T)``
+* ``y = f32(f32(base) + f32(a * c))`` with ``c = f32(alpha / rank)``,
+  then ``y = f32(y + bias)``
+
+and JAX's transpose of it, with ``g`` the float32 output cotangent:
+
+* ``dx = bf16(bf16(bf16(g) @ W) + bf16(f32(dh @ A)))``, ``dh = f32(g_a @ B)``,
+  ``g_a = f32(g * c)``
+* ``dB = f32(g_a^T @ h)``, ``dA = f32(dh^T @ x)``
+
+(the bf16 matmul's cotangent is bf16; the adapter's arrives through the
+transpose of the bf16 -> f32 convert of x; the two are summed in bf16).
 """
 
 from __future__ import annotations
@@ -39,7 +58,13 @@ def _rounder(compute: str):
         return lambda v: np.asarray(v, dtype=np.float32)
     if compute == "f64":
         return lambda v: np.asarray(v, dtype=np.float64)
+    if compute == "promoted":
+        return lambda v: np.asarray(v, dtype=np.float32)
     raise ValueError(compute)
+
+
+def _f32(v):
+    return np.asarray(v, dtype=np.float32)
 
 
 def _master(v, compute: str):
@@ -80,6 +105,9 @@ def lora_forward(
     may pass a precomputed dequantized base ``[N, K]``.
     """
 
+    if compute == "promoted":
+        return _promoted_forward(x, packed, scale_bits, lora_a, lora_b, alpha, rank, bias_bits,
+                                 group_size, acc, weight)
     rnd = _rounder(compute)
     x = rnd(x)
     k = x.shape[-1]
@@ -111,9 +139,17 @@ def lora_backward(
     compute: str = "bf16",
     acc=np.float64,
     weight=None,
+    dx_rows=None,
 ):
-    """Return ``(dx, dA, dB)``: dx in the compute dtype, dA/dB as float32."""
+    """Return ``(dx, dA, dB)``: dx in the compute dtype, dA/dB as float32.
 
+    ``dx_rows`` (an index array) restricts dx to those rows of the batch (dx
+    is row-separable); dA and dB always reduce over the whole batch.
+    """
+
+    if compute == "promoted":
+        return _promoted_backward(g, x, packed, scale_bits, lora_a, lora_b, h, alpha, rank,
+                                  group_size, acc, weight, dx_rows)
     rnd = _rounder(compute)
     g = rnd(g)
     x = rnd(x)
@@ -125,8 +161,48 @@ def lora_backward(
     g_a = rnd(g * c)
     dh = rnd(_dot(g_a, b_c, acc))
     d_b = _master(rnd(_dot(g_a.T, h, acc)), compute)
-    dx = rnd(rnd(_dot(g, w, acc)) + rnd(_dot(dh, a_c, acc)))
+    if dx_rows is not None:
+        dx = rnd(rnd(_dot(g[dx_rows], w, acc)) + rnd(_dot(dh[dx_rows], a_c, acc)))
+    else:
+        dx = rnd(rnd(_dot(g, w, acc)) + rnd(_dot(dh, a_c, acc)))
     d_a = _master(rnd(_dot(dh.T, x, acc)), compute)
+    return dx, d_a, d_b
+
+
+def _promoted_forward(x, packed, scale_bits, lora_a, lora_b, alpha, rank, bias_bits, group_size,
+                      acc, weight):
+    x = bf16_round(x)
+    k = x.shape[-1]
+    w = dequant_int4(packed, scale_bits, k, group_size) if weight is None else weight
+    a = _f32(lora_a)
+    b = _f32(lora_b)
+    c = np.float32(alpha / rank)
+    base = bf16_round(_dot(x, w.T, acc))
+    h = _f32(_dot(x, a.T, acc))
+    a_out = _f32(_dot(h, b.T, acc))
+    y = _f32(base + _f32(a_out * c))
+    if bias_bits is not None:
+        y = _f32(y + bf16_bits_to_f32(bias_bits))
+    return y, h
+
+
+def _promoted_backward(g, x, packed, scale_bits, lora_a, lora_b, h, alpha, rank, group_size, acc,
+                       weight, dx_rows):
+    g = _f32(g)
+    x = bf16_round(x)
+    k = x.shape[-1]
+    w = dequant_int4(packed, scale_bits, k, group_size) if weight is None else weight
+    a = _f32(lora_a)
+    b = _f32(lora_b)
+    c = np.float32(alpha / rank)
+    g_a = _f32(g * c)
+    dh = _f32(_dot(g_a, b, acc))
+    d_b = _f32(_dot(g_a.T, h, acc))
+    rows = slice(None) if dx_rows is None else dx_rows
+    dx_base = bf16_round(_dot(bf16_round(g[rows]), w, acc))
+    dx_adapter = bf16_round(_f32(_dot(dh[rows], a, acc)))
+    dx = bf16_round(dx_base + dx_adapter)
+    d_a = _f32(_dot(dh.T, x, acc))
     return dx, d_a, d_b
 
 

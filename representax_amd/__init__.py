@@ -25,11 +25,14 @@ from .precision import (
     PrecisionPolicy,
     activation_inputs,
     active_compute_dtype,
+    active_model_for_compute,
     compute_parameter,
     linear_matmul,
+    model_for_compute,
     precision_context,
     resolve_precision_policy,
 )
+from .sharding import activation_out_sharding, constrain_activation, replicate
 
 __all__ = [
     "DelayedScaling",
@@ -40,16 +43,21 @@ __all__ = [
     "QuantizedLoRAConfig",
     "QuantizedLoRALinear",
     "activation_inputs",
+    "activation_out_sharding",
     "active_compute_dtype",
+    "active_model_for_compute",
     "apply_quantized_lora",
     "compute_parameter",
+    "constrain_activation",
     "gelu_mlp",
     "linear_matmul",
     "lora_parameter_filter",
     "lora_parameters",
     "matched_linear_paths",
     "merge_quantized_lora",
+    "model_for_compute",
     "precision_context",
+    "replicate",
     "resolve_precision_policy",
     "shared_input_projections",
     "swiglu_mlp",

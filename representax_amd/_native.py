@@ -18,6 +18,7 @@ LIB_PATH = Path(__file__).resolve().parent / "_lib" / "librepresentax_amd.so"
 RPX_OK = 0
 RPX_ERR_INVALID = 1
 RPX_ERR_HIP = 2
+RPX_ERR_DEVICE = 3
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 FP8_E4M3FN = 0
@@ -25,6 +26,14 @@ FP8_E5M2 = 1
 ACT_GELU = 1
 ACT_SILU_MUL = 2
 ACT_ADD = 3
+# kernel-variant knobs (rpx_set_tuning)
+TUNE_INT4_TILE = 0
+TUNE_BF16_TILE = 1
+TUNE_FP8_TILE = 2
+TUNE_SKINNY_TILE = 3
+TUNE_SKINNY2 = 4
+TUNE_SKINNY2_ONE = 5
+TUNE_SPIN_LIMIT = 6
 
 _p = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -36,6 +45,9 @@ _size = ctypes.c_size_t
 SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "rpx_last_error": (ctypes.c_char_p, []),
     "rpx_abi_version": (_int, []),
+    "rpx_set_tuning": (_int, [_int, _int]),
+    "rpx_get_tuning": (_int, [_int]),
+    "rpx_check_device_errors": (_int, [_p, _p]),
     "rpx_int4_pack": (_int, [_p, _int, _i64, _i64, _i64, _p, _p, _p]),
     "rpx_int4_dequant": (_int, [_p, _p, _i64, _i64, _i64, _p, _p]),
     "rpx_int4_merge": (_int, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _f32, _p, _p]),
@@ -59,6 +71,17 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _int,
         [_p, _p, _int, _i64, _i64, _p, _p, _i64, _i64, _p, _p, _i64, _f32, _p, _int, _p, _p, _p,
          _p, _p, _p, _p, _size, _p],
+    ),
+    "rpx_int4lora_forward_promoted_workspace": (_size, [_i64, _i64, _i64, _i64, _i64]),
+    "rpx_int4lora_forward_promoted": (
+        _int,
+        [_p, _i64, _i64, _p, _p, _i64, _i64, _p, _p, _p, _i64, _f32, _p, _p, _p, _size, _p],
+    ),
+    "rpx_int4lora_backward_promoted_workspace": (_size, [_i64, _i64, _i64, _i64, _i64]),
+    "rpx_int4lora_backward_promoted": (
+        _int,
+        [_p, _p, _i64, _i64, _p, _p, _i64, _i64, _p, _p, _i64, _f32, _p, _p, _p, _p, _p, _size,
+         _p],
     ),
     "rpx_fp8_scale_workspace": (_size, [_i64]),
     "rpx_fp8_scale": (_int, [_p, _int, _i64, _int, _p, _p, _size, _p]),
@@ -101,6 +124,10 @@ class NativeError(RuntimeError):
     """A HIP-side failure reported by the library."""
 
 
+class DeviceError(NativeError):
+    """A kernel reported a problem through the device error word."""
+
+
 _LIB: ctypes.CDLL | None = None
 
 
@@ -131,6 +158,8 @@ def check(status: int) -> None:
     msg = (load().rpx_last_error() or b"").decode(errors="replace")
     if status == RPX_ERR_INVALID:
         raise ValueError(msg)
+    if status == RPX_ERR_DEVICE:
+        raise DeviceError(msg)
     raise NativeError(msg)
 
 

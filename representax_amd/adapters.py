@@ -24,6 +24,7 @@ import torch
 
 from . import ops
 from .components import Linear
+from .sharding import activation_out_sharding, constrain_activation, replicate
 from .precision import (
     active_compute_dtype,
     active_policy,
@@ -130,8 +131,8 @@ class QuantizedLoRALinear(torch.nn.Module):
     def base_weight(self) -> torch.Tensor:
         """bf16 base materialized at its use boundary (adapters.py:141-148)."""
 
-        return _unpack_int4_rows(self.packed_weight, self.scale_bits, self.input_size,
-                                 self.group_size)
+        return _unpack_int4_rows(replicate(self.packed_weight), replicate(self.scale_bits),
+                                 self.input_size, self.group_size)
 
     def merged_weight(self) -> torch.Tensor:
         """float32 ``base + (B @ A) * alpha / r`` (adapters.py:150-156)."""
@@ -163,7 +164,9 @@ class QuantizedLoRALinear(torch.nn.Module):
 
         Under a bf16 (or fp32) policy the whole projection is one fused HIP
         call; under the fp8 policy the three products go through
-        ``linear_matmul`` like the reference's.
+        ``linear_matmul`` like the reference's. Without a policy, bf16
+        activations meet the float32 masters and the adapter term and the
+        output are promoted to float32 (the reference's ``jnp.matmul``).
         """
 
         if self.packed_weight.ndim != 2:
@@ -178,19 +181,26 @@ class QuantizedLoRALinear(torch.nn.Module):
         x = value.to(compute_dtype)
         lead = x.shape[:-1]
         x2d = x.reshape(-1, self.input_size)
-        y = ops.Int4LoRALinearFn.apply(x2d, a, b, self.packed_weight, self.scale_bits,
-                                       self.bias_bits, self.scaling, self.group_size)
-        return y.reshape(*lead, self.output_size)
+        if x2d.dtype == torch.bfloat16 and a.dtype == torch.float32:
+            # no policy: jnp.matmul promotes the bf16 activations against the
+            # float32 masters, so the adapter term and the output are float32
+            y = ops.Int4LoRAPromotedFn.apply(x2d, a, b, self.packed_weight, self.scale_bits,
+                                             self.bias_bits, self.scaling, self.group_size)
+        else:
+            y = ops.Int4LoRALinearFn.apply(x2d, a, b, self.packed_weight, self.scale_bits,
+                                           self.bias_bits, self.scaling, self.group_size)
+        return constrain_activation(y.reshape(*lead, self.output_size))
 
     def _forward_fp8(self, value: torch.Tensor, compute_dtype: torch.dtype) -> torch.Tensor:
-        output = linear_matmul(value, self.base_weight().to(compute_dtype).transpose(-1, -2))
+        output = linear_matmul(value, self.base_weight().to(compute_dtype).transpose(-1, -2),
+                               out_sharding=activation_out_sharding(value.ndim))
         hidden = linear_matmul(value, compute_parameter(self.lora_a).transpose(-1, -2))
         adapter = linear_matmul(hidden, compute_parameter(self.lora_b).transpose(-1, -2))
         c = torch.tensor(self.scaling, dtype=torch.float32).to(adapter.dtype).item()
         output = output + adapter * c
         if self.bias_bits is not None:
-            output = output + _bfloat16_from_bits(self.bias_bits).to(compute_dtype)
-        return output
+            output = output + _bfloat16_from_bits(replicate(self.bias_bits)).to(compute_dtype)
+        return constrain_activation(output)
 
     def merge(self) -> Linear:
         """Conventional projection for export or inference (adapters.py:184-194)."""

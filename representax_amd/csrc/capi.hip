@@ -1,13 +1,18 @@
 // C-ABI of librepresentax_amd: validation, workspace planning and launch
 // sequencing for the quantized-linear path. No entry point allocates device
 // memory or synchronizes; every launch goes to the caller's stream.
+#include <atomic>
+#include <cstdlib>
 #include <cstring>
+#include <initializer_list>
 #include <string>
+#include <utility>
 
 #include "../../include/representax_amd.h"
 #include "common.h"
 #include "act.h"
 #include "kernels.h"
+#include "tuning.h"
 
 namespace rpx {
 
@@ -45,6 +50,12 @@ struct Sizer {
 
 size_t elem_size(int dtype) { return dtype == kBF16 ? 2 : 4; }
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+// Every non-null pointer 16-byte aligned.
+bool aligned16_all(std::initializer_list<const void*> ps) {
+  for (const void* p : ps)
+    if (p != nullptr && !aligned16(p)) return false;
+  return true;
+}
 bool pow2(int64_t v) { return v > 0 && (v & (v - 1)) == 0; }
 
 float round_to_dtype(float v, int dtype) {
@@ -184,6 +195,101 @@ int grid1d(int64_t work) {
 
 }  // namespace
 
+// --- tuning knobs --------------------------------------------------------------
+namespace {
+
+bool knob_value_ok(int knob, int v) {
+  switch (knob) {
+    case kTuneInt4Tile:
+      return v == kTileAuto || v == kTileI4_256x128 || v == kTileI4_128x128 ||
+             v == kTileI4_64x128 || v == kTileI4_256x256 || v == kTileI4_128x128s2 ||
+             v == kTileI4_128x128s3;
+    case kTuneBf16Tile:
+      return v == kTileAuto || v == kTileBf_256x128 || v == kTileBf_128x128 ||
+             v == kTileBf_64x128 || v == kTileBf_256x256 || v == kTileBf_128x96;
+    case kTuneFp8Tile: return v >= 0 && v < fp8_tile_count();
+    case kTuneSkinnyTile: return v >= 0 && v <= skinny_tile_count();
+    case kTuneSkinny2:
+    case kTuneSkinny2One: return v >= -1 && v <= 1;
+    case kTuneSpinLimit: return v >= 0;
+    default: return false;
+  }
+}
+
+int env_int(const char* name, int fallback) {
+  const char* v = std::getenv(name);
+  return v != nullptr && *v != '\0' ? std::atoi(v) : fallback;
+}
+
+struct Knobs {
+  std::atomic<int> v[kTuneCount];
+  Knobs() {
+    const int defaults[kTuneCount] = {0, 0, 0, 0, -1, -1, 0};
+    for (int i = 0; i < kTuneCount; ++i) v[i].store(defaults[i], std::memory_order_relaxed);
+    // RPX_GEMM_TILE names a tile of either GEMM (the id sets are disjoint)
+    const int gemm = env_int("RPX_GEMM_TILE", 0);
+    if (knob_value_ok(kTuneInt4Tile, gemm)) v[kTuneInt4Tile].store(gemm);
+    if (knob_value_ok(kTuneBf16Tile, gemm)) v[kTuneBf16Tile].store(gemm);
+    const std::pair<int, const char*> envs[] = {{kTuneFp8Tile, "RPX_FP8_TILE"},
+                                                {kTuneSkinnyTile, "RPX_SKINNY_TILE"},
+                                                {kTuneSkinny2, "RPX_SKINNY2"},
+                                                {kTuneSkinny2One, "RPX_SKINNY2_ONE"}};
+    for (const auto& e : envs) {
+      const int val = env_int(e.second, v[e.first].load());
+      if (knob_value_ok(e.first, val)) v[e.first].store(val);
+    }
+  }
+};
+
+Knobs& knobs() {
+  static Knobs k;  // thread-safe one-time initialization
+  return k;
+}
+
+}  // namespace
+
+int tune(int knob) {
+  if (knob < 0 || knob >= kTuneCount) return 0;
+  return knobs().v[knob].load(std::memory_order_relaxed);
+}
+
+bool tune_set(int knob, int value) {
+  if (!knob_value_ok(knob, value)) return false;
+  knobs().v[knob].store(value, std::memory_order_relaxed);
+  return true;
+}
+
+// --- device error word -----------------------------------------------------------
+namespace {
+__device__ unsigned int g_device_error;  // bits kDevErr*, per device
+constexpr int kMaxDevices = 64;
+std::atomic<unsigned int*> g_error_ptr[kMaxDevices];
+}  // namespace
+
+unsigned int* device_error_word() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  unsigned int* p = g_error_ptr[dev].load(std::memory_order_acquire);
+  if (p != nullptr) return p;
+  void* addr = nullptr;
+  if (hipGetSymbolAddress(&addr, HIP_SYMBOL(g_device_error)) != hipSuccess) return nullptr;
+  p = static_cast<unsigned int*>(addr);
+  g_error_ptr[dev].store(p, std::memory_order_release);
+  return p;
+}
+
+hipError_t ensure_lds_limit(const void* kernel, int bytes, std::atomic<unsigned>& done_devices) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  const unsigned bit = 1u << (dev & 31);
+  if (done_devices.load(std::memory_order_acquire) & bit) return hipSuccess;
+  e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (e != hipSuccess) return e;
+  done_devices.fetch_or(bit, std::memory_order_acq_rel);
+  return hipSuccess;
+}
+
 void set_error(const std::string& msg) { g_last_error = msg; }
 
 int fail_invalid(const std::string& msg) {
@@ -206,6 +312,31 @@ extern "C" {
 const char* rpx_last_error(void) { return g_last_error.c_str(); }
 
 int rpx_abi_version(void) { return RPX_ABI_VERSION; }
+
+int rpx_set_tuning(int knob, int value) {
+  if (!tune_set(knob, value)) return fail_invalid("rpx_set_tuning: unknown knob or value");
+  return kOk;
+}
+
+int rpx_get_tuning(int knob) { return tune(knob); }
+
+int rpx_check_device_errors(void* stream, uint32_t* flags_out) {
+  if (flags_out != nullptr) *flags_out = 0;
+  unsigned int* word = device_error_word();
+  if (word == nullptr) return check_hip(hipErrorInvalidSymbol, "rpx_check_device_errors");
+  RPX_HIP(hipStreamSynchronize(static_cast<hipStream_t>(stream)), "rpx_check_device_errors: sync");
+  unsigned int bits = 0;
+  RPX_HIP(hipMemcpy(&bits, word, sizeof(bits), hipMemcpyDeviceToHost),
+          "rpx_check_device_errors: read");
+  if (bits == 0) return kOk;
+  RPX_HIP(hipMemset(word, 0, sizeof(bits)), "rpx_check_device_errors: clear");
+  if (flags_out != nullptr) *flags_out = bits;
+  std::string msg = "a kernel's bounded wait expired (its outputs hold NaN):";
+  if (bits & kDevErrSkinnyWait) msg += " skinny-M forward (one launch, M <= 64): adapter arrivals;";
+  if (bits & kDevErrSkinnyOneWait) msg += " skinny-M forward (one launch, M <= 4): published h;";
+  set_error(msg);
+  return kErrDevice;
+}
 
 // ---------------------------------------------------------------------------
 // INT4 codec
@@ -300,8 +431,14 @@ int int4lora_forward_impl(const void* x, int dtype, int64_t m, int64_t k, const 
   w.scales = scale_bits;
   w.n_groups = ng;
   w.group = g;
-  const bool fast = lora_fast_shape(dtype, k, ng, g, rank) && aligned16(x) && aligned16(packed) &&
-                    aligned16(lora_a) && aligned16(y);
+  // the workspace query sizes the MFMA and skinny paths from the shape alone;
+  // those paths load every operand in 16-byte vectors
+  const bool fast = lora_fast_shape(dtype, k, ng, g, rank);
+  if ((fast || lora_skinny(dtype, m, n, k, ng, g, rank)) &&
+      !aligned16_all({x, packed, scale_bits, lora_a, y}))
+    return fail_invalid(
+        "rpx_int4lora_forward: this shape takes the vectorized kernels, which need x, packed, "
+        "scale_bits, lora_a and y 16-byte aligned");
   Arena arena(workspace, workspace_bytes);
   // where the paths without the activation epilogue put the linear's output;
   // the activation then runs elementwise from there into y
@@ -313,8 +450,7 @@ int int4lora_forward_impl(const void* x, int dtype, int64_t m, int64_t k, const 
               "int4lora_forward: activation");
     return kOk;
   };
-  if (lora_skinny(dtype, m, n, k, ng, g, rank) && aligned16(x) && aligned16(packed) &&
-      aligned16(lora_a)) {
+  if (lora_skinny(dtype, m, n, k, ng, g, rank)) {
     float* ws = arena.take<float>(skinny_workspace_floats(m, n, k, rank));
     if (arena.overflow) return fail_invalid("rpx_int4lora_forward: workspace too small");
     if (skinny2_selected(m, n, k, rank, ng, g)) {
@@ -451,8 +587,13 @@ int int4lora_backward_impl(const void* grad, const void* x, int dtype, int64_t m
   w.scales = scale_bits;
   w.n_groups = ng;
   w.group = g;
-  const bool fast = lora_fast_shape(dtype, k, ng, g, rank) && n % 64 == 0 && aligned16(grad) &&
-                    aligned16(x) && aligned16(dx) && aligned16(lora_b);
+  // the workspace query sizes the MFMA path from the shape alone; it loads
+  // every operand in 16-byte vectors
+  const bool fast = lora_fast_shape(dtype, k, ng, g, rank) && n % 64 == 0;
+  if (fast && !aligned16_all({grad, x, packed, scale_bits, lora_a, lora_b, dx}))
+    return fail_invalid(
+        "rpx_int4lora_backward: this shape takes the vectorized kernels, which need grad, x, "
+        "packed, scale_bits, lora_a, lora_b and dx 16-byte aligned");
   Arena arena(workspace, workspace_bytes);
   if (fast) {
     const uint16_t* gb = static_cast<const uint16_t*>(grad);
@@ -595,6 +736,185 @@ int rpx_int4lora_backward_act(const void* grad, const void* x, int dtype, int64_
 }
 
 // ---------------------------------------------------------------------------
+// INT4 + LoRA linear without a precision policy: bf16 activations, float32
+// adapter masters (jnp.matmul promotes the adapter products to float32)
+// ---------------------------------------------------------------------------
+}  // extern "C"
+
+namespace rpx {
+namespace {
+
+// y = f32(base_b) + low * c (+ f32(bias)): base_b the bf16-rounded base
+// product (bf16 bits when base_bf16, else f32 values rounded here).
+__global__ void __launch_bounds__(256)
+    k_promoted_combine(const void* __restrict__ base, int base_bf16,
+                       const float* __restrict__ low, int64_t rows, int64_t cols, float c,
+                       const uint16_t* __restrict__ bias, float* __restrict__ out) {
+  const int64_t total = rows * cols;
+  for (int64_t e = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; e < total;
+       e += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const float b = base_bf16 ? bf16_to_f32(static_cast<const uint16_t*>(base)[e])
+                              : round_bf16(static_cast<const float*>(base)[e]);
+    float y = b + low[e] * c;
+    if (bias != nullptr) y = y + bf16_to_f32(bias[e % cols]);
+    out[e] = y;
+  }
+}
+
+bool promoted_fast_base(int64_t k, int64_t n_groups, int64_t group, const void* x,
+                        const void* packed, const void* scales) {
+  return lora_fast_shape(kBF16, k, n_groups, group, 1) && aligned16_all({x, packed, scales});
+}
+
+template <typename A>
+void plan_forward_promoted(A& a, int64_t m, int64_t n) {
+  a.template take<float>(m * n);  // base product (f32, or bf16 bits from the MFMA GEMM)
+  a.template take<float>(m * n);  // adapter product
+}
+
+template <typename A>
+void plan_backward_promoted(A& a, int64_t m, int64_t n, int64_t k, int64_t rank) {
+  a.template take<uint16_t>(m * n);  // bf16(g)
+  a.template take<float>(m * n);     // g * c
+  a.template take<float>(m * rank);  // dh
+  a.template take<float>(m * k);     // bf16(g) W_b
+  a.template take<float>(m * k);     // dh A
+}
+
+}  // namespace
+}  // namespace rpx
+
+extern "C" {
+
+size_t rpx_int4lora_forward_promoted_workspace(int64_t m, int64_t n, int64_t k,
+                                               int64_t group_size, int64_t rank) {
+  (void)k;
+  (void)group_size;
+  (void)rank;
+  Sizer s;
+  plan_forward_promoted(s, m, n);
+  return s.used;
+}
+
+int rpx_int4lora_forward_promoted(const uint16_t* x, int64_t m, int64_t k, const uint8_t* packed,
+                                  const uint16_t* scale_bits, int64_t n, int64_t group_size,
+                                  const uint16_t* bias_bits, const float* lora_a,
+                                  const float* lora_b, int64_t rank, float scaling, float* y,
+                                  float* h, void* workspace, size_t workspace_bytes,
+                                  void* stream) {
+  int64_t ng, g;
+  RPX_TRY(check_int4_shape(n, k, group_size, &ng, &g));
+  if (m < 0) return fail_invalid("m must be non-negative");
+  if (rank < 1 || rank > n || rank > k) return fail_invalid("adapter rank must fit both linear dimensions");
+  if (m == 0 || n == 0) return kOk;
+  if (x == nullptr || packed == nullptr || scale_bits == nullptr || lora_a == nullptr ||
+      lora_b == nullptr || y == nullptr || h == nullptr)
+    return fail_invalid("rpx_int4lora_forward_promoted: null pointer");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  Int4Operand w;
+  w.packed = packed;
+  w.packed_cols = (k + 1) / 2;
+  w.scales = scale_bits;
+  w.n_groups = ng;
+  w.group = g;
+  Arena arena(workspace, workspace_bytes);
+  float* base = arena.take<float>(m * n);
+  float* low = arena.take<float>(m * n);
+  if (arena.overflow) return fail_invalid("rpx_int4lora_forward_promoted: workspace too small");
+  // base = bf16(x W_b^T): the MFMA GEMM with no epilogue term where it applies
+  const bool fast = promoted_fast_base(k, ng, g, x, packed, scale_bits);
+  if (fast) {
+    RPX_HIP(launch_gemm_int4(x, k, w, m, n, k, reinterpret_cast<uint16_t*>(base), n,
+                             LowRankEpilogue{}, st),
+            "int4lora_forward_promoted: base product");
+  } else {
+    RPX_HIP(launch_generic_gemm(x, kBF16, k, 1, nullptr, kBF16, 0, 0, &w, false, m, n, k, base,
+                                st),
+            "int4lora_forward_promoted: base product");
+  }
+  // h = f32(x A^T), a = f32(h B^T), on the float32 masters
+  RPX_HIP(launch_generic_gemm(x, kBF16, k, 1, lora_a, kF32, k, 1, nullptr, false, m, rank, k, h,
+                              st),
+          "int4lora_forward_promoted: adapter down-projection");
+  RPX_HIP(launch_generic_gemm(h, kF32, rank, 1, lora_b, kF32, rank, 1, nullptr, false, m, n, rank,
+                              low, st),
+          "int4lora_forward_promoted: adapter up-projection");
+  hipLaunchKernelGGL(k_promoted_combine, dim3(grid1d(m * n)), dim3(256), 0, st, base,
+                     fast ? 1 : 0, low, m, n, scaling, bias_bits, y);
+  RPX_HIP(hipGetLastError(), "int4lora_forward_promoted: combine");
+  return kOk;
+}
+
+size_t rpx_int4lora_backward_promoted_workspace(int64_t m, int64_t n, int64_t k,
+                                                int64_t group_size, int64_t rank) {
+  (void)group_size;
+  Sizer s;
+  plan_backward_promoted(s, m, n, k, rank);
+  return s.used;
+}
+
+int rpx_int4lora_backward_promoted(const float* grad, const uint16_t* x, int64_t m, int64_t k,
+                                   const uint8_t* packed, const uint16_t* scale_bits, int64_t n,
+                                   int64_t group_size, const float* lora_a, const float* lora_b,
+                                   int64_t rank, float scaling, const float* h, uint16_t* dx,
+                                   float* d_lora_a, float* d_lora_b, void* workspace,
+                                   size_t workspace_bytes, void* stream) {
+  int64_t ng, g;
+  RPX_TRY(check_int4_shape(n, k, group_size, &ng, &g));
+  if (m < 0) return fail_invalid("m must be non-negative");
+  if (rank < 1 || rank > n || rank > k) return fail_invalid("adapter rank must fit both linear dimensions");
+  if (packed == nullptr || scale_bits == nullptr || lora_a == nullptr || lora_b == nullptr ||
+      d_lora_a == nullptr || d_lora_b == nullptr ||
+      (m > 0 && (grad == nullptr || x == nullptr || dx == nullptr || h == nullptr)))
+    return fail_invalid("rpx_int4lora_backward_promoted: null pointer");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (m == 0) {
+    RPX_HIP(launch_fill_f32(d_lora_a, rank * k, 0.0f, st), "int4lora_backward_promoted: zero dA");
+    RPX_HIP(launch_fill_f32(d_lora_b, n * rank, 0.0f, st), "int4lora_backward_promoted: zero dB");
+    return kOk;
+  }
+  Int4Operand w;
+  w.packed = packed;
+  w.packed_cols = (k + 1) / 2;
+  w.scales = scale_bits;
+  w.n_groups = ng;
+  w.group = g;
+  Arena arena(workspace, workspace_bytes);
+  uint16_t* gb = arena.take<uint16_t>(m * n);
+  float* ga = arena.take<float>(m * n);
+  float* dh = arena.take<float>(m * rank);
+  float* p1 = arena.take<float>(m * k);
+  float* p2 = arena.take<float>(m * k);
+  if (arena.overflow) return fail_invalid("rpx_int4lora_backward_promoted: workspace too small");
+  // the base product's cotangent is bf16(g); dx_base = bf16(bf16(g) W_b)
+  RPX_HIP(launch_round_store(grad, m * n, kBF16, gb, st), "int4lora_backward_promoted: bf16(g)");
+  RPX_HIP(launch_generic_gemm(gb, kBF16, n, 1, nullptr, kBF16, 0, 0, &w, true, m, k, n, p1, st),
+          "int4lora_backward_promoted: g W");
+  // g_a = f32(g c), dh = f32(g_a B), dB = f32(g_a^T h)
+  hipLaunchKernelGGL(k_scale_round, dim3(grid1d(m * n)), dim3(256), 0, st, grad, m * n, scaling,
+                     kF32, ga);
+  RPX_HIP(hipGetLastError(), "int4lora_backward_promoted: g_a");
+  RPX_HIP(launch_generic_gemm(ga, kF32, n, 1, lora_b, kF32, 1, rank, nullptr, false, m, rank, n,
+                              dh, st),
+          "int4lora_backward_promoted: dh");
+  RPX_HIP(launch_generic_gemm(ga, kF32, 1, n, h, kF32, 1, rank, nullptr, false, n, rank, m,
+                              d_lora_b, st),
+          "int4lora_backward_promoted: dB");
+  // dx = bf16(bf16(g W_b) + bf16(f32(dh A))), summed in bf16
+  RPX_HIP(launch_generic_gemm(dh, kF32, rank, 1, lora_a, kF32, 1, k, nullptr, false, m, k, rank,
+                              p2, st),
+          "int4lora_backward_promoted: dh A");
+  hipLaunchKernelGGL(k_lora_combine, dim3(grid1d(m * k)), dim3(256), 0, st, p1, p2, m, k, 1.0f,
+                     nullptr, kBF16, dx);
+  RPX_HIP(hipGetLastError(), "int4lora_backward_promoted: combine dx");
+  // dA = f32(dh^T x)
+  RPX_HIP(launch_generic_gemm(dh, kF32, 1, rank, x, kBF16, 1, k, nullptr, false, rank, k, m,
+                              d_lora_a, st),
+          "int4lora_backward_promoted: dA");
+  return kOk;
+}
+
+// ---------------------------------------------------------------------------
 // FP8
 // ---------------------------------------------------------------------------
 size_t rpx_fp8_scale_workspace(int64_t numel) {
@@ -639,8 +959,41 @@ size_t rpx_fp8_gemm_workspace(int64_t m, int64_t n, int64_t k) {
 
 namespace rpx {
 namespace {
-__constant__ float c_fp8_table[2][256];
-bool g_table_ready = false;
+// OCP fp8 decode tables (e4m3fn, e5m2), built at compile time.
+constexpr float pow2_constexpr(int e) {
+  float v = 1.0f;
+  for (; e > 0; --e) v *= 2.0f;
+  for (; e < 0; ++e) v *= 0.5f;
+  return v;
+}
+
+constexpr float decode_fp8_constexpr(uint32_t code, int fmt) {
+  const int eb = fmt == kE4M3FN ? 4 : 5;
+  const int mb = fmt == kE4M3FN ? 3 : 2;
+  const int bias = fmt == kE4M3FN ? 7 : 15;
+  const float sign = (code & 0x80u) ? -1.0f : 1.0f;
+  const uint32_t e = (code >> mb) & ((1u << eb) - 1u);
+  const uint32_t mnt = code & ((1u << mb) - 1u);
+  const uint32_t all = (1u << eb) - 1u;
+  if (fmt == kE5M2 && e == all) return mnt == 0 ? sign * __builtin_inff() : __builtin_nanf("");
+  if (fmt == kE4M3FN && e == all && mnt == (1u << mb) - 1u) return __builtin_nanf("");
+  if (e == 0) return sign * static_cast<float>(mnt) * pow2_constexpr(1 - bias - mb);
+  return sign * (1.0f + static_cast<float>(mnt) / static_cast<float>(1u << mb)) *
+         pow2_constexpr(static_cast<int>(e) - bias);
+}
+
+struct Fp8Table {
+  float v[2][256];
+};
+
+constexpr Fp8Table make_fp8_table() {
+  Fp8Table t{};
+  for (int f = 0; f < 2; ++f)
+    for (int c = 0; c < 256; ++c) t.v[f][c] = decode_fp8_constexpr(static_cast<uint32_t>(c), f);
+  return t;
+}
+
+__constant__ Fp8Table c_fp8_table = make_fp8_table();
 
 __global__ void __launch_bounds__(256)
     k_fp8_gemm_generic(const uint8_t* __restrict__ a, int fmt_a, const uint8_t* __restrict__ b,
@@ -653,7 +1006,7 @@ __global__ void __launch_bounds__(256)
     const int64_t n = e % N;
     float acc = 0.0f;
     for (int64_t kk = 0; kk < K; ++kk)
-      acc = __builtin_fmaf(c_fp8_table[fmt_a][a[m * K + kk]], c_fp8_table[fmt_b][b[n * K + kk]], acc);
+      acc = __builtin_fmaf(c_fp8_table.v[fmt_a][a[m * K + kk]], c_fp8_table.v[fmt_b][b[n * K + kk]], acc);
     const float y = (acc * s_a[0]) * s_b[0];
     if (out_dtype == kBF16)
       static_cast<uint16_t*>(out)[e] = f32_to_bf16(y);
@@ -662,30 +1015,6 @@ __global__ void __launch_bounds__(256)
   }
 }
 
-float decode_fp8_host(uint32_t code, int fmt) {
-  const int eb = fmt == kE4M3FN ? 4 : 5;
-  const int mb = fmt == kE4M3FN ? 3 : 2;
-  const int bias = fmt == kE4M3FN ? 7 : 15;
-  const float sign = (code & 0x80u) ? -1.0f : 1.0f;
-  const uint32_t e = (code >> mb) & ((1u << eb) - 1u);
-  const uint32_t mnt = code & ((1u << mb) - 1u);
-  const uint32_t all = (1u << eb) - 1u;
-  if (fmt == kE5M2 && e == all) return mnt == 0 ? sign * __builtin_inff() : __builtin_nanf("");
-  if (fmt == kE4M3FN && e == all && mnt == (1u << mb) - 1u) return __builtin_nanf("");
-  if (e == 0) return sign * static_cast<float>(mnt) * __builtin_ldexpf(1.0f, 1 - bias - mb);
-  return sign * (1.0f + static_cast<float>(mnt) / static_cast<float>(1u << mb)) *
-         __builtin_ldexpf(1.0f, static_cast<int>(e) - bias);
-}
-
-int ensure_fp8_table() {
-  if (g_table_ready) return kOk;
-  float host[2][256];
-  for (int f = 0; f < 2; ++f)
-    for (int c = 0; c < 256; ++c) host[f][c] = decode_fp8_host(static_cast<uint32_t>(c), f);
-  RPX_HIP(hipMemcpyToSymbol(HIP_SYMBOL(c_fp8_table), host, sizeof(host)), "fp8 decode table");
-  g_table_ready = true;
-  return kOk;
-}
 }  // namespace
 }  // namespace rpx
 
@@ -712,7 +1041,6 @@ int rpx_fp8_gemm(const uint8_t* a, int fmt_a, const float* scale_a, const uint8_
             "rpx_fp8_gemm");
     return kOk;
   }
-  RPX_TRY(ensure_fp8_table());
   hipLaunchKernelGGL(k_fp8_gemm_generic, dim3(grid1d(m * n)), dim3(256), 0, st, a, fmt_a, b, fmt_b,
                      m, n, k, scale_a, scale_b, out, out_dtype);
   RPX_HIP(hipGetLastError(), "rpx_fp8_gemm (generic)");

@@ -14,6 +14,19 @@ __device__ __forceinline__ bool arrive(unsigned int* word, unsigned int target) 
   return true;
 }
 
+// Counts one participant of a call as done with its slot of arrival words
+// (after its last access to them); the last of `target` participants clears
+// slot[0 .. n_words), the done word among them, so every call leaves its slot
+// at zero however its waits ended.
+__device__ __forceinline__ void done_count(unsigned int* slot, int done_word, int n_words,
+                                           unsigned int target) {
+  const unsigned int old =
+      __hip_atomic_fetch_add(slot + done_word, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (old + 1u != target) return;
+  for (int i = 0; i < n_words; ++i)
+    __hip_atomic_store(slot + i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Partial sums cross blocks through agent-scope (device-coherent) 64-bit
 // stores and loads instead of plain accesses plus a release/acquire fence
 // pair: on this target an agent-scope release fence writes back the whole

@@ -112,6 +112,7 @@ int check_hip(hipError_t err, const char* what);
 constexpr int kOk = 0;
 constexpr int kErrInvalid = 1;
 constexpr int kErrHip = 2;
+constexpr int kErrDevice = 3;
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 

@@ -4,12 +4,14 @@
 // fp32 output. This is the dot_general + rescale of _scaled_fp8_dot
 // (representax/precision.py:154-170): the scaling is applied after the
 // fp32 dot as (acc * s_a) * s_b, in that order.
+#include <atomic>
 #include <cstdlib>
 #include <cstring>
 
 #include "common.h"
 #include "kernels.h"
 #include "lds_pipeline.h"
+#include "tuning.h"
 
 namespace rpx {
 namespace {
@@ -389,17 +391,6 @@ struct Fp8Plan {
   int64_t splits, k_per_split;
 };
 
-int fp8_tile_override() {
-  static int cached = -1;
-  if (cached < 0) {
-    const char* env = std::getenv("RPX_FP8_TILE");
-    cached = 0;
-    if (env != nullptr) cached = std::atoi(env);
-    if (cached < 0 || cached >= kNumCfg) cached = 0;
-  }
-  return cached;
-}
-
 // Estimated cycles of a plan on 256 CUs. Per round of resident blocks a CU
 // runs `per_cu` blocks whose MFMA work (8192 fp8 flops per clock per CU) and
 // global->LDS fill (about 64 bytes per clock per CU when every CU of an XCD
@@ -446,7 +437,7 @@ Fp8Plan plan_for(int cfg, int64_t m, int64_t n, int64_t kslices, double* cost_ou
 
 Fp8Plan plan_fp8(int64_t m, int64_t n, int64_t k) {
   const int64_t kslices = k / kBK;
-  const int forced = fp8_tile_override();
+  const int forced = tune(kTuneFp8Tile);
   if (forced != 0) return plan_for(forced, m, n, kslices, nullptr);
   Fp8Plan best{1, 1, k};
   double best_cost = -1.0;
@@ -493,13 +484,9 @@ hipError_t run_fp8(const uint8_t* a, const uint8_t* b, int64_t m, int64_t n, int
   const int tiles_m = static_cast<int>(ceil_div(m, BM));
   const int tiles_n = static_cast<int>(ceil_div(n, BN));
   auto kern = k_fp8_gemm<BM, BN, WM, WN, NS, WPE, FA, FB>;
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
+  static std::atomic<unsigned> lds_set{0};
+  hipError_t le = ensure_lds_limit(reinterpret_cast<const void*>(kern), kLds, lds_set);
+  if (le != hipSuccess) return le;
   const unsigned blocks = static_cast<unsigned>(tiles_m) * tiles_n * plan.splits;
   hipLaunchKernelGGL(kern, dim3(blocks), dim3(64 * WM * WN), kLds, stream, a, b, m, n, k,
                      plan.k_per_split, s_a, s_b, out, out_dtype, ldc,
@@ -533,6 +520,8 @@ hipError_t dispatch_fp8(const uint8_t* a, const uint8_t* b, int64_t m, int64_t n
 }
 
 }  // namespace
+
+int fp8_tile_count() { return kNumCfg; }
 
 int64_t fp8_gemm_workspace_floats(int64_t m, int64_t n, int64_t k) {
   const Fp8Plan p = plan_fp8(m, n, k);

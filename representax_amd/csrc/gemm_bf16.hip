@@ -14,6 +14,7 @@
 // fragment, so lane l of a 32x32 block owns output row m = l % 32 and the
 // registers v = 0..15 hold output columns n = 8*(v/4) + 4*(l/32) + v%4,
 // which lets each lane store 4 consecutive bf16 outputs at once.
+#include <atomic>
 #include <cstdlib>
 #include <cstring>
 
@@ -21,6 +22,7 @@
 #include "kernels.h"
 #include "act.h"
 #include "lds_pipeline.h"
+#include "tuning.h"
 
 namespace rpx {
 
@@ -687,13 +689,9 @@ hipError_t run_gemm_act(const uint16_t* a, int64_t lda, const uint16_t* b, int64
   const size_t lds = gemm_lds_bytes(BM, BN, NS, INT4) + ((scale_bytes + 15) & ~size_t{15});
   if (lds > 160 * 1024) return hipErrorInvalidValue;
   auto kern = k_gemm_nt<BM, BN, WM, WN, NS, WPE, INT4, JB, ACT>;
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
+  static std::atomic<unsigned> lds_set{0};
+  hipError_t e = ensure_lds_limit(reinterpret_cast<const void*>(kern), 160 * 1024, lds_set);
+  if (e != hipSuccess) return e;
   int group_shift = 0;
   if (INT4 && w.n_groups > 1) {
     while ((int64_t{1} << group_shift) < w.group) ++group_shift;
@@ -745,16 +743,6 @@ hipError_t run_gemm(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t l
                                                        stream);
 }
 
-// Tile configuration override for tuning sweeps: RPX_GEMM_TILE=<id>.
-int tile_override() {
-  static int cached = -1;
-  if (cached < 0) {
-    const char* env = std::getenv("RPX_GEMM_TILE");
-    cached = env != nullptr ? std::atoi(env) : 0;
-  }
-  return cached;
-}
-
 // INT4 B: one wave row (WM = 1) so every packed row is dequantized by a
 // single wave. bf16 B: 2 x 2 or 4 x 2 waves.
 hipError_t dispatch_int4(const uint16_t* a, int64_t lda, const Int4Operand& w, int64_t m,
@@ -765,17 +753,23 @@ hipError_t dispatch_int4(const uint16_t* a, int64_t lda, const Int4Operand& w, i
   if ((reinterpret_cast<uintptr_t>(w.scales) & 15) != 0 || (w.packed_cols & 15) != 0 ||
       (reinterpret_cast<uintptr_t>(w.packed) & 15) != 0)
     return hipErrorInvalidValue;
-  int cfg = tile_override();
-  if (cfg == 7)
+  int cfg = tune(kTuneInt4Tile);
+  if (cfg == kTileI4_256x256)
     return run_gemm<256, 256, 2, 2, 3, 1, true>(a, lda, nullptr, 0, w, m, n, k, out, ldc, epi,
                                                 stream);
-  if (cfg < 1 || cfg > 3) {
+  if (cfg == kTileI4_128x128s2)
+    return run_gemm<128, 128, 1, 4, 2, 3, true>(a, lda, nullptr, 0, w, m, n, k, out, ldc, epi,
+                                                stream);
+  if (cfg == kTileI4_128x128s3)
+    return run_gemm<128, 128, 1, 4, 3, 2, true>(a, lda, nullptr, 0, w, m, n, k, out, ldc, epi,
+                                                stream);
+  if (cfg < kTileI4_256x128 || cfg > kTileI4_64x128) {
     // 128 x 32 wave tiles, two or three workgroups (8 or 12 waves) per CU:
     // each dequantized B fragment feeds four MFMAs, and a CU's waves keep
     // the LDS fragment reads and the dequantization VALU work under the MFMAs
-    cfg = ceil_div(m, 128) * ceil_div(n, 128) >= 128 ? 2 : 3;
+    cfg = ceil_div(m, 128) * ceil_div(n, 128) >= 128 ? kTileI4_128x128 : kTileI4_64x128;
   }
-  if (cfg == 2) {
+  if (cfg == kTileI4_128x128) {
     // three workgroups per CU (12 waves) with a two-stage pipeline while the
     // block's scales leave room for them in LDS, else two with three stages;
     // when the scales (many groups) leave room for only one, the 256-row
@@ -786,12 +780,12 @@ hipError_t dispatch_int4(const uint16_t* a, int64_t lda, const Int4Operand& w, i
                                                   stream);
     if (gemm_lds_bytes(128, 128, 3, true) + scale_bytes > (160 * 1024) / 2 && m >= 256 &&
         gemm_lds_bytes(256, 128, 3, true) + scale_bytes <= 160 * 1024)
-      cfg = 1;
+      cfg = kTileI4_256x128;
     else
       return run_gemm<128, 128, 1, 4, 3, 2, true>(a, lda, nullptr, 0, w, m, n, k, out, ldc, epi,
                                                   stream);
   }
-  if (cfg == 1)
+  if (cfg == kTileI4_256x128)
     return run_gemm<256, 128, 1, 4, 3, 1, true>(a, lda, nullptr, 0, w, m, n, k, out, ldc, epi,
                                                 stream);
   return run_gemm<64, 128, 1, 4, 3, 2, true>(a, lda, nullptr, 0, w, m, n, k, out, ldc, epi,
@@ -802,26 +796,28 @@ hipError_t dispatch_bf16(const uint16_t* a, int64_t lda, const uint16_t* b, int6
                          int64_t m, int64_t n, int64_t k, uint16_t* out, int64_t ldc,
                          const LowRankEpilogue& epi, hipStream_t stream) {
   Int4Operand none;
-  int cfg = tile_override();
-  if (cfg == 8)
+  int cfg = tune(kTuneBf16Tile);
+  if (cfg == kTileBf_256x256)
     return run_gemm<256, 256, 2, 2, 2, 1, false>(a, lda, b, ldb, none, m, n, k, out, ldc, epi,
                                                  stream);
-  if (cfg < 4 || (cfg > 6 && cfg != 9)) {
+  if (cfg == kTileAuto) {
     // 128 x 96 tiles when they make one balanced round of 192-256 workgroups
     // where 128 x 128 would leave CUs idle (measured on 4096 x 768 outputs:
     // 31 us against 33 us for two uneven rounds of 64 x 128)
     const int64_t t128 = ceil_div(m, 128) * ceil_div(n, 128);
     const int64_t t96 = ceil_div(m, 128) * ceil_div(n, 96);
-    cfg = ceil_div(m, 256) * ceil_div(n, 128) >= 256 ? 4
-          : (t128 >= 256 ? 5 : (t96 >= 192 && t96 <= 256 ? 9 : 6));
+    cfg = ceil_div(m, 256) * ceil_div(n, 128) >= 256
+              ? kTileBf_256x128
+              : (t128 >= 256 ? kTileBf_128x128
+                             : (t96 >= 192 && t96 <= 256 ? kTileBf_128x96 : kTileBf_64x128));
   }
-  if (cfg == 9)
+  if (cfg == kTileBf_128x96)
     return run_gemm<128, 96, 4, 1, 3, 1, false>(a, lda, b, ldb, none, m, n, k, out, ldc, epi,
                                                 stream);
-  if (cfg == 4)
+  if (cfg == kTileBf_256x128)
     return run_gemm<256, 128, 4, 2, 2, 2, false>(a, lda, b, ldb, none, m, n, k, out, ldc, epi,
                                                  stream);
-  if (cfg == 5)
+  if (cfg == kTileBf_128x128)
     return run_gemm<128, 128, 2, 2, 2, 2, false>(a, lda, b, ldb, none, m, n, k, out, ldc, epi,
                                                  stream);
   return run_gemm<64, 128, 2, 2, 3, 2, false>(a, lda, b, ldb, none, m, n, k, out, ldc, epi,

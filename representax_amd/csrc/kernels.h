@@ -5,6 +5,14 @@
 
 namespace rpx {
 
+// Device error word ----------------------------------------------------------
+// One word per device that kernels raise bits in (atomic or) when a bounded
+// wait expired; read and cleared by rpx_check_device_errors.
+constexpr unsigned int kDevErrSkinnyWait = 1u;     // k_skinny: adapter arrivals
+constexpr unsigned int kDevErrSkinnyOneWait = 2u;  // k_skinny_one: published h
+// This device's word (nullptr if its address could not be resolved).
+unsigned int* device_error_word();
+
 // INT4 -----------------------------------------------------------------------
 hipError_t launch_int4_dequant(const uint8_t* packed, const uint16_t* scales, uint16_t* out,
                                int64_t n, int64_t k, int64_t packed_cols, int64_t n_groups,
@@ -64,6 +72,7 @@ bool gemm_fast_path_ok(int64_t k, int64_t lda, int64_t ldb_elems, const void* a,
                        int64_t ldc, const void* out);
 
 // Skinny-M (M <= 64) INT4 + LoRA forward -------------------------------------
+int skinny_tile_count();  // one-launch tile ids are 1 .. skinny_tile_count()
 bool skinny_ok(int64_t m, int64_t n, int64_t k, int64_t rank, int64_t n_groups, int64_t group);
 int64_t skinny_workspace_floats(int64_t m, int64_t n, int64_t k, int64_t rank);
 hipError_t launch_skinny_forward(const uint16_t* x, int64_t m, int64_t k, const Int4Operand& w,
@@ -173,6 +182,7 @@ hipError_t launch_fp8_gemm(const uint8_t* a, int fmt_a, const float* s_a, const 
                            void* out, int out_dtype, int64_t ldc, float* split_ws,
                            int64_t split_ws_floats, hipStream_t stream);
 int64_t fp8_gemm_workspace_floats(int64_t m, int64_t n, int64_t k);
+int fp8_tile_count();  // tile ids are 1 .. fp8_tile_count() - 1 (0: planner)
 // Delayed scaling: saturating casts with given scales that also record each
 // tensor's amax (atomic max of ordered f32 bits) into its slot's pending
 // lanes (fp8_rec_words() words per slot); up to two tensors of one dtype in

@@ -19,12 +19,19 @@
 // rounded again). Results do not depend on arrival order. Calls take the
 // counter slots in turn, so at most kSlots calls may run at once on a device
 // (kernels of one stream never overlap).
+//
+// Slot words return to zero at the end of every call, also when a wait
+// timed out: the adapter blocks and the tile finishers each count once more
+// into a "done" word after their last access to the slot, and whichever of
+// them counts last clears the slot. A finisher whose wait expired poisons h
+// (NaN) and raises a bit in the device error word.
 #include <atomic>
 #include <cstdlib>
 
 #include "coherent.h"
 #include "common.h"
 #include "kernels.h"
+#include "tuning.h"
 
 namespace rpx {
 
@@ -33,7 +40,7 @@ namespace {
 constexpr int kMaxTiles = 1024;
 constexpr int kSlots = 8;
 constexpr int kAdapterSpan = 256;  // columns of x A^T per adapter block
-constexpr int kSpinLimit = 1 << 22;
+constexpr int kSpinLimit = 1 << 22;  // default polls of the bounded wait
 
 struct SkinnyParams {
   const uint16_t* x;  // [M, K] bf16
@@ -59,6 +66,8 @@ struct SkinnyParams {
   float* part_w;           // [splits][tiles][frags][64][4]
   float* part_h;           // [a_splits][4][MB][64][4]
   int slot;               // counter slot of this call
+  int spin;               // polls of the bounded wait
+  unsigned int* err;      // device error word (kDevErrSkinnyWait on timeout)
 };
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(u32x4_t v) { return __builtin_bit_cast(bf16x8_t, v); }
@@ -78,8 +87,9 @@ __device__ __forceinline__ void dequant8_exact(uint32_t word, float s, float m8s
 }
 
 // Arrival counters, one slot per call in flight (calls take the slots in
-// turn): [0] adapter blocks, [1] finished tiles, [2 + t] K splits of tile t.
-// They are zero when the module loads and every call leaves its slot at zero.
+// turn): [0] adapter blocks, [1] done (adapter blocks and tile finishers past
+// their last access to the slot), [2 + t] K splits of tile t. They are zero
+// when the module loads and every call leaves its slot at zero.
 __device__ unsigned int g_skinny_counters[kSlots][kMaxTiles + 2];
 
 __device__ __forceinline__ u32x4_t load16(const void* p) {
@@ -395,8 +405,9 @@ __device__ __forceinline__ void finish_tile(const SkinnyParams& p, int64_t tile,
 // before any weight block, and none of them waits on anything, so the wait
 // ends as soon as they finish; the spin limit only guarantees that every
 // wave exits. Returns false if the limit was hit.
-__device__ __forceinline__ bool wait_adapters(const unsigned int* word, unsigned int target) {
-  for (int it = 0; it < kSpinLimit; ++it) {
+__device__ __forceinline__ bool wait_adapters(const unsigned int* word, unsigned int target,
+                                              int spin) {
+  for (int it = 0; it < spin; ++it) {
     if (__hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == target) return true;
     __builtin_amdgcn_s_sleep(2);
   }
@@ -414,11 +425,16 @@ __global__ void __launch_bounds__(256) k_skinny(SkinnyParams p) {
   const int tid = threadIdx.x;
   unsigned int* ctr = g_skinny_counters[p.slot];
   const unsigned int a_target = static_cast<unsigned int>(p.a_splits);
+  const unsigned int done_target = static_cast<unsigned int>(p.a_splits + p.tiles);
   if (static_cast<int64_t>(blockIdx.x) < p.a_splits) {
     adapter_part<MB>(p, blockIdx.x);
     drain_stores();
     __syncthreads();
-    if (tid == 0) __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0) {
+      __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      drain_stores();  // the arrival is performed before it is counted as done
+      done_count(ctr, 1, 2, done_target);
+    }
     return;
   }
   const int64_t b = static_cast<int64_t>(blockIdx.x) - p.a_splits;
@@ -432,23 +448,19 @@ __global__ void __launch_bounds__(256) k_skinny(SkinnyParams p) {
     // it only grows until every finisher is past its wait
     const unsigned int adapters = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     int last = arrive(ctr + 2 + tile, static_cast<unsigned int>(p.splits)) ? 1 : 0;
-    if (last && adapters != a_target && !wait_adapters(ctr, a_target)) last = 2;
+    if (last && adapters != a_target && !wait_adapters(ctr, a_target, p.spin)) {
+      last = 2;
+      __hip_atomic_fetch_or(p.err, kDevErrSkinnyWait, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    // a finisher is past its last access to the slot once its wait ended
+    if (last) done_count(ctr, 1, 2, done_target);
     flag = last;
   }
   __syncthreads();
   const int state = flag;
   if (state == 0) return;
-  // one lane of another wave counts the finished tile while the block works;
-  // the last one returns the adapter word to zero
-  unsigned int done_old = 0;
-  if (tid == 64)
-    done_old = __hip_atomic_fetch_add(ctr + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   // state 2: the adapters never arrived within the spin limit; h is poisoned
   finish_tile<MB, T, WK>(p, tile, h_lds, b_lds, state == 2);
-  if (tid == 64 && done_old + 1u == static_cast<unsigned int>(p.tiles)) {
-    __hip_atomic_store(ctr + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
 }
 
 // (id, T, U, WK): wave = 16 T rows x 128 U columns; block = 4 / WK waves of
@@ -503,10 +515,9 @@ SkinnyPlan make_plan(const SkinnyCfg& c, int64_t m, int64_t n, int64_t k) {
 // Measured on the three Qwen3-2B projection shapes for M in {1, 4, 16, 64}:
 // 64-row tiles with 512-column splits (two row waves x two column waves) are
 // best or within 5% except for single-block M with K >= N, where 32-row
-// tiles with 1024-column splits win. RPX_SKINNY_TILE=<id> forces a shape.
+// tiles with 1024-column splits win. The kTuneSkinnyTile knob forces a shape.
 SkinnyPlan plan_skinny(int64_t m, int64_t n, int64_t k) {
-  const char* env = std::getenv("RPX_SKINNY_TILE");
-  int want = env != nullptr ? std::atoi(env) : 0;
+  int want = tune(kTuneSkinnyTile);
   if (want <= 0) want = ((m + 15) / 16 == 1 && k >= n) ? 12 : 7;
   for (const SkinnyCfg& c : kSkinnyCfgs) {
     const SkinnyPlan p = make_plan(c, m, n, k);
@@ -546,6 +557,8 @@ bool launch_mb(int id, const SkinnyParams& a, hipStream_t stream) {
 }
 
 }  // namespace
+
+int skinny_tile_count() { return static_cast<int>(sizeof(kSkinnyCfgs) / sizeof(kSkinnyCfgs[0])); }
 
 bool skinny_ok(int64_t m, int64_t n, int64_t k, int64_t rank, int64_t n_groups, int64_t group) {
   if (m < 1 || m > 64 || k % 128 != 0 || rank < 1 || rank > 64) return false;
@@ -593,6 +606,9 @@ hipError_t launch_skinny_forward(const uint16_t* x, int64_t m, int64_t k, const 
   a.part_w = ws;
   a.part_h = a.part_w + p.splits * p.tiles * frags_per_tile(p) * 256;
   a.slot = static_cast<int>(g_calls.fetch_add(1, std::memory_order_relaxed) % kSlots);
+  a.spin = tune(kTuneSpinLimit) > 0 ? tune(kTuneSpinLimit) : kSpinLimit;
+  a.err = device_error_word();
+  if (a.err == nullptr) return hipErrorInvalidSymbol;
   bool ok = false;
   switch (p.mb) {
     case 1: ok = launch_mb<1>(p.cfg.id, a, stream); break;

@@ -34,6 +34,7 @@
 #include "coherent.h"
 #include "common.h"
 #include "kernels.h"
+#include "tuning.h"
 
 namespace rpx {
 
@@ -67,11 +68,14 @@ struct Skinny2Params {
   int a_blocks;          // slices * ceil(rank / 16)
   int b_vec;             // B rows may be touched with 16-byte loads
   // one-launch form: the call's slot of arrival words ([0] adapter blocks,
-  // [1] h published, [2] weight blocks; zero between calls) and the
-  // published h as f32 [M, rank]
+  // [1] h published, [2] done: weight blocks and the publishing adapter
+  // block; zero between calls), the published h as f32 [M, rank], the polls
+  // of the bounded wait and the device error word
   int slot;
   float* hf;
   int w_blocks;
+  int spin;
+  unsigned int* err;
 };
 
 __device__ __forceinline__ u32x4_t ld16(const void* p) {
@@ -342,12 +346,15 @@ __global__ void __launch_bounds__(kFinThreads) k_skinny_finish(Skinny2Params p) 
 // LoRA term to its own rows after a bounded wait for the flag, so the
 // finishing launch and its dispatch disappear. Adapter blocks come first in
 // the grid and wait on nothing, so the wait ends once they have run; the
-// spin limit only guarantees that every wave exits (h then reads as NaN).
-// Slots are taken in turn and left at zero by every call: at most kSlots
-// calls may run at once on a device.
+// spin limit only guarantees that every wave exits (h then reads as NaN and
+// the device error word gets kDevErrSkinnyOneWait). Slots are taken in turn:
+// at most kSlots calls may run at once on a device. Every call leaves its
+// slot at zero, also when waits expired: the weight blocks (after their
+// wait) and the publishing adapter block (after raising the flag) count into
+// a done word, and the last of them clears the slot.
 
 constexpr int kSlots2 = 8;
-constexpr int kSpin2 = 1 << 22;
+constexpr int kSpin2 = 1 << 22;  // default polls of the bounded wait
 __device__ unsigned int g_skinny2_state[kSlots2][4];
 
 template <int NW>
@@ -382,7 +389,11 @@ __device__ __forceinline__ void adapter_block_one(const Skinny2Params& p, int a,
   }
   drain_stores();
   __syncthreads();
-  if (threadIdx.x == 0) __hip_atomic_store(state + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (threadIdx.x == 0) {
+    __hip_atomic_store(state + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    drain_stores();  // the flag is visible before this block counts as done
+    done_count(state, 2, 3, static_cast<unsigned int>(p.w_blocks) + 1u);
+  }
 }
 
 template <int NW, int CPW>
@@ -435,13 +446,18 @@ __device__ __forceinline__ void weight_block_one(const Skinny2Params& p, int64_t
   int ready = 1;
   if (lane == 0) {
     ready = 0;
-    for (int it = 0; it < kSpin2; ++it) {
+    for (int it = 0; it < p.spin; ++it) {
       if (__hip_atomic_load(state + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u) {
         ready = 1;
         break;
       }
       __builtin_amdgcn_s_sleep(1);
     }
+    if (!ready)
+      __hip_atomic_fetch_or(p.err, kDevErrSkinnyOneWait, __ATOMIC_RELAXED,
+                            __HIP_MEMORY_SCOPE_AGENT);
+    // past its last access to the slot
+    done_count(state, 2, 3, static_cast<unsigned int>(p.w_blocks) + 1u);
   }
   ready = __shfl(ready, 0, 64);
   // the h loads below must not be issued before the flag was seen
@@ -461,9 +477,6 @@ __device__ __forceinline__ void weight_block_one(const Skinny2Params& p, int64_t
                       pack_bf16x2(hv[6], hv[7])};
     t = mfma16(bfr[q], hfr, t);
   }
-  // the last weight block to get here returns the h flag to zero
-  if (lane == 0 && arrive(state + 2, static_cast<unsigned int>(p.w_blocks)))
-    __hip_atomic_store(state + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   if (rl >= p.m) return;
   // lane: y[m = rl][n = n0 + 4 g + v]
   uint16_t o[4];
@@ -502,13 +515,10 @@ std::atomic<unsigned int> g_calls2{0};
 // flag, the weight blocks' reads) that the weight stream hides only when it
 // is long: measured on the Qwen3-2B shapes at M = 1, 6144 -> 2048 takes
 // 11.3 us against 13.5 us for two launches, but 2048 -> 6144 12.8 against
-// 10.5 and 2048 -> 2048 9.7 against 8.2. Chosen for K >= 4096;
-// RPX_SKINNY2_ONE=1 / 0 forces either form.
+// 10.5 and 2048 -> 2048 9.7 against 8.2. Chosen for K >= 4096; the
+// kTuneSkinny2One knob forces either form.
 bool one_launch_selected(int64_t k) {
-  static const int force = [] {
-    const char* env = std::getenv("RPX_SKINNY2_ONE");
-    return env == nullptr ? -1 : std::atoi(env);
-  }();
+  const int force = tune(kTuneSkinny2One);
   if (force == 0) return false;
   if (force > 0) return true;
   return k >= 4096;
@@ -552,15 +562,13 @@ bool skinny2_ok(int64_t m, int64_t n, int64_t k, int64_t rank, int64_t n_groups,
 // Measured on the three Qwen3-2B projection shapes (group 64, rank 32,
 // weights cycled beyond the 256 MB MALL): 30-40% faster than the one-launch
 // kernel for M <= 4, slower at M = 16, where every weight block re-reads all
-// of x and the finish handles 16 rows of y. RPX_SKINNY2=1 selects it for
-// every M <= 16, RPX_SKINNY2=0 never; RPX_SKINNY_TILE (a one-launch shape)
-// also turns it off.
+// of x and the finish handles 16 rows of y. The kTuneSkinny2 knob selects it
+// for every M <= 16 (1) or never (0); a forced one-launch tile shape
+// (kTuneSkinnyTile) also turns it off.
 bool skinny2_selected(int64_t m, int64_t n, int64_t k, int64_t rank, int64_t n_groups,
                       int64_t group) {
-  const char* tile = std::getenv("RPX_SKINNY_TILE");
-  if (tile != nullptr && std::atoi(tile) > 0) return false;
-  const char* env = std::getenv("RPX_SKINNY2");
-  const int force = env != nullptr ? std::atoi(env) : -1;
+  if (tune(kTuneSkinnyTile) > 0) return false;
+  const int force = tune(kTuneSkinny2);
   if (force == 0) return false;
   if (force != 1 && m > 4) return false;
   return skinny2_ok(m, n, k, rank, n_groups, group);
@@ -602,7 +610,11 @@ hipError_t launch_skinny2_forward(const uint16_t* x, int64_t m, int64_t k, const
   p.hf = ws + static_cast<int64_t>(p.slices) * m * rank;
   p.w_blocks = static_cast<int>(ceil_div(n, 16));
   p.slot = 0;
+  p.spin = tune(kTuneSpinLimit) > 0 ? tune(kTuneSpinLimit) : kSpin2;
+  p.err = nullptr;
   if (one_launch_selected(k)) {
+    p.err = device_error_word();
+    if (p.err == nullptr) return hipErrorInvalidSymbol;
     p.slot = static_cast<int>(g_calls2.fetch_add(1, std::memory_order_relaxed) % kSlots2);
     bool one = false;
 #define RPX_ONE(NW, CPW)                              \

@@ -58,6 +58,16 @@ def _workspace(nbytes: int, device: torch.device) -> torch.Tensor:
     return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
 
 
+def _aligned(t: torch.Tensor | None) -> torch.Tensor | None:
+    """Dense and 16-byte aligned (the vectorized kernels' contract); copies
+    only views that are not."""
+
+    if t is None:
+        return None
+    t = t.contiguous()
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
 def _u16(t: torch.Tensor) -> torch.Tensor:
     """View bf16/int16/uint16 storage as uint16 bit patterns."""
 
@@ -70,6 +80,66 @@ def _u16(t: torch.Tensor) -> torch.Tensor:
 
 def group_arg(group_size: int | None, k: int) -> int:
     return 0 if group_size is None or group_size == k else int(group_size)
+
+
+# ---------------------------------------------------------------------------
+# Kernel-variant knobs and the device error word
+# ---------------------------------------------------------------------------
+TUNING_KNOBS = {
+    "int4_tile": nat.TUNE_INT4_TILE,
+    "bf16_tile": nat.TUNE_BF16_TILE,
+    "fp8_tile": nat.TUNE_FP8_TILE,
+    "skinny_tile": nat.TUNE_SKINNY_TILE,
+    "skinny2": nat.TUNE_SKINNY2,
+    "skinny2_one": nat.TUNE_SKINNY2_ONE,
+    "spin_limit": nat.TUNE_SPIN_LIMIT,
+}
+
+
+def get_tuning(knob: str) -> int:
+    return int(nat.load().rpx_get_tuning(TUNING_KNOBS[knob]))
+
+
+def set_tuning(knob: str, value: int) -> int:
+    """Force a kernel variant for later calls (process-wide); returns the
+    previous value. ``ValueError`` for an unknown value."""
+
+    code = TUNING_KNOBS[knob]
+    previous = get_tuning(knob)
+    nat.call("rpx_set_tuning", code, int(value))
+    return previous
+
+
+class tuning:
+    """Context manager: ``with ops.tuning(int4_tile=10): ...`` sets knobs for
+    the block and restores their previous values afterwards."""
+
+    def __init__(self, **knobs: int):
+        self._knobs = knobs
+        self._saved: dict[str, int] = {}
+
+    def __enter__(self):
+        for name, value in self._knobs.items():
+            self._saved[name] = set_tuning(name, value)
+        return self
+
+    def __exit__(self, *exc):
+        for name, value in self._saved.items():
+            set_tuning(name, value)
+        return False
+
+
+def check_device_errors(device: torch.device | None = None) -> int:
+    """Synchronize the current stream and raise ``DeviceError`` if a kernel
+    reported an expired bounded wait since the last check (its outputs then
+    hold NaN); returns the raw bits otherwise (0)."""
+
+    nat.load()
+    dev = torch.device("cuda", torch.cuda.current_device()) if device is None else device
+    flags = ctypes.c_uint32(0)
+    with torch.cuda.device(dev):
+        nat.call("rpx_check_device_errors", _stream(dev), ctypes.byref(flags))
+    return int(flags.value)
 
 
 # ---------------------------------------------------------------------------
@@ -141,17 +211,17 @@ def int4lora_forward(x2d, packed, scale_bits, lora_a_c, lora_b_c, *, scaling: fl
     r = lora_a_c.shape[0]
     dt = x2d.dtype
     code = _dtype_code(dt)
-    x2d = x2d.contiguous()
-    a = lora_a_c.to(dt).contiguous()
-    b = lora_b_c.to(dt).contiguous()
+    x2d = _aligned(x2d)
+    a = _aligned(lora_a_c.to(dt))
+    b = _aligned(lora_b_c.to(dt))
     y = torch.empty((m, n), dtype=dt, device=device)
     h = torch.empty((m, r), dtype=dt, device=device)
     g = group_arg(group_size, k)
     ws_bytes = nat.query("rpx_int4lora_forward_workspace", m, n, k, g, r, code)
     ws = _workspace(ws_bytes, device)
     bias = None if bias_bits is None else _u16(bias_bits).contiguous()
-    nat.call("rpx_int4lora_forward", _ptr(x2d), code, m, k, _ptr(packed.contiguous()),
-             _ptr(_u16(scale_bits).contiguous()), n, g, _ptr(bias), _ptr(a), _ptr(b), r,
+    nat.call("rpx_int4lora_forward", _ptr(x2d), code, m, k, _ptr(_aligned(packed)),
+             _ptr(_aligned(_u16(scale_bits))), n, g, _ptr(bias), _ptr(a), _ptr(b), r,
              float(scaling), _ptr(y), _ptr(h), _ptr(ws), ws.numel(), _stream(device))
     return y, h
 
@@ -166,17 +236,17 @@ def int4lora_backward(grad, x2d, packed, scale_bits, lora_a_c, lora_b_c, h, *, s
     r = lora_a_c.shape[0]
     dt = x2d.dtype
     code = _dtype_code(dt)
-    grad = grad.to(dt).contiguous()
-    a = lora_a_c.to(dt).contiguous()
-    b = lora_b_c.to(dt).contiguous()
+    grad = _aligned(grad.to(dt))
+    a = _aligned(lora_a_c.to(dt))
+    b = _aligned(lora_b_c.to(dt))
     dx = torch.empty((m, k), dtype=dt, device=device)
     d_a = torch.empty((r, k), dtype=F32, device=device)
     d_b = torch.empty((n, r), dtype=F32, device=device)
     g = group_arg(group_size, k)
     ws_bytes = nat.query("rpx_int4lora_backward_workspace", m, n, k, g, r, code)
     ws = _workspace(ws_bytes, device)
-    nat.call("rpx_int4lora_backward", _ptr(grad), _ptr(x2d.contiguous()), code, m, k,
-             _ptr(packed.contiguous()), _ptr(_u16(scale_bits).contiguous()), n, g, _ptr(a),
+    nat.call("rpx_int4lora_backward", _ptr(grad), _ptr(_aligned(x2d)), code, m, k,
+             _ptr(_aligned(packed)), _ptr(_aligned(_u16(scale_bits))), n, g, _ptr(a),
              _ptr(b), r, float(scaling), _ptr(h.contiguous()), _ptr(dx), _ptr(d_a), _ptr(d_b),
              _ptr(ws), ws.numel(), _stream(device))
     return dx, d_a, d_b
@@ -199,18 +269,18 @@ def int4lora_forward_act(x2d, packed, scale_bits, lora_a_c, lora_b_c, *, activat
     r = lora_a_c.shape[0]
     dt = x2d.dtype
     code = _dtype_code(dt)
-    x2d = x2d.contiguous()
-    a = lora_a_c.to(dt).contiguous()
-    b = lora_b_c.to(dt).contiguous()
-    gate = None if gate is None else gate.to(dt).contiguous()
+    x2d = _aligned(x2d)
+    a = _aligned(lora_a_c.to(dt))
+    b = _aligned(lora_b_c.to(dt))
+    gate = None if gate is None else _aligned(gate.to(dt))
     y = torch.empty((m, n), dtype=dt, device=device)
     z = torch.empty((m, n), dtype=dt, device=device)
     h = torch.empty((m, r), dtype=dt, device=device)
     g = group_arg(group_size, k)
     ws = _workspace(nat.query("rpx_int4lora_forward_workspace", m, n, k, g, r, code), device)
     bias = None if bias_bits is None else _u16(bias_bits).contiguous()
-    nat.call("rpx_int4lora_forward_act", _ptr(x2d), code, m, k, _ptr(packed.contiguous()),
-             _ptr(_u16(scale_bits).contiguous()), n, g, _ptr(bias), _ptr(a), _ptr(b), r,
+    nat.call("rpx_int4lora_forward_act", _ptr(x2d), code, m, k, _ptr(_aligned(packed)),
+             _ptr(_aligned(_u16(scale_bits))), n, g, _ptr(bias), _ptr(a), _ptr(b), r,
              float(scaling), act, _ptr(gate), _ptr(y), _ptr(z), _ptr(h), _ptr(ws), ws.numel(),
              _stream(device))
     return y, z, h
@@ -232,19 +302,19 @@ def int4lora_backward_act(grad, x2d, packed, scale_bits, lora_a_c, lora_b_c, h, 
     r = lora_a_c.shape[0]
     dt = x2d.dtype
     code = _dtype_code(dt)
-    grad = grad.to(dt).contiguous()
-    a = lora_a_c.to(dt).contiguous()
-    b = lora_b_c.to(dt).contiguous()
-    z = z.to(dt).contiguous()
-    gate = None if gate is None else gate.to(dt).contiguous()
+    grad = _aligned(grad.to(dt))
+    a = _aligned(lora_a_c.to(dt))
+    b = _aligned(lora_b_c.to(dt))
+    z = _aligned(z.to(dt))
+    gate = None if gate is None else _aligned(gate.to(dt))
     dz = torch.empty((m, k), dtype=dt, device=device)
     dgate = torch.empty((m, k), dtype=dt, device=device) if act == nat.ACT_SILU_MUL else None
     d_a = torch.empty((r, k), dtype=F32, device=device)
     d_b = torch.empty((n, r), dtype=F32, device=device)
     g = group_arg(group_size, k)
     ws = _workspace(nat.query("rpx_int4lora_backward_workspace", m, n, k, g, r, code), device)
-    nat.call("rpx_int4lora_backward_act", _ptr(grad), _ptr(x2d.contiguous()), code, m, k,
-             _ptr(packed.contiguous()), _ptr(_u16(scale_bits).contiguous()), n, g, _ptr(a),
+    nat.call("rpx_int4lora_backward_act", _ptr(grad), _ptr(_aligned(x2d)), code, m, k,
+             _ptr(_aligned(packed)), _ptr(_aligned(_u16(scale_bits))), n, g, _ptr(a),
              _ptr(b), r, float(scaling), _ptr(h.contiguous()), act, _ptr(z), _ptr(gate),
              _ptr(dz), _ptr(dgate), _ptr(d_a), _ptr(d_b), _ptr(ws), ws.numel(), _stream(device))
     return dz, dgate, d_a, d_b
@@ -273,6 +343,78 @@ class Int4LoRALinearFn(torch.autograd.Function):
         dx, d_a, d_b = int4lora_backward(grad_y, x2d, packed, scale_bits, lora_a_c, lora_b_c, h,
                                          scaling=ctx.scaling, group_size=ctx.group_size)
         return (dx, d_a.to(lora_a_c.dtype), d_b.to(lora_b_c.dtype), None, None, None, None, None)
+
+
+def int4lora_forward_promoted(x2d, packed, scale_bits, lora_a, lora_b, *, scaling: float,
+                              group_size: int | None = None, bias_bits=None):
+    """No precision policy, bf16 ``x`` and float32 masters: ``(y f32 [M, N],
+    h f32 [M, r])`` with the base product in bf16 and the adapter promoted
+    to float32, as ``jnp.matmul`` does in the reference."""
+
+    device = _on_device(x2d, packed, scale_bits, lora_a, lora_b, bias_bits)
+    if x2d.dtype != BF16 or lora_a.dtype != F32 or lora_b.dtype != F32:
+        raise TypeError("the promoted INT4 + LoRA linear takes bf16 x and float32 masters")
+    m, k = x2d.shape
+    n = packed.shape[-2]
+    r = lora_a.shape[0]
+    x2d = _aligned(x2d)
+    y = torch.empty((m, n), dtype=F32, device=device)
+    h = torch.empty((m, r), dtype=F32, device=device)
+    g = group_arg(group_size, k)
+    ws = _workspace(nat.query("rpx_int4lora_forward_promoted_workspace", m, n, k, g, r), device)
+    bias = None if bias_bits is None else _aligned(_u16(bias_bits))
+    nat.call("rpx_int4lora_forward_promoted", _ptr(x2d), m, k, _ptr(_aligned(packed)),
+             _ptr(_aligned(_u16(scale_bits))), n, g, _ptr(bias), _ptr(_aligned(lora_a)),
+             _ptr(_aligned(lora_b)), r, float(scaling), _ptr(y), _ptr(h), _ptr(ws), ws.numel(),
+             _stream(device))
+    return y, h
+
+
+def int4lora_backward_promoted(grad, x2d, packed, scale_bits, lora_a, lora_b, h, *,
+                               scaling: float, group_size: int | None = None):
+    """``(dx bf16 [M, K], dA f32 [r, K], dB f32 [N, r])`` of the promoted
+    forward, from the float32 output gradient."""
+
+    device = _on_device(grad, x2d, packed, scale_bits, lora_a, lora_b, h)
+    m, k = x2d.shape
+    n = packed.shape[-2]
+    r = lora_a.shape[0]
+    grad = _aligned(grad.to(F32))
+    dx = torch.empty((m, k), dtype=BF16, device=device)
+    d_a = torch.empty((r, k), dtype=F32, device=device)
+    d_b = torch.empty((n, r), dtype=F32, device=device)
+    g = group_arg(group_size, k)
+    ws = _workspace(nat.query("rpx_int4lora_backward_promoted_workspace", m, n, k, g, r), device)
+    nat.call("rpx_int4lora_backward_promoted", _ptr(grad), _ptr(_aligned(x2d)), m, k,
+             _ptr(_aligned(packed)), _ptr(_aligned(_u16(scale_bits))), n, g,
+             _ptr(_aligned(lora_a)), _ptr(_aligned(lora_b)), r, float(scaling),
+             _ptr(_aligned(h)), _ptr(dx), _ptr(d_a), _ptr(d_b), _ptr(ws), ws.numel(),
+             _stream(device))
+    return dx, d_a, d_b
+
+
+class Int4LoRAPromotedFn(torch.autograd.Function):
+    """Autograd node of the promoted INT4 + LoRA linear (no policy, bf16
+    activations, float32 masters): float32 output, bf16 input gradient,
+    float32 master gradients."""
+
+    @staticmethod
+    def forward(ctx, x2d, lora_a, lora_b, packed, scale_bits, bias_bits, scaling, group_size):
+        y, h = int4lora_forward_promoted(x2d, packed, scale_bits, lora_a, lora_b,
+                                         scaling=scaling, group_size=group_size,
+                                         bias_bits=bias_bits)
+        ctx.save_for_backward(x2d, lora_a, lora_b, packed, scale_bits, h)
+        ctx.scaling = scaling
+        ctx.group_size = group_size
+        return y
+
+    @staticmethod
+    def backward(ctx, grad_y):
+        x2d, lora_a, lora_b, packed, scale_bits, h = ctx.saved_tensors
+        dx, d_a, d_b = int4lora_backward_promoted(grad_y, x2d, packed, scale_bits, lora_a, lora_b,
+                                                  h, scaling=ctx.scaling,
+                                                  group_size=ctx.group_size)
+        return dx, d_a, d_b, None, None, None, None, None
 
 
 class Int4LoRAGeluMLPFn(torch.autograd.Function):
@@ -485,14 +627,30 @@ def _dense_2d(t: torch.Tensor) -> torch.Tensor:
     return t.contiguous()
 
 
+def _check_fp8_operands(left, right) -> None:
+    """The reference's per-tensor scale is ``max(|t|)`` over each operand
+    (precision.py:133-135), a max-reduction with no identity: it raises on
+    an empty operand, so any zero among M, K, N is an error here too."""
+
+    if left.dim() != 2 or right.dim() != 2 or left.shape[1] != right.shape[0]:
+        raise ValueError(f"fp8 linear needs left [M, K] and right [K, N]; got "
+                         f"{tuple(left.shape)} and {tuple(right.shape)}")
+    m, k = left.shape
+    n = right.shape[1]
+    if m == 0 or n == 0 or k == 0:
+        raise ValueError(f"fp8 linear: empty operand (M={m}, K={k}, N={n}); the per-tensor "
+                         "amax of an empty tensor is undefined")
+
+
 def fp8_linear_forward(left, right, out_dtype=BF16, save_codes=False):
     """``(out [M, N], scales f32[2], codes)`` for ``left [M,K] . right [K,N]``.
 
     With ``save_codes`` the same cast pass also returns the backward's operand
     codes ``(left^T codes [K, M], right codes [K, N])``; otherwise ``codes``
-    is None.
+    is None. ``ValueError`` for an empty operand, as in the reference.
     """
 
+    _check_fp8_operands(left, right)
     device = _on_device(left, right)
     left = left.contiguous()
     right = _dense_2d(right)
@@ -504,10 +662,6 @@ def fp8_linear_forward(left, right, out_dtype=BF16, save_codes=False):
     if save_codes:
         codes = (torch.empty((k, m), dtype=torch.uint8, device=device),
                  torch.empty((k, n), dtype=torch.uint8, device=device))
-    if m == 0 or n == 0:
-        return out, scales, codes
-    if k == 0:
-        raise ValueError("fp8 linear needs a non-empty contraction")
     ws = _workspace(nat.query("rpx_fp8_linear_forward_workspace", m, n, k), device)
     nat.call("rpx_fp8_linear_forward", _ptr(left), _dtype_code(left.dtype), m, k, _ptr(right),
              _dtype_code(right.dtype), n, right.stride(0), right.stride(1), _ptr(out),
@@ -659,6 +813,7 @@ class Fp8DelayedLinearFn(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, left, right, out_dtype, state, slots):
+        _check_fp8_operands(left, right)
         _on_device(left, right)
         left = left.contiguous()
         right = _dense_2d(right)
@@ -666,10 +821,6 @@ class Fp8DelayedLinearFn(torch.autograd.Function):
         n = right.shape[1]
         s_l, s_r, s_g = (state.scales[i:i + 1] for i in slots)
         out = torch.empty((m, n), dtype=out_dtype, device=left.device)
-        if m == 0 or n == 0:
-            return out
-        if k == 0:
-            raise ValueError("fp8 linear needs a non-empty contraction")
         need = left.requires_grad or right.requires_grad
         # left -> codes [M, K] (+ [K, M] for d_right); right [K, N] -> codes
         # [N, K] for this product (+ [K, N] for d_left); one launch

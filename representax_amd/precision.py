@@ -9,6 +9,7 @@ matmul, as the reference does with ``jnp.matmul``.
 
 from __future__ import annotations
 
+import math
 from collections.abc import Iterator
 from contextlib import contextmanager
 from contextvars import ContextVar
@@ -43,6 +44,7 @@ class DelayedScaling:
     """
 
     FMAX = {"e4m3fn": 448.0, "e5m2": 57344.0}
+    _instances = 0
 
     def __init__(self, n_slots: int, history_len: int = 16,
                  device: torch.device | str = "cuda") -> None:
@@ -59,7 +61,9 @@ class DelayedScaling:
         self.amax_pending = torch.zeros((self.n_slots, words), dtype=torch.uint32, device=device)
         self.cursor = torch.zeros(1, dtype=torch.int32, device=device)
         self._next = 0
-        self._owners: dict[int, tuple[int, ...]] = {}
+        DelayedScaling._instances += 1
+        self._token = DelayedScaling._instances  # never reused within a process
+        self._named: dict[str, dict[int, tuple[int, ...]]] = {}
 
     def allocate(self, formats: tuple[str, ...]) -> tuple[int, ...]:
         """Fresh slots, one per entry of ``formats`` ("e4m3fn" / "e5m2")."""
@@ -74,12 +78,28 @@ class DelayedScaling:
         return slots
 
     def slots_for(self, owner: object, formats: tuple[str, ...]) -> tuple[int, ...]:
-        """The slots of ``owner`` (allocated on its first use)."""
+        """The slots of ``owner`` (allocated on its first use): a module, or a
+        name (a string such as the module's path).
 
-        key = id(owner)
-        if key not in self._owners:
-            self._owners[key] = self.allocate(formats)
-        return self._owners[key]
+        A module's assignment is stored on the module itself, keyed by this
+        state, so copies of it (``model_for_compute`` deep-copies the model
+        every step) keep using their original's slots, and no other module
+        can inherit a dead module's scale history.
+        """
+
+        if isinstance(owner, str):
+            table = self._named.setdefault(owner, {})
+        else:
+            table = getattr(owner, "_fp8_delayed_slots", None)
+            if table is None:
+                table = {}
+                object.__setattr__(owner, "_fp8_delayed_slots", table)
+        if self._token not in table:
+            table[self._token] = self.allocate(formats)
+        slots = table[self._token]
+        if len(slots) != len(formats):
+            raise ValueError("delayed-scale slots of this owner were allocated for other formats")
+        return slots
 
     def update(self) -> None:
         ops.fp8_scale_update(self)
@@ -253,7 +273,7 @@ def linear_matmul(left: torch.Tensor, right: torch.Tensor, *, out_sharding: Any 
     if policy is None or policy.matrix_dtype != torch.float8_e4m3fn:
         return torch.matmul(left, right)
     leading = left.shape[:-1]
-    flat = left.reshape(-1, left.shape[-1])
+    flat = left.reshape(math.prod(leading), left.shape[-1])
     if policy.fp8_state is not None and fp8_owner is not None:
         slots = policy.fp8_state.slots_for(fp8_owner, LINEAR_FORMATS)
         out = ops.Fp8DelayedLinearFn.apply(flat, right, policy.activation_dtype,

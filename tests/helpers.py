@@ -50,3 +50,59 @@ def rel_l2(actual, expected) -> float:
     if denom == 0:
         return float(np.linalg.norm(a))
     return float(np.linalg.norm(a - e) / denom)
+
+
+def ulp_diff(a_bits: np.ndarray, b_bits: np.ndarray) -> np.ndarray:
+    """Distance in bf16 units in the last place (same-sign finite values)."""
+
+    def ordered(u):
+        u = u.astype(np.int32)
+        return np.where(u & 0x8000, 0x8000 - (u & 0x7FFF), 0x8000 + u)
+
+    return np.abs(ordered(a_bits) - ordered(b_bits))
+
+
+TINY = 1e-30  # below it f32 intermediates are subnormal; results only need to stay tiny
+
+
+def assert_act_bits(got_bits: np.ndarray, want_f32: np.ndarray):
+    """The activation is evaluated in f32 on the GPU (an erfc fit with
+    fractional error < 1.2e-7, the hardware exp2 and reciprocal) and exactly
+    in the oracle: identical bits except where the exact value sits within a
+    few f32 ulps of a bf16 rounding boundary, and then one bf16 ulp. Results
+    below 1e-30 in magnitude (f32 subnormal intermediates) must stay below it."""
+
+    got_bits = got_bits.reshape(-1)
+    want = np.asarray(want_f32, np.float32).reshape(-1)
+    want_bits = f32_to_bf16_bits(want)
+    got = (got_bits.astype(np.uint32) << 16).view(np.float32)
+    tiny = np.abs(want) < TINY
+    assert np.all(np.abs(got[tiny]) < TINY)
+    d = ulp_diff(got_bits[~tiny], want_bits[~tiny])
+    if d.size:
+        i = int(np.argmax(d))
+        assert d[i] <= 1, (d[i], float(got[~tiny][i]), float(want[~tiny][i]))
+        assert np.mean(d > 0) < 1e-2
+
+
+# Parity bars for bf16 outputs of the fp32-accumulating kernels against the
+# oracle's float64 accumulation (the rounding points are the same; only
+# results whose exact value sits next to a bf16 rounding boundary can differ,
+# by one ulp).
+BF16_REL_TOL = 2e-3
+BF16_MIN_EQUAL = 0.99
+# dA / dB reduce over every token (32,768 in the BERT step) in float32
+# partials: about 1% of them land one ulp from the float64 oracle's value
+BF16_MIN_EQUAL_TOKEN_SUM = 0.97
+
+
+def assert_bf16_close(got: np.ndarray, want: np.ndarray, tol: float = BF16_REL_TOL,
+                      min_equal: float | None = BF16_MIN_EQUAL, what: str = ""):
+    """rel-L2 within ``tol`` and, when ``min_equal`` is given, at least that
+    fraction of elements equal to the oracle's bf16 value."""
+
+    err = rel_l2(got, want)
+    assert err < tol, (what, err)
+    if min_equal is not None and np.size(want):
+        eq = float(np.mean(np.asarray(got, np.float32) == np.asarray(want, np.float32)))
+        assert eq >= min_equal, (what, eq)

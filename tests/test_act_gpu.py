@@ -7,7 +7,8 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import DEVICE, bf16_values, bits_from_dev, from_dev, rel_l2, rng, to_dev, to_dev_bf16
+from tests.helpers import (BF16_REL_TOL, assert_act_bits, bf16_values, bits_from_dev, from_dev,
+                           rel_l2, rng, to_dev, to_dev_bf16)
 from oracle import act as oact
 from oracle import int4 as oint4
 from oracle import lora as olora
@@ -16,40 +17,7 @@ from representax_amd import ops
 
 pytestmark = pytest.mark.gpu
 
-TOL = 1e-2
-
-
-def _ulp_diff(a_bits: np.ndarray, b_bits: np.ndarray) -> np.ndarray:
-    """Distance in bf16 units in the last place (same-sign finite values)."""
-
-    def ordered(u):
-        u = u.astype(np.int32)
-        return np.where(u & 0x8000, 0x8000 - (u & 0x7FFF), 0x8000 + u)
-
-    return np.abs(ordered(a_bits) - ordered(b_bits))
-
-
-TINY = 1e-30  # below it f32 intermediates are subnormal; results only need to stay tiny
-
-
-def _assert_act_bits(got_bits: np.ndarray, want_f32: np.ndarray):
-    """The activation is evaluated in f32 on the GPU (an erfc fit with
-    fractional error < 1.2e-7, the hardware exp2 and reciprocal) and exactly
-    in the oracle: identical bits except where the exact value sits within a
-    few f32 ulps of a bf16 rounding boundary, and then one bf16 ulp. Results
-    below 1e-30 in magnitude (f32 subnormal intermediates) must stay below it."""
-
-    got_bits = got_bits.reshape(-1)
-    want = np.asarray(want_f32, np.float32).reshape(-1)
-    want_bits = f32_to_bf16_bits(want)
-    got = (got_bits.astype(np.uint32) << 16).view(np.float32)
-    tiny = np.abs(want) < TINY
-    assert np.all(np.abs(got[tiny]) < TINY)
-    d = _ulp_diff(got_bits[~tiny], want_bits[~tiny])
-    if d.size:
-        i = int(np.argmax(d))
-        assert d[i] <= 1, (d[i], float(got[~tiny][i]), float(want[~tiny][i]))
-        assert np.mean(d > 0) < 1e-2
+TOL = BF16_REL_TOL
 
 
 def _linear(g, n, k, r, group, bias, b_scale=1.0):
@@ -98,7 +66,7 @@ def test_forward_act_matches_oracle(activation, m, k, n, r, group):
     # the activation of the GPU's own z, rounded once
     zg = from_dev(z)
     want = oact.act_forward(activation, zg, gate if activation == "silu_mul" else None)
-    _assert_act_bits(bits_from_dev(y), want)
+    assert_act_bits(bits_from_dev(y), want)
     # z equals the plain forward's y bit for bit
     y_plain, _ = ops.int4lora_forward(to_dev_bf16(x), d["packed"], d["scale_bits"], d["a"], d["b"],
                                       scaling=d["scaling"], group_size=group, bias_bits=d["bias"])
@@ -137,9 +105,9 @@ def test_backward_act_matches_oracle(activation, m, k, n, r, group):
     dxg = from_dev(dx)
     want_dz, want_dg = oact.act_backward(activation, dxg, z,
                                          gate if activation == "silu_mul" else None)
-    _assert_act_bits(bits_from_dev(dz), want_dz)
+    assert_act_bits(bits_from_dev(dz), want_dz)
     if activation == "silu_mul":
-        _assert_act_bits(bits_from_dev(dgate), want_dg)
+        assert_act_bits(bits_from_dev(dgate), want_dg)
     else:
         assert dgate is None
     # and the input gradient itself against the oracle

@@ -133,6 +133,54 @@ def test_fp8_policy_on_cpu_fails_loudly():
                              torch.randn(8, 2, dtype=torch.bfloat16))
 
 
+def test_fp8_linear_matmul_rejects_empty_operands():
+    """The reference's per-tensor amax is a max-reduction with no identity
+    (precision.py:133-135): an empty operand raises, under dynamic and
+    delayed scaling alike, before anything touches a device."""
+
+    from representax_amd import DelayedScaling
+
+    st = DelayedScaling(3, device="cpu")
+    owner = rx.Linear(torch.zeros(4, 8))
+    dynamic = rx.resolve_precision_policy(rx.PrecisionConfig.float8_mixed())
+    delayed = rx.resolve_precision_policy(
+        rx.PrecisionConfig.float8_mixed(fp8_scaling="delayed"), fp8_state=st)
+    cases = [((0, 8), (8, 4)), ((3, 0), (0, 4)), ((3, 8), (8, 0)), ((0, 0), (0, 0))]
+    for policy, kw in ((dynamic, {}), (delayed, {"fp8_owner": owner})):
+        with rx.precision_context(policy):
+            for ls, rs in cases:
+                left = torch.zeros(ls, dtype=torch.bfloat16)
+                right = torch.zeros(rs, dtype=torch.bfloat16)
+                with pytest.raises(ValueError, match="empty operand"):
+                    rx.linear_matmul(left, right, **kw)
+
+
+def test_delayed_slots_follow_module_copies():
+    """model_for_compute deep-copies the model every step: the copies keep
+    their original's slots (a state sized by for_model lasts any number of
+    steps), other modules and other states get their own."""
+
+    import copy
+
+    from representax_amd import DelayedScaling, Linear
+    from representax_amd.precision import LINEAR_FORMATS
+
+    model = torch.nn.Sequential(Linear(torch.zeros(4, 8)), Linear(torch.zeros(8, 4)))
+    st = DelayedScaling.for_model(model, device="cpu")
+    first = [st.slots_for(m, LINEAR_FORMATS) for m in model]
+    assert first == [(0, 1, 2), (3, 4, 5)]
+    policy = rx.resolve_precision_policy(rx.PrecisionConfig.bfloat16_mixed())
+    for _ in range(3):
+        view = rx.model_for_compute(model, policy)
+        assert [st.slots_for(m, LINEAR_FORMATS) for m in view] == first
+    other = DelayedScaling(3, device="cpu")
+    assert other.slots_for(model[1], LINEAR_FORMATS) == (0, 1, 2)
+    assert st.slots_for(model[1], LINEAR_FORMATS) == (3, 4, 5)
+    with pytest.raises(ValueError, match="slots"):
+        st.slots_for(Linear(torch.zeros(2, 2)), LINEAR_FORMATS)
+    assert copy.deepcopy(model[0])._fp8_delayed_slots == model[0]._fp8_delayed_slots
+
+
 def test_delayed_scaling_state_and_policy_on_cpu():
     """Slot bookkeeping of the delayed-scale state and the policy's checks
     (the buffers are plain tensors; no kernel runs here)."""

@@ -13,7 +13,10 @@ from tests.helpers import bf16_values, from_dev, rel_l2, rng, to_dev, to_dev_bf1
 
 pytestmark = pytest.mark.gpu
 
-FP8_TOL = 5e-2  # rel-L2 bound for fp8 GEMM outputs and gradients
+# rel-L2 bound for fp8 GEMM outputs and gradients: the fp8 products are exact
+# in float32, so only the accumulation order (and the final bf16 rounding)
+# separates the kernels from the oracle
+FP8_TOL = 2e-3
 
 
 def _all_bf16_values() -> np.ndarray:

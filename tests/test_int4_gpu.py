@@ -10,12 +10,13 @@ from oracle import int4 as oint4
 from oracle import lora as olora
 from oracle.codecs import bf16_bits_to_f32, f32_to_bf16_bits
 from representax_amd import ops
-from tests.helpers import bits_from_dev, bf16_values, from_dev, rel_l2, rng, to_dev, to_dev_bf16
+from tests.helpers import (BF16_REL_TOL, bits_from_dev, bf16_values, from_dev, rel_l2, rng, to_dev,
+                           to_dev_bf16)
 
 pytestmark = pytest.mark.gpu
 
 # bf16 rel-L2 bound for GEMM outputs and gradients (accumulation order only)
-TOL = 1e-2
+TOL = BF16_REL_TOL
 
 
 def _scale_patterns(count: int, seed: int) -> np.ndarray:
@@ -234,18 +235,19 @@ SKINNY_TILE_IDS = list(range(1, 15))
 
 @pytest.mark.parametrize("tile", SKINNY_TILE_IDS)
 @pytest.mark.parametrize("m,k,n,r,group", [(3, 1024, 200, 32, 64), (40, 640, 136, 16, None)])
-def test_skinny_every_tile_shape_matches_oracle(monkeypatch, tile, m, k, n, r, group):
+def test_skinny_every_tile_shape_matches_oracle(tile, m, k, n, r, group):
     """Each row-tile x K-split shape of the one-launch skinny kernel, including
     ragged last tiles and last splits."""
 
-    monkeypatch.setenv("RPX_SKINNY_TILE", str(tile))
     x, packed, scales, a, b, bias_bits, _ = _lora_case(m, k, n, r, group, seed=tile + m, bias=True)
     y_o, h_o = olora.lora_forward(x, packed, scales, a, b, alpha=2.0 * r, rank=r,
                                   bias_bits=bias_bits, group_size=group)
     biasd = to_dev(bias_bits.view(np.int16)).view(torch.uint16)
-    y, h = ops.int4lora_forward(to_dev_bf16(x), to_dev(packed),
-                                to_dev(scales.view(np.int16)).view(torch.uint16), to_dev_bf16(a),
-                                to_dev_bf16(b), scaling=2.0, group_size=group, bias_bits=biasd)
+    with ops.tuning(skinny_tile=tile):
+        y, h = ops.int4lora_forward(to_dev_bf16(x), to_dev(packed),
+                                    to_dev(scales.view(np.int16)).view(torch.uint16),
+                                    to_dev_bf16(a), to_dev_bf16(b), scaling=2.0, group_size=group,
+                                    bias_bits=biasd)
     torch.cuda.synchronize()
     assert rel_l2(from_dev(h), h_o) < TOL
     assert rel_l2(from_dev(y), y_o) < TOL
@@ -254,19 +256,22 @@ def test_skinny_every_tile_shape_matches_oracle(monkeypatch, tile, m, k, n, r, g
 @pytest.mark.parametrize("m,k,n,r,group", [(3, 1024, 200, 32, 64), (16, 640, 136, 48, None),
                                            (9, 256, 70, 5, 128), (1, 4096, 80, 64, 64),
                                            (2, 6144, 2048, 32, 64), (4, 384, 33, 8, None)])
-def test_skinny_two_launch_matches_oracle(monkeypatch, m, k, n, r, group):
-    """The two-launch path (forced for M up to 16): ragged last row blocks,
-    ranks that are not multiples of 8 and ranks above 32, several K slices."""
+@pytest.mark.parametrize("one", [0, 1])
+def test_skinny_two_launch_matches_oracle(one, m, k, n, r, group):
+    """The M <= 16 row-block path, forced: two launches, or the one-launch
+    form with the published h. Ragged last row blocks, ranks
+    that are not multiples of 8 and ranks above 32, several K slices."""
 
-    monkeypatch.setenv("RPX_SKINNY2", "1")
     x, packed, scales, a, b, bias_bits, _ = _lora_case(m, k, n, r, group, seed=m + r, bias=True)
     b = b * 50.0  # the adapter term comparable to the base product
     y_o, h_o = olora.lora_forward(x, packed, scales, a, b, alpha=2.0 * r, rank=r,
                                   bias_bits=bias_bits, group_size=group)
     biasd = to_dev(bias_bits.view(np.int16)).view(torch.uint16)
-    y, h = ops.int4lora_forward(to_dev_bf16(x), to_dev(packed),
-                                to_dev(scales.view(np.int16)).view(torch.uint16), to_dev_bf16(a),
-                                to_dev_bf16(b), scaling=2.0, group_size=group, bias_bits=biasd)
+    with ops.tuning(skinny2=1, skinny2_one=one):
+        y, h = ops.int4lora_forward(to_dev_bf16(x), to_dev(packed),
+                                    to_dev(scales.view(np.int16)).view(torch.uint16),
+                                    to_dev_bf16(a), to_dev_bf16(b), scaling=2.0, group_size=group,
+                                    bias_bits=biasd)
     torch.cuda.synchronize()
     assert rel_l2(from_dev(h), h_o) < TOL
     assert rel_l2(from_dev(y), y_o) < TOL
@@ -383,3 +388,121 @@ def test_module_empty_batch_gradients_are_zero():
     assert x.grad.shape == (0, 256)
     assert torch.count_nonzero(layer.lora_a.grad).item() == 0
     assert torch.count_nonzero(layer.lora_b.grad).item() == 0
+
+
+@pytest.mark.parametrize("m,k,n,r,group,bias", [(64, 256, 192, 16, None, True),
+                                                (300, 512, 320, 8, 64, False),
+                                                (5, 100, 52, 3, None, True)])
+def test_promoted_forward_backward_matches_oracle(m, k, n, r, group, bias):
+    """No precision policy on bf16 activations with float32 masters: the
+    bf16 base product (MFMA GEMM where the shape allows it, generic kernel
+    otherwise), the float32 adapter and output, and their transpose."""
+
+    x, packed, scales, a, b, bias_bits, _ = _lora_case(m, k, n, r, group, seed=m + 5 * r,
+                                                       bias=bias)
+    b = b * 20.0
+    gy = rng(77 + m).standard_normal((m, n)).astype(np.float32)
+    alpha = 3.0 * r
+    y_o, h_o = olora.lora_forward(x, packed, scales, a, b, alpha=alpha, rank=r,
+                                  bias_bits=bias_bits, group_size=group, compute="promoted")
+    pd = to_dev(packed)
+    sd = to_dev(scales.view(np.int16)).view(torch.uint16)
+    biasd = None if bias_bits is None else to_dev(bias_bits.view(np.int16)).view(torch.uint16)
+    xd = to_dev_bf16(x)
+    y, h = ops.int4lora_forward_promoted(xd, pd, sd, to_dev(a), to_dev(b), scaling=alpha / r,
+                                         group_size=group, bias_bits=biasd)
+    dx, da, db = ops.int4lora_backward_promoted(to_dev(gy), xd, pd, sd, to_dev(a), to_dev(b), h,
+                                                scaling=alpha / r, group_size=group)
+    torch.cuda.synchronize()
+    assert y.dtype == torch.float32 and h.dtype == torch.float32 and dx.dtype == torch.bfloat16
+    dx_o, da_o, db_o = olora.lora_backward(gy, x, packed, scales, a, b, from_dev(h), alpha=alpha,
+                                           rank=r, group_size=group, compute="promoted")
+    assert rel_l2(from_dev(h), h_o) < 1e-5
+    assert rel_l2(from_dev(y), y_o) < TOL
+    assert rel_l2(from_dev(dx), dx_o) < TOL
+    assert rel_l2(from_dev(da), da_o) < 1e-4
+    assert rel_l2(from_dev(db), db_o) < 1e-4
+
+
+def test_module_without_policy_promotes_to_float32():
+    """QuantizedLoRALinear called on bf16 activations with no precision
+    context (the reference's inference setting) returns float32 and sends
+    float32 gradients to the masters."""
+
+    import representax_amd as rx
+
+    lin = rx.Linear.init(256, 192, key=1, scale=0.02, bias=True, device="cuda")
+    layer = rx.QuantizedLoRALinear.from_linear(lin, rank=8, alpha=16.0, key=3)
+    with torch.no_grad():
+        layer.lora_b.normal_(0.0, 0.5)
+    x = to_dev_bf16(bf16_values(rng(5).standard_normal((48, 256)))).requires_grad_(True)
+    y = layer(x)
+    assert y.dtype == torch.float32
+    gy = torch.from_numpy(rng(6).standard_normal((48, 192)).astype(np.float32)).cuda()
+    y.backward(gy)
+    torch.cuda.synchronize()
+    assert x.grad.dtype == torch.bfloat16 and layer.lora_a.grad.dtype == torch.float32
+    packed = layer.packed_weight.cpu().numpy()
+    scales = layer.scale_bits.view(torch.int16).cpu().numpy().view(np.uint16)
+    bias = layer.bias_bits.view(torch.int16).cpu().numpy().view(np.uint16)
+    a = layer.lora_a.detach().cpu().numpy()
+    b = layer.lora_b.detach().cpu().numpy()
+    xh = from_dev(x.detach())
+    y_o, h_o = olora.lora_forward(xh, packed, scales, a, b, alpha=16.0, rank=8, bias_bits=bias,
+                                  compute="promoted")
+    dx_o, da_o, db_o = olora.lora_backward(gy.cpu().numpy(), xh, packed, scales, a, b, h_o,
+                                           alpha=16.0, rank=8, compute="promoted")
+    assert rel_l2(from_dev(y.detach()), y_o) < TOL
+    assert rel_l2(from_dev(x.grad), dx_o) < TOL
+    assert rel_l2(layer.lora_a.grad.cpu().numpy(), da_o) < 1e-4
+    assert rel_l2(layer.lora_b.grad.cpu().numpy(), db_o) < 1e-4
+
+
+@pytest.mark.parametrize("form", ["skinny", "skinny_one"])
+def test_skinny_slots_recover_after_expired_waits(form):
+    """Force the one-launch kernels' bounded waits to expire from the host (a
+    one-poll spin limit; every kernel still exits normally), then run more
+    calls than there are slots with the default limit: each equals the
+    result taken before, bit for bit, so no expired call left its slot
+    dirty. Expired calls are reported through the device error word."""
+
+    if form == "skinny":
+        m, k, knobs = 8, 2048, dict(skinny2=0)
+    else:
+        m, k, knobs = 2, 4096, dict(skinny2=1, skinny2_one=1)
+    n, r = 1536, 32
+    x, packed, scales, a, b, _, _ = _lora_case(m, k, n, r, 64, seed=123, bias=False)
+    b = b * 50.0
+    xd, pd = to_dev_bf16(x), to_dev(packed)
+    sd = to_dev(scales.view(np.int16)).view(torch.uint16)
+    ad, bd = to_dev_bf16(a), to_dev_bf16(b)
+
+    def call():
+        return ops.int4lora_forward(xd, pd, sd, ad, bd, scaling=1.0, group_size=64)
+
+    with ops.tuning(**knobs):
+        assert ops.check_device_errors() == 0
+        y0, h0 = call()
+        torch.cuda.synchronize()
+        y_o, h_o = olora.lora_forward(x, packed, scales, a, b, alpha=float(r), rank=r,
+                                      group_size=64)
+        assert rel_l2(from_dev(y0), y_o) < TOL
+        with ops.tuning(spin_limit=1):
+            forced = [call() for _ in range(12)]
+        torch.cuda.synchronize()
+        expired = 0
+        try:
+            ops.check_device_errors()
+        except ops.nat.DeviceError:
+            expired = 1
+        nan_calls = sum(int(torch.isnan(y.float()).any().item()) for y, _ in forced)
+        # a call whose wait expired holds NaN; one that did not equals y0
+        assert expired == (nan_calls > 0)
+        for y, h in forced:
+            if not torch.isnan(y.float()).any():
+                assert torch.equal(y, y0)
+        for _ in range(20):
+            y1, h1 = call()
+            torch.cuda.synchronize()
+            assert torch.equal(y1, y0) and torch.equal(h1, h0)
+        assert ops.check_device_errors() == 0

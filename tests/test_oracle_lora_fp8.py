@@ -107,6 +107,61 @@ def test_bf16_backward_gradients_are_bf16_values():
     assert da.dtype == np.float32 and db.dtype == np.float32
 
 
+def test_promoted_forward_brute_force_loops():
+    """No policy, bf16 activations, fp32 masters: element-by-element loops
+    with bf16 rounding of the base product only, float32 elsewhere."""
+
+    x, packed, scales, a, b, bias = _case(seed=6)
+    alpha, r = 3.0, 2
+    y, h = olora.lora_forward(x, packed, scales, a, b, alpha=alpha, rank=r, bias_bits=bias,
+                              compute="promoted")
+    assert y.dtype == np.float32 and h.dtype == np.float32
+    w = oint4.dequant_int4(packed, scales, x.shape[1])
+    c = np.float32(alpha / r)
+    m, k = x.shape
+    n = w.shape[0]
+    for i in range(m):
+        hh = [np.float32(sum(float(x[i, t]) * float(a[j, t]) for t in range(k))) for j in range(r)]
+        assert np.array_equal(np.asarray(hh, np.float32), h[i])
+        for o in range(n):
+            base = bf16_round(np.float32(sum(float(x[i, t]) * float(w[o, t]) for t in range(k))))
+            ad = np.float32(sum(float(hh[j]) * float(b[o, j]) for j in range(r)))
+            yy = np.float32(np.float32(base) + np.float32(ad * c))
+            yy = np.float32(yy + bf16_bits_to_f32(bias[o]))
+            assert yy == y[i, o]
+
+
+def test_promoted_zero_adapter_equals_bf16_base():
+    """lora_b = 0 and no bias: the float32 output holds exactly the bf16
+    base product, the same values as under the bf16 policy."""
+
+    x, packed, scales, a, _, _ = _case(seed=7)
+    zero = np.zeros((6, 2), np.float32)
+    y_p, _ = olora.lora_forward(x, packed, scales, a, zero, alpha=4.0, rank=2, compute="promoted")
+    y_b, _ = olora.lora_forward(x, packed, scales, a, zero, alpha=4.0, rank=2)
+    assert np.array_equal(y_p, y_b)
+
+
+def test_promoted_backward_matches_float64_transpose():
+    """The promoted backward against the float64 transpose (itself pinned by
+    finite differences): dA and dB to float32 accuracy, dx to bf16
+    accuracy, and dx holds bf16 values."""
+
+    m, k, n, r = 7, 16, 12, 3
+    x, packed, scales, a, b, _ = _case(m, k, n, r, seed=8)
+    gy = np.random.Generator(np.random.PCG64(10)).standard_normal((m, n)).astype(np.float32)
+    kw = dict(alpha=5.0, rank=r)
+    _, h = olora.lora_forward(x, packed, scales, a, b, compute="promoted", **kw)
+    dx, da, db = olora.lora_backward(gy, x, packed, scales, a, b, h, compute="promoted", **kw)
+    _, h64 = olora.lora_forward(x, packed, scales, a, b, compute="f64", **kw)
+    dx64, da64, db64 = olora.lora_backward(gy, x, packed, scales, a, b, h64, compute="f64", **kw)
+    assert da.dtype == np.float32 and db.dtype == np.float32
+    np.testing.assert_allclose(da, da64, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(db, db64, rtol=1e-5, atol=1e-6)
+    assert np.array_equal(bf16_round(dx), dx)
+    np.testing.assert_allclose(dx, dx64, rtol=2e-2, atol=2e-2)
+
+
 def test_scaling_is_rounded_like_a_weak_scalar():
     assert olora.lora_scaling(32.0, 16) == 2.0
     assert olora.lora_scaling(1.0, 3) == bf16_round(np.float32(1 / 3))
