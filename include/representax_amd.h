@@ -146,6 +146,23 @@ int rpx_int4lora_forward(const void* x, int dtype, int64_t m, int64_t k, const u
                          int64_t rank, float scaling, void* y, void* h, void* workspace,
                          size_t workspace_bytes, void* stream);
 
+/* rpx_int4lora_forward without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc); no counterpart in the reference. Scratch
+ * (the skinny-M kernels' split partials) comes from a static device buffer of
+ * RPX_STATIC_SCRATCH_BYTES per GPU that the library holds until the process
+ * ends; the entry point itself calls no allocator. A call that needs more
+ * scratch than that (rpx_int4lora_forward_workspace() above the limit, e.g.
+ * the generic path of a large unaligned shape) is rejected with
+ * RPX_ERR_INVALID before anything is launched. Every call on a GPU shares that
+ * GPU's buffer: calls that overlap on one GPU (different streams) race. */
+#define RPX_STATIC_SCRATCH_BYTES (16u << 20)
+int rpx_int4lora_forward_static(const void* x, int dtype, int64_t m, int64_t k,
+                                const uint8_t* packed, const uint16_t* scale_bits, int64_t n,
+                                int64_t group_size, const uint16_t* bias_bits, const void* lora_a,
+                                const void* lora_b, int64_t rank, float scaling, void* y, void* h,
+                                void* stream);
+
 size_t rpx_int4lora_backward_workspace(int64_t m, int64_t n, int64_t k, int64_t group_size,
                                        int64_t rank, int dtype);
 

@@ -56,6 +56,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _int,
         [_p, _int, _i64, _i64, _p, _p, _i64, _i64, _p, _p, _p, _i64, _f32, _p, _p, _p, _size, _p],
     ),
+    "rpx_int4lora_forward_static": (
+        _int, [_p, _int, _i64, _i64, _p, _p, _i64, _i64, _p, _p, _p, _i64, _f32, _p, _p, _p],
+    ),
     "rpx_int4lora_backward_workspace": (_size, [_i64, _i64, _i64, _i64, _i64, _int]),
     "rpx_int4lora_backward": (
         _int,

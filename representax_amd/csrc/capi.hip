@@ -523,6 +523,55 @@ int rpx_int4lora_forward(const void* x, int dtype, int64_t m, int64_t k, const u
                                ActIO{});
 }
 
+}  // extern "C"
+
+// --- static scratch for the entry point that allocates nothing ----------------
+namespace rpx {
+namespace {
+// Scratch of rpx_int4lora_forward_static: a file-scope device array, one copy
+// per GPU, kept until the process ends. Host code must not pass the array's
+// name to a kernel (on the host it is only a stand-in for the symbol); the
+// device address of this GPU's copy comes from hipGetSymbolAddress, once per
+// device, on the device's first call.
+constexpr size_t kStaticScratchBytes = RPX_STATIC_SCRATCH_BYTES;
+__device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+
+int static_scratch(void** out) {
+  int dev = 0;
+  RPX_HIP(hipGetDevice(&dev), "static scratch: current device");
+  if (dev < 0 || dev >= kMaxDevices) return fail_invalid("static scratch: device index out of range");
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    RPX_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "static scratch: symbol address");
+    g_scratch_ptr[dev].store(p, std::memory_order_release);
+  }
+  *out = p;
+  return kOk;
+}
+}  // namespace
+}  // namespace rpx
+
+extern "C" {
+
+int rpx_int4lora_forward_static(const void* x, int dtype, int64_t m, int64_t k,
+                                const uint8_t* packed, const uint16_t* scale_bits, int64_t n,
+                                int64_t group_size, const uint16_t* bias_bits, const void* lora_a,
+                                const void* lora_b, int64_t rank, float scaling, void* y, void* h,
+                                void* stream) {
+  const size_t need = rpx_int4lora_forward_workspace(m, n, k, group_size, rank, dtype);
+  if (need > kStaticScratchBytes)
+    return fail_invalid("rpx_int4lora_forward_static: the call needs " + std::to_string(need) +
+                        " bytes of scratch, more than the " +
+                        std::to_string(kStaticScratchBytes) +
+                        " of the static buffer; use rpx_int4lora_forward with a workspace");
+  void* ws = nullptr;
+  if (m > 0 && n > 0) RPX_TRY(static_scratch(&ws));
+  return int4lora_forward_impl(x, dtype, m, k, packed, scale_bits, n, group_size, bias_bits, lora_a,
+                               lora_b, rank, scaling, y, h, ws, kStaticScratchBytes, stream,
+                               ActIO{});
+}
+
 int rpx_int4lora_forward_act(const void* x, int dtype, int64_t m, int64_t k, const uint8_t* packed,
                              const uint16_t* scale_bits, int64_t n, int64_t group_size,
                              const uint16_t* bias_bits, const void* lora_a, const void* lora_b,
