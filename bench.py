@@ -330,6 +330,25 @@ def run_copyref(nbytes=256 << 20):
     print(json.dumps({"copyref_bytes_each_way": nbytes, "launches": 3}))
 
 
+def host_threads():
+    """(threads the numpy baseline uses, CPUs this process may run on, CPU
+    model): BLAS runs OMP_NUM_THREADS threads, capped by the affinity mask."""
+
+    allowed = len(os.sched_getaffinity(0))
+    omp = os.environ.get("OMP_NUM_THREADS")
+    threads = min(allowed, int(omp)) if omp and omp.isdigit() and int(omp) > 0 else allowed
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return threads, allowed, model
+
+
 def fp8_cpu_baseline(seed=1):
     """Oracle fp8 linear fwd+bwd (numpy, float32 BLAS accumulate) on a bounded
     sample: the 768->3072 linear at 1024 tokens, repeated to ~10-20 s."""
@@ -352,14 +371,88 @@ def fp8_cpu_baseline(seed=1):
         if time.perf_counter() - t0 > 10.0 or reps >= 50:
             break
     dt = (time.perf_counter() - t0) / reps
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    threads, allowed, model = host_threads()
     return {
         "value": round(flops / dt / 1e12, 5),
         "unit": "TFLOP/s",
         "cores": threads,
         "kind": "port",
         "sample": f"numpy oracle fp8 linear fwd+bwd, 768->3072 at {m} tokens, {reps} reps, "
-                  f"{dt * 1e3:.0f} ms each (fp32 BLAS accumulate)",
+                  f"{dt * 1e3:.0f} ms each (fp32 BLAS accumulate); {threads} BLAS threads of "
+                  f"{allowed} allowed CPUs, {model}",
+    }
+
+
+def int4lora_cpu_baseline(group_size=None, seed=3):
+    """Oracle INT4 + LoRA linear fwd+bwd (numpy, float32 BLAS accumulate) on
+    a bounded sample of the config: 512 of the 4096 tokens, 768->3072,
+    rank 16, alpha 32, repeated to ~10 s."""
+
+    from oracle import int4 as oint4
+    from oracle import lora as olora
+    from oracle.codecs import bf16_round
+
+    g = np.random.Generator(np.random.PCG64(seed))
+    m, k, n, r = 512, 768, 3072, 16
+    x = bf16_round(g.standard_normal((m, k)).astype(np.float32))
+    w = (g.standard_normal((n, k)) * 0.02).astype(np.float32)
+    a = (g.standard_normal((r, k)) * 0.02).astype(np.float32)
+    b = (g.standard_normal((n, r)) * 0.02).astype(np.float32)
+    gy = bf16_round(g.standard_normal((m, n)).astype(np.float32))
+    packed, scales = oint4.pack_int4(w, group_size)
+    flops = 2 * m * n * k + 2 * m * k * r + 2 * m * r * n + 2 * m * n * k + 4 * m * n * r + 4 * m * r * k
+    reps = 0
+    t0 = time.perf_counter()
+    while True:
+        _, h = olora.lora_forward(x, packed, scales, a, b, alpha=32.0, rank=r,
+                                  group_size=group_size, acc=np.float32)
+        olora.lora_backward(gy, x, packed, scales, a, b, h, alpha=32.0, rank=r,
+                            group_size=group_size, acc=np.float32)
+        reps += 1
+        if time.perf_counter() - t0 > 10.0 or reps >= 50:
+            break
+    dt = (time.perf_counter() - t0) / reps
+    threads, allowed, model = host_threads()
+    scales_kind = "per-row" if group_size is None else f"group {group_size}"
+    return {
+        "value": round(flops / dt / 1e12, 5), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+        "sample": f"numpy oracle INT4-LoRA fwd+bwd ({scales_kind} scales, dequant included), "
+                  f"768->3072 r16 at {m} of the 4096 tokens, {reps} reps, {dt * 1e3:.0f} ms each; "
+                  f"{threads} BLAS threads of {allowed} allowed CPUs, {model}",
+    }
+
+
+def skinny_cpu_baseline(seed=4):
+    """Oracle skinny-M forward (numpy, float32 BLAS accumulate, dequant
+    included) at M = 1 on the 2048->6144 projection, group 64, rank 32."""
+
+    from oracle import int4 as oint4
+    from oracle import lora as olora
+    from oracle.codecs import bf16_round
+
+    g = np.random.Generator(np.random.PCG64(seed))
+    m, k, n, r, group = 1, 2048, 6144, 32, 64
+    x = bf16_round(g.standard_normal((m, k)).astype(np.float32))
+    w = (g.standard_normal((n, k)) * 0.02).astype(np.float32)
+    a = (g.standard_normal((r, k)) * 0.02).astype(np.float32)
+    b = (g.standard_normal((n, r)) * 0.02).astype(np.float32)
+    packed, scales = oint4.pack_int4(w, group)
+    nbytes = n * k / 2 + n * (k // group) * 2 + (r * k + n * r) * 2 + m * k * 2 + m * n * 2
+    reps = 0
+    t0 = time.perf_counter()
+    while True:
+        olora.lora_forward(x, packed, scales, a, b, alpha=64.0, rank=r, group_size=group,
+                           acc=np.float32)
+        reps += 1
+        if time.perf_counter() - t0 > 10.0 or reps >= 200:
+            break
+    dt = (time.perf_counter() - t0) / reps
+    threads, allowed, model = host_threads()
+    return {
+        "value": round(nbytes / dt / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+        "us_per_call": round(dt * 1e6, 1),
+        "sample": f"numpy oracle INT4-LoRA forward (dequant included), M=1, 2048->6144, group 64, "
+                  f"r32, {reps} reps; {threads} BLAS threads of {allowed} allowed CPUs, {model}",
     }
 
 
@@ -445,11 +538,62 @@ def run_int4lora(steps, warmup, use_graph, group_size=None):
 SKINNY_SHAPES = [(2048, 6144), (6144, 2048), (2048, 2048)]
 
 
-def run_bert(steps=10, warmup=3):
+def bert_linear_rooflines(tokens=32768, group=64, rank=16, reps=10):
+    """Each distinct linear of the BERT-base step at its step size (32,768
+    tokens, group 64, rank 16): forward and backward GPU time per call inside
+    a HIP graph of `reps` calls, TFLOP/s of the algorithmic work
+    (fwd 2MNK + 2MKr + 2MrN, bwd 2MNK + 4MNr + 4MrK) and its fraction of the
+    bf16 dense peak."""
+
+    import torch
+
+    from representax_amd import ops
+
+    dev = torch.device("cuda:0")
+    g = np.random.Generator(np.random.PCG64(8))
+    x0 = bf16_tensor(g.standard_normal((tokens, 3072)).astype(np.float32), dev)
+    gy0 = bf16_tensor(g.standard_normal((tokens, 3072)).astype(np.float32), dev)
+    out = []
+    for name, k, n, count in (("q/k/v/o", 768, 768, 4), ("ffn up", 768, 3072, 1),
+                              ("ffn down", 3072, 768, 1)):
+        w = torch.from_numpy((g.standard_normal((n, k)) * 0.02).astype(np.float32)).to(dev)
+        packed, scales = ops.int4_pack(w, group)
+        a = bf16_tensor(g.standard_normal((rank, k)).astype(np.float32) * 0.02, dev)
+        b = bf16_tensor(g.standard_normal((n, rank)).astype(np.float32) * 0.02, dev)
+        x = x0[:, :k].contiguous()
+        gy = gy0[:, :n].contiguous()
+        _, h = ops.int4lora_forward(x, packed, scales, a, b, scaling=2.0, group_size=group)
+
+        def fwd():
+            ops.int4lora_forward(x, packed, scales, a, b, scaling=2.0, group_size=group)
+
+        def bwd():
+            ops.int4lora_backward(gy, x, packed, scales, a, b, h, scaling=2.0, group_size=group)
+
+        f_ms = graph_time_per_call_ms([fwd] * reps, replays=3)
+        b_ms = graph_time_per_call_ms([bwd] * reps, replays=3)
+        m = tokens
+        f_fl = 2.0 * m * n * k + 2 * m * k * rank + 2 * m * rank * n
+        b_fl = 2.0 * m * n * k + 4 * m * n * rank + 4 * m * rank * k
+        f_tf = f_fl / (f_ms * 1e-3) / 1e12
+        b_tf = b_fl / (b_ms * 1e-3) / 1e12
+        out.append({"linear": name, "per_layer": count, "k": k, "n": n,
+                    "fwd_us": round(f_ms * 1e3, 1), "fwd_tflops": round(f_tf, 1),
+                    "fwd_frac": round(f_tf / BF16_PEAK_TFLOPS, 4),
+                    "bwd_us": round(b_ms * 1e3, 1), "bwd_tflops": round(b_tf, 1),
+                    "bwd_frac": round(b_tf / BF16_PEAK_TFLOPS, 4)})
+    del x0, gy0
+    torch.cuda.empty_cache()
+    return out
+
+
+def run_bert(steps=10, warmup=3, remat="full"):
     """BERT-base encoder train step with every Q/K/V/O/FFN linear packed INT4
     (group 64) + rank-16 LoRA (alpha 32): in-batch MNR loss over 64
-    query/document pairs x 256 tokens, bf16 compute, AdamW on the fp32 LoRA
-    masters, the whole step replayed as one HIP graph."""
+    query/document pairs x 256 tokens, bf16 compute, per-layer
+    rematerialization (the reference's default, full), global-norm clipping
+    at 1.0 and the non-finite step guard, AdamW on the fp32 LoRA masters, the
+    whole step replayed as one HIP graph."""
 
     import torch
 
@@ -459,34 +603,39 @@ def run_bert(steps=10, warmup=3):
     pairs, seq = 64, 256
     model = build_int4lora_encoder(cfg, rank=16, alpha=32.0, group_size=64, seed=0,
                                    device=torch.device("cuda:0"))
-    step = MNRTrainStep(model, batch=pairs, sequence=seq)
+    step = MNRTrainStep(model, batch=pairs, sequence=seq, remat=remat)
     step.capture(warmup=2)
     ms = time_region(step, steps, warmup)
     loss = float(step.loss)
     tokens = 2 * pairs * seq
-    flops = cfg.step_flops(2 * pairs, seq)
+    flops = cfg.step_flops(2 * pairs, seq, remat=remat == "full")
+    recompute = "full per-layer rematerialization" if remat == "full" else "no recompute"
     line = {
         "workload": "BERT-base (12L, H768, 12 heads, FFN 3072, vocab 30522) train step, every "
                     "Q/K/V/O/FFN linear INT4 group-64 + LoRA r16 a32, in-batch MNR loss (scale 20), "
                     "64 query/document pairs x 256 tokens, bf16 compute, AdamW on fp32 LoRA "
-                    "masters, no recompute, HIP graph",
+                    f"masters, max grad norm 1.0, non-finite step guard, {recompute}, HIP graph",
+        "remat": remat,
         "value": round(tokens / (ms * 1e-3), 1), "unit": "tokens/s",
         "ms_per_step": round(ms, 3), "tokens_per_step": tokens,
         "matrix_tflops": round(flops / (ms * 1e-3) / 1e12, 1),
         "matrix_tflop_per_step": round(flops / 1e12, 3),
         "loss_after_timed_steps": round(loss, 4),
+        "grad_norm_last_step": round(float(step.grad_norm), 4),
     }
     del step, model
     torch.cuda.empty_cache()
     return line
 
 
-def run_qwen3(steps=6, warmup=2):
+def run_qwen3(steps=6, warmup=2, remat="full"):
     """Qwen3-VL-2B-shaped text tower train step (28 layers, hidden 2048, 16 Q /
     8 KV heads of 128, SwiGLU 6144, vocab 151936) with all seven projections
     INT4 group 64 + LoRA r32 (alpha 64): last-token-pooled MNR loss over 16
-    query/document pairs x 512 tokens, bf16 compute, AdamW on the fp32 LoRA
-    masters, one HIP graph per step."""
+    query/document pairs x 512 tokens, bf16 compute, per-layer
+    rematerialization (full, the reference's default), global-norm clipping
+    at 1.0 and the non-finite step guard, AdamW on the fp32 LoRA masters, one
+    HIP graph per step."""
 
     import torch
 
@@ -496,21 +645,25 @@ def run_qwen3(steps=6, warmup=2):
     pairs, seq = 16, 512
     model = build_int4lora_qwen3(cfg, rank=32, alpha=64.0, group_size=64, seed=0,
                                  device=torch.device("cuda:0"))
-    step = MNRTrainStep(model, batch=pairs, sequence=seq)
+    step = MNRTrainStep(model, batch=pairs, sequence=seq, remat=remat)
     step.capture(warmup=2)
     ms = time_region(step, steps, warmup)
     tokens = 2 * pairs * seq
-    flops = cfg.step_flops(2 * pairs, seq)
+    flops = cfg.step_flops(2 * pairs, seq, remat=remat == "full")
+    recompute = "full per-layer rematerialization" if remat == "full" else "no recompute"
     line = {
         "workload": "Qwen3-VL-2B-shaped text tower train step (28L, H2048, 16 Q / 8 KV heads x 128, "
                     "SwiGLU 6144, vocab 151936), all 7 projections INT4 group-64 + LoRA r32 a64, "
                     "last-token MNR loss, 16 query/document pairs x 512 tokens, bf16 compute, AdamW "
-                    "on fp32 LoRA masters, no recompute, HIP graph",
+                    f"on fp32 LoRA masters, max grad norm 1.0, non-finite step guard, {recompute}, "
+                    "HIP graph",
+        "remat": remat,
         "value": round(tokens / (ms * 1e-3), 1), "unit": "tokens/s",
         "ms_per_step": round(ms, 3), "tokens_per_step": tokens,
         "matrix_tflops": round(flops / (ms * 1e-3) / 1e12, 1),
         "matrix_tflop_per_step": round(flops / 1e12, 3),
         "loss_after_timed_steps": round(float(step.loss), 4),
+        "grad_norm_last_step": round(float(step.grad_norm), 4),
     }
     del step, model
     torch.cuda.empty_cache()
@@ -601,7 +754,9 @@ def main():
         print(json.dumps(run_skinny()))
         return
     if args.only == "bert":
-        print(json.dumps(run_bert()))
+        line = run_bert()
+        line["per_linear"] = bert_linear_rooflines()
+        print(json.dumps(line))
         return
     if args.only == "qwen3":
         print(json.dumps(run_qwen3()))
@@ -654,14 +809,22 @@ def main():
         del layers, fn
         torch.cuda.empty_cache()
         log("int4lora: per-row and group-64")
-        result["secondary"] = [delayed, run_int4lora(args.steps, args.warmup, use_graph),
-                               run_int4lora(args.steps, args.warmup, use_graph, group_size=64)]
+        i4_row = run_int4lora(args.steps, args.warmup, use_graph)
+        i4_grp = run_int4lora(args.steps, args.warmup, use_graph, group_size=64)
+        result["secondary"] = [delayed, i4_row, i4_grp]
         log("skinny-M sweep")
-        result["secondary"].append(run_skinny())
-        log("bert-base int4-lora train step")
-        result["secondary"].append(run_bert())
-        log("qwen3-shaped int4-lora train step")
-        result["secondary"].append(run_qwen3())
+        skinny = run_skinny()
+        result["secondary"].append(skinny)
+        log("bert-base int4-lora train step (full remat), per-linear rooflines, no-remat step")
+        bert = run_bert()
+        bert["per_linear"] = bert_linear_rooflines()
+        result["secondary"] += [bert, run_bert(remat="none")]
+        log("qwen3-shaped int4-lora train step (full remat), no-remat step")
+        result["secondary"] += [run_qwen3(), run_qwen3(remat="none")]
+        if not args.no_cpu_baseline:
+            log("cpu baselines of the int4-lora and skinny lines (numpy oracle)")
+            i4_row["cpu_baseline"] = int4lora_cpu_baseline()
+            skinny["cpu_baseline"] = skinny_cpu_baseline()
     if args.only is None and not args.no_cpu_baseline:
         log("cpu baseline (numpy oracle)")
         result["cpu_baseline"] = fp8_cpu_baseline()

@@ -21,6 +21,13 @@ bf16 compute with fp32 masters follows the ``bfloat16_mixed`` policy
 the reference's benchmark configuration). Attention runs as explicit batched
 products with contiguous right-hand operands in float32, and through torch's
 fused flash / memory-efficient kernels in bf16.
+
+The step follows src/representax/train/step.py:346-393: per-layer activation
+rematerialization ("full" by default, config.py:483-490, applied per layer
+as in components.py:28-43), the global gradient norm in float32, clipping to
+``max_grad_norm`` (1.0 by default, step.py:123) and a step that leaves
+parameters and optimizer state unchanged when the loss, the gradients or
+their norm are not finite (``optax.tree.where(finite, proposed, state)``).
 """
 
 from __future__ import annotations
@@ -30,12 +37,13 @@ from dataclasses import dataclass
 
 import torch
 import torch.nn.functional as F
+from torch.utils.checkpoint import checkpoint
 
 from .adapters import apply_quantized_lora, lora_parameters
 from .components import Linear
 from .config import PrecisionConfig
 from .mlp import gelu_mlp, shared_input_projections, swiglu_mlp
-from .precision import precision_context, resolve_precision_policy
+from .precision import active_policy, precision_context, resolve_precision_policy
 
 
 @dataclass(frozen=True)
@@ -85,6 +93,34 @@ class LayerNorm(torch.nn.Module):
         # rounds the normalized, affine-transformed value once
         return F.layer_norm(value, value.shape[-1:], self.weight.to(value.dtype),
                             self.bias.to(value.dtype), self.eps)
+
+
+REMAT_POLICIES = ("none", "full")
+
+
+def run_layer(layer: torch.nn.Module, remat: str, *args):
+    """One layer, rematerialized in the backward pass under ``"full"`` (the
+    reference's nothing-saveable checkpoint around each layer): only the
+    layer's inputs are kept, and its forward, INT4 + LoRA kernels included,
+    runs again before its backward."""
+
+    if remat == "full" and torch.is_grad_enabled():
+        # the recompute runs inside backward(), outside the caller's precision
+        # context: it re-enters the policy the forward saw, as jax.checkpoint
+        # replays the function traced under it
+        policy = active_policy()
+
+        def layer_under_policy(*inputs):
+            if policy is None:
+                return layer(*inputs)
+            with precision_context(policy):
+                return layer(*inputs)
+
+        return checkpoint(layer_under_policy, *args, use_reentrant=False,
+                          preserve_rng_state=False)
+    if remat not in REMAT_POLICIES:
+        raise ValueError("rematerialization must be 'none' or 'full'")
+    return layer(*args)
 
 
 class _Attention(torch.autograd.Function):
@@ -199,6 +235,7 @@ class BertEncoder(torch.nn.Module):
         self.layers = torch.nn.ModuleList(
             BertLayer(config, seed * 1000 + 10 * (i + 1), device)
             for i in range(config.num_hidden_layers))
+        self.remat = "none"
 
     def hidden_states(self, input_ids: torch.Tensor, attention_mask: torch.Tensor | None = None,
                       compute_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
@@ -213,7 +250,7 @@ class BertEncoder(torch.nn.Module):
             bias = torch.zeros(attention_mask.shape, dtype=torch.float32, device=hidden.device)
             bias = bias.masked_fill(~attention_mask.bool(), float("-inf"))[:, None, None, :]
         for layer in self.layers:
-            hidden = layer(hidden, bias)
+            hidden = run_layer(layer, self.remat, hidden, bias)
         return hidden
 
     def encode(self, input_ids: torch.Tensor, attention_mask: torch.Tensor | None = None,
@@ -398,6 +435,7 @@ class Qwen3TextEncoder(torch.nn.Module):
         self.layers = torch.nn.ModuleList(
             Qwen3Layer(config, seed * 1000 + 10 * (i + 1), device)
             for i in range(config.num_hidden_layers))
+        self.remat = "none"
         self.final_norm = RMSNorm(config.hidden_size, config.norm_epsilon, device)
         inv = 1.0 / (config.rope_theta ** (torch.arange(0, config.head_dimension, 2,
                                                         dtype=torch.float32)
@@ -416,7 +454,7 @@ class Qwen3TextEncoder(torch.nn.Module):
         hidden = self.embedding[input_ids].to(compute_dtype)
         cos, sin = self.rotary(input_ids.shape[1])
         for layer in self.layers:
-            hidden = layer(hidden, cos, sin)
+            hidden = run_layer(layer, self.remat, hidden, cos, sin)
         pooled = self.final_norm(hidden)[:, -1].float()
         return pooled / pooled.norm(dim=-1, keepdim=True).clamp_min(1e-12)
 
@@ -440,42 +478,96 @@ def build_int4lora_qwen3(config: Qwen3TextConfig, *, rank: int = 32, alpha: floa
 class MNRTrainStep:
     """One AdamW step of the MNR loss on (query, document) token batches.
 
-    ``capture()`` records forward, backward and the optimizer update into one
-    HIP graph over static input buffers; ``__call__`` replays it (or runs
-    eagerly before capture).
+    The step restates src/representax/train/step.py:346-393 for the LoRA
+    masters: gradients of the loss (with ``remat`` applied per layer), their
+    float32 global norm, clipping by ``min(1, max_grad_norm / (norm + 1e-6))``
+    (none when ``max_grad_norm`` is None), an AdamW update, and the whole
+    update discarded (parameters and optimizer state restored) unless the
+    loss, the gradient norm and hence every gradient are finite.
+
+    The masters live in one flat float32 buffer (the modules' parameters are
+    views of it, and so are their gradients), so the norm, the clip, AdamW
+    and the finite guard are a handful of kernels per step.
+    ``capture()`` records forward, backward and the update into one HIP graph
+    over static input buffers; ``__call__`` replays it (or runs eagerly
+    before capture).
     """
 
     def __init__(self, model: torch.nn.Module, *, batch: int, sequence: int, lr: float = 1e-4,
-                 scale: float = 20.0, seed: int = 6) -> None:
+                 scale: float = 20.0, seed: int = 6, remat: str = "full",
+                 max_grad_norm: float | None = 1.0) -> None:
+        if remat not in REMAT_POLICIES:
+            raise ValueError("rematerialization must be 'none' or 'full'")
+        if max_grad_norm is not None and max_grad_norm <= 0:
+            raise ValueError("max_grad_norm must be positive or None")
         self.model = model
+        model.remat = remat
+        self.remat = remat
+        self.max_grad_norm = max_grad_norm
         self.policy = resolve_precision_policy(PrecisionConfig.bfloat16_mixed())
         device = next(model.parameters()).device
         self.params = lora_parameters(model)
-        self.optimizer = torch.optim.AdamW(self.params, lr=lr, weight_decay=0.01,
-                                           capturable=True, foreach=True)
+        # flat storage: every master (and its gradient) is a view of one buffer
+        sizes = [p.numel() for p in self.params]
+        self.flat = torch.nn.Parameter(torch.cat([p.detach().reshape(-1) for p in self.params]))
+        self.flat.grad = torch.zeros_like(self.flat)
+        offset = 0
+        for p, n in zip(self.params, sizes):
+            p.data = self.flat.data[offset:offset + n].view_as(p)
+            p.grad = self.flat.grad[offset:offset + n].view_as(p)
+            offset += n
+        self.optimizer = torch.optim.AdamW([self.flat], lr=lr, weight_decay=0.01,
+                                           capturable=True, foreach=False)
+        # the state AdamW would create on its first step, made up front so
+        # that every step can snapshot it
+        self.optimizer.state[self.flat] = {
+            "step": torch.zeros((), dtype=torch.float32, device=device),
+            "exp_avg": torch.zeros_like(self.flat, memory_format=torch.preserve_format),
+            "exp_avg_sq": torch.zeros_like(self.flat, memory_format=torch.preserve_format),
+        }
         g = torch.Generator(device="cpu").manual_seed(seed)
         vocab = model.config.vocab_size
         self.query_ids = torch.randint(0, vocab, (batch, sequence), generator=g).to(device)
         self.document_ids = torch.randint(0, vocab, (batch, sequence), generator=g).to(device)
         self.scale = scale
         self.loss = torch.zeros((), dtype=torch.float32, device=device)
+        self.grad_norm = torch.zeros((), dtype=torch.float32, device=device)
+        self.finite = torch.ones((), dtype=torch.bool, device=device)
+        self._backup = None
         self.graph = None
 
+    def _state_tensors(self) -> list[torch.Tensor]:
+        st = self.optimizer.state[self.flat]
+        return [self.flat.data, st["exp_avg"], st["exp_avg_sq"], st["step"]]
+
     def _step(self) -> None:
-        self.optimizer.zero_grad(set_to_none=False)
+        self.flat.grad.zero_()
         with precision_context(self.policy):
             ids = torch.cat([self.query_ids, self.document_ids], 0)
             emb = self.model.encode(ids)
             b = self.query_ids.shape[0]
             loss = mnr_loss(emb[:b], emb[b:], self.scale)
         loss.backward()
+        grad = self.flat.grad
+        norm = torch.linalg.vector_norm(grad, dtype=torch.float32)
+        finite = torch.isfinite(loss.detach()) & torch.isfinite(norm)
+        if self.max_grad_norm is not None:
+            coef = torch.clamp(self.max_grad_norm / (norm + 1e-6), max=1.0)
+            grad.mul_(coef)
+        state = self._state_tensors()
+        if self._backup is None:
+            self._backup = [t.clone() for t in state]
+        else:
+            for dst, src in zip(self._backup, state):
+                dst.copy_(src)
         self.optimizer.step()
+        for t, old in zip(state, self._backup):
+            t.copy_(torch.where(finite, t, old))
         self.loss.copy_(loss.detach())
+        self.grad_norm.copy_(norm)
+        self.finite.copy_(finite)
 
     def capture(self, warmup: int = 2) -> None:
-        for p in self.params:
-            if p.grad is None:
-                p.grad = torch.zeros_like(p)
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):
@@ -503,7 +595,9 @@ __all__ = [
     "causal_attention",
     "LAYER_LINEARS",
     "MNRTrainStep",
+    "REMAT_POLICIES",
     "attention",
     "build_int4lora_encoder",
     "mnr_loss",
+    "run_layer",
 ]

@@ -209,3 +209,15 @@ def test_delayed_scaling_state_and_policy_on_cpu():
     assert resolve_precision_policy(cfg, fp8_state=st).fp8_state is st
     # the dynamic (reference) policy ignores a state
     assert resolve_precision_policy(PrecisionConfig.float8_mixed(), fp8_state=st).fp8_state is None
+
+
+def test_train_step_rejects_unknown_policies():
+    from representax_amd.trainstep import MNRTrainStep, run_layer
+
+    with pytest.raises(ValueError, match="rematerialization"):
+        MNRTrainStep(torch.nn.Linear(2, 2), batch=1, sequence=1, remat="selective")
+    with pytest.raises(ValueError, match="max_grad_norm"):
+        MNRTrainStep(torch.nn.Linear(2, 2), batch=1, sequence=1, max_grad_norm=0.0)
+    with torch.no_grad():
+        with pytest.raises(ValueError, match="rematerialization"):
+            run_layer(torch.nn.Identity(), "sometimes", torch.zeros(1))
