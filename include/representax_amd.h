@@ -55,8 +55,8 @@ int rpx_abi_version(void);
  * query and the call it sizes.
  *   RPX_TUNE_INT4_TILE   INT4 fused GEMM tile: 0 planner, 1 256x128, 2 128x128
  *                        (stages by scale footprint), 3 64x128, 7 256x256,
- *                        10 128x128 two stages, 11 128x128 three stages
- *                        (env RPX_GEMM_TILE)
+ *                        10 128x128 two stages, 11 128x128 three stages,
+ *                        12 256x128 two stages (env RPX_GEMM_TILE)
  *   RPX_TUNE_BF16_TILE   bf16 GEMM tile: 0 planner, 4 256x128, 5 128x128,
  *                        6 64x128, 8 256x256, 9 128x96 (env RPX_GEMM_TILE)
  *   RPX_TUNE_FP8_TILE    fp8 GEMM tile: 0 planner, 1..11 (env RPX_FP8_TILE)

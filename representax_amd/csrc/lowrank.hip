@@ -44,7 +44,7 @@ __device__ __forceinline__ u32x4_t load8(const uint16_t* p, int valid, bool alig
 // One workgroup per 16 G output rows (G row groups of 16); its four waves
 // split K in interleaved 32-deep steps and reduce in LDS. Every fragment of R
 // a wave loads serves the G row groups, so R's L2 traffic per row falls by G.
-template <int RB, int G>
+template <int RB, int G, int U>
 __global__ void __launch_bounds__(256)
     k_rank_nt(const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ R,
               int64_t ldr, int64_t M, int64_t rank, int64_t K, int round_a, float a_scale,
@@ -63,7 +63,6 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) acc[gi][rb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   // each wave keeps the loads of U steps in flight before their MFMAs
-  constexpr int U = G >= 4 ? 2 : 4;
   for (int64_t kb = static_cast<int64_t>(wave) * 32; kb < K; kb += 128 * U) {
     u32x4_t av[U][G];
     u32x4_t rv[U][RB];
@@ -123,9 +122,33 @@ __global__ void __launch_bounds__(256)
     }
 }
 
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
+
+// Operand fragment of v_mfma_f32_16x16x32_bf16 whose reduction axis is the
+// row axis of a row-major LDS tile (tokens are rows, the output index is a
+// column): lane l gets tile[m0 + 8 (l >> 4) + t][c0 + (l & 15)], t = 0..7.
+// ds_read_b64_tr_b16 hands lane i of each 16-lane group element i & 3 of the
+// 8-byte chunks that lanes 4 e + (i >> 2) address (e = 0..3), so lane j
+// addresses row m0 + 8 g + (j >> 2) (+ 4 for the second read) at columns
+// c0 + 4 (j & 3): each read yields 4 consecutive tokens of column c0 + i.
+// `pitch` (elements) and c0 are multiples of 4, keeping every address 8-byte
+// aligned.
+__device__ __forceinline__ bf16x8_t tr_frag(const uint16_t* tile, int pitch, int m0, int c0,
+                                            int lane) {
+  const int j = lane & 15;
+  const uint16_t* p = tile + (m0 + 8 * (lane >> 4) + (j >> 2)) * pitch + c0 + 4 * (j & 3);
+  const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)p);
+  const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(p + 4 * pitch));
+  typedef short i16x8_t __attribute__((ext_vector_type(8)));
+  const i16x8_t v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+  return __builtin_bit_cast(bf16x8_t, v);
+}
+
 // Token-reduction product: partials[z][p][q] = sum over the token chunk z of
 // op(X[m, p]) * Y[m, q]. Tile BP x BQ outputs, `chunk` tokens per workgroup,
-// 256 tokens per LDS step.
+// 256 tokens per LDS step; the MFMA operands come straight from the
+// token-major LDS tiles through transposing reads.
 struct RankTnArgs {
   const uint16_t* X;
   int64_t ldx;
@@ -225,20 +248,9 @@ __device__ __forceinline__ void rank_tn_body(const RankTnArgs& a, int64_t bx, in
         if (blk < NB) {
           const int bp = blk / (BQ / 16);
           const int bq = blk % (BQ / 16);
-          const int pl = bp * 16 + (lane & 15);
-          const int ql = bq * 16 + (lane & 15);
-          const int mo = st * 32 + (lane >> 4) * 8;
-          uint32_t xw[4], yw[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            xw[e] = static_cast<uint32_t>(sX[mo + 2 * e][pl]) |
-                    (static_cast<uint32_t>(sX[mo + 2 * e + 1][pl]) << 16);
-            yw[e] = static_cast<uint32_t>(sY[mo + 2 * e][ql]) |
-                    (static_cast<uint32_t>(sY[mo + 2 * e + 1][ql]) << 16);
-          }
-          acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-              as_bf16x8(u32x4_t{xw[0], xw[1], xw[2], xw[3]}),
-              as_bf16x8(u32x4_t{yw[0], yw[1], yw[2], yw[3]}), acc[b], 0, 0, 0);
+          const bf16x8_t xf = tr_frag(&sX[0][0], BP + PP, st * 32, bp * 16, lane);
+          const bf16x8_t yf = tr_frag(&sY[0][0], BQ + PP, st * 32, bq * 16, lane);
+          acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf, yf, acc[b], 0, 0, 0);
         }
       }
     }
@@ -289,15 +301,20 @@ struct ReduceArgs {
   float* out;
 };
 
+// The splits' loads of an element are issued 16 at a time before any add,
+// and summed in split order.
 __device__ __forceinline__ void reduce_one(const ReduceArgs& a, int64_t e) {
+  constexpr int kBatch = 16;
   float s = 0.0f;
-  int64_t i = 0;
-  for (; i + 4 <= a.splits; i += 4) {
-    const float x0 = a.partials[i * a.count + e], x1 = a.partials[(i + 1) * a.count + e];
-    const float x2 = a.partials[(i + 2) * a.count + e], x3 = a.partials[(i + 3) * a.count + e];
-    s = (((s + x0) + x1) + x2) + x3;
+  for (int64_t i0 = 0; i0 < a.splits; i0 += kBatch) {
+    float v[kBatch];
+#pragma unroll
+    for (int t = 0; t < kBatch; ++t)
+      v[t] = i0 + t < a.splits ? a.partials[(i0 + t) * a.count + e] : 0.0f;
+#pragma unroll
+    for (int t = 0; t < kBatch; ++t)
+      if (i0 + t < a.splits) s += v[t];
   }
-  for (; i < a.splits; ++i) s += a.partials[i * a.count + e];
   a.out[e] = round_bf16(s);
 }
 
@@ -454,23 +471,38 @@ int rank_nt_groups(int64_t m) {
   return 1;
 }
 
+template <int G, int U>
+hipError_t launch_rank_nt_gu(const uint16_t* a, int64_t lda, const uint16_t* r_mat, int64_t ldr,
+                             int64_t m, int64_t rank, int64_t k, int ra, float a_scale,
+                             uint16_t* out, int64_t ldo, hipStream_t stream) {
+  const dim3 grid(static_cast<unsigned>(ceil_div(m, 16 * G)));
+  if (rank <= 16)
+    hipLaunchKernelGGL((k_rank_nt<1, G, U>), grid, dim3(256), 0, stream, a, lda, r_mat, ldr, m,
+                       rank, k, ra, a_scale, out, ldo);
+  else if (rank <= 32)
+    hipLaunchKernelGGL((k_rank_nt<2, G, U>), grid, dim3(256), 0, stream, a, lda, r_mat, ldr, m,
+                       rank, k, ra, a_scale, out, ldo);
+  else if (rank <= 64)
+    hipLaunchKernelGGL((k_rank_nt<4, G, U>), grid, dim3(256), 0, stream, a, lda, r_mat, ldr, m,
+                       rank, k, ra, a_scale, out, ldo);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+// Steps (128 columns each, over the four waves) in flight per round: the
+// whole K range in one round when it is short and a workgroup holds one row
+// group (h = x A^T at K = 768: one memory round trip instead of two).
 template <int G>
 hipError_t launch_rank_nt_g(const uint16_t* a, int64_t lda, const uint16_t* r_mat, int64_t ldr,
                             int64_t m, int64_t rank, int64_t k, int ra, float a_scale,
                             uint16_t* out, int64_t ldo, hipStream_t stream) {
-  const dim3 grid(static_cast<unsigned>(ceil_div(m, 16 * G)));
-  if (rank <= 16)
-    hipLaunchKernelGGL((k_rank_nt<1, G>), grid, dim3(256), 0, stream, a, lda, r_mat, ldr, m, rank,
-                       k, ra, a_scale, out, ldo);
-  else if (rank <= 32)
-    hipLaunchKernelGGL((k_rank_nt<2, G>), grid, dim3(256), 0, stream, a, lda, r_mat, ldr, m, rank,
-                       k, ra, a_scale, out, ldo);
-  else if (rank <= 64)
-    hipLaunchKernelGGL((k_rank_nt<4, G>), grid, dim3(256), 0, stream, a, lda, r_mat, ldr, m, rank,
-                       k, ra, a_scale, out, ldo);
-  else
-    return hipErrorInvalidValue;
-  return hipGetLastError();
+  if constexpr (G == 1) {
+    if (ceil_div(k, 128) > 4)
+      return launch_rank_nt_gu<1, 8>(a, lda, r_mat, ldr, m, rank, k, ra, a_scale, out, ldo, stream);
+  }
+  return launch_rank_nt_gu<G, (G >= 4 ? 2 : 4)>(a, lda, r_mat, ldr, m, rank, k, ra, a_scale, out,
+                                                ldo, stream);
 }
 
 hipError_t launch_rank_nt(const uint16_t* a, int64_t lda, const uint16_t* r_mat, int64_t ldr,
