@@ -245,12 +245,42 @@ def active_model_for_compute(model: torch.nn.Module) -> torch.nn.Module:
     return model_for_compute(model, policy)
 
 
+_COMPUTE_VIEWS: ContextVar[dict[int, torch.Tensor] | None] = ContextVar(
+    "representax_amd_compute_views", default=None
+)
+
+
+@contextmanager
+def compute_views(views: dict[int, torch.Tensor] | None) -> Iterator[None]:
+    """Make precomputed compute views visible to ``compute_parameter``:
+    ``views`` maps ``id(master)`` to a tensor holding exactly
+    ``master.to(compute_dtype)`` (for instance a slice of one buffer that a
+    train step converts from all its masters at once), which then stands for
+    the per-use cast; its gradient is the cast's gradient in the compute
+    dtype. Entries of another dtype than the active policy's are ignored."""
+
+    token = _COMPUTE_VIEWS.set(views)
+    try:
+        yield
+    finally:
+        _COMPUTE_VIEWS.reset(token)
+
+
+def active_compute_views() -> dict[int, torch.Tensor] | None:
+    return _COMPUTE_VIEWS.get()
+
+
 def compute_parameter(value: torch.Tensor) -> torch.Tensor:
     """Compute view of a parameter at its use site (precision.py:111-117)."""
 
     policy = _ACTIVE_PRECISION.get()
     if policy is None:
         return value
+    views = _COMPUTE_VIEWS.get()
+    if views is not None:
+        view = views.get(id(value))
+        if view is not None and view.dtype == policy.compute_dtype:
+            return view
     return value.to(policy.compute_dtype)
 
 
@@ -323,7 +353,9 @@ __all__ = [
     "active_policy",
     "activation_inputs",
     "cast_floating_tree",
+    "active_compute_views",
     "compute_parameter",
+    "compute_views",
     "linear_matmul",
     "loss_value",
     "model_for_compute",

@@ -43,7 +43,8 @@ from .adapters import apply_quantized_lora, lora_parameters
 from .components import Linear
 from .config import PrecisionConfig
 from .mlp import gelu_mlp, shared_input_projections, swiglu_mlp
-from .precision import active_policy, precision_context, resolve_precision_policy
+from .precision import (active_compute_views, active_policy, compute_views, precision_context,
+                        resolve_precision_policy)
 
 
 @dataclass(frozen=True)
@@ -106,14 +107,15 @@ def run_layer(layer: torch.nn.Module, remat: str, *args):
 
     if remat == "full" and torch.is_grad_enabled():
         # the recompute runs inside backward(), outside the caller's precision
-        # context: it re-enters the policy the forward saw, as jax.checkpoint
-        # replays the function traced under it
+        # context: it re-enters the policy (and compute views) the forward
+        # saw, as jax.checkpoint replays the function traced under them
         policy = active_policy()
+        views = active_compute_views()
 
         def layer_under_policy(*inputs):
             if policy is None:
                 return layer(*inputs)
-            with precision_context(policy):
+            with precision_context(policy), compute_views(views):
                 return layer(*inputs)
 
         return checkpoint(layer_under_policy, *args, use_reentrant=False,
@@ -487,7 +489,12 @@ class MNRTrainStep:
 
     The masters live in one flat float32 buffer (the modules' parameters are
     views of it, and so are their gradients), so the norm, the clip, AdamW
-    and the finite guard are a handful of kernels per step.
+    and the finite guard are a handful of kernels per step. Their bf16
+    compute views (``compute_parameter``) are slices of one bf16 buffer
+    converted from the masters once per step, each a leaf whose gradient
+    accumulates into one bf16 gradient buffer that becomes the masters'
+    float32 gradient (the transpose of the cast): three kernels per step
+    instead of a cast per parameter use and per gradient.
     ``capture()`` records forward, backward and the update into one HIP graph
     over static input buffers; ``__call__`` replays it (or runs eagerly
     before capture).
@@ -511,10 +518,16 @@ class MNRTrainStep:
         sizes = [p.numel() for p in self.params]
         self.flat = torch.nn.Parameter(torch.cat([p.detach().reshape(-1) for p in self.params]))
         self.flat.grad = torch.zeros_like(self.flat)
+        self.flat_c = torch.zeros(self.flat.numel(), dtype=torch.bfloat16, device=device)
+        self.flat_gc = torch.zeros_like(self.flat_c)
+        self.views: dict[int, torch.Tensor] = {}
         offset = 0
         for p, n in zip(self.params, sizes):
             p.data = self.flat.data[offset:offset + n].view_as(p)
             p.grad = self.flat.grad[offset:offset + n].view_as(p)
+            view = self.flat_c[offset:offset + n].view_as(p).detach().requires_grad_(True)
+            view.grad = self.flat_gc[offset:offset + n].view_as(p)
+            self.views[id(p)] = view
             offset += n
         self.optimizer = torch.optim.AdamW([self.flat], lr=lr, weight_decay=0.01,
                                            capturable=True, foreach=False)
@@ -541,14 +554,17 @@ class MNRTrainStep:
         return [self.flat.data, st["exp_avg"], st["exp_avg_sq"], st["step"]]
 
     def _step(self) -> None:
-        self.flat.grad.zero_()
-        with precision_context(self.policy):
+        self.flat_gc.zero_()
+        with torch.no_grad():
+            self.flat_c.copy_(self.flat)
+        with precision_context(self.policy), compute_views(self.views):
             ids = torch.cat([self.query_ids, self.document_ids], 0)
             emb = self.model.encode(ids)
             b = self.query_ids.shape[0]
             loss = mnr_loss(emb[:b], emb[b:], self.scale)
         loss.backward()
         grad = self.flat.grad
+        grad.copy_(self.flat_gc)
         norm = torch.linalg.vector_norm(grad, dtype=torch.float32)
         finite = torch.isfinite(loss.detach()) & torch.isfinite(norm)
         if self.max_grad_norm is not None:
