@@ -50,10 +50,12 @@ def parse_args():
     p.add_argument("--no-secondary", action="store_true")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--only", choices=["fp8", "fp8delayed", "int4lora", "skinny", "bert", "qwen3",
-                                      "fp8gemm", "copyref"], default=None,
+                                      "fp8gemm", "copyref", "int4shapes"], default=None,
                    help="run one workload and nothing else (profiling); fp8gemm: three eager "
                         "launches of each fp8 GEMM call of one step; copyref: a plain 256 MiB "
-                        "device copy, the reference for scaling FETCH_SIZE / WRITE_SIZE")
+                        "device copy, the reference for scaling FETCH_SIZE / WRITE_SIZE; "
+                        "int4shapes: three eager INT4 + LoRA forwards and backwards at each "
+                        "train-step linear shape (counter passes see eager launches only)")
     return p.parse_args()
 
 
@@ -317,6 +319,39 @@ def run_fp8gemm_only(layers):
         for _ in range(3):
             fn()
     torch.cuda.synchronize()
+
+
+INT4_STEP_SHAPES = [("bert q/k/v/o", 32768, 768, 768, 16), ("bert ffn up", 32768, 768, 3072, 16),
+                    ("bert ffn down", 32768, 3072, 768, 16), ("qwen3 q/o", 16384, 2048, 2048, 32),
+                    ("qwen3 gate/up", 16384, 2048, 6144, 32), ("qwen3 down", 16384, 6144, 2048, 32)]
+
+
+def run_int4_shapes(reps=3, group=64):
+    """Eager INT4 + LoRA forward and backward calls at every linear shape of
+    the BERT-base and Qwen3-2B-shaped steps (group 64), for counter passes."""
+
+    import torch
+
+    from representax_amd import ops
+
+    dev = torch.device("cuda:0")
+    g = np.random.Generator(np.random.PCG64(9))
+    out = []
+    for name, m, k, n, r in INT4_STEP_SHAPES:
+        x = bf16_tensor(g.standard_normal((m, k)).astype(np.float32), dev)
+        gy = bf16_tensor(g.standard_normal((m, n)).astype(np.float32), dev)
+        w = torch.from_numpy((g.standard_normal((n, k)) * 0.02).astype(np.float32)).to(dev)
+        packed, scales = ops.int4_pack(w, group)
+        a = bf16_tensor(g.standard_normal((r, k)).astype(np.float32) * 0.02, dev)
+        b = bf16_tensor(g.standard_normal((n, r)).astype(np.float32) * 0.02, dev)
+        for _ in range(reps):
+            _, h = ops.int4lora_forward(x, packed, scales, a, b, scaling=2.0, group_size=group)
+            ops.int4lora_backward(gy, x, packed, scales, a, b, h, scaling=2.0, group_size=group)
+        torch.cuda.synchronize()
+        out.append(name)
+        del x, gy, w
+        torch.cuda.empty_cache()
+    print(json.dumps({"int4_shapes": out, "reps": reps}))
 
 
 def run_copyref(nbytes=256 << 20):
@@ -763,6 +798,9 @@ def main():
         return
     if args.only == "copyref":
         run_copyref()
+        return
+    if args.only == "int4shapes":
+        run_int4_shapes()
         return
     if args.only == "fp8gemm":
         run_fp8gemm_only(fp8_setup(args.tokens, dev))

@@ -69,6 +69,9 @@ int rpx_abi_version(void);
  *                        0 two launches, 1 one launch (env RPX_SKINNY2_ONE)
  *   RPX_TUNE_SPIN_LIMIT  polls of the skinny kernels' bounded cross-block
  *                        waits (0: the default limit)
+ *   RPX_TUNE_GEMM_BAND   row-blocks per band of the bf16 / INT4 GEMMs' tile
+ *                        order: 0 planner, 1 (row-major) .. 64
+ *                        (env RPX_GEMM_BAND)
  * ------------------------------------------------------------------------- */
 #define RPX_TUNE_INT4_TILE 0
 #define RPX_TUNE_BF16_TILE 1
@@ -77,6 +80,7 @@ int rpx_abi_version(void);
 #define RPX_TUNE_SKINNY2 4
 #define RPX_TUNE_SKINNY2_ONE 5
 #define RPX_TUNE_SPIN_LIMIT 6
+#define RPX_TUNE_GEMM_BAND 7
 
 /* RPX_ERR_INVALID for an unknown knob or value. */
 int rpx_set_tuning(int knob, int value);

@@ -212,6 +212,7 @@ bool knob_value_ok(int knob, int v) {
     case kTuneSkinny2:
     case kTuneSkinny2One: return v >= -1 && v <= 1;
     case kTuneSpinLimit: return v >= 0;
+    case kTuneBand: return v >= 0 && v <= 64;
     default: return false;
   }
 }
@@ -224,7 +225,7 @@ int env_int(const char* name, int fallback) {
 struct Knobs {
   std::atomic<int> v[kTuneCount];
   Knobs() {
-    const int defaults[kTuneCount] = {0, 0, 0, 0, -1, -1, 0};
+    const int defaults[kTuneCount] = {0, 0, 0, 0, -1, -1, 0, 0};
     for (int i = 0; i < kTuneCount; ++i) v[i].store(defaults[i], std::memory_order_relaxed);
     // RPX_GEMM_TILE names a tile of either GEMM (the id sets are disjoint)
     const int gemm = env_int("RPX_GEMM_TILE", 0);
@@ -233,7 +234,8 @@ struct Knobs {
     const std::pair<int, const char*> envs[] = {{kTuneFp8Tile, "RPX_FP8_TILE"},
                                                 {kTuneSkinnyTile, "RPX_SKINNY_TILE"},
                                                 {kTuneSkinny2, "RPX_SKINNY2"},
-                                                {kTuneSkinny2One, "RPX_SKINNY2_ONE"}};
+                                                {kTuneSkinny2One, "RPX_SKINNY2_ONE"},
+                                                {kTuneBand, "RPX_GEMM_BAND"}};
     for (const auto& e : envs) {
       const int val = env_int(e.second, v[e.first].load());
       if (knob_value_ok(e.first, val)) v[e.first].store(val);

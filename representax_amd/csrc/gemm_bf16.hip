@@ -90,7 +90,7 @@ __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_
     k_gemm_nt(const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ B,
               int64_t ldb, Int4Operand w, int group_shift, int64_t M, int64_t N, int64_t K,
               uint16_t* __restrict__ out, int64_t ldc, LowRankEpilogue epi, int tiles_m,
-              int tiles_n) {
+              int tiles_n, int band) {
   constexpr int NW = WM * WN;
   constexpr int NT = 64 * NW;
   constexpr int TM = BM / WM;
@@ -113,9 +113,11 @@ __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave % WM;
   const int wn = wave / WM;
-  const int tile = xcd_block(blockIdx.x, static_cast<int>(gridDim.x));
-  const int64_t m0 = static_cast<int64_t>(tile / tiles_n) * BM;
-  const int64_t n0 = static_cast<int64_t>(tile % tiles_n) * BN;
+  int tile_m, tile_n;
+  band_tile(xcd_block(blockIdx.x, static_cast<int>(gridDim.x)), tiles_m, tiles_n, band, tile_m,
+            tile_n);
+  const int64_t m0 = static_cast<int64_t>(tile_m) * BM;
+  const int64_t n0 = static_cast<int64_t>(tile_n) * BN;
   const int nk = static_cast<int>(K / kBK);
   const int half = lane >> 5;
   const int frow = lane & 31;
@@ -679,6 +681,17 @@ constexpr int gemm_lds_bytes(int bm, int bn, int ns, bool int4) {
   return ns * (bm * 128 + bn * (int4 ? 32 : 128));
 }
 
+// Rows per band of the banded tile order: the tuning knob's value, else 1
+// (row-major). Row-major order makes each XCD re-read B once per A
+// row-block (1.8 GB of L2 misses for the 16384 x 6144 x 2048 input-gradient
+// GEMM against 92 MB of operands), yet bands of 2-16 measured within
+// run-to-run noise of it on every train-step shape: the re-reads presumably
+// hit the 256 MB Infinity Cache, which holds these operands.
+int tile_band(int tiles_m) {
+  const int band = tune(kTuneBand) > 0 ? tune(kTuneBand) : 1;
+  return band < tiles_m ? band : (tiles_m > 0 ? tiles_m : 1);
+}
+
 template <int BM, int BN, int WM, int WN, int NS, int WPE, bool INT4, int JB, int ACT>
 hipError_t run_gemm_act(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb,
                         const Int4Operand& w, int64_t m, int64_t n, int64_t k, uint16_t* out,
@@ -696,9 +709,10 @@ hipError_t run_gemm_act(const uint16_t* a, int64_t lda, const uint16_t* b, int64
   if (INT4 && w.n_groups > 1) {
     while ((int64_t{1} << group_shift) < w.group) ++group_shift;
   }
+  const int band = tile_band(tiles_m);
   hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(tiles_m) * tiles_n), dim3(64 * WM * WN),
                      lds, stream, a, lda, b, ldb, w, group_shift, m, n, k, out, ldc, epi, tiles_m,
-                     tiles_n);
+                     tiles_n, band);
   return hipGetLastError();
 }
 

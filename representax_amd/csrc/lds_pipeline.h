@@ -43,4 +43,19 @@ __device__ __forceinline__ int xcd_block(int block, int total) {
   return total % 8 == 0 ? (block % 8) * (total / 8) + block / 8 : block;
 }
 
+// Position (tm, tn) of tile t in banded order: bands of `band` row-blocks,
+// each walked column by column with the band's rows fastest. The tiles an
+// XCD runs at once then share `band` A row-blocks and about
+// (tiles in flight) / band B column-blocks, instead of one A row-block and
+// every B column-block (band 1 is plain row-major order). A bijection of
+// [0, tiles_m * tiles_n) for every band >= 1.
+__device__ __forceinline__ void band_tile(int t, int tiles_m, int tiles_n, int band, int& tm,
+                                          int& tn) {
+  const int first = (t / (band * tiles_n)) * band;
+  const int rows = tiles_m - first < band ? tiles_m - first : band;
+  const int w = t - first * tiles_n;
+  tm = first + w % rows;
+  tn = w / rows;
+}
+
 }  // namespace rpx

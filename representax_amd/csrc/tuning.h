@@ -19,7 +19,8 @@ enum TuneKnob : int {
   kTuneSkinny2 = 4,     // two-launch skinny: -1 planner, 0 never, 1 for M <= 16   RPX_SKINNY2
   kTuneSkinny2One = 5,  // M <= 4 form: -1 planner, 0 two launches, 1 one launch  RPX_SKINNY2_ONE
   kTuneSpinLimit = 6,   // polls of the skinny kernels' bounded waits (0: default)
-  kTuneCount = 7
+  kTuneBand = 7,        // row-blocks per band of the GEMM tile order (0: planner)  RPX_GEMM_BAND
+  kTuneCount = 8
 };
 
 // Current value of a knob.

@@ -93,6 +93,7 @@ TUNING_KNOBS = {
     "skinny2": nat.TUNE_SKINNY2,
     "skinny2_one": nat.TUNE_SKINNY2_ONE,
     "spin_limit": nat.TUNE_SPIN_LIMIT,
+    "gemm_band": nat.TUNE_GEMM_BAND,
 }
 
 

@@ -176,6 +176,60 @@ def test_bf16_dx_every_tile(activation, m, k, n, r, group):
                 assert torch.equal(dgate, first[2]), (tile, first[0])
 
 
+# Row-blocks per band of the tile order, forced: powers of two, bands that do
+# not divide the tile rows (3, 5: a short last band) and one wider than the
+# grid (64: clamped to the tile rows)
+BANDS = [1, 2, 3, 5, 64]
+
+
+@pytest.mark.parametrize("tile", [3, 10, 1])
+def test_int4_forward_every_band(tile):
+    """The tile order only moves tiles between workgroups: every band gives
+    the same bits, and those match the oracle."""
+
+    m, k, n, r, group = 1100, 512, 704, 16, 64
+    g = rng(4000 + tile)
+    p = _params(g, n, k, r, group, bias=True)
+    d = _dev(p)
+    x = bf16_values(g.standard_normal((m, k)))
+    xd = to_dev_bf16(x)
+    z_o, h_o = olora.lora_forward(x, p["packed"], p["scales"], p["a"], p["b"], alpha=p["alpha"],
+                                  rank=r, bias_bits=p["bias"], group_size=group)
+    results = {}
+    for band in BANDS:
+        with ops.tuning(int4_tile=tile, gemm_band=band):
+            results[band] = _forward(d, xd, "none", None)
+    torch.cuda.synchronize()
+    assert_bf16_close(from_dev(results[1][0]), z_o, what=f"tile {tile} band 1 y")
+    assert_bf16_close(from_dev(results[1][2]), h_o, what=f"tile {tile} band 1 h")
+    for band, (y, _, _) in results.items():
+        assert torch.equal(y, results[1][0]), (tile, band)
+
+
+@pytest.mark.parametrize("tile", [6, 5, 4])
+def test_bf16_dx_every_band(tile):
+    m, k, n, r, group = 1100, 704, 512, 16, 64
+    g = rng(4100 + tile)
+    p = _params(g, n, k, r, group, bias=False)
+    d = _dev(p)
+    x = bf16_values(g.standard_normal((m, k)))
+    gy = bf16_values(g.standard_normal((m, n)))
+    xd, gyd = to_dev_bf16(x), to_dev_bf16(gy)
+    _, h = ops.int4lora_forward(xd, d["packed"], d["scales"], d["a"], d["b"],
+                                scaling=d["scaling"], group_size=group)
+    torch.cuda.synchronize()
+    dx_o, _, _ = olora.lora_backward(gy, x, p["packed"], p["scales"], p["a"], p["b"], from_dev(h),
+                                     alpha=p["alpha"], rank=r, group_size=group)
+    results = {}
+    for band in BANDS:
+        with ops.tuning(bf16_tile=tile, gemm_band=band):
+            results[band] = _backward(d, gyd, xd, h, "none", None, None)[0]
+    torch.cuda.synchronize()
+    assert_bf16_close(from_dev(results[1]), dx_o, what=f"tile {tile} band 1 dx")
+    for band, dx in results.items():
+        assert torch.equal(dx, results[1]), (tile, band)
+
+
 # Full-size linears of the two train steps: (m, k, n, r, group, activation)
 FULL = [
     # BERT-base, 64 x 256 tokens: Q/K/V/O, FFN up (with GELU), FFN down
