@@ -38,9 +38,15 @@ __device__ __forceinline__ u32x4_t lds_chunk(const uint8_t* base, int row, int c
 }
 
 // Row-major tiles (n fastest) dealt to the 8 XCDs, which take workgroups
-// round-robin, in contiguous ranges so each XCD's L2 keeps a few A row-blocks.
+// round-robin (block b runs on XCD b % 8), in contiguous ranges so each
+// XCD's L2 keeps a few A row-blocks: XCD x, which gets q = total / 8 blocks
+// plus one more when x < total % 8, takes the tiles from
+// x q + min(x, total % 8) on. A bijection of [0, total).
 __device__ __forceinline__ int xcd_block(int block, int total) {
-  return total % 8 == 0 ? (block % 8) * (total / 8) + block / 8 : block;
+  const int q = total / 8;
+  const int r = total % 8;
+  const int x = block % 8;
+  return x * q + (x < r ? x : r) + block / 8;
 }
 
 // Position (tm, tn) of tile t in banded order: bands of `band` row-blocks,
