@@ -50,12 +50,13 @@ def parse_args():
     p.add_argument("--no-secondary", action="store_true")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--only", choices=["fp8", "fp8delayed", "int4lora", "skinny", "bert", "qwen3",
-                                      "fp8gemm", "copyref", "int4shapes"], default=None,
+                                      "fp8gemm", "copyref", "int4shapes", "vendor"], default=None,
                    help="run one workload and nothing else (profiling); fp8gemm: three eager "
                         "launches of each fp8 GEMM call of one step; copyref: a plain 256 MiB "
                         "device copy, the reference for scaling FETCH_SIZE / WRITE_SIZE; "
                         "int4shapes: three eager INT4 + LoRA forwards and backwards at each "
-                        "train-step linear shape (counter passes see eager launches only)")
+                        "train-step linear shape (counter passes see eager launches only); "
+                        "vendor: the fp8 GEMM calls and INT4 forwards next to hipBLASLt")
     return p.parse_args()
 
 
@@ -352,6 +353,57 @@ def run_int4_shapes(reps=3, group=64):
         del x, gy, w
         torch.cuda.empty_cache()
     print(json.dumps({"int4_shapes": out, "reps": reps}))
+
+
+def run_vendor(layers):
+    """The platform library on the same products, for comparison: every fp8
+    GEMM call of the BERT-base step against torch._scaled_mm (hipBLASLt,
+    e4m3 x e4m3 with scalar scales, bf16 out), and the INT4 + LoRA forward at
+    the train-step linear shapes against a plain bf16 torch.matmul (hipBLASLt)
+    of the same M, K, N without the adapter. GPU time per call inside a HIP
+    graph of 16 calls, as for the roofline."""
+
+    import torch
+
+    from representax_amd import ops
+
+    dev = torch.device("cuda:0")
+    names = []
+    for nm, k, n in BERT_LINEARS:
+        names += [(f"{nm} fwd", 8192, n, k), (f"{nm} dX", 8192, k, n), (f"{nm} dW", n, k, 8192)]
+    fp8 = []
+    for (fn, _), (nm, m, n, k) in zip(fp8_gemm_calls(layers), names):
+        ours = graph_time_per_call_ms([fn] * 16, replays=3) * 1e3
+        a = torch.randn(m, k, device=dev).to(torch.float8_e4m3fn)
+        b = torch.randn(n, k, device=dev).to(torch.float8_e4m3fn)
+        one = torch.tensor(1.0, device=dev)
+        lib = graph_time_per_call_ms(
+            [lambda: torch._scaled_mm(a, b.t(), scale_a=one, scale_b=one, out_dtype=torch.bfloat16)]
+            * 16, replays=3) * 1e3
+        fp8.append({"call": nm, "m": m, "n": n, "k": k, "ours_us": round(ours, 2),
+                    "hipblaslt_us": round(lib, 2)})
+        del a, b
+    g = np.random.Generator(np.random.PCG64(3))
+    int4 = []
+    for name, m, k, n, r in INT4_STEP_SHAPES:
+        x = bf16_tensor(g.standard_normal((m, k)).astype(np.float32), dev)
+        w = torch.from_numpy((g.standard_normal((n, k)) * 0.02).astype(np.float32)).to(dev)
+        packed, scales = ops.int4_pack(w, 64)
+        a = bf16_tensor(g.standard_normal((r, k)).astype(np.float32) * 0.02, dev)
+        b = bf16_tensor(g.standard_normal((n, r)).astype(np.float32) * 0.02, dev)
+        wt = w.to(torch.bfloat16).t().contiguous()
+        ours = graph_time_per_call_ms(
+            [lambda: ops.int4lora_forward(x, packed, scales, a, b, scaling=2.0, group_size=64)] * 16,
+            replays=3) * 1e3
+        lib = graph_time_per_call_ms([lambda: torch.matmul(x, wt)] * 16, replays=3) * 1e3
+        int4.append({"linear": name, "m": m, "k": k, "n": n, "rank": r,
+                     "int4lora_fwd_us": round(ours, 2), "bf16_matmul_us": round(lib, 2)})
+        del x, w, packed, scales, a, b, wt
+        torch.cuda.empty_cache()
+    print(json.dumps({"fp8_gemm_calls": fp8,
+                      "fp8_total_us": {"ours": round(sum(c["ours_us"] for c in fp8), 1),
+                                       "hipblaslt": round(sum(c["hipblaslt_us"] for c in fp8), 1)},
+                      "int4lora_forward_vs_bf16": int4}))
 
 
 def run_copyref(nbytes=256 << 20):
@@ -801,6 +853,9 @@ def main():
         return
     if args.only == "int4shapes":
         run_int4_shapes()
+        return
+    if args.only == "vendor":
+        run_vendor(fp8_setup(args.tokens, dev))
         return
     if args.only == "fp8gemm":
         run_fp8gemm_only(fp8_setup(args.tokens, dev))

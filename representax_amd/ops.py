@@ -18,12 +18,27 @@ BF16 = torch.bfloat16
 F32 = torch.float32
 
 
-def _ptr(t: torch.Tensor | None) -> ctypes.c_void_p | None:
-    return None if t is None else ctypes.c_void_p(t.data_ptr())
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
 
 
-def _stream(device: torch.device) -> ctypes.c_void_p:
-    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+# torch's current-stream handle without building a Stream object (a few
+# microseconds per call on the small-M path, where the kernels take ~10)
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def _device_index(device: torch.device) -> int:
+    return device.index if device.index is not None else torch.cuda.current_device()
+
+
+def _raw_stream(device: torch.device) -> int:
+    if _RAW_STREAM is not None:
+        return int(_RAW_STREAM(_device_index(device)))
+    return int(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _stream(device: torch.device) -> int:
+    return _raw_stream(device)
 
 
 def _dtype_code(dtype: torch.dtype) -> int:
@@ -54,8 +69,31 @@ def _on_device(*tensors: torch.Tensor | None) -> torch.device:
     return device
 
 
+# One scratch buffer per (device, stream), grown on demand. A stream runs its
+# calls one after another, so consecutive calls may share it; calls on other
+# streams get their own. Calls made under graph capture get a buffer of their
+# own from the graph's memory pool, since a graph keeps its buffer for every
+# replay.
+_WORKSPACES: dict[tuple[int, int], torch.Tensor] = {}
+
+
 def _workspace(nbytes: int, device: torch.device) -> torch.Tensor:
-    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+    nbytes = max(int(nbytes), 1)
+    if torch.cuda.is_current_stream_capturing():
+        return torch.empty(nbytes, dtype=torch.uint8, device=device)
+    index = _device_index(device)
+    key = (index, _raw_stream(device))
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=torch.device("cuda", index))
+        _WORKSPACES[key] = ws
+    return ws
+
+
+def release_workspaces() -> None:
+    """Drop the cached per-stream scratch buffers (back to torch's allocator)."""
+
+    _WORKSPACES.clear()
 
 
 def _aligned(t: torch.Tensor | None) -> torch.Tensor | None:
@@ -66,6 +104,10 @@ def _aligned(t: torch.Tensor | None) -> torch.Tensor | None:
         return None
     t = t.contiguous()
     return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
+def _as(t: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    return t if t.dtype == dtype else t.to(dtype)
 
 
 def _u16(t: torch.Tensor) -> torch.Tensor:
@@ -213,8 +255,8 @@ def int4lora_forward(x2d, packed, scale_bits, lora_a_c, lora_b_c, *, scaling: fl
     dt = x2d.dtype
     code = _dtype_code(dt)
     x2d = _aligned(x2d)
-    a = _aligned(lora_a_c.to(dt))
-    b = _aligned(lora_b_c.to(dt))
+    a = _aligned(_as(lora_a_c, dt))
+    b = _aligned(_as(lora_b_c, dt))
     y = torch.empty((m, n), dtype=dt, device=device)
     h = torch.empty((m, r), dtype=dt, device=device)
     g = group_arg(group_size, k)
@@ -238,8 +280,8 @@ def int4lora_backward(grad, x2d, packed, scale_bits, lora_a_c, lora_b_c, h, *, s
     dt = x2d.dtype
     code = _dtype_code(dt)
     grad = _aligned(grad.to(dt))
-    a = _aligned(lora_a_c.to(dt))
-    b = _aligned(lora_b_c.to(dt))
+    a = _aligned(_as(lora_a_c, dt))
+    b = _aligned(_as(lora_b_c, dt))
     dx = torch.empty((m, k), dtype=dt, device=device)
     d_a = torch.empty((r, k), dtype=F32, device=device)
     d_b = torch.empty((n, r), dtype=F32, device=device)
@@ -271,8 +313,8 @@ def int4lora_forward_act(x2d, packed, scale_bits, lora_a_c, lora_b_c, *, activat
     dt = x2d.dtype
     code = _dtype_code(dt)
     x2d = _aligned(x2d)
-    a = _aligned(lora_a_c.to(dt))
-    b = _aligned(lora_b_c.to(dt))
+    a = _aligned(_as(lora_a_c, dt))
+    b = _aligned(_as(lora_b_c, dt))
     gate = None if gate is None else _aligned(gate.to(dt))
     y = torch.empty((m, n), dtype=dt, device=device)
     z = torch.empty((m, n), dtype=dt, device=device)
@@ -304,8 +346,8 @@ def int4lora_backward_act(grad, x2d, packed, scale_bits, lora_a_c, lora_b_c, h, 
     dt = x2d.dtype
     code = _dtype_code(dt)
     grad = _aligned(grad.to(dt))
-    a = _aligned(lora_a_c.to(dt))
-    b = _aligned(lora_b_c.to(dt))
+    a = _aligned(_as(lora_a_c, dt))
+    b = _aligned(_as(lora_b_c, dt))
     z = _aligned(z.to(dt))
     gate = None if gate is None else _aligned(gate.to(dt))
     dz = torch.empty((m, k), dtype=dt, device=device)
