@@ -50,13 +50,15 @@ def parse_args():
     p.add_argument("--no-secondary", action="store_true")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--only", choices=["fp8", "fp8delayed", "int4lora", "skinny", "bert", "qwen3",
-                                      "fp8gemm", "copyref", "int4shapes", "vendor"], default=None,
+                                      "fp8gemm", "copyref", "int4shapes", "vendor", "castref"],
+                   default=None,
                    help="run one workload and nothing else (profiling); fp8gemm: three eager "
                         "launches of each fp8 GEMM call of one step; copyref: a plain 256 MiB "
                         "device copy, the reference for scaling FETCH_SIZE / WRITE_SIZE; "
                         "int4shapes: three eager INT4 + LoRA forwards and backwards at each "
                         "train-step linear shape (counter passes see eager launches only); "
-                        "vendor: the fp8 GEMM calls and INT4 forwards next to hipBLASLt")
+                        "vendor: the fp8 GEMM calls and INT4 forwards next to hipBLASLt; castref: the "
+                        "activation casts next to a plain copy of the same bytes")
     return p.parse_args()
 
 
@@ -404,6 +406,30 @@ def run_vendor(layers):
                       "fp8_total_us": {"ours": round(sum(c["ours_us"] for c in fp8), 1),
                                        "hipblaslt": round(sum(c["hipblaslt_us"] for c in fp8), 1)},
                       "int4lora_forward_vs_bf16": int4}))
+
+
+def run_castref(layers, reps=16):
+    """The dynamic cast of each distinct BERT-base activation shape (8192 x 768
+    and 8192 x 3072 bf16 -> e4m3 codes in both layouts, the scale given)
+    against a plain device copy that moves the same bytes (a bf16 tensor of
+    the same shape: 2 bytes read and 2 written per element, as the cast
+    reads 2 and writes 1 + 1). GPU time per call in a HIP graph of `reps`."""
+
+    import torch
+
+    from representax_amd import ops
+
+    out = []
+    for name, x, _, _, k, _ in (layers[0], layers[5]):
+        s = ops.fp8_scale(x, "e4m3fn")
+        cast = graph_time_per_call_ms(
+            [lambda: ops.fp8_cast(x, s, "e4m3fn", rowmajor=True, transposed=True)] * reps,
+            replays=3) * 1e3
+        dst = torch.empty_like(x)
+        copy = graph_time_per_call_ms([lambda: dst.copy_(x)] * reps, replays=3) * 1e3
+        out.append({"tensor": f"{x.shape[0]} x {k} bf16", "cast_both_layouts_us": round(cast, 2),
+                    "copy_same_bytes_us": round(copy, 2), "ratio": round(cast / copy, 3)})
+    print(json.dumps({"castref": out}))
 
 
 def run_copyref(nbytes=256 << 20):
@@ -853,6 +879,9 @@ def main():
         return
     if args.only == "int4shapes":
         run_int4_shapes()
+        return
+    if args.only == "castref":
+        run_castref(fp8_setup(args.tokens, dev))
         return
     if args.only == "vendor":
         run_vendor(fp8_setup(args.tokens, dev))

@@ -69,8 +69,8 @@ int rpx_abi_version(void);
  *                        0 two launches, 1 one launch (env RPX_SKINNY2_ONE)
  *   RPX_TUNE_SPIN_LIMIT  polls of the skinny kernels' bounded cross-block
  *                        waits (0: the default limit)
- *   RPX_TUNE_GEMM_BAND   row-blocks per band of the bf16 / INT4 GEMMs' tile
- *                        order: 0 planner, 1 (row-major) .. 64
+ *   RPX_TUNE_GEMM_BAND   row-blocks per band of the bf16, INT4 and fp8 GEMMs'
+ *                        tile order: 0 planner, 1 (row-major) .. 64
  *                        (env RPX_GEMM_BAND)
  * ------------------------------------------------------------------------- */
 #define RPX_TUNE_INT4_TILE 0

@@ -63,7 +63,7 @@ __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_
     k_fp8_gemm(const uint8_t* __restrict__ A, const uint8_t* __restrict__ B, int64_t M, int64_t N,
                int64_t K, int64_t k_per_split, const float* __restrict__ s_a,
                const float* __restrict__ s_b, void* __restrict__ out, int out_dtype, int64_t ldc,
-               float* __restrict__ partials, int tiles_m, int tiles_n) {
+               float* __restrict__ partials, int tiles_m, int tiles_n, int band) {
   constexpr int NW = WM * WN;
   constexpr int TM = BM / WM;
   constexpr int TN = BN / WN;
@@ -88,14 +88,18 @@ __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_
   const int wm = wave % WM;
   const int wn = wave / WM;
 
-  // Tiles (n fastest) are dealt to the 8 XCDs in contiguous ranges so each
-  // XCD's L2 holds a few A row-blocks; split-K slices are outermost.
+  // Tiles are dealt to the 8 XCDs in contiguous ranges of a banded order
+  // (bands of `band` row-blocks walked column by column), so the tiles an
+  // XCD holds share few A row-blocks and B column-blocks in its L2; split-K
+  // slices are outermost. Partial tiles are stored by the row-major id.
   const int tiles = tiles_m * tiles_n;
   const int b = xcd_block(blockIdx.x, static_cast<int>(gridDim.x));
   const int split = b / tiles;
-  const int tile = b % tiles;
-  const int64_t m0 = static_cast<int64_t>(tile / tiles_n) * BM;
-  const int64_t n0 = static_cast<int64_t>(tile % tiles_n) * BN;
+  int tile_m, tile_n;
+  band_tile(b % tiles, tiles_m, tiles_n, band, tile_m, tile_n);
+  const int tile = tile_m * tiles_n + tile_n;
+  const int64_t m0 = static_cast<int64_t>(tile_m) * BM;
+  const int64_t n0 = static_cast<int64_t>(tile_n) * BN;
   const int64_t kbeg = static_cast<int64_t>(split) * k_per_split;
   int64_t kend = kbeg + k_per_split;
   if (kend > K) kend = K;
@@ -475,6 +479,39 @@ Fp8Plan plan_fp8(int64_t m, int64_t n, int64_t k) {
   return best;
 }
 
+// Rows per band of the tile order. The XCD that runs t = blocks / 8
+// consecutive tiles of a b-row band order holds about `rows` A row-blocks and
+// `cols` B column-blocks (both fp8, over the same K range), and streams
+// rows * BM + cols * BN bytes per unit of K through its L2; b minimizes that
+// (ties keep the smaller b, row-major order at b = 1). The kTuneBand knob
+// forces a band.
+int fp8_band(int tiles_m, int tiles_n, int64_t blocks, int bm, int bn) {
+  const int forced = tune(kTuneBand);
+  if (forced > 0) return forced < tiles_m ? forced : tiles_m;
+  const int64_t t = blocks / 8 > 0 ? blocks / 8 : 1;
+  int best = 1;
+  int64_t best_cost = -1;
+  for (int b = 1; b <= tiles_m && b <= 64; ++b) {
+    const int64_t band_tiles = static_cast<int64_t>(b) * tiles_n;
+    int64_t rows, cols;
+    if (t <= band_tiles) {
+      rows = t < b ? t : b;
+      cols = ceil_div(t, b);
+    } else {
+      const int64_t full = t / band_tiles;
+      const int64_t rem = t - full * band_tiles;
+      rows = full * b + (rem < b ? rem : b);
+      cols = tiles_n;
+    }
+    const int64_t cost = rows * bm + cols * bn;
+    if (best_cost < 0 || cost < best_cost) {
+      best_cost = cost;
+      best = b;
+    }
+  }
+  return best;
+}
+
 template <int BM, int BN, int WM, int WN, int NS, int WPE, int FA, int FB>
 hipError_t run_fp8(const uint8_t* a, const uint8_t* b, int64_t m, int64_t n, int64_t k,
                    const Fp8Plan& plan, const float* s_a, const float* s_b, void* out,
@@ -488,9 +525,10 @@ hipError_t run_fp8(const uint8_t* a, const uint8_t* b, int64_t m, int64_t n, int
   hipError_t le = ensure_lds_limit(reinterpret_cast<const void*>(kern), kLds, lds_set);
   if (le != hipSuccess) return le;
   const unsigned blocks = static_cast<unsigned>(tiles_m) * tiles_n * plan.splits;
+  const int band = fp8_band(tiles_m, tiles_n, blocks, BM, BN);
   hipLaunchKernelGGL(kern, dim3(blocks), dim3(64 * WM * WN), kLds, stream, a, b, m, n, k,
                      plan.k_per_split, s_a, s_b, out, out_dtype, ldc,
-                     plan.splits > 1 ? partials : nullptr, tiles_m, tiles_n);
+                     plan.splits > 1 ? partials : nullptr, tiles_m, tiles_n, band);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || plan.splits == 1) return e;
   const int64_t tiles = static_cast<int64_t>(tiles_m) * tiles_n;
