@@ -259,18 +259,23 @@ TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "fp8_gemm_bert_shapes_hbm_traff
 
 
 def profiled_traffic():
-    """HBM bytes per fp8 GEMM call from the committed --pmc summary (FETCH_SIZE
-    and WRITE_SIZE of the 18 calls, scaled by a plain copy's reading), or
-    None when the summary is absent."""
+    """(HBM bytes per fp8 GEMM call, commit whose code they were measured on)
+    from the committed --pmc summary (FETCH_SIZE and WRITE_SIZE of the 18
+    calls, scaled by a plain copy's reading); (None, None) when the summary
+    is absent. Counter passes cannot run inside the timed bench, so the
+    figure is the summary's, tagged with its commit."""
 
+    found = {}
     try:
         with open(TRAFFIC_PROFILE) as f:
             for line in f:
-                if line.startswith("hbm_bytes_per_call:"):
-                    return float(line.split(":", 1)[1])
+                for key in ("hbm_bytes_per_call", "measured_at_commit"):
+                    if line.startswith(key + ":"):
+                        found[key] = line.split(":", 1)[1].strip()
     except OSError:
-        return None
-    return None
+        return None, None
+    bytes_ = float(found["hbm_bytes_per_call"]) if "hbm_bytes_per_call" in found else None
+    return bytes_, found.get("measured_at_commit")
 
 
 def fp8_gemm_roofline(layers, reps=16):
@@ -287,13 +292,16 @@ def fp8_gemm_roofline(layers, reps=16):
         total_ms += graph_time_per_call_ms([fn] * reps, replays=3)
         total_flops += flops
     achieved = total_flops / (total_ms * 1e-3) / 1e12
+    traffic, traffic_commit = profiled_traffic()
     return {
         "bound": "mfma",
         "achieved": round(achieved, 2),
         "peak": FP8_PEAK_TFLOPS,
         "unit": "TFLOP/s",
         "frac": round(achieved / FP8_PEAK_TFLOPS, 4),
-        "traffic": profiled_traffic(),
+        "traffic": traffic,
+        "traffic_source": {"profile": os.path.relpath(TRAFFIC_PROFILE, ROOT),
+                           "measured_at_commit": traffic_commit},
         "kernel": "k_fp8_gemm (+ k_fp8_split_reduce where split-K): fwd e4m3xe4m3, dX e5m2xe4m3, "
                   "dW e5m2xe4m3; 18 calls per step",
         "avg_launch_us": round(1e3 * total_ms / len(calls), 2),
