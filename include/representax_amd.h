@@ -58,7 +58,8 @@ int rpx_abi_version(void);
  *                        10 128x128 two stages, 11 128x128 three stages,
  *                        12 256x128 two stages (env RPX_GEMM_TILE)
  *   RPX_TUNE_BF16_TILE   bf16 GEMM tile: 0 planner, 4 256x128, 5 128x128,
- *                        6 64x128, 8 256x256, 9 128x96 (env RPX_GEMM_TILE)
+ *                        6 64x128, 8 256x256, 9 128x96, 13 256x128 three
+ *                        stages (env RPX_GEMM_TILE)
  *   RPX_TUNE_FP8_TILE    fp8 GEMM tile: 0 planner, 1..11 (env RPX_FP8_TILE)
  *   RPX_TUNE_SKINNY_TILE one-launch skinny tile: 0 planner, 1..14; a nonzero
  *                        value also turns the two-launch form off

@@ -206,7 +206,8 @@ bool knob_value_ok(int knob, int v) {
              v == kTileI4_128x128s3 || v == kTileI4_256x128s2;
     case kTuneBf16Tile:
       return v == kTileAuto || v == kTileBf_256x128 || v == kTileBf_128x128 ||
-             v == kTileBf_64x128 || v == kTileBf_256x256 || v == kTileBf_128x96;
+             v == kTileBf_64x128 || v == kTileBf_256x256 || v == kTileBf_128x96 ||
+             v == kTileBf_256x128s3;
     case kTuneFp8Tile: return v >= 0 && v < fp8_tile_count();
     case kTuneSkinnyTile: return v >= 0 && v <= skinny_tile_count();
     case kTuneSkinny2:

@@ -829,21 +829,32 @@ hipError_t dispatch_bf16(const uint16_t* a, int64_t lda, const uint16_t* b, int6
     return run_gemm<256, 256, 2, 2, 2, 1, false>(a, lda, b, ldb, none, m, n, k, out, ldc, epi,
                                                  stream);
   if (cfg == kTileAuto) {
-    // 128 x 96 tiles when they make one balanced round of 192-256 workgroups
-    // where 128 x 128 would leave CUs idle (measured on 4096 x 768 outputs:
-    // 31 us against 33 us for two uneven rounds of 64 x 128)
+    // Grids of at least 256 tiles of 256 x 128 take that tile with a
+    // three-stage pipeline (one workgroup of 8 waves per CU): the deeper
+    // prefetch pays on long reductions (the INT4 + LoRA backward at
+    // 16384 x 2048 <- 6144: 538 us against 628 with two stages; 16384 x 6144
+    // <- 2048: 597 against 636), except for short reductions (K <= 1024)
+    // with many tiles, where 128 x 128 tiles at two workgroups per CU are
+    // faster (32768 x 3072 <- 768: 323 against 330-341 us). 128 x 96 tiles
+    // when they make one balanced round of 192-256 workgroups where
+    // 128 x 128 would leave CUs idle (4096 x 768 outputs: 31 us against 33
+    // for two uneven rounds of 64 x 128).
     const int64_t t128 = ceil_div(m, 128) * ceil_div(n, 128);
     const int64_t t96 = ceil_div(m, 128) * ceil_div(n, 96);
-    cfg = ceil_div(m, 256) * ceil_div(n, 128) >= 256
-              ? kTileBf_256x128
-              : (t128 >= 256 ? kTileBf_128x128
-                             : (t96 >= 192 && t96 <= 256 ? kTileBf_128x96 : kTileBf_64x128));
+    if (ceil_div(m, 256) * ceil_div(n, 128) >= 256)
+      cfg = k <= 1024 && t128 >= 512 ? kTileBf_128x128 : kTileBf_256x128s3;
+    else
+      cfg = t128 >= 256 ? kTileBf_128x128
+                        : (t96 >= 192 && t96 <= 256 ? kTileBf_128x96 : kTileBf_64x128);
   }
   if (cfg == kTileBf_128x96)
     return run_gemm<128, 96, 4, 1, 3, 1, false>(a, lda, b, ldb, none, m, n, k, out, ldc, epi,
                                                 stream);
   if (cfg == kTileBf_256x128)
     return run_gemm<256, 128, 4, 2, 2, 2, false>(a, lda, b, ldb, none, m, n, k, out, ldc, epi,
+                                                 stream);
+  if (cfg == kTileBf_256x128s3)
+    return run_gemm<256, 128, 4, 2, 3, 2, false>(a, lda, b, ldb, none, m, n, k, out, ldc, epi,
                                                  stream);
   if (cfg == kTileBf_128x128)
     return run_gemm<128, 128, 2, 2, 2, 2, false>(a, lda, b, ldb, none, m, n, k, out, ldc, epi,

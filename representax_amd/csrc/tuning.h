@@ -43,6 +43,7 @@ enum GemmTile : int {
   kTileI4_128x128s2 = 10,  // INT4 128 x 128, two stages, three workgroups per CU
   kTileI4_128x128s3 = 11,  // INT4 128 x 128, three stages, two workgroups per CU
   kTileI4_256x128s2 = 12,  // INT4 256 x 128, two stages, two workgroups per CU
+  kTileBf_256x128s3 = 13,  // bf16 256 x 128, three stages, one workgroup per CU
 };
 
 // Sets the dynamic-LDS limit of a kernel once per device (idempotent, so
