@@ -402,6 +402,34 @@ int rpx_fp8_encode_selfcheck(int fmt, uint64_t first, uint64_t count, uint32_t* 
 int rpx_host_fp8_quantize(const float* host_in, int64_t n, float scale, int fmt,
                           uint8_t* host_out);
 
+/* ---------------------------------------------------------------------------
+ * In-batch multiple-negatives ranking loss, fused (the train-step objective
+ * next to the path): replaces `mnr_loss_terms(queries, documents,
+ * eye(n_queries, n_documents), scale=scale).loss` with unit weights and
+ * every row valid, src/representax/tasks/retrieval/mnr.py:48-52
+ * (`_normalize`), :132-158 (`_direction_row_terms`), :338-341 (forward
+ * loss). The embeddings (f32 or bf16, dense [n, dim]) are cast to f32 and
+ * normalised by max(||row||, 1e-12); logits = scale * cosine; loss = mean
+ * over queries of logsumexp_j(logits[i, j]) - logits[i, i].
+ * Requires 1 <= n_queries <= n_documents <= 8192, 1 <= dim <= 4096 and a
+ * finite scale > 0 (the reference's ValueError).
+ * ------------------------------------------------------------------------- */
+/* Bytes of the buffer the forward fills and the backward reads (0 for an
+ * unsupported shape). */
+size_t rpx_mnr_saved_bytes(int64_t n_queries, int64_t n_documents, int64_t dim);
+
+/* *loss (device f32) = the loss; `saved` keeps the normalised rows, norms
+ * and softmax rows for the backward. */
+int rpx_mnr_forward(const void* queries, const void* documents, int dtype, int64_t n_queries,
+                    int64_t n_documents, int64_t dim, float scale, float* loss, void* saved,
+                    size_t saved_bytes, void* stream);
+
+/* d_queries / d_documents (dtype as the embeddings) = *grad_loss (device
+ * f32) times the gradient of the loss, from the forward's `saved`. */
+int rpx_mnr_backward(const float* grad_loss, const void* saved, size_t saved_bytes,
+                     int64_t n_queries, int64_t n_documents, int64_t dim, float scale,
+                     void* d_queries, void* d_documents, int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

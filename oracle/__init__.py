@@ -11,6 +11,9 @@ codecs, the numerics of
 * ``src/representax/models/components.py:153-167``,
   ``bert/model.py:243-249`` and ``qwen3_vl/text.py:200-203`` (the GELU and
   SiLU-gated FFN steps next to the linears, ``act``),
+* ``src/representax/tasks/retrieval/mnr.py:48-52,132-158,338-341`` (the
+  in-batch multiple-negatives ranking loss of the train-step harnesses,
+  ``mnr``),
 
 so that tests, the smoke check and the benchmark's CPU-baseline leg can check
 the HIP kernels of ``representax_amd``. Nothing in the product imports it; the
@@ -32,6 +35,10 @@ Pinning (what checks each function against something other than itself):
 * ``fp8``: amax/scale closed forms (zero, inf, NaN tensors), cast through the
   torch-pinned codec, dot compared with an fp64 product of the exactly decoded
   operands, VJP compared with the transposed-product identities.
+* ``mnr``: brute-force loops, the orthonormal closed form
+  (log(e^s + n - 1) - s per row, a zero row clamped at 1e-12), torch's
+  float64 logsumexp and autograd, and central finite differences on exactly
+  representable steps.
 * ``act``: GELU and SiLU against torch's float64 routines and closed forms
   (gelu(0) = 0, gelu(-z) = gelu(z) - z, silu(-g) = silu(g) - g), their
   derivatives against central finite differences, the fused blocks' backward

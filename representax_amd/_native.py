@@ -121,6 +121,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _int, [_int, ctypes.c_uint64, ctypes.c_uint64, _p, _p, _i64, _p]
     ),
     "rpx_host_fp8_quantize": (_int, [_p, _i64, _f32, _int, _p]),
+    "rpx_mnr_saved_bytes": (ctypes.c_size_t, [_i64, _i64, _i64]),
+    "rpx_mnr_forward": (_int, [_p, _p, _int, _i64, _i64, _i64, _f32, _p, _p, ctypes.c_size_t, _p]),
+    "rpx_mnr_backward": (_int, [_p, _p, ctypes.c_size_t, _i64, _i64, _i64, _f32, _p, _p, _int, _p]),
 }
 
 

@@ -2,6 +2,7 @@
 // sequencing for the quantized-linear path. No entry point allocates device
 // memory or synchronizes; every launch goes to the caller's stream.
 #include <atomic>
+#include <cmath>
 #include <cstdlib>
 #include <cstring>
 #include <initializer_list>
@@ -1350,6 +1351,54 @@ int rpx_host_fp8_quantize(const float* in, int64_t n, float scale, int fmt, uint
     const float q = div_rn(in[i], scale, r);
     out[i] = static_cast<uint8_t>(fmt == kE4M3FN ? f32_to_e4m3fn(q) : f32_to_e5m2(q));
   }
+  return kOk;
+}
+
+// ---------------------------------------------------------------------------
+// Fused in-batch MNR loss (the train-step objective)
+// ---------------------------------------------------------------------------
+size_t rpx_mnr_saved_bytes(int64_t n_queries, int64_t n_documents, int64_t dim) {
+  if (!mnr_shape_ok(n_queries, n_documents, dim)) return 0;
+  return static_cast<size_t>(mnr_saved_floats(n_queries, n_documents, dim)) * sizeof(float);
+}
+
+static int check_mnr(int64_t nq, int64_t nd, int64_t dim, float scale, size_t saved_bytes,
+                     const char* who) {
+  if (!mnr_shape_ok(nq, nd, dim))
+    return fail_invalid(std::string(who) +
+                        ": need 1 <= n_queries <= n_documents <= 8192 and 1 <= dim <= 4096 "
+                        "(query i's positive is document i)");
+  if (!(scale > 0.0f) || !std::isfinite(scale))
+    return fail_invalid(std::string(who) + ": scale must be finite and positive");
+  if (saved_bytes < static_cast<size_t>(mnr_saved_floats(nq, nd, dim)) * sizeof(float))
+    return fail_invalid(std::string(who) + ": saved buffer too small");
+  return kOk;
+}
+
+int rpx_mnr_forward(const void* queries, const void* documents, int dtype, int64_t n_queries,
+                    int64_t n_documents, int64_t dim, float scale, float* loss, void* saved,
+                    size_t saved_bytes, void* stream) {
+  RPX_TRY(check_dtype(dtype));
+  RPX_TRY(check_mnr(n_queries, n_documents, dim, scale, saved_bytes, "rpx_mnr_forward"));
+  if (queries == nullptr || documents == nullptr || loss == nullptr || saved == nullptr)
+    return fail_invalid("rpx_mnr_forward: null pointer");
+  RPX_HIP(launch_mnr_forward(queries, documents, dtype, n_queries, n_documents, dim, scale, loss,
+                             static_cast<float*>(saved), static_cast<hipStream_t>(stream)),
+          "rpx_mnr_forward");
+  return kOk;
+}
+
+int rpx_mnr_backward(const float* grad_loss, const void* saved, size_t saved_bytes,
+                     int64_t n_queries, int64_t n_documents, int64_t dim, float scale,
+                     void* d_queries, void* d_documents, int dtype, void* stream) {
+  RPX_TRY(check_dtype(dtype));
+  RPX_TRY(check_mnr(n_queries, n_documents, dim, scale, saved_bytes, "rpx_mnr_backward"));
+  if (grad_loss == nullptr || saved == nullptr || d_queries == nullptr || d_documents == nullptr)
+    return fail_invalid("rpx_mnr_backward: null pointer");
+  RPX_HIP(launch_mnr_backward(grad_loss, static_cast<const float*>(saved), n_queries, n_documents,
+                              dim, scale, d_queries, d_documents, dtype,
+                              static_cast<hipStream_t>(stream)),
+          "rpx_mnr_backward");
   return kOk;
 }
 

@@ -206,4 +206,16 @@ hipError_t launch_fp8_scale_update(float* scales, const float* fmax, uint32_t* p
 hipError_t launch_fp8_encode_selfcheck(int fmt, uint64_t first, uint64_t count, uint32_t* counts,
                                        uint32_t* firsts, int64_t blocks, hipStream_t stream);
 
+// Fused in-batch MNR loss (query i's positive is document i). The forward
+// leaves in `saved` (mnr_saved_floats floats) what the backward reads.
+constexpr int64_t kMnrMaxDocuments = 8192;
+int64_t mnr_saved_floats(int64_t nq, int64_t nd, int64_t dim);
+bool mnr_shape_ok(int64_t nq, int64_t nd, int64_t dim);
+hipError_t launch_mnr_forward(const void* q, const void* d, int dtype, int64_t nq, int64_t nd,
+                              int64_t dim, float scale, float* loss, float* saved,
+                              hipStream_t stream);
+hipError_t launch_mnr_backward(const float* grad_loss, const float* saved, int64_t nq, int64_t nd,
+                               int64_t dim, float scale, void* dq, void* dd, int dtype,
+                               hipStream_t stream);
+
 }  // namespace rpx

@@ -597,6 +597,61 @@ class Int4LoRASharedInputFn(torch.autograd.Function):
 
 
 # ---------------------------------------------------------------------------
+# Fused in-batch MNR loss
+# ---------------------------------------------------------------------------
+class MNRLossFn(torch.autograd.Function):
+    """In-batch multiple-negatives ranking loss with query i's positive at
+    document i (src/representax/tasks/retrieval/mnr.py:48-52,132-158,
+    338-341): f32 casts, row normalisation, scaled cosine logits, row
+    log-sum-exp and the mean over queries in one fused forward, and its
+    gradient in one launch."""
+
+    @staticmethod
+    def forward(ctx, queries, documents, scale: float):
+        device = _on_device(queries, documents)
+        if queries.dim() != 2 or documents.dim() != 2:
+            raise ValueError("query and document embeddings must be matrices")
+        if queries.shape[1] != documents.shape[1]:
+            raise ValueError("query and document embedding dimensions must match")
+        if isinstance(scale, bool) or not math.isfinite(float(scale)) or float(scale) <= 0:
+            raise ValueError("scale must be finite and positive")
+        dtype = queries.dtype
+        q = queries.contiguous()
+        d = documents.to(dtype).contiguous()
+        nq, dim = q.shape
+        nd = d.shape[0]
+        nbytes = nat.query("rpx_mnr_saved_bytes", nq, nd, dim)
+        if nbytes == 0:
+            raise ValueError("fused MNR loss needs 1 <= queries <= documents <= 8192 and "
+                             "1 <= dim <= 4096 (query i's positive is document i)")
+        saved = torch.empty(nbytes // 4, dtype=F32, device=device)
+        loss = torch.empty((), dtype=F32, device=device)
+        nat.call("rpx_mnr_forward", _ptr(q), _ptr(d), _dtype_code(dtype), nq, nd, dim,
+                 float(scale), _ptr(loss), _ptr(saved), nbytes, _stream(device))
+        ctx.save_for_backward(saved)
+        ctx.shape = (nq, nd, dim, float(scale), dtype, documents.dtype)
+        return loss
+
+    @staticmethod
+    def backward(ctx, grad_loss):
+        (saved,) = ctx.saved_tensors
+        nq, nd, dim, scale, dtype, d_dtype = ctx.shape
+        device = saved.device
+        g = grad_loss.to(F32).contiguous().reshape(1)
+        dq = torch.empty((nq, dim), dtype=dtype, device=device)
+        dd = torch.empty((nd, dim), dtype=dtype, device=device)
+        nat.call("rpx_mnr_backward", _ptr(g), _ptr(saved), saved.numel() * 4, nq, nd, dim, scale,
+                 _ptr(dq), _ptr(dd), _dtype_code(dtype), _stream(device))
+        return dq, dd.to(d_dtype), None
+
+
+def mnr_loss(queries: torch.Tensor, documents: torch.Tensor, scale: float = 20.0) -> torch.Tensor:
+    """Scalar f32 loss; differentiable in both embedding sets (f32 or bf16)."""
+
+    return MNRLossFn.apply(queries, documents, scale)
+
+
+# ---------------------------------------------------------------------------
 # FP8
 # ---------------------------------------------------------------------------
 FORMATS = {"e4m3fn": nat.FP8_E4M3FN, "e5m2": nat.FP8_E5M2}

@@ -39,6 +39,7 @@ import torch
 import torch.nn.functional as F
 from torch.utils.checkpoint import checkpoint
 
+from . import ops
 from .adapters import apply_quantized_lora, lora_parameters
 from .components import Linear
 from .config import PrecisionConfig
@@ -268,12 +269,11 @@ class BertEncoder(torch.nn.Module):
 
 def mnr_loss(queries: torch.Tensor, documents: torch.Tensor, scale: float = 20.0) -> torch.Tensor:
     """Mean over queries of ``logsumexp_j(scale cos(q, d_j)) - scale cos(q, d_q)``
-    with each query's own document as its positive."""
+    with each query's own document as its positive
+    (src/representax/tasks/retrieval/mnr.py:48-52,132-158,338-341): the
+    fused HIP loss, f32 casts and normalisation included."""
 
-    q = queries.float() / queries.float().norm(dim=-1, keepdim=True).clamp_min(1e-12)
-    d = documents.float() / documents.float().norm(dim=-1, keepdim=True).clamp_min(1e-12)
-    logits = (q @ d.t()) * scale
-    return (torch.logsumexp(logits, dim=1) - logits.diagonal()).mean()
+    return ops.mnr_loss(queries, documents, scale)
 
 
 LAYER_LINEARS = r"\.layers\[\d+\]\.(attention\.(query|key|value|output)|mlp\.(input|output|gate|up|down))$"
