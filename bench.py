@@ -847,7 +847,71 @@ def run_skinny(batch=96, latency_calls=64):
             torch.cuda.empty_cache()
     return {"workload": "skinny-M INT4 + LoRA r32 forward, Qwen3-2B projection shapes, group-64 "
                         "and per-row scales; us_per_call inside a HIP graph of 96 calls cycling "
-                        "weight copies > 256 MB, p50_us over single eager calls", "points": out}
+                        "weight copies > 256 MB, p50_us over single eager calls", "points": out,
+            "shared_input": run_skinny_shared(batch, latency_calls)}
+
+
+SHARED_INPUT_GROUPS = [("qwen3 q/k/v", 2048, (2048, 1024, 1024)),
+                       ("qwen3 gate/up", 2048, (6144, 6144))]
+
+
+def run_skinny_shared(batch=96, latency_calls=64, group=64, r=32):
+    """Projections of one input (the Qwen3-2B tower's q/k/v and gate/up) at
+    M in {1, 4}: one rpx_int4lora_forward_multi call against one call per
+    projection, both per call inside a HIP graph of `batch` calls cycling
+    weight copies beyond the MALL, plus the multi call's eager p50. HBM bytes:
+    every projection's packed weight, scales, A, B and y, and x once."""
+
+    import torch
+
+    from representax_amd import ops
+
+    dev = torch.device("cuda:0")
+    g = np.random.Generator(np.random.PCG64(6))
+    out = []
+    for name, k, ns in SHARED_INPUT_GROUPS:
+        per_copy = sum(n * k // 2 + n * (k // group) * 2 + (r * k + n * r) * 2 for n in ns)
+        copies = max(8, int(np.ceil(300e6 / per_copy)))
+        base = []
+        for n in ns:
+            w = torch.from_numpy((g.standard_normal((n, k)) * 0.02).astype(np.float32)).to(dev)
+            packed, scales = ops.int4_pack(w, group_size=group)
+            a = bf16_tensor(g.standard_normal((r, k)).astype(np.float32) * 0.02, dev)
+            b = bf16_tensor(g.standard_normal((n, r)).astype(np.float32) * 0.02, dev)
+            base.append((packed, scales, a, b))
+        pool = [[tuple(t.clone() for t in p) for p in base] for _ in range(copies)]
+        for m in (1, 4):
+            x = bf16_tensor(g.standard_normal((m, k)).astype(np.float32), dev)
+            multi, separate = [], []
+            for i in range(batch):
+                projs = pool[i % copies]
+                multi.append(lambda projs=projs: ops.int4lora_forward_multi(
+                    x, [(p, s, a, b, 2.0, group, None) for p, s, a, b in projs]))
+                separate.append(lambda projs=projs: [
+                    ops.int4lora_forward(x, p, s, a, b, scaling=2.0, group_size=group)
+                    for p, s, a, b in projs])
+            us_multi = graph_time_per_call_ms(multi, replays=3) * 1e3
+            us_sep = graph_time_per_call_ms(separate, replays=3) * 1e3
+            lat = []
+            for i in range(latency_calls):
+                fn = multi[(i * 7) % batch]
+                e0 = torch.cuda.Event(enable_timing=True)
+                e1 = torch.cuda.Event(enable_timing=True)
+                e0.record()
+                fn()
+                e1.record()
+                e1.synchronize()
+                lat.append(e0.elapsed_time(e1) * 1e3)
+            nbytes = m * k * 2 + sum(n * k / 2 + n * (k // group) * 2 + (r * k + n * r) * 2
+                                     + m * n * 2 for n in ns)
+            out.append({"group": name, "m": m, "k": k, "n": list(ns),
+                        "us_per_call": round(us_multi, 2), "separate_us": round(us_sep, 2),
+                        "p50_us": round(float(np.median(lat)), 2),
+                        "gbs": round(nbytes / (us_multi * 1e-6) / 1e9, 1),
+                        "frac_hbm": round(nbytes / (us_multi * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
+        del pool, base
+        torch.cuda.empty_cache()
+    return out
 
 
 def main():

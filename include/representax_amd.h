@@ -151,6 +151,38 @@ int rpx_int4lora_forward(const void* x, int dtype, int64_t m, int64_t k, const u
                          int64_t rank, float scaling, void* y, void* h, void* workspace,
                          size_t workspace_bytes, void* stream);
 
+/* Several INT4 + LoRA projections of one input x (the q / k / v or gate / up
+ * projections of a layer), each with its own weight, scales, adapter, bias
+ * and outputs. Every projection's y and h are what rpx_int4lora_forward
+ * gives for it, within the same numerics (the fused form may split K
+ * differently). No single reference function: it replaces consecutive
+ * QuantizedLoRALinear.__call__ on one input (adapters.py:158-182), e.g.
+ * bert/model.py's query / key / value and qwen3_vl/text.py's gate / up.
+ * For bf16 with M <= 4 (the skinny-M regime), one rank and at most 4
+ * projections, all of them run in one pair of launches instead of one pair
+ * each; otherwise they run one after another. */
+typedef struct rpx_int4lora_projection {
+  const uint8_t* packed;       /* [n, ceil(k/2)] */
+  const uint16_t* scale_bits;  /* [n] or [n, k / group_size] */
+  int64_t n;
+  int64_t group_size;          /* 0 or k: per-row scales */
+  const uint16_t* bias_bits;   /* [n] or NULL */
+  const void* lora_a;          /* [rank, k], x's dtype */
+  const void* lora_b;          /* [n, rank], x's dtype */
+  int64_t rank;
+  float scaling;
+  void* y;                     /* [m, n] */
+  void* h;                     /* [m, rank] */
+} rpx_int4lora_projection;
+
+/* Sized from the shapes alone: the pointers may be unset. */
+size_t rpx_int4lora_forward_multi_workspace(int64_t m, int64_t k, int count,
+                                            const rpx_int4lora_projection* projections,
+                                            int dtype);
+int rpx_int4lora_forward_multi(const void* x, int dtype, int64_t m, int64_t k, int count,
+                               const rpx_int4lora_projection* projections, void* workspace,
+                               size_t workspace_bytes, void* stream);
+
 /* rpx_int4lora_forward without a workspace argument, for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc); no counterpart in the reference. Scratch

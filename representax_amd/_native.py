@@ -121,10 +121,30 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _int, [_int, ctypes.c_uint64, ctypes.c_uint64, _p, _p, _i64, _p]
     ),
     "rpx_host_fp8_quantize": (_int, [_p, _i64, _f32, _int, _p]),
+    "rpx_int4lora_forward_multi_workspace": (_size, [_i64, _i64, _int, _p, _int]),
+    "rpx_int4lora_forward_multi": (_int, [_p, _int, _i64, _i64, _int, _p, _p, _size, _p]),
     "rpx_mnr_saved_bytes": (ctypes.c_size_t, [_i64, _i64, _i64]),
     "rpx_mnr_forward": (_int, [_p, _p, _int, _i64, _i64, _i64, _f32, _p, _p, ctypes.c_size_t, _p]),
     "rpx_mnr_backward": (_int, [_p, _p, ctypes.c_size_t, _i64, _i64, _i64, _f32, _p, _p, _int, _p]),
 }
+
+
+class Int4LoraProjection(ctypes.Structure):
+    """``rpx_int4lora_projection`` of include/representax_amd.h."""
+
+    _fields_ = [
+        ("packed", ctypes.c_void_p),
+        ("scale_bits", ctypes.c_void_p),
+        ("n", ctypes.c_int64),
+        ("group_size", ctypes.c_int64),
+        ("bias_bits", ctypes.c_void_p),
+        ("lora_a", ctypes.c_void_p),
+        ("lora_b", ctypes.c_void_p),
+        ("rank", ctypes.c_int64),
+        ("scaling", ctypes.c_float),
+        ("y", ctypes.c_void_p),
+        ("h", ctypes.c_void_p),
+    ]
 
 
 class NativeError(RuntimeError):

@@ -529,6 +529,110 @@ int rpx_int4lora_forward(const void* x, int dtype, int64_t m, int64_t k, const u
 
 }  // extern "C"
 
+namespace {
+
+// The fused form of rpx_int4lora_forward_multi: bf16, every projection on
+// the two-launch skinny path (M <= 4 by default), one rank, at most 4
+// projections, 16-byte aligned operands. Fills `out` when it applies.
+bool multi_fused_shape(int dtype, int64_t m, int64_t k, int count,
+                       const rpx_int4lora_projection* proj, Skinny2Projection* out) {
+  if (dtype != kBF16 || count < 2 || count > 4 || m < 1) return false;
+  for (int i = 0; i < count; ++i) {
+    const rpx_int4lora_projection& q = proj[i];
+    int64_t ng = 1, g = k;
+    if (q.group_size > 0 && q.group_size != k) {
+      if (k % q.group_size != 0) return false;
+      ng = k / q.group_size;
+      g = q.group_size;
+    }
+    if (q.rank != proj[0].rank || q.n < 1 || q.rank < 1 || q.rank > q.n || q.rank > k)
+      return false;
+    if (!lora_skinny(dtype, m, q.n, k, ng, g, q.rank) ||
+        !skinny2_selected(m, q.n, k, q.rank, ng, g))
+      return false;
+    Skinny2Projection& o = out[i];
+    o.w.packed = q.packed;
+    o.w.packed_cols = (k + 1) / 2;
+    o.w.scales = q.scale_bits;
+    o.w.n_groups = ng;
+    o.w.group = g;
+    o.n = q.n;
+    o.lora_a = static_cast<const uint16_t*>(q.lora_a);
+    o.lora_b = static_cast<const uint16_t*>(q.lora_b);
+    o.rank = q.rank;
+    o.scale = round_to_dtype(q.scaling, dtype);
+    o.bias = q.bias_bits;
+    o.y = static_cast<uint16_t*>(q.y);
+    o.h = static_cast<uint16_t*>(q.h);
+  }
+  return skinny2_multi_ok(m, k, count, out);
+}
+
+bool multi_fused(const void* x, int dtype, int64_t m, int64_t k, int count,
+                 const rpx_int4lora_projection* proj, Skinny2Projection* out) {
+  if (x == nullptr || !multi_fused_shape(dtype, m, k, count, proj, out)) return false;
+  for (int i = 0; i < count; ++i) {
+    const rpx_int4lora_projection& q = proj[i];
+    if (q.packed == nullptr || q.scale_bits == nullptr || q.lora_a == nullptr ||
+        q.lora_b == nullptr || q.y == nullptr || q.h == nullptr ||
+        !aligned16_all({x, q.packed, q.scale_bits, q.lora_a, q.y}))
+      return false;
+  }
+  return true;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t rpx_int4lora_forward_multi_workspace(int64_t m, int64_t k, int count,
+                                            const rpx_int4lora_projection* projections,
+                                            int dtype) {
+  if (count < 1 || projections == nullptr) return 0;
+  // sized from the shapes alone (pointers may be unset at query time): the
+  // larger of the fused form and of one projection at a time
+  Skinny2Projection fused[4];
+  size_t most = 0;
+  if (multi_fused_shape(dtype, m, k, count, projections, fused)) {
+    Sizer s;
+    s.take<float>(skinny2_multi_workspace_floats(m, k, count, fused));
+    most = s.used;
+  }
+  for (int i = 0; i < count; ++i) {
+    const size_t b = rpx_int4lora_forward_workspace(m, projections[i].n, k,
+                                                    projections[i].group_size,
+                                                    projections[i].rank, dtype);
+    if (b > most) most = b;
+  }
+  return most;
+}
+
+int rpx_int4lora_forward_multi(const void* x, int dtype, int64_t m, int64_t k, int count,
+                               const rpx_int4lora_projection* projections, void* workspace,
+                               size_t workspace_bytes, void* stream) {
+  if (count < 1 || count > 64 || projections == nullptr)
+    return fail_invalid("rpx_int4lora_forward_multi: need 1..64 projections");
+  Skinny2Projection fused[4];
+  if (multi_fused(x, dtype, m, k, count, projections, fused)) {
+    Arena arena(workspace, workspace_bytes);
+    float* ws = arena.take<float>(skinny2_multi_workspace_floats(m, k, count, fused));
+    if (arena.overflow) return fail_invalid("rpx_int4lora_forward_multi: workspace too small");
+    RPX_HIP(launch_skinny2_forward_multi(static_cast<const uint16_t*>(x), m, k, count, fused, ws,
+                                         static_cast<hipStream_t>(stream)),
+            "rpx_int4lora_forward_multi: skinny-M kernels");
+    return kOk;
+  }
+  for (int i = 0; i < count; ++i) {
+    const rpx_int4lora_projection& q = projections[i];
+    RPX_TRY(rpx_int4lora_forward(x, dtype, m, k, q.packed, q.scale_bits, q.n, q.group_size,
+                                 q.bias_bits, q.lora_a, q.lora_b, q.rank, q.scaling, q.y, q.h,
+                                 workspace, workspace_bytes, stream));
+  }
+  return kOk;
+}
+
+}  // extern "C"
+
 // --- static scratch for the entry point that allocates nothing ----------------
 namespace rpx {
 namespace {

@@ -90,6 +90,24 @@ hipError_t launch_skinny2_forward(const uint16_t* x, int64_t m, int64_t k, const
                                   int64_t rank, float scale, const uint16_t* bias, uint16_t* y,
                                   uint16_t* h, float* ws, hipStream_t stream);
 int64_t skinny2_workspace_floats(int64_t m, int64_t n, int64_t k, int64_t rank);
+// Several projections of one x (same K and rank) in one pair of launches.
+struct Skinny2Projection {
+  Int4Operand w;
+  int64_t n;
+  const uint16_t* lora_a;
+  const uint16_t* lora_b;
+  int64_t rank;
+  float scale;
+  const uint16_t* bias;
+  uint16_t* y;
+  uint16_t* h;
+};
+bool skinny2_multi_ok(int64_t m, int64_t k, int count, const Skinny2Projection* proj);
+int64_t skinny2_multi_workspace_floats(int64_t m, int64_t k, int count,
+                                       const Skinny2Projection* proj);
+hipError_t launch_skinny2_forward_multi(const uint16_t* x, int64_t m, int64_t k, int count,
+                                        const Skinny2Projection* proj, float* ws,
+                                        hipStream_t stream);
 
 // Elementwise activation transform (ActMode in act.h) over count dense
 // elements: out = f(v, aux, aux2), out2 the second output of the SiLU-mul

@@ -277,11 +277,10 @@ __global__ void __launch_bounds__(64 * NW) k_skinny_main(Skinny2Params p) {
 // registers (RV 16-byte vectors) and produces y[m, n] for m = tid >> 6,
 // (tid >> 6) + 4, ...; h comes from the partials through LDS.
 template <int RV>
-__global__ void __launch_bounds__(kFinThreads) k_skinny_finish(Skinny2Params p) {
-  __shared__ float hs[16 * 64];
+__device__ __forceinline__ void finish_block(const Skinny2Params& p, int64_t block, float* hs) {
   const int tid = threadIdx.x;
   const int mr = p.m * p.rank;
-  const int64_t n = static_cast<int64_t>(blockIdx.x) * kFinRows + (tid & 63);
+  const int64_t n = block * kFinRows + (tid & 63);
   const bool nok = n < p.n;
   const int64_t nc = nok ? n : p.n - 1;
   uint32_t bw[4 * RV];
@@ -318,7 +317,7 @@ __global__ void __launch_bounds__(kFinThreads) k_skinny_finish(Skinny2Params p) 
     for (int s = 0; s < p.slices; ++s) sum += p.part[static_cast<int64_t>(s) * mr + e];
     const float hv = round_bf16(sum);
     hs[e] = hv;
-    if (blockIdx.x == 0) p.h[e] = f32_to_bf16(hv);
+    if (block == 0) p.h[e] = f32_to_bf16(hv);
   }
   __syncthreads();
   if (!nok) return;
@@ -336,6 +335,67 @@ __global__ void __launch_bounds__(kFinThreads) k_skinny_finish(Skinny2Params p) 
     float r = round_bf16(bf16_to_f32(base[i]) + round_bf16(round_bf16(t) * p.scale));
     if (p.bias != nullptr) r = round_bf16(r + bias);
     p.y[static_cast<int64_t>(m) * p.n + n] = f32_to_bf16(r);
+  }
+}
+
+template <int RV>
+__global__ void __launch_bounds__(kFinThreads) k_skinny_finish(Skinny2Params p) {
+  __shared__ float hs[16 * 64];
+  finish_block<RV>(p, blockIdx.x, hs);
+}
+
+// ---------------------------------------------------------------------------
+// Several projections of one input in one pair of launches (the q / k / v
+// or gate / up projections of a layer at small M): the first grid holds
+// every projection's adapter blocks, then every projection's weight blocks;
+// the finishing grid every projection's row blocks. Each block does what it
+// does in the single-projection launches, on its projection's operands.
+constexpr int kMaxProjections = 4;
+struct Skinny2Multi {
+  Skinny2Params p[kMaxProjections];
+  int count;
+};
+
+template <int NW, int CPW>
+__global__ void __launch_bounds__(64 * NW) k_skinny_main_multi(Skinny2Multi mp) {
+  __shared__ f32x4_v red[(NW > 1 ? NW - 1 : 1) * 64];
+  int64_t b = blockIdx.x;
+#pragma unroll
+  for (int i = 0; i < kMaxProjections; ++i) {
+    if (i < mp.count) {
+      if (b < mp.p[i].a_blocks) {
+        adapter_block<NW>(mp.p[i], static_cast<int>(b), red);
+        return;
+      }
+      b -= mp.p[i].a_blocks;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kMaxProjections; ++i) {
+    if (i < mp.count) {
+      if (b < mp.p[i].w_blocks) {
+        weight_block<NW, CPW>(mp.p[i], b, red);
+        return;
+      }
+      b -= mp.p[i].w_blocks;
+    }
+  }
+}
+
+template <int RV>
+__global__ void __launch_bounds__(kFinThreads) k_skinny_finish_multi(Skinny2Multi mp) {
+  __shared__ float hs[16 * 64];
+  int64_t b = blockIdx.x;
+#pragma unroll
+  for (int i = 0; i < kMaxProjections; ++i) {
+    if (i < mp.count) {
+      const int64_t blocks = (mp.p[i].n + kFinRows - 1) / kFinRows;
+      if (b < blocks) {
+        finish_block<RV>(mp.p[i], b, hs);
+        return;
+      }
+      b -= blocks;
+    }
   }
 }
 
@@ -651,6 +711,104 @@ hipError_t launch_skinny2_forward(const uint16_t* x, int64_t m, int64_t k, const
     case 6: hipLaunchKernelGGL(k_skinny_finish<6>, fin_grid, dim3(kFinThreads), 0, stream, p); break;
     case 7: hipLaunchKernelGGL(k_skinny_finish<7>, fin_grid, dim3(kFinThreads), 0, stream, p); break;
     default: hipLaunchKernelGGL(k_skinny_finish<8>, fin_grid, dim3(kFinThreads), 0, stream, p); break;
+  }
+  return hipGetLastError();
+}
+
+bool skinny2_multi_ok(int64_t m, int64_t k, int count, const Skinny2Projection* proj) {
+  if (count < 1 || count > kMaxProjections) return false;
+  int64_t n_total = 0;
+  for (int i = 0; i < count; ++i) {
+    if (proj[i].rank != proj[0].rank) return false;
+    if (!skinny2_ok(m, proj[i].n, k, proj[i].rank, proj[i].w.n_groups, proj[i].w.group))
+      return false;
+    n_total += proj[i].n;
+  }
+  // every weight wave covers its K range in at most 4 chunks of 128 columns
+  return k / 128 <= 4 * plan2(n_total, k).nw;
+}
+
+int64_t skinny2_multi_workspace_floats(int64_t m, int64_t k, int count,
+                                       const Skinny2Projection* proj) {
+  int64_t n_total = 0;
+  for (int i = 0; i < count; ++i) n_total += proj[i].n;
+  const int64_t slices = plan2(n_total, k).slices;
+  int64_t floats = 0;
+  for (int i = 0; i < count; ++i) floats += slices * m * proj[i].rank;
+  return floats;
+}
+
+hipError_t launch_skinny2_forward_multi(const uint16_t* x, int64_t m, int64_t k, int count,
+                                        const Skinny2Projection* proj, float* ws,
+                                        hipStream_t stream) {
+  int64_t n_total = 0;
+  for (int i = 0; i < count; ++i) n_total += proj[i].n;
+  // one block shape for the whole grid, planned for all rows together
+  const Skinny2Plan pl = plan2(n_total, k);
+  Skinny2Multi mp{};
+  mp.count = count;
+  int64_t a_total = 0, w_total = 0, fin_total = 0;
+  float* part = ws;
+  for (int i = 0; i < count; ++i) {
+    const Skinny2Projection& q = proj[i];
+    Skinny2Params& p = mp.p[i];
+    p.x = x;
+    p.m = static_cast<int>(m);
+    p.k = k;
+    p.n = q.n;
+    p.packed = q.w.packed;
+    p.pcols = q.w.packed_cols;
+    p.scales = q.w.scales;
+    p.n_groups = q.w.n_groups;
+    p.group_shift = 0;
+    if (q.w.n_groups > 1)
+      while ((int64_t{1} << p.group_shift) < q.w.group) ++p.group_shift;
+    p.lora_a = q.lora_a;
+    p.lora_b = q.lora_b;
+    p.rank = static_cast<int>(q.rank);
+    p.scale = q.scale;
+    p.bias = q.bias;
+    p.y = q.y;
+    p.h = q.h;
+    p.part = part;
+    p.slices = pl.slices;
+    p.a_blocks = p.slices * static_cast<int>(ceil_div(q.rank, 16));
+    p.b_vec = (reinterpret_cast<uintptr_t>(q.lora_b) & 15) == 0 && q.rank % 8 == 0 &&
+              q.rank * 16 <= 512;
+    p.hf = nullptr;
+    p.w_blocks = static_cast<int>(ceil_div(q.n, 16));
+    p.slot = 0;
+    p.spin = 0;
+    p.err = nullptr;
+    part += static_cast<int64_t>(pl.slices) * m * q.rank;
+    a_total += p.a_blocks;
+    w_total += p.w_blocks;
+    fin_total += ceil_div(q.n, kFinRows);
+  }
+  const dim3 main_grid(static_cast<unsigned>(a_total + w_total));
+  bool launched = false;
+#define RPX_MULTI(NW, CPW)                                                                  \
+  if (!launched && pl.nw == NW && pl.cpw == CPW) {                                          \
+    hipLaunchKernelGGL((k_skinny_main_multi<NW, CPW>), main_grid, dim3(64 * NW), 0, stream, mp); \
+    launched = true;                                                                        \
+  }
+  RPX_MULTI(4, 1) RPX_MULTI(4, 2) RPX_MULTI(4, 4)
+  RPX_MULTI(8, 1) RPX_MULTI(8, 2) RPX_MULTI(8, 4)
+  RPX_MULTI(16, 1) RPX_MULTI(16, 2) RPX_MULTI(16, 4)
+#undef RPX_MULTI
+  if (!launched) return hipErrorInvalidValue;
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const dim3 fin_grid(static_cast<unsigned>(fin_total));
+  switch ((proj[0].rank + 7) / 8) {
+    case 1: hipLaunchKernelGGL(k_skinny_finish_multi<1>, fin_grid, dim3(kFinThreads), 0, stream, mp); break;
+    case 2: hipLaunchKernelGGL(k_skinny_finish_multi<2>, fin_grid, dim3(kFinThreads), 0, stream, mp); break;
+    case 3: hipLaunchKernelGGL(k_skinny_finish_multi<3>, fin_grid, dim3(kFinThreads), 0, stream, mp); break;
+    case 4: hipLaunchKernelGGL(k_skinny_finish_multi<4>, fin_grid, dim3(kFinThreads), 0, stream, mp); break;
+    case 5: hipLaunchKernelGGL(k_skinny_finish_multi<5>, fin_grid, dim3(kFinThreads), 0, stream, mp); break;
+    case 6: hipLaunchKernelGGL(k_skinny_finish_multi<6>, fin_grid, dim3(kFinThreads), 0, stream, mp); break;
+    case 7: hipLaunchKernelGGL(k_skinny_finish_multi<7>, fin_grid, dim3(kFinThreads), 0, stream, mp); break;
+    default: hipLaunchKernelGGL(k_skinny_finish_multi<8>, fin_grid, dim3(kFinThreads), 0, stream, mp); break;
   }
   return hipGetLastError();
 }

@@ -29,7 +29,11 @@ def _fusable(value: torch.Tensor, *linears: QuantizedLoRALinear) -> bool:
         return False
     if active_compute_dtype(value.dtype) != torch.bfloat16:
         return False
-    return all(isinstance(l, QuantizedLoRALinear) and l.packed_weight.ndim == 2 for l in linears)
+    if not all(isinstance(l, QuantizedLoRALinear) and l.packed_weight.ndim == 2 for l in linears):
+        return False
+    # bf16 adapter views; float32 masters without a policy promote the
+    # adapter term to float32 (the module's own path handles that)
+    return all(compute_parameter(l.lora_a).dtype == torch.bfloat16 for l in linears)
 
 
 def _leaves(layer: QuantizedLoRALinear) -> tuple:
@@ -81,6 +85,14 @@ def shared_input_projections(value: torch.Tensor, linears) -> list[torch.Tensor]
     for layer in linears:
         views += list(_views(layer))
         leaves += list(_leaves(layer))
+    if not torch.is_grad_enabled() or not (x.requires_grad or any(v.requires_grad for v in views)):
+        # inference: every projection in one call (one pair of launches for
+        # all of them at small M, where a call is launch-latency bound)
+        x2d = x.reshape(-1, linears[0].input_size)
+        outs = ops.int4lora_forward_multi(
+            x2d, [(l.packed_weight, l.scale_bits, views[2 * i], views[2 * i + 1], l.scaling,
+                   l.group_size, l.bias_bits) for i, l in enumerate(linears)])
+        return [y.reshape(*lead, layer.output_size) for (y, _), layer in zip(outs, linears)]
     outs = ops.Int4LoRASharedInputFn.apply(x.reshape(-1, linears[0].input_size), len(linears),
                                            *views, *leaves)
     return [y.reshape(*lead, layer.output_size) for y, layer in zip(outs, linears)]

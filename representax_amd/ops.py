@@ -269,6 +269,48 @@ def int4lora_forward(x2d, packed, scale_bits, lora_a_c, lora_b_c, *, scaling: fl
     return y, h
 
 
+def int4lora_forward_multi(x2d, projections):
+    """Several INT4 + LoRA projections of one input: ``projections`` is a
+    sequence of ``(packed, scale_bits, lora_a_c, lora_b_c, scaling,
+    group_size, bias_bits)``; returns ``[(y, h), ...]`` as
+    ``int4lora_forward`` gives for each. At small M (bf16, M <= 4, one rank)
+    they run in one pair of launches."""
+
+    projections = list(projections)
+    tensors = [x2d]
+    for p in projections:
+        tensors += [p[0], p[1], p[2], p[3], p[6]]
+    device = _on_device(*tensors)
+    m, k = x2d.shape
+    dt = x2d.dtype
+    code = _dtype_code(dt)
+    x2d = _aligned(x2d)
+    count = len(projections)
+    table = (nat.Int4LoraProjection * count)()
+    keep, outs = [], []
+    for i, (packed, scale_bits, lora_a_c, lora_b_c, scaling, group_size, bias_bits) in enumerate(projections):
+        n = packed.shape[-2]
+        r = lora_a_c.shape[0]
+        a = _aligned(_as(lora_a_c, dt))
+        b = _aligned(_as(lora_b_c, dt))
+        pk = _aligned(packed)
+        sc = _aligned(_u16(scale_bits))
+        bias = None if bias_bits is None else _u16(bias_bits).contiguous()
+        y = torch.empty((m, n), dtype=dt, device=device)
+        h = torch.empty((m, r), dtype=dt, device=device)
+        keep += [a, b, pk, sc, bias]
+        outs.append((y, h))
+        table[i] = nat.Int4LoraProjection(pk.data_ptr(), sc.data_ptr(), n, group_arg(group_size, k),
+                                          _ptr(bias), a.data_ptr(), b.data_ptr(), r,
+                                          float(scaling), y.data_ptr(), h.data_ptr())
+    ws_bytes = nat.query("rpx_int4lora_forward_multi_workspace", m, k, count, table, code)
+    ws = _workspace(ws_bytes, device)
+    nat.call("rpx_int4lora_forward_multi", _ptr(x2d), code, m, k, count, table, _ptr(ws),
+             ws.numel(), _stream(device))
+    del keep
+    return outs
+
+
 def int4lora_backward(grad, x2d, packed, scale_bits, lora_a_c, lora_b_c, h, *, scaling: float,
                       group_size: int | None = None):
     """Return ``(dx [M, K], dA f32 [r, K], dB f32 [N, r])``."""

@@ -1,0 +1,119 @@
+"""Several INT4 + LoRA projections of one input in one call
+(rpx_int4lora_forward_multi) against the oracle and against one call per
+projection (GPU): the fused small-M form for the q / k / v and gate / up
+shapes of the Qwen3-2B tower, the sequential form at larger M and for
+mixed ranks, graph replay, and the inference path of
+``mlp.shared_input_projections``."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import int4 as oint4
+from oracle import lora as olora
+from oracle.codecs import f32_to_bf16_bits
+from representax_amd import mlp, ops
+from tests.helpers import assert_bf16_close, bf16_values, from_dev, rng, to_dev, to_dev_bf16
+
+pytestmark = pytest.mark.gpu
+
+
+def _proj(g, n, k, r, group, bias):
+    w = (g.standard_normal((n, k)) * 0.02).astype(np.float32)
+    packed, scales = oint4.pack_int4(w, group)
+    a = (g.standard_normal((r, k)) * 0.05).astype(np.float32)
+    b = (g.standard_normal((n, r)) * 0.5).astype(np.float32)
+    bias_bits = f32_to_bf16_bits((g.standard_normal(n) * 0.5).astype(np.float32)) if bias else None
+    host = dict(packed=packed, scales=scales, a=a, b=b, bias=bias_bits, alpha=2.0 * r, r=r, group=group)
+    dev = (to_dev(packed), to_dev(scales.view(np.int16)).view(torch.uint16), to_dev_bf16(a),
+           to_dev_bf16(b), 2.0, group,
+           None if bias_bits is None else to_dev(bias_bits.view(np.int16)).view(torch.uint16))
+    return host, dev
+
+
+SHAPES = [
+    pytest.param(2048, [(2048, 32), (1024, 32), (1024, 32)], id="qwen3-qkv"),
+    pytest.param(2048, [(6144, 32), (6144, 32)], id="qwen3-gate-up"),
+    pytest.param(768, [(768, 16), (768, 16), (768, 16)], id="bert-qkv"),
+    pytest.param(512, [(384, 32), (256, 16)], id="mixed-ranks"),
+]
+
+
+@pytest.mark.parametrize("m", [1, 4, 16, 300])
+@pytest.mark.parametrize("k,outs", SHAPES)
+def test_multi_matches_oracle_and_single_calls(m, k, outs):
+    g = rng(600 + m + k + len(outs))
+    projs = [_proj(g, n, k, r, 64, bias=(i % 2 == 0)) for i, (n, r) in enumerate(outs)]
+    x = bf16_values(g.standard_normal((m, k)))
+    xd = to_dev_bf16(x)
+    got = ops.int4lora_forward_multi(xd, [d for _, d in projs])
+    single = [ops.int4lora_forward(xd, d[0], d[1], d[2], d[3], scaling=d[4], group_size=d[5],
+                                   bias_bits=d[6]) for _, d in projs]
+    torch.cuda.synchronize()
+    for (host, _), (y, h), (ys, hs) in zip(projs, got, single):
+        y_o, h_o = olora.lora_forward(x, host["packed"], host["scales"], host["a"], host["b"],
+                                      alpha=host["alpha"], rank=host["r"], bias_bits=host["bias"],
+                                      group_size=host["group"])
+        assert_bf16_close(from_dev(y), y_o, what="y")
+        assert_bf16_close(from_dev(h), h_o, what="h")
+        if m > 4 or len({r for _, r in outs}) > 1:
+            # the sequential form is one call per projection: the same bits
+            assert torch.equal(y, ys) and torch.equal(h, hs)
+
+
+def test_multi_replays_in_a_graph():
+    g = rng(650)
+    projs = [_proj(g, n, 2048, 32, 64, bias=True) for n in (2048, 1024, 1024)]
+    xd = to_dev_bf16(bf16_values(g.standard_normal((1, 2048))))
+    eager = ops.int4lora_forward_multi(xd, [d for _, d in projs])
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        ops.int4lora_forward_multi(xd, [d for _, d in projs])
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = ops.int4lora_forward_multi(xd, [d for _, d in projs])
+    for _ in range(3):
+        for y, h in outs:
+            y.zero_()
+            h.zero_()
+        ops.int4lora_forward_multi(xd, [d for _, d in projs])  # eager work between the replays
+        graph.replay()
+        torch.cuda.synchronize()
+        for (y, h), (ye, he) in zip(outs, eager):
+            assert torch.equal(y, ye) and torch.equal(h, he)
+
+
+def test_shared_input_projections_inference_path():
+    from representax_amd import apply_quantized_lora, precision_context
+    from representax_amd.config import PrecisionConfig
+    from representax_amd.precision import resolve_precision_policy
+
+    from representax_amd import Linear
+
+    arg = dict(scale=0.02, bias=True, device="cuda")
+    layers = torch.nn.ModuleDict({
+        "query": Linear.init(2048, 2048, key=1, **arg),
+        "key": Linear.init(2048, 1024, key=2, **arg),
+        "value": Linear.init(2048, 1024, key=3, **arg),
+    })
+    with torch.no_grad():
+        for layer in layers.values():
+            layer.bias.normal_(0.0, 0.5)
+    model = apply_quantized_lora(layers, rank=32, alpha=64.0, key=0, target_pattern=r".*",
+                                 group_size=64)
+    with torch.no_grad():
+        for layer in model.values():
+            layer.lora_b.normal_(0.0, 0.05)
+    policy = resolve_precision_policy(PrecisionConfig.bfloat16_mixed())
+    x = torch.randn(1, 3, 2048, device="cuda", dtype=torch.bfloat16)
+    with precision_context(policy), torch.no_grad():
+        fused = mlp.shared_input_projections(x, (model["query"], model["key"], model["value"]))
+        separate = [model[name](x) for name in ("query", "key", "value")]
+    torch.cuda.synchronize()
+    for a, b in zip(fused, separate):
+        assert a.shape == b.shape and a.dtype == b.dtype
+        assert_bf16_close(from_dev(a), from_dev(b), what="shared-input inference")
