@@ -8,12 +8,16 @@ and torch's streams and device pointers are valid inside it.
 from __future__ import annotations
 
 import ctypes
+import importlib.machinery
+import importlib.util
 import os
+import sysconfig
 from pathlib import Path
 
 import torch  # noqa: F401  (load torch's HIP runtime before the library)
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "librepresentax_amd.so"
+FAST_PATH = LIB_PATH.parent / ("_rpxfast" + (sysconfig.get_config_var("EXT_SUFFIX") or ".so"))
 
 RPX_OK = 0
 RPX_ERR_INVALID = 1
@@ -177,6 +181,31 @@ def load() -> ctypes.CDLL:
         fn.argtypes = argtypes
     _LIB = lib
     return lib
+
+
+_FAST = None
+
+
+def fast():
+    """The CPython fast-call binding of the small-M forward entry points
+    (``csrc/pyfast.c``), or None where it is not built or the library was
+    loaded from another path (``RPX_LIBRARY``): it links the library in its
+    own directory, and a second copy of the library would not share its
+    state. Callers fall back to the ctypes functions, which reach the same
+    kernels."""
+
+    global _FAST
+    if _FAST is not None:
+        return _FAST or None
+    load()
+    mod = False
+    if FAST_PATH.exists() and Path(os.environ.get("RPX_LIBRARY", LIB_PATH)).resolve() == LIB_PATH:
+        loader = importlib.machinery.ExtensionFileLoader("_rpxfast", str(FAST_PATH))
+        spec = importlib.util.spec_from_file_location("_rpxfast", str(FAST_PATH), loader=loader)
+        mod = importlib.util.module_from_spec(spec)
+        loader.exec_module(mod)
+    _FAST = mod
+    return mod or None
 
 
 def check(status: int) -> None:

@@ -2,7 +2,9 @@
 
 ``python -m representax_amd.build`` compiles every HIP source under
 ``representax_amd/csrc`` in parallel and links them into
-``representax_amd/_lib/librepresentax_amd.so``.
+``representax_amd/_lib/librepresentax_amd.so``, then builds the CPython
+fast-call binding of the small-M forward entry points (``csrc/pyfast.c``)
+next to it.
 """
 
 from __future__ import annotations
@@ -11,6 +13,7 @@ import os
 import shutil
 import subprocess
 import sys
+import sysconfig
 from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
@@ -18,6 +21,7 @@ PACKAGE = Path(__file__).resolve().parent
 CSRC = PACKAGE / "csrc"
 OUT_DIR = PACKAGE / "_lib"
 LIB_NAME = "librepresentax_amd.so"
+FAST_NAME = "_rpxfast" + (sysconfig.get_config_var("EXT_SUFFIX") or ".so")
 ARCH = os.environ.get("RPX_OFFLOAD_ARCH", "gfx950")
 
 COMMON_FLAGS = [
@@ -75,7 +79,27 @@ def build(verbose: bool = False) -> Path:
     if proc.returncode != 0:
         raise RuntimeError(f"link failed:\n{proc.stdout}{proc.stderr}")
     os.replace(tmp, lib)
+    build_fast()
     return lib
+
+
+def build_fast() -> Path:
+    """The CPython binding: plain C, linked against the library in the same
+    directory (rpath $ORIGIN) so both bindings share one loaded instance."""
+
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        raise RuntimeError("no C compiler for the CPython binding")
+    out = OUT_DIR / FAST_NAME
+    tmp = OUT_DIR / (FAST_NAME + ".tmp")
+    cmd = [cc, "-O2", "-std=c11", "-fPIC", "-shared", "-Wall", "-Werror",
+           f"-I{sysconfig.get_paths()['include']}", str(CSRC / "pyfast.c"),
+           f"-L{OUT_DIR}", "-lrepresentax_amd", "-Wl,-rpath,$ORIGIN", "-o", str(tmp)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"building the CPython binding failed:\n{proc.stdout}{proc.stderr}")
+    os.replace(tmp, out)
+    return out
 
 
 if __name__ == "__main__":

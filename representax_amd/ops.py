@@ -51,17 +51,19 @@ def _dtype_code(dtype: torch.dtype) -> int:
 
 def _on_device(*tensors: torch.Tensor | None) -> torch.device:
     device = None
+    index = -1
     for t in tensors:
         if t is None:
             continue
-        if t.device.type != "cuda":
+        if not t.is_cuda:
             raise RuntimeError(
                 "representax_amd kernels run on ROCm devices only; got a tensor on "
                 f"{t.device}"
             )
         if device is None:
             device = t.device
-        elif t.device != device:
+            index = t.get_device()
+        elif t.get_device() != index:
             raise RuntimeError("all operands must be on the same device")
     if device is None:
         raise RuntimeError("no device tensor given")
@@ -260,12 +262,22 @@ def int4lora_forward(x2d, packed, scale_bits, lora_a_c, lora_b_c, *, scaling: fl
     y = torch.empty((m, n), dtype=dt, device=device)
     h = torch.empty((m, r), dtype=dt, device=device)
     g = group_arg(group_size, k)
+    bias = None if bias_bits is None else _u16(bias_bits).contiguous()
+    packed = _aligned(packed)
+    scale_bits = _aligned(_u16(scale_bits))
+    fast = nat.fast()
+    if fast is not None:
+        ws = _workspace(fast.int4lora_forward_workspace(m, n, k, g, r, code), device)
+        nat.check(fast.int4lora_forward(
+            x2d.data_ptr(), code, m, k, packed.data_ptr(), scale_bits.data_ptr(), n, g, _ptr(bias),
+            a.data_ptr(), b.data_ptr(), r, float(scaling), y.data_ptr(), h.data_ptr(),
+            ws.data_ptr(), ws.numel(), _stream(device)))
+        return y, h
     ws_bytes = nat.query("rpx_int4lora_forward_workspace", m, n, k, g, r, code)
     ws = _workspace(ws_bytes, device)
-    bias = None if bias_bits is None else _u16(bias_bits).contiguous()
-    nat.call("rpx_int4lora_forward", _ptr(x2d), code, m, k, _ptr(_aligned(packed)),
-             _ptr(_aligned(_u16(scale_bits))), n, g, _ptr(bias), _ptr(a), _ptr(b), r,
-             float(scaling), _ptr(y), _ptr(h), _ptr(ws), ws.numel(), _stream(device))
+    nat.call("rpx_int4lora_forward", _ptr(x2d), code, m, k, _ptr(packed), _ptr(scale_bits), n, g,
+             _ptr(bias), _ptr(a), _ptr(b), r, float(scaling), _ptr(y), _ptr(h), _ptr(ws),
+             ws.numel(), _stream(device))
     return y, h
 
 
@@ -286,7 +298,9 @@ def int4lora_forward_multi(x2d, projections):
     code = _dtype_code(dt)
     x2d = _aligned(x2d)
     count = len(projections)
-    table = (nat.Int4LoraProjection * count)()
+    fast = nat.fast() if count <= 16 else None
+    table = None if fast is not None else (nat.Int4LoraProjection * count)()
+    flat = []
     keep, outs = [], []
     for i, (packed, scale_bits, lora_a_c, lora_b_c, scaling, group_size, bias_bits) in enumerate(projections):
         n = packed.shape[-2]
@@ -300,13 +314,22 @@ def int4lora_forward_multi(x2d, projections):
         h = torch.empty((m, r), dtype=dt, device=device)
         keep += [a, b, pk, sc, bias]
         outs.append((y, h))
-        table[i] = nat.Int4LoraProjection(pk.data_ptr(), sc.data_ptr(), n, group_arg(group_size, k),
-                                          _ptr(bias), a.data_ptr(), b.data_ptr(), r,
-                                          float(scaling), y.data_ptr(), h.data_ptr())
-    ws_bytes = nat.query("rpx_int4lora_forward_multi_workspace", m, k, count, table, code)
-    ws = _workspace(ws_bytes, device)
-    nat.call("rpx_int4lora_forward_multi", _ptr(x2d), code, m, k, count, table, _ptr(ws),
-             ws.numel(), _stream(device))
+        fields = (pk.data_ptr(), sc.data_ptr(), n, group_arg(group_size, k), _ptr(bias),
+                  a.data_ptr(), b.data_ptr(), r, float(scaling), y.data_ptr(), h.data_ptr())
+        if fast is not None:
+            flat += fields
+        else:
+            table[i] = nat.Int4LoraProjection(*fields)
+    if fast is not None:
+        flat = tuple(flat)
+        ws = _workspace(fast.int4lora_forward_multi_workspace(m, k, flat, code), device)
+        nat.check(fast.int4lora_forward_multi(x2d.data_ptr(), code, m, k, flat, ws.data_ptr(),
+                                              ws.numel(), _stream(device)))
+    else:
+        ws_bytes = nat.query("rpx_int4lora_forward_multi_workspace", m, k, count, table, code)
+        ws = _workspace(ws_bytes, device)
+        nat.call("rpx_int4lora_forward_multi", _ptr(x2d), code, m, k, count, table, _ptr(ws),
+                 ws.numel(), _stream(device))
     del keep
     return outs
 

@@ -129,3 +129,40 @@ def test_fp8_linear_forward_rejects_empty_operands():
         with pytest.raises(ValueError, match="empty operand"):
             nat.call("rpx_fp8_linear_forward", p, nat.DTYPE_BF16, m, k, p, nat.DTYPE_BF16, n, n, 1,
                      p, nat.DTYPE_BF16, p, None, None, p, 1 << 20, None)
+
+
+def test_fast_binding_shares_the_library_and_validates():
+    """The CPython fast-call binding (small-M forward) is built next to the
+    library, sees the same loaded instance (a knob set through ctypes reads
+    back through it), sizes workspaces as the C ABI does, and passes invalid
+    arguments through to the library's own validation."""
+
+    fast = nat.fast()
+    assert fast is not None
+    lib = nat.load()
+    old = lib.rpx_get_tuning(nat.TUNE_GEMM_BAND)
+    try:
+        assert lib.rpx_set_tuning(nat.TUNE_GEMM_BAND, 5) == 0
+        assert fast.get_tuning(nat.TUNE_GEMM_BAND) == 5
+    finally:
+        lib.rpx_set_tuning(nat.TUNE_GEMM_BAND, old)
+    for shape in [(1, 6144, 2048, 64, 32), (4, 2048, 6144, 0, 32), (4096, 3072, 768, 0, 16),
+                  (4, 6, 8, 0, 2)]:
+        assert fast.int4lora_forward_workspace(*shape, nat.DTYPE_BF16) == \
+            lib.rpx_int4lora_forward_workspace(*shape, nat.DTYPE_BF16)
+    p = 16  # never dereferenced: validation fails first
+    with pytest.raises(ValueError, match="rank"):
+        nat.check(fast.int4lora_forward(p, nat.DTYPE_BF16, 2, 8, p, p, 6, 0, None, p, p, 7, 1.0,
+                                        p, p, None, 0, None))
+    with pytest.raises(TypeError):
+        fast.int4lora_forward(p, nat.DTYPE_BF16)
+    with pytest.raises(ValueError):
+        fast.int4lora_forward_multi(p, nat.DTYPE_BF16, 1, 8, (p,) * 10, None, 0, None)
+    proj = (p, p, 6, 0, None, p, p, 7, 1.0, p, p)
+    with pytest.raises(ValueError, match="rank"):
+        nat.check(fast.int4lora_forward_multi(p, nat.DTYPE_BF16, 1, 8, proj * 2, None, 0, None))
+    assert fast.int4lora_forward_multi_workspace(1, 2048, (p, p, 2048, 64, None, p, p, 32, 2.0, p,
+                                                            p) * 3, nat.DTYPE_BF16) == \
+        lib.rpx_int4lora_forward_multi_workspace(
+            1, 2048, 3, (nat.Int4LoraProjection * 3)(*[nat.Int4LoraProjection(
+                p, p, 2048, 64, None, p, p, 32, 2.0, p, p)] * 3), nat.DTYPE_BF16)

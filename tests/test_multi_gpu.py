@@ -117,3 +117,30 @@ def test_shared_input_projections_inference_path():
     for a, b in zip(fused, separate):
         assert a.shape == b.shape and a.dtype == b.dtype
         assert_bf16_close(from_dev(a), from_dev(b), what="shared-input inference")
+
+
+@pytest.mark.parametrize("m", [1, 4, 300])
+def test_fast_binding_equals_ctypes_binding(m, monkeypatch):
+    """The CPython fast-call binding and the ctypes binding reach the same
+    entry points: single and multi-projection forwards give identical bits
+    either way."""
+
+    from representax_amd import _native as nat
+
+    assert nat.fast() is not None
+    g = rng(700 + m)
+    k = 2048
+    projs = [_proj(g, n, k, 32, 64, bias=(i == 0)) for i, n in enumerate((2048, 1024, 1024))]
+    xd = to_dev_bf16(bf16_values(g.standard_normal((m, k))))
+    d = projs[0][1]
+    y_f, h_f = ops.int4lora_forward(xd, d[0], d[1], d[2], d[3], scaling=d[4], group_size=d[5],
+                                    bias_bits=d[6])
+    multi_f = ops.int4lora_forward_multi(xd, [p for _, p in projs])
+    monkeypatch.setattr(nat, "fast", lambda: None)
+    y_c, h_c = ops.int4lora_forward(xd, d[0], d[1], d[2], d[3], scaling=d[4], group_size=d[5],
+                                    bias_bits=d[6])
+    multi_c = ops.int4lora_forward_multi(xd, [p for _, p in projs])
+    torch.cuda.synchronize()
+    assert torch.equal(y_f, y_c) and torch.equal(h_f, h_c)
+    for (a, b), (c, e) in zip(multi_f, multi_c):
+        assert torch.equal(a, c) and torch.equal(b, e)
