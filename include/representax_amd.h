@@ -59,7 +59,9 @@ int rpx_abi_version(void);
  *                        12 256x128 two stages (env RPX_GEMM_TILE)
  *   RPX_TUNE_BF16_TILE   bf16 GEMM tile: 0 planner, 4 256x128, 5 128x128,
  *                        6 64x128, 8 256x256, 9 128x96, 13 256x128 three
- *                        stages (env RPX_GEMM_TILE)
+ *                        stages; for the input gradient read from the packed
+ *                        weight: 14 256x128, 15 128x128, 16 64x128
+ *                        (env RPX_GEMM_TILE)
  *   RPX_TUNE_FP8_TILE    fp8 GEMM tile: 0 planner, 1..11 (env RPX_FP8_TILE)
  *   RPX_TUNE_SKINNY_TILE one-launch skinny tile: 0 planner, 1..14; a nonzero
  *                        value also turns the two-launch form off
@@ -73,6 +75,10 @@ int rpx_abi_version(void);
  *   RPX_TUNE_GEMM_BAND   row-blocks per band of the bf16, INT4 and fp8 GEMMs'
  *                        tile order: 0 planner, 1 (row-major) .. 64
  *                        (env RPX_GEMM_BAND)
+ *   RPX_TUNE_DX_PACKED   INT4 + LoRA input gradient's weight operand: -1
+ *                        planner (a bf16 W_b^T written first), 0 the same,
+ *                        1 the packed weight dequantized inside the GEMM,
+ *                        where the shape allows (env RPX_DX_PACKED)
  * ------------------------------------------------------------------------- */
 #define RPX_TUNE_INT4_TILE 0
 #define RPX_TUNE_BF16_TILE 1
@@ -82,6 +88,7 @@ int rpx_abi_version(void);
 #define RPX_TUNE_SKINNY2_ONE 5
 #define RPX_TUNE_SPIN_LIMIT 6
 #define RPX_TUNE_GEMM_BAND 7
+#define RPX_TUNE_DX_PACKED 8
 
 /* RPX_ERR_INVALID for an unknown knob or value. */
 int rpx_set_tuning(int knob, int value);

@@ -39,6 +39,7 @@ TUNE_SKINNY2 = 4
 TUNE_SKINNY2_ONE = 5
 TUNE_SPIN_LIMIT = 6
 TUNE_GEMM_BAND = 7
+TUNE_DX_PACKED = 8
 
 _p = ctypes.c_void_p
 _i64 = ctypes.c_int64

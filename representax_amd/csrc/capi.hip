@@ -208,13 +208,15 @@ bool knob_value_ok(int knob, int v) {
     case kTuneBf16Tile:
       return v == kTileAuto || v == kTileBf_256x128 || v == kTileBf_128x128 ||
              v == kTileBf_64x128 || v == kTileBf_256x256 || v == kTileBf_128x96 ||
-             v == kTileBf_256x128s3;
+             v == kTileBf_256x128s3 || v == kTileT4_256x128 || v == kTileT4_128x128 ||
+             v == kTileT4_64x128;
     case kTuneFp8Tile: return v >= 0 && v < fp8_tile_count();
     case kTuneSkinnyTile: return v >= 0 && v <= skinny_tile_count();
     case kTuneSkinny2:
     case kTuneSkinny2One: return v >= -1 && v <= 1;
     case kTuneSpinLimit: return v >= 0;
     case kTuneBand: return v >= 0 && v <= 64;
+    case kTuneDxPacked: return v >= -1 && v <= 1;
     default: return false;
   }
 }
@@ -227,7 +229,7 @@ int env_int(const char* name, int fallback) {
 struct Knobs {
   std::atomic<int> v[kTuneCount];
   Knobs() {
-    const int defaults[kTuneCount] = {0, 0, 0, 0, -1, -1, 0, 0};
+    const int defaults[kTuneCount] = {0, 0, 0, 0, -1, -1, 0, 0, -1};
     for (int i = 0; i < kTuneCount; ++i) v[i].store(defaults[i], std::memory_order_relaxed);
     // RPX_GEMM_TILE names a tile of either GEMM (the id sets are disjoint)
     const int gemm = env_int("RPX_GEMM_TILE", 0);
@@ -237,7 +239,8 @@ struct Knobs {
                                                 {kTuneSkinnyTile, "RPX_SKINNY_TILE"},
                                                 {kTuneSkinny2, "RPX_SKINNY2"},
                                                 {kTuneSkinny2One, "RPX_SKINNY2_ONE"},
-                                                {kTuneBand, "RPX_GEMM_BAND"}};
+                                                {kTuneBand, "RPX_GEMM_BAND"},
+                                                {kTuneDxPacked, "RPX_DX_PACKED"}};
     for (const auto& e : envs) {
       const int val = env_int(e.second, v[e.first].load());
       if (knob_value_ok(e.first, val)) v[e.first].store(val);
@@ -765,11 +768,15 @@ int int4lora_backward_impl(const void* grad, const void* x, int dtype, int64_t m
     float* part_a = arena.take<float>(rank_tn_workspace_floats(m, rank, k));
     if (arena.overflow) return fail_invalid("rpx_int4lora_backward: workspace too small");
     // B^T [r, N] so that dh = g_a . B is an NT product; A^T [K, r] for the
-    // dx epilogue's contiguous fragment loads; W_b^T [K, N] for dx
-    const bool prep_fused = g % 32 == 0;
+    // dx epilogue's contiguous fragment loads; W_b^T [K, N] for dx unless dx
+    // reads the packed weight itself (its own GEMM operand form, on request:
+    // the planner keeps W_b^T, which measured faster on every train-step
+    // shape)
+    const bool dx_packed = tune(kTuneDxPacked) == 1 && int4t_gemm_ok(m, k, n, n, gb, w);
+    const bool prep_fused = g % 32 == 0 || dx_packed;
     if (prep_fused) {
-      RPX_HIP(launch_int4lora_bwd_prep(bb, bt, ab, at, packed, scale_bits, wt, n, k, rank, pc, ng, g,
-                                       st),
+      RPX_HIP(launch_int4lora_bwd_prep(bb, bt, ab, at, packed, scale_bits, dx_packed ? nullptr : wt,
+                                       n, k, rank, pc, ng, g, st),
               "int4lora_backward: B^T, A^T, W_b^T");
     } else {
       RPX_HIP(launch_transpose_bf16(bb, n, rank, rank, bt, n, st), "int4lora_backward: B^T");
@@ -800,8 +807,12 @@ int int4lora_backward_impl(const void* grad, const void* x, int dtype, int64_t m
     epi.aux = act.aux;
     epi.aux2 = act.aux2;
     epi.out2 = act.out2;
-    RPX_HIP(launch_gemm_bf16(gb, n, wt, n, m, k, n, static_cast<uint16_t*>(dx), k, epi, st),
-            "int4lora_backward: dx");
+    if (dx_packed)
+      RPX_HIP(launch_gemm_int4t(gb, n, w, m, k, n, static_cast<uint16_t*>(dx), k, epi, st),
+              "int4lora_backward: dx from the packed weight");
+    else
+      RPX_HIP(launch_gemm_bf16(gb, n, wt, n, m, k, n, static_cast<uint16_t*>(dx), k, epi, st),
+              "int4lora_backward: dx");
     return kOk;
   }
   const size_t es = elem_size(dtype);

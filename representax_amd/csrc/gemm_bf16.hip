@@ -10,6 +10,21 @@
 // (the same permutation for both operands), so one 16-byte LDS read per
 // packed B fragment serves the whole slice.
 //
+// A third B form serves the input gradient of the INT4 + LoRA linear,
+// dx = g . W_b: B[n, k] = W_b[k, n], read straight from the packed weight
+// ([K rows, N / 2 bytes], the reduction running over packed rows). Each
+// 64-row slice of packed bytes and its scales land in LDS by DMA one slice
+// ahead of A; during the previous slice the workgroup dequantizes it once,
+// bf16(q * s) as above, into a bf16 [64 k][BN n] buffer, and the MFMA
+// fragments come from that buffer through transposing LDS reads
+// (ds_read_b64_tr_b16). No bf16 copy of W_b^T is written to memory. It is
+// bit-identical to the bf16 W_b^T form but slower (the INT4 + LoRA backward
+// at 16384 x 2048 <- 6144: 790 against 535 us; at 4096 x 768 <- 3072: 90
+// against 62 us): the dequantized slice's LDS stores, its scale and packed
+// reads and two transposing reads per fragment about double the LDS
+// instructions per slice of a loop whose LDS traffic is already close to its
+// MFMA time. The backward uses it only on request (RPX_DX_PACKED=1).
+//
 // Accumulator orientation: the MFMA's first operand is the B (weight) row
 // fragment, so lane l of a 32x32 block owns output row m = l % 32 and the
 // registers v = 0..15 hold output columns n = 8*(v/4) + 4*(l/32) + v%4,
@@ -85,12 +100,35 @@ __device__ __forceinline__ void round2(float& a, float& b) {
 // is conflict-free.
 __device__ __forceinline__ int pswz(int row) { return (row >> 3) & 1; }
 
-template <int BM, int BN, int WM, int WN, int NS, int WPE, bool INT4, int JB, int ACT>
+// B operand forms of k_gemm_nt.
+constexpr int kBBf16 = 0;   // bf16 rows [N, K]
+constexpr int kBInt4 = 1;   // packed INT4 rows [N, K / 2] (the forward)
+constexpr int kBInt4T = 2;  // packed INT4 [K, N / 2], B[n, k] = W_b[k, n] (dx)
+
+// One direct-to-LDS load of 4 bytes per lane: lane l writes dst + 4 l.
+__device__ __forceinline__ void dma_dword(uint8_t* dst, const uint8_t* src) {
+  __builtin_amdgcn_global_load_lds(src, reinterpret_cast<lds_void_t*>(reinterpret_cast<uintptr_t>(dst)),
+                                   4, 0, 0);
+}
+
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+typedef short i16x8_t __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
+
+// kBInt4T's bf16 slice buffer: 64 rows (k) of BN columns (n), 16-bit
+// elements, rows of 2 BN bytes whose 64-byte blocks are XOR-swizzled by the
+// row's low two bits, so the four rows of a transposing read (64 contiguous
+// bytes each for a 32-lane half) fall on distinct banks.
+__device__ __forceinline__ int t4_off(int row, int byte) { return row * 256 + (byte ^ ((row & 3) << 6)); }
+
+template <int BM, int BN, int WM, int WN, int NS, int WPE, int BK, int JB, int ACT>
 __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
     k_gemm_nt(const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ B,
               int64_t ldb, Int4Operand w, int group_shift, int64_t M, int64_t N, int64_t K,
               uint16_t* __restrict__ out, int64_t ldc, LowRankEpilogue epi, int tiles_m,
               int tiles_n, int band) {
+  constexpr bool INT4 = BK == kBInt4;
+  constexpr bool T4 = BK == kBInt4T;
   constexpr int NW = WM * WN;
   constexpr int NT = 64 * NW;
   constexpr int TM = BM / WM;
@@ -100,13 +138,24 @@ __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_
   static_assert(TM % 32 == 0 && TN % 32 == 0, "wave tile must be made of 32x32 blocks");
   constexpr int A_BYTES = BM * 128;
   constexpr int B_ROW = INT4 ? 32 : 128;
-  constexpr int STAGE = A_BYTES + BN * B_ROW;
+  // kBInt4T: the stages hold A only; packed slices (64 rows of BN / 2 bytes)
+  // and their scales (one dword per row) rotate through NS + 1 stages of
+  // their own, one slice ahead of A, and two bf16 slice buffers follow
+  constexpr int STAGE = T4 ? A_BYTES : A_BYTES + BN * B_ROW;
+  constexpr int P_BYTES = T4 ? 64 * (BN / 2) : 0;
+  constexpr int P_SEGS = P_BYTES / 1024;
   constexpr int A_SEGS = BM / 8;
-  constexpr int SEGS = A_SEGS + BN * B_ROW / 1024;
-  static_assert((BN * B_ROW) % 1024 == 0 && SEGS % NW == 0, "DMA segments must split evenly");
-  constexpr int LPW = SEGS / NW;
-  static_assert(NS >= 2 && NS <= 4 && LPW * (NS - 1) < 64, "vmcnt range");
+  // kBInt4T slots: A segments, packed segments, then the scale load (slots
+  // past it repeat the scale load, which rewrites the same bytes)
+  constexpr int SEGS = T4 ? A_SEGS + P_SEGS + 1 : A_SEGS + BN * B_ROW / 1024;
+  static_assert(T4 || ((BN * B_ROW) % 1024 == 0 && SEGS % NW == 0), "DMA segments must split evenly");
+  static_assert(!T4 || (BN == 128 && BM % 64 == 0), "kBInt4T: 128-column tiles");
+  constexpr int LPW = (SEGS + NW - 1) / NW;
+  static_assert(NS >= 2 && NS <= 4 && LPW * NS < 64, "vmcnt range");
   extern __shared__ __align__(16) uint8_t smem[];
+  uint8_t* const t4_p = smem + NS * STAGE;             // packed stages
+  uint8_t* const t4_s = t4_p + (NS + 1) * P_BYTES;     // scale stages, 256 bytes each
+  uint8_t* const t4_b = t4_s + (NS + 1) * 256;         // two bf16 slices of 64 x 256 bytes
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -152,6 +201,19 @@ __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_
       int64_t r = m0 + trow;
       r = r < M ? r : M - 1;
       src[i] = reinterpret_cast<const uint8_t*>(A + r * lda) + (((lane & 7) ^ swz(trow)) << 4);
+    } else if constexpr (T4) {
+      if (j < A_SEGS + P_SEGS) {
+        // packed rows 16 p + lane / 4 of the slice, 16 bytes each of the
+        // tile's BN / 2
+        const int trow = 16 * (j - A_SEGS) + (lane >> 2);
+        src[i] = w.packed + trow * w.packed_cols + n0 / 2 + ((lane & 3) << 4);
+      } else if (w.n_groups == 1) {
+        // per-row scales: lane l loads the dword holding rows l & ~1, l | 1
+        src[i] = reinterpret_cast<const uint8_t*>(w.scales + (lane & ~1));
+      } else {
+        // 64-column groups: lane l loads row l's two groups of the tile
+        src[i] = reinterpret_cast<const uint8_t*>(w.scales + lane * w.n_groups + n0 / 64);
+      }
     } else if constexpr (INT4) {
       const int trow = 32 * (j - A_SEGS) + (lane >> 1);
       int64_t r = n0 + trow;
@@ -167,8 +229,23 @@ __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_
   // byte offset of slice s in the source rows
   auto koff = [&](int s, int i) -> int64_t {
     const int j = wave + i * NW;
+    if constexpr (T4) {
+      if (j >= A_SEGS + P_SEGS) return static_cast<int64_t>(s) * kBK * w.n_groups * 2;
+      if (j >= A_SEGS) return static_cast<int64_t>(s) * kBK * w.packed_cols;
+    }
     return (INT4 && j >= A_SEGS) ? static_cast<int64_t>(s) * (kBK / 2)
                                  : static_cast<int64_t>(s) * (kBK * 2);
+  };
+  // kBInt4T: slot i's load of A slice `as` into A stage `ast`, or of packed
+  // (or scale) slice `ps` into stage `pst` of its own
+  auto dma_t4 = [&](int i, int ast, int as, int pst, int ps) {
+    const int j = wave + i * NW;
+    if (j < A_SEGS)
+      dma_seg(smem + ast * STAGE, src[i], koff(as, i), j);
+    else if (j < A_SEGS + P_SEGS)
+      dma_seg(t4_p + pst * P_BYTES, src[i], koff(ps, i), j - A_SEGS);
+    else
+      dma_dword(t4_s + pst * 256, src[i] + koff(ps, i));
   };
 
   f32x16_t acc[FN][FM];
@@ -196,6 +273,97 @@ __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_
 #pragma unroll
     for (int fn = 0; fn < FN; ++fn)
       bfr[buf][fn] = as_bf16x8(lds_chunk(st + A_BYTES, wn * TN + fn * 32 + frow, 4 * half + kk));
+  };
+  // kBInt4T: B fragments of step kk from a bf16 slice buffer through
+  // transposing reads. Lane l needs B[n][k] for its row n = l % 32 of the
+  // 32-column block and the 8 k of step kk in its half (32 half + 8 kk +
+  // [0, 8), the order A uses); ds_read_b64_tr_b16 hands lane i of a 16-lane
+  // group element i % 4 of the 8-byte pieces that lanes 4 e + i / 4 address,
+  // so lane j addresses row 8 kk + 32 half + j / 4 (then + 4) at columns
+  // 4 (j % 4) of its 16-column half, and lane i receives 4 consecutive k of
+  // column i.
+  auto read_bt = [&](const uint8_t* bt, int kk, int buf) {
+    const int j = lane & 15;
+    const int row = 32 * half + 8 * kk + (j >> 2);
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn) {
+      const int col = wn * TN + fn * 32 + 16 * ((lane >> 4) & 1) + 4 * (j & 3);
+      const i16x4_t lo =
+          __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(bt + t4_off(row, 2 * col)));
+      const i16x4_t hi =
+          __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(bt + t4_off(row + 4, 2 * col)));
+      bfr[buf][fn] =
+          __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+    }
+  };
+  // kBInt4T dequantization of a packed slice into a bf16 slice buffer, once
+  // per workgroup: item q = tid + it * NT is packed row q / 8 of the slice
+  // and its 16 columns 16 (q % 8). t4_read loads every item's 8 packed bytes
+  // and scale, t4_pair(u) turns column pair u % 8 of item u / 8 into bf16,
+  // t4_write stores the items' 32-byte row pieces (odd rows write their
+  // second 16 bytes first, which spreads a 16-lane store over all banks).
+  constexpr int T4_IPT = T4 ? 64 * (BN / 16) / NT : 1;
+  static_assert(!T4 || (64 * (BN / 16)) % NT == 0, "kBInt4T items must split evenly");
+  uint32_t t4_raw[T4_IPT][2];
+  float t4_sc[T4_IPT];
+  uint32_t t4_out[T4_IPT][8];
+  auto t4_read = [&](int pst) {
+#pragma unroll
+    for (int it = 0; it < T4_IPT; ++it) {
+      const int q = tid + it * NT;
+      const int r = q >> 3;
+      const int c = (q & 7) * 16;
+      const u32x2_t v = *reinterpret_cast<const u32x2_t*>(t4_p + pst * P_BYTES + r * (BN / 2) + c / 2);
+      t4_raw[it][0] = v[0];
+      t4_raw[it][1] = v[1];
+      const uint16_t* s16 = reinterpret_cast<const uint16_t*>(t4_s + pst * 256);
+      t4_sc[it] = bf16_to_f32(s16[2 * r + (w.n_groups == 1 ? (r & 1) : (c >> 6))]);
+    }
+  };
+  auto t4_pair = [&](int u) {
+    const int it = u / 8;
+    const int pr = u % 8;
+    const uint32_t x = t4_raw[it][pr / 4] ^ 0x88888888u;
+    uint32_t lo = x & 0x0F0F0F0Fu;
+    uint32_t hi = (x >> 4) & 0x0F0F0F0Fu;
+    asm("" : "+v"(lo), "+v"(hi));
+    const float sv = t4_sc[it];
+    const float m8s = -8.0f * sv;
+    uint32_t r;
+    switch (pr % 4) {
+      case 0: r = dequant_pair<0>(lo, hi, sv, m8s); break;
+      case 1: r = dequant_pair<1>(lo, hi, sv, m8s); break;
+      case 2: r = dequant_pair<2>(lo, hi, sv, m8s); break;
+      default: r = dequant_pair<3>(lo, hi, sv, m8s); break;
+    }
+    t4_out[it][pr] = r;
+  };
+  auto t4_write = [&](int bi) {
+    uint8_t* bt = t4_b + bi * (64 * 256);
+#pragma unroll
+    for (int it = 0; it < T4_IPT; ++it) {
+      const int q = tid + it * NT;
+      const int r = q >> 3;
+      const int c = (q & 7) * 16;
+      const u32x4_t lo4{t4_out[it][0], t4_out[it][1], t4_out[it][2], t4_out[it][3]};
+      const u32x4_t hi4{t4_out[it][4], t4_out[it][5], t4_out[it][6], t4_out[it][7]};
+      const bool odd = (r & 1) != 0;
+      *reinterpret_cast<u32x4_t*>(bt + t4_off(r, 2 * c + (odd ? 16 : 0))) = odd ? hi4 : lo4;
+      *reinterpret_cast<u32x4_t*>(bt + t4_off(r, 2 * c + (odd ? 0 : 16))) = odd ? lo4 : hi4;
+    }
+  };
+  // slot gs (0 .. 3 NS1 - 1) of steps 0-2: the next slice's dequantization,
+  // read first, pairs spread over the middle slots, stores last
+  auto t4_slot = [&](int gs, int pst, int bi) {
+    constexpr int SL = 3 * FM * FN;
+    constexpr int U = 8 * T4_IPT;
+    constexpr int F = SL >= 4 ? 2 : 1;
+    if (gs == 0) t4_read(pst);
+    if (gs >= F && gs < SL - 1) {
+#pragma unroll
+      for (int u = (gs - F) * U / (SL - 1 - F); u < (gs - F + 1) * U / (SL - 1 - F); ++u) t4_pair(u);
+    }
+    if (gs == SL - 1) t4_write(bi);
   };
   auto read_bp = [&](const uint8_t* st) {
 #pragma unroll
@@ -244,11 +412,25 @@ __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_
 
   // prologue: NS slices in flight (refills past the end re-read the last
   // slice into a stage nothing reads again: LPW loads per slice always)
-#pragma unroll
-  for (int s = 0; s < NS; ++s)
+  if constexpr (T4) {
+    // packed slice 0 and its scales first, then A slice s with packed
+    // slice s + 1 (the loop's grouping); vmcnt counts the groups from the
+    // newest, so the extra first load needs no count of its own
 #pragma unroll
     for (int i = 0; i < LPW; ++i)
-      dma_seg(smem + s * STAGE, src[i], koff(s < nk ? s : nk - 1, i), wave + i * NW);
+      if (wave + i * NW >= A_SEGS) dma_t4(i, 0, 0, 0, 0);
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+#pragma unroll
+      for (int i = 0; i < LPW; ++i)
+        dma_t4(i, s, s < nk ? s : nk - 1, (s + 1) % (NS + 1), s + 1 < nk ? s + 1 : nk - 1);
+  } else {
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+#pragma unroll
+      for (int i = 0; i < LPW; ++i)
+        dma_seg(smem + s * STAGE, src[i], koff(s < nk ? s : nk - 1, i), wave + i * NW);
+  }
   if constexpr (INT4) {
 #pragma unroll
     for (int c = 0; c < SC_CAP; ++c) {
@@ -260,8 +442,18 @@ __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_
     for (int i = 8 * sc_vecs + tid; i < sc_total; i += NT) sc[i] = w.scales[n0 * ng + i];
   }
   wait_sync<(NS - 1) * LPW>();
+  if constexpr (T4) {
+    // slice 0 dequantized before the loop, visible to every wave
+    t4_read(0);
+#pragma unroll
+    for (int u = 0; u < 8 * T4_IPT; ++u) t4_pair(u);
+    t4_write(0);
+    wait_sync<(NS - 1) * LPW>();
+  }
   read_a(smem, 0, 0);
-  if constexpr (INT4) {
+  if constexpr (T4) {
+    read_bt(t4_b, 0, 0);
+  } else if constexpr (INT4) {
     read_bp(smem);
     read_bs(0);
 #pragma unroll
@@ -316,6 +508,10 @@ __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_
     auto slice = [&](int t) {
       const int next = stage + 1 == NS ? 0 : stage + 1;
       const uint8_t* st = smem + stage * STAGE;
+      // kBInt4T: bf16 buffers of slices t and t + 1, packed stage of t + 1
+      [[maybe_unused]] const uint8_t* bt_cur = t4_b + (t & 1) * (64 * 256);
+      [[maybe_unused]] const uint8_t* bt_next = t4_b + ((t + 1) & 1) * (64 * 256);
+      [[maybe_unused]] const int p_next = (t + 1) % (NS + 1);
       __builtin_amdgcn_sched_barrier(0);
   #pragma unroll
       for (int kk = 0; kk < 3; ++kk) {
@@ -327,6 +523,9 @@ __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_
           if constexpr (INT4) {
   #pragma unroll
             for (int u = i * NU / NS1; u < (i + 1) * NU / NS1; ++u) dq_unit(kk + 1, u);
+          } else if constexpr (T4) {
+            if (i == NS1 / 2) read_bt(bt_cur, kk + 1, (kk + 1) & 1);
+            t4_slot(kk * NS1 + i, p_next, (t + 1) & 1);
           } else {
             if (i == NS1 / 2) read_b(st, kk + 1, (kk + 1) & 1);
           }
@@ -345,7 +544,10 @@ __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_
         __builtin_amdgcn_sched_barrier(0);
   #pragma unroll
         for (int d = i * LPW / NS1; d < (i + 1) * LPW / NS1; ++d)
-          dma_seg(fill, src[d], koff(refill, d), wave + d * NW);
+          if constexpr (T4)
+            dma_t4(d, stage, refill, t % (NS + 1), t + NS + 1 < nk ? t + NS + 1 : nk - 1);
+          else
+            dma_seg(fill, src[d], koff(refill, d), wave + d * NW);
         if constexpr (INT4) {
           if (i == 0) {
             read_bp(nst);
@@ -359,7 +561,11 @@ __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_
           }
         } else {
           if (i == 0) read_a(nst, 0, 0);
-          if (i == NS1 / 2) read_b(nst, 0, 0);
+          if constexpr (T4) {
+            if (i == NS1 / 2) read_bt(bt_next, 0, 0);
+          } else {
+            if (i == NS1 / 2) read_b(nst, 0, 0);
+          }
         }
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -372,6 +578,10 @@ __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_
     for (int t = 0; t < nk; ++t) {
       const int next = stage + 1 == NS ? 0 : stage + 1;
       const uint8_t* st = smem + stage * STAGE;
+      // kBInt4T: bf16 buffers of slices t and t + 1, packed stage of t + 1
+      [[maybe_unused]] const uint8_t* bt_cur = t4_b + (t & 1) * (64 * 256);
+      [[maybe_unused]] const uint8_t* bt_next = t4_b + ((t + 1) & 1) * (64 * 256);
+      [[maybe_unused]] const int p_next = (t + 1) % (NS + 1);
       __builtin_amdgcn_sched_barrier(0);
   #pragma unroll
       for (int kk = 0; kk < 3; ++kk) {
@@ -383,6 +593,9 @@ __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_
           if constexpr (INT4) {
   #pragma unroll
             for (int u = i * NU / NS1; u < (i + 1) * NU / NS1; ++u) dq_unit(kk + 1, u);
+          } else if constexpr (T4) {
+            if (i == NS1 / 2) read_bt(bt_cur, kk + 1, (kk + 1) & 1);
+            t4_slot(kk * NS1 + i, p_next, (t + 1) & 1);
           } else {
             if (i == NS1 / 2) read_b(st, kk + 1, (kk + 1) & 1);
           }
@@ -401,7 +614,10 @@ __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_
         __builtin_amdgcn_sched_barrier(0);
   #pragma unroll
         for (int d = i * LPW / NS1; d < (i + 1) * LPW / NS1; ++d)
-          dma_seg(fill, src[d], koff(refill, d), wave + d * NW);
+          if constexpr (T4)
+            dma_t4(d, stage, refill, t % (NS + 1), t + NS + 1 < nk ? t + NS + 1 : nk - 1);
+          else
+            dma_seg(fill, src[d], koff(refill, d), wave + d * NW);
         if constexpr (INT4) {
           if (i == 0) {
             read_bp(nst);
@@ -415,7 +631,11 @@ __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_
           }
         } else {
           if (i == 0) read_a(nst, 0, 0);
-          if (i == NS1 / 2) read_b(nst, 0, 0);
+          if constexpr (T4) {
+            if (i == NS1 / 2) read_bt(bt_next, 0, 0);
+          } else {
+            if (i == NS1 / 2) read_b(nst, 0, 0);
+          }
         }
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -681,27 +901,71 @@ constexpr int gemm_lds_bytes(int bm, int bn, int ns, bool int4) {
   return ns * (bm * 128 + bn * (int4 ? 32 : 128));
 }
 
-// Rows per band of the banded tile order: the tuning knob's value, else 1
-// (row-major). Row-major order makes each XCD re-read B once per A
-// row-block (1.8 GB of L2 misses for the 16384 x 6144 x 2048 input-gradient
-// GEMM against 92 MB of operands), yet bands of 2-16 measured within
-// run-to-run noise of it on every train-step shape: the re-reads presumably
-// hit the 256 MB Infinity Cache, which holds these operands.
-int tile_band(int tiles_m) {
-  const int band = tune(kTuneBand) > 0 ? tune(kTuneBand) : 1;
-  return band < tiles_m ? band : (tiles_m > 0 ? tiles_m : 1);
+// kBInt4T (BN = 128): A stages, NS + 1 packed stages of 4 KB and scale
+// stages of 256 bytes, two bf16 slices of 16 KB
+constexpr int gemm_lds_bytes_t4(int bm, int ns) {
+  return ns * bm * 128 + (ns + 1) * (64 * 64 + 256) + 2 * 64 * 256;
 }
 
-template <int BM, int BN, int WM, int WN, int NS, int WPE, bool INT4, int JB, int ACT>
+// The kTuneBand knob's band (at most tiles_m rows) when it is set, else
+// `otherwise`.
+int forced_band(int tiles_m, int otherwise) {
+  const int forced = tune(kTuneBand);
+  if (forced <= 0) return otherwise;
+  return forced < tiles_m ? forced : (tiles_m > 0 ? tiles_m : 1);
+}
+
+// Rows per band of the banded tile order (band_tile). An XCD runs its tiles
+// `resident` at a time (32 CUs x workgroups per CU); with b-row bands such a
+// set spans about `rows` A row-blocks and `cols` B column-blocks, which it
+// streams through the XCD's L2 at rows * a_bytes + cols * b_bytes per unit
+// of K (BM or BN rows times the operand's bytes per element). b minimizes
+// that (ties keep the smaller b; b = 1 is row-major order). Measured on the
+// bf16 input-gradient GEMMs alone (two runs each, alternating): 16384 x 2048
+// <- 6144 344-349 -> 319-323 us, 16384 x 6144 <- 2048 395-402 -> 378-382 us,
+// 32768 x 3072 <- 768 163-164 -> 154-159 us, while 768-wide outputs, whose
+// row-major sets already span ~10 row blocks, are unchanged. The kTuneBand
+// knob forces a band.
+int gemm_band(int tiles_m, int tiles_n, int64_t resident, int64_t a_bytes, int64_t b_bytes) {
+  if (tune(kTuneBand) > 0) return forced_band(tiles_m, 1);
+  const int64_t per_xcd = ceil_div(static_cast<int64_t>(tiles_m) * tiles_n, 8);
+  const int64_t t = resident < per_xcd ? resident : per_xcd;
+  int best = 1;
+  int64_t best_cost = -1;
+  for (int b = 1; b <= tiles_m && b <= 64; ++b) {
+    const int64_t band_tiles = static_cast<int64_t>(b) * tiles_n;
+    int64_t rows, cols;
+    if (t <= band_tiles) {
+      rows = t < b ? t : b;
+      cols = ceil_div(t, b);
+    } else {
+      const int64_t full = t / band_tiles;
+      const int64_t rem = t - full * band_tiles;
+      rows = full * b + (rem < b ? rem : b);
+      cols = tiles_n;
+    }
+    const int64_t cost = rows * a_bytes + cols * b_bytes;
+    if (best_cost < 0 || cost < best_cost) {
+      best_cost = cost;
+      best = b;
+    }
+  }
+  return best;
+}
+
+template <int BM, int BN, int WM, int WN, int NS, int WPE, int BK, int JB, int ACT>
 hipError_t run_gemm_act(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb,
                         const Int4Operand& w, int64_t m, int64_t n, int64_t k, uint16_t* out,
                         int64_t ldc, const LowRankEpilogue& epi, hipStream_t stream) {
+  constexpr bool INT4 = BK == kBInt4;
+  constexpr bool T4 = BK == kBInt4T;
   const int tiles_m = static_cast<int>(ceil_div(m, BM));
   const int tiles_n = static_cast<int>(ceil_div(n, BN));
   const size_t scale_bytes = INT4 ? static_cast<size_t>(BN) * w.n_groups * 2 : 0;
-  const size_t lds = gemm_lds_bytes(BM, BN, NS, INT4) + ((scale_bytes + 15) & ~size_t{15});
+  const size_t lds = T4 ? static_cast<size_t>(gemm_lds_bytes_t4(BM, NS))
+                        : gemm_lds_bytes(BM, BN, NS, INT4) + ((scale_bytes + 15) & ~size_t{15});
   if (lds > 160 * 1024) return hipErrorInvalidValue;
-  auto kern = k_gemm_nt<BM, BN, WM, WN, NS, WPE, INT4, JB, ACT>;
+  auto kern = k_gemm_nt<BM, BN, WM, WN, NS, WPE, BK, JB, ACT>;
   static std::atomic<unsigned> lds_set{0};
   hipError_t e = ensure_lds_limit(reinterpret_cast<const void*>(kern), 160 * 1024, lds_set);
   if (e != hipSuccess) return e;
@@ -709,7 +973,17 @@ hipError_t run_gemm_act(const uint16_t* a, int64_t lda, const uint16_t* b, int64
   if (INT4 && w.n_groups > 1) {
     while ((int64_t{1} << group_shift) < w.group) ++group_shift;
   }
-  const int band = tile_band(tiles_m);
+  // workgroups per CU: waves per SIMD (WPE) x 4 SIMDs over the block's
+  // waves, or fewer when LDS runs out
+  int64_t per_cu = (4 * WPE) / (WM * WN);
+  if (per_cu * static_cast<int64_t>(lds) > 160 * 1024) per_cu = (160 * 1024) / static_cast<int64_t>(lds);
+  if (per_cu < 1) per_cu = 1;
+  // bf16 operands on both sides. The INT4 GEMMs keep row-major order (a
+  // forced band aside): their packed B is a quarter of the bytes, and bands
+  // measured within run-to-run noise of row-major on every train-step shape.
+  const int band = INT4 || T4 ? forced_band(tiles_m, 1)
+                        : gemm_band(tiles_m, tiles_n, 32 * per_cu, int64_t{2} * BM,
+                                    int64_t{2} * BN);
   hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(tiles_m) * tiles_n), dim3(64 * WM * WN),
                      lds, stream, a, lda, b, ldb, w, group_shift, m, n, k, out, ldc, epi, tiles_m,
                      tiles_n, band);
@@ -719,15 +993,15 @@ hipError_t run_gemm_act(const uint16_t* a, int64_t lda, const uint16_t* b, int64
 // Activation epilogues: the forward modes on the INT4 GEMM (the FFN's up
 // projection), the backward modes on the bf16 dx GEMM (the down projection's
 // input gradient), for the default tile shapes.
-template <int BM, int BN, int WM, int WN, int NS, int WPE, bool INT4, int JB>
+template <int BM, int BN, int WM, int WN, int NS, int WPE, int BK, int JB>
 hipError_t run_gemm_jb(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb,
                        const Int4Operand& w, int64_t m, int64_t n, int64_t k, uint16_t* out,
                        int64_t ldc, const LowRankEpilogue& epi, hipStream_t stream) {
 #define RPX_RUN_ACT(ACT) \
-  run_gemm_act<BM, BN, WM, WN, NS, WPE, INT4, JB, ACT>(a, lda, b, ldb, w, m, n, k, out, ldc, epi, stream)
+  run_gemm_act<BM, BN, WM, WN, NS, WPE, BK, JB, ACT>(a, lda, b, ldb, w, m, n, k, out, ldc, epi, stream)
   if (epi.act == kActNone) return RPX_RUN_ACT(kActNone);
   if constexpr (JB > 0 && !(BM == 256 && BN == 256)) {
-    if constexpr (INT4) {
+    if constexpr (BK == kBInt4) {
       if (epi.act == kActGeluFwd) return RPX_RUN_ACT(kActGeluFwd);
       if (epi.act == kActSiluMulFwd) return RPX_RUN_ACT(kActSiluMulFwd);
     } else {
@@ -740,20 +1014,20 @@ hipError_t run_gemm_jb(const uint16_t* a, int64_t lda, const uint16_t* b, int64_
   return hipErrorInvalidValue;
 }
 
-template <int BM, int BN, int WM, int WN, int NS, int WPE, bool INT4>
+template <int BM, int BN, int WM, int WN, int NS, int WPE, int BK>
 hipError_t run_gemm(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb,
                     const Int4Operand& w, int64_t m, int64_t n, int64_t k, uint16_t* out,
                     int64_t ldc, const LowRankEpilogue& epi, hipStream_t stream) {
   if (epi.rank <= 0)
-    return run_gemm_jb<BM, BN, WM, WN, NS, WPE, INT4, 0>(a, lda, b, ldb, w, m, n, k, out, ldc,
+    return run_gemm_jb<BM, BN, WM, WN, NS, WPE, BK, 0>(a, lda, b, ldb, w, m, n, k, out, ldc,
                                                          epi, stream);
   if (epi.rank <= 16)
-    return run_gemm_jb<BM, BN, WM, WN, NS, WPE, INT4, 1>(a, lda, b, ldb, w, m, n, k, out, ldc,
+    return run_gemm_jb<BM, BN, WM, WN, NS, WPE, BK, 1>(a, lda, b, ldb, w, m, n, k, out, ldc,
                                                          epi, stream);
   if (epi.rank <= 32)
-    return run_gemm_jb<BM, BN, WM, WN, NS, WPE, INT4, 2>(a, lda, b, ldb, w, m, n, k, out, ldc,
+    return run_gemm_jb<BM, BN, WM, WN, NS, WPE, BK, 2>(a, lda, b, ldb, w, m, n, k, out, ldc,
                                                          epi, stream);
-  return run_gemm_jb<BM, BN, WM, WN, NS, WPE, INT4, 4>(a, lda, b, ldb, w, m, n, k, out, ldc, epi,
+  return run_gemm_jb<BM, BN, WM, WN, NS, WPE, BK, 4>(a, lda, b, ldb, w, m, n, k, out, ldc, epi,
                                                        stream);
 }
 
@@ -769,16 +1043,16 @@ hipError_t dispatch_int4(const uint16_t* a, int64_t lda, const Int4Operand& w, i
     return hipErrorInvalidValue;
   int cfg = tune(kTuneInt4Tile);
   if (cfg == kTileI4_256x256)
-    return run_gemm<256, 256, 2, 2, 3, 1, true>(a, lda, nullptr, 0, w, m, n, k, out, ldc, epi,
+    return run_gemm<256, 256, 2, 2, 3, 1, kBInt4>(a, lda, nullptr, 0, w, m, n, k, out, ldc, epi,
                                                 stream);
   if (cfg == kTileI4_128x128s2)
-    return run_gemm<128, 128, 1, 4, 2, 3, true>(a, lda, nullptr, 0, w, m, n, k, out, ldc, epi,
+    return run_gemm<128, 128, 1, 4, 2, 3, kBInt4>(a, lda, nullptr, 0, w, m, n, k, out, ldc, epi,
                                                 stream);
   if (cfg == kTileI4_128x128s3)
-    return run_gemm<128, 128, 1, 4, 3, 2, true>(a, lda, nullptr, 0, w, m, n, k, out, ldc, epi,
+    return run_gemm<128, 128, 1, 4, 3, 2, kBInt4>(a, lda, nullptr, 0, w, m, n, k, out, ldc, epi,
                                                 stream);
   if (cfg == kTileI4_256x128s2)
-    return run_gemm<256, 128, 1, 4, 2, 2, true>(a, lda, nullptr, 0, w, m, n, k, out, ldc, epi,
+    return run_gemm<256, 128, 1, 4, 2, 2, kBInt4>(a, lda, nullptr, 0, w, m, n, k, out, ldc, epi,
                                                 stream);
   if (cfg < kTileI4_256x128 || cfg > kTileI4_64x128) {
     // 128 x 32 wave tiles, two or three workgroups (8 or 12 waves) per CU:
@@ -793,7 +1067,7 @@ hipError_t dispatch_int4(const uint16_t* a, int64_t lda, const Int4Operand& w, i
     const int64_t scale_bytes = 256 * w.n_groups * 2;
     if (n >= 2048 && ceil_div(m, 256) * ceil_div(n, 128) >= 512 &&
         gemm_lds_bytes(256, 128, 2, true) + scale_bytes <= 160 * 1024)
-      return run_gemm<256, 128, 1, 4, 2, 2, true>(a, lda, nullptr, 0, w, m, n, k, out, ldc, epi,
+      return run_gemm<256, 128, 1, 4, 2, 2, kBInt4>(a, lda, nullptr, 0, w, m, n, k, out, ldc, epi,
                                                   stream);
     cfg = ceil_div(m, 128) * ceil_div(n, 128) >= 128 ? kTileI4_128x128 : kTileI4_64x128;
   }
@@ -804,19 +1078,19 @@ hipError_t dispatch_int4(const uint16_t* a, int64_t lda, const Int4Operand& w, i
     // tile of the same LDS budget does twice the work per block
     const int64_t scale_bytes = 128 * w.n_groups * 2;
     if (gemm_lds_bytes(128, 128, 2, true) + scale_bytes <= (160 * 1024) / 3)
-      return run_gemm<128, 128, 1, 4, 2, 3, true>(a, lda, nullptr, 0, w, m, n, k, out, ldc, epi,
+      return run_gemm<128, 128, 1, 4, 2, 3, kBInt4>(a, lda, nullptr, 0, w, m, n, k, out, ldc, epi,
                                                   stream);
     if (gemm_lds_bytes(128, 128, 3, true) + scale_bytes > (160 * 1024) / 2 && m >= 256 &&
         gemm_lds_bytes(256, 128, 3, true) + scale_bytes <= 160 * 1024)
       cfg = kTileI4_256x128;
     else
-      return run_gemm<128, 128, 1, 4, 3, 2, true>(a, lda, nullptr, 0, w, m, n, k, out, ldc, epi,
+      return run_gemm<128, 128, 1, 4, 3, 2, kBInt4>(a, lda, nullptr, 0, w, m, n, k, out, ldc, epi,
                                                   stream);
   }
   if (cfg == kTileI4_256x128)
-    return run_gemm<256, 128, 1, 4, 3, 1, true>(a, lda, nullptr, 0, w, m, n, k, out, ldc, epi,
+    return run_gemm<256, 128, 1, 4, 3, 1, kBInt4>(a, lda, nullptr, 0, w, m, n, k, out, ldc, epi,
                                                 stream);
-  return run_gemm<64, 128, 1, 4, 3, 2, true>(a, lda, nullptr, 0, w, m, n, k, out, ldc, epi,
+  return run_gemm<64, 128, 1, 4, 3, 2, kBInt4>(a, lda, nullptr, 0, w, m, n, k, out, ldc, epi,
                                              stream);
 }
 
@@ -826,7 +1100,7 @@ hipError_t dispatch_bf16(const uint16_t* a, int64_t lda, const uint16_t* b, int6
   Int4Operand none;
   int cfg = tune(kTuneBf16Tile);
   if (cfg == kTileBf_256x256)
-    return run_gemm<256, 256, 2, 2, 2, 1, false>(a, lda, b, ldb, none, m, n, k, out, ldc, epi,
+    return run_gemm<256, 256, 2, 2, 2, 1, kBBf16>(a, lda, b, ldb, none, m, n, k, out, ldc, epi,
                                                  stream);
   if (cfg == kTileAuto) {
     // Grids of at least 256 tiles of 256 x 128 take that tile with a
@@ -848,22 +1122,67 @@ hipError_t dispatch_bf16(const uint16_t* a, int64_t lda, const uint16_t* b, int6
                         : (t96 >= 192 && t96 <= 256 ? kTileBf_128x96 : kTileBf_64x128);
   }
   if (cfg == kTileBf_128x96)
-    return run_gemm<128, 96, 4, 1, 3, 1, false>(a, lda, b, ldb, none, m, n, k, out, ldc, epi,
+    return run_gemm<128, 96, 4, 1, 3, 1, kBBf16>(a, lda, b, ldb, none, m, n, k, out, ldc, epi,
                                                 stream);
   if (cfg == kTileBf_256x128)
-    return run_gemm<256, 128, 4, 2, 2, 2, false>(a, lda, b, ldb, none, m, n, k, out, ldc, epi,
+    return run_gemm<256, 128, 4, 2, 2, 2, kBBf16>(a, lda, b, ldb, none, m, n, k, out, ldc, epi,
                                                  stream);
   if (cfg == kTileBf_256x128s3)
-    return run_gemm<256, 128, 4, 2, 3, 2, false>(a, lda, b, ldb, none, m, n, k, out, ldc, epi,
+    return run_gemm<256, 128, 4, 2, 3, 2, kBBf16>(a, lda, b, ldb, none, m, n, k, out, ldc, epi,
                                                  stream);
   if (cfg == kTileBf_128x128)
-    return run_gemm<128, 128, 2, 2, 2, 2, false>(a, lda, b, ldb, none, m, n, k, out, ldc, epi,
+    return run_gemm<128, 128, 2, 2, 2, 2, kBBf16>(a, lda, b, ldb, none, m, n, k, out, ldc, epi,
                                                  stream);
-  return run_gemm<64, 128, 2, 2, 3, 2, false>(a, lda, b, ldb, none, m, n, k, out, ldc, epi,
+  return run_gemm<64, 128, 2, 2, 3, 2, kBBf16>(a, lda, b, ldb, none, m, n, k, out, ldc, epi,
                                               stream);
 }
 
+// The packed-weight input gradient: 256 x 128 tiles (8 waves, one workgroup
+// per CU) when they make at least one round, else 128 x 128 (4 waves) when
+// those do, else 64 x 128 at two workgroups per CU. The bf16 tile knob
+// forces one of the three.
+hipError_t dispatch_int4t(const uint16_t* a, int64_t lda, const Int4Operand& w, int64_t m,
+                          int64_t n, int64_t k, uint16_t* out, int64_t ldc,
+                          const LowRankEpilogue& epi, hipStream_t stream) {
+  int cfg = tune(kTuneBf16Tile);
+  if (cfg != kTileT4_256x128 && cfg != kTileT4_128x128 && cfg != kTileT4_64x128) {
+    if (ceil_div(m, 256) * (n / 128) >= 256)
+      cfg = kTileT4_256x128;
+    else if (ceil_div(m, 128) * (n / 128) >= 256)
+      cfg = kTileT4_128x128;
+    else
+      cfg = kTileT4_64x128;
+  }
+  if (cfg == kTileT4_256x128)
+    return run_gemm<256, 128, 4, 2, 3, 2, kBInt4T>(a, lda, nullptr, 0, w, m, n, k, out, ldc, epi,
+                                                   stream);
+  if (cfg == kTileT4_128x128)
+    return run_gemm<128, 128, 2, 2, 3, 1, kBInt4T>(a, lda, nullptr, 0, w, m, n, k, out, ldc, epi,
+                                                   stream);
+  return run_gemm<64, 128, 2, 2, 3, 2, kBInt4T>(a, lda, nullptr, 0, w, m, n, k, out, ldc, epi,
+                                                stream);
+}
+
 }  // namespace
+
+bool int4t_gemm_ok(int64_t m, int64_t n, int64_t k, int64_t lda, const void* a,
+                   const Int4Operand& w) {
+  // 128-column tiles over whole packed bytes; the scale load takes one dword
+  // per packed row (a per-row scale pair, or the tile's two 64-column groups)
+  const bool scales_ok = w.n_groups == 1 || (w.group == 64 && w.n_groups * 64 == n);
+  return m > 0 && n > 0 && n % 128 == 0 && k > 0 && k % kBK == 0 && lda % 8 == 0 &&
+         (reinterpret_cast<uintptr_t>(a) & 15) == 0 && w.packed_cols * 2 == n &&
+         (reinterpret_cast<uintptr_t>(w.packed) & 15) == 0 &&
+         (reinterpret_cast<uintptr_t>(w.scales) & 3) == 0 && scales_ok;
+}
+
+hipError_t launch_gemm_int4t(const uint16_t* a, int64_t lda, const Int4Operand& w, int64_t m,
+                             int64_t n, int64_t k, uint16_t* out, int64_t ldc,
+                             const LowRankEpilogue& epi, hipStream_t stream) {
+  if (m == 0 || n == 0) return hipSuccess;
+  if (!int4t_gemm_ok(m, n, k, lda, a, w)) return hipErrorInvalidValue;
+  return dispatch_int4t(a, lda, w, m, n, k, out, ldc, epi, stream);
+}
 
 bool gemm_fast_path_ok(int64_t k, int64_t lda, int64_t ldb_elems, const void* a, const void* b,
                        int64_t ldc, const void* out) {

@@ -411,7 +411,9 @@ hipError_t launch_int4lora_bwd_prep(const uint16_t* b, uint16_t* bt, const uint1
   p.ta_x = ceil_div(k, 32);
   p.ta = p.ta_x * ceil_div(rank, 32);
   p.tw_x = ceil_div(k, 128);
-  const int64_t tw = p.tw_x * ceil_div(n, 64);
+  // wt == nullptr: B^T and A^T only (the input gradient reads the packed
+  // weight itself)
+  const int64_t tw = wt == nullptr ? 0 : p.tw_x * ceil_div(n, 64);
   hipLaunchKernelGGL(k_int4lora_bwd_prep, dim3(static_cast<unsigned>(p.tb + p.ta + tw)), dim3(256),
                      0, stream, p);
   return hipGetLastError();

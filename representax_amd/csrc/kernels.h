@@ -64,6 +64,15 @@ struct Int4Operand {
 hipError_t launch_gemm_int4(const uint16_t* a, int64_t lda, const Int4Operand& w, int64_t m,
                             int64_t n, int64_t k, uint16_t* out, int64_t ldc,
                             const LowRankEpilogue& epi, hipStream_t stream);
+// y[M, N] = epilogue(A[M, K] . B[N, K]^T) with B[n, k] = W_b[k, n], W packed
+// INT4 [K rows, N / 2 bytes] (the INT4 + LoRA input gradient, dx = g . W_b,
+// without a bf16 copy of W_b^T). Needs N % 128 == 0, K % 64 == 0, per-row
+// or 64-column group scales; int4t_gemm_ok() tells.
+bool int4t_gemm_ok(int64_t m, int64_t n, int64_t k, int64_t lda, const void* a,
+                   const Int4Operand& w);
+hipError_t launch_gemm_int4t(const uint16_t* a, int64_t lda, const Int4Operand& w, int64_t m,
+                             int64_t n, int64_t k, uint16_t* out, int64_t ldc,
+                             const LowRankEpilogue& epi, hipStream_t stream);
 // y[M, N] = epilogue(A[M, K] . B[N, K]^T); A, B bf16 row-major.
 hipError_t launch_gemm_bf16(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb,
                             int64_t m, int64_t n, int64_t k, uint16_t* out, int64_t ldc,
@@ -137,7 +146,7 @@ hipError_t launch_rank_tn2(const uint16_t* x0, int64_t ldx0, const uint16_t* y0,
                            bool round_x1, float x_scale1, float* partials1, float* out1,
                            hipStream_t stream);
 // B^T [r, N], A^T [K, r] and W_b^T [K, N] (groups that are multiples of 32)
-// in one launch.
+// in one launch; wt == nullptr skips W_b^T.
 hipError_t launch_int4lora_bwd_prep(const uint16_t* b, uint16_t* bt, const uint16_t* a,
                                    uint16_t* at, const uint8_t* packed, const uint16_t* scales,
                                    uint16_t* wt, int64_t n, int64_t k, int64_t rank,

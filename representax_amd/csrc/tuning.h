@@ -20,7 +20,9 @@ enum TuneKnob : int {
   kTuneSkinny2One = 5,  // M <= 4 form: -1 planner, 0 two launches, 1 one launch  RPX_SKINNY2_ONE
   kTuneSpinLimit = 6,   // polls of the skinny kernels' bounded waits (0: default)
   kTuneBand = 7,        // row-blocks per band of the GEMM tile order (0: planner)  RPX_GEMM_BAND
-  kTuneCount = 8
+  kTuneDxPacked = 8,    // INT4 + LoRA input gradient's weight operand: -1 planner (bf16
+                        // W_b^T), 0 bf16 W_b^T, 1 packed where allowed    RPX_DX_PACKED
+  kTuneCount = 9
 };
 
 // Current value of a knob.
@@ -44,6 +46,9 @@ enum GemmTile : int {
   kTileI4_128x128s3 = 11,  // INT4 128 x 128, three stages, two workgroups per CU
   kTileI4_256x128s2 = 12,  // INT4 256 x 128, two stages, two workgroups per CU
   kTileBf_256x128s3 = 13,  // bf16 256 x 128, three stages, one workgroup per CU
+  kTileT4_256x128 = 14,    // packed-weight input gradient 256 x 128, one workgroup per CU
+  kTileT4_128x128 = 15,    // packed-weight input gradient 128 x 128, one workgroup per CU
+  kTileT4_64x128 = 16,     // packed-weight input gradient 64 x 128, two workgroups per CU
 };
 
 // Sets the dynamic-LDS limit of a kernel once per device (idempotent, so

@@ -138,6 +138,7 @@ TUNING_KNOBS = {
     "skinny2_one": nat.TUNE_SKINNY2_ONE,
     "spin_limit": nat.TUNE_SPIN_LIMIT,
     "gemm_band": nat.TUNE_GEMM_BAND,
+    "dx_packed": nat.TUNE_DX_PACKED,
 }
 
 

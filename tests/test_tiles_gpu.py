@@ -275,3 +275,77 @@ def test_train_step_linears_full_size(m, k, n, r, group, activation):
     assert_bf16_close(from_dev(dx)[rows], dx_o, what="dx")
     assert_bf16_close(from_dev(d_a), da_o, min_equal=BF16_MIN_EQUAL_TOKEN_SUM, what="dA")
     assert_bf16_close(from_dev(d_b), db_o, min_equal=BF16_MIN_EQUAL_TOKEN_SUM, what="dB")
+
+
+# The input gradient read from the packed weight (no bf16 W_b^T): output
+# widths k that are multiples of 128, reductions n over whole 64-row slices
+# (n = 64: a single slice), ragged M, per-row and group-64 scales, ranks
+# 16 / 32 / 64
+PACKED_DX_TILES = [16, 15, 14]  # 64x128, 128x128, 256x128
+PACKED_DX_SHAPES = [(300, 768, 320, 16, 64), (300, 384, 512, 32, None), (264, 256, 192, 64, 64),
+                    (100, 128, 64, 16, None)]
+
+
+@pytest.mark.parametrize("activation", ["none", "gelu", "silu_mul", "add"])
+@pytest.mark.parametrize("m,k,n,r,group", PACKED_DX_SHAPES)
+def test_packed_dx_every_tile(activation, m, k, n, r, group):
+    """dx = g . W_b from the packed weight, dequantized in the GEMM, on every
+    tile: the oracle's values, and bit for bit the input gradient computed
+    from a bf16 W_b^T (the K accumulation order is the same)."""
+
+    g = rng(5000 + m + k + n + r)
+    p = _params(g, n, k, r, group, bias=False)
+    d = _dev(p)
+    x = bf16_values(g.standard_normal((m, k)))
+    z = bf16_values(g.standard_normal((m, k)) * 2.0)
+    gate = bf16_values(g.standard_normal((m, k)) * 2.0)
+    gy = bf16_values(g.standard_normal((m, n)))
+    xd, gyd, zd = to_dev_bf16(x), to_dev_bf16(gy), to_dev_bf16(z)
+    gated = to_dev_bf16(gate) if activation == "silu_mul" else None
+    _, h = ops.int4lora_forward(xd, d["packed"], d["scales"], d["a"], d["b"],
+                                scaling=d["scaling"], group_size=group)
+    with ops.tuning(dx_packed=0):
+        want = _backward(d, gyd, xd, h, activation, zd, gated)
+    results = {}
+    for tile in PACKED_DX_TILES:
+        with ops.tuning(bf16_tile=tile, dx_packed=1):
+            results[tile] = _backward(d, gyd, xd, h, activation, zd, gated)
+    torch.cuda.synchronize()
+    if activation == "none":
+        dx_o, da_o, db_o = olora.lora_backward(gy, x, p["packed"], p["scales"], p["a"], p["b"],
+                                               from_dev(h), alpha=p["alpha"], rank=r,
+                                               group_size=group)
+        assert_bf16_close(from_dev(want[0]), dx_o, what="bf16 W_b^T dx")
+    for tile, res in results.items():
+        if activation == "none":
+            assert_bf16_close(from_dev(res[0]), dx_o, what=f"tile {tile} dx")
+        for i, name in enumerate(("out", "dgate", "dA", "dB")):
+            if want[i] is None:
+                assert res[i] is None
+            else:
+                assert torch.equal(res[i], want[i]), (tile, name)
+
+
+@pytest.mark.parametrize("dx_packed,cases", [
+    (1, [(300, 704, 320, 16, 64), (200, 256, 128, 16, 32)]),
+    (-1, [(300, 768, 320, 16, 64)])])
+def test_packed_dx_falls_back_where_not_allowed(dx_packed, cases):
+    """Shapes the packed form does not take (an output width that is not a
+    multiple of 128, 32-column groups), and every shape under the planner's
+    default, run the bf16 W_b^T form unchanged."""
+
+    for (m, k, n, r, group) in cases:
+        g = rng(5100 + k + (group or 0))
+        p = _params(g, n, k, r, group, bias=False)
+        d = _dev(p)
+        x = to_dev_bf16(bf16_values(g.standard_normal((m, k))))
+        gy = to_dev_bf16(bf16_values(g.standard_normal((m, n))))
+        _, h = ops.int4lora_forward(x, d["packed"], d["scales"], d["a"], d["b"],
+                                    scaling=d["scaling"], group_size=group)
+        with ops.tuning(dx_packed=0):
+            want = _backward(d, gy, x, h, "none", None, None)
+        with ops.tuning(dx_packed=dx_packed):
+            got = _backward(d, gy, x, h, "none", None, None)
+        torch.cuda.synchronize()
+        assert torch.equal(got[0], want[0]) and torch.equal(got[2], want[2])
+        assert torch.equal(got[3], want[3])
