@@ -826,8 +826,9 @@ def run_skinny(batch=96, latency_calls=64):
     graph of `batch` calls that cycle through a pool of weight copies larger
     than the 256 MB Infinity Cache, so every call streams its packed weight
     from HBM. `p50_us`: median over `latency_calls` single eager calls (HIP
-    events around each, weights cycling the same way). HBM bytes: packed
-    weight, scales, A, B, x and y."""
+    events around each, weights cycling the same way). Every call is the
+    inference form (``need_h=False``: h stays in the call's scratch, y is the
+    one output). HBM bytes: packed weight, scales, A, B, x and y."""
 
     import torch
 
@@ -854,7 +855,7 @@ def run_skinny(batch=96, latency_calls=64):
                 for i in range(batch):
                     p, s, a, b = pool[i % copies]
                     calls.append(lambda p=p, s=s, a=a, b=b: ops.int4lora_forward(
-                        x, p, s, a, b, scaling=2.0, group_size=group))
+                        x, p, s, a, b, scaling=2.0, group_size=group, need_h=False))
                 us = graph_time_per_call_ms(calls, replays=3) * 1e3
                 lat = []
                 for i in range(latency_calls):
@@ -887,7 +888,8 @@ def run_skinny_shared(batch=96, latency_calls=64, group=64, r=32):
     """Projections of one input (the Qwen3-2B tower's q/k/v and gate/up) at
     M in {1, 4}: one rpx_int4lora_forward_multi call against one call per
     projection, both per call inside a HIP graph of `batch` calls cycling
-    weight copies beyond the MALL, plus the multi call's eager p50. HBM bytes:
+    weight copies beyond the MALL, plus the multi call's eager p50 (inference
+    form, ``need_h=False``, as the model's shared-input path calls it). HBM bytes:
     every projection's packed weight, scales, A, B and y, and x once."""
 
     import torch
@@ -914,9 +916,10 @@ def run_skinny_shared(batch=96, latency_calls=64, group=64, r=32):
             for i in range(batch):
                 projs = pool[i % copies]
                 multi.append(lambda projs=projs: ops.int4lora_forward_multi(
-                    x, [(p, s, a, b, 2.0, group, None) for p, s, a, b in projs]))
+                    x, [(p, s, a, b, 2.0, group, None) for p, s, a, b in projs], need_h=False))
                 separate.append(lambda projs=projs: [
-                    ops.int4lora_forward(x, p, s, a, b, scaling=2.0, group_size=group)
+                    ops.int4lora_forward(x, p, s, a, b, scaling=2.0, group_size=group,
+                                         need_h=False)
                     for p, s, a, b in projs])
             us_multi = graph_time_per_call_ms(multi, replays=3) * 1e3
             us_sep = graph_time_per_call_ms(separate, replays=3) * 1e3

@@ -186,9 +186,14 @@ class QuantizedLoRALinear(torch.nn.Module):
             # float32 masters, so the adapter term and the output are float32
             y = ops.Int4LoRAPromotedFn.apply(x2d, a, b, self.packed_weight, self.scale_bits,
                                              self.bias_bits, self.scaling, self.group_size)
-        else:
+        elif torch.is_grad_enabled() and (x2d.requires_grad or a.requires_grad or b.requires_grad):
             y = ops.Int4LoRALinearFn.apply(x2d, a, b, self.packed_weight, self.scale_bits,
                                            self.bias_bits, self.scaling, self.group_size)
+        else:
+            # no backward will run: the fused call alone, h kept in its scratch
+            y, _ = ops.int4lora_forward(x2d, self.packed_weight, self.scale_bits, a, b,
+                                        scaling=self.scaling, group_size=self.group_size,
+                                        bias_bits=self.bias_bits, need_h=False)
         return constrain_activation(y.reshape(*lead, self.output_size))
 
     def _forward_fp8(self, value: torch.Tensor, compute_dtype: torch.dtype) -> torch.Tensor:

@@ -91,7 +91,7 @@ def shared_input_projections(value: torch.Tensor, linears) -> list[torch.Tensor]
         x2d = x.reshape(-1, linears[0].input_size)
         outs = ops.int4lora_forward_multi(
             x2d, [(l.packed_weight, l.scale_bits, views[2 * i], views[2 * i + 1], l.scaling,
-                   l.group_size, l.bias_bits) for i, l in enumerate(linears)])
+                   l.group_size, l.bias_bits) for i, l in enumerate(linears)], need_h=False)
         return [y.reshape(*lead, layer.output_size) for (y, _), layer in zip(outs, linears)]
     outs = ops.Int4LoRASharedInputFn.apply(x.reshape(-1, linears[0].input_size), len(linears),
                                            *views, *leaves)

@@ -55,15 +55,16 @@ def _on_device(*tensors: torch.Tensor | None) -> torch.device:
     for t in tensors:
         if t is None:
             continue
-        if not t.is_cuda:
+        i = t.get_device()  # -1 off the GPU
+        if i < 0:
             raise RuntimeError(
                 "representax_amd kernels run on ROCm devices only; got a tensor on "
                 f"{t.device}"
             )
         if device is None:
             device = t.device
-            index = t.get_device()
-        elif t.get_device() != index:
+            index = i
+        elif i != index:
             raise RuntimeError("all operands must be on the same device")
     if device is None:
         raise RuntimeError("no device tensor given")
@@ -79,17 +80,38 @@ def _on_device(*tensors: torch.Tensor | None) -> torch.device:
 _WORKSPACES: dict[tuple[int, int], torch.Tensor] = {}
 
 
-def _workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+def _workspace(nbytes: int, device: torch.device, stream: int | None = None) -> torch.Tensor:
+    """``stream``: the device's current raw stream when the caller has it."""
+
     nbytes = max(int(nbytes), 1)
     if torch.cuda.is_current_stream_capturing():
         return torch.empty(nbytes, dtype=torch.uint8, device=device)
     index = _device_index(device)
-    key = (index, _raw_stream(device))
+    key = (index, _raw_stream(device) if stream is None else stream)
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
         ws = torch.empty(nbytes, dtype=torch.uint8, device=torch.device("cuda", index))
         _WORKSPACES[key] = ws
     return ws
+
+
+def _round16(nbytes: int) -> int:
+    return -(-int(nbytes) // 16) * 16
+
+
+def _workspace_with_tails(nbytes: int, tails, device: torch.device,
+                          stream: int | None = None) -> tuple[torch.Tensor, list[int]]:
+    """The call's scratch (its first ``nbytes``, which the library is given)
+    followed by one 16-byte aligned region per entry of ``tails`` (bytes):
+    ``(buffer, [address of each region])``."""
+
+    head = _round16(max(int(nbytes), 1))
+    ws = _workspace(head + sum(_round16(t) for t in tails), device, stream)
+    addrs, at = [], ws.data_ptr() + head
+    for t in tails:
+        addrs.append(at)
+        at += _round16(t)
+    return ws, addrs
 
 
 def release_workspaces() -> None:
@@ -120,6 +142,30 @@ def _u16(t: torch.Tensor) -> torch.Tensor:
     if t.dtype in (BF16, torch.int16):
         return t.view(torch.uint16)
     raise TypeError(f"expected 16-bit bit patterns, got {t.dtype}")
+
+
+def _ready(index: int, tensors) -> list[int] | None:
+    """The addresses of ``tensors`` when each is on device ``index``, dense
+    and 16-byte aligned (the form the kernels take as is); None otherwise."""
+
+    ptrs = []
+    for t in tensors:
+        p = t.data_ptr()
+        if p & 15 or t.get_device() != index or not t.is_contiguous():
+            return None
+        ptrs.append(p)
+    return ptrs
+
+
+def _bias_ready(bias_bits, index: int):
+    """(ok, address) of optional bias bits already in the kernels' form:
+    uint16, on device ``index``, dense."""
+
+    if bias_bits is None:
+        return True, None
+    if bias_bits.dtype != torch.uint16 or bias_bits.get_device() != index or not bias_bits.is_contiguous():
+        return False, None
+    return True, bias_bits.data_ptr()
 
 
 def group_arg(group_size: int | None, k: int) -> int:
@@ -247,10 +293,59 @@ def int4_merge(packed, scale_bits, lora_a, lora_b, *, alpha: float, rank: int, i
 # ---------------------------------------------------------------------------
 # INT4 + LoRA linear
 # ---------------------------------------------------------------------------
-def int4lora_forward(x2d, packed, scale_bits, lora_a_c, lora_b_c, *, scaling: float,
-                     group_size: int | None = None, bias_bits=None):
-    """Return ``(y [M, N], h [M, r])`` in x's compute dtype."""
+def _forward_ready(fast, x2d, packed, scale_bits, a, b, scaling, group_size, bias_bits, need_h):
+    """int4lora_forward through the fast binding when every operand is
+    already in the kernels' form (one device, dense, 16-byte aligned, A and B
+    in x's dtype, uint16 scale and bias bits): one pass over the operands
+    instead of a check and a conversion each, which is most of a small-M
+    call's host time. None otherwise; the general path then converts, copies
+    or raises."""
 
+    dt = x2d.dtype
+    if (a.dtype != dt or b.dtype != dt or scale_bits.dtype != torch.uint16
+            or x2d.dim() != 2):
+        return None
+    index = x2d.get_device()
+    ptrs = _ready(index, (x2d, packed, scale_bits, a, b))
+    ok, pb = _bias_ready(bias_bits, index)
+    if index < 0 or ptrs is None or not ok:
+        return None
+    code = _dtype_code(dt)
+    m, k = x2d.shape
+    n = packed.shape[-2]
+    r = a.shape[0]
+    g = group_arg(group_size, k)
+    device = x2d.device
+    y = torch.empty((m, n), dtype=dt, device=device)
+    stream = _stream(device)
+    ws_bytes = fast.int4lora_forward_workspace(m, n, k, g, r, code)
+    if need_h:
+        h = torch.empty((m, r), dtype=dt, device=device)
+        ws = _workspace(ws_bytes, device, stream)
+        ws_bytes, h_ptr = ws.numel(), h.data_ptr()
+    else:
+        h = None
+        ws, (h_ptr,) = _workspace_with_tails(ws_bytes, (m * r * dt.itemsize,), device, stream)
+    nat.check(fast.int4lora_forward(ptrs[0], code, m, k, ptrs[1], ptrs[2], n, g, pb, ptrs[3],
+                                    ptrs[4], r, float(scaling), y.data_ptr(), h_ptr,
+                                    ws.data_ptr(), ws_bytes, stream))
+    return y, h
+
+
+def int4lora_forward(x2d, packed, scale_bits, lora_a_c, lora_b_c, *, scaling: float,
+                     group_size: int | None = None, bias_bits=None, need_h: bool = True):
+    """Return ``(y [M, N], h [M, r])`` in x's compute dtype.
+
+    ``need_h=False`` (inference: no backward will read h) returns
+    ``(y, None)``: the kernels still form h, in the call's scratch, and only
+    y is allocated."""
+
+    fast = nat.fast()
+    if fast is not None:
+        out = _forward_ready(fast, x2d, packed, scale_bits, lora_a_c, lora_b_c, scaling,
+                             group_size, bias_bits, need_h)
+        if out is not None:
+            return out
     device = _on_device(x2d, packed, scale_bits, lora_a_c, lora_b_c, bias_bits)
     m, k = x2d.shape
     n = packed.shape[-2]
@@ -261,35 +356,122 @@ def int4lora_forward(x2d, packed, scale_bits, lora_a_c, lora_b_c, *, scaling: fl
     a = _aligned(_as(lora_a_c, dt))
     b = _aligned(_as(lora_b_c, dt))
     y = torch.empty((m, n), dtype=dt, device=device)
-    h = torch.empty((m, r), dtype=dt, device=device)
+    h = torch.empty((m, r), dtype=dt, device=device) if need_h else None
     g = group_arg(group_size, k)
     bias = None if bias_bits is None else _u16(bias_bits).contiguous()
     packed = _aligned(packed)
     scale_bits = _aligned(_u16(scale_bits))
     fast = nat.fast()
+    stream = _stream(device)
     if fast is not None:
-        ws = _workspace(fast.int4lora_forward_workspace(m, n, k, g, r, code), device)
+        ws_bytes = fast.int4lora_forward_workspace(m, n, k, g, r, code)
+    else:
+        ws_bytes = nat.query("rpx_int4lora_forward_workspace", m, n, k, g, r, code)
+    if need_h:
+        ws = _workspace(ws_bytes, device, stream)
+        ws_bytes, h_ptr = ws.numel(), h.data_ptr()
+    else:
+        ws, (h_ptr,) = _workspace_with_tails(ws_bytes, (m * r * dt.itemsize,), device, stream)
+    if fast is not None:
         nat.check(fast.int4lora_forward(
             x2d.data_ptr(), code, m, k, packed.data_ptr(), scale_bits.data_ptr(), n, g, _ptr(bias),
-            a.data_ptr(), b.data_ptr(), r, float(scaling), y.data_ptr(), h.data_ptr(),
-            ws.data_ptr(), ws.numel(), _stream(device)))
-        return y, h
-    ws_bytes = nat.query("rpx_int4lora_forward_workspace", m, n, k, g, r, code)
-    ws = _workspace(ws_bytes, device)
-    nat.call("rpx_int4lora_forward", _ptr(x2d), code, m, k, _ptr(packed), _ptr(scale_bits), n, g,
-             _ptr(bias), _ptr(a), _ptr(b), r, float(scaling), _ptr(y), _ptr(h), _ptr(ws),
-             ws.numel(), _stream(device))
+            a.data_ptr(), b.data_ptr(), r, float(scaling), y.data_ptr(), h_ptr,
+            ws.data_ptr(), ws_bytes, stream))
+    else:
+        nat.call("rpx_int4lora_forward", _ptr(x2d), code, m, k, _ptr(packed), _ptr(scale_bits), n,
+                 g, _ptr(bias), _ptr(a), _ptr(b), r, float(scaling), _ptr(y), h_ptr, _ptr(ws),
+                 ws_bytes, stream)
     return y, h
 
 
-def int4lora_forward_multi(x2d, projections):
+# Up to this many rows, int4lora_forward_multi takes all of its outputs from
+# one allocation: at small M a call costs more host time than GPU time, and
+# one allocator call in place of two per projection is a large share of it.
+# The outputs then share one storage, which lives until the last of them is
+# freed (a few KB per projection at these sizes).
+SHARED_OUTPUT_ROWS = 64
+# fields per projection in the fast binding's flat tuple
+PROJECTION_FIELDS = 11
+
+
+def _dense_views(m: int, cols, dtype: torch.dtype, device: torch.device) -> list[torch.Tensor]:
+    """``[t [m, c] for c in cols]`` as dense views of one allocation, each
+    starting on a 16-byte boundary."""
+
+    per16 = 16 // dtype.itemsize
+    offsets, total = [], 0
+    for c in cols:
+        offsets.append(total)
+        total += -(-m * c // per16) * per16
+    buf = torch.empty(total, dtype=dtype, device=device)
+    return [buf.as_strided((m, c), (c, 1), o) for c, o in zip(cols, offsets)]
+
+
+def _multi_ready(fast, x2d, projections, need_h):
+    """int4lora_forward_multi through the fast binding at M <= 64 when every
+    operand is already in the kernels' form (as for ``_forward_ready``);
+    None otherwise."""
+
+    dt = x2d.dtype
+    if x2d.dim() != 2 or x2d.shape[0] > SHARED_OUTPUT_ROWS:
+        return None
+    index = x2d.get_device()
+    px = _ready(index, (x2d,))
+    if index < 0 or px is None:
+        return None
+    m, k = x2d.shape
+    flat, dims = [], []
+    for packed, scale_bits, a, b, scaling, group_size, bias_bits in projections:
+        if a.dtype != dt or b.dtype != dt or scale_bits.dtype != torch.uint16:
+            return None
+        ptrs = _ready(index, (packed, scale_bits, a, b))
+        ok, pb = _bias_ready(bias_bits, index)
+        if ptrs is None or not ok:
+            return None
+        n, r = packed.shape[-2], a.shape[0]
+        dims.append((n, r))
+        # y's and h's addresses (the last two fields) are filled in below;
+        # the size query reads the shapes only
+        flat += (ptrs[0], ptrs[1], n, group_arg(group_size, k), pb, ptrs[2], ptrs[3], r,
+                 float(scaling), 0, 0)
+    code = _dtype_code(dt)
+    device = x2d.device
+    if need_h:
+        views = _dense_views(m, [c for nr in dims for c in nr], dt, device)
+        ys, hs = views[0::2], views[1::2]
+    else:
+        ys, hs = _dense_views(m, [n for n, _ in dims], dt, device), [None] * len(dims)
+    stream = _stream(device)
+    ws_bytes = fast.int4lora_forward_multi_workspace(m, k, tuple(flat), code)
+    if need_h:
+        ws = _workspace(ws_bytes, device, stream)
+        ws_bytes = ws.numel()
+        h_ptrs = [h.data_ptr() for h in hs]
+    else:
+        ws, h_ptrs = _workspace_with_tails(ws_bytes, [m * r * dt.itemsize for _, r in dims],
+                                           device, stream)
+    for i, (y, h_ptr) in enumerate(zip(ys, h_ptrs)):
+        flat[PROJECTION_FIELDS * i + 9] = y.data_ptr()
+        flat[PROJECTION_FIELDS * i + 10] = h_ptr
+    nat.check(fast.int4lora_forward_multi(px[0], code, m, k, tuple(flat), ws.data_ptr(), ws_bytes,
+                                          stream))
+    return list(zip(ys, hs))
+
+
+def int4lora_forward_multi(x2d, projections, need_h: bool = True):
     """Several INT4 + LoRA projections of one input: ``projections`` is a
     sequence of ``(packed, scale_bits, lora_a_c, lora_b_c, scaling,
     group_size, bias_bits)``; returns ``[(y, h), ...]`` as
-    ``int4lora_forward`` gives for each. At small M (bf16, M <= 4, one rank)
-    they run in one pair of launches."""
+    ``int4lora_forward`` gives for each (``h`` None with ``need_h=False``).
+    At small M (bf16, M <= 4, one rank) they run in one pair of launches."""
 
     projections = list(projections)
+    count = len(projections)
+    fast = nat.fast() if count <= 16 else None
+    if fast is not None:
+        out = _multi_ready(fast, x2d, projections, need_h)
+        if out is not None:
+            return out
     tensors = [x2d]
     for p in projections:
         tensors += [p[0], p[1], p[2], p[3], p[6]]
@@ -298,41 +480,60 @@ def int4lora_forward_multi(x2d, projections):
     dt = x2d.dtype
     code = _dtype_code(dt)
     x2d = _aligned(x2d)
-    count = len(projections)
-    fast = nat.fast() if count <= 16 else None
     table = None if fast is not None else (nat.Int4LoraProjection * count)()
+    dims = [(p[0].shape[-2], p[2].shape[0]) for p in projections]
+    if m <= SHARED_OUTPUT_ROWS:
+        if need_h:
+            views = _dense_views(m, [c for nr in dims for c in nr], dt, device)
+            ys, hs = views[0::2], views[1::2]
+        else:
+            ys, hs = _dense_views(m, [n for n, _ in dims], dt, device), [None] * count
+    else:
+        ys = [torch.empty((m, n), dtype=dt, device=device) for n, _ in dims]
+        hs = [torch.empty((m, r), dtype=dt, device=device) if need_h else None for _, r in dims]
     flat = []
-    keep, outs = [], []
+    keep = []
     for i, (packed, scale_bits, lora_a_c, lora_b_c, scaling, group_size, bias_bits) in enumerate(projections):
-        n = packed.shape[-2]
-        r = lora_a_c.shape[0]
+        n, r = dims[i]
         a = _aligned(_as(lora_a_c, dt))
         b = _aligned(_as(lora_b_c, dt))
         pk = _aligned(packed)
         sc = _aligned(_u16(scale_bits))
         bias = None if bias_bits is None else _u16(bias_bits).contiguous()
-        y = torch.empty((m, n), dtype=dt, device=device)
-        h = torch.empty((m, r), dtype=dt, device=device)
         keep += [a, b, pk, sc, bias]
-        outs.append((y, h))
+        # h's address (the last field) is filled in below once the scratch
+        # is known; the size queries read the shapes only
         fields = (pk.data_ptr(), sc.data_ptr(), n, group_arg(group_size, k), _ptr(bias),
-                  a.data_ptr(), b.data_ptr(), r, float(scaling), y.data_ptr(), h.data_ptr())
+                  a.data_ptr(), b.data_ptr(), r, float(scaling), ys[i].data_ptr(),
+                  0 if hs[i] is None else hs[i].data_ptr())
         if fast is not None:
             flat += fields
         else:
             table[i] = nat.Int4LoraProjection(*fields)
+    stream = _stream(device)
     if fast is not None:
-        flat = tuple(flat)
-        ws = _workspace(fast.int4lora_forward_multi_workspace(m, k, flat, code), device)
-        nat.check(fast.int4lora_forward_multi(x2d.data_ptr(), code, m, k, flat, ws.data_ptr(),
-                                              ws.numel(), _stream(device)))
+        ws_bytes = fast.int4lora_forward_multi_workspace(m, k, tuple(flat), code)
     else:
         ws_bytes = nat.query("rpx_int4lora_forward_multi_workspace", m, k, count, table, code)
-        ws = _workspace(ws_bytes, device)
+    if need_h:
+        ws = _workspace(ws_bytes, device, stream)
+        ws_bytes = ws.numel()
+    else:
+        ws, h_ptrs = _workspace_with_tails(ws_bytes, [m * r * dt.itemsize for _, r in dims],
+                                           device, stream)
+        for i, h_ptr in enumerate(h_ptrs):
+            if fast is not None:
+                flat[PROJECTION_FIELDS * i + PROJECTION_FIELDS - 1] = h_ptr
+            else:
+                table[i].h = h_ptr
+    if fast is not None:
+        nat.check(fast.int4lora_forward_multi(x2d.data_ptr(), code, m, k, tuple(flat),
+                                              ws.data_ptr(), ws_bytes, stream))
+    else:
         nat.call("rpx_int4lora_forward_multi", _ptr(x2d), code, m, k, count, table, _ptr(ws),
-                 ws.numel(), _stream(device))
+                 ws_bytes, stream)
     del keep
-    return outs
+    return list(zip(ys, hs))
 
 
 def int4lora_backward(grad, x2d, packed, scale_bits, lora_a_c, lora_b_c, h, *, scaling: float,

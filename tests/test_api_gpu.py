@@ -137,6 +137,28 @@ def test_bf16_module_gradients_match_oracle():
     assert layer.lora_a.grad.dtype == torch.float32
 
 
+@pytest.mark.parametrize("m", [1, 4, 128])
+def test_bf16_module_inference_equals_training_forward(m):
+    """Without autograd the module calls the fused forward directly and keeps
+    h in the call's scratch; its output is bitwise the output of the
+    autograd path (small M runs the skinny kernels, M = 128 the GEMM)."""
+
+    g = np.random.Generator(np.random.PCG64(13 + m))
+    lin = rx.Linear.init(2048, 1024, key=4, scale=0.02, bias=True, device=DEV)
+    layer = rx.QuantizedLoRALinear.from_linear(lin, rank=32, alpha=64.0, key=5, group_size=64)
+    with torch.no_grad():
+        layer.lora_b.normal_(0, 0.05)
+    x = torch.from_numpy(g.standard_normal((m, 2048)).astype(np.float32)).to(DEV).to(torch.bfloat16)
+    bf = rx.resolve_precision_policy(rx.PrecisionConfig.bfloat16_mixed())
+    with rx.precision_context(bf):
+        y_train = layer(x.clone().requires_grad_(True))
+        with torch.no_grad():
+            y_infer = layer(x)
+    torch.cuda.synchronize()
+    assert y_train.grad_fn is not None and y_infer.grad_fn is None
+    assert torch.equal(y_train.detach(), y_infer)
+
+
 def test_float8_step_keeps_master_state_finite_and_fp32():
     """tests/train/test_precision.py:214-228 on a small dense model."""
 

@@ -144,3 +144,86 @@ def test_fast_binding_equals_ctypes_binding(m, monkeypatch):
     assert torch.equal(y_f, y_c) and torch.equal(h_f, h_c)
     for (a, b), (c, e) in zip(multi_f, multi_c):
         assert torch.equal(a, c) and torch.equal(b, e)
+
+
+@pytest.mark.parametrize("fast", [True, False], ids=["fast-binding", "ctypes"])
+@pytest.mark.parametrize("m", [1, 4, 64, 300])
+def test_forward_without_h_gives_the_same_outputs(m, fast, monkeypatch):
+    """need_h=False (inference) keeps h in the call's scratch: y is bitwise
+    the y of the call that returns h, for the single and the multi-projection
+    forwards on either binding. The outputs of one multi call (one
+    allocation at M <= 64) are dense, 16-byte aligned and disjoint."""
+
+    from representax_amd import _native as nat
+
+    if not fast:
+        monkeypatch.setattr(nat, "fast", lambda: None)
+    g = rng(800 + m)
+    k = 2048
+    projs = [_proj(g, n, k, 32, 64, bias=(i == 0)) for i, n in enumerate((2048, 1024, 1024))]
+    xd = to_dev_bf16(bf16_values(g.standard_normal((m, k))))
+    d = projs[0][1]
+    y_h, h = ops.int4lora_forward(xd, d[0], d[1], d[2], d[3], scaling=d[4], group_size=d[5],
+                                  bias_bits=d[6])
+    y_n, no_h = ops.int4lora_forward(xd, d[0], d[1], d[2], d[3], scaling=d[4], group_size=d[5],
+                                     bias_bits=d[6], need_h=False)
+    multi_h = ops.int4lora_forward_multi(xd, [p for _, p in projs])
+    multi_n = ops.int4lora_forward_multi(xd, [p for _, p in projs], need_h=False)
+    torch.cuda.synchronize()
+    assert no_h is None and h is not None
+    assert torch.equal(y_h, y_n)
+    for (ya, ha), (yb, hb) in zip(multi_h, multi_n):
+        assert hb is None and torch.equal(ya, yb)
+    for outs in (multi_h, multi_n):
+        spans = []
+        for pair in outs:
+            for t in pair:
+                if t is None:
+                    continue
+                assert t.is_contiguous() and t.data_ptr() % 16 == 0
+                spans.append((t.data_ptr(), t.data_ptr() + t.numel() * t.element_size()))
+        spans.sort()
+        assert all(end <= start for (_, end), (start, _) in zip(spans, spans[1:]))
+
+
+@pytest.mark.parametrize("m", [1, 4, 300])
+def test_operands_in_other_forms_give_the_same_bits(m):
+    """Operands the kernels cannot take as they are (float32 adapters holding
+    bf16 values, scale bits typed bf16, bias bits typed int16, a strided or misaligned x)
+    go through the general path, which converts them: the same bits as the
+    call whose operands are already in the kernels' form."""
+
+    g = rng(900 + m)
+    k = 2048
+    projs = [_proj(g, n, k, 32, 64, bias=(i == 0)) for i, n in enumerate((2048, 1024, 1024))]
+    x = bf16_values(g.standard_normal((m, k)))
+    xd = to_dev_bf16(x)
+    wide = torch.zeros((m, k + 64), dtype=torch.bfloat16, device="cuda")
+    wide[:, 1:1 + k] = xd
+    x_strided = wide[:, 1:1 + k]  # strided for M > 1, 2 bytes off alignment at M = 1
+    assert not x_strided.is_contiguous() or x_strided.data_ptr() % 16
+
+
+    def other(d):
+        return (d[0], d[1].view(torch.bfloat16), d[2].float(), d[3].float(), d[4], d[5],
+                None if d[6] is None else d[6].view(torch.int16))
+
+    for need_h in (True, False):
+        d = projs[0][1]
+        y_r, h_r = ops.int4lora_forward(xd, d[0], d[1], d[2], d[3], scaling=d[4], group_size=d[5],
+                                        bias_bits=d[6], need_h=need_h)
+        o = other(d)
+        y_o, h_o = ops.int4lora_forward(x_strided, o[0], o[1], o[2], o[3], scaling=o[4],
+                                        group_size=o[5], bias_bits=o[6], need_h=need_h)
+        multi_r = ops.int4lora_forward_multi(xd, [p for _, p in projs], need_h=need_h)
+        multi_o = ops.int4lora_forward_multi(x_strided, [other(p) for _, p in projs],
+                                             need_h=need_h)
+        torch.cuda.synchronize()
+        assert torch.equal(y_r, y_o)
+        assert (h_r is None) == (not need_h) and (h_o is None) == (not need_h)
+        if need_h:
+            assert torch.equal(h_r, h_o)
+        for (ya, ha), (yb, hb) in zip(multi_r, multi_o):
+            assert torch.equal(ya, yb)
+            if need_h:
+                assert torch.equal(ha, hb)
