@@ -661,7 +661,28 @@ def int4lora_roofline(c, reps=20):
     return {"bound": "mfma", "achieved": round(achieved, 2), "peak": BF16_PEAK_TFLOPS,
             "unit": "TFLOP/s", "frac": round(achieved / BF16_PEAK_TFLOPS, 4),
             "kernel": "int4lora_forward (rank-r down kernel + fused dequant GEMM)",
-            "avg_call_us": round(ms * 1e3, 2)}
+            "avg_call_us": round(ms * 1e3, 2), "dequant": int4_dequant_rate(c, reps)}
+
+
+def int4_dequant_rate(c, reps=20):
+    """The dequantization stage on its own: the config's packed weight to a
+    bf16 [N, K] matrix (rpx_int4_dequant, bit-exact bf16(q * s)), the same
+    unpack the GEMM applies to its B tiles in LDS. Algorithmic bytes: packed
+    codes and scales read once, the bf16 weight written once."""
+
+    from representax_amd import ops
+
+    n, k = c["n"], c["k"]
+
+    def deq():
+        ops.int4_dequant(c["packed"], c["scales"], k, c["group"])
+
+    ms = graph_time_per_call_ms([deq] * reps)
+    nbytes = float(c["packed"].numel() + 2 * c["scales"].numel() + 2 * n * k)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"kernel": "k_int4_dequant (rpx_int4_dequant)", "us_per_call": round(ms * 1e3, 2),
+            "algorithmic_bytes": nbytes, "gbs": round(gbs, 1),
+            "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
 
 
 def run_int4lora(steps, warmup, use_graph, group_size=None):

@@ -79,6 +79,15 @@ int rpx_abi_version(void);
  *                        planner (a bf16 W_b^T written first), 0 the same,
  *                        1 the packed weight dequantized inside the GEMM,
  *                        where the shape allows (env RPX_DX_PACKED)
+ *   RPX_TUNE_RANK_BLOCKS workgroups each token-reduction product of the
+ *                        LoRA backward (dA, dB) is split for: 0 planner,
+ *                        16..8192
+ *   RPX_TUNE_RANK_NT_U   128-column steps each wave of the rank-r row kernel
+ *                        (h = x A^T, dh = g_a B) keeps in flight: 0 planner,
+ *                        4, 8, 16
+ *   RPX_TUNE_FP8_SPLITS  fp8 GEMM split-K count: 0 planner, 1..32 where the
+ *                        128-deep K slices split into exactly that many
+ *                        parts (otherwise the planner's count)
  * ------------------------------------------------------------------------- */
 #define RPX_TUNE_INT4_TILE 0
 #define RPX_TUNE_BF16_TILE 1
@@ -89,6 +98,9 @@ int rpx_abi_version(void);
 #define RPX_TUNE_SPIN_LIMIT 6
 #define RPX_TUNE_GEMM_BAND 7
 #define RPX_TUNE_DX_PACKED 8
+#define RPX_TUNE_RANK_BLOCKS 9
+#define RPX_TUNE_RANK_NT_U 10
+#define RPX_TUNE_FP8_SPLITS 11
 
 /* RPX_ERR_INVALID for an unknown knob or value. */
 int rpx_set_tuning(int knob, int value);

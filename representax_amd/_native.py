@@ -40,6 +40,9 @@ TUNE_SKINNY2_ONE = 5
 TUNE_SPIN_LIMIT = 6
 TUNE_GEMM_BAND = 7
 TUNE_DX_PACKED = 8
+TUNE_RANK_BLOCKS = 9
+TUNE_RANK_NT_U = 10
+TUNE_FP8_SPLITS = 11
 
 _p = ctypes.c_void_p
 _i64 = ctypes.c_int64

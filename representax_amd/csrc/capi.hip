@@ -217,6 +217,9 @@ bool knob_value_ok(int knob, int v) {
     case kTuneSpinLimit: return v >= 0;
     case kTuneBand: return v >= 0 && v <= 64;
     case kTuneDxPacked: return v >= -1 && v <= 1;
+    case kTuneRankBlocks: return v == 0 || (v >= 16 && v <= 8192);
+    case kTuneRankNtU: return v == 0 || v == 4 || v == 8 || v == 16;
+    case kTuneFp8Splits: return v >= 0 && v <= 32;
     default: return false;
   }
 }
@@ -229,7 +232,7 @@ int env_int(const char* name, int fallback) {
 struct Knobs {
   std::atomic<int> v[kTuneCount];
   Knobs() {
-    const int defaults[kTuneCount] = {0, 0, 0, 0, -1, -1, 0, 0, -1};
+    const int defaults[kTuneCount] = {0, 0, 0, 0, -1, -1, 0, 0, -1, 0, 0, 0};
     for (int i = 0; i < kTuneCount; ++i) v[i].store(defaults[i], std::memory_order_relaxed);
     // RPX_GEMM_TILE names a tile of either GEMM (the id sets are disjoint)
     const int gemm = env_int("RPX_GEMM_TILE", 0);

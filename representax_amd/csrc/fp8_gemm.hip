@@ -424,6 +424,14 @@ Fp8Plan plan_for(int cfg, int64_t m, int64_t n, int64_t kslices, double* cost_ou
   Fp8Plan best{cfg, 1, kslices * kBK};
   double best_cost = -1.0;
   const int64_t tiles = ceil_div(m, kCfgBM[cfg]) * ceil_div(n, kCfgBN[cfg]);
+  const int64_t forced = tune(kTuneFp8Splits);
+  if (forced > 0 && forced <= kslices) {
+    const int64_t kps = ceil_div(kslices, forced);
+    if (ceil_div(kslices, kps) == forced) {
+      if (cost_out != nullptr) *cost_out = plan_cycles(cfg, m, n, kslices, kps, forced);
+      return Fp8Plan{cfg, forced, kps * kBK};
+    }
+  }
   for (int64_t s = 1; s <= 32 && s <= kslices; ++s) {
     if (s > 1 && tiles * s > 2 * kCfgSlots[cfg]) break;
     const int64_t kps = ceil_div(kslices, s);

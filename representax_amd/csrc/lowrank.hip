@@ -10,6 +10,7 @@
 
 #include "common.h"
 #include "kernels.h"
+#include "tuning.h"
 
 namespace rpx {
 
@@ -341,7 +342,11 @@ TiledPlan plan_tiled(int64_t m, int64_t p, int64_t q) {
   const int64_t bq = pl.wide_p ? 16 : 64;
   pl.gp = ceil_div(p, bp);
   pl.gq = ceil_div(q, bq);
-  int64_t want = ceil_div(512, pl.gp * pl.gq);
+  // 384 workgroups per product: at 4096 tokens (768 -> 3072, r 16) the dA + dB
+  // launch fits one round of three workgroups per CU (bwd 60.7 -> 56.9 us);
+  // the train-step shapes are unchanged within run-to-run noise
+  const int target = tune(kTuneRankBlocks) > 0 ? tune(kTuneRankBlocks) : 384;
+  int64_t want = ceil_div(target, pl.gp * pl.gq);
   const int64_t max_splits = ceil_div(m, 64);
   if (want > max_splits) want = max_splits;
   if (want < 1) want = 1;
@@ -498,7 +503,12 @@ hipError_t launch_rank_nt_g(const uint16_t* a, int64_t lda, const uint16_t* r_ma
                             int64_t m, int64_t rank, int64_t k, int ra, float a_scale,
                             uint16_t* out, int64_t ldo, hipStream_t stream) {
   if constexpr (G == 1) {
-    if (ceil_div(k, 128) > 4)
+    const int u = tune(kTuneRankNtU);
+    if (u == 16)
+      return launch_rank_nt_gu<1, 16>(a, lda, r_mat, ldr, m, rank, k, ra, a_scale, out, ldo, stream);
+    if (u == 4)
+      return launch_rank_nt_gu<1, 4>(a, lda, r_mat, ldr, m, rank, k, ra, a_scale, out, ldo, stream);
+    if (u == 8 || ceil_div(k, 128) > 4)
       return launch_rank_nt_gu<1, 8>(a, lda, r_mat, ldr, m, rank, k, ra, a_scale, out, ldo, stream);
   }
   return launch_rank_nt_gu<G, (G >= 4 ? 2 : 4)>(a, lda, r_mat, ldr, m, rank, k, ra, a_scale, out,

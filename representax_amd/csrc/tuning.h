@@ -22,7 +22,10 @@ enum TuneKnob : int {
   kTuneBand = 7,        // row-blocks per band of the GEMM tile order (0: planner)  RPX_GEMM_BAND
   kTuneDxPacked = 8,    // INT4 + LoRA input gradient's weight operand: -1 planner (bf16
                         // W_b^T), 0 bf16 W_b^T, 1 packed where allowed    RPX_DX_PACKED
-  kTuneCount = 9
+  kTuneRankBlocks = 9,  // workgroups a token-reduction product (dA, dB) aims for (0: planner)
+  kTuneRankNtU = 10,    // rank_nt 128-column steps in flight per wave (0: planner; 4, 8, 16)
+  kTuneFp8Splits = 11,  // fp8 GEMM split-K count (0: planner; else forced where it divides K)
+  kTuneCount = 12
 };
 
 // Current value of a knob.

@@ -185,6 +185,9 @@ TUNING_KNOBS = {
     "spin_limit": nat.TUNE_SPIN_LIMIT,
     "gemm_band": nat.TUNE_GEMM_BAND,
     "dx_packed": nat.TUNE_DX_PACKED,
+    "rank_blocks": nat.TUNE_RANK_BLOCKS,
+    "rank_nt_u": nat.TUNE_RANK_NT_U,
+    "fp8_splits": nat.TUNE_FP8_SPLITS,
 }
 
 

@@ -506,3 +506,31 @@ def test_skinny_slots_recover_after_expired_waits(form):
             torch.cuda.synchronize()
             assert torch.equal(y1, y0) and torch.equal(h1, h0)
         assert ops.check_device_errors() == 0
+
+
+@pytest.mark.parametrize("rank_blocks", [16, 100, 384, 2048])
+@pytest.mark.parametrize("m,k,n,r,group", [(700, 320, 448, 16, 64), (1000, 256, 192, 32, None)])
+def test_backward_every_token_split(rank_blocks, m, k, n, r, group):
+    """dA / dB under every token-split plan the rank-r reduction can take (one
+    to many token chunks per tile, ragged last chunk), against the oracle."""
+
+    x, packed, scales, a, b, bias_bits, gy = _lora_case(m, k, n, r, group, seed=m + rank_blocks)
+    alpha = 2.0 * r
+    _, h_o = olora.lora_forward(x, packed, scales, a, b, alpha=alpha, rank=r, group_size=group)
+    dx_o, da_o, db_o = olora.lora_backward(gy, x, packed, scales, a, b, h_o, alpha=alpha, rank=r,
+                                           group_size=group)
+    xd = to_dev_bf16(x)
+    pd = to_dev(packed)
+    sd = to_dev(scales.view(np.int16)).view(torch.uint16)
+    ad = to_dev_bf16(a)
+    bd = to_dev_bf16(b)
+    with ops.tuning(rank_blocks=rank_blocks):
+        _, h = ops.int4lora_forward(xd, pd, sd, ad, bd, scaling=alpha / r, group_size=group)
+        dx, da, db = ops.int4lora_backward(to_dev_bf16(gy), xd, pd, sd, ad, bd, h,
+                                           scaling=alpha / r, group_size=group)
+    torch.cuda.synchronize()
+    assert rel_l2(from_dev(dx), dx_o) < TOL
+    assert rel_l2(from_dev(da), da_o) < TOL
+    assert rel_l2(from_dev(db), db_o) < TOL
+    assert np.array_equal(bf16_values(from_dev(da)), from_dev(da))
+    assert np.array_equal(bf16_values(from_dev(db)), from_dev(db))
