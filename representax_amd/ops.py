@@ -172,6 +172,50 @@ def group_arg(group_size: int | None, k: int) -> int:
     return 0 if group_size is None or group_size == k else int(group_size)
 
 
+def _shape_error(what: str, got, want) -> ValueError:
+    return ValueError(f"{what}: shape {tuple(got)}, expected {tuple(want)}")
+
+
+def _lora_dims(x2d, packed, scale_bits, lora_a, lora_b, group_size, bias_bits=None):
+    """``(m, k, n, r)`` of an INT4 + LoRA call after checking that every
+    operand has the extent the kernels will read: packed ``[N, ceil(K/2)]``
+    uint8, N * (K / G) scale values (N for one scale per row), A ``[r, K]``,
+    B ``[N, r]`` and N bias values. The C ABI takes plain pointers and sizes,
+    so a mismatched tensor would be read past its end; this raises
+    ``ValueError`` before any launch. (Written for host time: each torch
+    attribute is read once.)"""
+
+    xs = x2d.shape
+    if len(xs) != 2:
+        raise ValueError(f"x must be 2-D [M, K], got shape {tuple(xs)}")
+    m, k = xs
+    ps = packed.shape
+    if packed.dtype != torch.uint8 or len(ps) != 2:
+        raise ValueError(f"packed weight must be uint8 [N, ceil(K/2)], got {packed.dtype} "
+                         f"{tuple(ps)}")
+    n, pc = ps
+    if pc != (k + 1) // 2:
+        raise _shape_error("packed weight", ps, (n, (k + 1) // 2))
+    g = 0 if group_size is None or group_size == k else group_size
+    groups = k // g if g > 0 and k % g == 0 else 1
+    if scale_bits.numel() != n * groups:
+        raise _shape_error("scale_bits", scale_bits.shape, (n, groups))
+    sa = lora_a.shape
+    if len(sa) != 2 or sa[1] != k:
+        raise _shape_error("lora_a", sa, ("r", k))
+    r = sa[0]
+    if lora_b.shape != (n, r):
+        raise _shape_error("lora_b", lora_b.shape, (n, r))
+    if bias_bits is not None and bias_bits.numel() != n:
+        raise _shape_error("bias", bias_bits.shape, (n,))
+    return m, k, n, r
+
+
+def _check_extent(name: str, t, shape) -> None:
+    if t is not None and tuple(t.shape) != tuple(shape):
+        raise _shape_error(name, t.shape, shape)
+
+
 # ---------------------------------------------------------------------------
 # Kernel-variant knobs and the device error word
 # ---------------------------------------------------------------------------
@@ -305,18 +349,15 @@ def _forward_ready(fast, x2d, packed, scale_bits, a, b, scaling, group_size, bia
     or raises."""
 
     dt = x2d.dtype
-    if (a.dtype != dt or b.dtype != dt or scale_bits.dtype != torch.uint16
-            or x2d.dim() != 2):
+    if a.dtype != dt or b.dtype != dt or scale_bits.dtype != torch.uint16:
         return None
+    m, k, n, r = _lora_dims(x2d, packed, scale_bits, a, b, group_size, bias_bits)
     index = x2d.get_device()
     ptrs = _ready(index, (x2d, packed, scale_bits, a, b))
     ok, pb = _bias_ready(bias_bits, index)
     if index < 0 or ptrs is None or not ok:
         return None
     code = _dtype_code(dt)
-    m, k = x2d.shape
-    n = packed.shape[-2]
-    r = a.shape[0]
     g = group_arg(group_size, k)
     device = x2d.device
     y = torch.empty((m, n), dtype=dt, device=device)
@@ -349,10 +390,8 @@ def int4lora_forward(x2d, packed, scale_bits, lora_a_c, lora_b_c, *, scaling: fl
                              group_size, bias_bits, need_h)
         if out is not None:
             return out
+    m, k, n, r = _lora_dims(x2d, packed, scale_bits, lora_a_c, lora_b_c, group_size, bias_bits)
     device = _on_device(x2d, packed, scale_bits, lora_a_c, lora_b_c, bias_bits)
-    m, k = x2d.shape
-    n = packed.shape[-2]
-    r = lora_a_c.shape[0]
     dt = x2d.dtype
     code = _dtype_code(dt)
     x2d = _aligned(x2d)
@@ -427,11 +466,11 @@ def _multi_ready(fast, x2d, projections, need_h):
     for packed, scale_bits, a, b, scaling, group_size, bias_bits in projections:
         if a.dtype != dt or b.dtype != dt or scale_bits.dtype != torch.uint16:
             return None
+        _, _, n, r = _lora_dims(x2d, packed, scale_bits, a, b, group_size, bias_bits)
         ptrs = _ready(index, (packed, scale_bits, a, b))
         ok, pb = _bias_ready(bias_bits, index)
         if ptrs is None or not ok:
             return None
-        n, r = packed.shape[-2], a.shape[0]
         dims.append((n, r))
         # y's and h's addresses (the last two fields) are filled in below;
         # the size query reads the shapes only
@@ -478,6 +517,7 @@ def int4lora_forward_multi(x2d, projections, need_h: bool = True):
     tensors = [x2d]
     for p in projections:
         tensors += [p[0], p[1], p[2], p[3], p[6]]
+        _lora_dims(x2d, p[0], p[1], p[2], p[3], p[5], p[6])
     device = _on_device(*tensors)
     m, k = x2d.shape
     dt = x2d.dtype
@@ -543,10 +583,10 @@ def int4lora_backward(grad, x2d, packed, scale_bits, lora_a_c, lora_b_c, h, *, s
                       group_size: int | None = None):
     """Return ``(dx [M, K], dA f32 [r, K], dB f32 [N, r])``."""
 
+    m, k, n, r = _lora_dims(x2d, packed, scale_bits, lora_a_c, lora_b_c, group_size)
+    _check_extent("grad", grad, (m, n))
+    _check_extent("h", h, (m, r))
     device = _on_device(grad, x2d, packed, scale_bits, lora_a_c, lora_b_c, h)
-    m, k = x2d.shape
-    n = packed.shape[-2]
-    r = lora_a_c.shape[0]
     dt = x2d.dtype
     code = _dtype_code(dt)
     grad = _aligned(grad.to(dt))
@@ -576,10 +616,9 @@ def int4lora_forward_act(x2d, packed, scale_bits, lora_a_c, lora_b_c, *, activat
     (``"gelu"``) or silu(gate) * z (``"silu_mul"``, gate [M, N])."""
 
     act = ACTIVATIONS[activation]
+    m, k, n, r = _lora_dims(x2d, packed, scale_bits, lora_a_c, lora_b_c, group_size, bias_bits)
+    _check_extent("gate", gate, (m, n))
     device = _on_device(x2d, packed, scale_bits, lora_a_c, lora_b_c, bias_bits, gate)
-    m, k = x2d.shape
-    n = packed.shape[-2]
-    r = lora_a_c.shape[0]
     dt = x2d.dtype
     code = _dtype_code(dt)
     x2d = _aligned(x2d)
@@ -609,10 +648,12 @@ def int4lora_backward_act(grad, x2d, packed, scale_bits, lora_a_c, lora_b_c, h, 
     added to ``z``, the gradient accumulated so far for a shared input."""
 
     act = ACTIVATIONS[activation]
+    m, k, n, r = _lora_dims(x2d, packed, scale_bits, lora_a_c, lora_b_c, group_size)
+    _check_extent("grad", grad, (m, n))
+    _check_extent("h", h, (m, r))
+    _check_extent("z", z, (m, k))
+    _check_extent("gate", gate, (m, k))
     device = _on_device(grad, x2d, packed, scale_bits, lora_a_c, lora_b_c, h, z, gate)
-    m, k = x2d.shape
-    n = packed.shape[-2]
-    r = lora_a_c.shape[0]
     dt = x2d.dtype
     code = _dtype_code(dt)
     grad = _aligned(grad.to(dt))
@@ -667,9 +708,7 @@ def int4lora_forward_promoted(x2d, packed, scale_bits, lora_a, lora_b, *, scalin
     device = _on_device(x2d, packed, scale_bits, lora_a, lora_b, bias_bits)
     if x2d.dtype != BF16 or lora_a.dtype != F32 or lora_b.dtype != F32:
         raise TypeError("the promoted INT4 + LoRA linear takes bf16 x and float32 masters")
-    m, k = x2d.shape
-    n = packed.shape[-2]
-    r = lora_a.shape[0]
+    m, k, n, r = _lora_dims(x2d, packed, scale_bits, lora_a, lora_b, group_size, bias_bits)
     x2d = _aligned(x2d)
     y = torch.empty((m, n), dtype=F32, device=device)
     h = torch.empty((m, r), dtype=F32, device=device)
@@ -688,10 +727,10 @@ def int4lora_backward_promoted(grad, x2d, packed, scale_bits, lora_a, lora_b, h,
     """``(dx bf16 [M, K], dA f32 [r, K], dB f32 [N, r])`` of the promoted
     forward, from the float32 output gradient."""
 
+    m, k, n, r = _lora_dims(x2d, packed, scale_bits, lora_a, lora_b, group_size)
+    _check_extent("grad", grad, (m, n))
+    _check_extent("h", h, (m, r))
     device = _on_device(grad, x2d, packed, scale_bits, lora_a, lora_b, h)
-    m, k = x2d.shape
-    n = packed.shape[-2]
-    r = lora_a.shape[0]
     grad = _aligned(grad.to(F32))
     dx = torch.empty((m, k), dtype=BF16, device=device)
     d_a = torch.empty((r, k), dtype=F32, device=device)
@@ -1050,6 +1089,12 @@ def fp8_linear_backward(left, right, grad, scales, *, need_left=True, need_right
     """``(d_left [M,K] or None, d_right [K,N] or None)`` in the operand dtypes,
     re-quantizing the bf16 operands with the forward's scales."""
 
+    if left.dim() != 2 or right.dim() != 2 or left.shape[1] != right.shape[0]:
+        raise ValueError(f"fp8 linear needs left [M, K] and right [K, N]; got "
+                         f"{tuple(left.shape)} and {tuple(right.shape)}")
+    _check_extent("grad", grad, (left.shape[0], right.shape[1]))
+    if scales.numel() != 2:
+        raise _shape_error("scales", scales.shape, (2,))
     device = _on_device(left, right, grad, scales)
     left = left.contiguous()
     right = _dense_2d(right)
@@ -1081,6 +1126,12 @@ def fp8_linear_backward_codes(codes, scales, grad, *, k, dtype, right_transposed
     """Backward from the codes saved by ``fp8_linear_forward(save_codes=True)``."""
 
     left_t, right_c = codes
+    if grad.dim() != 2:
+        raise ValueError(f"grad must be 2-D [M, N], got shape {tuple(grad.shape)}")
+    _check_extent("saved left codes", left_t, (k, grad.shape[0]))
+    _check_extent("saved right codes", right_c, (k, grad.shape[1]))
+    if scales.numel() != 2:
+        raise _shape_error("scales", scales.shape, (2,))
     device = _on_device(left_t, right_c, grad, scales)
     grad = grad.contiguous()
     m, n = grad.shape

@@ -221,3 +221,86 @@ def test_train_step_rejects_unknown_policies():
     with torch.no_grad():
         with pytest.raises(ValueError, match="rematerialization"):
             run_layer(torch.nn.Identity(), "sometimes", torch.zeros(1))
+
+
+def _lora_operands(m=4, k=64, n=32, r=4, group=None):
+    packed = torch.zeros((n, (k + 1) // 2), dtype=torch.uint8)
+    groups = 1 if group is None else k // group
+    scales = torch.zeros((n, groups), dtype=torch.uint16)
+    x = torch.zeros((m, k), dtype=torch.bfloat16)
+    a = torch.zeros((r, k), dtype=torch.bfloat16)
+    b = torch.zeros((n, r), dtype=torch.bfloat16)
+    return x, packed, scales, a, b
+
+
+@pytest.mark.parametrize("case", ["packed_width", "packed_dtype", "scales", "lora_a", "lora_b",
+                                  "bias", "x_dim"])
+def test_int4lora_forward_rejects_mismatched_extents(case):
+    """The C ABI takes pointers and sizes only, so the wrappers check that every
+    operand holds what the kernels will read; a mismatch is a ValueError raised
+    before any device work (here on CPU tensors, before the device check)."""
+
+    from representax_amd import ops
+
+    x, packed, scales, a, b = _lora_operands(group=16)
+    bias = None
+    if case == "packed_width":
+        packed = torch.zeros((32, 31), dtype=torch.uint8)
+    elif case == "packed_dtype":
+        packed = packed.to(torch.int16)
+    elif case == "scales":
+        scales = torch.zeros((32, 1), dtype=torch.uint16)  # group 16 needs 4 per row
+    elif case == "lora_a":
+        a = torch.zeros((4, 63), dtype=torch.bfloat16)
+    elif case == "lora_b":
+        b = torch.zeros((32, 5), dtype=torch.bfloat16)
+    elif case == "bias":
+        bias = torch.zeros(31, dtype=torch.uint16)
+    elif case == "x_dim":
+        x = x.reshape(1, 4, 64)
+    with pytest.raises(ValueError):
+        ops.int4lora_forward(x, packed, scales, a, b, scaling=2.0, group_size=16, bias_bits=bias)
+
+
+def test_int4lora_backward_rejects_mismatched_gradients():
+    from representax_amd import ops
+
+    x, packed, scales, a, b = _lora_operands()
+    h = torch.zeros((4, 4), dtype=torch.bfloat16)
+    with pytest.raises(ValueError):
+        ops.int4lora_backward(torch.zeros((4, 31), dtype=torch.bfloat16), x, packed, scales, a, b,
+                              h, scaling=2.0)
+    with pytest.raises(ValueError):
+        ops.int4lora_backward(torch.zeros((4, 32), dtype=torch.bfloat16), x, packed, scales, a, b,
+                              torch.zeros((4, 3), dtype=torch.bfloat16), scaling=2.0)
+    with pytest.raises(ValueError):
+        ops.int4lora_backward_act(torch.zeros((4, 32), dtype=torch.bfloat16), x, packed, scales, a,
+                                  b, h, activation="gelu", z=torch.zeros((4, 32)), scaling=2.0)
+
+
+def test_int4lora_matching_extents_reach_the_device_check():
+    """With every extent right, a CPU tensor is refused by the device check
+    (no CPU fallback)."""
+
+    from representax_amd import ops
+
+    x, packed, scales, a, b = _lora_operands(group=16)
+    with pytest.raises(RuntimeError, match="ROCm"):
+        ops.int4lora_forward(x, packed, scales, a, b, scaling=2.0, group_size=16)
+
+
+def test_fp8_backward_rejects_mismatched_extents():
+    from representax_amd import ops
+
+    left = torch.zeros((8, 16), dtype=torch.bfloat16)
+    right = torch.zeros((16, 4), dtype=torch.bfloat16)
+    scales = torch.ones(2)
+    with pytest.raises(ValueError):
+        ops.fp8_linear_backward(left, right, torch.zeros((8, 5), dtype=torch.bfloat16), scales)
+    codes = (torch.zeros((16, 8), dtype=torch.uint8), torch.zeros((16, 4), dtype=torch.uint8))
+    with pytest.raises(ValueError):
+        ops.fp8_linear_backward_codes(codes, scales, torch.zeros((8, 4), dtype=torch.bfloat16),
+                                      k=15, dtype=torch.bfloat16, right_transposed=False)
+    with pytest.raises(ValueError):
+        ops.fp8_linear_backward_codes(codes, scales, torch.zeros((9, 4), dtype=torch.bfloat16),
+                                      k=16, dtype=torch.bfloat16, right_transposed=False)
