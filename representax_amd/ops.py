@@ -326,9 +326,12 @@ def int4_merge(packed, scale_bits, lora_a, lora_b, *, alpha: float, rank: int, i
                group_size: int | None = None) -> torch.Tensor:
     """float32 ``f32(W_b) + (B @ A) * (alpha / rank)`` for one ``[N, K]`` slice."""
 
-    device = _on_device(packed, scale_bits, lora_a, lora_b)
-    n = packed.shape[-2]
     k = int(input_size)
+    _, _, n, _ = _lora_dims(packed.new_empty((0, k), dtype=torch.bfloat16), packed, scale_bits,
+                            lora_a, lora_b, group_size)
+    if lora_a.shape[0] != int(rank):
+        raise _shape_error("lora_a", lora_a.shape, (int(rank), k))
+    device = _on_device(packed, scale_bits, lora_a, lora_b)
     out = torch.empty((n, k), dtype=F32, device=device)
     nat.call("rpx_int4_merge", _ptr(packed.contiguous()), _ptr(_u16(scale_bits).contiguous()),
              _ptr(lora_a.to(F32).contiguous()), _ptr(lora_b.to(F32).contiguous()), n, k,
@@ -1015,6 +1018,11 @@ def fp8_encode_selfcheck(fmt: str, first: int = 0, count: int = 1 << 31, blocks:
 def fp8_gemm(a_codes, fmt_a, scale_a, b_codes, fmt_b, scale_b, out_dtype=BF16):
     """``((a [M,K] . b [N,K]^T) * s_a) * s_b`` -> ``[M, N]``."""
 
+    if a_codes.dim() != 2 or b_codes.dim() != 2 or a_codes.shape[1] != b_codes.shape[1]:
+        raise ValueError(f"fp8 GEMM needs a [M, K] and b [N, K] codes; got {tuple(a_codes.shape)} "
+                         f"and {tuple(b_codes.shape)}")
+    if a_codes.element_size() != 1 or b_codes.element_size() != 1:
+        raise ValueError("fp8 GEMM operands are one-byte codes")
     device = _on_device(a_codes, b_codes, scale_a, scale_b)
     m, k = a_codes.shape
     n = b_codes.shape[0]
