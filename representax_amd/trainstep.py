@@ -491,10 +491,12 @@ class MNRTrainStep:
     views of it, and so are their gradients), so the norm, the clip, AdamW
     and the finite guard are a handful of kernels per step. Their bf16
     compute views (``compute_parameter``) are slices of one bf16 buffer
-    converted from the masters once per step, each a leaf whose gradient
-    accumulates into one bf16 gradient buffer that becomes the masters'
-    float32 gradient (the transpose of the cast): three kernels per step
-    instead of a cast per parameter use and per gradient.
+    converted from the masters once per step, each a leaf whose gradient is
+    left to autograd (no preset ``.grad``, so each view takes its gradient
+    tensor as returned, with no accumulate kernel) and then gathered into the
+    masters' float32 gradient by one concatenation (the transpose of the
+    cast): two kernels per step instead of a cast per parameter use and an
+    add per gradient.
     ``capture()`` records forward, backward and the update into one HIP graph
     over static input buffers; ``__call__`` replays it (or runs eagerly
     before capture).
@@ -519,15 +521,15 @@ class MNRTrainStep:
         self.flat = torch.nn.Parameter(torch.cat([p.detach().reshape(-1) for p in self.params]))
         self.flat.grad = torch.zeros_like(self.flat)
         self.flat_c = torch.zeros(self.flat.numel(), dtype=torch.bfloat16, device=device)
-        self.flat_gc = torch.zeros_like(self.flat_c)
         self.views: dict[int, torch.Tensor] = {}
+        self.view_list: list[torch.Tensor] = []
         offset = 0
         for p, n in zip(self.params, sizes):
             p.data = self.flat.data[offset:offset + n].view_as(p)
             p.grad = self.flat.grad[offset:offset + n].view_as(p)
             view = self.flat_c[offset:offset + n].view_as(p).detach().requires_grad_(True)
-            view.grad = self.flat_gc[offset:offset + n].view_as(p)
             self.views[id(p)] = view
+            self.view_list.append(view)
             offset += n
         self.optimizer = torch.optim.AdamW([self.flat], lr=lr, weight_decay=0.01,
                                            capturable=True, foreach=False)
@@ -554,7 +556,8 @@ class MNRTrainStep:
         return [self.flat.data, st["exp_avg"], st["exp_avg_sq"], st["step"]]
 
     def _step(self) -> None:
-        self.flat_gc.zero_()
+        for view in self.view_list:
+            view.grad = None
         with torch.no_grad():
             self.flat_c.copy_(self.flat)
         with precision_context(self.policy), compute_views(self.views):
@@ -564,7 +567,10 @@ class MNRTrainStep:
             loss = mnr_loss(emb[:b], emb[b:], self.scale)
         loss.backward()
         grad = self.flat.grad
-        grad.copy_(self.flat_gc)
+        # bf16 view gradients -> the masters' float32 gradient, one kernel (a
+        # view that took no part in the loss has gradient zero)
+        torch.cat([(v.grad if v.grad is not None else torch.zeros_like(v)).reshape(-1)
+                   for v in self.view_list], out=grad)
         norm = torch.linalg.vector_norm(grad, dtype=torch.float32)
         finite = torch.isfinite(loss.detach()) & torch.isfinite(norm)
         if self.max_grad_norm is not None:
