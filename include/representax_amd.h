@@ -179,7 +179,11 @@ int rpx_int4lora_forward(const void* x, int dtype, int64_t m, int64_t k, const u
  * bert/model.py's query / key / value and qwen3_vl/text.py's gate / up.
  * For bf16 with M <= 4 (the skinny-M regime), one rank and at most 4
  * projections, all of them run in one pair of launches instead of one pair
- * each; otherwise they run one after another. */
+ * each. Above the skinny sizes, when every projection takes the fused MFMA
+ * path and their ranks add up to at most 64 in 16-rank blocks (q / k / v at
+ * rank 16, gate / up at rank 32), one launch forms every h from one pass
+ * over x, bit-identical to the per-projection h, and then each projection's
+ * GEMM runs. Otherwise they run one after another. */
 typedef struct rpx_int4lora_projection {
   const uint8_t* packed;       /* [n, ceil(k/2)] */
   const uint16_t* scale_bits;  /* [n] or [n, k / group_size] */

@@ -416,6 +416,7 @@ struct ActIO {
   const uint16_t* aux2 = nullptr;
   uint16_t* pre_out = nullptr;  // forward modes: the linear's own output
   uint16_t* out2 = nullptr;     // SiLU-mul backward: d gate
+  bool h_given = false;         // forward: h = x A^T is already in h (MFMA path only)
 };
 
 int int4lora_forward_impl(const void* x, int dtype, int64_t m, int64_t k, const uint8_t* packed,
@@ -479,12 +480,14 @@ int int4lora_forward_impl(const void* x, int dtype, int64_t m, int64_t k, const 
             "int4lora_forward: skinny-M kernels");
     return finish_act();
   }
+  if (act.h_given && !fast) return fail_invalid("int4lora_forward: a given h needs the MFMA path");
   if (fast) {
     const uint16_t* xb = static_cast<const uint16_t*>(x);
     uint16_t* hb = static_cast<uint16_t*>(h);
-    RPX_HIP(launch_rank_nt(xb, k, static_cast<const uint16_t*>(lora_a), k, m, rank, k, false, 1.0f,
-                           hb, rank, st),
-            "int4lora_forward: adapter down-projection");
+    if (!act.h_given)
+      RPX_HIP(launch_rank_nt(xb, k, static_cast<const uint16_t*>(lora_a), k, m, rank, k, false,
+                             1.0f, hb, rank, st),
+              "int4lora_forward: adapter down-projection");
     LowRankEpilogue epi;
     epi.rows = static_cast<const uint16_t*>(lora_b);
     epi.rows_sn = rank;
@@ -574,6 +577,35 @@ bool multi_fused_shape(int dtype, int64_t m, int64_t k, int count,
   return skinny2_multi_ok(m, k, count, out);
 }
 
+// The MFMA form of rpx_int4lora_forward_multi above the small-M sizes: every
+// projection on the fused dequant GEMM path (bf16, not skinny, the usual
+// alignment), their adapters together at most four 16-rank blocks. The h of
+// every projection then comes from one pass over x, and each GEMM takes its
+// h as given.
+bool multi_shared_h(const void* x, int dtype, int64_t m, int64_t k, int count,
+                    const rpx_int4lora_projection* proj) {
+  if (x == nullptr || dtype != kBF16 || count < 2 || m < 1) return false;
+  int blocks = 0;
+  for (int i = 0; i < count; ++i) {
+    const rpx_int4lora_projection& q = proj[i];
+    int64_t ng = 1, g = k;
+    if (q.group_size > 0 && q.group_size != k) {
+      if (k % q.group_size != 0) return false;
+      ng = k / q.group_size;
+      g = q.group_size;
+    }
+    if (q.n < 1 || q.rank < 1 || q.rank > q.n || q.rank > k) return false;
+    if (!lora_fast_shape(dtype, k, ng, g, q.rank) || lora_skinny(dtype, m, q.n, k, ng, g, q.rank))
+      return false;
+    if (q.packed == nullptr || q.scale_bits == nullptr || q.lora_a == nullptr ||
+        q.lora_b == nullptr || q.y == nullptr || q.h == nullptr ||
+        !aligned16_all({x, q.packed, q.scale_bits, q.lora_a, q.y}))
+      return false;
+    blocks += rank_nt_blocks_of(q.rank);
+  }
+  return blocks <= rank_nt_max_blocks();
+}
+
 bool multi_fused(const void* x, int dtype, int64_t m, int64_t k, int count,
                  const rpx_int4lora_projection* proj, Skinny2Projection* out) {
   if (x == nullptr || !multi_fused_shape(dtype, m, k, count, proj, out)) return false;
@@ -628,11 +660,26 @@ int rpx_int4lora_forward_multi(const void* x, int dtype, int64_t m, int64_t k, i
             "rpx_int4lora_forward_multi: skinny-M kernels");
     return kOk;
   }
+  ActIO io;
+  if (multi_shared_h(x, dtype, m, k, count, projections)) {
+    const uint16_t* r_mats[4];
+    int64_t ranks[4];
+    uint16_t* outs[4];
+    for (int i = 0; i < count; ++i) {
+      r_mats[i] = static_cast<const uint16_t*>(projections[i].lora_a);
+      ranks[i] = projections[i].rank;
+      outs[i] = static_cast<uint16_t*>(projections[i].h);
+    }
+    RPX_HIP(launch_rank_nt_multi(static_cast<const uint16_t*>(x), k, m, k, count, r_mats, ranks,
+                                 outs, static_cast<hipStream_t>(stream)),
+            "rpx_int4lora_forward_multi: adapter down-projections");
+    io.h_given = true;
+  }
   for (int i = 0; i < count; ++i) {
     const rpx_int4lora_projection& q = projections[i];
-    RPX_TRY(rpx_int4lora_forward(x, dtype, m, k, q.packed, q.scale_bits, q.n, q.group_size,
-                                 q.bias_bits, q.lora_a, q.lora_b, q.rank, q.scaling, q.y, q.h,
-                                 workspace, workspace_bytes, stream));
+    RPX_TRY(int4lora_forward_impl(x, dtype, m, k, q.packed, q.scale_bits, q.n, q.group_size,
+                                  q.bias_bits, q.lora_a, q.lora_b, q.rank, q.scaling, q.y, q.h,
+                                  workspace, workspace_bytes, stream, io));
   }
   return kOk;
 }

@@ -130,6 +130,15 @@ hipError_t launch_act(int mode, const uint16_t* v, const uint16_t* aux, const ui
 hipError_t launch_rank_nt(const uint16_t* a, int64_t lda, const uint16_t* r_mat, int64_t ldr,
                           int64_t m, int64_t rank, int64_t k, bool round_a, float a_scale,
                           uint16_t* out, int64_t ldo, hipStream_t stream);
+// h_i = bf16(A . R_i^T) for several R_i [rank_i, K] (row stride K) of one A
+// [M, K] in one launch, h_i [M, rank_i] dense; each h_i has the bits
+// launch_rank_nt gives it alone. At most rank_nt_max_blocks() 16-rank blocks
+// in all (rank_nt_blocks_of(rank_i) each), else hipErrorInvalidValue.
+int rank_nt_blocks_of(int64_t rank);
+constexpr int rank_nt_max_blocks() { return 4; }
+hipError_t launch_rank_nt_multi(const uint16_t* a, int64_t lda, int64_t m, int64_t k, int count,
+                                const uint16_t* const* r_mats, const int64_t* ranks,
+                                uint16_t* const* outs, hipStream_t stream);
 // out[P, Q] = f32(bf16(sum_m op(X[m, p]) * Y[m, q])); X [M, P] (ldx), Y [M, Q] (ldy)
 // bf16 row-major; op as above on X. Uses `partials` (fp32) workspace of
 // rank_tn_workspace_floats(...) elements.

@@ -42,14 +42,30 @@ __device__ __forceinline__ u32x4_t load8(const uint16_t* p, int valid, bool alig
   return u32x4_t{w[0], w[1], w[2], w[3]};
 }
 
+// Output column blocks of the rank-r row kernel: block b is up to 16 rows of
+// some R (the rank rows r[b], r[b] + ldr[b], ..., `valid[b]` of them) and
+// the matching columns out[b], out[b] + 1, ... of an output with row stride
+// ldo[b]. One matrix R [rank, K] is blocks of 16 consecutive rows; several
+// adapters of one input (shared-input projections) are their blocks side by
+// side.
+constexpr int kRankNtMaxBlocks = 4;
+struct RankNtBlocks {
+  const uint16_t* r[kRankNtMaxBlocks];
+  int64_t ldr[kRankNtMaxBlocks];
+  uint16_t* out[kRankNtMaxBlocks];
+  int64_t ldo[kRankNtMaxBlocks];
+  int valid[kRankNtMaxBlocks];
+};
+
 // One workgroup per 16 G output rows (G row groups of 16); its four waves
 // split K in interleaved 32-deep steps and reduce in LDS. Every fragment of R
 // a wave loads serves the G row groups, so R's L2 traffic per row falls by G.
+// Each column block's sums are independent of the others', so a block gives
+// the same bits whichever blocks share its launch.
 template <int RB, int G, int U>
 __global__ void __launch_bounds__(256)
-    k_rank_nt(const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ R,
-              int64_t ldr, int64_t M, int64_t rank, int64_t K, int round_a, float a_scale,
-              uint16_t* __restrict__ out, int64_t ldo) {
+    k_rank_nt(const uint16_t* __restrict__ A, int64_t lda, RankNtBlocks blk, int64_t M, int64_t K,
+              int round_a, float a_scale) {
   __shared__ float red[3][G][RB][64][4];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -57,7 +73,10 @@ __global__ void __launch_bounds__(256)
   const int64_t m0 = static_cast<int64_t>(blockIdx.x) * 16 * G;
   const int koff = (lane >> 4) * 8;
   const bool a_al = (lda % 8 == 0) && ((reinterpret_cast<uintptr_t>(A) & 15) == 0);
-  const bool r_al = (ldr % 8 == 0) && ((reinterpret_cast<uintptr_t>(R) & 15) == 0);
+  bool r_al[RB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+    r_al[rb] = (blk.ldr[rb] % 8 == 0) && ((reinterpret_cast<uintptr_t>(blk.r[rb]) & 15) == 0);
   f32x4_t acc[G][RB];
 #pragma unroll
   for (int gi = 0; gi < G; ++gi)
@@ -79,8 +98,8 @@ __global__ void __launch_bounds__(256)
       }
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) {
-        const int64_t j = rb * 16 + (lane & 15);
-        rv[u][rb] = load8(R + j * ldr + kc, j < rank ? kv : 0, r_al);
+        const int j = lane & 15;
+        rv[u][rb] = load8(blk.r[rb] + j * blk.ldr[rb] + kc, j < blk.valid[rb] ? kv : 0, r_al[rb]);
       }
     }
 #pragma unroll
@@ -112,13 +131,13 @@ __global__ void __launch_bounds__(256)
   for (int gi = 0; gi < G; ++gi)
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
-      const int j = rb * 16 + (lane & 15);
+      const int j = lane & 15;
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int64_t mm = m0 + 16 * gi + 4 * (lane >> 4) + v;
         const float s = acc[gi][rb][v] + red[0][gi][rb][lane][v] + red[1][gi][rb][lane][v] +
                         red[2][gi][rb][lane][v];
-        if (mm < M && j < rank) out[mm * ldo + j] = f32_to_bf16(s);
+        if (mm < M && j < blk.valid[rb]) blk.out[rb][mm * blk.ldo[rb] + j] = f32_to_bf16(s);
       }
     }
 }
@@ -477,21 +496,29 @@ int rank_nt_groups(int64_t m) {
 }
 
 template <int G, int U>
-hipError_t launch_rank_nt_gu(const uint16_t* a, int64_t lda, const uint16_t* r_mat, int64_t ldr,
-                             int64_t m, int64_t rank, int64_t k, int ra, float a_scale,
-                             uint16_t* out, int64_t ldo, hipStream_t stream) {
+hipError_t launch_rank_nt_gu(const uint16_t* a, int64_t lda, const RankNtBlocks& blk, int nblk,
+                             int64_t m, int64_t k, int ra, float a_scale, hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>(ceil_div(m, 16 * G)));
-  if (rank <= 16)
-    hipLaunchKernelGGL((k_rank_nt<1, G, U>), grid, dim3(256), 0, stream, a, lda, r_mat, ldr, m,
-                       rank, k, ra, a_scale, out, ldo);
-  else if (rank <= 32)
-    hipLaunchKernelGGL((k_rank_nt<2, G, U>), grid, dim3(256), 0, stream, a, lda, r_mat, ldr, m,
-                       rank, k, ra, a_scale, out, ldo);
-  else if (rank <= 64)
-    hipLaunchKernelGGL((k_rank_nt<4, G, U>), grid, dim3(256), 0, stream, a, lda, r_mat, ldr, m,
-                       rank, k, ra, a_scale, out, ldo);
-  else
-    return hipErrorInvalidValue;
+  switch (nblk) {
+    case 1:
+      hipLaunchKernelGGL((k_rank_nt<1, G, U>), grid, dim3(256), 0, stream, a, lda, blk, m, k, ra,
+                         a_scale);
+      break;
+    case 2:
+      hipLaunchKernelGGL((k_rank_nt<2, G, U>), grid, dim3(256), 0, stream, a, lda, blk, m, k, ra,
+                         a_scale);
+      break;
+    case 3:
+      hipLaunchKernelGGL((k_rank_nt<3, G, U>), grid, dim3(256), 0, stream, a, lda, blk, m, k, ra,
+                         a_scale);
+      break;
+    case 4:
+      hipLaunchKernelGGL((k_rank_nt<4, G, U>), grid, dim3(256), 0, stream, a, lda, blk, m, k, ra,
+                         a_scale);
+      break;
+    default:
+      return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 
@@ -499,35 +526,65 @@ hipError_t launch_rank_nt_gu(const uint16_t* a, int64_t lda, const uint16_t* r_m
 // whole K range in one round when it is short and a workgroup holds one row
 // group (h = x A^T at K = 768: one memory round trip instead of two).
 template <int G>
-hipError_t launch_rank_nt_g(const uint16_t* a, int64_t lda, const uint16_t* r_mat, int64_t ldr,
-                            int64_t m, int64_t rank, int64_t k, int ra, float a_scale,
-                            uint16_t* out, int64_t ldo, hipStream_t stream) {
+hipError_t launch_rank_nt_g(const uint16_t* a, int64_t lda, const RankNtBlocks& blk, int nblk,
+                            int64_t m, int64_t k, int ra, float a_scale, hipStream_t stream) {
   if constexpr (G == 1) {
     const int u = tune(kTuneRankNtU);
-    if (u == 16)
-      return launch_rank_nt_gu<1, 16>(a, lda, r_mat, ldr, m, rank, k, ra, a_scale, out, ldo, stream);
-    if (u == 4)
-      return launch_rank_nt_gu<1, 4>(a, lda, r_mat, ldr, m, rank, k, ra, a_scale, out, ldo, stream);
+    if (u == 16) return launch_rank_nt_gu<1, 16>(a, lda, blk, nblk, m, k, ra, a_scale, stream);
+    if (u == 4) return launch_rank_nt_gu<1, 4>(a, lda, blk, nblk, m, k, ra, a_scale, stream);
     if (u == 8 || ceil_div(k, 128) > 4)
-      return launch_rank_nt_gu<1, 8>(a, lda, r_mat, ldr, m, rank, k, ra, a_scale, out, ldo, stream);
+      return launch_rank_nt_gu<1, 8>(a, lda, blk, nblk, m, k, ra, a_scale, stream);
   }
-  return launch_rank_nt_gu<G, (G >= 4 ? 2 : 4)>(a, lda, r_mat, ldr, m, rank, k, ra, a_scale, out,
-                                                ldo, stream);
+  return launch_rank_nt_gu<G, (G >= 4 ? 2 : 4)>(a, lda, blk, nblk, m, k, ra, a_scale, stream);
+}
+
+hipError_t launch_rank_nt_blocks(const uint16_t* a, int64_t lda, const RankNtBlocks& blk, int nblk,
+                                 int64_t m, int64_t k, int ra, float a_scale, hipStream_t stream) {
+  switch (rank_nt_groups(m)) {
+    case 4: return launch_rank_nt_g<4>(a, lda, blk, nblk, m, k, ra, a_scale, stream);
+    case 2: return launch_rank_nt_g<2>(a, lda, blk, nblk, m, k, ra, a_scale, stream);
+    default: return launch_rank_nt_g<1>(a, lda, blk, nblk, m, k, ra, a_scale, stream);
+  }
+}
+
+// Adds the 16-rank column blocks of one product (R [rank, K], out columns
+// [0, rank)) to blk; false when they do not fit.
+bool add_rank_blocks(RankNtBlocks& blk, int& nblk, const uint16_t* r_mat, int64_t ldr, int64_t rank,
+                     uint16_t* out, int64_t ldo) {
+  for (int64_t j0 = 0; j0 < rank; j0 += 16) {
+    if (nblk == kRankNtMaxBlocks) return false;
+    blk.r[nblk] = r_mat + j0 * ldr;
+    blk.ldr[nblk] = ldr;
+    blk.out[nblk] = out + j0;
+    blk.ldo[nblk] = ldo;
+    blk.valid[nblk] = static_cast<int>(rank - j0 < 16 ? rank - j0 : 16);
+    ++nblk;
+  }
+  return true;
 }
 
 hipError_t launch_rank_nt(const uint16_t* a, int64_t lda, const uint16_t* r_mat, int64_t ldr,
                           int64_t m, int64_t rank, int64_t k, bool round_a, float a_scale,
                           uint16_t* out, int64_t ldo, hipStream_t stream) {
   if (m == 0 || rank == 0) return hipSuccess;
-  const int ra = round_a ? 1 : 0;
-  switch (rank_nt_groups(m)) {
-    case 4:
-      return launch_rank_nt_g<4>(a, lda, r_mat, ldr, m, rank, k, ra, a_scale, out, ldo, stream);
-    case 2:
-      return launch_rank_nt_g<2>(a, lda, r_mat, ldr, m, rank, k, ra, a_scale, out, ldo, stream);
-    default:
-      return launch_rank_nt_g<1>(a, lda, r_mat, ldr, m, rank, k, ra, a_scale, out, ldo, stream);
-  }
+  RankNtBlocks blk{};
+  int nblk = 0;
+  if (!add_rank_blocks(blk, nblk, r_mat, ldr, rank, out, ldo)) return hipErrorInvalidValue;
+  return launch_rank_nt_blocks(a, lda, blk, nblk, m, k, round_a ? 1 : 0, a_scale, stream);
+}
+
+int rank_nt_blocks_of(int64_t rank) { return static_cast<int>(ceil_div(rank, 16)); }
+
+hipError_t launch_rank_nt_multi(const uint16_t* a, int64_t lda, int64_t m, int64_t k, int count,
+                                const uint16_t* const* r_mats, const int64_t* ranks,
+                                uint16_t* const* outs, hipStream_t stream) {
+  if (m == 0) return hipSuccess;
+  RankNtBlocks blk{};
+  int nblk = 0;
+  for (int i = 0; i < count; ++i)
+    if (!add_rank_blocks(blk, nblk, r_mats[i], k, ranks[i], outs[i], ranks[i]))
+      return hipErrorInvalidValue;
+  return launch_rank_nt_blocks(a, lda, blk, nblk, m, k, 0, 1.0f, stream);
 }
 
 int64_t rank_tn_workspace_floats(int64_t m, int64_t p, int64_t q) {

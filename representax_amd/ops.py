@@ -856,7 +856,9 @@ class Int4LoRASwiGLUMLPFn(torch.autograd.Function):
 
 class Int4LoRASharedInputFn(torch.autograd.Function):
     """Several INT4 + LoRA linears of one input (the q / k / v projections):
-    the forward runs them one after another; in the backward every input
+    the forward runs them as one multi-projection call (their adapters'
+    down-projections in one pass over the input, then one GEMM each); in the
+    backward every input
     gradient after the first is added to the running sum in its dx GEMM's
     epilogue (bf16, in projection order) instead of by a separate pass.
 
@@ -869,12 +871,21 @@ class Int4LoRASharedInputFn(torch.autograd.Function):
         views = args[:2 * n]
         leaves = args[2 * n:]
         outs, hs = [], []
-        for i in range(n):
-            packed, scales, bias, scaling, group = leaves[5 * i:5 * i + 5]
-            y, h = int4lora_forward(x2d, packed, scales, views[2 * i], views[2 * i + 1],
-                                    scaling=scaling, group_size=group, bias_bits=bias)
-            outs.append(y)
-            hs.append(h)
+        if x2d.dim() == 2 and x2d.shape[0] > SHARED_OUTPUT_ROWS:
+            # one call: the projections' h = x A^T come from one pass over x
+            # where the ranks allow, and each output is its own allocation
+            pairs = int4lora_forward_multi(
+                x2d, [(leaves[5 * i], leaves[5 * i + 1], views[2 * i], views[2 * i + 1],
+                       leaves[5 * i + 3], leaves[5 * i + 4], leaves[5 * i + 2]) for i in range(n)])
+            outs = [y for y, _ in pairs]
+            hs = [h for _, h in pairs]
+        else:
+            for i in range(n):
+                packed, scales, bias, scaling, group = leaves[5 * i:5 * i + 5]
+                y, h = int4lora_forward(x2d, packed, scales, views[2 * i], views[2 * i + 1],
+                                        scaling=scaling, group_size=group, bias_bits=bias)
+                outs.append(y)
+                hs.append(h)
         ctx.n = n
         ctx.cfg = [(leaves[5 * i + 3], leaves[5 * i + 4]) for i in range(n)]
         ctx.save_for_backward(x2d, *views, *[leaves[5 * i] for i in range(n)],

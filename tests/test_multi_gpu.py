@@ -227,3 +227,25 @@ def test_operands_in_other_forms_give_the_same_bits(m):
             assert torch.equal(ya, yb)
             if need_h:
                 assert torch.equal(ha, hb)
+
+
+@pytest.mark.parametrize("m", [2000, 16384, 32768])
+@pytest.mark.parametrize("k,outs", [(768, [(768, 16), (768, 16), (768, 16)]),
+                                    (2048, [(6144, 32), (6144, 32)]),
+                                    (1024, [(512, 48), (256, 16)])],
+                         ids=["bert-qkv", "qwen3-gate-up", "ranks-48-16"])
+def test_shared_down_projection_equals_single_calls(m, k, outs):
+    """Above the small-M sizes the projections' h come from one launch over x
+    (row groups of 16, 32 and 64 rows at these M); y and h must equal one
+    call per projection bit for bit."""
+
+    g = rng(900 + m + k)
+    projs = [_proj(g, n, k, r, 64, bias=(i == 0))[1] for i, (n, r) in enumerate(outs)]
+    xd = to_dev_bf16(bf16_values(g.standard_normal((m, k))))
+    got = ops.int4lora_forward_multi(xd, projs)
+    single = [ops.int4lora_forward(xd, d[0], d[1], d[2], d[3], scaling=d[4], group_size=d[5],
+                                   bias_bits=d[6]) for d in projs]
+    torch.cuda.synchronize()
+    for (y, h), (ys, hs) in zip(got, single):
+        assert torch.equal(h, hs)
+        assert torch.equal(y, ys)
