@@ -180,8 +180,8 @@ int rpx_int4lora_forward(const void* x, int dtype, int64_t m, int64_t k, const u
  * For bf16 with M <= 4 (the skinny-M regime), one rank and at most 4
  * projections, all of them run in one pair of launches instead of one pair
  * each. Above the skinny sizes, when every projection takes the fused MFMA
- * path and their ranks add up to at most 64 in 16-rank blocks (q / k / v at
- * rank 16, gate / up at rank 32), one launch forms every h from one pass
+ * path and their ranks add up to at most 128 in 16-rank blocks (q / k / v
+ * at rank 16 or 32, gate / up at rank 32), one launch forms every h from one pass
  * over x, bit-identical to the per-projection h, and then each projection's
  * GEMM runs. Otherwise they run one after another. */
 typedef struct rpx_int4lora_projection {

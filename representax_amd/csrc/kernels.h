@@ -135,7 +135,7 @@ hipError_t launch_rank_nt(const uint16_t* a, int64_t lda, const uint16_t* r_mat,
 // launch_rank_nt gives it alone. At most rank_nt_max_blocks() 16-rank blocks
 // in all (rank_nt_blocks_of(rank_i) each), else hipErrorInvalidValue.
 int rank_nt_blocks_of(int64_t rank);
-constexpr int rank_nt_max_blocks() { return 4; }
+constexpr int rank_nt_max_blocks() { return 8; }
 hipError_t launch_rank_nt_multi(const uint16_t* a, int64_t lda, int64_t m, int64_t k, int count,
                                 const uint16_t* const* r_mats, const int64_t* ranks,
                                 uint16_t* const* outs, hipStream_t stream);

@@ -48,7 +48,7 @@ __device__ __forceinline__ u32x4_t load8(const uint16_t* p, int valid, bool alig
 // ldo[b]. One matrix R [rank, K] is blocks of 16 consecutive rows; several
 // adapters of one input (shared-input projections) are their blocks side by
 // side.
-constexpr int kRankNtMaxBlocks = 4;
+constexpr int kRankNtMaxBlocks = 8;
 struct RankNtBlocks {
   const uint16_t* r[kRankNtMaxBlocks];
   int64_t ldr[kRankNtMaxBlocks];
@@ -516,6 +516,22 @@ hipError_t launch_rank_nt_gu(const uint16_t* a, int64_t lda, const RankNtBlocks&
       hipLaunchKernelGGL((k_rank_nt<4, G, U>), grid, dim3(256), 0, stream, a, lda, blk, m, k, ra,
                          a_scale);
       break;
+    case 5:
+    case 6:
+    case 7:
+    case 8:
+      // 5-8 blocks (several adapters of one input); not with all of a long K
+      // in flight, whose registers would spill
+      if constexpr (U <= 8) {
+        if (nblk <= 6)
+          hipLaunchKernelGGL((k_rank_nt<6, G, U>), grid, dim3(256), 0, stream, a, lda, blk, m, k,
+                             ra, a_scale);
+        else
+          hipLaunchKernelGGL((k_rank_nt<8, G, U>), grid, dim3(256), 0, stream, a, lda, blk, m, k,
+                             ra, a_scale);
+        break;
+      }
+      return hipErrorInvalidValue;
     default:
       return hipErrorInvalidValue;
   }
@@ -530,7 +546,8 @@ hipError_t launch_rank_nt_g(const uint16_t* a, int64_t lda, const RankNtBlocks& 
                             int64_t m, int64_t k, int ra, float a_scale, hipStream_t stream) {
   if constexpr (G == 1) {
     const int u = tune(kTuneRankNtU);
-    if (u == 16) return launch_rank_nt_gu<1, 16>(a, lda, blk, nblk, m, k, ra, a_scale, stream);
+    if (u == 16 && nblk <= 4)
+      return launch_rank_nt_gu<1, 16>(a, lda, blk, nblk, m, k, ra, a_scale, stream);
     if (u == 4) return launch_rank_nt_gu<1, 4>(a, lda, blk, nblk, m, k, ra, a_scale, stream);
     if (u == 8 || ceil_div(k, 128) > 4)
       return launch_rank_nt_gu<1, 8>(a, lda, blk, nblk, m, k, ra, a_scale, stream);

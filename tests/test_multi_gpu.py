@@ -232,8 +232,11 @@ def test_operands_in_other_forms_give_the_same_bits(m):
 @pytest.mark.parametrize("m", [2000, 16384, 32768])
 @pytest.mark.parametrize("k,outs", [(768, [(768, 16), (768, 16), (768, 16)]),
                                     (2048, [(6144, 32), (6144, 32)]),
-                                    (1024, [(512, 48), (256, 16)])],
-                         ids=["bert-qkv", "qwen3-gate-up", "ranks-48-16"])
+                                    (1024, [(512, 48), (256, 16)]),
+                                    (2048, [(2048, 32), (1024, 32), (1024, 32)]),
+                                    (512, [(256, 32), (256, 32), (128, 48), (128, 16)])],
+                         ids=["bert-qkv", "qwen3-gate-up", "ranks-48-16", "qwen3-qkv",
+                              "eight-blocks"])
 def test_shared_down_projection_equals_single_calls(m, k, outs):
     """Above the small-M sizes the projections' h come from one launch over x
     (row groups of 16, 32 and 64 rows at these M); y and h must equal one
