@@ -579,7 +579,7 @@ bool multi_fused_shape(int dtype, int64_t m, int64_t k, int count,
 
 // The MFMA form of rpx_int4lora_forward_multi above the small-M sizes: every
 // projection on the fused dequant GEMM path (bf16, not skinny, the usual
-// alignment), their adapters together at most four 16-rank blocks. The h of
+// alignment), their adapters together at most eight 16-rank blocks. The h of
 // every projection then comes from one pass over x, and each GEMM takes its
 // h as given.
 bool multi_shared_h(const void* x, int dtype, int64_t m, int64_t k, int count,
@@ -602,8 +602,9 @@ bool multi_shared_h(const void* x, int dtype, int64_t m, int64_t k, int count,
         !aligned16_all({x, q.packed, q.scale_bits, q.lora_a, q.y}))
       return false;
     blocks += rank_nt_blocks_of(q.rank);
+    if (blocks > rank_nt_max_blocks()) return false;
   }
-  return blocks <= rank_nt_max_blocks();
+  return true;
 }
 
 bool multi_fused(const void* x, int dtype, int64_t m, int64_t k, int count,
@@ -662,9 +663,11 @@ int rpx_int4lora_forward_multi(const void* x, int dtype, int64_t m, int64_t k, i
   }
   ActIO io;
   if (multi_shared_h(x, dtype, m, k, count, projections)) {
-    const uint16_t* r_mats[4];
-    int64_t ranks[4];
-    uint16_t* outs[4];
+    // multi_shared_h admits at most rank_nt_max_blocks() projections (one
+    // 16-rank block each at least)
+    const uint16_t* r_mats[rank_nt_max_blocks()];
+    int64_t ranks[rank_nt_max_blocks()];
+    uint16_t* outs[rank_nt_max_blocks()];
     for (int i = 0; i < count; ++i) {
       r_mats[i] = static_cast<const uint16_t*>(projections[i].lora_a);
       ranks[i] = projections[i].rank;

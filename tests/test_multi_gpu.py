@@ -234,9 +234,11 @@ def test_operands_in_other_forms_give_the_same_bits(m):
                                     (2048, [(6144, 32), (6144, 32)]),
                                     (1024, [(512, 48), (256, 16)]),
                                     (2048, [(2048, 32), (1024, 32), (1024, 32)]),
-                                    (512, [(256, 32), (256, 32), (128, 48), (128, 16)])],
+                                    (512, [(256, 32), (256, 32), (128, 48), (128, 16)]),
+                                    (256, [(64, 16)] * 8),
+                                    (256, [(64, 16)] * 9)],
                          ids=["bert-qkv", "qwen3-gate-up", "ranks-48-16", "qwen3-qkv",
-                              "eight-blocks"])
+                              "eight-blocks", "eight-projections", "nine-projections"])
 def test_shared_down_projection_equals_single_calls(m, k, outs):
     """Above the small-M sizes the projections' h come from one launch over x
     (row groups of 16, 32 and 64 rows at these M); y and h must equal one
