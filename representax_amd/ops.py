@@ -189,6 +189,14 @@ def _lora_dims(x2d, packed, scale_bits, lora_a, lora_b, group_size, bias_bits=No
     if len(xs) != 2:
         raise ValueError(f"x must be 2-D [M, K], got shape {tuple(xs)}")
     m, k = xs
+    n, r = _weight_dims(k, packed, scale_bits, lora_a, lora_b, group_size, bias_bits)
+    return m, k, n, r
+
+
+def _weight_dims(k, packed, scale_bits, lora_a, lora_b, group_size, bias_bits=None):
+    """``(n, r)`` of an INT4 + LoRA weight with K inputs, after the extent
+    checks of ``_lora_dims``."""
+
     ps = packed.shape
     if packed.dtype != torch.uint8 or len(ps) != 2:
         raise ValueError(f"packed weight must be uint8 [N, ceil(K/2)], got {packed.dtype} "
@@ -208,7 +216,7 @@ def _lora_dims(x2d, packed, scale_bits, lora_a, lora_b, group_size, bias_bits=No
         raise _shape_error("lora_b", lora_b.shape, (n, r))
     if bias_bits is not None and bias_bits.numel() != n:
         raise _shape_error("bias", bias_bits.shape, (n,))
-    return m, k, n, r
+    return n, r
 
 
 def _check_extent(name: str, t, shape) -> None:
@@ -327,8 +335,7 @@ def int4_merge(packed, scale_bits, lora_a, lora_b, *, alpha: float, rank: int, i
     """float32 ``f32(W_b) + (B @ A) * (alpha / rank)`` for one ``[N, K]`` slice."""
 
     k = int(input_size)
-    _, _, n, _ = _lora_dims(packed.new_empty((0, k), dtype=torch.bfloat16), packed, scale_bits,
-                            lora_a, lora_b, group_size)
+    n, _ = _weight_dims(k, packed, scale_bits, lora_a, lora_b, group_size)
     if lora_a.shape[0] != int(rank):
         raise _shape_error("lora_a", lora_a.shape, (int(rank), k))
     device = _on_device(packed, scale_bits, lora_a, lora_b)
