@@ -708,24 +708,25 @@ def run_int4lora(steps, warmup, use_graph, group_size=None):
 SKINNY_SHAPES = [(2048, 6144), (6144, 2048), (2048, 2048)]
 
 
-def bert_linear_rooflines(tokens=32768, group=64, rank=16, reps=10):
-    """Each distinct linear of the BERT-base step at its step size (32,768
-    tokens, group 64, rank 16): forward and backward GPU time per call inside
-    a HIP graph of `reps` calls, TFLOP/s of the algorithmic work
-    (fwd 2MNK + 2MKr + 2MrN, bwd 2MNK + 4MNr + 4MrK) and its fraction of the
-    bf16 dense peak."""
+def linear_rooflines(shapes, tokens, group, rank, reps=10, seed=8):
+    """Each distinct INT4 + LoRA linear of a train step at its step size:
+    forward and backward GPU time per call inside a HIP graph of `reps`
+    calls, TFLOP/s of the algorithmic work (fwd 2MNK + 2MKr + 2MrN, bwd
+    2MNK + 4MNr + 4MrK) and its fraction of the bf16 dense peak. `shapes`
+    holds (name, K, N, calls per layer)."""
 
     import torch
 
     from representax_amd import ops
 
     dev = torch.device("cuda:0")
-    g = np.random.Generator(np.random.PCG64(8))
-    x0 = bf16_tensor(g.standard_normal((tokens, 3072)).astype(np.float32), dev)
-    gy0 = bf16_tensor(g.standard_normal((tokens, 3072)).astype(np.float32), dev)
+    g = np.random.Generator(np.random.PCG64(seed))
+    k_max = max(k for _, k, _, _ in shapes)
+    n_max = max(n for _, _, n, _ in shapes)
+    x0 = bf16_tensor(g.standard_normal((tokens, k_max)).astype(np.float32), dev)
+    gy0 = bf16_tensor(g.standard_normal((tokens, n_max)).astype(np.float32), dev)
     out = []
-    for name, k, n, count in (("q/k/v/o", 768, 768, 4), ("ffn up", 768, 3072, 1),
-                              ("ffn down", 3072, 768, 1)):
+    for name, k, n, count in shapes:
         w = torch.from_numpy((g.standard_normal((n, k)) * 0.02).astype(np.float32)).to(dev)
         packed, scales = ops.int4_pack(w, group)
         a = bf16_tensor(g.standard_normal((rank, k)).astype(np.float32) * 0.02, dev)
@@ -751,10 +752,111 @@ def bert_linear_rooflines(tokens=32768, group=64, rank=16, reps=10):
                     "fwd_us": round(f_ms * 1e3, 1), "fwd_tflops": round(f_tf, 1),
                     "fwd_frac": round(f_tf / BF16_PEAK_TFLOPS, 4),
                     "bwd_us": round(b_ms * 1e3, 1), "bwd_tflops": round(b_tf, 1),
-                    "bwd_frac": round(b_tf / BF16_PEAK_TFLOPS, 4)})
+                    "bwd_frac": round(b_tf / BF16_PEAK_TFLOPS, 4),
+                    "_flops": (f_fl, b_fl)})
+        del w, packed, scales, a, b, x, gy, h
     del x0, gy0
     torch.cuda.empty_cache()
     return out
+
+
+BERT_STEP_LINEARS = (("q/k/v/o", 768, 768, 4), ("ffn up", 768, 3072, 1),
+                     ("ffn down", 3072, 768, 1))
+QWEN3_STEP_LINEARS = (("q/o", 2048, 2048, 2), ("k/v", 2048, 1024, 2),
+                      ("gate/up", 2048, 6144, 2), ("down", 6144, 2048, 1))
+
+
+def step_linear_roofline(per_linear, remat):
+    """The step's INT4 + LoRA linears as one roofline entry: their
+    algorithmic FLOPs over their measured per-call times, weighted by the
+    step's call mix (per layer: each linear's forward once, again under full
+    rematerialization, and its backward once)."""
+
+    fwd_calls = 2 if remat == "full" else 1
+    flops = sum(p["per_layer"] * (fwd_calls * p["_flops"][0] + p["_flops"][1]) for p in per_linear)
+    us = sum(p["per_layer"] * (fwd_calls * p["fwd_us"] + p["bwd_us"]) for p in per_linear)
+    achieved = flops / (us * 1e-6) / 1e12
+    for p in per_linear:
+        p.pop("_flops", None)
+    return {
+        "bound": "mfma", "achieved": round(achieved, 1), "peak": BF16_PEAK_TFLOPS,
+        "unit": "TFLOP/s", "frac": round(achieved / BF16_PEAK_TFLOPS, 4), "traffic": None,
+        "kernel": "INT4-LoRA linear fwd+bwd (fused dequant MFMA GEMM + rank-r kernels; dx "
+                  "GEMM + dA/dB), each distinct linear timed per call in HIP graphs of 10 calls "
+                  f"at the step's token count, weighted by the step's calls per layer ({fwd_calls} "
+                  "forward(s) and one backward each)",
+        "per_linear": per_linear,
+    }
+
+
+def bert_linear_rooflines(tokens=32768, group=64, rank=16, reps=10):
+    return linear_rooflines(BERT_STEP_LINEARS, tokens, group, rank, reps)
+
+
+def qwen3_linear_rooflines(tokens=16384, group=64, rank=32, reps=10):
+    return linear_rooflines(QWEN3_STEP_LINEARS, tokens, group, rank, reps)
+
+
+def trainstep_cpu_baseline(shapes, layers, rank, group, sample_tokens, remat="full", seed=5,
+                           budget_s=10.0):
+    """Oracle INT4 + LoRA fwd+bwd (numpy, float32 BLAS accumulate, dequant
+    included) of one layer's linears at `sample_tokens` tokens, repeated to
+    about `budget_s` seconds, scaled to the step's linear work per token:
+    `layers` layers, each linear's forward twice under full remat and its
+    backward once. Attention, norms, the loss and the optimizer are left out,
+    so the figure bounds the CPU's tokens/s from above."""
+
+    from oracle import int4 as oint4
+    from oracle import lora as olora
+    from oracle.codecs import bf16_round
+
+    g = np.random.Generator(np.random.PCG64(seed))
+    m = sample_tokens
+    cases = []
+    for _, k, n, count in shapes:
+        x = bf16_round(g.standard_normal((m, k)).astype(np.float32))
+        w = (g.standard_normal((n, k)) * 0.02).astype(np.float32)
+        a = (g.standard_normal((rank, k)) * 0.02).astype(np.float32)
+        b = (g.standard_normal((n, rank)) * 0.02).astype(np.float32)
+        gy = bf16_round(g.standard_normal((m, n)).astype(np.float32))
+        packed, scales = oint4.pack_int4(w, group)
+        cases.append((count, x, packed, scales, a, b, gy))
+    fwd_calls = 2 if remat == "full" else 1
+    t_layer = 0.0
+    reps = 0
+    t0 = time.perf_counter()
+    while True:
+        t_rep = 0.0
+        for count, x, packed, scales, a, b, gy in cases:
+            t1 = time.perf_counter()
+            _, h = olora.lora_forward(x, packed, scales, a, b, alpha=2.0 * rank, rank=rank,
+                                      group_size=group, acc=np.float32)
+            t2 = time.perf_counter()
+            olora.lora_backward(gy, x, packed, scales, a, b, h, alpha=2.0 * rank, rank=rank,
+                                group_size=group, acc=np.float32)
+            t3 = time.perf_counter()
+            t_rep += count * (fwd_calls * (t2 - t1) + (t3 - t2))
+        t_layer += t_rep
+        reps += 1
+        if time.perf_counter() - t0 > budget_s or reps >= 20:
+            break
+    t_layer /= reps
+    flops = sum(count * (fwd_calls * (2.0 * m * n * k + 2 * m * k * rank + 2 * m * rank * n)
+                         + 2.0 * m * n * k + 4 * m * n * rank + 4 * m * rank * k)
+                for (_, k, n, count) in shapes) * layers
+    step_s = t_layer * layers
+    threads, allowed, model = host_threads()
+    names = ", ".join(f"{name} {k}->{n} x{count}" for name, k, n, count in shapes)
+    return {
+        "value": round(m / step_s, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
+        "tflops": round(flops / step_s / 1e12, 5),
+        "sample": f"numpy oracle INT4-LoRA fwd+bwd of one layer's linears ({names}; group "
+                  f"{group}, r{rank}, dequant included) at {m} tokens, {reps} reps, "
+                  f"{t_layer * 1e3:.0f} ms per layer with {fwd_calls} forward(s) + 1 backward "
+                  f"per linear, scaled to {layers} layers; linears only (no attention, norms, "
+                  f"loss or optimizer), so an upper bound on the CPU's tokens/s; {threads} BLAS "
+                  f"threads of {allowed} allowed CPUs, {model}",
+    }
 
 
 def run_bert(steps=10, warmup=3, remat="full"):
@@ -992,11 +1094,17 @@ def main():
         return
     if args.only == "bert":
         line = run_bert()
-        line["per_linear"] = bert_linear_rooflines()
+        line["roofline"] = step_linear_roofline(bert_linear_rooflines(), "full")
+        if not args.no_cpu_baseline:
+            line["cpu_baseline"] = trainstep_cpu_baseline(BERT_STEP_LINEARS, 12, 16, 64, 512)
         print(json.dumps(line))
         return
     if args.only == "qwen3":
-        print(json.dumps(run_qwen3()))
+        line = run_qwen3()
+        line["roofline"] = step_linear_roofline(qwen3_linear_rooflines(), "full")
+        if not args.no_cpu_baseline:
+            line["cpu_baseline"] = trainstep_cpu_baseline(QWEN3_STEP_LINEARS, 28, 32, 64, 128)
+        print(json.dumps(line))
         return
     if args.only == "copyref":
         run_copyref()
@@ -1065,14 +1173,18 @@ def main():
         result["secondary"].append(skinny)
         log("bert-base int4-lora train step (full remat), per-linear rooflines, no-remat step")
         bert = run_bert()
-        bert["per_linear"] = bert_linear_rooflines()
+        bert["roofline"] = step_linear_roofline(bert_linear_rooflines(), "full")
         result["secondary"] += [bert, run_bert(remat="none")]
-        log("qwen3-shaped int4-lora train step (full remat), no-remat step")
-        result["secondary"] += [run_qwen3(), run_qwen3(remat="none")]
+        log("qwen3-shaped int4-lora train step (full remat), per-linear rooflines, no-remat step")
+        qwen3 = run_qwen3()
+        qwen3["roofline"] = step_linear_roofline(qwen3_linear_rooflines(), "full")
+        result["secondary"] += [qwen3, run_qwen3(remat="none")]
         if not args.no_cpu_baseline:
-            log("cpu baselines of the int4-lora and skinny lines (numpy oracle)")
+            log("cpu baselines of the int4-lora, skinny and train-step lines (numpy oracle)")
             i4_row["cpu_baseline"] = int4lora_cpu_baseline()
             skinny["cpu_baseline"] = skinny_cpu_baseline()
+            bert["cpu_baseline"] = trainstep_cpu_baseline(BERT_STEP_LINEARS, 12, 16, 64, 512)
+            qwen3["cpu_baseline"] = trainstep_cpu_baseline(QWEN3_STEP_LINEARS, 28, 32, 64, 128)
     if args.only is None and not args.no_cpu_baseline:
         log("cpu baseline (numpy oracle)")
         result["cpu_baseline"] = fp8_cpu_baseline()

@@ -109,8 +109,10 @@ int rpx_get_tuning(int knob);
 
 /* Kernels with bounded cross-block waits (the one-launch skinny-M forward)
  * raise a bit in a per-device error word when a wait expires; that call's
- * outputs then hold NaN instead of hanging. This synchronizes `stream`, reads
- * and clears the current device's word, and returns RPX_ERR_DEVICE (with a
+ * outputs then hold NaN instead of hanging. This takes the current device's
+ * word with one atomic exchange (queued on `stream`, after the work already
+ * there; a bit raised later by another stream's kernel stays for the next
+ * check), synchronizes `stream`, and returns RPX_ERR_DEVICE (with a
  * message naming the kernel) if any bit was set; flags_out (host, may be
  * NULL) receives the bits: 1 = skinny M <= 64 adapter arrivals, 2 = skinny
  * M <= 4 published h. Synchronizes, so it must not be called during graph

@@ -271,9 +271,17 @@ bool tune_set(int knob, int value) {
 
 // --- device error word -----------------------------------------------------------
 namespace {
-__device__ unsigned int g_device_error;  // bits kDevErr*, per device
+// [0]: bits kDevErr*, per device; [1]: the bits the last check took
+__device__ unsigned int g_device_error[2];
 constexpr int kMaxDevices = 64;
 std::atomic<unsigned int*> g_error_ptr[kMaxDevices];
+
+// Takes the error bits in one atomic exchange, so a bit that another
+// stream's kernel raises after it stays in the word for the next check.
+__global__ void k_take_device_errors(unsigned int* word) {
+  if (threadIdx.x == 0)
+    word[1] = __hip_atomic_exchange(word, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 }  // namespace
 
 unsigned int* device_error_word() {
@@ -334,12 +342,15 @@ int rpx_check_device_errors(void* stream, uint32_t* flags_out) {
   if (flags_out != nullptr) *flags_out = 0;
   unsigned int* word = device_error_word();
   if (word == nullptr) return check_hip(hipErrorInvalidSymbol, "rpx_check_device_errors");
-  RPX_HIP(hipStreamSynchronize(static_cast<hipStream_t>(stream)), "rpx_check_device_errors: sync");
+  // the exchange runs after the work already queued on `stream`
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(k_take_device_errors, dim3(1), dim3(64), 0, s, word);
+  RPX_HIP(hipGetLastError(), "rpx_check_device_errors: take");
   unsigned int bits = 0;
-  RPX_HIP(hipMemcpy(&bits, word, sizeof(bits), hipMemcpyDeviceToHost),
+  RPX_HIP(hipMemcpyAsync(&bits, word + 1, sizeof(bits), hipMemcpyDeviceToHost, s),
           "rpx_check_device_errors: read");
+  RPX_HIP(hipStreamSynchronize(s), "rpx_check_device_errors: sync");
   if (bits == 0) return kOk;
-  RPX_HIP(hipMemset(word, 0, sizeof(bits)), "rpx_check_device_errors: clear");
   if (flags_out != nullptr) *flags_out = bits;
   std::string msg = "a kernel's bounded wait expired (its outputs hold NaN):";
   if (bits & kDevErrSkinnyWait) msg += " skinny-M forward (one launch, M <= 64): adapter arrivals;";

@@ -421,13 +421,9 @@ double plan_cycles(int cfg, int64_t m, int64_t n, int64_t kslices, int64_t kps, 
   return cyc;
 }
 
-// Cheapest split count for one tile configuration under plan_cycles. The
-// tile comparison uses 2 KB per clock for the partial tiles; the split count
-// of the three-stage split-K tile below uses 700 bytes per clock, measured on
-// the 768 x 768 weight gradient over 8192 tokens (3 splits 16.1 us against
-// 16.9 us for 5 and 17.1 us for 4).
+// Cheapest split count for one tile configuration under plan_cycles, with
+// the partial tiles priced at 2 KB per clock.
 constexpr double kPartialRate = 2048.0;
-constexpr double kPartialRateSplitTile = 700.0;
 Fp8Plan plan_for(int cfg, int64_t m, int64_t n, int64_t kslices, double* cost_out,
                  double partial_rate = kPartialRate) {
   Fp8Plan best{cfg, 1, kslices * kBK};
@@ -454,6 +450,31 @@ Fp8Plan plan_for(int cfg, int64_t m, int64_t n, int64_t kslices, double* cost_ou
   }
   if (cost_out != nullptr) *cost_out = best_cost;
   return best;
+}
+
+// The three-stage 128 x 128 tile for long reductions over few tiles (the
+// weight gradients, K = tokens). Its split count aims for about 21 128-deep
+// slices per split, within one round of blocks (at most 256): a block that
+// runs alone on its CU takes ~770 clocks per slice (latency, not the
+// MFMA or fill rate plan_cycles assumes), and each split's partial tiles and
+// reduce cost about as much as three slices. Measured on the 768 x 768
+// weight gradient (36 tiles, graph-timed per call): 4096 tokens, 2-3 splits
+// 13.8 us against 14.7 unsplit; 8192 tokens, 3 splits 16.1 us against 17.1
+// for 4 and 16.9 for 5; 16384 tokens, 6 splits 19.5 us against 20.0 for 5
+// and 20.9 for 4. Wider outputs (144 tiles of 3072 x 768) stay unsplit, and
+// unsplit reductions of 16 or more slices gain from the third stage
+// (3072 x 768 x 4096: 17.0 us against 23.5 with two stages).
+Fp8Plan split_tile_plan(int64_t m, int64_t n, int64_t kslices) {
+  const int64_t tiles = ceil_div(m, kCfgBM[9]) * ceil_div(n, kCfgBN[9]);
+  int64_t s = (kslices + 10) / 21;
+  const int64_t cap = 256 / tiles;
+  if (s > cap) s = cap;
+  if (s > kslices) s = kslices;
+  if (s < 1) s = 1;
+  const int64_t forced = tune(kTuneFp8Splits);
+  if (forced > 0 && forced <= kslices) s = forced;
+  const int64_t kps = ceil_div(kslices, s);
+  return Fp8Plan{9, ceil_div(kslices, kps), kps * kBK};
 }
 
 Fp8Plan plan_fp8(int64_t m, int64_t n, int64_t k) {
@@ -485,10 +506,10 @@ Fp8Plan plan_fp8(int64_t m, int64_t n, int64_t k) {
     // against 11.1-11.7) when those fill one or two rounds of CUs. Each keeps
     // its own split count.
     const int64_t tiles192 = ceil_div(m, kCfgBM[4]) * ceil_div(n, kCfgBN[4]);
-    if (best.splits > 1) {
-      best = plan_for(9, m, n, kslices, nullptr, kPartialRateSplitTile);
-    } else if (kslices >= 16 && tiles192 >= 200 && tiles192 <= 512) {
+    if (best.splits == 1 && kslices >= 16 && tiles192 >= 200 && tiles192 <= 512) {
       best = plan_for(7, m, n, kslices, nullptr);
+    } else if (best.splits > 1 || kslices >= 16) {
+      best = split_tile_plan(m, n, kslices);
     } else if (tiles192 >= 256 && tiles192 <= 512) {
       best = plan_for(4, m, n, kslices, nullptr);
     }

@@ -945,8 +945,11 @@ class MNRLossFn(torch.autograd.Function):
             raise ValueError("query and document embedding dimensions must match")
         if isinstance(scale, bool) or not math.isfinite(float(scale)) or float(scale) <= 0:
             raise ValueError("scale must be finite and positive")
-        dtype = queries.dtype
-        q = queries.contiguous()
+        # each set is cast to float32 on its own (mnr.py:48-52): mixed
+        # bf16 / f32 inputs run the f32 kernel on exact upcasts, so neither
+        # set is rounded to the other's dtype first
+        dtype = queries.dtype if queries.dtype == documents.dtype else F32
+        q = queries.to(dtype).contiguous()
         d = documents.to(dtype).contiguous()
         nq, dim = q.shape
         nd = d.shape[0]
@@ -959,20 +962,20 @@ class MNRLossFn(torch.autograd.Function):
         nat.call("rpx_mnr_forward", _ptr(q), _ptr(d), _dtype_code(dtype), nq, nd, dim,
                  float(scale), _ptr(loss), _ptr(saved), nbytes, _stream(device))
         ctx.save_for_backward(saved)
-        ctx.shape = (nq, nd, dim, float(scale), dtype, documents.dtype)
+        ctx.shape = (nq, nd, dim, float(scale), dtype, queries.dtype, documents.dtype)
         return loss
 
     @staticmethod
     def backward(ctx, grad_loss):
         (saved,) = ctx.saved_tensors
-        nq, nd, dim, scale, dtype, d_dtype = ctx.shape
+        nq, nd, dim, scale, dtype, q_dtype, d_dtype = ctx.shape
         device = saved.device
         g = grad_loss.to(F32).contiguous().reshape(1)
         dq = torch.empty((nq, dim), dtype=dtype, device=device)
         dd = torch.empty((nd, dim), dtype=dtype, device=device)
         nat.call("rpx_mnr_backward", _ptr(g), _ptr(saved), saved.numel() * 4, nq, nd, dim, scale,
                  _ptr(dq), _ptr(dd), _dtype_code(dtype), _stream(device))
-        return dq, dd.to(d_dtype), None
+        return dq.to(q_dtype), dd.to(d_dtype), None
 
 
 def mnr_loss(queries: torch.Tensor, documents: torch.Tensor, scale: float = 20.0) -> torch.Tensor:

@@ -99,10 +99,15 @@ BF16_MIN_EQUAL_TOKEN_SUM = 0.97
 def assert_bf16_close(got: np.ndarray, want: np.ndarray, tol: float = BF16_REL_TOL,
                       min_equal: float | None = BF16_MIN_EQUAL, what: str = ""):
     """rel-L2 within ``tol`` and, when ``min_equal`` is given, at least that
-    fraction of elements equal to the oracle's bf16 value."""
+    fraction of elements equal to the oracle's bf16 value. Outputs so small
+    that the allowed fraction is under one element (fewer than 100 at 99%)
+    may still differ in one element: a single rounding-boundary case there
+    is the same event the fraction allows on larger outputs."""
 
     err = rel_l2(got, want)
     assert err < tol, (what, err)
     if min_equal is not None and np.size(want):
-        eq = float(np.mean(np.asarray(got, np.float32) == np.asarray(want, np.float32)))
-        assert eq >= min_equal, (what, eq)
+        same = np.asarray(got, np.float32) == np.asarray(want, np.float32)
+        eq = float(np.mean(same))
+        allowed = max(1, int(np.floor((1.0 - min_equal) * same.size)))
+        assert eq >= min_equal or int(same.size - same.sum()) <= allowed, (what, eq)

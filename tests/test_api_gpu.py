@@ -179,28 +179,6 @@ def test_float8_step_keeps_master_state_finite_and_fp32():
                if isinstance(s, torch.Tensor))
 
 
-def test_quantized_lora_under_float8_policy():
-    """All three products of the adapter go through the fp8 path
-    (adapters.py:164-176 call linear_matmul)."""
-
-    lin = rx.Linear.init(128, 96, key=1, scale=0.05, bias=True, device=DEV)
-    layer = rx.QuantizedLoRALinear.from_linear(lin, rank=8, alpha=16.0, key=2)
-    with torch.no_grad():
-        layer.lora_b.normal_(0, 0.05)
-    x = torch.randn(64, 128, device=DEV)
-    policy = rx.resolve_precision_policy(rx.PrecisionConfig.float8_mixed())
-    bf = rx.resolve_precision_policy(rx.PrecisionConfig.bfloat16_mixed())
-    with rx.precision_context(policy):
-        y8 = layer(x)
-    with rx.precision_context(bf):
-        y16 = layer(x)
-    y8.float().sum().backward()
-    assert y8.dtype == torch.bfloat16
-    assert rel_l2(from_dev(y8.detach()), from_dev(y16.detach())) < 8e-2
-    assert torch.isfinite(layer.lora_a.grad).all() and torch.isfinite(layer.lora_b.grad).all()
-    assert layer.packed_weight.grad is None
-
-
 def test_stacked_adapter_layers():
     """Stacked [L, N, K] weights pack per layer and run one layer at a time."""
 

@@ -46,6 +46,45 @@ def test_mnr_matches_oracle(nq, nd, dim, dtype):
     assert _rel_l2(d.grad.float().cpu().numpy(), gd) <= tol
 
 
+@pytest.mark.parametrize("nq,nd,dim", [(8, 8, 4096), (4, 8192, 64)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_mnr_at_the_kernel_limits(nq, nd, dim, dtype):
+    """The largest embedding width (4096: the 16-element register array per
+    thread) and the most documents (8192: a logits row in the 32 KB LDS row
+    buffer), forward and both gradients."""
+
+    test_mnr_matches_oracle(nq, nd, dim, dtype)
+
+
+@pytest.mark.parametrize("q_dtype,d_dtype", [(torch.bfloat16, torch.float32),
+                                             (torch.float32, torch.bfloat16)])
+def test_mnr_mixed_dtypes_cast_each_set_on_its_own(q_dtype, d_dtype):
+    """mnr.py:48-52 casts each embedding set to float32 separately: a bf16
+    set and an f32 set meet without rounding the f32 one to bf16. Each
+    gradient comes back in its own set's dtype."""
+
+    nq, nd, dim = 24, 40, 320
+    g = rng(911)
+    q = torch.from_numpy(g.standard_normal((nq, dim)).astype(np.float32)).to(DEV, q_dtype)
+    # f32 values with bits below bf16 precision, which a bf16 round would drop
+    d = torch.from_numpy((g.standard_normal((nd, dim)) * (1 + 2.0 ** -12)).astype(np.float32)
+                         ).to(DEV, d_dtype)
+    qv = q.float().cpu().numpy()
+    dv = d.float().cpu().numpy()
+    q.requires_grad_(True)
+    d.requires_grad_(True)
+    loss = ops.mnr_loss(q, d, 20.0)
+    loss.backward()
+    torch.cuda.synchronize()
+    want = omnr.mnr_forward(qv, dv, 20.0)
+    assert abs(loss.item() - want) <= 1e-5 * max(1.0, abs(want))
+    gq, gd = omnr.mnr_backward(qv, dv, 20.0)
+    assert q.grad.dtype == q_dtype and d.grad.dtype == d_dtype
+    for grad, want_g, dt in ((q.grad, gq, q_dtype), (d.grad, gd, d_dtype)):
+        tol = 1e-5 if dt == torch.float32 else 4e-3
+        assert _rel_l2(grad.float().cpu().numpy(), want_g) <= tol
+
+
 def test_mnr_zero_row_and_orthonormal_closed_form():
     n, s = 8, 20.0
     q = torch.eye(n, 64, device=DEV) * 3.0
