@@ -204,7 +204,7 @@ bool knob_value_ok(int knob, int v) {
     case kTuneInt4Tile:
       return v == kTileAuto || v == kTileI4_256x128 || v == kTileI4_128x128 ||
              v == kTileI4_64x128 || v == kTileI4_256x256 || v == kTileI4_128x128s2 ||
-             v == kTileI4_128x128s3 || v == kTileI4_256x128s2;
+             v == kTileI4_128x128s3 || v == kTileI4_256x128s2 || v == kTileI4L_256x192;
     case kTuneBf16Tile:
       return v == kTileAuto || v == kTileBf_256x128 || v == kTileBf_128x128 ||
              v == kTileBf_64x128 || v == kTileBf_256x256 || v == kTileBf_128x96 ||

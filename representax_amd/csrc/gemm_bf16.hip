@@ -32,6 +32,7 @@
 #include <atomic>
 #include <cstdlib>
 #include <cstring>
+#include <type_traits>
 
 #include "common.h"
 #include "kernels.h"
@@ -104,11 +105,39 @@ __device__ __forceinline__ int pswz(int row) { return (row >> 3) & 1; }
 constexpr int kBBf16 = 0;   // bf16 rows [N, K]
 constexpr int kBInt4 = 1;   // packed INT4 rows [N, K / 2] (the forward)
 constexpr int kBInt4T = 2;  // packed INT4 [K, N / 2], B[n, k] = W_b[k, n] (dx)
+constexpr int kBInt4L = 3;  // packed INT4 rows [N, K / 2], dequantized once per workgroup
+                            // into a bf16 slice buffer in LDS (the forward, 256-row tiles)
+
+// One direct-to-LDS load of 16 bytes per lane: lane l writes dst + 16 l.
+// (A device function: the LDS address-space cast must stay out of code the
+// host pass also parses, such as lambdas in a kernel body.)
+__device__ __forceinline__ void dma16(const uint8_t* src, uint8_t* dst) {
+  __builtin_amdgcn_global_load_lds(src, reinterpret_cast<lds_void_t*>(reinterpret_cast<uintptr_t>(dst)),
+                                   16, 0, 0);
+}
 
 // One direct-to-LDS load of 4 bytes per lane: lane l writes dst + 4 l.
 __device__ __forceinline__ void dma_dword(uint8_t* dst, const uint8_t* src) {
   __builtin_amdgcn_global_load_lds(src, reinterpret_cast<lds_void_t*>(reinterpret_cast<uintptr_t>(dst)),
                                    4, 0, 0);
+}
+
+// s_waitcnt as an instruction the compiler's own wait insertion accounts
+// for (an inline-asm wait is opaque to it): at most VM vector-memory
+// operations pending, LGKM LDS operations (15: no wait on them).
+template <int VM, int LGKM>
+__device__ __forceinline__ void waitcnt() {
+  static_assert(VM >= 0 && VM < 64 && LGKM >= 0 && LGKM < 16, "waitcnt range");
+  __builtin_amdgcn_s_waitcnt((VM & 15) | ((VM >> 4) << 14) | (7 << 4) | (LGKM << 8));
+  asm volatile("" ::: "memory");
+}
+
+// waitcnt<N, 0>, then the workgroup barrier (memory clobber: no memory
+// access moves across it).
+template <int N>
+__device__ __forceinline__ void wait_sync_c() {
+  waitcnt<N, 0>();
+  asm volatile("s_barrier" ::: "memory");
 }
 
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
@@ -129,6 +158,7 @@ __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_
               int tiles_n, int band) {
   constexpr bool INT4 = BK == kBInt4;
   constexpr bool T4 = BK == kBInt4T;
+  constexpr bool I4L = BK == kBInt4L;
   constexpr int NW = WM * WN;
   constexpr int NT = 64 * NW;
   constexpr int TM = BM / WM;
@@ -141,15 +171,21 @@ __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_
   // kBInt4T: the stages hold A only; packed slices (64 rows of BN / 2 bytes)
   // and their scales (one dword per row) rotate through NS + 1 stages of
   // their own, one slice ahead of A, and two bf16 slice buffers follow
-  constexpr int STAGE = T4 ? A_BYTES : A_BYTES + BN * B_ROW;
+  // kBInt4L: the stages hold A only; two bf16 B slice buffers (BN rows of
+  // 128 bytes, swizzled like the A rows) follow them
+  constexpr int STAGE = (T4 || I4L) ? A_BYTES : A_BYTES + BN * B_ROW;
   constexpr int P_BYTES = T4 ? 64 * (BN / 2) : 0;
   constexpr int P_SEGS = P_BYTES / 1024;
   constexpr int A_SEGS = BM / 8;
   // kBInt4T slots: A segments, packed segments, then the scale load (slots
   // past it repeat the scale load, which rewrites the same bytes)
-  constexpr int SEGS = T4 ? A_SEGS + P_SEGS + 1 : A_SEGS + BN * B_ROW / 1024;
+  constexpr int SEGS = T4 ? A_SEGS + P_SEGS + 1 : (I4L ? A_SEGS : A_SEGS + BN * B_ROW / 1024);
   static_assert(T4 || ((BN * B_ROW) % 1024 == 0 && SEGS % NW == 0), "DMA segments must split evenly");
   static_assert(!T4 || (BN == 128 && BM % 64 == 0), "kBInt4T: 128-column tiles");
+  static_assert(!I4L || (NS == 3 && (BN * 8) % NT == 0 && A_SEGS % NW == 0),
+                "kBInt4L: three stages, whole packed dwords and A segments per thread");
+  // LDS the epilogue may stage the output tile in
+  constexpr int LDS_ALL = I4L ? NS * STAGE + 2 * BN * 128 : NS * STAGE;
   constexpr int LPW = (SEGS + NW - 1) / NW;
   static_assert(NS >= 2 && NS <= 4 && LPW * NS < 64, "vmcnt range");
   extern __shared__ __align__(16) uint8_t smem[];
@@ -411,8 +447,10 @@ __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_
   };
 
   // prologue: NS slices in flight (refills past the end re-read the last
-  // slice into a stage nothing reads again: LPW loads per slice always)
-  if constexpr (T4) {
+  // slice into a stage nothing reads again: LPW loads per slice always);
+  // kBInt4L has its own, with its main loop below
+  if constexpr (I4L) {
+  } else if constexpr (T4) {
     // packed slice 0 and its scales first, then A slice s with packed
     // slice s + 1 (the loop's grouping); vmcnt counts the groups from the
     // newest, so the extra first load needs no count of its own
@@ -441,7 +479,7 @@ __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_
       reinterpret_cast<u32x4_t*>(sc)[v] = sc_src[v];
     for (int i = 8 * sc_vecs + tid; i < sc_total; i += NT) sc[i] = w.scales[n0 * ng + i];
   }
-  wait_sync<(NS - 1) * LPW>();
+  if constexpr (!I4L) wait_sync<(NS - 1) * LPW>();
   if constexpr (T4) {
     // slice 0 dequantized before the loop, visible to every wave
     t4_read(0);
@@ -450,8 +488,9 @@ __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_
     t4_write(0);
     wait_sync<(NS - 1) * LPW>();
   }
-  read_a(smem, 0, 0);
-  if constexpr (T4) {
+  if constexpr (!I4L) read_a(smem, 0, 0);
+  if constexpr (I4L) {
+  } else if constexpr (T4) {
     read_bt(t4_b, 0, 0);
   } else if constexpr (INT4) {
     read_bp(smem);
@@ -480,7 +519,7 @@ __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_
   // does not carry their registers.
   constexpr bool AUX_OPS = ACT != kActNone && ACT != kActGeluFwd;
   constexpr bool TWO_OPS = ACT == kActSiluMulBwd;
-  constexpr bool PREFETCH = AUX_OPS && !INT4;
+  constexpr bool PREFETCH = AUX_OPS && !INT4 && !I4L;
   constexpr int SEG_ROW = BN / 8;  // 8-column segments per tile row
   constexpr int SEG_ITS = BM * SEG_ROW / NT;
   static_assert(ACT == kActNone || (BM * SEG_ROW) % NT == 0,
@@ -504,7 +543,231 @@ __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_
   };
 
   int stage = 0;
-  if constexpr (PREFETCH) {
+  if constexpr (I4L) {
+    // Packed B through registers, dequantized once per workgroup. Thread
+    // tid owns dword d = tid % 8 of a slice's 32 packed bytes (k = 8 d ..
+    // 8 d + 7) in rows tid / 8 + i (NT / 8), i < PD; each dword becomes one
+    // 16-byte chunk of its row in a bf16 slice buffer, with the swizzle of
+    // the A rows, from which the B fragments are read as in the bf16 form.
+    //
+    // Slice t: A[t] in stage t % 3, its B in buffer t & 1. Packed slice t + 1
+    // (register set (t + 1) & 1) is dequantized into buffer (t + 1) & 1
+    // during step 3 of slice t - 1 and steps 0-2 of slice t, one unit (a
+    // bf16 pair) per two MFMA slots. The barrier before step 3 then hands
+    // over A[t + 1] and buffer (t + 1) & 1; step 3 waits for packed slice
+    // t + 2, issues packed slice t + 3 (registers) and A[t + 3] (into stage
+    // t % 3, free after the barrier), starts dequantizing slice t + 2 into
+    // buffer t & 1 (free as well) and reads the step-0 fragments of slice
+    // t + 1. Per thread and slice: E = 2 PD loads of packed dwords and
+    // scales, then LPW A segments, in that order, so vmcnt counts groups.
+    constexpr int PD = BN * 8 / NT;
+    constexpr int U = 4 * PD;        // dequantization units per slice
+    constexpr int SLOTS = 4 * NS1;   // MFMA slots they spread over
+    constexpr int E = 2 * PD;
+    constexpr int LA = LPW;
+    constexpr int BQ = BN * 128;     // bytes of one bf16 slice buffer
+    const int ngq = static_cast<int>(w.n_groups);
+    const int pdw = tid & 7;
+    // Loop-invariant per-lane offsets; the per-slice advance of every global
+    // address is uniform (a scalar base), and every LDS address is a
+    // per-lane offset plus a compile-time stage or buffer base (the slice
+    // loop is unrolled over the 3 A stages x 2 buffer parities), so the loop
+    // spends no vector instructions on addresses. The host keeps A and the
+    // packed weight under 4 GB for the 32-bit offsets.
+    uint32_t poff[PD], soff[PD], qoff[PD];
+#pragma unroll
+    for (int i = 0; i < PD; ++i) {
+      const int lr = (tid >> 3) + i * (NT / 8);
+      int64_t r = n0 + lr;
+      r = r < N ? r : N - 1;
+      poff[i] = static_cast<uint32_t>(r * w.packed_cols + 4 * pdw);
+      soff[i] = static_cast<uint32_t>(r * ngq + (ngq == 1 ? 0 : ((8 * pdw) >> group_shift)));
+      qoff[i] = static_cast<uint32_t>(lr * 128 + ((pdw ^ swz(lr)) << 4));
+    }
+    uint32_t aoff[LA];
+#pragma unroll
+    for (int d = 0; d < LA; ++d) {
+      const int trow = 8 * (wave + d * NW) + (lane >> 3);
+      int64_t r = m0 + trow;
+      r = r < M ? r : M - 1;
+      aoff[d] = static_cast<uint32_t>(r * lda * 2 + (((lane & 7) ^ swz(trow)) << 4));
+    }
+    uint32_t a_off[FM][4], b_off[FN][4];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm) {
+        const int row = wm * TM + fm * 32 + frow;
+        a_off[fm][kk] = row * 128 + (((4 * half + kk) ^ swz(row)) << 4);
+      }
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn) {
+        const int row = wn * TN + fn * 32 + frow;
+        b_off[fn][kk] = NS * STAGE + row * 128 + (((4 * half + kk) ^ swz(row)) << 4);
+      }
+    }
+    uint32_t pk[2][PD], ps[2][PD];
+    auto p_load = [&](auto set_c, int s) {
+      constexpr int set = decltype(set_c)::value;
+      const int sl = s < nk ? s : nk - 1;
+      const uint8_t* pb = w.packed + static_cast<int64_t>(sl) * (kBK / 2);
+      const uint16_t* sb = w.scales + (ngq == 1 ? 0 : ((sl * kBK) >> group_shift));
+#pragma unroll
+      for (int i = 0; i < PD; ++i) pk[set][i] = *reinterpret_cast<const uint32_t*>(pb + poff[i]);
+#pragma unroll
+      for (int i = 0; i < PD; ++i) ps[set][i] = sb[soff[i]];
+    };
+    uint32_t ulo[PD], uhi[PD], uo[PD][4];
+    float us[PD], um[PD];
+    // unit u: item u / 4, bf16 pair u % 4 (k = 8 d + 2 (u % 4) + {0, 1});
+    // the item's first unit unpacks it
+    auto p_unit = [&](auto set_c, int u) {
+      constexpr int set = decltype(set_c)::value;
+      const int i = u / 4;
+      const int pr = u % 4;
+      if (pr == 0) {
+        const uint32_t x = pk[set][i] ^ 0x88888888u;
+        uint32_t lo = x & 0x0F0F0F0Fu;
+        uint32_t hi = (x >> 4) & 0x0F0F0F0Fu;
+        asm("" : "+v"(lo), "+v"(hi));
+        ulo[i] = lo;
+        uhi[i] = hi;
+        us[i] = __builtin_bit_cast(float, ps[set][i] << 16);
+        um[i] = -8.0f * us[i];
+      }
+      switch (pr) {
+        case 0: uo[i][0] = dequant_pair<0>(ulo[i], uhi[i], us[i], um[i]); break;
+        case 1: uo[i][1] = dequant_pair<1>(ulo[i], uhi[i], us[i], um[i]); break;
+        case 2: uo[i][2] = dequant_pair<2>(ulo[i], uhi[i], us[i], um[i]); break;
+        default: uo[i][3] = dequant_pair<3>(ulo[i], uhi[i], us[i], um[i]); break;
+      }
+    };
+    // units of slot g (0 .. SLOTS - 1; slot g of step 3 is g < NS1)
+    auto p_units = [&](auto set_c, int g) {
+#pragma unroll
+      for (int u = g * U / SLOTS; u < (g + 1) * U / SLOTS; ++u) p_unit(set_c, u);
+    };
+    // The chunk stores of the items finished by the end of step q (0: step 3
+    // of the previous slice, 1-3: steps 0-2), issued early in step q + 1 so
+    // that no LDS store is in flight at a step boundary (the compiler waits
+    // for every LDS operation there); the last ones go out before the barrier.
+    auto done_items = [](int q) { return (q + 1) * PD / 4; };
+    auto p_store = [&](auto buf_c, int i0, int i1) {
+      constexpr int buf = decltype(buf_c)::value;
+#pragma unroll
+      for (int i = i0; i < i1; ++i)
+        *reinterpret_cast<u32x4_t*>(smem + NS * STAGE + buf * BQ + qoff[i]) =
+            u32x4_t{uo[i][0], uo[i][1], uo[i][2], uo[i][3]};
+    };
+    // B fragments double-buffered like A: all of the next step's fragments
+    // are read early in the step (at most three 32-column blocks per wave:
+    // a fourth would not fit the two-waves-per-SIMD register budget)
+    static_assert(FN <= 3, "kBInt4L: at most three B fragments per wave");
+    auto read_ac = [&](auto stg_c, int kk) {
+      constexpr int stg = decltype(stg_c)::value;
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm)
+        af[kk & 1][fm] = *reinterpret_cast<const bf16x8_t*>(smem + stg * STAGE + a_off[fm][kk]);
+    };
+    auto read_bq = [&](auto buf_c, int kk) {
+      constexpr int buf = decltype(buf_c)::value;
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn)
+        bfr[kk & 1][fn] = *reinterpret_cast<const bf16x8_t*>(smem + buf * BQ + b_off[fn][kk]);
+    };
+    auto mma_l = [&](int i, int kk) {
+      const int fn = i / FM;
+      const int fm = i % FM;
+      acc[fn][fm] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[kk & 1][fn], af[kk & 1][fm],
+                                                            acc[fn][fm], 0, 0, 0);
+    };
+    // next-step fragment reads in slot i of a step (kk: the next step)
+    auto frag_reads = [&](auto stg_c, auto buf_c, int kk, int i) {
+      if (i == 0) read_ac(stg_c, kk);
+      if (i == 1) read_bq(buf_c, kk);
+    };
+    // A slice s into stage stg: segments d0 .. d1 - 1 of this wave
+    auto dma_a = [&](auto stg_c, int s, int d0, int d1) {
+      constexpr int stg = decltype(stg_c)::value;
+      const uint8_t* ab = reinterpret_cast<const uint8_t*>(A) +
+                          static_cast<int64_t>(s < nk ? s : nk - 1) * (kBK * 2);
+#pragma unroll
+      for (int d = d0; d < d1; ++d) dma16(ab + aoff[d], smem + stg * STAGE + (wave + d * NW) * 1024);
+    };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+
+    // prologue: packed slices 0, 1, 2 and A slices 0, 1, 2 in flight;
+    // slice 0 dequantized whole, slice 1 its step-3 share
+    p_load(I0{}, 0);
+    dma_a(I0{}, 0, 0, LA);
+    p_load(I1{}, 1);
+    dma_a(I1{}, 1, 0, LA);
+    waitcnt<LA + E + LA, 15>();
+#pragma unroll
+    for (int u = 0; u < U; ++u) p_unit(I0{}, u);
+    p_store(I0{}, 0, PD);
+    p_load(I0{}, 2);
+    dma_a(I2{}, 2, 0, LA);
+    wait_sync_c<LA + E + LA>();
+#pragma unroll
+    for (int i = 0; i < NS1; ++i) frag_reads(I0{}, I0{}, 0, i);
+#pragma unroll
+    for (int g = 0; g < NS1; ++g) p_units(I1{}, g);
+
+    // slice t: A in stage STG = t % 3, B in buffer PAR = t % 2
+    auto slice = [&](auto stg_c, auto par_c, int t) {
+      constexpr int STG = decltype(stg_c)::value;
+      constexpr int PAR = decltype(par_c)::value;
+      const std::integral_constant<int, (STG + 1) % 3> nstg{};
+      const std::integral_constant<int, 1 - PAR> cur{};  // packed slice t + 1, buffer of t + 1
+      const std::integral_constant<int, PAR> nxt{};      // packed slice t + 2, buffer of t
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int kk = 0; kk < 3; ++kk) {
+#pragma unroll
+        for (int i = 0; i < NS1; ++i) {
+          mma_l(i, kk);
+          __builtin_amdgcn_sched_barrier(0);
+          frag_reads(stg_c, par_c, kk + 1, i);
+          if (i == 2) p_store(cur, done_items(kk - 1), done_items(kk));
+          p_units(cur, NS1 * (kk + 1) + i);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+      p_store(cur, done_items(2), PD);
+      __builtin_amdgcn_sched_barrier(0);
+      wait_sync_c<E + LA>();
+#pragma unroll
+      for (int i = 0; i < NS1; ++i) {
+        mma_l(i, 3);
+        __builtin_amdgcn_sched_barrier(0);
+        if (i == 0) {
+          waitcnt<LA, 15>();
+          p_load(cur, t + 3);
+        }
+        dma_a(stg_c, t + 3, i * LA / NS1, (i + 1) * LA / NS1);
+        frag_reads(nstg, cur, 0, i);
+        p_units(nxt, i);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    };
+    int t = 0;
+    for (; t + 6 <= nk; t += 6) {
+      slice(I0{}, I0{}, t);
+      slice(I1{}, I1{}, t + 1);
+      slice(I2{}, I0{}, t + 2);
+      slice(I0{}, I1{}, t + 3);
+      slice(I1{}, I0{}, t + 4);
+      slice(I2{}, I1{}, t + 5);
+    }
+    if (t < nk) slice(I0{}, I0{}, t);
+    if (t + 1 < nk) slice(I1{}, I1{}, t + 1);
+    if (t + 2 < nk) slice(I2{}, I0{}, t + 2);
+    if (t + 3 < nk) slice(I0{}, I1{}, t + 3);
+    if (t + 4 < nk) slice(I1{}, I0{}, t + 4);
+  } else if constexpr (PREFETCH) {
     auto slice = [&](int t) {
       const int next = stage + 1 == NS ? 0 : stage + 1;
       const uint8_t* st = smem + stage * STAGE;
@@ -754,7 +1017,7 @@ __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_
   constexpr int P = BN * 2 + 16;  // LDS row pitch of the staged tile
   if constexpr (ACT == kActNone) {
     const bool vec_out = (ldc & 7) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0;
-    if constexpr (BM * P <= NS * STAGE) {
+    if constexpr (BM * P <= LDS_ALL) {
       wait_sync<0>();  // every wave is done reading the pipeline stages
 #pragma unroll
       for (int fn = 0; fn < FN; ++fn)
@@ -828,7 +1091,7 @@ __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_
     // then transforms whole 8-column row segments, with the auxiliary
     // operands' 16-byte loads issued before the staging. Forward modes also
     // store v itself.
-    static_assert(BM * P <= NS * STAGE, "activation epilogues stage the tile in LDS");
+    static_assert(BM * P <= LDS_ALL, "activation epilogues stage the tile in LDS");
     constexpr bool FWD = ACT == kActGeluFwd || ACT == kActSiluMulFwd;
     constexpr bool AUX = AUX_OPS;
     constexpr bool TWO = TWO_OPS;
@@ -907,6 +1170,9 @@ constexpr int gemm_lds_bytes_t4(int bm, int ns) {
   return ns * bm * 128 + (ns + 1) * (64 * 64 + 256) + 2 * 64 * 256;
 }
 
+// kBInt4L: A stages and two bf16 B slice buffers
+constexpr int gemm_lds_bytes_i4l(int bm, int bn, int ns) { return ns * bm * 128 + 2 * bn * 128; }
+
 // The kTuneBand knob's band (at most tiles_m rows) when it is set, else
 // `otherwise`.
 int forced_band(int tiles_m, int otherwise) {
@@ -959,18 +1225,20 @@ hipError_t run_gemm_act(const uint16_t* a, int64_t lda, const uint16_t* b, int64
                         int64_t ldc, const LowRankEpilogue& epi, hipStream_t stream) {
   constexpr bool INT4 = BK == kBInt4;
   constexpr bool T4 = BK == kBInt4T;
+  constexpr bool I4L = BK == kBInt4L;
   const int tiles_m = static_cast<int>(ceil_div(m, BM));
   const int tiles_n = static_cast<int>(ceil_div(n, BN));
   const size_t scale_bytes = INT4 ? static_cast<size_t>(BN) * w.n_groups * 2 : 0;
-  const size_t lds = T4 ? static_cast<size_t>(gemm_lds_bytes_t4(BM, NS))
-                        : gemm_lds_bytes(BM, BN, NS, INT4) + ((scale_bytes + 15) & ~size_t{15});
+  const size_t lds = T4    ? static_cast<size_t>(gemm_lds_bytes_t4(BM, NS))
+                     : I4L ? static_cast<size_t>(gemm_lds_bytes_i4l(BM, BN, NS))
+                           : gemm_lds_bytes(BM, BN, NS, INT4) + ((scale_bytes + 15) & ~size_t{15});
   if (lds > 160 * 1024) return hipErrorInvalidValue;
   auto kern = k_gemm_nt<BM, BN, WM, WN, NS, WPE, BK, JB, ACT>;
   static std::atomic<unsigned> lds_set{0};
   hipError_t e = ensure_lds_limit(reinterpret_cast<const void*>(kern), 160 * 1024, lds_set);
   if (e != hipSuccess) return e;
   int group_shift = 0;
-  if (INT4 && w.n_groups > 1) {
+  if ((INT4 || I4L) && w.n_groups > 1) {
     while ((int64_t{1} << group_shift) < w.group) ++group_shift;
   }
   // workgroups per CU: waves per SIMD (WPE) x 4 SIMDs over the block's
@@ -981,7 +1249,7 @@ hipError_t run_gemm_act(const uint16_t* a, int64_t lda, const uint16_t* b, int64
   // bf16 operands on both sides. The INT4 GEMMs keep row-major order (a
   // forced band aside): their packed B is a quarter of the bytes, and bands
   // measured within run-to-run noise of row-major on every train-step shape.
-  const int band = INT4 || T4 ? forced_band(tiles_m, 1)
+  const int band = INT4 || T4 || I4L ? forced_band(tiles_m, 1)
                         : gemm_band(tiles_m, tiles_n, 32 * per_cu, int64_t{2} * BM,
                                     int64_t{2} * BN);
   hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(tiles_m) * tiles_n), dim3(64 * WM * WN),
@@ -1001,7 +1269,7 @@ hipError_t run_gemm_jb(const uint16_t* a, int64_t lda, const uint16_t* b, int64_
   run_gemm_act<BM, BN, WM, WN, NS, WPE, BK, JB, ACT>(a, lda, b, ldb, w, m, n, k, out, ldc, epi, stream)
   if (epi.act == kActNone) return RPX_RUN_ACT(kActNone);
   if constexpr (JB > 0 && !(BM == 256 && BN == 256)) {
-    if constexpr (BK == kBInt4) {
+    if constexpr (BK == kBInt4 || BK == kBInt4L) {
       if (epi.act == kActGeluFwd) return RPX_RUN_ACT(kActGeluFwd);
       if (epi.act == kActSiluMulFwd) return RPX_RUN_ACT(kActSiluMulFwd);
     } else {
@@ -1042,6 +1310,11 @@ hipError_t dispatch_int4(const uint16_t* a, int64_t lda, const Int4Operand& w, i
       (reinterpret_cast<uintptr_t>(w.packed) & 15) != 0)
     return hipErrorInvalidValue;
   int cfg = tune(kTuneInt4Tile);
+  // kBInt4L addresses A and the packed weight with 32-bit per-lane offsets
+  const bool i4l_ok = m * lda * 2 < (int64_t{1} << 32) && n * w.packed_cols < (int64_t{1} << 32);
+  if (cfg == kTileI4L_256x192 && i4l_ok)
+    return run_gemm<256, 192, 4, 2, 3, 2, kBInt4L>(a, lda, nullptr, 0, w, m, n, k, out, ldc, epi,
+                                                   stream);
   if (cfg == kTileI4_256x256)
     return run_gemm<256, 256, 2, 2, 3, 1, kBInt4>(a, lda, nullptr, 0, w, m, n, k, out, ldc, epi,
                                                 stream);
@@ -1055,6 +1328,15 @@ hipError_t dispatch_int4(const uint16_t* a, int64_t lda, const Int4Operand& w, i
     return run_gemm<256, 128, 1, 4, 2, 2, kBInt4>(a, lda, nullptr, 0, w, m, n, k, out, ldc, epi,
                                                 stream);
   if (cfg < kTileI4_256x128 || cfg > kTileI4_64x128) {
+    // Long reductions over outputs that split into whole 192-column tiles,
+    // at least one round of them: the 256 x 192 tile that dequantizes each
+    // packed element once per 256 rows into LDS (BERT FFN down, 32768 x 768
+    // <- 3072: 195 against 214 us). The K = 768 products, ragged column
+    // tiles and the Qwen3-2B shapes measured as fast or faster on the
+    // 128-row tiles below.
+    if (i4l_ok && k >= 3072 && n % 192 == 0 && ceil_div(m, 256) * (n / 192) >= 256)
+      return run_gemm<256, 192, 4, 2, 3, 2, kBInt4L>(a, lda, nullptr, 0, w, m, n, k, out, ldc, epi,
+                                                     stream);
     // 128 x 32 wave tiles, two or three workgroups (8 or 12 waves) per CU:
     // each dequantized B fragment feeds four MFMAs, and a CU's waves keep
     // the LDS fragment reads and the dequantization VALU work under the MFMAs.

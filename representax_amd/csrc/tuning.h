@@ -52,6 +52,7 @@ enum GemmTile : int {
   kTileT4_256x128 = 14,    // packed-weight input gradient 256 x 128, one workgroup per CU
   kTileT4_128x128 = 15,    // packed-weight input gradient 128 x 128, one workgroup per CU
   kTileT4_64x128 = 16,     // packed-weight input gradient 64 x 128, two workgroups per CU
+  kTileI4L_256x192 = 17,   // INT4 256 x 192, B dequantized once per workgroup into LDS
 };
 
 // Sets the dynamic-LDS limit of a kernel once per device (idempotent, so

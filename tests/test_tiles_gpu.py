@@ -33,8 +33,9 @@ from tests.helpers import (BF16_MIN_EQUAL_TOKEN_SUM, assert_act_bits, assert_bf1
 
 pytestmark = pytest.mark.gpu
 
-INT4_TILES = [3, 10, 11, 1, 12, 7]  # 64x128, 128x128 two / three stages, 256x128 three /
-                                     # two stages, 256x256
+INT4_TILES = [3, 10, 11, 1, 12, 7, 17]  # 64x128, 128x128 two / three stages, 256x128 three /
+                                         # two stages, 256x256; B dequantized once per
+                                         # workgroup: 256x192
 BF16_TILES = [6, 9, 5, 4, 13, 8]  # 64x128, 128x96, 128x128, 256x128 two / three stages, 256x256
 NO_ACT_TILES = {7, 8}           # sweep-only shapes without activation epilogues
 
