@@ -267,7 +267,7 @@ __device__ __forceinline__ float resolve_scale(const float* scale, const uint32_
 // (NaN amax -> NaN), broadcast through LDS; `publish` also stores it.
 __device__ __forceinline__ float finalize_scale(uint32_t m, float fmax, float* scale_out, float* sh,
                                                 bool publish) {
-  __shared__ uint32_t red[4];
+  __shared__ uint32_t red[16];
   m = block_reduce_max(m, red);
   if (threadIdx.x == 0) {
     float s;
@@ -300,11 +300,17 @@ __device__ __forceinline__ void transpose4(uint32_t a, uint32_t b, uint32_t c, u
 }
 
 // Row-major input [rows, cols] (unit column stride, ld % 8 == 0, 16-byte
-// aligned), cut into 128-row tiles of 16 CW columns, one tile per block:
-// thread (rq, cq) owns rows 8 rq + [0, 8) x columns CW cq + [0, CW) (CW = 8
-// or 4). All loads are issued before the scale reduction; the row-major codes
-// go out as 16 CW-byte row segments per 16 lanes, the transposed codes as
-// 8-byte column pieces after an in-register byte transpose.
+// aligned), cut into 128-row tiles of 16 CW columns, one tile per block of
+// kTileThreads: thread (rq, cq) owns rows kRpt rq + [0, kRpt) x columns
+// CW cq + [0, CW) (CW = 8 or 4). All loads are issued before the scale
+// reduction; the row-major codes go out as 16 CW-byte row segments per 16
+// lanes, the transposed codes as kRpt-byte column pieces after an
+// in-register byte transpose. Four rows per thread (512 threads) instead of
+// eight (256) spreads a tile's quantize arithmetic over twice the waves:
+// amax + cast of 8192 x 768 plus a 768 x 768 weight 13.7 us against 14.5,
+// of 8192 x 3072 plus 768 x 3072 34.3 against 35.1 (cold operands).
+constexpr int kRpt = 4;
+constexpr int kTileThreads = 16 * 128 / kRpt;
 // Delayed-scale amax records: each slot has kRecLanes words, one per
 // 128-byte line, so the atomic maxima of a cast's blocks spread over that
 // many lines instead of queueing on one.
@@ -333,25 +339,25 @@ struct TileWords {
 };
 
 // Thread (rq, cq) of a tile; elements outside the matrix load as zero.
-template <int DT, int CW>
+// FULL: the tile lies inside the matrix (no checks).
+template <int DT, int CW, bool FULL>
 __device__ __forceinline__ void tile_load(const CastTile& a, int64_t bx, int64_t by,
-                                          uint32_t (&raw)[8][TileWords<DT, CW>::kWords]) {
+                                          uint32_t (&raw)[kRpt][TileWords<DT, CW>::kWords]) {
   constexpr int kW = TileWords<DT, CW>::kWords;
   const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int cq = lane & 15;
-  const int rq = (lane >> 4) + 4 * (tid >> 6);
-  const int64_t r0 = by * 128 + 8 * rq;
+  const int cq = tid & 15;
+  const int rq = tid >> 4;
+  const int64_t r0 = by * 128 + kRpt * rq;
   const int64_t c0 = bx * (16 * CW) + CW * cq;
-  const bool col_ok = c0 < a.cols;  // cols % 8 == 0: the CW columns are all in or out
+  const bool col_ok = FULL || c0 < a.cols;  // cols % 8 == 0: the CW columns are all in or out
+  // row stride in dwords (ld is even for bf16)
+  const int64_t ldw = DT == kBF16 ? a.ld / 2 : a.ld;
+  const uint32_t* base = static_cast<const uint32_t*>(a.t) + (DT == kBF16 ? (r0 * a.ld + c0) / 2
+                                                                            : r0 * a.ld + c0);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int64_t r = r0 + i;
-    const bool ok = col_ok && r < a.rows;
-    const int64_t off = ok ? r * a.ld + c0 : 0;
-    const uint32_t* p = DT == kBF16
-                            ? reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(a.t) + off)
-                            : static_cast<const uint32_t*>(a.t) + off;
+  for (int i = 0; i < kRpt; ++i) {
+    const bool ok = FULL || (col_ok && r0 + i < a.rows);
+    const uint32_t* p = ok ? base + i * ldw : static_cast<const uint32_t*>(a.t);
     if constexpr (kW == 2) {
       const u32x2_t w0 = *reinterpret_cast<const u32x2_t*>(p);
       raw[i][0] = ok ? w0[0] : 0u;
@@ -369,10 +375,10 @@ __device__ __forceinline__ void tile_load(const CastTile& a, int64_t bx, int64_t
 
 // max |t| of the thread's loaded elements as ordered f32 bits.
 template <int DT, int CW>
-__device__ __forceinline__ uint32_t tile_amax(const uint32_t (&raw)[8][TileWords<DT, CW>::kWords]) {
+__device__ __forceinline__ uint32_t tile_amax(const uint32_t (&raw)[kRpt][TileWords<DT, CW>::kWords]) {
   uint32_t m = 0;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+  for (int i = 0; i < kRpt; ++i) {
 #pragma unroll
     for (int e = 0; e < TileWords<DT, CW>::kWords; ++e) {
       if constexpr (DT == kBF16)
@@ -443,37 +449,37 @@ __device__ __forceinline__ uint32_t quantize4(const float* x4, const uint32_t* w
   return (c & 0x7F7F7F7Fu) | (sign & 0x80808080u);
 }
 
-template <int DT, int FMT, int CW, bool SAT>
+template <int DT, int FMT, int CW, bool SAT, bool FULL>
 __device__ __forceinline__ void cast_tile_body(const CastTile& a, int64_t bx, int64_t by,
                                                float* s_sh) {
   constexpr int kW = TileWords<DT, CW>::kWords;
   constexpr int kC = CW / 4;  // code dwords per row
+  constexpr int kPv = 2048 / kTileThreads;  // partials per thread loaded up front
   const int64_t rows = a.rows;
   const int64_t cols = a.cols;
   uint8_t* __restrict__ out = a.out;
   uint8_t* __restrict__ out_t = a.out_t;
   constexpr float fmax = FMT == kE4M3FN ? 448.0f : 57344.0f;
   const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int cq = lane & 15;
-  const int rq = (lane >> 4) + 4 * (tid >> 6);
-  const int64_t r0 = by * 128 + 8 * rq;
+  const int cq = tid & 15;
+  const int rq = tid >> 4;
+  const int64_t r0 = by * 128 + kRpt * rq;
   const int64_t c0 = bx * (16 * CW) + CW * cq;
-  const bool col_ok = c0 < cols;
+  const bool col_ok = FULL || c0 < cols;
   // the amax partials are loaded first, so their block reduction waits only
   // for them and overlaps the tile's loads
-  uint32_t pv[8];
+  uint32_t pv[kPv];
   const bool have_partials = a.partials != nullptr;
   const int64_t np = have_partials ? a.n_partials : 0;
 #pragma unroll
-  for (int u = 0; u < 8; ++u) {
-    const int64_t i = tid + 256 * u;
+  for (int u = 0; u < kPv; ++u) {
+    const int64_t i = tid + kTileThreads * u;
     pv[u] = have_partials ? a.partials[i < np ? i : 0] : 0u;
   }
-  uint32_t raw[8][kW];
-  tile_load<DT, CW>(a, bx, by, raw);
+  uint32_t raw[kRpt][kW];
+  tile_load<DT, CW, FULL>(a, bx, by, raw);
   if (a.rec != nullptr) {
-    __shared__ uint32_t rec_red[4];
+    __shared__ uint32_t rec_red[kTileThreads / 64];
     const uint32_t m = block_reduce_max(tile_amax<DT, CW>(raw), rec_red);
     if (tid == 0)
       __hip_atomic_fetch_max(a.rec + (blockIdx.x % kRecLanes) * kRecStride, m, __ATOMIC_RELAXED,
@@ -483,8 +489,8 @@ __device__ __forceinline__ void cast_tile_body(const CastTile& a, int64_t bx, in
   if (have_partials) {
     uint32_t m = 0;
 #pragma unroll
-    for (int u = 0; u < 8; ++u) m = umax(m, tid + 256 * u < np ? pv[u] : 0u);
-    for (int64_t i = tid + 2048; i < np; i += 256) m = umax(m, a.partials[i]);
+    for (int u = 0; u < kPv; ++u) m = umax(m, tid + kTileThreads * u < np ? pv[u] : 0u);
+    for (int64_t i = tid + 2048; i < np; i += kTileThreads) m = umax(m, a.partials[i]);
     s = finalize_scale(m, fmax, a.scale_out, s_sh, bx == 0 && by == 0);
   } else {
     s = a.scale[0];
@@ -494,9 +500,9 @@ __device__ __forceinline__ void cast_tile_body(const CastTile& a, int64_t bx, in
   // wherever it can give a nonzero code, since the residual of any x that
   // matters stays normal
   const bool fast = s >= 0x1p-40f && s <= 0x1p40f;
-  uint32_t code[8][kC];
+  uint32_t code[kRpt][kC];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+  for (int i = 0; i < kRpt; ++i) {
 #pragma unroll
     for (int h = 0; h < kC; ++h) {
       float x4[4];
@@ -515,8 +521,8 @@ __device__ __forceinline__ void cast_tile_body(const CastTile& a, int64_t bx, in
   }
   if (out != nullptr && col_ok) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      if (r0 + i >= rows) continue;
+    for (int i = 0; i < kRpt; ++i) {
+      if (!FULL && r0 + i >= rows) continue;
       uint8_t* dst = out + (r0 + i) * cols + c0;
       if constexpr (kC == 2)
         *reinterpret_cast<u32x2_t*>(dst) = u32x2_t{code[i][0], code[i][1]};
@@ -525,69 +531,84 @@ __device__ __forceinline__ void cast_tile_body(const CastTile& a, int64_t bx, in
     }
   }
   if (out_t == nullptr) return;
-  // column j of the 8 x CW block: rows 0-3 in cl[j], rows 4-7 in ch[j]
-  uint32_t cl[CW], ch[CW];
+  // column j of the kRpt x CW block: its kRpt row bytes in ct[j]
+  static_assert(kRpt == 4, "one code dword per column piece");
+  uint32_t ct[CW];
 #pragma unroll
-  for (int h = 0; h < kC; ++h) {
-    transpose4(code[0][h], code[1][h], code[2][h], code[3][h], cl + 4 * h);
-    transpose4(code[4][h], code[5][h], code[6][h], code[7][h], ch + 4 * h);
-  }
+  for (int h = 0; h < kC; ++h)
+    transpose4(code[0][h], code[1][h], code[2][h], code[3][h], ct + 4 * h);
   // Tiles with all 128 rows (and 16-byte aligned rows of out_t) go out
   // through LDS: the tile's 16 CW columns become 16 CW rows of 128 code
   // bytes there (16-byte chunk c of row q at chunk c ^ ((q >> 3) & 7), which
-  // spreads both the 8-byte writes and the 16-byte reads over the banks),
+  // spreads both the 4-byte writes and the 16-byte reads over the banks),
   // and every 8 lanes then store one whole 128-byte line of out_t. Storing
-  // the 8-byte column pieces directly leaves each line to four waves
-  // (measured on 8192 x 768: 4.8 us for both layouts against 5.9). The
-  // condition is uniform over the block, so every wave reaches the barrier.
+  // the column pieces directly leaves each line to several waves (measured
+  // on 8192 x 768 with 8-byte pieces: 4.8 us for both layouts against 5.9).
+  // The condition is uniform over the block, so every wave reaches the
+  // barrier.
   const int64_t tr0 = by * 128;
   if (tr0 + 128 <= rows && (rows & 15) == 0 && (reinterpret_cast<uintptr_t>(out_t) & 15) == 0) {
     __shared__ __align__(16) uint8_t stage_t[16 * CW * 128];
 #pragma unroll
     for (int j = 0; j < CW; ++j) {
       const int q = CW * cq + j;
-      *reinterpret_cast<u32x2_t*>(stage_t + q * 128 + ((((rq >> 1) ^ (q >> 3)) & 7) << 4) +
-                                  8 * (rq & 1)) = u32x2_t{cl[j], ch[j]};
+      *reinterpret_cast<uint32_t*>(stage_t + q * 128 + ((((rq >> 2) ^ (q >> 3)) & 7) << 4) +
+                                   4 * (rq & 3)) = ct[j];
     }
     __syncthreads();
     const int64_t tc0 = bx * (16 * CW);
 #pragma unroll
-    for (int it = 0; it < CW / 2; ++it) {
-      const int c = tid + 256 * it;
+    for (int it = 0; it < 16 * CW * 8 / kTileThreads; ++it) {
+      const int c = tid + kTileThreads * it;
       const int q = c >> 3;
       const int piece = c & 7;
-      if (tc0 + q >= cols) continue;
+      if (!FULL && tc0 + q >= cols) continue;
       *reinterpret_cast<u32x4_t*>(out_t + (tc0 + q) * rows + tr0 + 16 * piece) =
           *reinterpret_cast<const u32x4_t*>(stage_t + q * 128 + ((piece ^ (q >> 3)) & 7) * 16);
     }
     return;
   }
   if (!col_ok || r0 >= rows) return;
-  const bool vec = r0 + 8 <= rows && (rows & 7) == 0 && (reinterpret_cast<uintptr_t>(out_t) & 7) == 0;
+  const bool vec =
+      r0 + kRpt <= rows && (rows & 3) == 0 && (reinterpret_cast<uintptr_t>(out_t) & 3) == 0;
 #pragma unroll
   for (int j = 0; j < CW; ++j) {
     uint8_t* dst = out_t + (c0 + j) * rows + r0;
     if (vec) {
-      *reinterpret_cast<u32x2_t*>(dst) = u32x2_t{cl[j], ch[j]};
+      *reinterpret_cast<uint32_t*>(dst) = ct[j];
     } else {
-      for (int e = 0; e < 8 && r0 + e < rows; ++e)
-        dst[e] = static_cast<uint8_t>((e < 4 ? cl[j] : ch[j]) >> (8 * (e & 3)));
+      for (int e = 0; e < kRpt && r0 + e < rows; ++e)
+        dst[e] = static_cast<uint8_t>(ct[j] >> (8 * e));
     }
   }
+}
+
+// Whether tile (bx, by) lies inside the matrix (uniform over the block).
+template <int CW>
+__device__ __forceinline__ bool tile_inside(const CastTile& a, int64_t bx, int64_t by) {
+  return (by + 1) * 128 <= a.rows && (bx + 1) * (16 * CW) <= a.cols;
+}
+
+template <int DT, int FMT, int CW, bool SAT>
+__device__ __forceinline__ void cast_tile(const CastTile& a, int64_t b, float* s_sh) {
+  const int64_t bx = b % a.tiles_x;
+  const int64_t by = b / a.tiles_x;
+  if (tile_inside<CW>(a, bx, by))
+    cast_tile_body<DT, FMT, CW, SAT, true>(a, bx, by, s_sh);
+  else
+    cast_tile_body<DT, FMT, CW, SAT, false>(a, bx, by, s_sh);
 }
 
 // Up to two row-major cast problems of one input type and format in one
 // launch: blocks [0, a0.tiles) take the first, the rest the second.
 template <int DT, int FMT, int CW, bool SAT = false>
-__global__ void __launch_bounds__(256) k_fp8_cast_tile(CastTile a0, CastTile a1) {
+__global__ void __launch_bounds__(kTileThreads) k_fp8_cast_tile(CastTile a0, CastTile a1) {
   __shared__ float s_sh;
-  int64_t b = blockIdx.x;
-  if (b < a0.tiles) {
-    cast_tile_body<DT, FMT, CW, SAT>(a0, b % a0.tiles_x, b / a0.tiles_x, &s_sh);
-  } else {
-    b -= a0.tiles;
-    cast_tile_body<DT, FMT, CW, SAT>(a1, b % a1.tiles_x, b / a1.tiles_x, &s_sh);
-  }
+  const int64_t b = blockIdx.x;
+  if (b < a0.tiles)
+    cast_tile<DT, FMT, CW, SAT>(a0, b, &s_sh);
+  else
+    cast_tile<DT, FMT, CW, SAT>(a1, b - a0.tiles, &s_sh);
 }
 
 // Amax partials, one per tile, over the same block -> tile mapping as
@@ -596,14 +617,19 @@ __global__ void __launch_bounds__(256) k_fp8_cast_tile(CastTile a0, CastTile a1)
 // Partials of part 0 go to a0.partials, of part 1 to a1.partials (written
 // through the const pointers' storage).
 template <int DT, int CW>
-__global__ void __launch_bounds__(256) k_amax_tiles(CastTile a0, CastTile a1) {
-  __shared__ uint32_t sh[4];
+__global__ void __launch_bounds__(kTileThreads) k_amax_tiles(CastTile a0, CastTile a1) {
+  __shared__ uint32_t sh[kTileThreads / 64];
   int64_t b = blockIdx.x;
   const bool first = b < a0.tiles;
   const CastTile& a = first ? a0 : a1;
   if (!first) b -= a0.tiles;
-  uint32_t raw[8][TileWords<DT, CW>::kWords];
-  tile_load<DT, CW>(a, b % a.tiles_x, b / a.tiles_x, raw);
+  const int64_t bx = b % a.tiles_x;
+  const int64_t by = b / a.tiles_x;
+  uint32_t raw[kRpt][TileWords<DT, CW>::kWords];
+  if (tile_inside<CW>(a, bx, by))
+    tile_load<DT, CW, true>(a, bx, by, raw);
+  else
+    tile_load<DT, CW, false>(a, bx, by, raw);
   const uint32_t m = block_reduce_max(tile_amax<DT, CW>(raw), sh);
   if (threadIdx.x == 0) const_cast<uint32_t*>(a.partials)[b] = m;
 }
@@ -766,7 +792,7 @@ void launch_tiles_cw(int dtype, int fmt, const CastTile& a0, const CastTile& a1,
                                                : k_fp8_cast_tile<kBF16, kE5M2, CW>)
                              : (fmt == kE4M3FN ? k_fp8_cast_tile<kF32, kE4M3FN, CW>
                                                : k_fp8_cast_tile<kF32, kE5M2, CW>);
-  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(a0.tiles + a1.tiles)), dim3(256), 0, stream,
+  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(a0.tiles + a1.tiles)), dim3(kTileThreads), 0, stream,
                      a0, a1);
 }
 
@@ -797,11 +823,11 @@ template <int DT, int FMT>
 void launch_tile_delayed(const CastTile& a0, const CastTile& a1, hipStream_t stream) {
   const unsigned blocks = static_cast<unsigned>(a0.tiles + a1.tiles);
   if (cast_cw() == 8)
-    hipLaunchKernelGGL((k_fp8_cast_tile<DT, FMT, 8, true>), dim3(blocks), dim3(256), 0, stream, a0,
-                       a1);
+    hipLaunchKernelGGL((k_fp8_cast_tile<DT, FMT, 8, true>), dim3(blocks), dim3(kTileThreads), 0,
+                       stream, a0, a1);
   else
-    hipLaunchKernelGGL((k_fp8_cast_tile<DT, FMT, 4, true>), dim3(blocks), dim3(256), 0, stream, a0,
-                       a1);
+    hipLaunchKernelGGL((k_fp8_cast_tile<DT, FMT, 4, true>), dim3(blocks), dim3(kTileThreads), 0,
+                       stream, a0, a1);
 }
 
 // One block for every slot: the slot's pending lanes (maxima recorded since
@@ -992,7 +1018,7 @@ hipError_t launch_fp8_quantize2(const void* t0, int dtype0, int64_t rows0, int64
     const unsigned blocks = static_cast<unsigned>(a0.tiles + a1.tiles);
     auto kern = cast_cw() == 8 ? (dtype0 == kBF16 ? k_amax_tiles<kBF16, 8> : k_amax_tiles<kF32, 8>)
                                : (dtype0 == kBF16 ? k_amax_tiles<kBF16, 4> : k_amax_tiles<kF32, 4>);
-    hipLaunchKernelGGL(kern, dim3(blocks), dim3(256), 0, stream, a0, a1);
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(kTileThreads), 0, stream, a0, a1);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     launch_tiles(dtype0, fmt, a0, a1, stream);

@@ -207,6 +207,26 @@ def test_fp8_linear_bert_ffn_full_size():
     assert max(errs) < FP8_TOL, errs
 
 
+@pytest.mark.parametrize("m,k,n", [(300, 200, 136), (1000, 8, 40), (129, 96, 8),
+                                   (2100 * 128 + 5, 8, 16)])
+def test_fused_quantize_scales_and_codes_bit_exact(m, k, n):
+    """The linear's own quantize (amax tile partials, then every cast block
+    reducing them to the scale): scales and the saved transposed codes of
+    both operands equal the oracle's, on ragged tiles and on an operand of
+    more than 2048 tiles (partials beyond the ones each thread loads up
+    front)."""
+
+    x, w, _ = _fp8_case(m, k, n, seed=m + 3 * k + n)
+    _, scales, codes = ops.fp8_linear_forward(to_dev_bf16(x), to_dev_bf16(w).t(), save_codes=True)
+    torch.cuda.synchronize()
+    s = from_dev(scales)
+    s_x = ofp8.scale_from_amax(ofp8.amax(x), E4M3FN)
+    s_w = ofp8.scale_from_amax(ofp8.amax(w), E4M3FN)
+    assert s[0] == s_x and s[1] == s_w
+    assert np.array_equal(codes[0].cpu().numpy(), ofp8.cast_with_scale(x, s_x, E4M3FN).T)
+    assert np.array_equal(codes[1].cpu().numpy(), ofp8.cast_with_scale(w, s_w, E4M3FN).T)
+
+
 def test_fp8_linear_natural_right_layout():
     """right given as a row-major [K, N] matrix (not a transposed view)."""
 
