@@ -203,10 +203,9 @@ def fp8_delayed_step_fn(layers, history_len=16):
             ops._gemm_into(qx, "e4m3fn", sc[sx:sx + 1], qw, "e4m3fn", sc[sw:sw + 1],
                            torch.empty((m, n), dtype=x.dtype, device=dev))
             qg, qgt = ops.fp8_cast_delayed(gy, state, sg, "e5m2", rowmajor=True, transposed=True)
-            ops._gemm_into(qg, "e5m2", sc[sg:sg + 1], qwt, "e4m3fn", sc[sw:sw + 1],
-                           torch.empty((m, k), dtype=x.dtype, device=dev))
-            ops._gemm_into(qgt, "e5m2", sc[sx:sx + 1], qxt, "e4m3fn", sc[sg:sg + 1],
-                           torch.empty((n, k), dtype=x.dtype, device=dev))
+            ops.fp8_linear_backward_gemms(qg, qgt, sc[sg:sg + 1], qxt, sc[sx:sx + 1], qwt,
+                                          sc[sw:sw + 1], k=k, dtype=x.dtype,
+                                          right_transposed=True)
         state.update()
 
     return step
@@ -228,10 +227,14 @@ def fp8_flops(tokens):
     return sum(6.0 * tokens * k * n for _, k, n in BERT_LINEARS)
 
 
-def fp8_gemm_calls(layers):
-    """The 18 fp8 GEMM calls of one step (forward, dX, dW per linear) on the
-    codes and scales the step produces, with their algorithmic FLOPs and
-    compulsory HBM bytes (fp8 operands read once, bf16 output written once)."""
+def fp8_gemm_calls(layers, paired=True):
+    """The fp8 GEMM launches of one step on the codes and scales the step
+    produces, with their algorithmic FLOPs and compulsory HBM bytes (fp8
+    operands read once, bf16 outputs written once): per linear the forward
+    product and the backward's input- and weight-gradient products. paired:
+    the backward's two products as the step runs them, one
+    fp8_linear_backward_gemms call (12 calls per step); otherwise each product
+    alone (18 calls, for the per-product vendor comparison)."""
 
     import torch
 
@@ -246,12 +249,22 @@ def fp8_gemm_calls(layers):
         qx, qxt = ops.fp8_cast(x, s_x, "e4m3fn", rowmajor=True, transposed=True)
         qw, qwt = ops.fp8_cast(w, s_w, "e4m3fn", rowmajor=True, transposed=True)
         qg, qgt = ops.fp8_cast(gy, s_g, "e5m2", rowmajor=True, transposed=True)
+        fwd_bytes = m * k + n * k + 2.0 * m * n
+        dx_bytes = m * n + n * k + 2.0 * m * k
+        dw_bytes = m * n + m * k + 2.0 * n * k
         calls.append((lambda a=qx, b=qw, sa=s_x, sb=s_w: ops.fp8_gemm(a, "e4m3fn", sa, b, "e4m3fn", sb),
-                      2.0 * m * n * k, m * k + n * k + 2.0 * m * n))
-        calls.append((lambda a=qg, b=qwt, sa=s_g, sb=s_w: ops.fp8_gemm(a, "e5m2", sa, b, "e4m3fn", sb),
-                      2.0 * m * n * k, m * n + n * k + 2.0 * m * k))
-        calls.append((lambda a=qgt, b=qxt, sa=s_x, sb=s_g: ops.fp8_gemm(a, "e5m2", sa, b, "e4m3fn", sb),
-                      2.0 * m * n * k, m * n + m * k + 2.0 * n * k))
+                      2.0 * m * n * k, fwd_bytes))
+        if paired:
+            calls.append((lambda qg=qg, qgt=qgt, s_g=s_g, qxt=qxt, s_x=s_x, qwt=qwt, s_w=s_w, k=k:
+                          ops.fp8_linear_backward_gemms(qg, qgt, s_g, qxt, s_x, qwt, s_w, k=k,
+                                                        dtype=torch.bfloat16,
+                                                        right_transposed=True),
+                          4.0 * m * n * k, dx_bytes + dw_bytes))
+        else:
+            calls.append((lambda a=qg, b=qwt, sa=s_g, sb=s_w: ops.fp8_gemm(a, "e5m2", sa, b, "e4m3fn", sb),
+                          2.0 * m * n * k, dx_bytes))
+            calls.append((lambda a=qgt, b=qxt, sa=s_x, sb=s_g: ops.fp8_gemm(a, "e5m2", sa, b, "e4m3fn", sb),
+                          2.0 * m * n * k, dw_bytes))
     torch.cuda.synchronize()
     return calls
 
@@ -280,11 +293,12 @@ def profiled_traffic():
 
 
 def fp8_gemm_roofline(layers, reps=16):
-    """Dominant kernel: the fp8 MFMA GEMM calls of one step (k_fp8_gemm, plus
-    the split-K reduce for the calls that use one). Each call is timed as GPU
-    time per call inside a HIP graph of `reps` launches (HIP events on the
-    capturing stream); achieved = algorithmic FLOPs of the 18 calls / their
-    summed time."""
+    """Dominant kernels: the fp8 MFMA GEMM launches of one step (k_fp8_gemm
+    for each forward, k_fp8_gemm_pair for each backward's two products, plus
+    the split-K reduce where the weight gradient uses one). Each call is timed
+    as GPU time per call inside a HIP graph of `reps` launches (HIP events on
+    the capturing stream); achieved = algorithmic FLOPs of the 12 calls /
+    their summed time."""
 
     calls = fp8_gemm_calls(layers)
     total_ms = 0.0
@@ -308,8 +322,9 @@ def fp8_gemm_roofline(layers, reps=16):
         "traffic": traffic,
         "traffic_source": {"profile": os.path.relpath(TRAFFIC_PROFILE, ROOT),
                            "measured_at_commit": traffic_commit},
-        "kernel": "k_fp8_gemm (+ k_fp8_split_reduce where split-K): fwd e4m3xe4m3, dX e5m2xe4m3, "
-                  "dW e5m2xe4m3; 18 calls per step",
+        "kernel": "k_fp8_gemm (forward, e4m3xe4m3) and k_fp8_gemm_pair (backward dX and dW, "
+                  "e5m2xe4m3, in one launch; + k_fp8_split_reduce where dW is split-K); 12 calls "
+                  "per step",
         "avg_launch_us": round(1e3 * total_ms / len(calls), 2),
         "flops_per_launch_avg": total_flops / len(calls),
         "algorithmic_bytes_per_launch_avg": fp8_gemm_bytes(layers) / len(calls),
@@ -320,7 +335,7 @@ def fp8_gemm_roofline(layers, reps=16):
 def fp8_quantize_report(layers, step_ms, gemm_us):
     """The dynamic quantize passes of one step (amax, then the cast into both
     code layouts) against HBM bandwidth. Their time is the step's minus its
-    18 GEMM calls' (each timed alone in a graph); their algorithmic bytes per
+    12 GEMM launches' (each timed alone in a graph); their algorithmic bytes per
     linear are 6 (MK + NK + MN): the amax pass reads x, W and g in bf16, the
     cast reads them again and writes one byte per element in each of the two
     layouts."""
@@ -335,12 +350,12 @@ def fp8_quantize_report(layers, step_ms, gemm_us):
             "gbs": None if gbs is None else round(gbs, 1),
             "frac_hbm": None if gbs is None else round(gbs / HBM_PEAK_GBS, 4),
             "kernels": "k_amax_tiles + k_fp8_cast_tile (12 each per step)",
-            "timing": "step time minus the 18 GEMM calls' graph-timed time"}
+            "timing": "step time minus the 12 GEMM launches' graph-timed time"}
 
 
 def fp8_gemm_bytes(layers):
-    """Compulsory HBM bytes of the 18 GEMM calls: fp8 operands read once, the
-    bf16 outputs (y, dX, dW) written once."""
+    """Compulsory HBM bytes of the step's GEMM products: fp8 operands read
+    once, the bf16 outputs (y, dX, dW) written once."""
 
     total = 0.0
     for _, x, _, _, k, n in layers:
@@ -410,7 +425,7 @@ def run_vendor(layers):
     for nm, k, n in BERT_LINEARS:
         names += [(f"{nm} fwd", 8192, n, k), (f"{nm} dX", 8192, k, n), (f"{nm} dW", n, k, 8192)]
     fp8 = []
-    for (fn, _, _), (nm, m, n, k) in zip(fp8_gemm_calls(layers), names):
+    for (fn, _, _), (nm, m, n, k) in zip(fp8_gemm_calls(layers, paired=False), names):
         ours = graph_time_per_call_ms([fn] * 16, replays=3) * 1e3
         a = torch.randn(m, k, device=dev).to(torch.float8_e4m3fn)
         b = torch.randn(n, k, device=dev).to(torch.float8_e4m3fn)

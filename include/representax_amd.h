@@ -88,6 +88,9 @@ int rpx_abi_version(void);
  *   RPX_TUNE_FP8_SPLITS  fp8 GEMM split-K count: 0 planner, 1..32 where the
  *                        128-deep K slices split into exactly that many
  *                        parts (otherwise the planner's count)
+ *   RPX_TUNE_FP8_PAIR    fp8 linear backward's input and weight gradients in
+ *                        one launch: -1 planner (where both products' tiles
+ *                        allow it), 0 two launches (env RPX_FP8_PAIR)
  * ------------------------------------------------------------------------- */
 #define RPX_TUNE_INT4_TILE 0
 #define RPX_TUNE_BF16_TILE 1
@@ -101,6 +104,7 @@ int rpx_abi_version(void);
 #define RPX_TUNE_RANK_BLOCKS 9
 #define RPX_TUNE_RANK_NT_U 10
 #define RPX_TUNE_FP8_SPLITS 11
+#define RPX_TUNE_FP8_PAIR 12
 
 /* RPX_ERR_INVALID for an unknown knob or value. */
 int rpx_set_tuning(int knob, int value);
@@ -395,6 +399,30 @@ int rpx_fp8_linear_backward_codes(const uint8_t* left_t_codes, const uint8_t* ri
                                   const void* grad, int grad_dtype, void* d_left, void* d_right,
                                   int d_right_transposed, int out_dtype, void* workspace,
                                   size_t workspace_bytes, void* stream);
+
+/* The two products of that backward from the gradient's codes, for a caller
+ * that quantizes the gradient itself (delayed scaling):
+ *   d_left [m, k] = ((g . right^T) * s_grad) * s_right, from g_codes [m, n]
+ *     (e5m2) and right_codes [k, n] (e4m3);
+ *   d_right = ((left^T . g) * s_left) * s_grad, as [k, n] or as [n, k] when
+ *     d_right_transposed, from g_t_codes [n, m] (e5m2) and left_t_codes
+ *     [k, m] (e4m3).
+ * Either output may be NULL (then its codes and scale may be too). With both
+ * outputs and d_right_transposed, the two products run in one launch where
+ * their tile plans allow it (RPX_TUNE_FP8_PAIR), with the same results as
+ * two launches. m, n, k > 0. Workspace:
+ * rpx_fp8_linear_backward_gemms_workspace(m, n, k).
+ * Replaces the two _scaled_fp8_dot calls of _fp8_linear_dot_backward,
+ * src/representax/precision.py:201-218. */
+int rpx_fp8_linear_backward_gemms(const uint8_t* g_codes, const uint8_t* g_t_codes,
+                                  const float* s_grad, const uint8_t* left_t_codes,
+                                  const float* s_left, const uint8_t* right_codes,
+                                  const float* s_right, int64_t m, int64_t k, int64_t n,
+                                  void* d_left, void* d_right, int d_right_transposed,
+                                  int out_dtype, void* workspace, size_t workspace_bytes,
+                                  void* stream);
+
+size_t rpx_fp8_linear_backward_gemms_workspace(int64_t m, int64_t n, int64_t k);
 
 /* ---------------------------------------------------------------------------
  * Delayed-scale fp8 state, one entry ("slot") per scaled tensor of a model:

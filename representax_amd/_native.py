@@ -43,6 +43,7 @@ TUNE_DX_PACKED = 8
 TUNE_RANK_BLOCKS = 9
 TUNE_RANK_NT_U = 10
 TUNE_FP8_SPLITS = 11
+TUNE_FP8_PAIR = 12
 
 _p = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -114,6 +115,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
     "rpx_fp8_linear_backward_codes": (
         _int, [_p, _p, _p, _i64, _i64, _i64, _p, _int, _p, _p, _int, _int, _p, _size, _p]
+    ),
+    "rpx_fp8_linear_backward_gemms_workspace": (_size, [_i64, _i64, _i64]),
+    "rpx_fp8_linear_backward_gemms": (
+        _int, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _p, _int, _int, _p, _size, _p]
     ),
     "rpx_fp8_delayed_pending_words": (_size, []),
     "rpx_fp8_cast_delayed": (

@@ -220,6 +220,7 @@ bool knob_value_ok(int knob, int v) {
     case kTuneRankBlocks: return v == 0 || (v >= 16 && v <= 8192);
     case kTuneRankNtU: return v == 0 || v == 4 || v == 8 || v == 16;
     case kTuneFp8Splits: return v >= 0 && v <= 32;
+    case kTuneFp8Pair: return v == -1 || v == 0;
     default: return false;
   }
 }
@@ -232,7 +233,7 @@ int env_int(const char* name, int fallback) {
 struct Knobs {
   std::atomic<int> v[kTuneCount];
   Knobs() {
-    const int defaults[kTuneCount] = {0, 0, 0, 0, -1, -1, 0, 0, -1, 0, 0, 0};
+    const int defaults[kTuneCount] = {0, 0, 0, 0, -1, -1, 0, 0, -1, 0, 0, 0, -1};
     for (int i = 0; i < kTuneCount; ++i) v[i].store(defaults[i], std::memory_order_relaxed);
     // RPX_GEMM_TILE names a tile of either GEMM (the id sets are disjoint)
     const int gemm = env_int("RPX_GEMM_TILE", 0);
@@ -243,7 +244,8 @@ struct Knobs {
                                                 {kTuneSkinny2, "RPX_SKINNY2"},
                                                 {kTuneSkinny2One, "RPX_SKINNY2_ONE"},
                                                 {kTuneBand, "RPX_GEMM_BAND"},
-                                                {kTuneDxPacked, "RPX_DX_PACKED"}};
+                                                {kTuneDxPacked, "RPX_DX_PACKED"},
+                                                {kTuneFp8Pair, "RPX_FP8_PAIR"}};
     for (const auto& e : envs) {
       const int val = env_int(e.second, v[e.first].load());
       if (knob_value_ok(e.first, val)) v[e.first].store(val);
@@ -1298,11 +1300,7 @@ void plan_fp8_backward(A& a, int64_t m, int64_t n, int64_t k) {
   a.template take<uint8_t>(n * m);  // g codes [N, M]
   a.template take<uint8_t>(k * n);  // right codes [K, N]
   a.template take<uint8_t>(k * m);  // left codes [K, M]
-  size_t g1 = rpx_fp8_gemm_workspace(m, k, n);
-  size_t g2 = rpx_fp8_gemm_workspace(k, n, m);
-  const size_t g3 = rpx_fp8_gemm_workspace(n, k, m);
-  if (g2 < g3) g2 = g3;
-  a.template take<uint8_t>(static_cast<int64_t>(g1 > g2 ? g1 : g2));
+  a.template take<uint8_t>(static_cast<int64_t>(rpx_fp8_linear_backward_gemms_workspace(m, n, k)));
 }
 }  // namespace
 
@@ -1376,11 +1374,7 @@ int rpx_fp8_linear_backward_codes(const uint8_t* left_t_codes, const uint8_t* ri
   uint8_t* qgt = ar.take<uint8_t>(n * m);
   ar.take<uint8_t>(k * n);
   ar.take<uint8_t>(k * m);
-  size_t g1 = rpx_fp8_gemm_workspace(m, k, n);
-  size_t g2 = rpx_fp8_gemm_workspace(k, n, m);
-  const size_t g3 = rpx_fp8_gemm_workspace(n, k, m);
-  if (g2 < g3) g2 = g3;
-  const size_t gws = g1 > g2 ? g1 : g2;
+  const size_t gws = rpx_fp8_linear_backward_gemms_workspace(m, n, k);
   uint8_t* gw = ar.take<uint8_t>(static_cast<int64_t>(gws));
   if (ar.overflow) return fail_invalid("rpx_fp8_linear_backward: workspace too small");
   // s_g (e5m2) and the gradient codes in the layouts the two products need
@@ -1388,18 +1382,61 @@ int rpx_fp8_linear_backward_codes(const uint8_t* left_t_codes, const uint8_t* ri
                                d_right ? qgt : nullptr, nullptr, grad_dtype, 0, 0, 0, 1, nullptr,
                                nullptr, nullptr, nullptr, kE5M2, st),
           "fp8_linear_backward: quantize(grad)");
+  return rpx_fp8_linear_backward_gemms(d_left ? qg : nullptr, d_right ? qgt : nullptr, sg,
+                                       left_t_codes, scales, right_codes, scales + 1, m, k, n,
+                                       d_left, d_right, d_right_transposed, out_dtype, gw, gws,
+                                       stream);
+}
+
+size_t rpx_fp8_linear_backward_gemms_workspace(int64_t m, int64_t n, int64_t k) {
+  size_t g1 = rpx_fp8_gemm_workspace(m, k, n);
+  size_t g2 = rpx_fp8_gemm_workspace(k, n, m);
+  const size_t g3 = rpx_fp8_gemm_workspace(n, k, m);
+  if (g2 < g3) g2 = g3;
+  return g1 > g2 ? g1 : g2;
+}
+
+int rpx_fp8_linear_backward_gemms(const uint8_t* g_codes, const uint8_t* g_t_codes,
+                                  const float* s_grad, const uint8_t* left_t_codes,
+                                  const float* s_left, const uint8_t* right_codes,
+                                  const float* s_right, int64_t m, int64_t k, int64_t n,
+                                  void* d_left, void* d_right, int d_right_transposed,
+                                  int out_dtype, void* workspace, size_t workspace_bytes,
+                                  void* stream) {
+  RPX_TRY(check_dtype(out_dtype));
+  if (m <= 0 || n <= 0 || k <= 0)
+    return fail_invalid("rpx_fp8_linear_backward_gemms: m, n, k must be positive");
+  if (s_grad == nullptr ||
+      (d_left != nullptr && (g_codes == nullptr || right_codes == nullptr || s_right == nullptr)) ||
+      (d_right != nullptr && (g_t_codes == nullptr || left_t_codes == nullptr || s_left == nullptr)))
+    return fail_invalid("rpx_fp8_linear_backward_gemms: null pointer");
+  const size_t gws = rpx_fp8_linear_backward_gemms_workspace(m, n, k);
+  if (workspace_bytes < gws || (gws > 0 && workspace == nullptr))
+    return fail_invalid("rpx_fp8_linear_backward_gemms: workspace too small");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (d_left != nullptr && d_right != nullptr && d_right_transposed &&
+      aligned16_all({g_codes, g_t_codes, right_codes, left_t_codes})) {
+    // both products in one launch where their plans allow it
+    bool paired = false;
+    RPX_HIP(launch_fp8_backward_pair(g_codes, right_codes, g_t_codes, left_t_codes, s_grad,
+                                     s_right, s_left, m, k, n, d_left, d_right, out_dtype,
+                                     static_cast<float*>(workspace),
+                                     static_cast<int64_t>(gws / sizeof(float)), st, &paired),
+            "fp8_linear_backward: paired products");
+    if (paired) return kOk;
+  }
   // d_left [M, K] = ((g . right^T) * s_g) * s_r
   if (d_left != nullptr)
-    RPX_TRY(rpx_fp8_gemm(qg, kE5M2, sg, right_codes, kE4M3FN, scales + 1, m, k, n, d_left,
-                         out_dtype, gw, gws, stream));
+    RPX_TRY(rpx_fp8_gemm(g_codes, kE5M2, s_grad, right_codes, kE4M3FN, s_right, m, k, n, d_left,
+                         out_dtype, workspace, gws, stream));
   if (d_right == nullptr) return kOk;
   // d_right = ((left^T . g) * s_l) * s_g, as [K, N] or transposed [N, K]
   if (d_right_transposed) {
-    RPX_TRY(rpx_fp8_gemm(qgt, kE5M2, scales, left_t_codes, kE4M3FN, sg, n, k, m, d_right,
-                         out_dtype, gw, gws, stream));
+    RPX_TRY(rpx_fp8_gemm(g_t_codes, kE5M2, s_left, left_t_codes, kE4M3FN, s_grad, n, k, m,
+                         d_right, out_dtype, workspace, gws, stream));
   } else {
-    RPX_TRY(rpx_fp8_gemm(left_t_codes, kE4M3FN, scales, qgt, kE5M2, sg, k, n, m, d_right,
-                         out_dtype, gw, gws, stream));
+    RPX_TRY(rpx_fp8_gemm(left_t_codes, kE4M3FN, s_left, g_t_codes, kE5M2, s_grad, k, n, m,
+                         d_right, out_dtype, workspace, gws, stream));
   }
   return kOk;
 }

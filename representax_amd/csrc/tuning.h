@@ -25,7 +25,8 @@ enum TuneKnob : int {
   kTuneRankBlocks = 9,  // workgroups a token-reduction product (dA, dB) aims for (0: planner)
   kTuneRankNtU = 10,    // rank_nt 128-column steps in flight per wave (0: planner; 4, 8, 16)
   kTuneFp8Splits = 11,  // fp8 GEMM split-K count (0: planner; else forced where it divides K)
-  kTuneCount = 12
+  kTuneFp8Pair = 12,    // fp8 backward's two products in one launch: -1 planner, 0 never  RPX_FP8_PAIR
+  kTuneCount = 13
 };
 
 // Current value of a knob.

@@ -1181,6 +1181,36 @@ def fp8_linear_backward_codes(codes, scales, grad, *, k, dtype, right_transposed
     return d_left, d_right
 
 
+def fp8_linear_backward_gemms(g_codes, g_t_codes, s_grad, left_t_codes, s_left, right_codes,
+                              s_right, *, k, dtype, right_transposed, need_left=True,
+                              need_right=True):
+    """The backward's two products from the gradient's codes (e5m2 ``g_codes``
+    [M, N] and ``g_t_codes`` [N, M]) and the forward's operand codes
+    (``left_t_codes`` [K, M], ``right_codes`` [K, N]), each scale a one-element
+    float32 tensor: ``(d_left [M, K] or None, d_right or None)`` as in
+    ``fp8_linear_backward_codes``. For callers that quantize the gradient
+    themselves (delayed scaling)."""
+
+    m, n = g_codes.shape if g_codes is not None else tuple(g_t_codes.shape)[::-1]
+    device = _on_device(g_codes, g_t_codes, left_t_codes, right_codes, s_grad)
+    d_left, d_right = _grad_buffers(m, k, n, dtype, True, need_left, need_right, device)
+    if m == 0 or n == 0 or k == 0:
+        for t in (d_left, d_right):
+            if t is not None:
+                t.zero_()
+    elif need_left or need_right:
+        ws = _workspace(nat.query("rpx_fp8_linear_backward_gemms_workspace", m, n, k), device)
+        nat.call("rpx_fp8_linear_backward_gemms", _ptr(g_codes if need_left else None),
+                 _ptr(g_t_codes if need_right else None), _ptr(s_grad), _ptr(left_t_codes),
+                 _ptr(s_left), _ptr(right_codes), _ptr(s_right), m, k, n, _ptr(d_left),
+                 _ptr(d_right), 1, _dtype_code(dtype), _ptr(ws), ws.numel(), _stream(device))
+    if d_right is not None:
+        # computed as [N, K]; the [K, N] gradient of a natural right operand
+        # is its transpose, made contiguous
+        d_right = d_right.t() if right_transposed else d_right.t().contiguous()
+    return d_left, d_right
+
+
 # ---------------------------------------------------------------------------
 # Delayed-scale fp8 (state: precision.DelayedScaling)
 # ---------------------------------------------------------------------------
@@ -1287,20 +1317,16 @@ class Fp8DelayedLinearFn(torch.autograd.Function):
     def backward(ctx, grad):
         qlt, qr, s_l, s_r, s_g = ctx.saved_tensors
         grad = grad.contiguous()
-        m, n = grad.shape
         k = qlt.shape[0]
         need_l, need_r = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
         qg, qgt = fp8_cast_delayed(grad, ctx.state, ctx.g_slot, "e5m2", rowmajor=need_l,
                                    transposed=need_r)
-        d_left = d_right = None
-        if need_l:
-            d_left = _gemm_into(qg, "e5m2", s_g, qr, "e4m3fn", s_r,
-                                torch.empty((m, k), dtype=ctx.dtype, device=grad.device))
-        if need_r:
-            # ((acc * s_left) * s_grad): the reference's order for this product
-            d_rt = _gemm_into(qgt, "e5m2", s_l, qlt, "e4m3fn", s_g,
-                              torch.empty((n, k), dtype=ctx.dtype, device=grad.device))
-            d_right = d_rt.t() if ctx.right_t else d_rt.t().contiguous()
+        if not (need_l or need_r):
+            return None, None, None, None, None
+        d_left, d_right = fp8_linear_backward_gemms(qg, qgt, s_g, qlt, s_l, qr, s_r, k=k,
+                                                    dtype=ctx.dtype,
+                                                    right_transposed=ctx.right_t,
+                                                    need_left=need_l, need_right=need_r)
         return d_left, d_right, None, None, None
 
 

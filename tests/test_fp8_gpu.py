@@ -8,6 +8,7 @@ import torch
 
 from oracle import fp8 as ofp8
 from oracle.codecs import E4M3FN, E5M2, bf16_bits_to_f32
+from representax_amd import _native as nat
 from representax_amd import ops
 from tests.helpers import bf16_values, from_dev, rel_l2, rng, to_dev, to_dev_bf16
 
@@ -225,6 +226,69 @@ def test_fused_quantize_scales_and_codes_bit_exact(m, k, n):
     assert s[0] == s_x and s[1] == s_w
     assert np.array_equal(codes[0].cpu().numpy(), ofp8.cast_with_scale(x, s_x, E4M3FN).T)
     assert np.array_equal(codes[1].cpu().numpy(), ofp8.cast_with_scale(w, s_w, E4M3FN).T)
+
+
+def _kernel_names(fn):
+    with torch.profiler.profile(activities=[torch.profiler.ProfilerActivity.CUDA]) as prof:
+        out = fn()
+        torch.cuda.synchronize()
+    return out, [e.key for e in prof.key_averages()]
+
+
+@pytest.mark.parametrize("m,k,n,paired", [(8192, 768, 768, True), (8192, 768, 3072, True),
+                                          (8192, 3072, 768, True), (8192, 700, 768, None)])
+def test_paired_backward_equals_two_launches(m, k, n, paired):
+    """The backward's input and weight gradients in one launch (the default
+    where both products' plans allow it: the BERT-base linears at 8192
+    tokens) equal the two separate launches bit for bit."""
+
+    x, w, gy = _fp8_case(m, k, n, seed=m + 5 * k + n)
+    _, scales, codes = ops.fp8_linear_forward(to_dev_bf16(x), to_dev_bf16(w).t(),
+                                              save_codes=True)
+    gd = to_dev_bf16(gy)
+    lib = nat.load()
+    old = lib.rpx_get_tuning(nat.TUNE_FP8_PAIR)
+    got = {}
+    try:
+        for v in (-1, 0):
+            assert lib.rpx_set_tuning(nat.TUNE_FP8_PAIR, v) == 0
+            got[v] = _kernel_names(lambda: ops.fp8_linear_backward_codes(
+                codes, scales, gd, k=k, dtype=torch.bfloat16, right_transposed=True))
+    finally:
+        lib.rpx_set_tuning(nat.TUNE_FP8_PAIR, old)
+    ran = {v: any("k_fp8_gemm_pair" in name for name in got[v][1]) for v in got}
+    assert not ran[0]
+    if paired is not None:
+        assert ran[-1] == paired
+    (dl1, dr1), (dl0, dr0) = got[-1][0], got[0][0]
+    assert torch.equal(dl1, dl0) and torch.equal(dr1, dr0)
+
+
+@pytest.mark.parametrize("m,k,n", [(8192, 768, 768), (300, 200, 256)])
+def test_backward_gemms_from_gradient_codes(m, k, n):
+    """rpx_fp8_linear_backward_gemms on gradient codes quantized by the
+    caller equals the backward that quantizes the gradient itself, for each
+    subset of outputs and both right-operand layouts."""
+
+    x, w, gy = _fp8_case(m, k, n, seed=m + 7 * k + n)
+    _, scales, codes = ops.fp8_linear_forward(to_dev_bf16(x), to_dev_bf16(w).t(), save_codes=True)
+    gd = to_dev_bf16(gy)
+    s_g = ops.fp8_scale(gd, E5M2)
+    qg, qgt = ops.fp8_cast(gd, s_g, E5M2, rowmajor=True, transposed=True)
+    for right_t in (True, False):
+        for need_l, need_r in ((True, True), (True, False), (False, True)):
+            want = ops.fp8_linear_backward_codes(codes, scales, gd, k=k, dtype=torch.bfloat16,
+                                                 right_transposed=right_t, need_left=need_l,
+                                                 need_right=need_r)
+            got = ops.fp8_linear_backward_gemms(qg, qgt, s_g, codes[0], scales[0:1], codes[1],
+                                                scales[1:2], k=k, dtype=torch.bfloat16,
+                                                right_transposed=right_t, need_left=need_l,
+                                                need_right=need_r)
+            torch.cuda.synchronize()
+            for a, b in zip(got, want):
+                assert (a is None) == (b is None)
+                if a is not None:
+                    assert a.shape == b.shape and torch.equal(a, b), (right_t, need_l, need_r)
 
 
 def test_fp8_linear_natural_right_layout():
