@@ -736,11 +736,15 @@ hipError_t launch_fp8_gemm(const uint8_t* a, int fmt_a, const float* s_a, const 
   return dispatch_fp8<1, 1>(a, b, m, n, k, s_a, s_b, out, out_dtype, ldc, split_ws, stream);
 }
 
-// Measured per backward (graph of 10, dX + dW + split reduce), 8192 tokens:
-// 768 -> 768 28.8 -> 23.6 us, 768 -> 3072 52.4 -> 49.5, 3072 -> 768
-// 62.0 -> 56.8. Each product keeps its own plan (the 512-thread 256 x 192
-// input-gradient tile becomes 128 x 192, which sums every output in the
-// same order), so the outputs equal the two separate launches' bit for bit.
+// Each product keeps its own plan (the 512-thread 256 x 192 input-gradient
+// tile becomes 128 x 192, which sums every output in the same order), so the
+// outputs equal the two separate launches' bit for bit. The BERT-base fp8
+// step at 8192 tokens (graph replays, one process): 0.5455 ms with two
+// launches per backward, 0.5240 with only the split-K weight gradients
+// (768 -> 768) paired, 0.5150 with every backward paired. Kernel traces
+// put the gain in the 768 -> 768 backward (31.2 -> 23.7 us, its weight
+// gradient runs 108 latency-bound blocks); the FFN backwards look even
+// under the profiler, which serializes the graph's nodes.
 hipError_t launch_fp8_backward_pair(const uint8_t* g, const uint8_t* right_codes,
                                     const uint8_t* g_t, const uint8_t* left_t_codes,
                                     const float* s_g, const float* s_right, const float* s_left,

@@ -235,8 +235,9 @@ def _kernel_names(fn):
     return out, [e.key for e in prof.key_averages()]
 
 
-@pytest.mark.parametrize("m,k,n,paired", [(8192, 768, 768, True), (8192, 768, 3072, True),
-                                          (8192, 3072, 768, True), (8192, 700, 768, None)])
+@pytest.mark.parametrize("m,k,n,paired", [(8192, 768, 768, True), (16384, 768, 768, True),
+                                          (8192, 768, 3072, True), (8192, 3072, 768, True),
+                                          (8192, 700, 768, None)])
 def test_paired_backward_equals_two_launches(m, k, n, paired):
     """The backward's input and weight gradients in one launch (the default
     where both products' plans allow it: the BERT-base linears at 8192
