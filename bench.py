@@ -198,12 +198,12 @@ def fp8_delayed_step_fn(layers, history_len=16):
     def step():
         for (_, x, w, gy, k, n), (sx, sw, sg) in zip(layers, slots):
             m = x.shape[0]
-            (qx, qxt), (qw, qwt) = ops.fp8_cast_delayed2(x, sx, w, sw, state, "e4m3fn",
-                                                         rowmajor=True, transposed=True)
+            (qx, _), (qw, qwt) = ops.fp8_cast_delayed2(x, sx, w, sw, state, "e4m3fn",
+                                                       rowmajor=True, transposed=(False, True))
             ops._gemm_into(qx, "e4m3fn", sc[sx:sx + 1], qw, "e4m3fn", sc[sw:sw + 1],
                            torch.empty((m, n), dtype=x.dtype, device=dev))
-            qg, qgt = ops.fp8_cast_delayed(gy, state, sg, "e5m2", rowmajor=True, transposed=True)
-            ops.fp8_linear_backward_gemms(qg, qgt, sc[sg:sg + 1], qxt, sc[sx:sx + 1], qwt,
+            qg, _ = ops.fp8_cast_delayed(gy, state, sg, "e5m2", rowmajor=True)
+            ops.fp8_linear_backward_gemms(qg, sc[sg:sg + 1], qx, sc[sx:sx + 1], qwt,
                                           sc[sw:sw + 1], k=k, dtype=x.dtype,
                                           right_transposed=True)
         state.update()
@@ -255,8 +255,8 @@ def fp8_gemm_calls(layers, paired=True):
         calls.append((lambda a=qx, b=qw, sa=s_x, sb=s_w: ops.fp8_gemm(a, "e4m3fn", sa, b, "e4m3fn", sb),
                       2.0 * m * n * k, fwd_bytes))
         if paired:
-            calls.append((lambda qg=qg, qgt=qgt, s_g=s_g, qxt=qxt, s_x=s_x, qwt=qwt, s_w=s_w, k=k:
-                          ops.fp8_linear_backward_gemms(qg, qgt, s_g, qxt, s_x, qwt, s_w, k=k,
+            calls.append((lambda qg=qg, s_g=s_g, qx=qx, s_x=s_x, qwt=qwt, s_w=s_w, k=k:
+                          ops.fp8_linear_backward_gemms(qg, s_g, qx, s_x, qwt, s_w, k=k,
                                                         dtype=torch.bfloat16,
                                                         right_transposed=True),
                           4.0 * m * n * k, dx_bytes + dw_bytes))
@@ -333,17 +333,18 @@ def fp8_gemm_roofline(layers, reps=16):
 
 
 def fp8_quantize_report(layers, step_ms, gemm_us):
-    """The dynamic quantize passes of one step (amax, then the cast into both
-    code layouts) against HBM bandwidth. Their time is the step's minus its
-    12 GEMM launches' (each timed alone in a graph); their algorithmic bytes per
-    linear are 6 (MK + NK + MN): the amax pass reads x, W and g in bf16, the
-    cast reads them again and writes one byte per element in each of the two
-    layouts."""
+    """The dynamic quantize passes of one step (amax, then the cast) against
+    HBM bandwidth. Their time is the step's minus its 12 GEMM launches' (each
+    timed alone in a graph); their algorithmic bytes per linear are
+    5 MK + 6 NK + 5 MN: the amax pass reads x, W and g in bf16, the cast reads
+    them again and writes one byte per element of x and g (row-major; the
+    weight gradient reads them along the tokens) and two of W (row-major for
+    the forward, transposed for the input gradient)."""
 
     nbytes = 0.0
     for _, x, _, _, k, n in layers:
         m = x.shape[0]
-        nbytes += 6.0 * (m * k + n * k + m * n)
+        nbytes += 5.0 * m * k + 6.0 * n * k + 5.0 * m * n
     us = 1e3 * step_ms - gemm_us
     gbs = nbytes / (us * 1e-6) / 1e9 if us > 0 else None
     return {"us_per_step": round(us, 1), "algorithmic_bytes_per_step": nbytes,

@@ -364,15 +364,16 @@ size_t rpx_fp8_linear_forward_workspace(int64_t m, int64_t n, int64_t k);
 /* out [m, n] = _fp8_linear_dot(left [m, k], right [k, n]) with e4m3 operands;
  * right is addressed through (row_stride, col_stride) so a transposed weight
  * view needs no copy. scales_out[0..1] receive (s_left, s_right). The same
- * pass can also write the backward's operand codes: left_t_codes [k, m] and
- * right_codes [k, n] (either may be NULL). m, n, k > 0: an empty operand has
- * no amax, and the reference's max reduction raises on it. Replaces _fp8_linear_dot /
+ * pass can also write the backward's operand codes: left_codes [m, k]
+ * (row-major, the product's own) and right_codes [k, n] (either may be
+ * NULL). m, n, k > 0: an empty operand has no amax, and the reference's max
+ * reduction raises on it. Replaces _fp8_linear_dot /
  * _fp8_linear_dot_forward, src/representax/precision.py:173-198 (as used by
  * linear_matmul, :224-239). */
 int rpx_fp8_linear_forward(const void* left, int left_dtype, int64_t m, int64_t k,
                            const void* right, int right_dtype, int64_t n, int64_t right_row_stride,
                            int64_t right_col_stride, void* out, int out_dtype, float* scales_out,
-                           uint8_t* left_t_codes, uint8_t* right_codes, void* workspace,
+                           uint8_t* left_codes, uint8_t* right_codes, void* workspace,
                            size_t workspace_bytes, void* stream);
 
 size_t rpx_fp8_linear_backward_workspace(int64_t m, int64_t n, int64_t k);
@@ -391,10 +392,10 @@ int rpx_fp8_linear_backward(const void* left, int left_dtype, const void* right,
                             size_t workspace_bytes, void* stream);
 
 /* The same backward from the operand codes that rpx_fp8_linear_forward
- * saved (left_t_codes [k, m], right_codes [k, n]); the bf16 operands are not
+ * saved (left_codes [m, k], right_codes [k, n]); the bf16 operands are not
  * read again. Workspace: rpx_fp8_linear_backward_workspace(m, n, k).
  * Replaces _fp8_linear_dot_backward, src/representax/precision.py:201-218. */
-int rpx_fp8_linear_backward_codes(const uint8_t* left_t_codes, const uint8_t* right_codes,
+int rpx_fp8_linear_backward_codes(const uint8_t* left_codes, const uint8_t* right_codes,
                                   const float* scales, int64_t m, int64_t k, int64_t n,
                                   const void* grad, int grad_dtype, void* d_left, void* d_right,
                                   int d_right_transposed, int out_dtype, void* workspace,
@@ -405,8 +406,8 @@ int rpx_fp8_linear_backward_codes(const uint8_t* left_t_codes, const uint8_t* ri
  *   d_left [m, k] = ((g . right^T) * s_grad) * s_right, from g_codes [m, n]
  *     (e5m2) and right_codes [k, n] (e4m3);
  *   d_right = ((left^T . g) * s_left) * s_grad, as [k, n] or as [n, k] when
- *     d_right_transposed, from g_t_codes [n, m] (e5m2) and left_t_codes
- *     [k, m] (e4m3).
+ *     d_right_transposed, from the same g_codes and left_codes [m, k]
+ *     (e4m3), both row-major: the kernel reads them along the tokens.
  * Either output may be NULL (then its codes and scale may be too). With both
  * outputs and d_right_transposed, the two products run in one launch where
  * their tile plans allow it (RPX_TUNE_FP8_PAIR), with the same results as
@@ -414,13 +415,12 @@ int rpx_fp8_linear_backward_codes(const uint8_t* left_t_codes, const uint8_t* ri
  * rpx_fp8_linear_backward_gemms_workspace(m, n, k).
  * Replaces the two _scaled_fp8_dot calls of _fp8_linear_dot_backward,
  * src/representax/precision.py:201-218. */
-int rpx_fp8_linear_backward_gemms(const uint8_t* g_codes, const uint8_t* g_t_codes,
-                                  const float* s_grad, const uint8_t* left_t_codes,
-                                  const float* s_left, const uint8_t* right_codes,
-                                  const float* s_right, int64_t m, int64_t k, int64_t n,
-                                  void* d_left, void* d_right, int d_right_transposed,
-                                  int out_dtype, void* workspace, size_t workspace_bytes,
-                                  void* stream);
+int rpx_fp8_linear_backward_gemms(const uint8_t* g_codes, const float* s_grad,
+                                  const uint8_t* left_codes, const float* s_left,
+                                  const uint8_t* right_codes, const float* s_right, int64_t m,
+                                  int64_t k, int64_t n, void* d_left, void* d_right,
+                                  int d_right_transposed, int out_dtype, void* workspace,
+                                  size_t workspace_bytes, void* stream);
 
 size_t rpx_fp8_linear_backward_gemms_workspace(int64_t m, int64_t n, int64_t k);
 

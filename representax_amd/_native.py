@@ -118,7 +118,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
     "rpx_fp8_linear_backward_gemms_workspace": (_size, [_i64, _i64, _i64]),
     "rpx_fp8_linear_backward_gemms": (
-        _int, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _p, _int, _int, _p, _size, _p]
+        _int, [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _p, _int, _int, _p, _size, _p]
     ),
     "rpx_fp8_delayed_pending_words": (_size, []),
     "rpx_fp8_cast_delayed": (

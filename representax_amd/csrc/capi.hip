@@ -1229,9 +1229,12 @@ constexpr Fp8Table make_fp8_table() {
 
 __constant__ Fp8Table c_fp8_table = make_fp8_table();
 
+// a(m, kk) = a[m * a_sm + kk * a_sk], b(n, kk) = b[n * b_sn + kk * b_sk]:
+// row-major [M, K] / [N, K] codes, or K-row [K, M] / [K, N] ones.
 __global__ void __launch_bounds__(256)
     k_fp8_gemm_generic(const uint8_t* __restrict__ a, int fmt_a, const uint8_t* __restrict__ b,
-                       int fmt_b, int64_t M, int64_t N, int64_t K, const float* __restrict__ s_a,
+                       int fmt_b, int64_t M, int64_t N, int64_t K, int64_t a_sm, int64_t a_sk,
+                       int64_t b_sn, int64_t b_sk, const float* __restrict__ s_a,
                        const float* __restrict__ s_b, void* __restrict__ out, int out_dtype) {
   const int64_t total = M * N;
   for (int64_t e = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; e < total;
@@ -1240,7 +1243,8 @@ __global__ void __launch_bounds__(256)
     const int64_t n = e % N;
     float acc = 0.0f;
     for (int64_t kk = 0; kk < K; ++kk)
-      acc = __builtin_fmaf(c_fp8_table.v[fmt_a][a[m * K + kk]], c_fp8_table.v[fmt_b][b[n * K + kk]], acc);
+      acc = __builtin_fmaf(c_fp8_table.v[fmt_a][a[m * a_sm + kk * a_sk]],
+                           c_fp8_table.v[fmt_b][b[n * b_sn + kk * b_sk]], acc);
     const float y = (acc * s_a[0]) * s_b[0];
     if (out_dtype == kBF16)
       static_cast<uint16_t*>(out)[e] = f32_to_bf16(y);
@@ -1276,7 +1280,7 @@ int rpx_fp8_gemm(const uint8_t* a, int fmt_a, const float* scale_a, const uint8_
     return kOk;
   }
   hipLaunchKernelGGL(k_fp8_gemm_generic, dim3(grid1d(m * n)), dim3(256), 0, st, a, fmt_a, b, fmt_b,
-                     m, n, k, scale_a, scale_b, out, out_dtype);
+                     m, n, k, k, int64_t{1}, k, int64_t{1}, scale_a, scale_b, out, out_dtype);
   RPX_HIP(hipGetLastError(), "rpx_fp8_gemm (generic)");
   return kOk;
 }
@@ -1284,6 +1288,33 @@ int rpx_fp8_gemm(const uint8_t* a, int fmt_a, const float* scale_a, const uint8_
 }  // extern "C"
 
 namespace {
+// out [m, n] = ((a^T . b) * s_a) * s_b from K-row codes a [k, m] and b [k, n]:
+// the pipelined K-row GEMM where the shapes and alignment allow it, else the
+// generic kernel. Workspace: fp8_krows_bytes(m, n, k).
+size_t fp8_krows_bytes(int64_t m, int64_t n, int64_t k) {
+  if (k % 128 != 0 || m % 16 != 0 || n % 16 != 0) return 0;
+  return static_cast<size_t>(fp8_gemm_krows_workspace_floats(m, n, k)) * sizeof(float);
+}
+
+int fp8_gemm_krows(const uint8_t* a, int fmt_a, const float* s_a, const uint8_t* b, int fmt_b,
+                   const float* s_b, int64_t m, int64_t n, int64_t k, void* out, int out_dtype,
+                   void* workspace, size_t workspace_bytes, hipStream_t st) {
+  if (k % 128 == 0 && m % 16 == 0 && n % 16 == 0 && aligned16(a) && aligned16(b)) {
+    const size_t need = fp8_krows_bytes(m, n, k);
+    if (need > workspace_bytes || (need > 0 && workspace == nullptr))
+      return fail_invalid("fp8 K-row GEMM: workspace too small");
+    RPX_HIP(launch_fp8_gemm_krows(a, fmt_a, s_a, b, fmt_b, s_b, m, n, k, out, out_dtype, n,
+                                  static_cast<float*>(workspace),
+                                  static_cast<int64_t>(need / sizeof(float)), st),
+            "fp8 K-row GEMM");
+    return kOk;
+  }
+  hipLaunchKernelGGL(k_fp8_gemm_generic, dim3(grid1d(m * n)), dim3(256), 0, st, a, fmt_a, b, fmt_b,
+                     m, n, k, int64_t{1}, m, int64_t{1}, n, s_a, s_b, out, out_dtype);
+  RPX_HIP(hipGetLastError(), "fp8 K-row GEMM (generic)");
+  return kOk;
+}
+
 template <typename A>
 void plan_fp8_forward(A& a, int64_t m, int64_t n, int64_t k) {
   a.template take<uint32_t>(fp8_quant_partials(m, k));
@@ -1297,9 +1328,8 @@ void plan_fp8_backward(A& a, int64_t m, int64_t n, int64_t k) {
   a.template take<uint32_t>(fp8_quant_partials(m, n));
   a.template take<float>(1);
   a.template take<uint8_t>(m * n);  // g codes [M, N]
-  a.template take<uint8_t>(n * m);  // g codes [N, M]
   a.template take<uint8_t>(k * n);  // right codes [K, N]
-  a.template take<uint8_t>(k * m);  // left codes [K, M]
+  a.template take<uint8_t>(m * k);  // left codes [M, K]
   a.template take<uint8_t>(static_cast<int64_t>(rpx_fp8_linear_backward_gemms_workspace(m, n, k)));
 }
 }  // namespace
@@ -1315,7 +1345,7 @@ size_t rpx_fp8_linear_forward_workspace(int64_t m, int64_t n, int64_t k) {
 int rpx_fp8_linear_forward(const void* left, int left_dtype, int64_t m, int64_t k,
                            const void* right, int right_dtype, int64_t n, int64_t right_row_stride,
                            int64_t right_col_stride, void* out, int out_dtype, float* scales_out,
-                           uint8_t* left_t_codes, uint8_t* right_codes, void* workspace,
+                           uint8_t* left_codes, uint8_t* right_codes, void* workspace,
                            size_t workspace_bytes, void* stream) {
   RPX_TRY(check_dtype(left_dtype));
   RPX_TRY(check_dtype(right_dtype));
@@ -1332,16 +1362,18 @@ int rpx_fp8_linear_forward(const void* left, int left_dtype, int64_t m, int64_t 
   Arena ar(workspace, workspace_bytes);
   uint32_t* pl = ar.take<uint32_t>(fp8_quant_partials(m, k));
   uint32_t* pr = ar.take<uint32_t>(fp8_quant_partials(k, n));
-  uint8_t* ql = ar.take<uint8_t>(m * k);
+  uint8_t* ql_ws = ar.take<uint8_t>(m * k);
   uint8_t* qr = ar.take<uint8_t>(n * k);
   const size_t gws = rpx_fp8_gemm_workspace(m, n, k);
   uint8_t* gw = ar.take<uint8_t>(static_cast<int64_t>(gws));
   if (ar.overflow) return fail_invalid("rpx_fp8_linear_forward: workspace too small");
   // both tensors' amaxes in one launch, then both casts in one launch:
-  // left [M, K] -> codes [M, K] (+ [K, M] for the weight gradient);
-  // right [K, N] -> codes [N, K] for this product (+ [K, N] for the input gradient)
-  RPX_HIP(launch_fp8_quantize2(left, left_dtype, m, k, k, 1, pl, scales_out, ql, left_t_codes,
-                               right, right_dtype, k, n, right_row_stride, right_col_stride, pr,
+  // left [M, K] -> codes [M, K] (this product's, and the weight gradient's
+  // K-row operand); right [K, N] -> codes [N, K] for this product (+ [K, N]
+  // for the input gradient)
+  uint8_t* ql = left_codes != nullptr ? left_codes : ql_ws;
+  RPX_HIP(launch_fp8_quantize2(left, left_dtype, m, k, k, 1, pl, scales_out, ql, nullptr, right,
+                               right_dtype, k, n, right_row_stride, right_col_stride, pr,
                                scales_out + 1, right_codes, qr, kE4M3FN, st),
           "fp8_linear_forward: quantize");
   return rpx_fp8_gemm(ql, kE4M3FN, scales_out, qr, kE4M3FN, scales_out + 1, m, n, k, out,
@@ -1354,7 +1386,7 @@ size_t rpx_fp8_linear_backward_workspace(int64_t m, int64_t n, int64_t k) {
   return s.used;
 }
 
-int rpx_fp8_linear_backward_codes(const uint8_t* left_t_codes, const uint8_t* right_codes,
+int rpx_fp8_linear_backward_codes(const uint8_t* left_codes, const uint8_t* right_codes,
                                   const float* scales, int64_t m, int64_t k, int64_t n,
                                   const void* grad, int grad_dtype, void* d_left, void* d_right,
                                   int d_right_transposed, int out_dtype, void* workspace,
@@ -1364,62 +1396,59 @@ int rpx_fp8_linear_backward_codes(const uint8_t* left_t_codes, const uint8_t* ri
   if (m <= 0 || n <= 0 || k <= 0)
     return fail_invalid("rpx_fp8_linear_backward: m, n, k must be positive");
   if (grad == nullptr || scales == nullptr || (d_left != nullptr && right_codes == nullptr) ||
-      (d_right != nullptr && left_t_codes == nullptr))
+      (d_right != nullptr && left_codes == nullptr))
     return fail_invalid("rpx_fp8_linear_backward: null pointer");
   hipStream_t st = static_cast<hipStream_t>(stream);
   Arena ar(workspace, workspace_bytes);
   uint32_t* pg = ar.take<uint32_t>(fp8_quant_partials(m, n));
   float* sg = ar.take<float>(1);
   uint8_t* qg = ar.take<uint8_t>(m * n);
-  uint8_t* qgt = ar.take<uint8_t>(n * m);
   ar.take<uint8_t>(k * n);
-  ar.take<uint8_t>(k * m);
+  ar.take<uint8_t>(m * k);
   const size_t gws = rpx_fp8_linear_backward_gemms_workspace(m, n, k);
   uint8_t* gw = ar.take<uint8_t>(static_cast<int64_t>(gws));
   if (ar.overflow) return fail_invalid("rpx_fp8_linear_backward: workspace too small");
-  // s_g (e5m2) and the gradient codes in the layouts the two products need
-  RPX_HIP(launch_fp8_quantize2(grad, grad_dtype, m, n, n, 1, pg, sg, d_left ? qg : nullptr,
-                               d_right ? qgt : nullptr, nullptr, grad_dtype, 0, 0, 0, 1, nullptr,
-                               nullptr, nullptr, nullptr, kE5M2, st),
+  // s_g (e5m2) and the gradient's codes [M, N], the operand of both products
+  RPX_HIP(launch_fp8_quantize2(grad, grad_dtype, m, n, n, 1, pg, sg, qg, nullptr, nullptr,
+                               grad_dtype, 0, 0, 0, 1, nullptr, nullptr, nullptr, nullptr, kE5M2,
+                               st),
           "fp8_linear_backward: quantize(grad)");
-  return rpx_fp8_linear_backward_gemms(d_left ? qg : nullptr, d_right ? qgt : nullptr, sg,
-                                       left_t_codes, scales, right_codes, scales + 1, m, k, n,
-                                       d_left, d_right, d_right_transposed, out_dtype, gw, gws,
+  return rpx_fp8_linear_backward_gemms(qg, sg, left_codes, scales, right_codes, scales + 1, m, k,
+                                       n, d_left, d_right, d_right_transposed, out_dtype, gw, gws,
                                        stream);
 }
 
 size_t rpx_fp8_linear_backward_gemms_workspace(int64_t m, int64_t n, int64_t k) {
   size_t g1 = rpx_fp8_gemm_workspace(m, k, n);
-  size_t g2 = rpx_fp8_gemm_workspace(k, n, m);
-  const size_t g3 = rpx_fp8_gemm_workspace(n, k, m);
+  size_t g2 = fp8_krows_bytes(k, n, m);
+  const size_t g3 = fp8_krows_bytes(n, k, m);
   if (g2 < g3) g2 = g3;
   return g1 > g2 ? g1 : g2;
 }
 
-int rpx_fp8_linear_backward_gemms(const uint8_t* g_codes, const uint8_t* g_t_codes,
-                                  const float* s_grad, const uint8_t* left_t_codes,
-                                  const float* s_left, const uint8_t* right_codes,
-                                  const float* s_right, int64_t m, int64_t k, int64_t n,
-                                  void* d_left, void* d_right, int d_right_transposed,
-                                  int out_dtype, void* workspace, size_t workspace_bytes,
-                                  void* stream) {
+int rpx_fp8_linear_backward_gemms(const uint8_t* g_codes, const float* s_grad,
+                                  const uint8_t* left_codes, const float* s_left,
+                                  const uint8_t* right_codes, const float* s_right, int64_t m,
+                                  int64_t k, int64_t n, void* d_left, void* d_right,
+                                  int d_right_transposed, int out_dtype, void* workspace,
+                                  size_t workspace_bytes, void* stream) {
   RPX_TRY(check_dtype(out_dtype));
   if (m <= 0 || n <= 0 || k <= 0)
     return fail_invalid("rpx_fp8_linear_backward_gemms: m, n, k must be positive");
-  if (s_grad == nullptr ||
-      (d_left != nullptr && (g_codes == nullptr || right_codes == nullptr || s_right == nullptr)) ||
-      (d_right != nullptr && (g_t_codes == nullptr || left_t_codes == nullptr || s_left == nullptr)))
+  if (g_codes == nullptr || s_grad == nullptr ||
+      (d_left != nullptr && (right_codes == nullptr || s_right == nullptr)) ||
+      (d_right != nullptr && (left_codes == nullptr || s_left == nullptr)))
     return fail_invalid("rpx_fp8_linear_backward_gemms: null pointer");
   const size_t gws = rpx_fp8_linear_backward_gemms_workspace(m, n, k);
   if (workspace_bytes < gws || (gws > 0 && workspace == nullptr))
     return fail_invalid("rpx_fp8_linear_backward_gemms: workspace too small");
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (d_left != nullptr && d_right != nullptr && d_right_transposed &&
-      aligned16_all({g_codes, g_t_codes, right_codes, left_t_codes})) {
+      aligned16_all({g_codes, right_codes, left_codes})) {
     // both products in one launch where their plans allow it
     bool paired = false;
-    RPX_HIP(launch_fp8_backward_pair(g_codes, right_codes, g_t_codes, left_t_codes, s_grad,
-                                     s_right, s_left, m, k, n, d_left, d_right, out_dtype,
+    RPX_HIP(launch_fp8_backward_pair(g_codes, right_codes, left_codes, s_grad, s_right, s_left, m,
+                                     k, n, d_left, d_right, out_dtype,
                                      static_cast<float*>(workspace),
                                      static_cast<int64_t>(gws / sizeof(float)), st, &paired),
             "fp8_linear_backward: paired products");
@@ -1430,15 +1459,13 @@ int rpx_fp8_linear_backward_gemms(const uint8_t* g_codes, const uint8_t* g_t_cod
     RPX_TRY(rpx_fp8_gemm(g_codes, kE5M2, s_grad, right_codes, kE4M3FN, s_right, m, k, n, d_left,
                          out_dtype, workspace, gws, stream));
   if (d_right == nullptr) return kOk;
-  // d_right = ((left^T . g) * s_l) * s_g, as [K, N] or transposed [N, K]
-  if (d_right_transposed) {
-    RPX_TRY(rpx_fp8_gemm(g_t_codes, kE5M2, s_left, left_t_codes, kE4M3FN, s_grad, n, k, m,
-                         d_right, out_dtype, workspace, gws, stream));
-  } else {
-    RPX_TRY(rpx_fp8_gemm(left_t_codes, kE4M3FN, s_left, g_t_codes, kE5M2, s_grad, k, n, m,
-                         d_right, out_dtype, workspace, gws, stream));
-  }
-  return kOk;
+  // d_right = ((left^T . g) * s_l) * s_g over the tokens, from the K-row
+  // (tokens-major) codes of both operands, as [K, N] or transposed [N, K]
+  if (d_right_transposed)
+    return fp8_gemm_krows(g_codes, kE5M2, s_left, left_codes, kE4M3FN, s_grad, n, k, m, d_right,
+                          out_dtype, workspace, gws, st);
+  return fp8_gemm_krows(left_codes, kE4M3FN, s_left, g_codes, kE5M2, s_grad, k, n, m, d_right,
+                        out_dtype, workspace, gws, st);
 }
 
 int rpx_fp8_linear_backward(const void* left, int left_dtype, const void* right, int right_dtype,
@@ -1460,9 +1487,8 @@ int rpx_fp8_linear_backward(const void* left, int left_dtype, const void* right,
   ar.take<uint32_t>(fp8_quant_partials(m, n));
   ar.take<float>(1);
   ar.take<uint8_t>(m * n);
-  ar.take<uint8_t>(n * m);
   uint8_t* qr = ar.take<uint8_t>(k * n);
-  uint8_t* qlt = ar.take<uint8_t>(k * m);
+  uint8_t* ql = ar.take<uint8_t>(m * k);
   if (ar.overflow) return fail_invalid("rpx_fp8_linear_backward: workspace too small");
   if (d_left != nullptr)
     RPX_HIP(launch_fp8_cast(right, right_dtype, k, n, right_row_stride, right_col_stride,
@@ -1470,9 +1496,9 @@ int rpx_fp8_linear_backward(const void* left, int left_dtype, const void* right,
             "fp8_linear_backward: cast(right)");
   if (d_right != nullptr)
     RPX_HIP(launch_fp8_cast(left, left_dtype, m, k, k, 1, scales, nullptr, 0, nullptr, kE4M3FN,
-                            nullptr, qlt, st),
+                            ql, nullptr, st),
             "fp8_linear_backward: cast(left)");
-  return rpx_fp8_linear_backward_codes(qlt, qr, scales, m, k, n, grad, grad_dtype, d_left, d_right,
+  return rpx_fp8_linear_backward_codes(ql, qr, scales, m, k, n, grad, grad_dtype, d_left, d_right,
                                        d_right_transposed, out_dtype, workspace, workspace_bytes,
                                        stream);
 }

@@ -48,6 +48,35 @@ __device__ __forceinline__ i32x8_t load_frag(const uint8_t* stage, int row, int 
                  (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
 }
 
+typedef int i32x2_t __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) i32x2_t lds_i32x2_t;
+
+// The same fragment from a K-row tile (LDS row k holds the 128 code bytes of
+// columns [0, 128) at reduction index k, 16-byte chunks swizzled by swz(k)):
+// lane l needs column col0 + (l & 31) at k = 64 kk + 32 (l >> 5) + [0, 32).
+// ds_read_b64_tr_b8 gives lane i of each 16-lane group byte i & 7 of the
+// 8-byte pieces that lanes (i >> 3) + 2 e of the group address (e = 0..7),
+// as byte e: lane j of the group addresses row k0 + (j >> 1) at column
+// c0 + 8 (j & 1), so lane i receives column c0 + i at rows k0 .. k0 + 7.
+// Four reads give the 32 reduction bytes, in order.
+__device__ __forceinline__ i32x8_t load_frag_krows(const uint8_t* stage, int col0, int kk,
+                                                   int lane) {
+  const int g = lane >> 4;
+  const int j = lane & 15;
+  const int col = col0 + 16 * (g & 1) + 8 * (j & 1);
+  const int k0 = 64 * kk + 32 * (g >> 1) + (j >> 1);
+  i32x8_t f;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int k = k0 + 8 * r;
+    const uint8_t* q = stage + k * kBK + ((((col >> 4) ^ swz(k))) << 4) + (col & 15);
+    const i32x2_t v = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2_t*)q);
+    f[2 * r] = v[0];
+    f[2 * r + 1] = v[1];
+  }
+  return f;
+}
+
 // Pipelined fp8 GEMM. A workgroup of WM x WN waves computes a BM x BN tile
 // (each wave a (BM/WM) x (BN/WN) sub-tile of 32x32 MFMA blocks) over the
 // K-range of its split. K-slices of 128 bytes of A and B move global -> LDS
@@ -60,7 +89,16 @@ __device__ __forceinline__ i32x8_t load_frag(const uint8_t* stage, int row, int 
 // registers (16 bytes per lane).
 // Block `bid` of the `nblk` that run this product (a launch may hold other
 // products' blocks too; see k_fp8_gemm_pair).
-template <int BM, int BN, int WM, int WN, int NS, int FA, int FB>
+//
+// KROWS: both operands are stored with the reduction index as their row, A
+// as [K, M] and B as [K, N] row-major codes (out = A^T B, the weight
+// gradient from the tokens-major codes of the gradient and the input, with
+// no transposed copies). A slice is then 128 rows of 128 code bytes of each
+// operand (128 x 128 tiles only), loaded by the same direct-to-LDS segments
+// and read back through transposing LDS reads (load_frag_krows). Columns
+// past the edge re-read the last 16 bytes of their row (M, N multiples of
+// 16), which only feeds outputs that are never stored.
+template <int BM, int BN, int WM, int WN, int NS, int FA, int FB, bool KROWS = false>
 __device__ __forceinline__ void fp8_gemm_block(
     int bid, int nblk, const uint8_t* __restrict__ A, const uint8_t* __restrict__ B, int64_t M,
     int64_t N, int64_t K, int64_t k_per_split, const float* __restrict__ s_a,
@@ -78,6 +116,7 @@ __device__ __forceinline__ void fp8_gemm_block(
   constexpr int LPW = SEGS / NW;
   static_assert(NS >= 2 && NS <= 4 && LPW * (NS - 1) < 64, "vmcnt range");
   constexpr int STAGE = (BM + BN) * kBK;
+  static_assert(!KROWS || (BM == kBK && BN == kBK), "K-row operands need 128 x 128 tiles");
   extern __shared__ __align__(16) uint8_t smem[];
 
   // the scales are needed only by the epilogue; their load is issued first so
@@ -108,18 +147,29 @@ __device__ __forceinline__ void fp8_gemm_block(
   const int nk = static_cast<int>((kend - kbeg) / kBK);
 
   // Per-lane DMA sources: segment j = wave + i * NW covers tile rows 8j..8j+7
-  // of A (j < A_SEGS) or of B; rows past the edge re-read the last row.
+  // of A (j < A_SEGS) or of B; rows past the edge re-read the last row. With
+  // KROWS a segment is 8 reduction rows of the operand's 128-column block,
+  // and a K offset moves by whole rows (kstep[i] bytes per unit).
   const int seg_row = lane >> 3;
   const uint8_t* src[LPW];
+  int64_t kstep[LPW];
 #pragma unroll
   for (int i = 0; i < LPW; ++i) {
     const int j = wave + i * NW;
     const bool is_a = j < A_SEGS;
     const int trow = (is_a ? 8 * j : 8 * (j - A_SEGS)) + seg_row;
-    int64_t r = (is_a ? m0 : n0) + trow;
     const int64_t lim = is_a ? M : N;
-    r = r < lim ? r : lim - 1;
-    src[i] = (is_a ? A : B) + r * K + kbeg + (((lane & 7) ^ swz(trow)) << 4);
+    if constexpr (KROWS) {
+      int64_t c = (is_a ? m0 : n0) + (((lane & 7) ^ swz(trow)) << 4);
+      c = c + 16 <= lim ? c : lim - 16;
+      src[i] = (is_a ? A : B) + (kbeg + trow) * lim + c;
+      kstep[i] = lim;
+    } else {
+      int64_t r = (is_a ? m0 : n0) + trow;
+      r = r < lim ? r : lim - 1;
+      src[i] = (is_a ? A : B) + r * K + kbeg + (((lane & 7) ^ swz(trow)) << 4);
+      kstep[i] = 1;
+    }
   }
 
   f32x16_t acc[FN][FM];
@@ -133,12 +183,17 @@ __device__ __forceinline__ void fp8_gemm_block(
   const int frow = lane & 31;
   const int half = lane >> 5;
   i32x8_t a_cur[FM], b_cur[FN], a_nxt[FM], b_nxt[FN];
+  auto frag = [&](const uint8_t* st, int row0, int kk) {
+    if constexpr (KROWS)
+      return load_frag_krows(st, row0, kk, lane);
+    else
+      return load_frag(st, row0 + frow, kk, half);
+  };
   auto load_all = [&](const uint8_t* st, int kk, i32x8_t* af, i32x8_t* bf) {
 #pragma unroll
-    for (int fm = 0; fm < FM; ++fm) af[fm] = load_frag(st, wm * TM + fm * 32 + frow, kk, half);
+    for (int fm = 0; fm < FM; ++fm) af[fm] = frag(st, wm * TM + fm * 32, kk);
 #pragma unroll
-    for (int fn = 0; fn < FN; ++fn)
-      bf[fn] = load_frag(st + BM * kBK, wn * TN + fn * 32 + frow, kk, half);
+    for (int fn = 0; fn < FN; ++fn) bf[fn] = frag(st + BM * kBK, wn * TN + fn * 32, kk);
   };
   // Main loop, branch-free. Slice t lives in stage t % NS. Per slice:
   //   A: MFMAs of 64-deep step 0, each followed by DS reads of step 1's
@@ -158,14 +213,20 @@ __device__ __forceinline__ void fp8_gemm_block(
   };
   auto frag_one = [&](const uint8_t* st, int kk, int j, i32x8_t* af, i32x8_t* bf) {
     if (j < FM)
-      af[j] = load_frag(st, wm * TM + j * 32 + frow, kk, half);
+      af[j] = frag(st, wm * TM + j * 32, kk);
     else
-      bf[j - FM] = load_frag(st + BM * kBK, wn * TN + (j - FM) * 32 + frow, kk, half);
+      bf[j - FM] = frag(st + BM * kBK, wn * TN + (j - FM) * 32, kk);
   };
 #pragma unroll
-  for (int s = 0; s < NS; ++s)
-    dma_slice<LPW, NW>(smem + s * STAGE, src, static_cast<int64_t>(s < nk ? s : nk - 1) * kBK,
-                       wave);
+  for (int s = 0; s < NS; ++s) {
+    const int64_t koff = static_cast<int64_t>(s < nk ? s : nk - 1) * kBK;
+    if constexpr (KROWS) {
+#pragma unroll
+      for (int i = 0; i < LPW; ++i) dma_seg(smem + s * STAGE, src[i], koff * kstep[i], wave + i * NW);
+    } else {
+      dma_slice<LPW, NW>(smem + s * STAGE, src, koff, wave);
+    }
+  }
   wait_sync<(NS - 1) * LPW>();
   load_all(smem, 0, a_cur, b_cur);
   int stage = 0;
@@ -190,7 +251,7 @@ __device__ __forceinline__ void fp8_gemm_block(
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int d = i * LPW / NMF; d < (i + 1) * LPW / NMF; ++d)
-        dma_seg(fill, src[d], refill, wave + d * NW);
+        dma_seg(fill, src[d], KROWS ? refill * kstep[d] : refill, wave + d * NW);
 #pragma unroll
       for (int j = i * NFR / NMF; j < (i + 1) * NFR / NMF; ++j) frag_one(nst, 0, j, a_cur, b_cur);
       __builtin_amdgcn_sched_barrier(0);
@@ -304,16 +365,16 @@ __device__ __forceinline__ void fp8_gemm_block(
   }
 }
 
-template <int BM, int BN, int WM, int WN, int NS, int WPE, int FA, int FB>
+template <int BM, int BN, int WM, int WN, int NS, int WPE, int FA, int FB, bool KROWS = false>
 __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
     k_fp8_gemm(const uint8_t* __restrict__ A, const uint8_t* __restrict__ B, int64_t M, int64_t N,
                int64_t K, int64_t k_per_split, const float* __restrict__ s_a,
                const float* __restrict__ s_b, void* __restrict__ out, int out_dtype, int64_t ldc,
                float* __restrict__ partials, int tiles_m, int tiles_n, int band) {
-  fp8_gemm_block<BM, BN, WM, WN, NS, FA, FB>(static_cast<int>(blockIdx.x),
-                                             static_cast<int>(gridDim.x), A, B, M, N, K,
-                                             k_per_split, s_a, s_b, out, out_dtype, ldc, partials,
-                                             tiles_m, tiles_n, band);
+  fp8_gemm_block<BM, BN, WM, WN, NS, FA, FB, KROWS>(static_cast<int>(blockIdx.x),
+                                                    static_cast<int>(gridDim.x), A, B, M, N, K,
+                                                    k_per_split, s_a, s_b, out, out_dtype, ldc,
+                                                    partials, tiles_m, tiles_n, band);
 }
 
 // Sums the split-K partial tiles written by k_fp8_gemm<BM, BN, WM, WN, ...>
@@ -564,7 +625,7 @@ int fp8_band(int tiles_m, int tiles_n, int64_t blocks, int bm, int bn) {
   return best;
 }
 
-template <int BM, int BN, int WM, int WN, int NS, int WPE, int FA, int FB>
+template <int BM, int BN, int WM, int WN, int NS, int WPE, int FA, int FB, bool KROWS = false>
 hipError_t run_fp8(const uint8_t* a, const uint8_t* b, int64_t m, int64_t n, int64_t k,
                    const Fp8Plan& plan, const float* s_a, const float* s_b, void* out,
                    int out_dtype, int64_t ldc, float* partials, hipStream_t stream) {
@@ -572,7 +633,7 @@ hipError_t run_fp8(const uint8_t* a, const uint8_t* b, int64_t m, int64_t n, int
   static_assert(kLds <= 160 * 1024, "LDS budget");
   const int tiles_m = static_cast<int>(ceil_div(m, BM));
   const int tiles_n = static_cast<int>(ceil_div(n, BN));
-  auto kern = k_fp8_gemm<BM, BN, WM, WN, NS, WPE, FA, FB>;
+  auto kern = k_fp8_gemm<BM, BN, WM, WN, NS, WPE, FA, FB, KROWS>;
   static std::atomic<unsigned> lds_set{0};
   hipError_t le = ensure_lds_limit(reinterpret_cast<const void*>(kern), kLds, lds_set);
   if (le != hipSuccess) return le;
@@ -609,6 +670,37 @@ hipError_t dispatch_fp8(const uint8_t* a, const uint8_t* b, int64_t m, int64_t n
   }
 }
 
+// Plans of the K-row form (128 x 128 tiles only): the three-stage split-K
+// tile for long reductions, as for the weight gradients of the row-major
+// form, else the two-stage tile; a forced 128 x 128 configuration is kept.
+Fp8Plan plan_fp8_krows(int64_t m, int64_t n, int64_t k) {
+  const int64_t kslices = k / kBK;
+  const int forced = tune(kTuneFp8Tile);
+  if (forced == 1 || forced == 6 || forced == 9) return plan_for(forced, m, n, kslices, nullptr);
+  if (kslices >= 16) return split_tile_plan(m, n, kslices);
+  return plan_for(1, m, n, kslices, nullptr);
+}
+
+template <int FA, int FB>
+hipError_t dispatch_fp8_krows(const uint8_t* a, const uint8_t* b, int64_t m, int64_t n, int64_t k,
+                              const float* s_a, const float* s_b, void* out, int out_dtype,
+                              int64_t ldc, float* partials, hipStream_t stream) {
+  const Fp8Plan p = plan_fp8_krows(m, n, k);
+  switch (p.cfg) {
+    case 1:
+      return run_fp8<128, 128, 2, 2, 2, 2, FA, FB, true>(a, b, m, n, k, p, s_a, s_b, out,
+                                                        out_dtype, ldc, partials, stream);
+    case 6:
+      return run_fp8<128, 128, 2, 2, 4, 1, FA, FB, true>(a, b, m, n, k, p, s_a, s_b, out,
+                                                        out_dtype, ldc, partials, stream);
+    case 9:
+      return run_fp8<128, 128, 2, 2, 3, 2, FA, FB, true>(a, b, m, n, k, p, s_a, s_b, out,
+                                                        out_dtype, ldc, partials, stream);
+    default:
+      return hipErrorInvalidValue;
+  }
+}
+
 // One product of a paired launch.
 struct Fp8Part {
   const uint8_t* a;
@@ -636,27 +728,28 @@ struct Fp8Cfg {
                        NS = kCfgNS[ID], WPE = kCfgWPE[ID];
 };
 
-template <int ID, int FA, int FB>
+template <int ID, int FA, int FB, bool KROWS>
 __device__ __forceinline__ void fp8_part_block(int bid, int nblk, const Fp8Part& p, int out_dtype) {
   using C = Fp8Cfg<ID>;
-  fp8_gemm_block<C::BM, C::BN, C::WM, C::WN, C::NS, FA, FB>(
+  fp8_gemm_block<C::BM, C::BN, C::WM, C::WN, C::NS, FA, FB, KROWS>(
       bid, nblk, p.a, p.b, p.m, p.n, p.k, p.k_per_split, p.s_a, p.s_b, p.out, out_dtype, p.ldc,
       p.partials, p.tiles_m, p.tiles_n, p.band);
 }
 
 // The weight and input gradients of one fp8 linear in one launch (both
 // e5m2 x e4m3, four-wave tiles): blocks [0, w.blocks) run the weight
-// gradient's tiles, the long reductions over the tokens, which leave most
-// CUs idle on their own (36 tiles x 3 splits for a 768 x 768 weight); the
-// input gradient's tiles, dispatched after them, fill those CUs.
+// gradient's tiles (K-row form, from the tokens-major codes of the gradient
+// and the input), the long reductions over the tokens, which leave most CUs
+// idle on their own (36 tiles x 3 splits for a 768 x 768 weight); the input
+// gradient's tiles, dispatched after them, fill those CUs.
 template <int CW, int CX, int WPE>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
     k_fp8_gemm_pair(Fp8Part w, Fp8Part x, int out_dtype) {
   const int b = static_cast<int>(blockIdx.x);
   if (b < w.blocks)
-    fp8_part_block<CW, 1, 0>(b, w.blocks, w, out_dtype);
+    fp8_part_block<CW, 1, 0, true>(b, w.blocks, w, out_dtype);
   else
-    fp8_part_block<CX, 1, 0>(b - w.blocks, x.blocks, x, out_dtype);
+    fp8_part_block<CX, 1, 0, false>(b - w.blocks, x.blocks, x, out_dtype);
 }
 
 template <int CW, int CX>
@@ -746,17 +839,18 @@ hipError_t launch_fp8_gemm(const uint8_t* a, int fmt_a, const float* s_a, const 
 // gradient runs 108 latency-bound blocks); the FFN backwards look even
 // under the profiler, which serializes the graph's nodes.
 hipError_t launch_fp8_backward_pair(const uint8_t* g, const uint8_t* right_codes,
-                                    const uint8_t* g_t, const uint8_t* left_t_codes,
-                                    const float* s_g, const float* s_right, const float* s_left,
-                                    int64_t m, int64_t k, int64_t n, void* d_left, void* d_right_t,
+                                    const uint8_t* left_codes, const float* s_g,
+                                    const float* s_right, const float* s_left, int64_t m,
+                                    int64_t k, int64_t n, void* d_left, void* d_right_t,
                                     int out_dtype, float* split_ws, int64_t split_ws_floats,
                                     hipStream_t stream, bool* launched) {
   *launched = false;
   if (tune(kTuneFp8Pair) == 0) return hipSuccess;
-  if (n % kBK != 0 || m % kBK != 0) return hipSuccess;
-  // d_left [m, k] = g [m, n] . right^T; d_right^T [n, k] = g^T [n, m] . left
+  if (n % kBK != 0 || m % kBK != 0 || k % 16 != 0) return hipSuccess;
+  // d_left [m, k] = g [m, n] . right^T; d_right^T [n, k] = g^T . left, from
+  // g [m, n] and left [m, k] as K-row operands
   Fp8Plan px = plan_fp8(m, k, n);
-  const Fp8Plan pw = plan_fp8(n, k, m);
+  const Fp8Plan pw = plan_fp8_krows(n, k, m);
   if (px.cfg == 3 && px.splits == 1) px = Fp8Plan{4, 1, n};
   if (px.splits != 1 || pw.cfg != 9) return hipSuccess;
   if (pw.splits > 1 &&
@@ -765,8 +859,7 @@ hipError_t launch_fp8_backward_pair(const uint8_t* g, const uint8_t* right_codes
     return hipSuccess;
   const Fp8Part x = make_part(g, right_codes, m, k, n, px, s_g, s_right, d_left, k, nullptr);
   // d_right^T = ((g^T . left) * s_left) * s_g, the separate launch's order
-  const Fp8Part w =
-      make_part(g_t, left_t_codes, n, k, m, pw, s_left, s_g, d_right_t, k, split_ws);
+  const Fp8Part w = make_part(g, left_codes, n, k, m, pw, s_left, s_g, d_right_t, k, split_ws);
   hipError_t e;
   if (px.cfg == 4)
     e = run_fp8_pair<9, 4>(w, x, static_cast<int>(pw.splits), out_dtype, stream);
@@ -776,6 +869,30 @@ hipError_t launch_fp8_backward_pair(const uint8_t* g, const uint8_t* right_codes
     return hipSuccess;
   *launched = e == hipSuccess;
   return e;
+}
+
+int64_t fp8_gemm_krows_workspace_floats(int64_t m, int64_t n, int64_t k) {
+  const Fp8Plan p = plan_fp8_krows(m, n, k);
+  if (p.splits <= 1) return 0;
+  return p.splits * ceil_div(m, kCfgBM[p.cfg]) * ceil_div(n, kCfgBN[p.cfg]) * kCfgBM[p.cfg] *
+         kCfgBN[p.cfg];
+}
+
+hipError_t launch_fp8_gemm_krows(const uint8_t* a, int fmt_a, const float* s_a, const uint8_t* b,
+                                 int fmt_b, const float* s_b, int64_t m, int64_t n, int64_t k,
+                                 void* out, int out_dtype, int64_t ldc, float* split_ws,
+                                 int64_t split_ws_floats, hipStream_t stream) {
+  if (m == 0 || n == 0) return hipSuccess;
+  if (k % kBK != 0 || m % 16 != 0 || n % 16 != 0 ||
+      split_ws_floats < fp8_gemm_krows_workspace_floats(m, n, k))
+    return hipErrorInvalidValue;
+  if (fmt_a == kE4M3FN && fmt_b == kE4M3FN)
+    return dispatch_fp8_krows<0, 0>(a, b, m, n, k, s_a, s_b, out, out_dtype, ldc, split_ws, stream);
+  if (fmt_a == kE5M2 && fmt_b == kE4M3FN)
+    return dispatch_fp8_krows<1, 0>(a, b, m, n, k, s_a, s_b, out, out_dtype, ldc, split_ws, stream);
+  if (fmt_a == kE4M3FN && fmt_b == kE5M2)
+    return dispatch_fp8_krows<0, 1>(a, b, m, n, k, s_a, s_b, out, out_dtype, ldc, split_ws, stream);
+  return dispatch_fp8_krows<1, 1>(a, b, m, n, k, s_a, s_b, out, out_dtype, ldc, split_ws, stream);
 }
 
 }  // namespace rpx

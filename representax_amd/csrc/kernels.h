@@ -219,15 +219,23 @@ hipError_t launch_fp8_gemm(const uint8_t* a, int fmt_a, const float* s_a, const 
                            int64_t split_ws_floats, hipStream_t stream);
 int64_t fp8_gemm_workspace_floats(int64_t m, int64_t n, int64_t k);
 // The fp8 linear backward's d_left [m, k] = g . right^T and d_right^T [n, k]
-// = g^T . left (codes: g [m, n] and g^T [n, m] e5m2, right^T [k, n] and
-// left^T [k, m] e4m3) in one launch, where both plans allow it; *launched
-// says whether it did (otherwise nothing was launched).
+// = g^T . left (codes: g [m, n] e5m2, right^T [k, n] and left [m, k] e4m3)
+// in one launch, where both plans allow it; *launched says whether it did
+// (otherwise nothing was launched).
 hipError_t launch_fp8_backward_pair(const uint8_t* g, const uint8_t* right_codes,
-                                    const uint8_t* g_t, const uint8_t* left_t_codes,
-                                    const float* s_g, const float* s_right, const float* s_left,
-                                    int64_t m, int64_t k, int64_t n, void* d_left, void* d_right_t,
+                                    const uint8_t* left_codes, const float* s_g,
+                                    const float* s_right, const float* s_left, int64_t m,
+                                    int64_t k, int64_t n, void* d_left, void* d_right_t,
                                     int out_dtype, float* split_ws, int64_t split_ws_floats,
                                     hipStream_t stream, bool* launched);
+// out [m, n] = ((a^T . b) * s_a) * s_b from K-row codes a [k, m] and b [k, n]
+// (row strides m and n): k % 128 == 0, m % 16 == 0, n % 16 == 0, 16-byte
+// aligned operands; split_ws as fp8_gemm_krows_workspace_floats(m, n, k).
+int64_t fp8_gemm_krows_workspace_floats(int64_t m, int64_t n, int64_t k);
+hipError_t launch_fp8_gemm_krows(const uint8_t* a, int fmt_a, const float* s_a, const uint8_t* b,
+                                 int fmt_b, const float* s_b, int64_t m, int64_t n, int64_t k,
+                                 void* out, int out_dtype, int64_t ldc, float* split_ws,
+                                 int64_t split_ws_floats, hipStream_t stream);
 int fp8_tile_count();  // tile ids are 1 .. fp8_tile_count() - 1 (0: planner)
 // Delayed scaling: saturating casts with given scales that also record each
 // tensor's amax (atomic max of ordered f32 bits) into its slot's pending

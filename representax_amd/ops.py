@@ -1082,8 +1082,8 @@ def fp8_linear_forward(left, right, out_dtype=BF16, save_codes=False):
     """``(out [M, N], scales f32[2], codes)`` for ``left [M,K] . right [K,N]``.
 
     With ``save_codes`` the same cast pass also returns the backward's operand
-    codes ``(left^T codes [K, M], right codes [K, N])``; otherwise ``codes``
-    is None. ``ValueError`` for an empty operand, as in the reference.
+    codes ``(left codes [M, K], right codes [K, N])``; otherwise ``codes`` is
+    None. ``ValueError`` for an empty operand, as in the reference.
     """
 
     _check_fp8_operands(left, right)
@@ -1096,7 +1096,7 @@ def fp8_linear_forward(left, right, out_dtype=BF16, save_codes=False):
     scales = torch.empty(2, dtype=F32, device=device)
     codes = None
     if save_codes:
-        codes = (torch.empty((k, m), dtype=torch.uint8, device=device),
+        codes = (torch.empty((m, k), dtype=torch.uint8, device=device),
                  torch.empty((k, n), dtype=torch.uint8, device=device))
     ws = _workspace(nat.query("rpx_fp8_linear_forward_workspace", m, n, k), device)
     nat.call("rpx_fp8_linear_forward", _ptr(left), _dtype_code(left.dtype), m, k, _ptr(right),
@@ -1154,14 +1154,14 @@ def fp8_linear_backward_codes(codes, scales, grad, *, k, dtype, right_transposed
                               need_left=True, need_right=True):
     """Backward from the codes saved by ``fp8_linear_forward(save_codes=True)``."""
 
-    left_t, right_c = codes
+    left_c, right_c = codes
     if grad.dim() != 2:
         raise ValueError(f"grad must be 2-D [M, N], got shape {tuple(grad.shape)}")
-    _check_extent("saved left codes", left_t, (k, grad.shape[0]))
+    _check_extent("saved left codes", left_c, (grad.shape[0], k))
     _check_extent("saved right codes", right_c, (k, grad.shape[1]))
     if scales.numel() != 2:
         raise _shape_error("scales", scales.shape, (2,))
-    device = _on_device(left_t, right_c, grad, scales)
+    device = _on_device(left_c, right_c, grad, scales)
     grad = grad.contiguous()
     m, n = grad.shape
     d_left, d_right = _grad_buffers(m, k, n, dtype, right_transposed, need_left, need_right,
@@ -1172,7 +1172,7 @@ def fp8_linear_backward_codes(codes, scales, grad, *, k, dtype, right_transposed
                 t.zero_()
     elif need_left or need_right:
         ws = _workspace(nat.query("rpx_fp8_linear_backward_workspace", m, n, k), device)
-        nat.call("rpx_fp8_linear_backward_codes", _ptr(left_t), _ptr(right_c), _ptr(scales), m, k,
+        nat.call("rpx_fp8_linear_backward_codes", _ptr(left_c), _ptr(right_c), _ptr(scales), m, k,
                  n, _ptr(grad), _dtype_code(grad.dtype), _ptr(d_left), _ptr(d_right),
                  1 if right_transposed else 0, _dtype_code(dtype), _ptr(ws), ws.numel(),
                  _stream(device))
@@ -1181,18 +1181,19 @@ def fp8_linear_backward_codes(codes, scales, grad, *, k, dtype, right_transposed
     return d_left, d_right
 
 
-def fp8_linear_backward_gemms(g_codes, g_t_codes, s_grad, left_t_codes, s_left, right_codes,
-                              s_right, *, k, dtype, right_transposed, need_left=True,
-                              need_right=True):
-    """The backward's two products from the gradient's codes (e5m2 ``g_codes``
-    [M, N] and ``g_t_codes`` [N, M]) and the forward's operand codes
-    (``left_t_codes`` [K, M], ``right_codes`` [K, N]), each scale a one-element
-    float32 tensor: ``(d_left [M, K] or None, d_right or None)`` as in
+def fp8_linear_backward_gemms(g_codes, s_grad, left_codes, s_left, right_codes, s_right, *, k,
+                              dtype, right_transposed, need_left=True, need_right=True):
+    """The backward's two products from the gradient's codes (e5m2
+    ``g_codes`` [M, N]) and the forward's operand codes (``left_codes``
+    [M, K], ``right_codes`` [K, N]), each scale a one-element float32 tensor:
+    ``(d_left [M, K] or None, d_right or None)`` as in
     ``fp8_linear_backward_codes``. For callers that quantize the gradient
     themselves (delayed scaling)."""
 
-    m, n = g_codes.shape if g_codes is not None else tuple(g_t_codes.shape)[::-1]
-    device = _on_device(g_codes, g_t_codes, left_t_codes, right_codes, s_grad)
+    m, n = g_codes.shape
+    _check_extent("left codes", left_codes, (m, k))
+    _check_extent("right codes", right_codes, (k, n))
+    device = _on_device(g_codes, left_codes, right_codes, s_grad)
     d_left, d_right = _grad_buffers(m, k, n, dtype, True, need_left, need_right, device)
     if m == 0 or n == 0 or k == 0:
         for t in (d_left, d_right):
@@ -1200,8 +1201,7 @@ def fp8_linear_backward_gemms(g_codes, g_t_codes, s_grad, left_t_codes, s_left, 
                 t.zero_()
     elif need_left or need_right:
         ws = _workspace(nat.query("rpx_fp8_linear_backward_gemms_workspace", m, n, k), device)
-        nat.call("rpx_fp8_linear_backward_gemms", _ptr(g_codes if need_left else None),
-                 _ptr(g_t_codes if need_right else None), _ptr(s_grad), _ptr(left_t_codes),
+        nat.call("rpx_fp8_linear_backward_gemms", _ptr(g_codes), _ptr(s_grad), _ptr(left_codes),
                  _ptr(s_left), _ptr(right_codes), _ptr(s_right), m, k, n, _ptr(d_left),
                  _ptr(d_right), 1, _dtype_code(dtype), _ptr(ws), ws.numel(), _stream(device))
     if d_right is not None:
@@ -1238,13 +1238,16 @@ def fp8_cast_delayed(t: torch.Tensor, state, slot: int, fmt: str = "e4m3fn", *, 
 def fp8_cast_delayed2(t0: torch.Tensor, slot0: int, t1: torch.Tensor, slot1: int, state,
                       fmt: str = "e4m3fn", *, rowmajor=True, transposed=False):
     """Two ``fp8_cast_delayed`` casts of one dtype in one launch:
-    ``((out0, out0_t), (out1, out1_t))``."""
+    ``((out0, out0_t), (out1, out1_t))``. ``rowmajor`` and ``transposed``
+    are a bool for both tensors or a pair, one per tensor."""
 
     device = _on_device(t0, t1, state.scales)
     if t0.dtype != t1.dtype:
         raise TypeError("fp8_cast_delayed2 casts two tensors of one dtype")
-    o0, o0t = _delayed_outputs(t0, rowmajor, transposed)
-    o1, o1t = _delayed_outputs(t1, rowmajor, transposed)
+    rm = rowmajor if isinstance(rowmajor, tuple) else (rowmajor, rowmajor)
+    tr = transposed if isinstance(transposed, tuple) else (transposed, transposed)
+    o0, o0t = _delayed_outputs(t0, rm[0], tr[0])
+    o1, o1t = _delayed_outputs(t1, rm[1], tr[1])
     nat.call("rpx_fp8_cast_delayed2", _ptr(t0), t0.shape[0], t0.shape[1], t0.stride(0),
              t0.stride(1), int(slot0), _ptr(o0), _ptr(o0t), _ptr(t1), t1.shape[0], t1.shape[1],
              t1.stride(0), t1.stride(1), int(slot1), _ptr(o1), _ptr(o1t), _dtype_code(t0.dtype),
@@ -1300,13 +1303,14 @@ class Fp8DelayedLinearFn(torch.autograd.Function):
         s_l, s_r, s_g = (state.scales[i:i + 1] for i in slots)
         out = torch.empty((m, n), dtype=out_dtype, device=left.device)
         need = left.requires_grad or right.requires_grad
-        # left -> codes [M, K] (+ [K, M] for d_right); right [K, N] -> codes
-        # [N, K] for this product (+ [K, N] for d_left); one launch
-        (ql, qlt), (qrt, qr) = fp8_cast_delayed2(left, slots[0], right.t(), slots[1], state,
-                                                 "e4m3fn", rowmajor=True, transposed=need)
+        # left -> codes [M, K] (this product's, and d_right's read along the
+        # tokens); right [K, N] -> codes [N, K] for this product (+ [K, N] for
+        # d_left); one launch
+        (ql, _), (qrt, qr) = fp8_cast_delayed2(left, slots[0], right.t(), slots[1], state,
+                                               "e4m3fn", rowmajor=True, transposed=(False, need))
         _gemm_into(ql, "e4m3fn", s_l, qrt, "e4m3fn", s_r, out)
         if need:
-            ctx.save_for_backward(qlt, qr, s_l, s_r, s_g)
+            ctx.save_for_backward(ql, qr, s_l, s_r, s_g)
             ctx.state = state
             ctx.g_slot = slots[2]
             ctx.dtype = left.dtype
@@ -1315,15 +1319,15 @@ class Fp8DelayedLinearFn(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad):
-        qlt, qr, s_l, s_r, s_g = ctx.saved_tensors
+        ql, qr, s_l, s_r, s_g = ctx.saved_tensors
         grad = grad.contiguous()
-        k = qlt.shape[0]
+        k = ql.shape[1]
         need_l, need_r = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
-        qg, qgt = fp8_cast_delayed(grad, ctx.state, ctx.g_slot, "e5m2", rowmajor=need_l,
-                                   transposed=need_r)
+        qg, _ = fp8_cast_delayed(grad, ctx.state, ctx.g_slot, "e5m2", rowmajor=True,
+                                 transposed=False)
         if not (need_l or need_r):
             return None, None, None, None, None
-        d_left, d_right = fp8_linear_backward_gemms(qg, qgt, s_g, qlt, s_l, qr, s_r, k=k,
+        d_left, d_right = fp8_linear_backward_gemms(qg, s_g, ql, s_l, qr, s_r, k=k,
                                                     dtype=ctx.dtype,
                                                     right_transposed=ctx.right_t,
                                                     need_left=need_l, need_right=need_r)
@@ -1353,9 +1357,9 @@ class Fp8LinearFn(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad):
-        scales, left_t, right_c = ctx.saved_tensors
+        scales, left_c, right_c = ctx.saved_tensors
         d_left, d_right = fp8_linear_backward_codes(
-            (left_t, right_c), scales, grad, k=ctx.k, dtype=ctx.dtype,
+            (left_c, right_c), scales, grad, k=ctx.k, dtype=ctx.dtype,
             right_transposed=ctx.right_t, need_left=ctx.needs_input_grad[0],
             need_right=ctx.needs_input_grad[1])
         return d_left, d_right, None

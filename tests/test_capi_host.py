@@ -42,7 +42,8 @@ def test_workspace_queries():
     assert lib.rpx_int4lora_backward_workspace(4096, 3072, 768, 0, 16, nat.DTYPE_BF16) > 768 * 3072 * 2
     assert lib.rpx_int4lora_forward_workspace(4, 6, 8, 0, 2, nat.DTYPE_BF16) > 0  # generic path
     assert lib.rpx_fp8_linear_forward_workspace(8192, 3072, 768) >= 8192 * 768 + 3072 * 768
-    assert lib.rpx_fp8_linear_backward_workspace(8192, 3072, 768) >= 2 * 8192 * 3072
+    # gradient codes [M, N] plus both operands' codes
+    assert lib.rpx_fp8_linear_backward_workspace(8192, 3072, 768) >= 8192 * 3072 + 768 * 3072 + 8192 * 768
 
 
 def test_invalid_arguments_are_rejected_before_any_launch():
@@ -87,15 +88,15 @@ def test_invalid_arguments_are_rejected_before_any_launch():
         nat.call("rpx_int4lora_backward_act", p, p, nat.DTYPE_BF16, 2, 8, p, p, 6, 0, p, p, 2,
                  ctypes.c_float(1.0), p, nat.ACT_ADD, p, None, p, None, p, p, None, 0, None)
     with pytest.raises(ValueError, match="null pointer"):
-        nat.call("rpx_fp8_linear_backward_gemms", p, p, None, p, p, p, p, 256, 256, 256, p, p, 1,
+        nat.call("rpx_fp8_linear_backward_gemms", p, None, p, p, p, p, 256, 256, 256, p, p, 1,
                  nat.DTYPE_BF16, p, 1 << 30, None)
     with pytest.raises(ValueError, match="null pointer"):
-        nat.call("rpx_fp8_linear_backward_gemms", None, p, p, p, p, p, p, 256, 256, 256, p, None,
-                 1, nat.DTYPE_BF16, p, 1 << 30, None)
+        nat.call("rpx_fp8_linear_backward_gemms", p, p, None, p, p, p, 256, 256, 256, p, p, 1,
+                 nat.DTYPE_BF16, p, 1 << 30, None)
     with pytest.raises(ValueError, match="workspace too small"):
         need = nat.load().rpx_fp8_linear_backward_gemms_workspace(8192, 768, 768)
         assert need > 0  # the 768 x 768 weight gradient over 8192 tokens is split-K
-        nat.call("rpx_fp8_linear_backward_gemms", p, p, p, p, p, p, p, 8192, 768, 768, p, p, 1,
+        nat.call("rpx_fp8_linear_backward_gemms", p, p, p, p, p, p, 8192, 768, 768, p, p, 1,
                  nat.DTYPE_BF16, p, need - 1, None)
 
 

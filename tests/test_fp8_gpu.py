@@ -212,10 +212,10 @@ def test_fp8_linear_bert_ffn_full_size():
                                    (2100 * 128 + 5, 8, 16)])
 def test_fused_quantize_scales_and_codes_bit_exact(m, k, n):
     """The linear's own quantize (amax tile partials, then every cast block
-    reducing them to the scale): scales and the saved transposed codes of
-    both operands equal the oracle's, on ragged tiles and on an operand of
-    more than 2048 tiles (partials beyond the ones each thread loads up
-    front)."""
+    reducing them to the scale): scales and the saved codes (left row-major
+    [M, K], right [K, N]) equal the oracle's, on ragged tiles and on an
+    operand of more than 2048 tiles (partials beyond the ones each thread
+    loads up front)."""
 
     x, w, _ = _fp8_case(m, k, n, seed=m + 3 * k + n)
     _, scales, codes = ops.fp8_linear_forward(to_dev_bf16(x), to_dev_bf16(w).t(), save_codes=True)
@@ -224,7 +224,7 @@ def test_fused_quantize_scales_and_codes_bit_exact(m, k, n):
     s_x = ofp8.scale_from_amax(ofp8.amax(x), E4M3FN)
     s_w = ofp8.scale_from_amax(ofp8.amax(w), E4M3FN)
     assert s[0] == s_x and s[1] == s_w
-    assert np.array_equal(codes[0].cpu().numpy(), ofp8.cast_with_scale(x, s_x, E4M3FN).T)
+    assert np.array_equal(codes[0].cpu().numpy(), ofp8.cast_with_scale(x, s_x, E4M3FN))
     assert np.array_equal(codes[1].cpu().numpy(), ofp8.cast_with_scale(w, s_w, E4M3FN).T)
 
 
@@ -275,13 +275,13 @@ def test_backward_gemms_from_gradient_codes(m, k, n):
     _, scales, codes = ops.fp8_linear_forward(to_dev_bf16(x), to_dev_bf16(w).t(), save_codes=True)
     gd = to_dev_bf16(gy)
     s_g = ops.fp8_scale(gd, E5M2)
-    qg, qgt = ops.fp8_cast(gd, s_g, E5M2, rowmajor=True, transposed=True)
+    qg, _ = ops.fp8_cast(gd, s_g, E5M2, rowmajor=True)
     for right_t in (True, False):
         for need_l, need_r in ((True, True), (True, False), (False, True)):
             want = ops.fp8_linear_backward_codes(codes, scales, gd, k=k, dtype=torch.bfloat16,
                                                  right_transposed=right_t, need_left=need_l,
                                                  need_right=need_r)
-            got = ops.fp8_linear_backward_gemms(qg, qgt, s_g, codes[0], scales[0:1], codes[1],
+            got = ops.fp8_linear_backward_gemms(qg, s_g, codes[0], scales[0:1], codes[1],
                                                 scales[1:2], k=k, dtype=torch.bfloat16,
                                                 right_transposed=right_t, need_left=need_l,
                                                 need_right=need_r)

@@ -166,6 +166,107 @@ def test_fp8_step_calls_full_size_match_oracle(call):
     assert torch.equal(b16.view(torch.int16), f32.to(torch.bfloat16).view(torch.int16))
 
 
+def _weight_grad_krows(qx, s_x, qg, s_g, right_t):
+    """d_right of the fp8 linear backward through the K-row kernel (the
+    tokens-major codes of the input and the gradient as they are): [N, K]
+    when right_t, else [K, N]."""
+
+    m, k = qx.shape
+    n = qg.shape[1]
+    dummy = torch.zeros((k, n), dtype=torch.uint8, device="cuda")
+    _, d_right = ops.fp8_linear_backward_gemms(
+        qg, torch.tensor([s_g], device="cuda"), qx, torch.tensor([s_x], device="cuda"), dummy,
+        torch.tensor([1.0], device="cuda"), k=k, dtype=torch.bfloat16, right_transposed=right_t,
+        need_left=False)
+    return d_right.t() if right_t else d_right
+
+
+def _weight_grad_rowmajor(qx, s_x, qg, s_g, right_t):
+    """The same product through the row-major kernel on transposed copies."""
+
+    xt, gt = qx.t().contiguous(), qg.t().contiguous()
+    sx, sg = torch.tensor([s_x], device="cuda"), torch.tensor([s_g], device="cuda")
+    if right_t:
+        return ops.fp8_gemm(gt, E5M2, sx, xt, E4M3FN, sg, out_dtype=torch.bfloat16)
+    return ops.fp8_gemm(xt, E4M3FN, sx, gt, E5M2, sg, out_dtype=torch.bfloat16)
+
+
+# (tokens, K, N, split counts): N and K multiples of 16 but not of 128, the
+# tokens ten and five 128-deep slices
+KROWS_RAGGED = [(1280, 208, 400, (1, 3, 4)), (640, 96, 144, (1, 2, 5))]
+
+
+@pytest.mark.parametrize("right_t", [True, False])
+@pytest.mark.parametrize("cfg", [0, 1, 6, 9])
+def test_weight_gradient_krows_plans(cfg, right_t):
+    """The weight gradient read along the tokens from row-major codes (the
+    128 x 128 configurations, forced split counts, edge tiles): the oracle's
+    product, and bit for bit the row-major kernel's on transposed copies
+    under the same plan (cfg 0: the planner's, checked against the oracle
+    only)."""
+
+    for m, k, n, splits in KROWS_RAGGED:
+        g = rng(cfg * 100 + m + k + n)
+        qx = _finite_codes(g, (m, k), E4M3FN)
+        qg = _finite_codes(g, (m, n), E5M2)
+        s_x, s_g = np.float32(0.0123), np.float32(3.7)
+        if right_t:
+            want = ofp8.scaled_dot_codes(np.ascontiguousarray(qg.T), s_x, E5M2, qx, s_g, E4M3FN)
+        else:
+            want = ofp8.scaled_dot_codes(np.ascontiguousarray(qx.T), s_x, E4M3FN, qg, s_g, E5M2)
+        qxd, qgd = to_dev(qx), to_dev(qg)
+        for sp in splits:
+            with ops.tuning(fp8_tile=cfg, fp8_splits=sp):
+                got = _weight_grad_krows(qxd, s_x, qgd, s_g, right_t)
+                ref = _weight_grad_rowmajor(qxd, s_x, qgd, s_g, right_t) if cfg else None
+            torch.cuda.synchronize()
+            assert_bf16_close(from_dev(got), bf16_round(want), tol=FP8_TOL, min_equal=None,
+                              what=f"cfg {cfg} splits {sp} {m}x{k}x{n}")
+            if ref is not None:
+                assert torch.equal(got, ref), (cfg, sp, m, k, n, right_t)
+
+
+@pytest.mark.parametrize("m,k,n", [(200, 40, 30), (256, 24, 136), (384, 128, 100)])
+def test_weight_gradient_krows_generic_shapes(m, k, n):
+    """Shapes the pipelined K-row kernel does not take (tokens not a multiple
+    of 128, or K, N not multiples of 16) go to the generic kernel."""
+
+    g = rng(m * 3 + k + n)
+    qx = _finite_codes(g, (m, k), E4M3FN)
+    qg = _finite_codes(g, (m, n), E5M2)
+    s_x, s_g = np.float32(0.05), np.float32(2.0)
+    for right_t in (True, False):
+        got = _weight_grad_krows(to_dev(qx), s_x, to_dev(qg), s_g, right_t)
+        torch.cuda.synchronize()
+        if right_t:
+            want = ofp8.scaled_dot_codes(np.ascontiguousarray(qg.T), s_x, E5M2, qx, s_g, E4M3FN)
+        else:
+            want = ofp8.scaled_dot_codes(np.ascontiguousarray(qx.T), s_x, E4M3FN, qg, s_g, E5M2)
+        assert_bf16_close(from_dev(got), bf16_round(want), tol=FP8_TOL, min_equal=None,
+                          what=f"{m}x{k}x{n} right_t={right_t}")
+
+
+@pytest.mark.parametrize("k,n", [(768, 768), (768, 3072), (3072, 768)])
+def test_weight_gradient_krows_step_shapes(k, n):
+    """The step's three weight gradients at 8192 tokens, from the tokens-major
+    codes: the oracle's product, and bit for bit the row-major kernel's (the
+    planners agree on these shapes: three-stage 128 x 128 tiles, three splits
+    for 768 x 768, unsplit otherwise)."""
+
+    m = 8192
+    g = rng(900 + k + n)
+    qx, s_x = _quantized(g, (m, k), E4M3FN, outliers=True)
+    qg, s_g = _quantized(g, (m, n), E5M2)
+    want = ofp8.scaled_dot_codes(np.ascontiguousarray(qg.T), s_x, E5M2, qx, s_g, E4M3FN)
+    qxd, qgd = to_dev(qx), to_dev(qg)
+    got = _weight_grad_krows(qxd, s_x, qgd, s_g, True)
+    ref = _weight_grad_rowmajor(qxd, s_x, qgd, s_g, True)
+    torch.cuda.synchronize()
+    assert_bf16_close(from_dev(got), bf16_round(want), tol=FP8_TOL, min_equal=None,
+                      what=f"dW {n}x{k}")
+    assert torch.equal(got, ref)
+
+
 def _fp8_adapter_oracle(x, packed, scales, a, b, bias_bits, alpha, rank, k, gy):
     """The fp8-policy forward and backward of QuantizedLoRALinear from the
     oracle's pieces, at the reference's bf16 rounding points
