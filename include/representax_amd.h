@@ -68,8 +68,9 @@ int rpx_abi_version(void);
  *                        (env RPX_SKINNY_TILE)
  *   RPX_TUNE_SKINNY2     two-launch skinny form: -1 planner (M <= 4), 0 never,
  *                        1 for every M <= 16 (env RPX_SKINNY2)
- *   RPX_TUNE_SKINNY2_ONE M <= 4 form: -1 planner (one launch for K >= 4096),
- *                        0 two launches, 1 one launch (env RPX_SKINNY2_ONE)
+ *   RPX_TUNE_SKINNY2_ONE M <= 4 form: -1 planner (one launch where the rank is a
+ *                        multiple of 8 and B 16-byte aligned), 0 two
+ *                        launches, 1 one launch (env RPX_SKINNY2_ONE)
  *   RPX_TUNE_SPIN_LIMIT  polls of the skinny kernels' bounded cross-block
  *                        waits (0: the default limit)
  *   RPX_TUNE_GEMM_BAND   row-blocks per band of the bf16, INT4 and fp8 GEMMs'
@@ -119,7 +120,7 @@ int rpx_get_tuning(int knob);
  * check), synchronizes `stream`, and returns RPX_ERR_DEVICE (with a
  * message naming the kernel) if any bit was set; flags_out (host, may be
  * NULL) receives the bits: 1 = skinny M <= 64 adapter arrivals, 2 = skinny
- * M <= 4 published h. Synchronizes, so it must not be called during graph
+ * M <= 4 adapter partials. Synchronizes, so it must not be called during graph
  * capture. No reference counterpart (XLA's kernels have no cross-block waits). */
 int rpx_check_device_errors(void* stream, uint32_t* flags_out);
 

@@ -212,7 +212,7 @@ bool knob_value_ok(int knob, int v) {
              v == kTileT4_64x128;
     case kTuneFp8Tile: return v >= 0 && v < fp8_tile_count();
     case kTuneSkinnyTile: return v >= 0 && v <= skinny_tile_count();
-    case kTuneSkinny2:
+    case kTuneSkinny2: return v >= -1 && v <= 1;
     case kTuneSkinny2One: return v >= -1 && v <= 1;
     case kTuneSpinLimit: return v >= 0;
     case kTuneBand: return v >= 0 && v <= 64;
@@ -356,7 +356,7 @@ int rpx_check_device_errors(void* stream, uint32_t* flags_out) {
   if (flags_out != nullptr) *flags_out = bits;
   std::string msg = "a kernel's bounded wait expired (its outputs hold NaN):";
   if (bits & kDevErrSkinnyWait) msg += " skinny-M forward (one launch, M <= 64): adapter arrivals;";
-  if (bits & kDevErrSkinnyOneWait) msg += " skinny-M forward (one launch, M <= 4): published h;";
+  if (bits & kDevErrSkinnyOneWait) msg += " skinny-M forward (one launch, M <= 4): adapter partials;";
   set_error(msg);
   return kErrDevice;
 }

@@ -9,7 +9,7 @@ namespace rpx {
 // One word per device that kernels raise bits in (atomic or) when a bounded
 // wait expired; read and cleared by rpx_check_device_errors.
 constexpr unsigned int kDevErrSkinnyWait = 1u;     // k_skinny: adapter arrivals
-constexpr unsigned int kDevErrSkinnyOneWait = 2u;  // k_skinny_one: published h
+constexpr unsigned int kDevErrSkinnyOneWait = 2u;  // k_skinny_one: adapter partials
 // This device's word (nullptr if its address could not be resolved).
 unsigned int* device_error_word();
 

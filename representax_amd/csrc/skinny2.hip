@@ -67,12 +67,10 @@ struct Skinny2Params {
   int slices;            // adapter K slices of 128 * NW columns
   int a_blocks;          // slices * ceil(rank / 16)
   int b_vec;             // B rows may be touched with 16-byte loads
-  // one-launch form: the call's slot of arrival words ([0] adapter blocks,
-  // [1] h published, [2] done: weight blocks and the publishing adapter
-  // block; zero between calls), the published h as f32 [M, rank], the polls
-  // of the bounded wait and the device error word
+  // one-launch form: the call's slot, the host's call count (mixed into the
+  // tag), the polls of the bounded wait and the device error word
   int slot;
-  float* hf;
+  unsigned int tag;
   int w_blocks;
   int spin;
   unsigned int* err;
@@ -88,11 +86,18 @@ __device__ __forceinline__ f32x4_v mfma16(u32x4_t a, u32x4_t b, f32x4_v c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_frag(a), as_frag(b), c, 0, 0, 0);
 }
 
-// 8 bf16 of x row m from column k (zeros for rows past M or chunks past K)
-__device__ __forceinline__ u32x4_t x_frag(const Skinny2Params& p, int m, int64_t k, bool ok) {
-  const u32x4_t z{0u, 0u, 0u, 0u};
-  if (!ok || m >= p.m) return z;
-  return ld16(p.x + static_cast<int64_t>(m) * p.k + k);
+// 8 bf16 of x row m from column k. Every fragment load is unconditional
+// (rows past M read row M - 1; for chunks past K callers pass a column of
+// the first chunk) and keep() turns the fragments that lie outside x (or
+// outside the weight) into zeros where they are used: a load under a
+// branch made the compiler wait for it inside the branch, which put a full
+// memory round trip between a wave's first loads and the rest.
+__device__ __forceinline__ u32x4_t x_load(const Skinny2Params& p, int m, int64_t k) {
+  return ld16(p.x + static_cast<int64_t>(m < p.m ? m : p.m - 1) * p.k + k);
+}
+
+__device__ __forceinline__ u32x4_t keep(u32x4_t v, bool ok) {
+  return ok ? v : u32x4_t{0u, 0u, 0u, 0u};
 }
 
 // 8 nibbles (k ascending, low nibble first) -> 8 bf16: bf16(q * s), exact
@@ -127,6 +132,29 @@ __device__ __forceinline__ f32x4_v reduce_waves(f32x4_v acc, f32x4_v* red) {
   return acc;
 }
 
+// One-launch form state (k_skinny_one, described further down).
+constexpr int kSlots2 = 8;
+constexpr int kSpin2 = 1 << 22;  // default polls of the bounded wait
+constexpr int kOneMaxM = 4;      // rows of x the one-launch form takes
+// partial words of a slot: [slice][m][rank], slices <= 4, rank <= 64
+constexpr int kOneWords = 4 * kOneMaxM * 64;
+constexpr int kOnePerLane = kOneWords / 64;
+__device__ unsigned long long g_skinny2_words[kSlots2][kOneWords];
+
+// The launch's dispatch id (an LLVM intrinsic without a clang builtin).
+extern "C" __device__ unsigned long long rpx_amdgcn_dispatch_id() __asm("llvm.amdgcn.dispatch.id");
+
+__device__ __forceinline__ unsigned int call_tag(const Skinny2Params& p) {
+  const unsigned long long id = rpx_amdgcn_dispatch_id();
+  const unsigned long long pkt = reinterpret_cast<uintptr_t>(__builtin_amdgcn_dispatch_ptr());
+  unsigned long long h = (id * 0x9E3779B97F4A7C15ull) ^ (pkt * 0xC2B2AE3D27D4EB4Full) ^ p.tag;
+  h ^= h >> 31;
+  h *= 0xBF58476D1CE4E5B9ull;
+  h ^= h >> 32;
+  const unsigned int t = static_cast<unsigned int>(h);
+  return t != 0u ? t : 1u;
+}
+
 // Adapter block a = (K slice s, 16-rank group q): the fp32 partial of
 // x A^T over the slice's 128 NW columns, one 128-column chunk per wave,
 // summed over the waves in wave order; valid in wave 0, where lane l holds
@@ -146,16 +174,18 @@ __device__ __forceinline__ f32x4_v adapter_partial(const Skinny2Params& p, int a
   const uint16_t* arow = p.lora_a + static_cast<int64_t>(jok ? j : p.rank - 1) * p.k;
   const int64_t c = static_cast<int64_t>(s) * NW + wave;
   const bool ok = c < p.k / 128;
-  const int64_t k0 = ok ? c * 128 + 32 * g : 0;
+  const int64_t k0 = (ok ? c * 128 : 0) + 32 * g;
   u32x4_t av[4], xv[4];
 #pragma unroll
   for (int st = 0; st < 4; ++st) {
-    av[st] = ok && jok ? ld16(arow + k0 + 8 * st) : u32x4_t{0u, 0u, 0u, 0u};
-    xv[st] = x_frag(p, rl, k0 + 8 * st, ok);
+    av[st] = ld16(arow + k0 + 8 * st);
+    xv[st] = x_load(p, rl, k0 + 8 * st);
   }
+  const bool aok = ok && jok;
+  const bool xok = ok && rl < p.m;
   f32x4_v acc{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int st = 0; st < 4; ++st) acc = mfma16(av[st], xv[st], acc);
+  for (int st = 0; st < 4; ++st) acc = mfma16(keep(av[st], aok), keep(xv[st], xok), acc);
   *s_out = s;
   *q_out = q;
   return reduce_waves<NW>(acc, red);
@@ -201,26 +231,39 @@ __device__ __forceinline__ void weight_loads(const Skinny2Params& p, int64_t n0,
   for (int i = 0; i < CPW; ++i) {
     const int64_t c = wave + static_cast<int64_t>(i) * NW;
     const bool ok = c < nchunks;
-    const int64_t k0 = ok ? c * 128 + 32 * g : 0;
-    f.wv[i] = ok ? ld16(wrow + k0 / 2) : u32x4_t{0u, 0u, 0u, 0u};
+    const int64_t k0 = (ok ? c * 128 : 0) + 32 * g;
+    f.wv[i] = ld16(wrow + k0 / 2);
     f.sv[i] = srow[p.n_groups == 1 ? 0 : (k0 >> p.group_shift)];
 #pragma unroll
-    for (int st = 0; st < 4; ++st) f.xv[i][st] = x_frag(p, rl, k0 + 8 * st, ok);
+    for (int st = 0; st < 4; ++st) f.xv[i][st] = x_load(p, rl, k0 + 8 * st);
   }
 }
 
-// Dequantized MFMAs over the loaded chunks, summed over the waves in wave
-// order: valid in wave 0, lane l holding D[n0 + 4 (l >> 4) + v][m = l & 15].
+// Dequantized MFMAs over the wave's loaded chunks (chunks past K and rows
+// past M as zeros).
 template <int NW, int CPW>
-__device__ __forceinline__ f32x4_v weight_mfma(const WeightFrags<CPW>& f, f32x4_v* red) {
+__device__ __forceinline__ f32x4_v weight_partial(const Skinny2Params& p, const WeightFrags<CPW>& f) {
+  const int wave = threadIdx.x >> 6;
+  const bool mok = (threadIdx.x & 15) < p.m;
   f32x4_v acc{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int i = 0; i < CPW; ++i) {
+    const bool ok = wave + static_cast<int64_t>(i) * NW < p.k / 128;
     const float s = bf16_to_f32(f.sv[i]);
+    const u32x4_t w = keep(f.wv[i], ok);
 #pragma unroll
-    for (int st = 0; st < 4; ++st) acc = mfma16(dequant8(f.wv[i][st], s), f.xv[i][st], acc);
+    for (int st = 0; st < 4; ++st)
+      acc = mfma16(dequant8(w[st], s), keep(f.xv[i][st], ok && mok), acc);
   }
-  return reduce_waves<NW>(acc, red);
+  return acc;
+}
+
+// The same, summed over the waves in wave order: valid in wave 0, lane l
+// holding D[n0 + 4 (l >> 4) + v][m = l & 15].
+template <int NW, int CPW>
+__device__ __forceinline__ f32x4_v weight_mfma(const Skinny2Params& p, const WeightFrags<CPW>& f,
+                                               f32x4_v* red) {
+  return reduce_waves<NW>(weight_partial<NW, CPW>(p, f), red);
 }
 
 // y[m][nb .. nb + 3] = o (bf16 bits), one 8-byte store when whole and aligned
@@ -252,7 +295,7 @@ __device__ __forceinline__ void weight_block(const Skinny2Params& p, int64_t b, 
     if (p.b_vec && 8 * lane < rows * p.rank) touch = ld16(p.lora_b + n0 * p.rank + 8 * lane).x;
     if (p.bias != nullptr && lane < rows) touch ^= p.bias[n0 + lane];
   }
-  const f32x4_v acc = weight_mfma<NW, CPW>(f, red);
+  const f32x4_v acc = weight_mfma<NW, CPW>(p, f, red);
   if (wave != 0) return;
   asm volatile("" ::"v"(touch));
   if (rl >= p.m) return;
@@ -400,64 +443,97 @@ __global__ void __launch_bounds__(kFinThreads) k_skinny_finish_multi(Skinny2Mult
 }
 
 // ---------------------------------------------------------------------------
-// One-launch form (k_skinny_one): the same two block roles, but the last
-// adapter block to arrive sums the partials into h and publishes it
-// (device-coherent stores, then a flag), and every weight block applies the
-// LoRA term to its own rows after a bounded wait for the flag, so the
-// finishing launch and its dispatch disappear. Adapter blocks come first in
-// the grid and wait on nothing, so the wait ends once they have run; the
-// spin limit only guarantees that every wave exits (h then reads as NaN and
-// the device error word gets kDevErrSkinnyOneWait). Slots are taken in turn:
-// at most kSlots calls may run at once on a device. Every call leaves its
-// slot at zero, also when waits expired: the weight blocks (after their
-// wait) and the publishing adapter block (after raising the flag) count into
-// a done word, and the last of them clears the slot.
-
-constexpr int kSlots2 = 8;
-constexpr int kSpin2 = 1 << 22;  // default polls of the bounded wait
-__device__ unsigned int g_skinny2_state[kSlots2][4];
+// One-launch form (k_skinny_one): the same two block roles, but the adapter
+// blocks hand their partials straight to the weight blocks, so the
+// finishing launch and its dispatch disappear. Each partial travels as one
+// 64-bit word (the f32 bits, and the call's 32-bit tag above them) written
+// with a single device-coherent store into the call's slot; a weight block
+// polls the words it needs until every one carries the call's tag, sums
+// them in slice order into h and applies the LoRA term to its own rows.
+//
+// The tag is a hash of the dispatch (its dispatch id, which the command
+// processor counts up per queue, and the address of its packet, which
+// tells queues apart) and of the host's call count, so every launch,
+// graph replays included, carries its own tag without any block having to
+// count in, and a word left in the slot by an earlier launch is taken for
+// this one's only if their 32-bit tags collide. Tags are never zero, the
+// value of a fresh slot's words. Adapter blocks come first in the grid and
+// wait on nothing, so the wait ends once they have run; the spin limit
+// only guarantees that every wave exits (h then reads as NaN and the device
+// error word gets kDevErrSkinnyOneWait). Slots are taken in turn: at most
+// kSlots2 calls may run at once on a device.
 
 template <int NW>
-__device__ __forceinline__ void adapter_block_one(const Skinny2Params& p, int a, f32x4_v* red,
-                                                  int* last_sh) {
+__device__ __forceinline__ void adapter_block_one(const Skinny2Params& p, int a, f32x4_v* red) {
   int s, q;
   const f32x4_v acc = adapter_partial<NW>(p, a, red, &s, &q);
+  if ((threadIdx.x >> 6) != 0) return;
+  const unsigned long long tag = static_cast<unsigned long long>(call_tag(p)) << 32;
   const int lane = threadIdx.x & 63;
   const int rl = lane & 15;
-  if ((threadIdx.x >> 6) == 0 && rl < p.m) {
-    float* dst = p.part + (static_cast<int64_t>(s) * p.m + rl) * p.rank;
+  if (rl >= p.m) return;
+  unsigned long long* dst = g_skinny2_words[p.slot] + (s * p.m + rl) * p.rank;
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int jj = 16 * q + 4 * (lane >> 4) + v;
-      if (jj < p.rank) store_coherent_f32(dst + jj, acc[v]);
-    }
-  }
-  drain_stores();
-  __syncthreads();
-  unsigned int* state = g_skinny2_state[p.slot];
-  if (threadIdx.x == 0) *last_sh = arrive(state, static_cast<unsigned int>(p.a_blocks)) ? 1 : 0;
-  __syncthreads();
-  if (*last_sh == 0) return;
-  // the last adapter block: h = bf16(sum over slices in slice order)
-  const int mr = p.m * p.rank;
-  for (int e = threadIdx.x; e < mr; e += 64 * NW) {
-    float sum = 0.0f;
-    for (int sl = 0; sl < p.slices; ++sl) sum += load_coherent_f32(p.part + static_cast<int64_t>(sl) * mr + e);
-    const float hv = round_bf16(sum);
-    store_coherent_f32(p.hf + e, hv);
-    p.h[e] = f32_to_bf16(hv);
-  }
-  drain_stores();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    __hip_atomic_store(state + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    drain_stores();  // the flag is visible before this block counts as done
-    done_count(state, 2, 3, static_cast<unsigned int>(p.w_blocks) + 1u);
+  for (int v = 0; v < 4; ++v) {
+    const int jj = 16 * q + 4 * (lane >> 4) + v;
+    // (the element goes through a scalar first: a bit cast of a vector
+    // element operand compiled to element 0 for every v)
+    const float val = acc[v];
+    if (jj < p.rank)
+      __hip_atomic_store(dst + jj, tag | __builtin_bit_cast(unsigned int, val), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
+// Wave 0 of a weight block: every partial word of the call, polled until
+// all carry the call's tag (bounded), into pv[slice][m][rank]. Returns
+// whether the wait succeeded; on expiry the values are NaN.
+__device__ __forceinline__ bool poll_partials(const Skinny2Params& p, unsigned int tag, float* pv) {
+  const int lane = threadIdx.x & 63;
+  const int words = p.slices * p.m * p.rank;
+  const unsigned long long* src = g_skinny2_words[p.slot];
+  // every lane's loads go out at once (indices past the call's words read
+  // word 0 and are ignored)
+  unsigned long long w[kOnePerLane];
+#pragma unroll
+  for (int u = 0; u < kOnePerLane; ++u) {
+    const int e = lane + 64 * u;
+    w[u] = __hip_atomic_load(const_cast<unsigned long long*>(src) + (e < words ? e : 0),
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  auto missing = [&]() {
+    bool miss = false;
+#pragma unroll
+    for (int u = 0; u < kOnePerLane; ++u)
+      miss |= lane + 64 * u < words && static_cast<unsigned int>(w[u] >> 32) != tag;
+    return miss;
+  };
+  bool ready = __ballot(missing()) == 0;
+  for (int it = 0; !ready && it < p.spin; ++it) {
+    __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+    for (int u = 0; u < kOnePerLane; ++u) {
+      const int e = lane + 64 * u;
+      if (e < words && static_cast<unsigned int>(w[u] >> 32) != tag)
+        w[u] = __hip_atomic_load(const_cast<unsigned long long*>(src) + e, __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+    }
+    ready = __ballot(missing()) == 0;
+  }
+  if (!ready && lane == 0)
+    __hip_atomic_fetch_or(p.err, kDevErrSkinnyOneWait, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+  for (int u = 0; u < kOnePerLane; ++u) {
+    const int e = lane + 64 * u;
+    if (e < words)
+      pv[e] = ready ? __builtin_bit_cast(float, static_cast<unsigned int>(w[u])) : __builtin_nanf("");
+  }
+  return ready;
+}
+
 template <int NW, int CPW>
-__device__ __forceinline__ void weight_block_one(const Skinny2Params& p, int64_t b, f32x4_v* red) {
+__device__ __forceinline__ void weight_block_one(const Skinny2Params& p, int64_t b, f32x4_v* red,
+                                                 float* pv) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int rl = lane & 15;
@@ -466,62 +542,31 @@ __device__ __forceinline__ void weight_block_one(const Skinny2Params& p, int64_t
   const int64_t rc = n0 + rl < p.n ? n0 + rl : p.n - 1;
   WeightFrags<CPW> f;
   weight_loads<NW, CPW>(p, n0, f);
-  // wave 0 also loads its rows of B as MFMA row fragments (rank <= 64: two
-  // 32-rank steps, j = 32 q + 8 g + [0, 8)) and its 4 bias values
-  u32x4_t bfr[2] = {u32x4_t{0u, 0u, 0u, 0u}, u32x4_t{0u, 0u, 0u, 0u}};
-  float bias4[4] = {0.f, 0.f, 0.f, 0.f};
-  if (wave == 0) {
-    const uint16_t* brow = p.lora_b + rc * p.rank;
+  // every wave also loads its rows of B as MFMA row fragments (rank <= 64,
+  // a multiple of 8: two 32-rank steps, j = 32 q + 8 g + [0, 8); steps past
+  // the rank read j = 0 and become zeros) and its 4 bias values; wave 0
+  // uses them. All loads are unconditional.
+  const uint16_t* brow = p.lora_b + rc * p.rank;
+  u32x4_t bfr[2];
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const int j0 = 32 * q + 8 * g;
-      if (j0 >= p.rank) continue;
-      if (p.b_vec && j0 + 8 <= p.rank) {
-        bfr[q] = ld16(brow + j0);
-      } else {
-        uint32_t w4[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const uint32_t lo = j0 + 2 * e < p.rank ? brow[j0 + 2 * e] : 0u;
-          const uint32_t hi = j0 + 2 * e + 1 < p.rank ? brow[j0 + 2 * e + 1] : 0u;
-          w4[e] = lo | (hi << 16);
-        }
-        bfr[q] = u32x4_t{w4[0], w4[1], w4[2], w4[3]};
-      }
-    }
-    if (p.bias != nullptr) {
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int64_t nn = n0 + 4 * g + v;
-        bias4[v] = nn < p.n ? bf16_to_f32(p.bias[nn]) : 0.0f;
-      }
-    }
+  for (int q = 0; q < 2; ++q) {
+    const int j0 = 32 * q + 8 * g;
+    bfr[q] = ld16(brow + (j0 < p.rank ? j0 : 0));
   }
-  const f32x4_v acc = weight_mfma<NW, CPW>(f, red);
+  // (without a bias the loads read B and are ignored)
+  const uint16_t* bias_src = p.bias != nullptr ? p.bias : p.lora_b;
+  uint16_t bias_raw[4];
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int64_t nn = n0 + 4 * g + v;
+    bias_raw[v] = bias_src[nn < p.n ? nn : p.n - 1];
+  }
+  const f32x4_v acc = weight_mfma<NW, CPW>(p, f, red);
   if (wave != 0) return;
 
-  // wait (lane 0, bounded) for the published h, then read it as MFMA
-  // column fragments: lane (m = rl, g) takes h[m][32 q + 8 g + e]
-  unsigned int* state = g_skinny2_state[p.slot];
-  int ready = 1;
-  if (lane == 0) {
-    ready = 0;
-    for (int it = 0; it < p.spin; ++it) {
-      if (__hip_atomic_load(state + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u) {
-        ready = 1;
-        break;
-      }
-      __builtin_amdgcn_s_sleep(1);
-    }
-    if (!ready)
-      __hip_atomic_fetch_or(p.err, kDevErrSkinnyOneWait, __ATOMIC_RELAXED,
-                            __HIP_MEMORY_SCOPE_AGENT);
-    // past its last access to the slot
-    done_count(state, 2, 3, static_cast<unsigned int>(p.w_blocks) + 1u);
-  }
-  ready = __shfl(ready, 0, 64);
-  // the h loads below must not be issued before the flag was seen
-  asm volatile("" ::: "memory");
+  poll_partials(p, call_tag(p), pv);
+  // h = bf16(sum over slices in slice order) as MFMA column fragments: lane
+  // (m = rl, g) takes h[m][32 q + 8 g + e]; block 0 also stores h
   f32x4_v t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int q = 0; q < 2; ++q) {
@@ -530,12 +575,16 @@ __device__ __forceinline__ void weight_block_one(const Skinny2Params& p, int64_t
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const int jj = 32 * q + 8 * g + e;
-      hv[e] = (rl < p.m && jj < p.rank) ? load_coherent_f32(p.hf + rl * p.rank + jj) : 0.0f;
-      if (!ready) hv[e] = __builtin_nanf("");
+      float sum = 0.0f;
+      if (rl < p.m && jj < p.rank) {
+        for (int sl = 0; sl < p.slices; ++sl) sum += pv[(sl * p.m + rl) * p.rank + jj];
+        if (b == 0) p.h[rl * p.rank + jj] = f32_to_bf16(round_bf16(sum));
+      }
+      hv[e] = round_bf16(sum);
     }
     const u32x4_t hfr{pack_bf16x2(hv[0], hv[1]), pack_bf16x2(hv[2], hv[3]), pack_bf16x2(hv[4], hv[5]),
                       pack_bf16x2(hv[6], hv[7])};
-    t = mfma16(bfr[q], hfr, t);
+    t = mfma16(keep(bfr[q], 32 * q + 8 * g < p.rank), hfr, t);
   }
   if (rl >= p.m) return;
   // lane: y[m = rl][n = n0 + 4 g + v]
@@ -544,7 +593,7 @@ __device__ __forceinline__ void weight_block_one(const Skinny2Params& p, int64_t
   for (int v = 0; v < 4; ++v) {
     float r = round_bf16(acc[v]);
     r = round_bf16(r + round_bf16(round_bf16(t[v]) * p.scale));
-    if (p.bias != nullptr) r = round_bf16(r + bias4[v]);
+    if (p.bias != nullptr) r = round_bf16(r + bf16_to_f32(bias_raw[v]));
     o[v] = f32_to_bf16(r);
   }
   store_row4(p, rl, n0 + 4 * g, o);
@@ -553,12 +602,12 @@ __device__ __forceinline__ void weight_block_one(const Skinny2Params& p, int64_t
 template <int NW, int CPW>
 __global__ void __launch_bounds__(64 * NW) k_skinny_one(Skinny2Params p) {
   __shared__ f32x4_v red[(NW > 1 ? NW - 1 : 1) * 64];
-  __shared__ int last_sh;
+  __shared__ float pv[kOneWords];
   const int b = static_cast<int>(blockIdx.x);
   if (b < p.a_blocks) {
-    adapter_block_one<NW>(p, b, red, &last_sh);
+    adapter_block_one<NW>(p, b, red);
   } else {
-    weight_block_one<NW, CPW>(p, b - p.a_blocks, red);
+    weight_block_one<NW, CPW>(p, b - p.a_blocks, red, pv);
   }
 }
 
@@ -570,18 +619,16 @@ void launch_one(const Skinny2Params& p, hipStream_t stream) {
 
 std::atomic<unsigned int> g_calls2{0};
 
-// The one-launch form pays for its published h with a chain of dependent
-// round trips (the adapter blocks' partials, the last one's sums, the
-// flag, the weight blocks' reads) that the weight stream hides only when it
-// is long: measured on the Qwen3-2B shapes at M = 1, 6144 -> 2048 takes
-// 11.3 us against 13.5 us for two launches, but 2048 -> 6144 12.8 against
-// 10.5 and 2048 -> 2048 9.7 against 8.2. Chosen for K >= 4096; the
-// kTuneSkinny2One knob forces either form.
-bool one_launch_selected(int64_t k) {
-  const int force = tune(kTuneSkinny2One);
-  if (force == 0) return false;
-  if (force > 0) return true;
-  return k >= 4096;
+// The one-launch form is the default for M <= 4 (rank a multiple of 8, B
+// 16-byte aligned): the weight blocks' one poll of the tagged partials
+// replaces the finishing launch. Measured on the Qwen3-2B shapes at M = 1
+// (rank 32, group 64, weights cycled beyond the MALL, graph of 96 calls):
+// 2048 -> 6144 8.5 us against 9.9 us for two launches, 6144 -> 2048 11.2
+// against 13.0, 2048 -> 2048 7.5 against 8.0. The kTuneSkinny2One knob
+// forces two launches (0).
+bool one_launch_selected(int64_t m, bool b_frag) {
+  if (m > kOneMaxM || !b_frag) return false;
+  return tune(kTuneSkinny2One) != 0;
 }
 
 template <int NW, int CPW>
@@ -635,8 +682,8 @@ bool skinny2_selected(int64_t m, int64_t n, int64_t k, int64_t rank, int64_t n_g
 }
 
 int64_t skinny2_workspace_floats(int64_t m, int64_t n, int64_t k, int64_t rank) {
-  // K-slice partials of h, then the published h
-  return static_cast<int64_t>(plan2(n, k).slices) * m * rank + m * rank;
+  // K-slice partials of h (the two-launch form)
+  return static_cast<int64_t>(plan2(n, k).slices) * m * rank;
 }
 
 hipError_t launch_skinny2_forward(const uint16_t* x, int64_t m, int64_t k, const Int4Operand& w,
@@ -667,15 +714,18 @@ hipError_t launch_skinny2_forward(const uint16_t* x, int64_t m, int64_t k, const
   p.slices = pl.slices;
   p.a_blocks = p.slices * static_cast<int>(ceil_div(rank, 16));
   p.b_vec = (reinterpret_cast<uintptr_t>(lora_b) & 15) == 0 && rank % 8 == 0 && rank * 16 <= 512;
-  p.hf = ws + static_cast<int64_t>(p.slices) * m * rank;
   p.w_blocks = static_cast<int>(ceil_div(n, 16));
   p.slot = 0;
+  p.tag = 0;
   p.spin = tune(kTuneSpinLimit) > 0 ? tune(kTuneSpinLimit) : kSpin2;
   p.err = nullptr;
-  if (one_launch_selected(k)) {
+  // the one-launch weight blocks load B rows as 16-byte MFMA fragments
+  const bool b_frag = (reinterpret_cast<uintptr_t>(lora_b) & 15) == 0 && rank % 8 == 0;
+  if (one_launch_selected(m, b_frag)) {
     p.err = device_error_word();
     if (p.err == nullptr) return hipErrorInvalidSymbol;
-    p.slot = static_cast<int>(g_calls2.fetch_add(1, std::memory_order_relaxed) % kSlots2);
+    p.tag = g_calls2.fetch_add(1, std::memory_order_relaxed);
+    p.slot = static_cast<int>(p.tag % kSlots2);
     bool one = false;
 #define RPX_ONE(NW, CPW)                              \
   if (!one && pl.nw == NW && pl.cpw == CPW) {         \
@@ -775,9 +825,9 @@ hipError_t launch_skinny2_forward_multi(const uint16_t* x, int64_t m, int64_t k,
     p.a_blocks = p.slices * static_cast<int>(ceil_div(q.rank, 16));
     p.b_vec = (reinterpret_cast<uintptr_t>(q.lora_b) & 15) == 0 && q.rank % 8 == 0 &&
               q.rank * 16 <= 512;
-    p.hf = nullptr;
     p.w_blocks = static_cast<int>(ceil_div(q.n, 16));
     p.slot = 0;
+    p.tag = 0;
     p.spin = 0;
     p.err = nullptr;
     part += static_cast<int64_t>(pl.slices) * m * q.rank;

@@ -261,8 +261,10 @@ def test_skinny_every_tile_shape_matches_oracle(tile, m, k, n, r, group):
 @pytest.mark.parametrize("one", [0, 1])
 def test_skinny_two_launch_matches_oracle(one, m, k, n, r, group):
     """The M <= 16 row-block path, forced: two launches, or the one-launch
-    form with the published h. Ragged last row blocks, ranks
-    that are not multiples of 8 and ranks above 32, several K slices."""
+    form (M <= 4 with the rank a multiple of 8; the others fall back to two
+    launches) that hands the adapter partials to the weight blocks as tagged
+    words. Ragged last row blocks, ranks that are not multiples of 8 and
+    ranks above 32, several K slices."""
 
     x, packed, scales, a, b, bias_bits, _ = _lora_case(m, k, n, r, group, seed=m + r, bias=True)
     b = b * 50.0  # the adapter term comparable to the base product
@@ -309,10 +311,10 @@ def test_skinny_one_launch_consecutive_calls_match_oracle():
 
 @pytest.mark.parametrize("m,k", [(8, 2048), (2, 2048), (1, 4096)])
 def test_skinny_graph_replays_and_repeats_are_bit_identical(m, k):
-    """The arrival words of the one-launch kernels (M = 8: per-tile split
-    counters; M = 1, K = 4096: the published h) return to their resting
-    value after each call, and the two-launch path (M = 2, K = 2048) keeps
-    no state: eager repeats and graph replays give the same bits."""
+    """The arrival words of the M > 4 one-launch kernel (M = 8: per-tile
+    split counters) return to their resting value after each call, and the
+    M <= 4 one-launch form (M = 2 and 1) tags its partials per launch: eager
+    repeats and graph replays give the same bits."""
 
     n, r = 1536, 32
     x, packed, scales, a, b, bias_bits, _ = _lora_case(m, k, n, r, 64, seed=91, bias=False)
@@ -344,6 +346,73 @@ def test_skinny_graph_replays_and_repeats_are_bit_identical(m, k):
         ye, _ = call()
         torch.cuda.synchronize()
         assert torch.equal(ye, y0)
+
+
+@pytest.mark.parametrize("m,k,n,r,group", [(1, 2048, 6144, 32, 64), (4, 6144, 2048, 32, 64),
+                                           (2, 2048, 2048, 64, None), (3, 1024, 1000, 24, 64),
+                                           (1, 8192, 512, 40, 64), (4, 512, 96, 8, None)])
+def test_skinny_one_launch_h_equals_two_launches(m, k, n, r, group):
+    """The one-launch form sums the same partials in the same order as the
+    two-launch form's finishing launch: h is bit-identical; y matches the
+    oracle."""
+
+    x, packed, scales, a, b, bias_bits, _ = _lora_case(m, k, n, r, group, seed=7 * m + r, bias=True)
+    b = b * 50.0
+    args = (to_dev_bf16(x), to_dev(packed), to_dev(scales.view(np.int16)).view(torch.uint16),
+            to_dev_bf16(a), to_dev_bf16(b))
+    biasd = to_dev(bias_bits.view(np.int16)).view(torch.uint16)
+    out = {}
+    for one in (0, 1):
+        with ops.tuning(skinny2_one=one):
+            out[one] = ops.int4lora_forward(*args, scaling=2.0, group_size=group, bias_bits=biasd)
+    torch.cuda.synchronize()
+    assert torch.equal(out[0][1].view(torch.uint16), out[1][1].view(torch.uint16))
+    y_o, h_o = olora.lora_forward(x, packed, scales, a, b, alpha=2.0 * r, rank=r,
+                                  bias_bits=bias_bits, group_size=group)
+    assert_bf16_close(from_dev(out[1][0]), y_o, what="y")
+    assert_bf16_close(from_dev(out[1][1]), h_o, what="h")
+
+
+def test_skinny_one_launch_graph_replays_follow_new_inputs():
+    """A graph of one M = 1 one-launch call replayed with new x each time
+    (the launch's parameters, slot included, stay the same): every replay
+    equals the two-launch form on the same x, so no replay takes the
+    partials its previous replay left in the slot."""
+
+    m, k, n, r = 1, 2048, 1536, 32
+    x, packed, scales, a, b, _, _ = _lora_case(m, k, n, r, 64, seed=301, bias=False)
+    b = b * 50.0
+    xd, pd = to_dev_bf16(x), to_dev(packed)
+    sd = to_dev(scales.view(np.int16)).view(torch.uint16)
+    ad, bd = to_dev_bf16(a), to_dev_bf16(b)
+
+    def call():
+        return ops.int4lora_forward(xd, pd, sd, ad, bd, scaling=1.0, group_size=64)
+
+    with ops.tuning(skinny2_one=1):
+        call()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            call()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            yg, hg = call()
+    for i in range(6):
+        xi = bf16_values(rng(400 + i).standard_normal((m, k)))
+        xd.copy_(to_dev_bf16(xi))
+        graph.replay()
+        torch.cuda.synchronize()
+        with ops.tuning(skinny2_one=0):
+            y0, h0 = call()
+        torch.cuda.synchronize()
+        assert torch.equal(hg.view(torch.uint16), h0.view(torch.uint16)), i
+        y_o, _ = olora.lora_forward(xi, packed, scales, a, b, alpha=float(r), rank=r,
+                                    group_size=64)
+        assert_bf16_close(from_dev(yg), y_o, what="y")
+    assert ops.check_device_errors() == 0
 
 
 @pytest.mark.parametrize("group", [None, 64])
@@ -466,7 +535,8 @@ def test_skinny_slots_recover_after_expired_waits(form):
     one-poll spin limit; every kernel still exits normally), then run more
     calls than there are slots with the default limit: each equals the
     result taken before, bit for bit, so no expired call left its slot
-    dirty. Expired calls are reported through the device error word."""
+    dirty (M > 4) or handed its late partials to a later call (M <= 4).
+    Expired calls are reported through the device error word."""
 
     if form == "skinny":
         m, k, knobs = 8, 2048, dict(skinny2=0)

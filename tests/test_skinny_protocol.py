@@ -1,19 +1,28 @@
-"""Model check of the one-launch skinny kernels' slot protocols (CPU).
+"""Model check of the skinny kernels' cross-block hand-offs (CPU).
 
-``k_skinny`` (csrc/skinny.hip) and ``k_skinny_one`` (csrc/skinny2.hip) hand
-partial results between the blocks of one launch through a slot of arrival
-words, and a call only works if the slot is all-zero when it starts. Each
-block is modelled here as a sequence of atomic operations on the slot words
-(the fetch-adds, loads and stores of the kernels, in program order; a
-bounded wait is a run of loads that gives up after ``spin`` polls), and a
-scheduler interleaves the blocks at random. For every schedule, including
-those where a wait expires because the blocks it waits for have not run
-yet, the slot must be all-zero once every block has finished, and a wait
-that succeeded must only have succeeded on this call's own arrivals.
+``k_skinny`` (csrc/skinny.hip) hands partial results between the blocks of
+one launch through a slot of arrival words, and a call only works if the
+slot is all-zero when it starts. Each block is modelled here as a sequence
+of atomic operations on the slot words (the fetch-adds, loads and stores of
+the kernel, in program order; a bounded wait is a run of loads that gives
+up after ``spin`` polls), and a scheduler interleaves the blocks at random.
+For every schedule, including those where a wait expires because the
+blocks it waits for have not run yet, the slot must be all-zero once every
+block has finished, and a wait that succeeded must only have succeeded on
+this call's own arrivals. The protocol the kernel used before (the last
+finisher clears the adapter word; a late adapter then increments it again)
+is kept as a negative control: the checker must find the schedules that
+leave its slot dirty.
 
-The protocol the kernels used before (the last finisher clears the adapter
-word; a late adapter then increments it again) is kept as a negative
-control: the checker must find the schedules that leave its slot dirty.
+``k_skinny_one`` (csrc/skinny2.hip) needs no clean-up: every partial travels
+as one word holding its value and the launch's tag, a hash of the dispatch
+(the queue's dispatch id and the packet address) and the host's call
+count, and a weight block takes a word only when the word carries its own
+launch's tag. Modelled with the tag as the pair (dispatch, host count),
+back-to-back launches and graph replays (the same host count, a new
+dispatch) must never read a word of an earlier launch. A tag made of the
+host's call count alone is the negative control: a replayed launch then
+takes the words its previous replay left.
 """
 
 from __future__ import annotations
@@ -84,54 +93,36 @@ def skinny_blocks(slot: Slot, adapters: int, tiles: int, splits: int, spin: int,
     return gens
 
 
-def skinny_one_blocks(slot: Slot, adapters: int, weights: int, spin: int, log: list,
-                      fixed: bool = True):
-    """Generators for the blocks of one k_skinny_one launch. Words: [0]
-    adapter arrivals, [1] h published, [2] done."""
+def skinny_one_blocks(words: dict, tag, launch: int, adapters: int, weights: int, spin: int,
+                      log: list):
+    """Generators for the blocks of one k_skinny_one launch (number
+    ``launch``). ``words`` maps a partial's index (one per adapter block
+    here) to (tag, launch that wrote it); each adapter block stores its word
+    once, each weight block polls every word until all carry ``tag`` (at most
+    ``spin`` polls) and logs whether the words it accepted were this
+    launch's."""
 
-    done_target = weights + 1
-
-    def done_count():
-        old = slot.fetch_add(2)
-        if old + 1 == done_target:
-            slot.w[0] = 0
-            yield
-            slot.w[1] = 0
-            yield
-            slot.w[2] = 0
+    def adapter(i: int):
         yield
-
-    def adapter():
-        old = slot.fetch_add(0)
-        last = old + 1 == adapters
-        if last:
-            slot.w[0] = 0
+        words[i] = (tag, launch)
         yield
-        if not last:
-            return
-        slot.w[1] = 1  # h published
-        yield
-        if fixed:
-            yield from done_count()
 
     def weight():
-        ok = False
+        seen = {}
         polls = 0
-        while not ok and polls < spin:
-            ok = slot.w[1] != 0
+        while True:
+            for i in range(adapters):
+                if i not in seen and words.get(i, (0, None))[0] == tag:
+                    seen[i] = words[i][1]
             polls += 1
+            if len(seen) == adapters or polls >= spin:
+                break
             yield
-        log.append(("weight", ok))
-        if fixed:
-            yield from done_count()
-        else:
-            old = slot.fetch_add(2)
-            if old + 1 == weights:
-                slot.w[2] = 0
-                slot.w[1] = 0
-            yield
+        ok = len(seen) == adapters
+        log.append(("weight", ok, ok and all(w == launch for w in seen.values())))
+        yield
 
-    return [adapter() for _ in range(adapters)] + [weight() for _ in range(weights)]
+    return [adapter(i) for i in range(adapters)] + [weight() for _ in range(weights)]
 
 
 def run(gens, rng: random.Random, adapters_late: bool) -> None:
@@ -150,12 +141,13 @@ def run(gens, rng: random.Random, adapters_late: bool) -> None:
             live.pop(idx)
 
 
-def _calls(kind: str, fixed: bool, seed: int, n_calls: int = 6):
-    """Runs n_calls launches on one slot back to back (a stream's order);
-    returns (slot clean after every call, every successful wait legitimate)."""
+def _calls(fixed: bool, seed: int, n_calls: int = 6):
+    """Runs n_calls k_skinny launches on one slot back to back (a stream's
+    order); returns (slot clean after every call, every successful wait
+    legitimate)."""
 
     rng = random.Random(seed)
-    slot = Slot(2 + 3 if kind == "skinny" else 3)
+    slot = Slot(2 + 3)
     clean = True
     legit = True
     for _ in range(n_calls):
@@ -165,15 +157,9 @@ def _calls(kind: str, fixed: bool, seed: int, n_calls: int = 6):
         spin = rng.choice([1, 2, 3, 50])
         late = rng.random() < 0.5
         start = list(slot.w)
-        if kind == "skinny":
-            adapters, tiles, splits = rng.choice([(1, 1, 2), (2, 2, 2), (3, 3, 1), (2, 3, 3)])
-            gens = skinny_blocks(slot, adapters, tiles, splits, spin, log, fixed)
-        else:
-            adapters, weights = rng.choice([(1, 1), (2, 3), (3, 2), (4, 4)])
-            gens = skinny_one_blocks(slot, adapters, weights, spin, log, fixed)
-        run(gens, rng, late)
+        adapters, tiles, splits = rng.choice([(1, 1, 2), (2, 2, 2), (3, 3, 1), (2, 3, 3)])
+        run(skinny_blocks(slot, adapters, tiles, splits, spin, log, fixed), rng, late)
         # a wait that succeeds on a dirty slot may have counted stale arrivals
-        # (k_skinny) or seen the previous call's h flag (k_skinny_one)
         if any(start):
             legit = legit and not any(entry[-1] for entry in log)
     if any(slot.w):
@@ -181,25 +167,64 @@ def _calls(kind: str, fixed: bool, seed: int, n_calls: int = 6):
     return clean, legit
 
 
-@pytest.mark.parametrize("kind", ["skinny", "skinny_one"])
-def test_slot_returns_to_zero_under_every_schedule(kind):
+def _one_calls(dispatch_tags: bool, seed: int, n_calls: int = 8):
+    """Launches of k_skinny_one on one slot, some of them replays of the
+    previous launch (same host call count); returns whether every weight
+    block that accepted words accepted only its own launch's."""
+
+    rng = random.Random(seed)
+    words: dict = {}
+    host = 0
+    dispatch = 0
+    legit = True
+    for i in range(n_calls):
+        if i == 0 or rng.random() < 0.5:
+            host += 1  # a new call; otherwise a graph replay of the last one
+        dispatch += 1
+        tag = (dispatch, host) if dispatch_tags else host
+        log: list = []
+        adapters, weights = rng.choice([(1, 1), (2, 3), (3, 2), (4, 4)])
+        spin = rng.choice([1, 2, 3, 50])
+        run(skinny_one_blocks(words, tag, i, adapters, weights, spin, log), rng,
+            adapters_late=rng.random() < 0.5)
+        legit = legit and all(own for _, ok, own in log if ok)
+    return legit
+
+
+def test_skinny_slot_returns_to_zero_under_every_schedule():
     for seed in range(3000):
-        clean, legit = _calls(kind, fixed=True, seed=seed)
-        assert clean and legit, (kind, seed)
+        clean, legit = _calls(fixed=True, seed=seed)
+        assert clean and legit, seed
 
 
-@pytest.mark.parametrize("kind", ["skinny", "skinny_one"])
-def test_checker_catches_the_former_protocol(kind):
+def test_checker_catches_the_former_skinny_protocol():
     """Negative control: the protocol without the done count leaves the slot
     dirty after an expired wait, in some schedules."""
 
-    dirty = sum(not _calls(kind, fixed=False, seed=seed)[0] for seed in range(3000))
+    dirty = sum(not _calls(fixed=False, seed=seed)[0] for seed in range(3000))
     assert dirty > 0
+
+
+def test_skinny_one_takes_only_its_own_launchs_words():
+    """Dispatch-derived tags: no schedule, replay or expired wait lets a
+    launch read a word that an earlier launch left in the slot."""
+
+    for seed in range(3000):
+        assert _one_calls(dispatch_tags=True, seed=seed), seed
+
+
+def test_checker_catches_host_only_tags_on_replays():
+    """Negative control: with the host's call count as the tag, a graph
+    replay takes the words of its previous replay in some schedules."""
+
+    stale = sum(not _one_calls(dispatch_tags=False, seed=seed) for seed in range(3000))
+    assert stale > 0
 
 
 def test_slot_is_clean_when_no_wait_expires():
     """With unbounded waits (spin large, blocks interleaved fairly) both
-    protocols leave the slot clean; the fix changes only the expired case."""
+    k_skinny protocols leave the slot clean; the fix changes only the
+    expired case. k_skinny_one's waits all succeed on their own words."""
 
     for seed in range(500):
         rng = random.Random(seed)
@@ -208,7 +233,9 @@ def test_slot_is_clean_when_no_wait_expires():
             log: list = []
             run(skinny_blocks(slot, 2, 2, 2, 10_000, log, fixed), rng, adapters_late=False)
             assert not any(slot.w) and all(ok for _, _, ok in log)
-            slot = Slot(3)
+        words: dict = {}
+        for call in range(3):
             log = []
-            run(skinny_one_blocks(slot, 3, 2, 10_000, log, fixed), rng, adapters_late=False)
-            assert not any(slot.w) and all(ok for _, ok in log)
+            run(skinny_one_blocks(words, (call, 1), call, 3, 2, 10_000, log), rng,
+                adapters_late=False)
+            assert all(ok and own for _, ok, own in log)
