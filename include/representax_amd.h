@@ -185,8 +185,8 @@ int rpx_int4lora_forward(const void* x, int dtype, int64_t m, int64_t k, const u
  * QuantizedLoRALinear.__call__ on one input (adapters.py:158-182), e.g.
  * bert/model.py's query / key / value and qwen3_vl/text.py's gate / up.
  * For bf16 with M <= 4 (the skinny-M regime), one rank and at most 4
- * projections, all of them run in one pair of launches instead of one pair
- * each. Above the skinny sizes, when every projection takes the fused MFMA
+ * projections, all of them run in one launch (one pair of launches when
+ * the rank is not a multiple of 8) instead of one or two each. Above the skinny sizes, when every projection takes the fused MFMA
  * path and their ranks add up to at most 128 in 16-rank blocks (q / k / v
  * at rank 16 or 32, gate / up at rank 32), one launch forms every h from one pass
  * over x, bit-identical to the per-projection h, and then each projection's

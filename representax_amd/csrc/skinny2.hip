@@ -70,6 +70,7 @@ struct Skinny2Params {
   // one-launch form: the call's slot, the host's call count (mixed into the
   // tag), the polls of the bounded wait and the device error word
   int slot;
+  int proj;  // -1, or the projection's index in a shared-input call
   unsigned int tag;
   int w_blocks;
   int spin;
@@ -139,7 +140,14 @@ constexpr int kOneMaxM = 4;      // rows of x the one-launch form takes
 // partial words of a slot: [slice][m][rank], slices <= 4, rank <= 64
 constexpr int kOneWords = 4 * kOneMaxM * 64;
 constexpr int kOnePerLane = kOneWords / 64;
+constexpr int kMaxProjections = 4;
 __device__ unsigned long long g_skinny2_words[kSlots2][kOneWords];
+// the shared-input calls' own slots, one set of words per projection
+__device__ unsigned long long g_skinny2_multi_words[kSlots2][kMaxProjections][kOneWords];
+
+__device__ __forceinline__ unsigned long long* slot_words(const Skinny2Params& p) {
+  return p.proj < 0 ? g_skinny2_words[p.slot] : g_skinny2_multi_words[p.slot][p.proj];
+}
 
 // The launch's dispatch id (an LLVM intrinsic without a clang builtin).
 extern "C" __device__ unsigned long long rpx_amdgcn_dispatch_id() __asm("llvm.amdgcn.dispatch.id");
@@ -393,7 +401,7 @@ __global__ void __launch_bounds__(kFinThreads) k_skinny_finish(Skinny2Params p) 
 // every projection's adapter blocks, then every projection's weight blocks;
 // the finishing grid every projection's row blocks. Each block does what it
 // does in the single-projection launches, on its projection's operands.
-constexpr int kMaxProjections = 4;
+// The one-launch form of the same grid (k_skinny_one_multi) is further down.
 struct Skinny2Multi {
   Skinny2Params p[kMaxProjections];
   int count;
@@ -472,7 +480,7 @@ __device__ __forceinline__ void adapter_block_one(const Skinny2Params& p, int a,
   const int lane = threadIdx.x & 63;
   const int rl = lane & 15;
   if (rl >= p.m) return;
-  unsigned long long* dst = g_skinny2_words[p.slot] + (s * p.m + rl) * p.rank;
+  unsigned long long* dst = slot_words(p) + (s * p.m + rl) * p.rank;
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
     const int jj = 16 * q + 4 * (lane >> 4) + v;
@@ -491,7 +499,7 @@ __device__ __forceinline__ void adapter_block_one(const Skinny2Params& p, int a,
 __device__ __forceinline__ bool poll_partials(const Skinny2Params& p, unsigned int tag, float* pv) {
   const int lane = threadIdx.x & 63;
   const int words = p.slices * p.m * p.rank;
-  const unsigned long long* src = g_skinny2_words[p.slot];
+  const unsigned long long* src = slot_words(p);
   // every lane's loads go out at once (indices past the call's words read
   // word 0 and are ignored)
   unsigned long long w[kOnePerLane];
@@ -611,6 +619,36 @@ __global__ void __launch_bounds__(64 * NW) k_skinny_one(Skinny2Params p) {
   }
 }
 
+// Several projections of one input in one launch: every projection's
+// adapter blocks, then every projection's weight blocks, each doing what it
+// does in k_skinny_one with its projection's operands and words.
+template <int NW, int CPW>
+__global__ void __launch_bounds__(64 * NW) k_skinny_one_multi(Skinny2Multi mp) {
+  __shared__ f32x4_v red[(NW > 1 ? NW - 1 : 1) * 64];
+  __shared__ float pv[kOneWords];
+  int64_t b = blockIdx.x;
+#pragma unroll
+  for (int i = 0; i < kMaxProjections; ++i) {
+    if (i < mp.count) {
+      if (b < mp.p[i].a_blocks) {
+        adapter_block_one<NW>(mp.p[i], static_cast<int>(b), red);
+        return;
+      }
+      b -= mp.p[i].a_blocks;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kMaxProjections; ++i) {
+    if (i < mp.count) {
+      if (b < mp.p[i].w_blocks) {
+        weight_block_one<NW, CPW>(mp.p[i], b, red, pv);
+        return;
+      }
+      b -= mp.p[i].w_blocks;
+    }
+  }
+}
+
 template <int NW, int CPW>
 void launch_one(const Skinny2Params& p, hipStream_t stream) {
   hipLaunchKernelGGL((k_skinny_one<NW, CPW>), dim3(static_cast<unsigned>(p.a_blocks + p.w_blocks)),
@@ -618,6 +656,7 @@ void launch_one(const Skinny2Params& p, hipStream_t stream) {
 }
 
 std::atomic<unsigned int> g_calls2{0};
+std::atomic<unsigned int> g_calls2_multi{0};
 
 // The one-launch form is the default for M <= 4 (rank a multiple of 8, B
 // 16-byte aligned): the weight blocks' one poll of the tagged partials
@@ -640,7 +679,7 @@ void launch_main(const Skinny2Params& p, hipStream_t stream) {
 
 struct Skinny2Plan {
   int nw;      // waves per block
-  int cpw;     // 128-column chunks per weight wave (1, 2 or 4)
+  int cpw;     // 128-column chunks per weight wave (1 to 4)
   int slices;  // adapter K slices
 };
 
@@ -652,7 +691,7 @@ Skinny2Plan plan2(int64_t n, int64_t k) {
   p.nw = 4;
   while (p.nw < 16 && blocks * p.nw < 2048) p.nw *= 2;
   const int64_t c = ceil_div(k / 128, p.nw);
-  p.cpw = c <= 1 ? 1 : (c <= 2 ? 2 : 4);
+  p.cpw = static_cast<int>(c);
   p.slices = static_cast<int>(c);
   return p;
 }
@@ -716,6 +755,7 @@ hipError_t launch_skinny2_forward(const uint16_t* x, int64_t m, int64_t k, const
   p.b_vec = (reinterpret_cast<uintptr_t>(lora_b) & 15) == 0 && rank % 8 == 0 && rank * 16 <= 512;
   p.w_blocks = static_cast<int>(ceil_div(n, 16));
   p.slot = 0;
+  p.proj = -1;
   p.tag = 0;
   p.spin = tune(kTuneSpinLimit) > 0 ? tune(kTuneSpinLimit) : kSpin2;
   p.err = nullptr;
@@ -732,9 +772,9 @@ hipError_t launch_skinny2_forward(const uint16_t* x, int64_t m, int64_t k, const
     launch_one<NW, CPW>(p, stream);                   \
     one = true;                                       \
   }
-    RPX_ONE(4, 1) RPX_ONE(4, 2) RPX_ONE(4, 4)
-    RPX_ONE(8, 1) RPX_ONE(8, 2) RPX_ONE(8, 4)
-    RPX_ONE(16, 1) RPX_ONE(16, 2) RPX_ONE(16, 4)
+    RPX_ONE(4, 1) RPX_ONE(4, 2) RPX_ONE(4, 3) RPX_ONE(4, 4)
+    RPX_ONE(8, 1) RPX_ONE(8, 2) RPX_ONE(8, 3) RPX_ONE(8, 4)
+    RPX_ONE(16, 1) RPX_ONE(16, 2) RPX_ONE(16, 3) RPX_ONE(16, 4)
 #undef RPX_ONE
     return one ? hipGetLastError() : hipErrorInvalidValue;
   }
@@ -744,9 +784,9 @@ hipError_t launch_skinny2_forward(const uint16_t* x, int64_t m, int64_t k, const
     launch_main<NW, CPW>(p, stream);                  \
     launched = true;                                  \
   }
-  RPX_MAIN(4, 1) RPX_MAIN(4, 2) RPX_MAIN(4, 4)
-  RPX_MAIN(8, 1) RPX_MAIN(8, 2) RPX_MAIN(8, 4)
-  RPX_MAIN(16, 1) RPX_MAIN(16, 2) RPX_MAIN(16, 4)
+  RPX_MAIN(4, 1) RPX_MAIN(4, 2) RPX_MAIN(4, 3) RPX_MAIN(4, 4)
+  RPX_MAIN(8, 1) RPX_MAIN(8, 2) RPX_MAIN(8, 3) RPX_MAIN(8, 4)
+  RPX_MAIN(16, 1) RPX_MAIN(16, 2) RPX_MAIN(16, 3) RPX_MAIN(16, 4)
 #undef RPX_MAIN
   if (!launched) return hipErrorInvalidValue;
   hipError_t e = hipGetLastError();
@@ -827,8 +867,9 @@ hipError_t launch_skinny2_forward_multi(const uint16_t* x, int64_t m, int64_t k,
               q.rank * 16 <= 512;
     p.w_blocks = static_cast<int>(ceil_div(q.n, 16));
     p.slot = 0;
+    p.proj = i;
     p.tag = 0;
-    p.spin = 0;
+    p.spin = tune(kTuneSpinLimit) > 0 ? tune(kTuneSpinLimit) : kSpin2;
     p.err = nullptr;
     part += static_cast<int64_t>(pl.slices) * m * q.rank;
     a_total += p.a_blocks;
@@ -836,15 +877,42 @@ hipError_t launch_skinny2_forward_multi(const uint16_t* x, int64_t m, int64_t k,
     fin_total += ceil_div(q.n, kFinRows);
   }
   const dim3 main_grid(static_cast<unsigned>(a_total + w_total));
+  bool one = true;
+  for (int i = 0; i < count; ++i) {
+    const bool b_frag =
+        (reinterpret_cast<uintptr_t>(proj[i].lora_b) & 15) == 0 && proj[i].rank % 8 == 0;
+    one = one && one_launch_selected(m, b_frag);
+  }
+  if (one) {
+    unsigned int* err = device_error_word();
+    if (err == nullptr) return hipErrorInvalidSymbol;
+    const unsigned int tag = g_calls2_multi.fetch_add(1, std::memory_order_relaxed);
+    for (int i = 0; i < count; ++i) {
+      mp.p[i].err = err;
+      mp.p[i].tag = tag;
+      mp.p[i].slot = static_cast<int>(tag % kSlots2);
+    }
+    bool launched_one = false;
+#define RPX_ONE_MULTI(NW, CPW)                                                                  \
+  if (!launched_one && pl.nw == NW && pl.cpw == CPW) {                                          \
+    hipLaunchKernelGGL((k_skinny_one_multi<NW, CPW>), main_grid, dim3(64 * NW), 0, stream, mp); \
+    launched_one = true;                                                                        \
+  }
+    RPX_ONE_MULTI(4, 1) RPX_ONE_MULTI(4, 2) RPX_ONE_MULTI(4, 3) RPX_ONE_MULTI(4, 4)
+    RPX_ONE_MULTI(8, 1) RPX_ONE_MULTI(8, 2) RPX_ONE_MULTI(8, 3) RPX_ONE_MULTI(8, 4)
+    RPX_ONE_MULTI(16, 1) RPX_ONE_MULTI(16, 2) RPX_ONE_MULTI(16, 3) RPX_ONE_MULTI(16, 4)
+#undef RPX_ONE_MULTI
+    return launched_one ? hipGetLastError() : hipErrorInvalidValue;
+  }
   bool launched = false;
 #define RPX_MULTI(NW, CPW)                                                                  \
   if (!launched && pl.nw == NW && pl.cpw == CPW) {                                          \
     hipLaunchKernelGGL((k_skinny_main_multi<NW, CPW>), main_grid, dim3(64 * NW), 0, stream, mp); \
     launched = true;                                                                        \
   }
-  RPX_MULTI(4, 1) RPX_MULTI(4, 2) RPX_MULTI(4, 4)
-  RPX_MULTI(8, 1) RPX_MULTI(8, 2) RPX_MULTI(8, 4)
-  RPX_MULTI(16, 1) RPX_MULTI(16, 2) RPX_MULTI(16, 4)
+  RPX_MULTI(4, 1) RPX_MULTI(4, 2) RPX_MULTI(4, 3) RPX_MULTI(4, 4)
+  RPX_MULTI(8, 1) RPX_MULTI(8, 2) RPX_MULTI(8, 3) RPX_MULTI(8, 4)
+  RPX_MULTI(16, 1) RPX_MULTI(16, 2) RPX_MULTI(16, 3) RPX_MULTI(16, 4)
 #undef RPX_MULTI
   if (!launched) return hipErrorInvalidValue;
   hipError_t e = hipGetLastError();

@@ -87,6 +87,42 @@ def test_multi_replays_in_a_graph():
             assert torch.equal(y, ye) and torch.equal(h, he)
 
 
+def test_multi_one_launch_replays_follow_new_inputs():
+    """The one-launch shared-input form replayed in a graph with new x each
+    time: every replay's h equals the two-launch form's on the same x, bit
+    for bit, and y matches the oracle, so no replay takes partials that its
+    previous replay left in the slot."""
+
+    g = rng(660)
+    projs = [_proj(g, n, 2048, 32, 64, bias=False) for n in (6144, 6144)]
+    xd = to_dev_bf16(bf16_values(g.standard_normal((1, 2048))))
+    with ops.tuning(skinny2_one=1):
+        ops.int4lora_forward_multi(xd, [d for _, d in projs])
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            ops.int4lora_forward_multi(xd, [d for _, d in projs])
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            outs = ops.int4lora_forward_multi(xd, [d for _, d in projs])
+    for i in range(4):
+        x = bf16_values(rng(670 + i).standard_normal((1, 2048)))
+        xd.copy_(to_dev_bf16(x))
+        graph.replay()
+        torch.cuda.synchronize()
+        with ops.tuning(skinny2_one=0):
+            two = ops.int4lora_forward_multi(xd, [d for _, d in projs])
+        torch.cuda.synchronize()
+        for (host, _), (y, h), (_, h2) in zip(projs, outs, two):
+            assert torch.equal(h.view(torch.uint16), h2.view(torch.uint16)), i
+            y_o, _ = olora.lora_forward(x, host["packed"], host["scales"], host["a"], host["b"],
+                                        alpha=host["alpha"], rank=host["r"], group_size=host["group"])
+            assert_bf16_close(from_dev(y), y_o, what="y")
+    assert ops.check_device_errors() == 0
+
+
 def test_shared_input_projections_inference_path():
     from representax_amd import apply_quantized_lora, precision_context
     from representax_amd.config import PrecisionConfig
