@@ -50,6 +50,27 @@ __device__ __forceinline__ f32x4_t load_coherent(const f32x4_t* src) {
 }
 __device__ __forceinline__ void drain_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+// The running launch's dispatch id (an LLVM intrinsic without a clang
+// builtin): the command processor counts it up per queue.
+extern "C" __device__ unsigned long long rpx_amdgcn_dispatch_id() __asm("llvm.amdgcn.dispatch.id");
+
+// A 32-bit tag of the running launch, never zero: a hash of its dispatch id,
+// the address of its dispatch packet (which tells the queues apart) and a
+// count the host passes. Every launch, graph replays included, gets its own
+// tag without any block counting in; words that blocks of one launch hand
+// to each other carry it, so a word left by an earlier launch is taken only
+// if the two 32-bit tags collide.
+__device__ __forceinline__ unsigned int launch_tag(unsigned int host) {
+  const unsigned long long id = rpx_amdgcn_dispatch_id();
+  const unsigned long long pkt = reinterpret_cast<uintptr_t>(__builtin_amdgcn_dispatch_ptr());
+  unsigned long long h = (id * 0x9E3779B97F4A7C15ull) ^ (pkt * 0xC2B2AE3D27D4EB4Full) ^ host;
+  h ^= h >> 31;
+  h *= 0xBF58476D1CE4E5B9ull;
+  h ^= h >> 32;
+  const unsigned int t = static_cast<unsigned int>(h);
+  return t != 0u ? t : 1u;
+}
+
 // 32-bit coherent store and load (single values, flags).
 __device__ __forceinline__ void store_coherent_f32(float* dst, float v) {
   __hip_atomic_store(reinterpret_cast<unsigned int*>(dst), __builtin_bit_cast(unsigned int, v),

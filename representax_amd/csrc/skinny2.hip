@@ -149,19 +149,7 @@ __device__ __forceinline__ unsigned long long* slot_words(const Skinny2Params& p
   return p.proj < 0 ? g_skinny2_words[p.slot] : g_skinny2_multi_words[p.slot][p.proj];
 }
 
-// The launch's dispatch id (an LLVM intrinsic without a clang builtin).
-extern "C" __device__ unsigned long long rpx_amdgcn_dispatch_id() __asm("llvm.amdgcn.dispatch.id");
-
-__device__ __forceinline__ unsigned int call_tag(const Skinny2Params& p) {
-  const unsigned long long id = rpx_amdgcn_dispatch_id();
-  const unsigned long long pkt = reinterpret_cast<uintptr_t>(__builtin_amdgcn_dispatch_ptr());
-  unsigned long long h = (id * 0x9E3779B97F4A7C15ull) ^ (pkt * 0xC2B2AE3D27D4EB4Full) ^ p.tag;
-  h ^= h >> 31;
-  h *= 0xBF58476D1CE4E5B9ull;
-  h ^= h >> 32;
-  const unsigned int t = static_cast<unsigned int>(h);
-  return t != 0u ? t : 1u;
-}
+__device__ __forceinline__ unsigned int call_tag(const Skinny2Params& p) { return launch_tag(p.tag); }
 
 // Adapter block a = (K slice s, 16-rank group q): the fp32 partial of
 // x A^T over the slice's 128 NW columns, one 128-column chunk per wave,

@@ -240,6 +240,7 @@ TUNING_KNOBS = {
     "rank_blocks": nat.TUNE_RANK_BLOCKS,
     "rank_nt_u": nat.TUNE_RANK_NT_U,
     "fp8_splits": nat.TUNE_FP8_SPLITS,
+    "fp8_pair": nat.TUNE_FP8_PAIR,
 }
 
 
