@@ -66,7 +66,8 @@ template <int RB, int G, int U>
 __global__ void __launch_bounds__(256)
     k_rank_nt(const uint16_t* __restrict__ A, int64_t lda, RankNtBlocks blk, int64_t M, int64_t K,
               int round_a, float a_scale) {
-  __shared__ float red[3][G][RB][64][4];
+  // [v][lane]: a wave's reads and writes of one v are 64 consecutive words
+  __shared__ float red[3][G][RB][4][64];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -123,7 +124,7 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-        for (int v = 0; v < 4; ++v) red[wave - 1][gi][rb][lane][v] = acc[gi][rb][v];
+        for (int v = 0; v < 4; ++v) red[wave - 1][gi][rb][v][lane] = acc[gi][rb][v];
   }
   __syncthreads();
   if (wave != 0) return;
@@ -135,8 +136,8 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int64_t mm = m0 + 16 * gi + 4 * (lane >> 4) + v;
-        const float s = acc[gi][rb][v] + red[0][gi][rb][lane][v] + red[1][gi][rb][lane][v] +
-                        red[2][gi][rb][lane][v];
+        const float s = acc[gi][rb][v] + red[0][gi][rb][v][lane] + red[1][gi][rb][v][lane] +
+                        red[2][gi][rb][v][lane];
         if (mm < M && j < blk.valid[rb]) blk.out[rb][mm * blk.ldo[rb] + j] = f32_to_bf16(s);
       }
     }
