@@ -286,11 +286,14 @@ __device__ __forceinline__ void adapter_part(const SkinnyParams& p, int64_t a_sp
 // Outputs of one row tile. Each lane sums (in split order) the weight
 // fragments it would have written and, in waves below rank / 16, the h
 // fragments; both sets of loads issue from one loop. h = bf16(.) goes to LDS
-// (row stride rank + 1); the tile's rows of B are in LDS (row stride rank + 8)
-// when they load as vectors.
+// as fp32 (row stride rank + 1) and as bf16 (row stride rank + 8); the
+// tile's rows of B are in LDS (row stride rank + 8) when they load as
+// vectors, and then t = h B^T of each fragment is one 16x16x32 MFMA per 32
+// ranks (B rows as the row operand, h rows as the column operand), which
+// leaves t in the fragment's own layout, D[n = 4 g + v][m = rl].
 template <int MB, int T, int WK>
 __device__ __forceinline__ void finish_tile(const SkinnyParams& p, int64_t tile, float* h_lds,
-                                            const uint16_t* b_lds, bool poison) {
+                                            uint16_t* hb_lds, const uint16_t* b_lds, bool poison) {
   constexpr int WR = 4 / WK;
   constexpr int F = WR * T * MB;
   constexpr int FI = (F + 3) / 4;
@@ -342,7 +345,11 @@ __device__ __forceinline__ void finish_tile(const SkinnyParams& p, int64_t tile,
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int j = 16 * wave + 4 * g + v;
-        if (j < r) h_lds[m * (r + 1) + j] = poison ? __builtin_nanf("") : round_bf16(hacc[mb][v]);
+        if (j < r) {
+          const float hv = poison ? __builtin_nanf("") : round_bf16(hacc[mb][v]);
+          h_lds[m * (r + 1) + j] = hv;
+          hb_lds[m * (r + 8) + j] = f32_to_bf16(hv);
+        }
       }
     }
   }
@@ -361,6 +368,22 @@ __device__ __forceinline__ void finish_tile(const SkinnyParams& p, int64_t tile,
     const int t = (f / MB) % T;
     const int wr = f / (MB * T);
     const int m = 16 * mb + rl;
+    // rank chunks past r are zero in both operands (the LDS rows' padding is
+    // never written); h rows past M only reach outputs that are not stored
+    f32x4_t tv = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    if (p.b_vec) {
+      const uint16_t* bfr = b_lds + (wr * (16 * T) + 16 * t + rl) * (r + 8);
+      const uint16_t* hfr = hb_lds + m * (r + 8);
+      for (int c = 0; c < r; c += 32) {
+        const bool ok = c + 8 * g < r;
+        const int jc = ok ? c + 8 * g : 0;
+        const u32x4_t bw = *reinterpret_cast<const u32x4_t*>(bfr + jc);
+        const u32x4_t hw = *reinterpret_cast<const u32x4_t*>(hfr + jc);
+        const u32x4_t zero{0u, 0u, 0u, 0u};
+        tv = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ok ? bw : zero),
+                                                     as_bf16x8(ok ? hw : zero), tv, 0, 0, 0);
+      }
+    }
     if (m >= p.m) continue;
     const int lrow0 = wr * (16 * T) + 16 * t + 4 * g;
     const int64_t n0 = tile * ROWS + lrow0;
@@ -372,15 +395,7 @@ __device__ __forceinline__ void finish_tile(const SkinnyParams& p, int64_t tile,
       if (n >= p.n) break;
       float tt = 0.0f;
       if (p.b_vec) {
-        const uint16_t* brow = b_lds + (lrow0 + v) * (r + 8);
-        for (int j = 0; j < r; j += 8) {
-          const u32x4_t b8 = *reinterpret_cast<const u32x4_t*>(brow + j);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            tt = __builtin_fmaf(hrow[j + 2 * e], bf16lo_to_f32(b8[e]), tt);
-            tt = __builtin_fmaf(hrow[j + 2 * e + 1], bf16hi_to_f32(b8[e]), tt);
-          }
-        }
+        tt = tv[v];
       } else {
         const uint16_t* brow = p.lora_b + n * r;
         for (int j = 0; j < r; ++j) tt = __builtin_fmaf(hrow[j], bf16_to_f32(brow[j]), tt);
@@ -420,6 +435,7 @@ __global__ void __launch_bounds__(256) k_skinny(SkinnyParams p) {
   constexpr int kRed = WK > 1 ? (WK - 1) * WR * T * MB * 64 : 1;
   __shared__ f32x4_t red[kRed];
   __shared__ float h_lds[64 * 65];
+  __shared__ __align__(16) uint16_t hb_lds[64 * 72];
   __shared__ __align__(16) uint16_t b_lds[16 * T * WR * 72];
   __shared__ int flag;
   const int tid = threadIdx.x;
@@ -460,7 +476,7 @@ __global__ void __launch_bounds__(256) k_skinny(SkinnyParams p) {
   const int state = flag;
   if (state == 0) return;
   // state 2: the adapters never arrived within the spin limit; h is poisoned
-  finish_tile<MB, T, WK>(p, tile, h_lds, b_lds, state == 2);
+  finish_tile<MB, T, WK>(p, tile, h_lds, hb_lds, b_lds, state == 2);
 }
 
 // (id, T, U, WK): wave = 16 T rows x 128 U columns; block = 4 / WK waves of
