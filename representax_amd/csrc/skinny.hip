@@ -12,9 +12,11 @@
 //     block's K range are reduced through LDS in a fixed order.
 // Partials go to the workspace through device-coherent stores. Arrival
 // counters (a small per-device array, one slot per call in flight) pick the
-// finisher of each row tile: the last of the tile's K-split blocks, which
-// waits (bounded) until every adapter block has arrived, sums the partials in
-// split order and applies the reference's rounding points: h = bf16(.),
+// last adapter block to arrive, which sums the adapter partials in split
+// order into one fp32 h, and the finisher of each row tile: the last of the
+// tile's K-split blocks, which waits (bounded) until that sum has arrived,
+// sums the weight partials in split order and applies the reference's
+// rounding points: h = bf16(.),
 // base = bf16(.), t = bf16(h B^T), y = bf16(base + bf16(t * c)) (+ bias,
 // rounded again). Results do not depend on arrival order. Calls take the
 // counter slots in turn, so at most kSlots calls may run at once on a device
@@ -65,6 +67,7 @@ struct SkinnyParams {
   int64_t a_splits;        // adapter blocks (kAdapterSpan columns each)
   float* part_w;           // [splits][tiles][frags][64][4]
   float* part_h;           // [a_splits][4][MB][64][4]
+  float* h_sum;            // [4][MB][64][4]: the partials summed in split order
   int slot;               // counter slot of this call
   int spin;               // polls of the bounded wait
   unsigned int* err;      // device error word (kDevErrSkinnyWait on timeout)
@@ -87,7 +90,8 @@ __device__ __forceinline__ void dequant8_exact(uint32_t word, float s, float m8s
 }
 
 // Arrival counters, one slot per call in flight (calls take the slots in
-// turn): [0] adapter blocks, [1] done (adapter blocks and tile finishers past
+// turn): [0] adapter blocks (one count each, and one more from the last of
+// them once the summed h is stored), [1] done (adapter blocks and tile finishers past
 // their last access to the slot), [2 + t] K splits of tile t. They are zero
 // when the module loads and every call leaves its slot at zero.
 __device__ unsigned int g_skinny_counters[kSlots][kMaxTiles + 2];
@@ -283,9 +287,35 @@ __device__ __forceinline__ void adapter_part(const SkinnyParams& p, int64_t a_sp
     if (16 * mb + rl < p.m) store_coherent(dst + (wave * MB + mb) * 64 + lane, acc[mb]);
 }
 
+// The last adapter block of a call: h = the adapter partials summed in split
+// order (fp32, from zero), one fragment set that every tile finisher loads
+// instead of summing all a_splits partials itself.
+template <int MB>
+__device__ __forceinline__ void adapter_sum(const SkinnyParams& p) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  if (16 * wave >= p.rank) return;
+  const f32x4_t* part_h = reinterpret_cast<const f32x4_t*>(p.part_h);
+  f32x4_t acc[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 8
+  for (int64_t sp = 0; sp < p.a_splits; ++sp) {
+    f32x4_t v[MB];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) v[mb] = load_coherent(part_h + (sp * 4 * MB + wave * MB + mb) * 64 + lane);
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) acc[mb] += v[mb];
+  }
+  f32x4_t* dst = reinterpret_cast<f32x4_t*>(p.h_sum);
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) store_coherent(dst + (wave * MB + mb) * 64 + lane, acc[mb]);
+}
+
 // Outputs of one row tile. Each lane sums (in split order) the weight
-// fragments it would have written and, in waves below rank / 16, the h
-// fragments; both sets of loads issue from one loop. h = bf16(.) goes to LDS
+// fragments it would have written and, in waves below rank / 16, loads the
+// summed h fragments (issued first). h = bf16(.) goes to LDS
 // as fp32 (row stride rank + 1) and as bf16 (row stride rank + 8); the
 // tile's rows of B are in LDS (row stride rank + 8) when they load as
 // vectors, and then t = h B^T of each fragment is one 16x16x32 MFMA per 32
@@ -306,36 +336,24 @@ __device__ __forceinline__ void finish_tile(const SkinnyParams& p, int64_t tile,
   const int r = p.rank;
   const bool h_wave = 16 * wave < r;
   const f32x4_t* part = reinterpret_cast<const f32x4_t*>(p.part_w);
-  const f32x4_t* part_h = reinterpret_cast<const f32x4_t*>(p.part_h);
-  f32x4_t wacc[FI];
+  const f32x4_t* h_sum = reinterpret_cast<const f32x4_t*>(p.h_sum);
+  const int hw = h_wave ? wave : 0;
   f32x4_t hacc[MB];
 #pragma unroll
-  for (int i = 0; i < FI; ++i) wacc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int mb = 0; mb < MB; ++mb) hacc[mb] = load_coherent(h_sum + (hw * MB + mb) * 64 + lane);
+  f32x4_t wacc[FI];
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb) hacc[mb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  const int64_t rounds = p.splits > p.a_splits ? p.splits : p.a_splits;
-  const int hw = h_wave ? wave : 0;
+  for (int i = 0; i < FI; ++i) wacc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll 8
-  for (int64_t sp = 0; sp < rounds; ++sp) {
-    const int64_t sw = sp < p.splits ? sp : p.splits - 1;
-    const int64_t sh = sp < p.a_splits ? sp : p.a_splits - 1;
+  for (int64_t sp = 0; sp < p.splits; ++sp) {
     f32x4_t vw[FI];
-    f32x4_t vh[MB];
 #pragma unroll
     for (int i = 0; i < FI; ++i) {
       const int f = wave + 4 * i < F ? wave + 4 * i : 0;
-      vw[i] = load_coherent(part + ((sw * p.tiles + tile) * F + f) * 64 + lane);
+      vw[i] = load_coherent(part + ((sp * p.tiles + tile) * F + f) * 64 + lane);
     }
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb) vh[mb] = load_coherent(part_h + (sh * 4 * MB + hw * MB + mb) * 64 + lane);
-    if (sp < p.splits) {
-#pragma unroll
-      for (int i = 0; i < FI; ++i) wacc[i] += vw[i];
-    }
-    if (sp < p.a_splits) {
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb) hacc[mb] += vh[mb];
-    }
+    for (int i = 0; i < FI; ++i) wacc[i] += vw[i];
   }
   if (h_wave) {
 #pragma unroll
@@ -416,10 +434,11 @@ __device__ __forceinline__ void finish_tile(const SkinnyParams& p, int64_t tile,
 }
 
 // Bounded wait (lane 0 of the block) until all adapter blocks of this call
-// have arrived. Adapter blocks come first in the grid and are dispatched
-// before any weight block, and none of them waits on anything, so the wait
-// ends as soon as they finish; the spin limit only guarantees that every
-// wave exits. Returns false if the limit was hit.
+// have arrived and the last of them has stored the summed h. Adapter blocks
+// come first in the grid and are dispatched before any weight block, and
+// none of them waits on anything, so the wait ends as soon as they finish;
+// the spin limit only guarantees that every wave exits. Returns false if the
+// limit was hit.
 __device__ __forceinline__ bool wait_adapters(const unsigned int* word, unsigned int target,
                                               int spin) {
   for (int it = 0; it < spin; ++it) {
@@ -440,15 +459,32 @@ __global__ void __launch_bounds__(256) k_skinny(SkinnyParams p) {
   __shared__ int flag;
   const int tid = threadIdx.x;
   unsigned int* ctr = g_skinny_counters[p.slot];
-  const unsigned int a_target = static_cast<unsigned int>(p.a_splits);
+  // the adapter word counts the a_splits arrivals, then once more when the
+  // last adapter block has stored the summed h
+  const unsigned int a_target = static_cast<unsigned int>(p.a_splits + 1);
   const unsigned int done_target = static_cast<unsigned int>(p.a_splits + p.tiles);
   if (static_cast<int64_t>(blockIdx.x) < p.a_splits) {
     adapter_part<MB>(p, blockIdx.x);
     drain_stores();
     __syncthreads();
     if (tid == 0) {
+      const unsigned int old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const int last = old + 1u == static_cast<unsigned int>(p.a_splits) ? 1 : 0;
+      if (!last) {
+        drain_stores();  // the arrival is performed before it is counted as done
+        done_count(ctr, 1, 2, done_target);
+      }
+      flag = last;
+    }
+    __syncthreads();
+    if (flag == 0) return;
+    // every other adapter block's partials were performed before its arrival
+    adapter_sum<MB>(p);
+    drain_stores();
+    __syncthreads();
+    if (tid == 0) {
       __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      drain_stores();  // the arrival is performed before it is counted as done
+      drain_stores();
       done_count(ctr, 1, 2, done_target);
     }
     return;
@@ -584,7 +620,8 @@ bool skinny_ok(int64_t m, int64_t n, int64_t k, int64_t rank, int64_t n_groups, 
 
 int64_t skinny_workspace_floats(int64_t m, int64_t n, int64_t k, int64_t rank) {
   const SkinnyPlan p = plan_skinny(m, n, k);
-  const int64_t one = p.splits * p.tiles * frags_per_tile(p) * 256 + p.a_splits * 4 * p.mb * 256;
+  const int64_t one =
+      p.splits * p.tiles * frags_per_tile(p) * 256 + (p.a_splits + 1) * 4 * p.mb * 256;
   const int64_t two = skinny2_ok(m, n, k, rank, 1, 0) ? skinny2_workspace_floats(m, n, k, rank) : 0;
   return one > two ? one : two;
 }
@@ -621,6 +658,7 @@ hipError_t launch_skinny_forward(const uint16_t* x, int64_t m, int64_t k, const 
   a.a_splits = p.a_splits;
   a.part_w = ws;
   a.part_h = a.part_w + p.splits * p.tiles * frags_per_tile(p) * 256;
+  a.h_sum = a.part_h + p.a_splits * 4 * p.mb * 256;
   a.slot = static_cast<int>(g_calls.fetch_add(1, std::memory_order_relaxed) % kSlots);
   a.spin = tune(kTuneSpinLimit) > 0 ? tune(kTuneSpinLimit) : kSpinLimit;
   a.err = device_error_word();

@@ -9,7 +9,9 @@ up after ``spin`` polls), and a scheduler interleaves the blocks at random.
 For every schedule, including those where a wait expires because the
 blocks it waits for have not run yet, the slot must be all-zero once every
 block has finished, and a wait that succeeded must only have succeeded on
-this call's own arrivals. The protocol the kernel used before (the last
+this call's own arrivals. The last adapter block to arrive counts the
+adapter word once more after it has summed every adapter partial, and the
+finishers wait for that count. The protocol the kernel used before (the last
 finisher clears the adapter word; a late adapter then increments it again)
 is kept as a negative control: the checker must find the schedules that
 leave its slot dirty.
@@ -45,9 +47,12 @@ class Slot:
 def skinny_blocks(slot: Slot, adapters: int, tiles: int, splits: int, spin: int, log: list,
                   fixed: bool = True):
     """Generators for the blocks of one k_skinny launch. Words: [0] adapter
-    arrivals, [1] done, [2 + t] split arrivals of tile t."""
+    arrivals (and, with ``fixed``, one more count from the last adapter
+    once it has summed the partials), [1] done, [2 + t] split arrivals of
+    tile t."""
 
     done_target = adapters + tiles
+    h_target = adapters + 1 if fixed else adapters
 
     def done_count():
         old = slot.fetch_add(1)
@@ -58,9 +63,14 @@ def skinny_blocks(slot: Slot, adapters: int, tiles: int, splits: int, spin: int,
         yield
 
     def adapter():
-        slot.fetch_add(0)
+        old = slot.fetch_add(0)
         yield
         if fixed:
+            if old + 1 == adapters:
+                # the last arrival sums the partials, then counts once more
+                yield
+                slot.fetch_add(0)
+                yield
             yield from done_count()
 
     def weight(t: int):
@@ -72,10 +82,10 @@ def skinny_blocks(slot: Slot, adapters: int, tiles: int, splits: int, spin: int,
         yield
         if not last:
             return
-        ok = snapshot == adapters
+        ok = snapshot == h_target
         polls = 0
         while not ok and polls < spin:
-            ok = slot.w[0] == adapters
+            ok = slot.w[0] == h_target
             polls += 1
             yield
         log.append(("finisher", t, ok))
