@@ -63,7 +63,7 @@ int rpx_abi_version(void);
  *                        weight: 14 256x128, 15 128x128, 16 64x128
  *                        (env RPX_GEMM_TILE)
  *   RPX_TUNE_FP8_TILE    fp8 GEMM tile: 0 planner, 1..11 (env RPX_FP8_TILE)
- *   RPX_TUNE_SKINNY_TILE one-launch skinny tile: 0 planner, 1..14; a nonzero
+ *   RPX_TUNE_SKINNY_TILE one-launch skinny tile: 0 planner, 1..15; a nonzero
  *                        value also turns the two-launch form off
  *                        (env RPX_SKINNY_TILE)
  *   RPX_TUNE_SKINNY2     two-launch skinny form: -1 planner (M <= 4), 0 never,

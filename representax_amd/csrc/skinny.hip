@@ -531,7 +531,8 @@ __global__ void __launch_bounds__(256) k_skinny(SkinnyParams p) {
   X(11, 1, 2, 2)              \
   X(12, 1, 4, 2)              \
   X(13, 1, 1, 2)              \
-  X(14, 2, 1, 4)
+  X(14, 2, 1, 4)              \
+  X(15, 2, 2, 4)
 
 struct SkinnyCfg {
   int id, t, u, wk;
@@ -564,13 +565,25 @@ SkinnyPlan make_plan(const SkinnyCfg& c, int64_t m, int64_t n, int64_t k) {
 // round trip, the partials' coherent stores, one arrival and the finisher's
 // loads each cost a device round trip, so the shapes differ mainly in how
 // many blocks they dispatch and how long the finisher's reductions are.
-// Measured on the three Qwen3-2B projection shapes for M in {1, 4, 16, 64}:
-// 64-row tiles with 512-column splits (two row waves x two column waves) are
-// best or within 5% except for single-block M with K >= N, where 32-row
-// tiles with 1024-column splits win. The kTuneSkinnyTile knob forces a shape.
+// Measured on the three Qwen3-2B projection shapes for M in {8, 16, 32, 64}
+// (graph-replayed, weights cycled through HBM): from three 16-row M blocks
+// up, and from two when K >= N, 32-row tiles with 1024-column splits over
+// four column waves are fastest (M = 64: 26.7 / 33.5 / 19.3 -> 23.1 / 25.6 /
+// 14.6 us on 2048->6144 / 6144->2048 / 2048->2048): half the K splits of the
+// 64-row tile, so half the fp32 partials of y, at the same x fragments per
+// wave. Below that, 64-row tiles with 512-column splits (two row waves x two
+// column waves), or for one M block with K >= N 32-row tiles with
+// 1024-column splits over two column waves, are best or within 5%. The
+// kTuneSkinnyTile knob forces a shape.
 SkinnyPlan plan_skinny(int64_t m, int64_t n, int64_t k) {
   int want = tune(kTuneSkinnyTile);
-  if (want <= 0) want = ((m + 15) / 16 == 1 && k >= n) ? 12 : 7;
+  if (want <= 0) {
+    const int64_t mb = (m + 15) / 16;
+    if (mb >= 3 || (mb == 2 && k >= n))
+      want = 15;
+    else
+      want = (mb == 1 && k >= n) ? 12 : 7;
+  }
   for (const SkinnyCfg& c : kSkinnyCfgs) {
     const SkinnyPlan p = make_plan(c, m, n, k);
     if (c.id == want && p.tiles <= kMaxTiles) return p;

@@ -232,7 +232,7 @@ def test_skinny_forward_matches_oracle(m, k, n, r, group, bias):
     assert_bf16_close(from_dev(y), y_o, what="y")
 
 
-SKINNY_TILE_IDS = list(range(1, 15))
+SKINNY_TILE_IDS = list(range(1, 16))
 
 
 @pytest.mark.parametrize("tile", SKINNY_TILE_IDS)
