@@ -33,18 +33,25 @@ __device__ __forceinline__ void done_count(unsigned int* slot, int done_word, in
 // L2 of the XCD, which at one fence per block costs more than the weight
 // stream itself. A coherent store has reached the coherence point once the
 // wave's vmcnt drains (drain_stores), before the block's arrival is counted.
-__device__ __forceinline__ void store_coherent(f32x4_t* dst, f32x4_t v) {
-  unsigned long long* d = reinterpret_cast<unsigned long long*>(dst);
+//
+// A wave's fragment (64 lanes x 4 floats, 1 KB at `frag`) is stored by
+// halves: lane l's floats 0-1 go to 64-bit word l and floats 2-3 to word
+// 64 + l, so each of the two store instructions writes 512 contiguous bytes
+// (with the halves interleaved per lane, each instruction covered every
+// 64-byte segment only half and the segments were written twice).
+__device__ __forceinline__ void store_coherent(f32x4_t* frag, int lane, f32x4_t v) {
+  unsigned long long* d = reinterpret_cast<unsigned long long*>(frag);
   const u32x4_t u = __builtin_bit_cast(u32x4_t, v);
-  __hip_atomic_store(d, static_cast<unsigned long long>(u[0]) | (static_cast<unsigned long long>(u[1]) << 32),
+  __hip_atomic_store(d + lane, static_cast<unsigned long long>(u[0]) | (static_cast<unsigned long long>(u[1]) << 32),
                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  __hip_atomic_store(d + 1, static_cast<unsigned long long>(u[2]) | (static_cast<unsigned long long>(u[3]) << 32),
+  __hip_atomic_store(d + 64 + lane,
+                     static_cast<unsigned long long>(u[2]) | (static_cast<unsigned long long>(u[3]) << 32),
                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ f32x4_t load_coherent(const f32x4_t* src) {
-  unsigned long long* s = reinterpret_cast<unsigned long long*>(const_cast<f32x4_t*>(src));
-  const unsigned long long a = __hip_atomic_load(s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  const unsigned long long b = __hip_atomic_load(s + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ f32x4_t load_coherent(const f32x4_t* frag, int lane) {
+  unsigned long long* s = reinterpret_cast<unsigned long long*>(const_cast<f32x4_t*>(frag));
+  const unsigned long long a = __hip_atomic_load(s + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const unsigned long long b = __hip_atomic_load(s + 64 + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   return __builtin_bit_cast(f32x4_t, u32x4_t{static_cast<uint32_t>(a), static_cast<uint32_t>(a >> 32),
                                              static_cast<uint32_t>(b), static_cast<uint32_t>(b >> 32)});
 }

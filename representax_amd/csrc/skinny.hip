@@ -239,7 +239,7 @@ __device__ __forceinline__ void weight_part(const SkinnyParams& p, int64_t tile,
     for (int t = 0; t < T; ++t)
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb)
-        if (16 * mb + rl < p.m) store_coherent(dst + ((wr * T + t) * MB + mb) * 64 + lane, acc[t][mb]);
+        if (16 * mb + rl < p.m) store_coherent(dst + ((wr * T + t) * MB + mb) * 64, lane, acc[t][mb]);
   }
 }
 
@@ -284,7 +284,7 @@ __device__ __forceinline__ void adapter_part(const SkinnyParams& p, int64_t a_sp
   f32x4_t* dst = reinterpret_cast<f32x4_t*>(p.part_h) + a_split * (4 * MB * 64);
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb)
-    if (16 * mb + rl < p.m) store_coherent(dst + (wave * MB + mb) * 64 + lane, acc[mb]);
+    if (16 * mb + rl < p.m) store_coherent(dst + (wave * MB + mb) * 64, lane, acc[mb]);
 }
 
 // The last adapter block of a call: h = the adapter partials summed in split
@@ -304,13 +304,13 @@ __device__ __forceinline__ void adapter_sum(const SkinnyParams& p) {
   for (int64_t sp = 0; sp < p.a_splits; ++sp) {
     f32x4_t v[MB];
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb) v[mb] = load_coherent(part_h + (sp * 4 * MB + wave * MB + mb) * 64 + lane);
+    for (int mb = 0; mb < MB; ++mb) v[mb] = load_coherent(part_h + (sp * 4 * MB + wave * MB + mb) * 64, lane);
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) acc[mb] += v[mb];
   }
   f32x4_t* dst = reinterpret_cast<f32x4_t*>(p.h_sum);
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb) store_coherent(dst + (wave * MB + mb) * 64 + lane, acc[mb]);
+  for (int mb = 0; mb < MB; ++mb) store_coherent(dst + (wave * MB + mb) * 64, lane, acc[mb]);
 }
 
 // Outputs of one row tile. Each lane sums (in split order) the weight
@@ -340,7 +340,7 @@ __device__ __forceinline__ void finish_tile(const SkinnyParams& p, int64_t tile,
   const int hw = h_wave ? wave : 0;
   f32x4_t hacc[MB];
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb) hacc[mb] = load_coherent(h_sum + (hw * MB + mb) * 64 + lane);
+  for (int mb = 0; mb < MB; ++mb) hacc[mb] = load_coherent(h_sum + (hw * MB + mb) * 64, lane);
   f32x4_t wacc[FI];
 #pragma unroll
   for (int i = 0; i < FI; ++i) wacc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
@@ -350,7 +350,7 @@ __device__ __forceinline__ void finish_tile(const SkinnyParams& p, int64_t tile,
 #pragma unroll
     for (int i = 0; i < FI; ++i) {
       const int f = wave + 4 * i < F ? wave + 4 * i : 0;
-      vw[i] = load_coherent(part + ((sp * p.tiles + tile) * F + f) * 64 + lane);
+      vw[i] = load_coherent(part + ((sp * p.tiles + tile) * F + f) * 64, lane);
     }
 #pragma unroll
     for (int i = 0; i < FI; ++i) wacc[i] += vw[i];
