@@ -215,10 +215,13 @@ def test_cpu_tensor_is_rejected():
     "m,k,n,r,group,bias",
     [(1, 2048, 6144, 32, None, False), (4, 6144, 2048, 32, None, True),
      (16, 2048, 2048, 32, 64, False), (17, 1024, 640, 16, None, True),
-     (64, 2048, 1024, 32, 64, True), (33, 384, 200, 8, 128, False), (2, 128, 70, 3, None, True)],
+     (64, 2048, 1024, 32, 64, True), (33, 384, 200, 8, 128, False), (2, 128, 70, 3, None, True),
+     (9, 256, 48, 16, None, True), (40, 256, 300, 24, 64, False)],
 )
 def test_skinny_forward_matches_oracle(m, k, n, r, group, bias):
-    """M <= 64 runs the split-K skinny kernels (rotating nothing: parity only)."""
+    """M <= 64 runs the split-K skinny kernels (rotating nothing: parity only),
+    including one adapter block and one K split (K = 256), where every
+    block finishes its own tile and the only adapter block sums h alone."""
 
     x, packed, scales, a, b, bias_bits, _ = _lora_case(m, k, n, r, group, seed=m + n, bias=bias)
     y_o, h_o = olora.lora_forward(x, packed, scales, a, b, alpha=float(r), rank=r,
